@@ -1,0 +1,360 @@
+"""Python binding of the gfx950 Q4/g64 quantized-linear engine (libhyperion_hip.so).
+
+This is the ctypes counterpart of the reference's safe FFI crate
+(crates/hyperion-ffi/src/lib.rs: raw externs :225-269, RAII handles :513-690,
+status mapping :303): every call checks the HypStatus, raises HypError with the
+thread-local message, and handles free themselves exactly once.
+
+The native library is the product; this module only marshals pointers. It never
+falls back to another implementation: if the library is missing or no GPU is
+present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhyperion_hip.so")
+
+HYP_STATUS = {
+    0: "OK",
+    1: "INVALID_ARGUMENT",
+    2: "NOT_FOUND",
+    3: "IO",
+    4: "OOM_GOVERNOR",
+    5: "UNSUPPORTED",
+    6: "INTERNAL",
+    7: "CANCELLED",
+}
+PROJ = {"q": 0, "k": 1, "v": 2, "o": 3, "gate": 4, "up": 5, "down": 6}
+EPILOGUE_NONE = 0
+EPILOGUE_SOFTCAP = 1
+
+# Every symbol declared in include/hyperion_hip.h.
+EXPORTED = [
+    "hyp_last_error", "hyp_runtime_info",
+    "hyp_device_alloc", "hyp_device_free",
+    "hyp_stream_create", "hyp_stream_destroy", "hyp_stream_synchronize",
+    "hyp_memcpy_htod", "hyp_memcpy_dtoh", "hyp_memcpy_dtod", "hyp_memset_device",
+    "hyp_event_create", "hyp_event_destroy", "hyp_event_record", "hyp_event_elapsed_ms",
+    "hyp_qweight_create", "hyp_qweight_create_device", "hyp_qweight_free",
+    "hyp_qweight_shape", "hyp_qweight_export",
+    "hyp_qmatmul", "hyp_qmatmul_ex", "hyp_qmlp_gate_up_gelu",
+    "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed",
+    "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
+    "hyp_qmodel_linear", "hyp_qmodel_embed",
+]
+
+
+class HypError(RuntimeError):
+    def __init__(self, status: int, op: str, message: str):
+        self.status = status
+        self.status_name = HYP_STATUS.get(status, f"UNKNOWN({status})")
+        super().__init__(f"{op}: {self.status_name}: {message}")
+
+
+class RuntimeInfo(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_uint32),
+        ("device_count", ctypes.c_int32),
+        ("device", ctypes.c_int32),
+        ("compute_units", ctypes.c_uint32),
+        ("hbm_bytes", ctypes.c_uint64),
+        ("clock_khz", ctypes.c_uint32),
+        ("l2_bytes", ctypes.c_uint32),
+        ("arch_name", ctypes.c_char * 64),
+        ("device_name", ctypes.c_char * 128),
+    ]
+
+
+_lib = None
+_P = ctypes.c_void_p
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_U32 = ctypes.c_uint32
+_SZ = ctypes.c_size_t
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhyperion_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    L = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "hyp_last_error": [ctypes.c_char_p, _SZ],
+        "hyp_runtime_info": [ctypes.POINTER(RuntimeInfo)],
+        "hyp_device_alloc": [_SZ, _PP],
+        "hyp_device_free": [_PP],
+        "hyp_stream_create": [_PP],
+        "hyp_stream_destroy": [_PP],
+        "hyp_stream_synchronize": [_P],
+        "hyp_memcpy_htod": [_P, _P, _SZ, _P],
+        "hyp_memcpy_dtoh": [_P, _P, _SZ, _P],
+        "hyp_memcpy_dtod": [_P, _P, _SZ, _P],
+        "hyp_memset_device": [_P, ctypes.c_int, _SZ, _P],
+        "hyp_event_create": [_PP],
+        "hyp_event_destroy": [_PP],
+        "hyp_event_record": [_P, _P],
+        "hyp_event_elapsed_ms": [_P, _P, ctypes.POINTER(ctypes.c_float)],
+        "hyp_qweight_create": [_P, _P, _P, _U32, _U32, _U32, _U32, _PP],
+        "hyp_qweight_create_device": [_P, _P, _P, _U32, _U32, _U32, _U32, _P, _PP],
+        "hyp_qweight_free": [_PP],
+        "hyp_qweight_shape": [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32)],
+        "hyp_qweight_export": [_P, _P, _P, _P],
+        "hyp_qmatmul": [_P, _P, _U32, _P, _P],
+        "hyp_qmatmul_ex": [_P, _P, _U32, _P, ctypes.c_int, ctypes.c_float, _P],
+        "hyp_qmlp_gate_up_gelu": [_P, _P, _P, _U32, _P, _P],
+        "hyp_quantize_q4g64": [_P, _U32, _U32, _P, _P, _P, _P],
+        "hyp_dequantize_q4g64": [_P, _P, _P, _U32, _U32, _P, _U32, ctypes.c_float, _P, _P],
+        "hyp_embed": [_P, _P, _U32, _P, _P],
+        "hyp_qmodel_load": [ctypes.c_char_p, _U32, _PP],
+        "hyp_qmodel_free": [_PP],
+        "hyp_qmodel_num_layers": [_P, ctypes.POINTER(_U32)],
+        "hyp_qmodel_linear": [_P, _U32, ctypes.c_int, _PP],
+        "hyp_qmodel_embed": [_P, _PP],
+    }
+    for name, args in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    buf = ctypes.create_string_buffer(1024)
+    lib().hyp_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def check(status: int, op: str) -> None:
+    if status != 0:
+        raise HypError(status, op, last_error())
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def runtime_info() -> RuntimeInfo:
+    info = RuntimeInfo()
+    call("hyp_runtime_info", ctypes.byref(info))
+    return info
+
+
+class Stream:
+    """An explicit HIP stream (the reference passes mx::Stream explicitly)."""
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+        call("hyp_stream_create", ctypes.byref(self._h))
+
+    @property
+    def handle(self):
+        return self._h
+
+    def synchronize(self) -> None:
+        call("hyp_stream_synchronize", self._h)
+
+    def close(self) -> None:
+        if self._h:
+            call("hyp_stream_destroy", ctypes.byref(self._h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+        call("hyp_event_create", ctypes.byref(self._h))
+
+    def record(self, stream: Stream) -> None:
+        call("hyp_event_record", self._h, stream.handle)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        out = ctypes.c_float()
+        call("hyp_event_elapsed_ms", self._h, end._h, ctypes.byref(out))
+        return float(out.value)
+
+    def close(self) -> None:
+        if self._h:
+            call("hyp_event_destroy", ctypes.byref(self._h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype and shape (bf16 travels as uint16)."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self._p = ctypes.c_void_p()
+        call("hyp_device_alloc", max(self.nbytes, 1), ctypes.byref(self._p))
+
+    @property
+    def ptr(self):
+        return self._p
+
+    @classmethod
+    def from_host(cls, a: np.ndarray, stream: Stream) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        if a.nbytes:
+            call("hyp_memcpy_htod", d.ptr, a.ctypes.data_as(_P), a.nbytes, stream.handle)
+            stream.synchronize()
+        return d
+
+    def to_host(self, stream: Stream) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            call("hyp_memcpy_dtoh", out.ctypes.data_as(_P), self.ptr, self.nbytes, stream.handle)
+            stream.synchronize()
+        return out
+
+    def upload(self, a: np.ndarray, stream: Stream) -> None:
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes
+        call("hyp_memcpy_htod", self.ptr, a.ctypes.data_as(_P), a.nbytes, stream.handle)
+        stream.synchronize()
+
+    def fill_zero(self, stream: Stream) -> None:
+        call("hyp_memset_device", self.ptr, 0, self.nbytes, stream.handle)
+
+    def close(self) -> None:
+        if self._p:
+            call("hyp_device_free", ctypes.byref(self._p))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QWeight:
+    """A device-resident Q4/g64 projection (QuantizedLinear, weights.h:18-37)."""
+
+    def __init__(self, handle: ctypes.c_void_p, owner=None):
+        self._h = handle
+        self._owner = owner   # a QModel for borrowed handles
+
+    @classmethod
+    def from_host(cls, w: np.ndarray, scales: np.ndarray, biases: np.ndarray,
+                  group_size: int = 64, bits: int = 4) -> "QWeight":
+        w = np.ascontiguousarray(w, np.uint32)
+        s = np.ascontiguousarray(scales, np.uint16)
+        b = np.ascontiguousarray(biases, np.uint16)
+        n = w.shape[0]
+        k = s.shape[1] * group_size
+        h = ctypes.c_void_p()
+        call("hyp_qweight_create", w.ctypes.data_as(_P), s.ctypes.data_as(_P), b.ctypes.data_as(_P),
+             n, k, group_size, bits, ctypes.byref(h))
+        return cls(h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def shape(self):
+        n, k = _U32(), _U32()
+        call("hyp_qweight_shape", self._h, ctypes.byref(n), ctypes.byref(k))
+        return int(n.value), int(k.value)
+
+    def export(self):
+        n, k = self.shape
+        w = np.empty((n, k // 8), np.uint32)
+        s = np.empty((n, k // 64), np.uint16)
+        b = np.empty((n, k // 64), np.uint16)
+        call("hyp_qweight_export", self._h, w.ctypes.data_as(_P), s.ctypes.data_as(_P), b.ctypes.data_as(_P))
+        return w, s, b
+
+    def close(self) -> None:
+        if self._h and self._owner is None:
+            call("hyp_qweight_free", ctypes.byref(self._h))
+        self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QModel:
+    """All resident Q4 projections of an MLX artifact (load_model_weights)."""
+
+    def __init__(self, path: str, num_layers: int = 0):
+        self._h = ctypes.c_void_p()
+        call("hyp_qmodel_load", path.encode(), num_layers, ctypes.byref(self._h))
+
+    @property
+    def num_layers(self) -> int:
+        out = _U32()
+        call("hyp_qmodel_num_layers", self._h, ctypes.byref(out))
+        return int(out.value)
+
+    def linear(self, layer: int, proj: str) -> QWeight:
+        h = ctypes.c_void_p()
+        call("hyp_qmodel_linear", self._h, layer, PROJ[proj], ctypes.byref(h))
+        return QWeight(h, owner=self)
+
+    def embed(self) -> QWeight:
+        h = ctypes.c_void_p()
+        call("hyp_qmodel_embed", self._h, ctypes.byref(h))
+        return QWeight(h, owner=self)
+
+    def close(self) -> None:
+        if self._h:
+            call("hyp_qmodel_free", ctypes.byref(self._h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def qmatmul(w: QWeight, x: DeviceArray, m: int, y: DeviceArray, stream: Stream,
+            softcap: Optional[float] = None) -> None:
+    if softcap is None:
+        call("hyp_qmatmul", w.handle, x.ptr, m, y.ptr, stream.handle)
+    else:
+        call("hyp_qmatmul_ex", w.handle, x.ptr, m, y.ptr, EPILOGUE_SOFTCAP, softcap, stream.handle)
+
+
+def qmlp_gate_up_gelu(gate: QWeight, up: QWeight, x: DeviceArray, m: int, h: DeviceArray,
+                      stream: Stream) -> None:
+    call("hyp_qmlp_gate_up_gelu", gate.handle, up.handle, x.ptr, m, h.ptr, stream.handle)
+
+
+def quantize(w: DeviceArray, n: int, k: int, wq: DeviceArray, s: DeviceArray, b: DeviceArray,
+             stream: Stream) -> None:
+    call("hyp_quantize_q4g64", w.ptr, n, k, wq.ptr, s.ptr, b.ptr, stream.handle)
+
+
+def dequantize(wq: DeviceArray, s: DeviceArray, b: DeviceArray, n_total: int, k: int,
+               rows: Optional[DeviceArray], n_rows: int, out: DeviceArray, stream: Stream,
+               out_scale: float = 0.0) -> None:
+    call("hyp_dequantize_q4g64", wq.ptr, s.ptr, b.ptr, n_total, k,
+         rows.ptr if rows is not None else None, n_rows, out_scale, out.ptr, stream.handle)
+
+
+def embed(table: QWeight, ids: DeviceArray, n_ids: int, out: DeviceArray, stream: Stream) -> None:
+    call("hyp_embed", table.handle, ids.ptr, n_ids, out.ptr, stream.handle)

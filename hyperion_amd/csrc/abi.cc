@@ -1,0 +1,523 @@
+// The hyp_* C ABI (include/hyperion_hip.h). Conventions mirror the reference ABI:
+// status codes and thread-local last error (native/hyperion_mlx/src/abi_error.cc:7-19),
+// the no-throw abi_call wrapper (runtime.mm:79-97), magic-tagged handles with
+// idempotent free (model.cc:66-68,170-207).
+#include <array>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <filesystem>
+#include <memory>
+#include <new>
+#include <string>
+
+#include "hyperion_hip.h"
+#include "kernels.h"
+#include "qlinear.h"
+
+using hyperion::hip::Epilogue;
+using hyperion::hip::NativeError;
+using hyperion::model::ModelWeights;
+using hyperion::model::QuantizedLinear;
+
+namespace {
+
+constexpr std::uint32_t kQWeightMagic = 0x48505157U;   // "HPQW"
+constexpr std::uint32_t kQModelMagic = 0x4850514DU;    // "HPQM"
+constexpr std::uint32_t kStreamMagic = 0x48505354U;    // "HPST"
+constexpr std::uint32_t kEventMagic = 0x48504556U;     // "HPEV"
+
+constexpr std::size_t kLastErrorCapacity = 1024;
+thread_local std::array<char, kLastErrorCapacity> g_last_error{};
+
+HypStatus fail(HypStatus status, const char* message) noexcept {
+    std::snprintf(g_last_error.data(), g_last_error.size(), "%s",
+                  message != nullptr ? message : "unknown native error");
+    return status;
+}
+
+HypStatus ok() noexcept {
+    g_last_error[0] = '\0';
+    return HYP_STATUS_OK;
+}
+
+template <typename Function>
+HypStatus abi_call(const char* operation, Function&& function) noexcept {
+    try {
+        function();
+        return ok();
+    } catch (const NativeError& error) {
+        return fail(error.status(), error.what());
+    } catch (const std::bad_alloc&) {
+        return fail(HYP_STATUS_INTERNAL, "native host allocation failed");
+    } catch (const std::filesystem::filesystem_error& error) {
+        return fail(HYP_STATUS_IO, error.what());
+    } catch (const std::exception& error) {
+        return fail(HYP_STATUS_INTERNAL, error.what());
+    } catch (...) {
+        std::snprintf(g_last_error.data(), g_last_error.size(), "%s failed with a non-standard exception",
+                      operation != nullptr ? operation : "native operation");
+        return HYP_STATUS_INTERNAL;
+    }
+}
+
+#define REQUIRE_ARG(cond, msg) HYP_REQUIRE((cond), HYP_STATUS_INVALID_ARGUMENT, (msg))
+
+// Throws UNSUPPORTED when no HIP device is usable, before any other HIP call.
+void require_device() {
+    int count = 0;
+    const hipError_t err = hipGetDeviceCount(&count);
+    if (err != hipSuccess || count <= 0) {
+        throw NativeError(HYP_STATUS_UNSUPPORTED, "no HIP device is available");
+    }
+}
+
+// fp32 -> nearest-even bf16 value, on the host (constants handed to kernels).
+float round_to_bf16(float f) {
+    std::uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+}
+
+}  // namespace
+
+struct HypQWeightOpaque {
+    std::uint32_t magic = 0;
+    bool owned_by_model = false;
+    QuantizedLinear lin;
+};
+
+struct HypQModelOpaque {
+    std::uint32_t magic = 0;
+    ModelWeights weights;
+    std::unique_ptr<HypQWeightOpaque> embed;
+    // Per layer, per HypProj; null for a global layer's V.
+    std::vector<std::array<std::unique_ptr<HypQWeightOpaque>, 7>> layers;
+};
+
+struct HypStreamOpaque {
+    std::uint32_t magic = 0;
+    hipStream_t stream = nullptr;
+};
+
+struct HypEventOpaque {
+    std::uint32_t magic = 0;
+    hipEvent_t event = nullptr;
+};
+
+namespace {
+
+const QuantizedLinear& qweight_ref(HypQWeight w, const char* what) {
+    REQUIRE_ARG(w != nullptr, std::string(what) + " handle is null");
+    REQUIRE_ARG(w->magic == kQWeightMagic,
+                std::string(what) + " handle magic mismatch (wrong type, freed, or corrupted)");
+    return w->lin;
+}
+
+hipStream_t stream_of(HypStream s) {
+    REQUIRE_ARG(s != nullptr, "stream handle is null (an explicit stream is required)");
+    REQUIRE_ARG(s->magic == kStreamMagic, "stream handle magic mismatch (wrong type, freed, or corrupted)");
+    return s->stream;
+}
+
+void validate_quant(std::uint32_t n, std::uint32_t k, std::uint32_t group_size, std::uint32_t bits) {
+    if (group_size != 64 || bits != 4) {
+        throw NativeError(HYP_STATUS_UNSUPPORTED, "only affine group_size=64 bits=4 is supported (got group_size=" +
+                                                      std::to_string(group_size) + " bits=" + std::to_string(bits) + ")");
+    }
+    REQUIRE_ARG(n > 0 && k > 0, "n and k must be positive");
+    REQUIRE_ARG(k % 64 == 0, "k must be a multiple of 64");
+}
+
+template <typename Handle>
+HypStatus free_handle(Handle** handle, std::uint32_t magic) noexcept {
+    if (handle == nullptr) return fail(HYP_STATUS_INVALID_ARGUMENT, "free requires a non-null handle pointer");
+    Handle* ptr = *handle;
+    if (ptr == nullptr) return ok();
+    if (ptr->magic != magic) return fail(HYP_STATUS_INVALID_ARGUMENT, "handle magic mismatch (wrong type, freed, or corrupted)");
+    ptr->magic = 0;
+    delete ptr;
+    *handle = nullptr;
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+HypStatus hyp_last_error(char* buffer, size_t buffer_len) {
+    if (buffer == nullptr || buffer_len == 0) {
+        return HYP_STATUS_INVALID_ARGUMENT;   // leaves the stored message intact
+    }
+    std::snprintf(buffer, buffer_len, "%s", g_last_error.data());
+    return HYP_STATUS_OK;
+}
+
+HypStatus hyp_runtime_info(HypRuntimeInfo* out) {
+    return abi_call("hyp_runtime_info", [&] {
+        REQUIRE_ARG(out != nullptr, "runtime info requires a non-null out pointer");
+        std::memset(out, 0, sizeof(*out));
+        out->abi_version = HYP_HIP_ABI_VERSION;
+        require_device();
+        int count = 0;
+        HYP_HIP_CHECK(hipGetDeviceCount(&count));
+        int dev = 0;
+        HYP_HIP_CHECK(hipGetDevice(&dev));
+        hipDeviceProp_t prop{};
+        HYP_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+        out->device_count = count;
+        out->device = dev;
+        out->compute_units = static_cast<std::uint32_t>(prop.multiProcessorCount);
+        out->hbm_bytes = static_cast<std::uint64_t>(prop.totalGlobalMem);
+        out->clock_khz = static_cast<std::uint32_t>(prop.clockRate);
+        out->l2_bytes = static_cast<std::uint32_t>(prop.l2CacheSize);
+        std::snprintf(out->arch_name, sizeof(out->arch_name), "%s", prop.gcnArchName);
+        std::snprintf(out->device_name, sizeof(out->device_name), "%s", prop.name);
+    });
+}
+
+HypStatus hyp_device_alloc(size_t bytes, void** out_ptr) {
+    return abi_call("hyp_device_alloc", [&] {
+        REQUIRE_ARG(out_ptr != nullptr, "alloc requires a non-null out pointer");
+        *out_ptr = nullptr;
+        REQUIRE_ARG(bytes > 0, "alloc of zero bytes");
+        require_device();
+        void* p = nullptr;
+        const hipError_t err = hipMalloc(&p, bytes);
+        if (err != hipSuccess) {
+            throw NativeError(HYP_STATUS_INTERNAL, "device allocation of " + std::to_string(bytes) +
+                                                       " bytes failed: " + hipGetErrorString(err));
+        }
+        *out_ptr = p;
+    });
+}
+
+HypStatus hyp_device_free(void** ptr) {
+    return abi_call("hyp_device_free", [&] {
+        REQUIRE_ARG(ptr != nullptr, "free requires a non-null pointer to the allocation");
+        if (*ptr == nullptr) return;
+        HYP_HIP_CHECK(hipFree(*ptr));
+        *ptr = nullptr;
+    });
+}
+
+HypStatus hyp_stream_create(HypStream* out_stream) {
+    return abi_call("hyp_stream_create", [&] {
+        REQUIRE_ARG(out_stream != nullptr, "create requires a non-null out handle");
+        require_device();
+        auto h = std::make_unique<HypStreamOpaque>();
+        HYP_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+        h->magic = kStreamMagic;
+        *out_stream = h.release();
+    });
+}
+
+HypStatus hyp_stream_destroy(HypStream* stream) {
+    if (stream == nullptr) return fail(HYP_STATUS_INVALID_ARGUMENT, "free requires a non-null handle pointer");
+    if (*stream == nullptr) return ok();
+    if ((*stream)->magic != kStreamMagic) {
+        return fail(HYP_STATUS_INVALID_ARGUMENT, "handle magic mismatch (wrong type, freed, or corrupted)");
+    }
+    const hipError_t err = hipStreamDestroy((*stream)->stream);
+    (*stream)->magic = 0;
+    delete *stream;
+    *stream = nullptr;
+    if (err != hipSuccess) return fail(HYP_STATUS_INTERNAL, hipGetErrorString(err));
+    return ok();
+}
+
+HypStatus hyp_stream_synchronize(HypStream stream) {
+    return abi_call("hyp_stream_synchronize", [&] { HYP_HIP_CHECK(hipStreamSynchronize(stream_of(stream))); });
+}
+
+HypStatus hyp_memcpy_htod(void* dst, const void* src, size_t bytes, HypStream stream) {
+    return abi_call("hyp_memcpy_htod", [&] {
+        hipStream_t s = stream_of(stream);
+        if (bytes == 0) return;
+        REQUIRE_ARG(dst != nullptr && src != nullptr, "memcpy requires non-null buffers");
+        HYP_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+    });
+}
+
+HypStatus hyp_memcpy_dtoh(void* dst, const void* src, size_t bytes, HypStream stream) {
+    return abi_call("hyp_memcpy_dtoh", [&] {
+        hipStream_t s = stream_of(stream);
+        if (bytes == 0) return;
+        REQUIRE_ARG(dst != nullptr && src != nullptr, "memcpy requires non-null buffers");
+        HYP_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+    });
+}
+
+HypStatus hyp_memcpy_dtod(void* dst, const void* src, size_t bytes, HypStream stream) {
+    return abi_call("hyp_memcpy_dtod", [&] {
+        hipStream_t s = stream_of(stream);
+        if (bytes == 0) return;
+        REQUIRE_ARG(dst != nullptr && src != nullptr, "memcpy requires non-null buffers");
+        HYP_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s));
+    });
+}
+
+HypStatus hyp_memset_device(void* dst, int value, size_t bytes, HypStream stream) {
+    return abi_call("hyp_memset_device", [&] {
+        hipStream_t s = stream_of(stream);
+        if (bytes == 0) return;
+        REQUIRE_ARG(dst != nullptr, "memset requires a non-null buffer");
+        HYP_HIP_CHECK(hipMemsetAsync(dst, value, bytes, s));
+    });
+}
+
+HypStatus hyp_event_create(HypEvent* out_event) {
+    return abi_call("hyp_event_create", [&] {
+        REQUIRE_ARG(out_event != nullptr, "create requires a non-null out handle");
+        require_device();
+        auto h = std::make_unique<HypEventOpaque>();
+        HYP_HIP_CHECK(hipEventCreate(&h->event));
+        h->magic = kEventMagic;
+        *out_event = h.release();
+    });
+}
+
+HypStatus hyp_event_destroy(HypEvent* event) {
+    if (event == nullptr) return fail(HYP_STATUS_INVALID_ARGUMENT, "free requires a non-null handle pointer");
+    if (*event == nullptr) return ok();
+    if ((*event)->magic != kEventMagic) {
+        return fail(HYP_STATUS_INVALID_ARGUMENT, "handle magic mismatch (wrong type, freed, or corrupted)");
+    }
+    const hipError_t err = hipEventDestroy((*event)->event);
+    (*event)->magic = 0;
+    delete *event;
+    *event = nullptr;
+    if (err != hipSuccess) return fail(HYP_STATUS_INTERNAL, hipGetErrorString(err));
+    return ok();
+}
+
+HypStatus hyp_event_record(HypEvent event, HypStream stream) {
+    return abi_call("hyp_event_record", [&] {
+        REQUIRE_ARG(event != nullptr && event->magic == kEventMagic, "event handle is invalid");
+        HYP_HIP_CHECK(hipEventRecord(event->event, stream_of(stream)));
+    });
+}
+
+HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms) {
+    return abi_call("hyp_event_elapsed_ms", [&] {
+        REQUIRE_ARG(start != nullptr && start->magic == kEventMagic, "start event handle is invalid");
+        REQUIRE_ARG(end != nullptr && end->magic == kEventMagic, "end event handle is invalid");
+        REQUIRE_ARG(out_ms != nullptr, "elapsed requires a non-null out pointer");
+        HYP_HIP_CHECK(hipEventSynchronize(end->event));
+        HYP_HIP_CHECK(hipEventElapsedTime(out_ms, start->event, end->event));
+    });
+}
+
+HypStatus hyp_qweight_create(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, uint32_t n,
+                             uint32_t k, uint32_t group_size, uint32_t bits, HypQWeight* out_weight) {
+    return abi_call("hyp_qweight_create", [&] {
+        REQUIRE_ARG(out_weight != nullptr, "create requires a non-null out handle");
+        validate_quant(n, k, group_size, bits);
+        REQUIRE_ARG(w != nullptr && scales != nullptr && biases != nullptr,
+                    "weight, scales and biases must be non-null");
+        require_device();
+        auto h = std::make_unique<HypQWeightOpaque>();
+        h->lin = QuantizedLinear::from_host(w, scales, biases, n, k);
+        h->magic = kQWeightMagic;
+        *out_weight = h.release();
+    });
+}
+
+HypStatus hyp_qweight_create_device(const uint32_t* w, const void* scales, const void* biases, uint32_t n,
+                                    uint32_t k, uint32_t group_size, uint32_t bits, HypStream stream,
+                                    HypQWeight* out_weight) {
+    return abi_call("hyp_qweight_create_device", [&] {
+        REQUIRE_ARG(out_weight != nullptr, "create requires a non-null out handle");
+        validate_quant(n, k, group_size, bits);
+        REQUIRE_ARG(w != nullptr && scales != nullptr && biases != nullptr,
+                    "weight, scales and biases must be non-null");
+        hipStream_t s = stream_of(stream);
+        auto h = std::make_unique<HypQWeightOpaque>();
+        h->lin = QuantizedLinear::from_device(w, static_cast<const uint16_t*>(scales),
+                                              static_cast<const uint16_t*>(biases), n, k, s);
+        h->magic = kQWeightMagic;
+        *out_weight = h.release();
+    });
+}
+
+HypStatus hyp_qweight_free(HypQWeight* weight) {
+    if (weight != nullptr && *weight != nullptr && (*weight)->magic == kQWeightMagic && (*weight)->owned_by_model) {
+        return fail(HYP_STATUS_INVALID_ARGUMENT, "weight handle is owned by a model; free the model instead");
+    }
+    return free_handle(weight, kQWeightMagic);
+}
+
+HypStatus hyp_qweight_shape(HypQWeight weight, uint32_t* out_n, uint32_t* out_k) {
+    return abi_call("hyp_qweight_shape", [&] {
+        const QuantizedLinear& lin = qweight_ref(weight, "weight");
+        REQUIRE_ARG(out_n != nullptr && out_k != nullptr, "shape requires non-null out pointers");
+        *out_n = lin.mat.n;
+        *out_k = lin.mat.k;
+    });
+}
+
+HypStatus hyp_qweight_export(HypQWeight weight, uint32_t* w, uint16_t* scales, uint16_t* biases) {
+    return abi_call("hyp_qweight_export", [&] {
+        const QuantizedLinear& lin = qweight_ref(weight, "weight");
+        REQUIRE_ARG(w != nullptr && scales != nullptr && biases != nullptr, "export requires non-null buffers");
+        const size_t wb = static_cast<size_t>(lin.mat.n) * (lin.mat.k / 8u) * 4u;
+        const size_t sb = static_cast<size_t>(lin.mat.n) * (lin.mat.k / 64u) * 2u;
+        HYP_HIP_CHECK(hipMemcpy(w, lin.mat.w, wb, hipMemcpyDeviceToHost));
+        HYP_HIP_CHECK(hipMemcpy(scales, lin.mat.scales, sb, hipMemcpyDeviceToHost));
+        HYP_HIP_CHECK(hipMemcpy(biases, lin.mat.biases, sb, hipMemcpyDeviceToHost));
+    });
+}
+
+HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y, HypEpilogue epilogue, float cap,
+                         HypStream stream) {
+    return abi_call("hyp_qmatmul", [&] {
+        const QuantizedLinear& lin = qweight_ref(weight, "weight");
+        hipStream_t s = stream_of(stream);
+        Epilogue epi = Epilogue::kNone;
+        float cap_bf16 = 0.0f;
+        if (epilogue == HYP_EPILOGUE_SOFTCAP) {
+            REQUIRE_ARG(std::isfinite(cap) && cap > 0.0f, "softcap requires a finite positive cap");
+            epi = Epilogue::kSoftcap;
+            cap_bf16 = round_to_bf16(cap);
+        } else {
+            REQUIRE_ARG(epilogue == HYP_EPILOGUE_NONE, "unknown epilogue");
+        }
+        if (m == 0) return;
+        REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
+        lin.apply(static_cast<const uint16_t*>(x), m, static_cast<uint16_t*>(y), s, epi, cap_bf16);
+    });
+}
+
+HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, HypStream stream) {
+    return hyp_qmatmul_ex(weight, x, m, y, HYP_EPILOGUE_NONE, 0.0f, stream);
+}
+
+HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, uint32_t m, void* h,
+                                HypStream stream) {
+    return abi_call("hyp_qmlp_gate_up_gelu", [&] {
+        const QuantizedLinear& g = qweight_ref(gate, "gate");
+        const QuantizedLinear& u = qweight_ref(up, "up");
+        hipStream_t s = stream_of(stream);
+        REQUIRE_ARG(g.mat.n == u.mat.n && g.mat.k == u.mat.k, "gate and up must have the same shape");
+        if (m == 0) return;
+        REQUIRE_ARG(x != nullptr && h != nullptr, "x and h must be non-null device pointers");
+        hyperion::model::mlp_gate_up(g, u, static_cast<const uint16_t*>(x), m, static_cast<uint16_t*>(h), s);
+    });
+}
+
+HypStatus hyp_quantize_q4g64(const void* w, uint32_t n, uint32_t k, uint32_t* w_out, void* scales_out,
+                             void* biases_out, HypStream stream) {
+    return abi_call("hyp_quantize_q4g64", [&] {
+        hipStream_t s = stream_of(stream);
+        validate_quant(n, k, 64, 4);
+        REQUIRE_ARG(w != nullptr && w_out != nullptr && scales_out != nullptr && biases_out != nullptr,
+                    "quantize requires non-null device buffers");
+        hyperion::hip::launch_q4_quantize(static_cast<const uint16_t*>(w), n, k, w_out,
+                                          static_cast<uint16_t*>(scales_out), static_cast<uint16_t*>(biases_out), s);
+    });
+}
+
+HypStatus hyp_dequantize_q4g64(const uint32_t* w, const void* scales, const void* biases, uint32_t n_total,
+                               uint32_t k, const uint32_t* rows, uint32_t n_rows, float out_scale, void* out,
+                               HypStream stream) {
+    return abi_call("hyp_dequantize_q4g64", [&] {
+        hipStream_t s = stream_of(stream);
+        validate_quant(n_total, k, 64, 4);
+        REQUIRE_ARG(std::isfinite(out_scale), "out_scale must be finite");
+        if (n_rows == 0) return;
+        REQUIRE_ARG(w != nullptr && scales != nullptr && biases != nullptr && out != nullptr,
+                    "dequantize requires non-null device buffers");
+        REQUIRE_ARG(rows != nullptr || n_rows <= n_total, "n_rows exceeds the table without a row list");
+        hyperion::hip::launch_q4_dequantize(w, static_cast<const uint16_t*>(scales),
+                                            static_cast<const uint16_t*>(biases), n_total, k, rows, n_rows,
+                                            round_to_bf16(out_scale), static_cast<uint16_t*>(out), s);
+    });
+}
+
+HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void* out, HypStream stream) {
+    return abi_call("hyp_embed", [&] {
+        const QuantizedLinear& t = qweight_ref(table, "table");
+        hipStream_t s = stream_of(stream);
+        if (n_ids == 0) return;
+        REQUIRE_ARG(ids != nullptr && out != nullptr, "ids and out must be non-null device pointers");
+        const float scale = round_to_bf16(std::sqrt(static_cast<float>(t.mat.k)));
+        hyperion::hip::launch_q4_dequantize(t.mat.w, t.mat.scales, t.mat.biases, t.mat.n, t.mat.k, ids, n_ids,
+                                            scale, static_cast<uint16_t*>(out), s);
+    });
+}
+
+HypStatus hyp_qmodel_load(const char* dir, uint32_t num_layers, HypQModel* out_model) {
+    return abi_call("hyp_qmodel_load", [&] {
+        REQUIRE_ARG(out_model != nullptr, "load requires a non-null out handle");
+        REQUIRE_ARG(dir != nullptr, "weights path is null");
+        // Every artifact check (directory, shards, headers, names, shapes) runs on the
+        // host before the first device call, so those errors surface without a GPU.
+        const hyperion::model::ModelManifest manifest(dir, num_layers);
+        require_device();
+        auto model = std::make_unique<HypQModelOpaque>();
+        model->weights = manifest.upload();
+        auto wrap = [](QuantizedLinear* lin) {
+            auto h = std::make_unique<HypQWeightOpaque>();
+            h->magic = kQWeightMagic;
+            h->owned_by_model = true;
+            h->lin.mat = lin->mat;   // borrowed view; storage stays in the model
+            return h;
+        };
+        model->embed = wrap(&model->weights.embed);
+        for (auto& lw : model->weights.layers) {
+            std::array<std::unique_ptr<HypQWeightOpaque>, 7> hs;
+            hs[HYP_PROJ_Q] = wrap(&lw.q_proj);
+            hs[HYP_PROJ_K] = wrap(&lw.k_proj);
+            if (lw.v_proj) hs[HYP_PROJ_V] = wrap(&*lw.v_proj);
+            hs[HYP_PROJ_O] = wrap(&lw.o_proj);
+            hs[HYP_PROJ_GATE] = wrap(&lw.gate_proj);
+            hs[HYP_PROJ_UP] = wrap(&lw.up_proj);
+            hs[HYP_PROJ_DOWN] = wrap(&lw.down_proj);
+            model->layers.push_back(std::move(hs));
+        }
+        model->magic = kQModelMagic;
+        *out_model = model.release();
+    });
+}
+
+HypStatus hyp_qmodel_free(HypQModel* model) {
+    return free_handle(model, kQModelMagic);
+}
+
+HypStatus hyp_qmodel_num_layers(HypQModel model, uint32_t* out_num_layers) {
+    return abi_call("hyp_qmodel_num_layers", [&] {
+        REQUIRE_ARG(model != nullptr && model->magic == kQModelMagic, "model handle is invalid");
+        REQUIRE_ARG(out_num_layers != nullptr, "requires a non-null out pointer");
+        *out_num_layers = static_cast<uint32_t>(model->layers.size());
+    });
+}
+
+HypStatus hyp_qmodel_linear(HypQModel model, uint32_t layer, HypProj proj, HypQWeight* out_weight) {
+    return abi_call("hyp_qmodel_linear", [&] {
+        REQUIRE_ARG(model != nullptr && model->magic == kQModelMagic, "model handle is invalid");
+        REQUIRE_ARG(out_weight != nullptr, "requires a non-null out handle");
+        REQUIRE_ARG(layer < model->layers.size(), "layer index out of range");
+        REQUIRE_ARG(static_cast<int>(proj) >= 0 && static_cast<int>(proj) < 7, "unknown projection");
+        HypQWeightOpaque* h = model->layers[layer][static_cast<int>(proj)].get();
+        if (h == nullptr) {
+            throw NativeError(HYP_STATUS_NOT_FOUND, "layer " + std::to_string(layer) +
+                                                        " is a global (K = V) layer and has no v_proj");
+        }
+        *out_weight = h;
+    });
+}
+
+HypStatus hyp_qmodel_embed(HypQModel model, HypQWeight* out_weight) {
+    return abi_call("hyp_qmodel_embed", [&] {
+        REQUIRE_ARG(model != nullptr && model->magic == kQModelMagic, "model handle is invalid");
+        REQUIRE_ARG(out_weight != nullptr, "requires a non-null out handle");
+        *out_weight = model->embed.get();
+    });
+}
+
+}  // extern "C"

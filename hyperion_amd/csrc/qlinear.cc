@@ -1,0 +1,119 @@
+// QuantizedLinear on HIP: residency and dispatch between the decode GEMV and the
+// prefill MFMA GEMM (the reference leaves this choice to MLX's qmv/qmm routing,
+// native/hyperion_mlx/src/weights.h:14-17).
+#include "qlinear.h"
+
+#include <utility>
+
+namespace hyperion::model {
+
+using hip::NativeError;
+
+DeviceBuffer::DeviceBuffer(size_t bytes) : bytes_(bytes) {
+    if (bytes == 0) return;
+    const hipError_t err = hipMalloc(&ptr_, bytes);
+    if (err != hipSuccess) {
+        ptr_ = nullptr;
+        throw NativeError(HYP_STATUS_INTERNAL, std::string("device allocation of ") + std::to_string(bytes) +
+                                                   " bytes failed: " + hipGetErrorString(err));
+    }
+}
+
+DeviceBuffer::~DeviceBuffer() {
+    if (ptr_ != nullptr) {
+        (void)hipFree(ptr_);
+    }
+}
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& other) noexcept
+    : ptr_(std::exchange(other.ptr_, nullptr)), bytes_(std::exchange(other.bytes_, 0)) {}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& other) noexcept {
+    if (this != &other) {
+        if (ptr_ != nullptr) (void)hipFree(ptr_);
+        ptr_ = std::exchange(other.ptr_, nullptr);
+        bytes_ = std::exchange(other.bytes_, 0);
+    }
+    return *this;
+}
+
+namespace {
+
+constexpr size_t align256(size_t v) { return (v + 255u) & ~size_t{255u}; }
+
+struct Sizes {
+    size_t w, s, off_s, off_b, total;
+};
+
+Sizes sizes_for(uint32_t n, uint32_t k) {
+    Sizes z{};
+    z.w = static_cast<size_t>(n) * (k / 8u) * sizeof(uint32_t);
+    z.s = static_cast<size_t>(n) * (k / 64u) * sizeof(uint16_t);
+    z.off_s = align256(z.w);
+    z.off_b = z.off_s + align256(z.s);
+    z.total = z.off_b + align256(z.s);
+    return z;
+}
+
+QuantizedLinear make_storage(uint32_t n, uint32_t k, Sizes& z) {
+    z = sizes_for(n, k);
+    QuantizedLinear q;
+    q.storage = DeviceBuffer(z.total);
+    auto* base = static_cast<uint8_t*>(q.storage.data());
+    q.mat.w = reinterpret_cast<const uint32_t*>(base);
+    q.mat.scales = reinterpret_cast<const uint16_t*>(base + z.off_s);
+    q.mat.biases = reinterpret_cast<const uint16_t*>(base + z.off_b);
+    q.mat.n = n;
+    q.mat.k = k;
+    return q;
+}
+
+}  // namespace
+
+QuantizedLinear QuantizedLinear::from_host(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                           uint32_t n, uint32_t k) {
+    Sizes z{};
+    QuantizedLinear q = make_storage(n, k, z);
+    auto* base = static_cast<uint8_t*>(q.storage.data());
+    HYP_HIP_CHECK(hipMemcpy(base, w, z.w, hipMemcpyHostToDevice));
+    HYP_HIP_CHECK(hipMemcpy(base + z.off_s, scales, z.s, hipMemcpyHostToDevice));
+    HYP_HIP_CHECK(hipMemcpy(base + z.off_b, biases, z.s, hipMemcpyHostToDevice));
+    return q;
+}
+
+QuantizedLinear QuantizedLinear::from_device(const uint32_t* w, const uint16_t* scales,
+                                             const uint16_t* biases, uint32_t n, uint32_t k,
+                                             hipStream_t stream) {
+    Sizes z{};
+    QuantizedLinear q = make_storage(n, k, z);
+    auto* base = static_cast<uint8_t*>(q.storage.data());
+    HYP_HIP_CHECK(hipMemcpyAsync(base, w, z.w, hipMemcpyDeviceToDevice, stream));
+    HYP_HIP_CHECK(hipMemcpyAsync(base + z.off_s, scales, z.s, hipMemcpyDeviceToDevice, stream));
+    HYP_HIP_CHECK(hipMemcpyAsync(base + z.off_b, biases, z.s, hipMemcpyDeviceToDevice, stream));
+    return q;
+}
+
+void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream, Epilogue epi,
+                            float cap_bf16) const {
+    if (m == 0) return;
+    if (m <= hip::kGemvMaxM && mat.k <= hip::kGemvMaxK) {
+        hip::launch_q4_gemv(mat, nullptr, x, m, y, epi, cap_bf16, stream);
+    } else {
+        hip::launch_q4_gemm(mat, x, m, y, epi, cap_bf16, stream);
+    }
+}
+
+void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const uint16_t* x, uint32_t m,
+                 uint16_t* h, hipStream_t stream) {
+    if (m == 0) return;
+    if (m <= hip::kGemvMaxM && gate.mat.k <= hip::kGemvMaxK) {
+        hip::launch_q4_gemv(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f, stream);
+    } else {
+        // h <- gate(x); then the up GEMM's epilogue reads each gate value back and
+        // writes gelu(gate) * up in place (same thread reads and writes an element).
+        hip::launch_q4_gemm(gate.mat, x, m, h, Epilogue::kNone, 0.0f, stream);
+        hip::launch_q4_gemm(up.mat, x, m, h, Epilogue::kGeluMul, 0.0f, stream);
+    }
+}
+
+}  // namespace hyperion::model

@@ -1,0 +1,109 @@
+// Host-side mirror of the reference's quantized-linear layer and weight
+// residency, re-expressed on device-resident HIP buffers.
+//
+//   QuantizedLinear   native/hyperion_mlx/src/weights.h:18-37
+//   LayerWeights      native/hyperion_mlx/src/weights_loader.h:24-44 (projections only)
+//   ModelWeights      native/hyperion_mlx/src/weights_loader.h:49-66 (Q4 tables only)
+//
+// The reference keeps MLX arrays that are lazily mmapped and moved to the GPU on first
+// use (weights_loader.h:70-79). Here every projection is copied to HBM once at load
+// time in MLX layout; the kernels read that layout directly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace hyperion::model {
+
+using hip::Epilogue;
+using hip::Q4Matrix;
+
+// One device allocation, freed on destruction.
+class DeviceBuffer {
+  public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& other) noexcept;
+    DeviceBuffer& operator=(DeviceBuffer&& other) noexcept;
+
+    [[nodiscard]] void* data() const noexcept { return ptr_; }
+    [[nodiscard]] size_t bytes() const noexcept { return bytes_; }
+
+  private:
+    void* ptr_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+// One Q4/g64 projection [out_features = n, in_features = k] resident in HBM.
+struct QuantizedLinear {
+    DeviceBuffer storage;   // w | scales | biases, each 256-byte aligned
+    Q4Matrix mat;
+    int group_size = 64;
+    int bits = 4;
+
+    // Copy from host (MLX layout) or from device pointers.
+    static QuantizedLinear from_host(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                     uint32_t n, uint32_t k);
+    static QuantizedLinear from_device(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                       uint32_t n, uint32_t k, hipStream_t stream);
+
+    // y[m, n] = x[m, k] . dequant(W)^T (weights.h:26-37); device pointers.
+    void apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream,
+               Epilogue epi = Epilogue::kNone, float cap_bf16 = 0.0f) const;
+};
+
+// gelu_tanh(gate(x)) * up(x) (forward.cc:338-343 minus the down projection).
+void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const uint16_t* x, uint32_t m,
+                 uint16_t* h, hipStream_t stream);
+
+enum class LayerType { Sliding, Full };
+
+struct LayerWeights {
+    QuantizedLinear q_proj;
+    QuantizedLinear k_proj;
+    std::optional<QuantizedLinear> v_proj;   // absent on global (K = V) layers
+    QuantizedLinear o_proj;
+    QuantizedLinear gate_proj;
+    QuantizedLinear up_proj;
+    QuantizedLinear down_proj;
+    LayerType kind = LayerType::Sliding;
+};
+
+struct ModelWeights {
+    QuantizedLinear embed;   // tied: also the LM head (forward.cc:137-152)
+    std::vector<LayerWeights> layers;
+};
+
+// Host phase of load_model_weights: maps every shard, resolves and shape-checks
+// each projection. Touches no device, so artifact errors surface without a GPU.
+class ModelManifest {
+  public:
+    ModelManifest(const std::string& dir, uint32_t num_layers);
+    ~ModelManifest();
+    ModelManifest(const ModelManifest&) = delete;
+    ModelManifest& operator=(const ModelManifest&) = delete;
+    [[nodiscard]] uint32_t num_layers() const noexcept;
+    // Device phase: copy every planned projection into HBM.
+    [[nodiscard]] ModelWeights upload() const;
+
+  private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+// load_model_weights (weights_loader.cc:71-153) for the Q4 projections and the
+// embed table. num_layers == 0 loads every layer the shards hold.
+ModelWeights load_model_weights(const std::string& dir, uint32_t num_layers);
+
+}  // namespace hyperion::model

@@ -1,0 +1,207 @@
+/*
+ * hyperion_hip.h - C ABI of the MI355X (gfx950) Q4/g64 quantized-linear engine.
+ *
+ * Drop-in for the reference's quantized-linear path: every quantized linear in the
+ * reference is mlx::core::quantized_matmul(x, w, scales, biases, transpose=true,
+ * 64, 4, "affine") (native/hyperion_mlx/src/weights.h:26-37). This library replaces
+ * that call, the tied LM head (forward.cc:137-152), the MLP gating (forward.cc:324-343),
+ * the embed dequantize-gather (weights_loader.cc:53-69), the quantize used to make
+ * weights (mx.quantize, build_gemma4_unified_tiny.py:54-57) and the weight residency
+ * built by load_model_weights (weights_loader.cc:71-153).
+ *
+ * Conventions follow the reference ABI (native/hyperion_mlx/include/hyperion_mlx.h):
+ *  - every function returns HypStatus (same values as hyperion_mlx.h:12-21);
+ *  - a non-OK return stores a message in a thread-local buffer read by
+ *    hyp_last_error (abi_error.cc:7-19); an OK return clears it;
+ *  - no C++ exception crosses the boundary (the abi_call pattern, runtime.mm:79-97);
+ *  - handles are opaque and magic-tagged; create(out) rejects a NULL out pointer;
+ *    free(&h) sets h to NULL, is a no-op on NULL and rejects a wrong magic
+ *    (model.cc:170-207);
+ *  - input buffers are borrowed for the call only;
+ *  - one thread drives a device's work; calls are synchronous with respect to the
+ *    host only where stated (kernels are enqueued on the caller's stream).
+ *
+ * Layouts (MLX affine, transpose=true; tensor shapes as stored by mlx-lm):
+ *  - packed weight  uint32 [n, k/8]: code of column c lives in word c/8, bits
+ *                   [4*(c%8), 4*(c%8)+4) (lowest k in the lowest nibble);
+ *  - scales, biases bf16 [n, k/64];  dequant(W)[r, c] = scale[r, c/64] * q + bias[r, c/64];
+ *  - activations    bf16 row-major x [m, k], y [m, n]; y = x * dequant(W)^T.
+ * bf16 values cross the ABI as their 16-bit patterns (uint16_t or void*).
+ * "device pointer" means memory from hyp_device_alloc (or any hipMalloc'd memory
+ * on the current device).
+ */
+#ifndef HYPERION_HIP_H
+#define HYPERION_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HYP_HIP_ABI_VERSION 1u
+
+/* Same numbering as the reference (hyperion_mlx.h:12-21). OOM_GOVERNOR is unused here:
+ * device allocation failures report HYP_STATUS_INTERNAL as the reference does for
+ * allocation outside governor admission (model.cc:442-452). */
+typedef enum HypStatus {
+    HYP_STATUS_OK = 0,
+    HYP_STATUS_INVALID_ARGUMENT = 1,
+    HYP_STATUS_NOT_FOUND = 2,
+    HYP_STATUS_IO = 3,
+    HYP_STATUS_OOM_GOVERNOR = 4,
+    HYP_STATUS_UNSUPPORTED = 5,
+    HYP_STATUS_INTERNAL = 6,
+    HYP_STATUS_CANCELLED = 7
+} HypStatus;
+
+/* Opaque handles. */
+typedef struct HypQWeightOpaque* HypQWeight;   /* magic "HPQW": one resident Q4 projection */
+typedef struct HypQModelOpaque* HypQModel;     /* magic "HPQM": all resident Q4 projections */
+typedef struct HypStreamOpaque* HypStream;     /* a HIP stream (hipStream_t) */
+typedef struct HypEventOpaque* HypEvent;       /* a HIP event (hipEvent_t) */
+
+/* Device and build facts; replaces the Apple platform canary (runtime.mm:223-284). */
+typedef struct HypRuntimeInfo {
+    uint32_t abi_version;
+    int32_t device_count;
+    int32_t device;                 /* current device */
+    uint32_t compute_units;
+    uint64_t hbm_bytes;
+    uint32_t clock_khz;
+    uint32_t l2_bytes;
+    char arch_name[64];             /* e.g. "gfx950:sramecc+:xnack-" */
+    char device_name[128];
+} HypRuntimeInfo;
+
+/* Projection selector for hyp_qmodel_linear (weights_loader.cc:132-141 names). */
+typedef enum HypProj {
+    HYP_PROJ_Q = 0,
+    HYP_PROJ_K = 1,
+    HYP_PROJ_V = 2,
+    HYP_PROJ_O = 3,
+    HYP_PROJ_GATE = 4,
+    HYP_PROJ_UP = 5,
+    HYP_PROJ_DOWN = 6
+} HypProj;
+
+/* Epilogue applied by hyp_qmatmul_ex to the bf16 output. */
+typedef enum HypEpilogue {
+    HYP_EPILOGUE_NONE = 0,
+    HYP_EPILOGUE_SOFTCAP = 1        /* y = bf16(bf16(tanh(bf16(y / cap))) * cap), forward.cc:154-160 */
+} HypEpilogue;
+
+/* ---- errors and runtime ------------------------------------------------------- */
+
+/* Copy the calling thread's last error into buffer (NUL-terminated, truncated).
+ * Replaces hyp_last_error (hyperion_mlx.h:41, runtime.mm:286-298). */
+HypStatus hyp_last_error(char* buffer, size_t buffer_len);
+
+/* Fill *out with the ABI version and the current device's facts.
+ * Replaces hyp_runtime_canary (hyperion_mlx.h:38). UNSUPPORTED when no HIP device. */
+HypStatus hyp_runtime_info(HypRuntimeInfo* out);
+
+/* Device memory, streams and events. The reference gets these from MLX
+ * (lazy arrays moved to the GPU on first use, weights_loader.h:70-79, and explicit
+ * mx::Stream arguments, weights.h:26); a C caller of this engine gets them here. */
+HypStatus hyp_device_alloc(size_t bytes, void** out_ptr);
+HypStatus hyp_device_free(void** ptr);
+HypStatus hyp_stream_create(HypStream* out_stream);
+HypStatus hyp_stream_destroy(HypStream* stream);
+HypStatus hyp_stream_synchronize(HypStream stream);
+/* Copies are enqueued on stream and complete before hyp_stream_synchronize returns.
+ * Host buffers may be pageable (then the copy is synchronous with the host). */
+HypStatus hyp_memcpy_htod(void* dst_device, const void* src_host, size_t bytes, HypStream stream);
+HypStatus hyp_memcpy_dtoh(void* dst_host, const void* src_device, size_t bytes, HypStream stream);
+HypStatus hyp_memcpy_dtod(void* dst_device, const void* src_device, size_t bytes, HypStream stream);
+HypStatus hyp_memset_device(void* dst_device, int value, size_t bytes, HypStream stream);
+HypStatus hyp_event_create(HypEvent* out_event);
+HypStatus hyp_event_destroy(HypEvent* event);
+HypStatus hyp_event_record(HypEvent event, HypStream stream);
+/* Milliseconds between two recorded events; waits for `end` to complete. */
+HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
+
+/* ---- resident Q4 weights (QuantizedLinear, weights.h:18-25; make_proj,
+ *      weights_loader.cc:33-45) --------------------------------------------------- */
+
+/* Copy one projection from host memory into device-resident storage.
+ * w: uint32 [n, k/8]; scales/biases: bf16 [n, k/64] (MLX affine layout).
+ * group_size != 64 or bits != 4 -> UNSUPPORTED (the locked quantization,
+ * model.cc:73-74, hyperion-model/src/weights.rs:35-58); n == 0, k == 0 or
+ * k % 64 != 0 -> INVALID_ARGUMENT. */
+HypStatus hyp_qweight_create(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                             uint32_t n, uint32_t k, uint32_t group_size, uint32_t bits,
+                             HypQWeight* out_weight);
+/* Same, from device pointers (copied; the caller keeps ownership of its buffers). */
+HypStatus hyp_qweight_create_device(const uint32_t* w, const void* scales, const void* biases,
+                                    uint32_t n, uint32_t k, uint32_t group_size, uint32_t bits,
+                                    HypStream stream, HypQWeight* out_weight);
+HypStatus hyp_qweight_free(HypQWeight* weight);
+HypStatus hyp_qweight_shape(HypQWeight weight, uint32_t* out_n, uint32_t* out_k);
+/* Copy the resident projection back to host in MLX layout (synchronous). */
+HypStatus hyp_qweight_export(HypQWeight weight, uint32_t* w, uint16_t* scales, uint16_t* biases);
+
+/* ---- quantized matmul ---------------------------------------------------------- */
+
+/* y[m, n] = x[m, k] * dequant(W)^T with fp32 accumulation, bf16 out.
+ * Replaces QuantizedLinear::apply (weights.h:26-37) for every M: m <= 8 runs the
+ * decode GEMV, larger m the MFMA GEMM. x and y are device pointers; m == 0 is a
+ * no-op. */
+HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, HypStream stream);
+
+/* hyp_qmatmul with an epilogue; HYP_EPILOGUE_SOFTCAP with cap > 0 is the tied
+ * LM head + softcap of ForwardPass::lm_head/softcap (forward.cc:137-160). */
+HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y,
+                         HypEpilogue epilogue, float cap, HypStream stream);
+
+/* h[m, n] = gelu_tanh(x * dequant(G)^T) * (x * dequant(U)^T), the gate/up half of
+ * ForwardPass::mlp (forward.cc:338-343) with gelu_tanh rounded op-by-op in bf16 as
+ * forward.cc:324-336 composes it. gate and up must share (n, k). */
+HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, uint32_t m,
+                                void* h, HypStream stream);
+
+/* ---- quantize / dequantize ----------------------------------------------------- */
+
+/* mx.quantize(w, group_size=64, bits=4, mode="affine") of a bf16 [n, k] device matrix
+ * into w_out uint32 [n, k/8], scales_out/biases_out bf16 [n, k/64] (device). */
+HypStatus hyp_quantize_q4g64(const void* w, uint32_t n, uint32_t k, uint32_t* w_out,
+                             void* scales_out, void* biases_out, HypStream stream);
+
+/* mx.dequantize(..., dtype=bfloat16) of rows rows[0..n_rows) (rows == NULL: rows
+ * 0..n_rows) of a Q4 matrix of k columns into out bf16 [n_rows, k]; each value is
+ * bf16(bf16(scale*q) + bias). If out_scale != 0 the result is further multiplied
+ * by bf16(out_scale) and rounded (the embed scale, forward.cc:126-131). Row ids
+ * are device uint32; the kernel never reads outside the table: an id >= n_total
+ * yields a row of zeros (mx::take would raise; ids are not visible to the host
+ * without a synchronizing copy, so the check happens on the device). */
+HypStatus hyp_dequantize_q4g64(const uint32_t* w, const void* scales, const void* biases,
+                               uint32_t n_total, uint32_t k, const uint32_t* rows,
+                               uint32_t n_rows, float out_scale, void* out, HypStream stream);
+
+/* ModelWeights::embed + ForwardPass::embed (weights_loader.cc:53-69, forward.cc:126-131):
+ * gather rows ids[0..n_ids) of the resident table, dequantize to bf16 and multiply
+ * by bf16(sqrt(k)). ids are device uint32 < n (out-of-range ids produce zero rows). */
+HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void* out,
+                    HypStream stream);
+
+/* ---- weight residency (load_model_weights, weights_loader.cc:71-153) ------------ */
+
+/* Load every *.safetensors shard in dir, resolve the MLX names
+ * language_model.model.layers.{i}.{self_attn.{q,k,v,o}_proj | mlp.{gate,up,down}_proj}
+ * .{weight,scales,biases} and language_model.model.embed_tokens.* and make each a
+ * resident HypQWeight. A layer without v_proj is a global (K = V) layer.
+ * num_layers == 0 means "as many as the shards hold". Missing dir -> NOT_FOUND;
+ * unreadable shard -> IO; malformed header or a missing tensor -> INVALID_ARGUMENT. */
+HypStatus hyp_qmodel_load(const char* dir, uint32_t num_layers, HypQModel* out_model);
+HypStatus hyp_qmodel_free(HypQModel* model);
+HypStatus hyp_qmodel_num_layers(HypQModel model, uint32_t* out_num_layers);
+/* Borrowed handle (owned by the model; do not free). A global layer's V -> NOT_FOUND. */
+HypStatus hyp_qmodel_linear(HypQModel model, uint32_t layer, HypProj proj, HypQWeight* out_weight);
+HypStatus hyp_qmodel_embed(HypQModel model, HypQWeight* out_weight);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

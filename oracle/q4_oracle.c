@@ -1,0 +1,297 @@
+/*
+ * CPU oracle for the MLX-affine Q4/g64 path. TEST INFRASTRUCTURE ONLY: loaded by
+ * tests/, the smoke check and the benchmark's CPU-baseline leg as the checker,
+ * never by the product library. Function-by-function provenance and pinning
+ * status are in q4_oracle.h.
+ *
+ * Build flags matter: -ffp-contract=off (no fused multiply-add may be formed,
+ * because every restated MLX op rounds on its own) and no -ffast-math.
+ */
+#include "q4_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define GROUP 64
+#define NBINS 15.0f
+#define EPS 1e-7f
+
+/* Round-to-nearest-even fp32 -> bf16, quiet NaN kept quiet. MLX's bfloat16
+ * conversion (mlx/types/bf16.h) does the same. */
+uint16_t orc_bf16_from_f32(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (uint16_t)((u >> 16) | 0x0040u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float orc_f32_from_bf16(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void orc_bf16_from_f32_array(const float* in, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_bf16_from_f32(in[i]);
+}
+
+void orc_f32_from_bf16_array(const uint16_t* in, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_from_bf16(in[i]);
+}
+
+static inline float bf(float f) { return orc_f32_from_bf16(orc_bf16_from_f32(f)); }
+
+static inline float maxf_std(float a, float b) { return (a < b) ? b : a; } /* std::max */
+static inline float minf_std(float a, float b) { return (b < a) ? b : a; } /* std::min */
+
+/*
+ * MLX affine quantize, one group of 64 (MLX 0.32.0 CPU backend; the reference
+ * calls it at crates/hyperion-model/fixtures/build_gemma4_unified_tiny.py:54-57
+ * and scripts/nax-probe.py:74-76):
+ *   zero-point ("edge") rule - the scale is re-derived from the group's
+ *   larger-magnitude extreme so that that extreme and zero are both exactly
+ *   representable; all arithmetic in fp32 with IEEE division and rint.
+ */
+static void quantize_group(const uint16_t* w, uint32_t* wq, uint16_t* s_out, uint16_t* b_out) {
+    float w_min = INFINITY;
+    float w_max = -INFINITY;
+    for (int j = 0; j < GROUP; ++j) {
+        const float v = orc_f32_from_bf16(w[j]);
+        w_max = maxf_std(w_max, v);
+        w_min = minf_std(w_min, v);
+    }
+    const int mask = fabsf(w_min) > fabsf(w_max);
+    float scale = maxf_std((w_max - w_min) / NBINS, EPS);
+    scale = mask ? scale : -scale;
+    const float edge = mask ? w_min : w_max;
+    const float q0 = rintf(edge / scale);
+    float bias = 0.0f;
+    if (q0 != 0.0f) {
+        scale = edge / q0;
+        bias = edge;
+    }
+    for (int word = 0; word < GROUP / 8; ++word) {
+        uint32_t packed = 0;
+        for (int e = 0; e < 8; ++e) {
+            float v = orc_f32_from_bf16(w[word * 8 + e]);
+            v = rintf((v - bias) / scale);
+            v = minf_std(maxf_std(v, 0.0f), NBINS);
+            /* NaN input: both clamps keep NaN; define the code as 0. */
+            const uint32_t code = (v == v) ? (uint32_t)v : 0u;
+            packed |= code << (4 * e);
+        }
+        wq[word] = packed;
+    }
+    *s_out = orc_bf16_from_f32(scale);
+    *b_out = orc_bf16_from_f32(bias);
+}
+
+void orc_quantize_q4g64(const uint16_t* w, int64_t n, int64_t k,
+                        uint32_t* wq, uint16_t* scales, uint16_t* biases) {
+    const int64_t groups = k / GROUP;
+    for (int64_t r = 0; r < n; ++r) {
+        for (int64_t g = 0; g < groups; ++g) {
+            quantize_group(w + r * k + g * GROUP, wq + r * (k / 8) + g * (GROUP / 8),
+                           scales + r * groups + g, biases + r * groups + g);
+        }
+    }
+}
+
+/* Unpack code k of a row: word k/8, bits [4*(k%8), 4*(k%8)+4), low nibble first. */
+static inline uint32_t code_at(const uint32_t* row, int64_t kk) {
+    return (row[kk >> 3] >> (4 * (kk & 7))) & 0xFu;
+}
+
+/*
+ * mx.dequantize(w, s, b, 64, 4, "affine", dtype=bf16) as used by ModelWeights::embed
+ * (native/hyperion_mlx/src/weights_loader.cc:53-69) on gathered rows.
+ */
+void orc_dequantize_q4g64(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                          const uint32_t* rows, int64_t n_rows, int64_t k, int mode,
+                          uint16_t* out) {
+    const int64_t groups = k / GROUP;
+    for (int64_t i = 0; i < n_rows; ++i) {
+        const int64_t r = rows ? (int64_t)rows[i] : i;
+        const uint32_t* wr = wq + r * (k / 8);
+        for (int64_t kk = 0; kk < k; ++kk) {
+            const float s = orc_f32_from_bf16(scales[r * groups + kk / GROUP]);
+            const float b = orc_f32_from_bf16(biases[r * groups + kk / GROUP]);
+            const float q = (float)code_at(wr, kk);
+            float v;
+            if (mode == 0) {
+                v = bf(s * q);
+                v = v + b;
+            } else {
+                v = s * q + b; /* s*q is exact in fp32: 8-bit x 4-bit significands */
+            }
+            out[i * k + kk] = orc_bf16_from_f32(v);
+        }
+    }
+}
+
+/* Ground truth, following the reference's own accuracy definition: dequantize and
+ * multiply with no intermediate rounding (native/hyperion_mlx/tests/weights_test.cc:110-120). */
+void orc_qmatmul_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                     const uint16_t* biases, int64_t m, int64_t n, int64_t k, double* y) {
+    const int64_t groups = k / GROUP;
+    for (int64_t r = 0; r < n; ++r) {
+        const uint32_t* wr = wq + r * (k / 8);
+        for (int64_t i = 0; i < m; ++i) {
+            const uint16_t* xr = x + i * k;
+            double acc = 0.0;
+            for (int64_t g = 0; g < groups; ++g) {
+                const double s = orc_f32_from_bf16(scales[r * groups + g]);
+                const double b = orc_f32_from_bf16(biases[r * groups + g]);
+                for (int64_t j = 0; j < GROUP; ++j) {
+                    const int64_t kk = g * GROUP + j;
+                    acc += (double)orc_f32_from_bf16(xr[kk]) * (s * (double)code_at(wr, kk) + b);
+                }
+            }
+            y[i * n + r] = acc;
+        }
+    }
+}
+
+void orc_qmatmul_deq_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                         const uint16_t* biases, int64_t m, int64_t n, int64_t k, int mode,
+                         double* y) {
+    double* row = (double*)malloc((size_t)k * sizeof(double));
+    uint16_t* deq = (uint16_t*)malloc((size_t)k * sizeof(uint16_t));
+    if (row == NULL || deq == NULL) {
+        free(row);
+        free(deq);
+        return;
+    }
+    for (int64_t r = 0; r < n; ++r) {
+        const uint32_t id = (uint32_t)r;
+        orc_dequantize_q4g64(wq, scales, biases, &id, 1, k, mode, deq);
+        for (int64_t kk = 0; kk < k; ++kk) row[kk] = orc_f32_from_bf16(deq[kk]);
+        for (int64_t i = 0; i < m; ++i) {
+            const uint16_t* xr = x + i * k;
+            double acc = 0.0;
+            for (int64_t kk = 0; kk < k; ++kk) acc += (double)orc_f32_from_bf16(xr[kk]) * row[kk];
+            y[i * n + r] = acc;
+        }
+    }
+    free(row);
+    free(deq);
+}
+
+void orc_qmatmul_f32_grouped(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                             const uint16_t* biases, int64_t m, int64_t n, int64_t k, float* y) {
+    const int64_t groups = k / GROUP;
+    for (int64_t r = 0; r < n; ++r) {
+        const uint32_t* wr = wq + r * (k / 8);
+        for (int64_t i = 0; i < m; ++i) {
+            const uint16_t* xr = x + i * k;
+            float acc = 0.0f;
+            for (int64_t g = 0; g < groups; ++g) {
+                const float s = orc_f32_from_bf16(scales[r * groups + g]);
+                const float b = orc_f32_from_bf16(biases[r * groups + g]);
+                float sxq = 0.0f;
+                float sx = 0.0f;
+                for (int64_t j = 0; j < GROUP; ++j) {
+                    const int64_t kk = g * GROUP + j;
+                    const float xv = orc_f32_from_bf16(xr[kk]);
+                    sxq += xv * (float)code_at(wr, kk);
+                    sx += xv;
+                }
+                acc += s * sxq;
+                acc += b * sx;
+            }
+            y[i * n + r] = acc;
+        }
+    }
+}
+
+/*
+ * MLX CPU quantized_matmul with transpose=true, scalar loop, accumulator of the
+ * input type: sum += x * (scale * q + bias), each op rounded to bf16 as MLX's
+ * bfloat16_t operators do. Parity unpinned (see header).
+ */
+void orc_qmatmul_mlx_cpu_rows(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, int64_t m, int64_t n0, int64_t n1,
+                              int64_t k, uint16_t* y) {
+    const int64_t groups = k / GROUP;
+    const int64_t n_out = n1 - n0;
+    for (int64_t i = 0; i < m; ++i) {
+        const uint16_t* xr = x + i * k;
+        for (int64_t r = n0; r < n1; ++r) {
+            const uint32_t* wr = wq + r * (k / 8);
+            float sum = 0.0f;
+            for (int64_t g = 0; g < groups; ++g) {
+                const float s = orc_f32_from_bf16(scales[r * groups + g]);
+                const float b = orc_f32_from_bf16(biases[r * groups + g]);
+                for (int64_t j = 0; j < GROUP; ++j) {
+                    const int64_t kk = g * GROUP + j;
+                    const float dq = bf(bf(s * (float)code_at(wr, kk)) + b);
+                    sum = bf(sum + bf(orc_f32_from_bf16(xr[kk]) * dq));
+                }
+            }
+            y[i * n_out + (r - n0)] = orc_bf16_from_f32(sum);
+        }
+    }
+}
+
+void orc_qmatmul_mlx_cpu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                         const uint16_t* biases, int64_t m, int64_t n, int64_t k, uint16_t* y) {
+    orc_qmatmul_mlx_cpu_rows(x, wq, scales, biases, m, 0, n, k, y);
+}
+
+/*
+ * gelu_pytorch_tanh as the reference composes it (forward.cc:324-336): each MLX op
+ * produces a bf16 array, constants are bf16 arrays.
+ *   x3    = x * square(x)
+ *   inner = bf16(0.044715) * x3 ; inner = inner + x ; inner = bf16(sqrt(2/pi)) * inner
+ *   out   = (bf16(0.5) * x) * (bf16(1) + tanh(inner))
+ */
+static inline float gelu_chain(float xv) {
+    const float c_coeff = bf(0.044715f);
+    const float c_inner = bf(0.7978845608028654f);
+    const float sq = bf(xv * xv);
+    const float x3 = bf(xv * sq);
+    float inner = bf(c_coeff * x3);
+    inner = bf(inner + xv);
+    inner = bf(c_inner * inner);
+    const float t = bf(tanhf(inner));
+    const float half_x = bf(0.5f * xv);
+    const float one_t = bf(1.0f + t);
+    return bf(half_x * one_t);
+}
+
+void orc_gelu_tanh_bf16(const uint16_t* x, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = orc_bf16_from_f32(gelu_chain(orc_f32_from_bf16(x[i])));
+    }
+}
+
+/* ForwardPass::mlp (forward.cc:338-343): multiply(gelu_tanh(gate), up) in bf16. */
+void orc_gelu_tanh_mul_bf16(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = gelu_chain(orc_f32_from_bf16(gate[i]));
+        out[i] = orc_bf16_from_f32(g * orc_f32_from_bf16(up[i]));
+    }
+}
+
+/* ForwardPass::softcap (forward.cc:154-160): tanh(x / cap) * cap in the logits dtype. */
+void orc_softcap_bf16(const uint16_t* x, int64_t n, float cap, uint16_t* out) {
+    const float c = bf(cap);
+    for (int64_t i = 0; i < n; ++i) {
+        const float d = bf(orc_f32_from_bf16(x[i]) / c);
+        const float t = bf(tanhf(d));
+        out[i] = orc_bf16_from_f32(t * c);
+    }
+}
+
+/* ForwardPass::embed scale (forward.cc:126-131): rows * bf16(sqrt(hidden)). */
+void orc_scale_bf16(const uint16_t* x, int64_t n, float c, uint16_t* out) {
+    const float cb = bf(c);
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = orc_bf16_from_f32(orc_f32_from_bf16(x[i]) * cb);
+    }
+}

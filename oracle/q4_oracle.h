@@ -1,0 +1,111 @@
+/*
+ * CPU oracle for the MLX-affine Q4/g64 quantized-linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: the tests, the smoke
+ * check and the CPU-baseline leg of the benchmark load it to produce expected
+ * values. Nothing on the product path (the HIP library under hyperion_amd/)
+ * links, loads or calls it.
+ *
+ * Every function restates the arithmetic of MLX 0.32.0 (the third-party
+ * library the reference calls; pinned at native/hyperion_mlx/CMakeLists.txt:17,
+ * oracle/pyproject.toml:6-9, commit 7a1d4f5c per
+ * docs/research/0001-m0-vendor-verification.md:8). MLX is not vendored in the
+ * reference, so the restatements follow MLX's published algorithm and are
+ * anchored on the reference's call sites:
+ *   quantize      crates/hyperion-model/fixtures/build_gemma4_unified_tiny.py:54-57
+ *   dequantize    native/hyperion_mlx/src/weights_loader.cc:53-69
+ *   qmatmul       native/hyperion_mlx/src/weights.h:26-37, forward.cc:137-152
+ *   gelu_tanh     native/hyperion_mlx/src/forward.cc:324-343
+ *   softcap       native/hyperion_mlx/src/forward.cc:154-160
+ *   embed scale   native/hyperion_mlx/src/forward.cc:126-131
+ *
+ * Pinning status (what checks each function; see tests/test_oracle.py):
+ *   orc_bf16_from_f32       pinned: numpy float32 -> bfloat16 RNE bit patterns computed
+ *                           independently in the test, plus special values.
+ *   orc_quantize_q4g64      pinned: the reference's tiny fixture (42 Q4 tensors,
+ *                           19,456 groups) - dequant->requant round trip reproduces the
+ *                           fixture's (q, scale, bias) bit-exactly on every group that
+ *                           holds q=15; sign/zero-point invariants on all groups;
+ *                           closed-form cases (exact grids, constant and zero groups).
+ *   orc_dequantize_q4g64    pinned where the value is exact (power-of-two scales, bias
+ *                           grids) and by the fixture round trip; the choice between
+ *                           single and double bf16 rounding is parity unpinned (no
+ *                           committed dequantized values exist in the reference).
+ *   orc_qmatmul_f64         pinned: closed-form known-answer cases and brute force.
+ *   orc_qmatmul_deq_f64     pinned: equals orc_qmatmul_f64 wherever the dequantized
+ *                           weights are exact in bf16, and brute force over
+ *                           orc_dequantize_q4g64 output.
+ *   orc_qmatmul_f32_grouped pinned: exact-arithmetic known-answer cases (every partial
+ *                           sum representable) and against orc_qmatmul_f64.
+ *   orc_qmatmul_mlx_cpu     parity unpinned: restates MLX's scalar CPU loop with
+ *                           bf16-typed accumulation; only an MLX import could pin it.
+ *                           Used only to report the reference-side error.
+ *   orc_gelu_tanh_mul_bf16  pinned against the closed-form fp64 GELU within the
+ *                           rounding the bf16 op chain implies, and special values.
+ *   orc_softcap_bf16        pinned likewise against 30*tanh(x/30) in fp64.
+ */
+#ifndef HYPERION_Q4_ORACLE_H
+#define HYPERION_Q4_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+uint16_t orc_bf16_from_f32(float f);
+float orc_f32_from_bf16(uint16_t h);
+void orc_bf16_from_f32_array(const float* in, int64_t n, uint16_t* out);
+void orc_f32_from_bf16_array(const uint16_t* in, int64_t n, float* out);
+
+/* mx.quantize(w, group_size=64, bits=4, mode="affine") on a bf16 [n, k] matrix. */
+void orc_quantize_q4g64(const uint16_t* w, int64_t n, int64_t k,
+                        uint32_t* wq, uint16_t* scales, uint16_t* biases);
+
+/* mx.dequantize(..., dtype=bfloat16) of rows `rows[0..n_rows)` (rows==NULL: 0..n_rows).
+ * mode 0: bf16(bf16(s*q) + b)  (op-composed, one rounding per MLX op)
+ * mode 1: bf16(s*q + b)        (fp32 math, single rounding to bf16) */
+void orc_dequantize_q4g64(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                          const uint32_t* rows, int64_t n_rows, int64_t k, int mode,
+                          uint16_t* out);
+
+/* Ground truth: y[m,n] = sum_k x[m,k] * (s*q + b), all in fp64. */
+void orc_qmatmul_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                     const uint16_t* biases, int64_t m, int64_t n, int64_t k, double* y);
+
+/* y[m,n] = sum_k x[m,k] * W~[n,k] in fp64, where W~ is the bf16 dequantization of
+ * orc_dequantize_q4g64 in `mode` (the weight values a bf16 MFMA GEMM consumes). */
+void orc_qmatmul_deq_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                         const uint16_t* biases, int64_t m, int64_t n, int64_t k, int mode,
+                         double* y);
+
+/* fp32, per group g: acc += s_g * sum(x*q) + b_g * sum(x), sequential order. */
+void orc_qmatmul_f32_grouped(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                             const uint16_t* biases, int64_t m, int64_t n, int64_t k, float* y);
+
+/* Restatement of MLX's scalar CPU quantized_matmul (transpose=true) with the
+ * accumulator typed as the input dtype (bf16): every multiply/add rounds to bf16. */
+void orc_qmatmul_mlx_cpu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                         const uint16_t* biases, int64_t m, int64_t n, int64_t k, uint16_t* y);
+
+/* Rows [n0, n1) only of orc_qmatmul_mlx_cpu (bounded CPU-baseline samples). */
+void orc_qmatmul_mlx_cpu_rows(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, int64_t m, int64_t n0, int64_t n1,
+                              int64_t k, uint16_t* y);
+
+/* gelu_tanh(gate) * up as the reference's chain of bf16-rounded ops. */
+void orc_gelu_tanh_mul_bf16(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out);
+void orc_gelu_tanh_bf16(const uint16_t* x, int64_t n, uint16_t* out);
+
+/* softcap: bf16(bf16(tanh(bf16(x / cap))) * cap) with cap rounded to bf16. */
+void orc_softcap_bf16(const uint16_t* x, int64_t n, float cap, uint16_t* out);
+
+/* Elementwise bf16 multiply by a bf16 constant (embed scale). */
+void orc_scale_bf16(const uint16_t* x, int64_t n, float c, uint16_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

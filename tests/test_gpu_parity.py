@@ -1,0 +1,340 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Bars (stated per test):
+  * quantize / dequantize: bit-exact (integer and bf16-bit work);
+  * qmatmul: within 1 bf16 ulp of the bf16-rounded fp64 reference (the GEMV against
+    exact dequantization, the MFMA GEMM against its bf16 weights), and
+    sig_rel = max|d|/max|ref| <= 1e-2 against the fp64 ground truth;
+  * exact-arithmetic inputs (x in {-1,0,1}, scale 2^-7): bit-exact;
+  * fused gelu/softcap epilogues: bit-exact against the oracle applied to the
+    kernel's own matmul outputs, allowing a 1-ulp difference on at most 0.1% of
+    elements where device tanhf and glibc tanhf round differently.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import hyperion_amd as hy
+import oracle as O
+import st_reader
+from hyperion_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def ulp_diff(a_bits, b_bits):
+    """Distance in bf16 ulps between two bf16 bit arrays (same sign assumed near 0)."""
+    def key(h):
+        h = h.astype(np.int32)
+        return np.where(h & 0x8000, -(h & 0x7FFF), h)
+    return np.abs(key(a_bits) - key(b_bits))
+
+
+def dev(a, stream):
+    return hy.DeviceArray.from_host(a, stream)
+
+
+def run_qmatmul(w, s, b, x, stream, softcap=None):
+    qw = hy.QWeight.from_host(w, s, b)
+    m, k = x.shape
+    n = w.shape[0]
+    xd = dev(x, stream)
+    yd = hy.DeviceArray((m, n), np.uint16)
+    hy.qmatmul(qw, xd, m, yd, stream, softcap=softcap)
+    y = yd.to_host(stream)
+    qw.close()
+    return y
+
+
+def test_runtime_is_gfx950():
+    info = hy.runtime_info()
+    say(f"device {info.device_name.decode()} arch {info.arch_name.decode()} CUs {info.compute_units} "
+        f"HBM {info.hbm_bytes / 2**30:.0f} GiB")
+    assert info.arch_name.decode().startswith("gfx950")
+    assert info.abi_version == 1
+
+
+# ---------------------------------------------------------------- quantize / dequantize
+
+def _gpu_quantize(wbf, stream):
+    n, k = wbf.shape
+    wd = dev(wbf, stream)
+    wq = hy.DeviceArray((n, k // 8), np.uint32)
+    sd = hy.DeviceArray((n, k // 64), np.uint16)
+    bd = hy.DeviceArray((n, k // 64), np.uint16)
+    hy.quantize(wd, n, k, wq, sd, bd, stream)
+    return wq.to_host(stream), sd.to_host(stream), bd.to_host(stream)
+
+
+def test_quantize_pack_config_bit_exact(stream):
+    """Quantize/pack workload: bf16 [15360, 3840] N(0, 0.02^2) with 1% x8 outliers."""
+    n, k = 15360, 3840
+    say(f"quantize n={n} k={k}")
+    wbf = syn.quantize_input(n, k, seed=101)
+    got = _gpu_quantize(wbf, stream)
+    ref = O.quantize(wbf)
+    for g, r, name in zip(got, ref, ("packed", "scales", "biases")):
+        bad = np.count_nonzero(g != r)
+        assert bad == 0, f"{name}: {bad} mismatches"
+
+
+def test_quantize_reproduces_reference_fixture(stream, fixture_dir):
+    """GPU requantization of the fixture's dequantized weights returns MLX's own
+    (codes, scale, bias) on every group holding code 15, and equals the oracle on all."""
+    total = exact = 0
+    for name, (w, s, b) in st_reader.q4_tensors(fixture_dir).items():
+        wd = O.dequantize(w, s, b, mode=0)
+        gw, gs, gb = _gpu_quantize(wd, stream)
+        ow, os_, ob = O.quantize(wd)
+        assert np.array_equal(gw, ow) and np.array_equal(gs, os_) and np.array_equal(gb, ob), name
+        codes = syn.unpack_codes(w).reshape(w.shape[0], -1, 64)
+        gcodes = syn.unpack_codes(gw).reshape(w.shape[0], -1, 64)
+        has15 = (codes == 15).any(-1)
+        same = (codes == gcodes).all(-1) & (s == gs) & (b == gb)
+        total += int(has15.sum())
+        exact += int((same & has15).sum())
+    assert total == 16578 and exact == total
+
+
+def test_quantize_edge_groups(stream):
+    """Zero, constant, negative-only, tie-heavy, huge/tiny-magnitude and subnormal groups."""
+    rng = np.random.default_rng(5)
+    groups = []
+    c = np.tile(np.arange(16), 4).astype(np.float64)
+    groups.append(np.zeros(64))
+    groups.append(np.full(64, 0.01))
+    groups.append(np.full(64, -0.25))
+    groups.append((c - 8) * 2.0**-7)
+    half = c.copy(); half[::3] += 0.5
+    groups.append((half - 8) * 2.0**-7)                    # exact .5 quotients
+    groups.append(-np.abs(rng.standard_normal(64)) * 0.01)  # all negative
+    groups.append(np.abs(rng.standard_normal(64)) * 0.01)   # all positive
+    g = rng.standard_normal(64); g[7] = -g.max()            # |min| == |max|
+    groups.append(g)
+    groups.append(rng.standard_normal(64) * 1e30)
+    groups.append(rng.standard_normal(64) * 1e-30)
+    groups.append(rng.standard_normal(64) * 1e-39)          # bf16 subnormals
+    for _ in range(53):
+        groups.append(rng.standard_normal(64) * 10.0 ** rng.uniform(-4, 2))
+    w = syn.bf16_bits(np.stack(groups).astype(np.float32).reshape(8, -1))
+    got = _gpu_quantize(w, stream)
+    ref = O.quantize(w)
+    for gv, rv, name in zip(got, ref, ("packed", "scales", "biases")):
+        assert np.array_equal(gv, rv), name
+
+
+def test_dequantize_table_bit_exact(stream):
+    n, k = 15360, 3840
+    say(f"dequantize n={n} k={k}")
+    w, s, b = syn.q4_weights(n, k, seed=102)
+    wd, sd, bd = dev(w, stream), dev(s, stream), dev(b, stream)
+    out = hy.DeviceArray((n, k), np.uint16)
+    hy.dequantize(wd, sd, bd, n, k, None, n, out, stream)
+    got = out.to_host(stream)
+    ref = O.dequantize(w, s, b, mode=0)
+    assert np.count_nonzero(got != ref) == 0
+
+
+def test_dequantize_gather_scale_and_out_of_range(stream):
+    n, k = 1000, 512
+    w, s, b = syn.q4_weights(n, k, seed=103)
+    ids = np.array([5, 999, 0, 5, 1000, 123456, 77], np.uint32)
+    wd, sd, bd = dev(w, stream), dev(s, stream), dev(b, stream)
+    idd = dev(ids, stream)
+    out = hy.DeviceArray((ids.size, k), np.uint16)
+    hy.dequantize(wd, sd, bd, n, k, idd, ids.size, out, stream, out_scale=float(np.sqrt(k)))
+    got = out.to_host(stream)
+    valid = ids < n
+    ref = O.scale(O.dequantize(w, s, b, rows=ids[valid], mode=0), float(np.sqrt(np.float32(k))))
+    np.testing.assert_array_equal(got[valid], ref)
+    assert np.all(got[~valid] == 0)
+
+
+# ---------------------------------------------------------------- decode GEMV
+
+def test_gemv_decode_config(stream):
+    """Decode GEMV: x [1,3840] N(0,1), W [15360,3840] Q4/g64 (scale |N|*0.02/7.5, bias -8*scale)."""
+    n, k = 15360, 3840
+    say(f"gemv m=1 n={n} k={k}")
+    x = syn.activations(1, k, seed=104)
+    w, s, b = syn.q4_weights(n, k, seed=105)
+    y = run_qmatmul(w, s, b, x, stream)
+    truth = O.qmatmul_f64(x, w, s, b)
+    rel = syn.sig_rel(syn.bf16_to_f32(y), truth)
+    mlx_rows = 2048
+    mlx = syn.bf16_to_f32(O.qmatmul_mlx_cpu(x, w, s, b, rows=(0, mlx_rows)))
+    ref_rel = syn.sig_rel(mlx, truth[:, :mlx_rows])
+    say(f"  sig_rel gpu={rel:.3e}  mlx-cpu restatement={ref_rel:.3e} (first {mlx_rows} rows)")
+    assert rel <= 1e-2
+    assert np.max(ulp_diff(y, syn.bf16_bits(truth.astype(np.float32)))) <= 1
+
+
+def test_gemv_exact_integer_inputs(stream):
+    rng = np.random.default_rng(7)
+    for m, n, k in ((1, 512, 3840), (4, 300, 4096), (3, 64, 15360), (2, 33, 128)):
+        x = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+        codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+        w = syn.pack_codes(codes)
+        s = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+        b = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+        exact = (x.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
+        y = run_qmatmul(w, s, b, syn.bf16_bits(x), stream)
+        np.testing.assert_array_equal(y, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"{m}x{n}x{k}")
+
+
+def test_gemv_one_hot_pins_layout(stream):
+    n, k = 96, 4096
+    w, s, b = syn.q4_weights(n, k, seed=106)
+    deq = O.dequantize(w, s, b, mode=1)
+    for j in (0, 1, 7, 8, 31, 32, 63, 64, 2047, 2048, 4095):
+        x = np.zeros((1, k), np.float32)
+        x[0, j] = 1.0
+        y = run_qmatmul(w, s, b, syn.bf16_bits(x), stream)
+        np.testing.assert_array_equal(y[0], deq[:, j], err_msg=f"column {j}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_gemv_layer_projections(stream, m):
+    """The decoder-layer projection set at decode batch m (split-K path for down)."""
+    for i, (name, (n, k)) in enumerate(syn.LAYER_SHAPES.items()):
+        say(f"gemv m={m} {name} n={n} k={k}")
+        x = syn.activations(m, k, seed=200 + i)
+        w, s, b = syn.q4_weights(n, k, seed=300 + i)
+        y = run_qmatmul(w, s, b, x, stream)
+        truth = O.qmatmul_f64(x, w, s, b)
+        assert syn.sig_rel(syn.bf16_to_f32(y), truth) <= 1e-2, name
+        assert np.max(ulp_diff(y, syn.bf16_bits(truth.astype(np.float32)))) <= 1, name
+
+
+# ---------------------------------------------------------------- prefill GEMM
+
+@pytest.mark.parametrize("m", [512, 2048])
+def test_gemm_prefill_projections_sampled(stream, m):
+    """Prefill GEMM for the seven projections; output rows are checked on a sample of
+    16 rows per projection (the fp64 oracle over all rows would take minutes)."""
+    rng = np.random.default_rng(m)
+    for i, (name, (n, k)) in enumerate(syn.LAYER_SHAPES.items()):
+        say(f"gemm m={m} {name} n={n} k={k}")
+        x = syn.activations(m, k, seed=400 + i)
+        w, s, b = syn.q4_weights(n, k, seed=500 + i)
+        y = run_qmatmul(w, s, b, x, stream)
+        rows = np.sort(rng.choice(m, size=16, replace=False))
+        rows[0], rows[-1] = 0, m - 1
+        xs = x[rows]
+        ref_bf16w = O.qmatmul_deq_f64(xs, w, s, b, mode=1)
+        truth = O.qmatmul_f64(xs, w, s, b)
+        assert syn.sig_rel(syn.bf16_to_f32(y[rows]), truth) <= 1e-2, name
+        assert np.max(ulp_diff(y[rows], syn.bf16_bits(ref_bf16w.astype(np.float32)))) <= 1, name
+
+
+def test_gemm_exact_integer_and_ragged_tiles(stream):
+    rng = np.random.default_rng(8)
+    for m, n, k in ((300, 200, 512), (257, 33, 64), (5, 1000, 3840), (2048, 40, 128)):
+        say(f"gemm exact m={m} n={n} k={k}")
+        x = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+        codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+        w = syn.pack_codes(codes)
+        s = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+        b = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+        exact = (x.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
+        y = run_qmatmul(w, s, b, syn.bf16_bits(x), stream)
+        np.testing.assert_array_equal(y, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"{m}x{n}x{k}")
+
+
+# ---------------------------------------------------------------- fused epilogues
+
+def _assert_close_bits(got, ref, what):
+    d = ulp_diff(got, ref)
+    assert d.max() <= 1, what
+    assert np.count_nonzero(d) <= max(1, d.size // 1000), what
+
+
+@pytest.mark.parametrize("m", [1, 4, 300])
+def test_gate_up_gelu_fused(stream, m):
+    n, k = 15360, 3840
+    say(f"gate/up gelu m={m}")
+    x = syn.activations(m, k, seed=600 + m)
+    gw, gs, gb = syn.q4_weights(n, k, seed=601)
+    uw, us, ub = syn.q4_weights(n, k, seed=602)
+    gate = hy.QWeight.from_host(gw, gs, gb)
+    up = hy.QWeight.from_host(uw, us, ub)
+    xd = dev(x, stream)
+    g = hy.DeviceArray((m, n), np.uint16)
+    u = hy.DeviceArray((m, n), np.uint16)
+    h = hy.DeviceArray((m, n), np.uint16)
+    hy.qmatmul(gate, xd, m, g, stream)
+    hy.qmatmul(up, xd, m, u, stream)
+    hy.qmlp_gate_up_gelu(gate, up, xd, m, h, stream)
+    _assert_close_bits(h.to_host(stream), O.gelu_tanh_mul(g.to_host(stream), u.to_host(stream)), f"m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 300])
+def test_lm_head_softcap(stream, m):
+    n, k = 32768, 3840
+    say(f"lm head softcap m={m}")
+    x = syn.activations(m, k, seed=700 + m)
+    w, s, b = syn.q4_weights(n, k, seed=701)
+    s = syn.bf16_bits(syn.bf16_to_f32(s) * np.float32(64.0))       # logits of magnitude ~30+
+    b = syn.bf16_bits(syn.bf16_to_f32(b) * np.float32(64.0))
+    plain = run_qmatmul(w, s, b, x, stream)
+    capped = run_qmatmul(w, s, b, x, stream, softcap=30.0)
+    assert np.max(np.abs(syn.bf16_to_f32(plain))) > 30.0
+    _assert_close_bits(capped, O.softcap(plain, 30.0), f"m={m}")
+
+
+# ---------------------------------------------------------------- residency (tiny artifact)
+
+def test_qmodel_fixture_reference_weights_test(stream, fixture_dir):
+    """weights_test.cc:101-139 on every projection of the reference's tiny artifact:
+    x = 0.1 (M=4, and M=300 for the GEMM path) against dequantize+matmul at
+    allclose(rtol=1e-3, atol=1e-2)."""
+    model = hy.QModel(fixture_dir)
+    tensors = st_reader.q4_tensors(fixture_dir)
+    assert model.num_layers == 6
+    with pytest.raises(hy.HypError) as err:
+        model.linear(5, "v")
+    assert err.value.status_name == "NOT_FOUND"
+    for layer in range(6):
+        for proj in ("q", "k", "v", "o", "gate", "up", "down"):
+            if layer == 5 and proj == "v":
+                continue
+            sect = "mlp" if proj in ("gate", "up", "down") else "self_attn"
+            w, s, b = tensors[f"language_model.model.layers.{layer}.{sect}.{proj}_proj"]
+            qw = model.linear(layer, proj)
+            n, k = qw.shape
+            assert (n, k) == (w.shape[0], w.shape[1] * 8)
+            ew, es, eb = qw.export()
+            assert np.array_equal(ew, w) and np.array_equal(es, s) and np.array_equal(eb, b)
+            for m in (4, 300):
+                x = syn.bf16_bits(np.full((m, k), 0.1, np.float32))
+                xd = dev(x, stream)
+                yd = hy.DeviceArray((m, n), np.uint16)
+                hy.qmatmul(qw, xd, m, yd, stream)
+                ref = syn.bf16_to_f32(x) @ syn.bf16_to_f32(O.dequantize(w, s, b, mode=1)).T
+                np.testing.assert_allclose(syn.bf16_to_f32(yd.to_host(stream)), ref, rtol=1e-3, atol=1e-2)
+    emb = model.embed()
+    ids = np.array([0, 5, 127, 64], np.uint32)
+    out = hy.DeviceArray((ids.size, 128), np.uint16)
+    hy.embed(emb, dev(ids, stream), ids.size, out, stream)
+    w, s, b = tensors["language_model.model.embed_tokens"]
+    ref = O.scale(O.dequantize(w, s, b, rows=ids, mode=0), float(np.sqrt(np.float32(128))))
+    np.testing.assert_array_equal(out.to_host(stream), ref)
+    with pytest.raises(hy.HypError):
+        hy.call("hyp_qweight_free", __import__("ctypes").byref(emb.handle))
+    model.close()
+
+
+def test_zero_rows_is_a_noop(stream):
+    w, s, b = syn.q4_weights(64, 128, seed=9)
+    qw = hy.QWeight.from_host(w, s, b)
+    y = hy.DeviceArray((1, 64), np.uint16)
+    y.fill_zero(stream)
+    hy.qmatmul(qw, y, 0, y, stream)
+    stream.synchronize()
+    assert np.all(y.to_host(stream) == 0)

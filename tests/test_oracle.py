@@ -1,0 +1,340 @@
+"""Pins for the CPU oracle (oracle/q4_oracle.c) - no GPU.
+
+Each function of the oracle is checked against something it did not compute itself:
+the reference's committed Q4 fixture (real mx.quantize output), exact rational
+arithmetic, closed forms and brute force. See oracle/q4_oracle.h for the map.
+"""
+from fractions import Fraction
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+import st_reader
+from hyperion_amd import synthetic as syn
+
+
+def rne_bf16(value) -> float:
+    """Round a finite rational to the nearest bf16 value, ties to even (exact arithmetic)."""
+    fr = Fraction(value)
+    if fr == 0:
+        return 0.0
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = math.floor(math.log2(a))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)                      # subnormal spacing below the normal range
+    ulp = Fraction(2) ** (e - 7)
+    q = round(a / ulp)                    # Fraction.__round__ is half-to-even
+    return sign * float(q * ulp)
+
+
+def bits_of(x: float) -> int:
+    return int(np.array([x], np.float32).view(np.uint32)[0] >> 16)
+
+
+# ---------------------------------------------------------------- bf16 conversion
+
+def test_bf16_rne_matches_exact_rounding():
+    rng = np.random.default_rng(1)
+    u = rng.integers(0, 2**32, size=20000, dtype=np.uint64).astype(np.uint32)
+    f = u.view(np.float32)
+    f = f[np.isfinite(f) & (np.abs(f) < np.float32(3.3e38))]
+    got = O.bf16_from_f32(f)
+    for x, g in zip(f[:4000], got[:4000]):
+        assert g == bits_of(rne_bf16(float(x))) or (rne_bf16(float(x)) == 0.0 and g in (0, 0x8000))
+    # the numpy path used by the benchmark's data generator agrees everywhere
+    np.testing.assert_array_equal(got, syn.bf16_bits(f))
+
+
+def test_bf16_special_values():
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, 1.0, -2.5, 3.3895314e38], np.float32)
+    got = O.bf16_from_f32(specials)
+    assert list(got[:6]) == [0x0000, 0x8000, 0x7F80, 0xFF80, 0x3F80, 0xC020]
+    assert got[6] == 0x7F7F                          # largest finite bf16 stays finite
+    # exact ties: 1 + 2^-8 sits halfway between 1 and 1 + 2^-7 -> even (1.0)
+    tie_lo = np.array([1.0 + 2.0**-8], np.float32)
+    tie_hi = np.array([1.0 + 3 * 2.0**-8], np.float32)   # halfway to an even mantissa above
+    assert O.bf16_from_f32(tie_lo)[0] == 0x3F80
+    assert O.bf16_from_f32(tie_hi)[0] == 0x3F82
+    nan = O.bf16_from_f32(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7F80) == 0x7F80 and (nan & 0x7F) != 0
+
+
+def test_bf16_matches_torch_if_present():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(2)
+    f = (rng.standard_normal(50000) * 10.0 ** rng.integers(-30, 30, 50000)).astype(np.float32)
+    ref = torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(O.bf16_from_f32(f), ref)
+
+
+# ---------------------------------------------------------------- quantize
+
+@pytest.fixture(scope="module")
+def fixture_q4(fixture_dir):
+    return st_reader.q4_tensors(fixture_dir)
+
+
+def test_fixture_layout(fixture_q4):
+    # 42 Q4 projections, 19,456 groups of 64 (the reference's tiny artifact)
+    assert len(fixture_q4) == 42
+    assert sum(s.size for _, s, _ in fixture_q4.values()) == 19456
+    w, s, b = fixture_q4["language_model.model.layers.0.self_attn.q_proj"]
+    assert w.shape == (256, 16) and s.shape == (256, 2) and b.shape == (256, 2)
+
+
+def test_fixture_zero_point_invariants(fixture_q4):
+    """mx.quantize's edge rule: sign(scale) = -sign(bias); code 0 in every group."""
+    for name, (w, s, b) in fixture_q4.items():
+        sf = syn.bf16_to_f32(s)
+        bf = syn.bf16_to_f32(b)
+        assert np.all(np.sign(sf) == -np.sign(bf)), name
+        codes = syn.unpack_codes(w).reshape(w.shape[0], -1, 64)
+        assert np.all((codes == 0).any(-1)), name
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_quantize_reproduces_fixture(fixture_q4, mode):
+    """dequantize -> requantize returns MLX's own (codes, scale, bias) bit-exactly on
+    every group whose codes reach 15 (16,578 of 19,456 groups)."""
+    total = exact = 0
+    for name, (w, s, b) in fixture_q4.items():
+        wd = O.dequantize(w, s, b, mode=mode)
+        w2, s2, b2 = O.quantize(wd)
+        codes = syn.unpack_codes(w).reshape(w.shape[0], -1, 64)
+        codes2 = syn.unpack_codes(w2).reshape(w.shape[0], -1, 64)
+        same = (codes == codes2).all(-1) & (s == s2) & (b == b2)
+        has15 = (codes == 15).any(-1)
+        total += int(has15.sum())
+        exact += int((same & has15).sum())
+    assert total == 16578
+    assert exact == total
+
+
+def test_quantize_exact_grid():
+    """Values on a 2^-7 grid spanning codes 0..15 with the negative extreme larger."""
+    c = np.tile(np.arange(16), 4)
+    w = ((c - 8) * 2.0**-7).astype(np.float32)[None, :]
+    wq, s, b = O.quantize(syn.bf16_bits(w))
+    assert syn.bf16_to_f32(s)[0, 0] == 2.0**-7
+    assert syn.bf16_to_f32(b)[0, 0] == -(2.0**-4)
+    np.testing.assert_array_equal(syn.unpack_codes(wq)[0], c)
+
+
+def test_quantize_rounds_half_to_even():
+    """(w - b)/s = 2.5 exactly must give code 2 (rint), not 3 (round half away)."""
+    c = np.tile(np.arange(16), 4).astype(np.float64)
+    c[5] = 2.5
+    w = ((c - 8) * 2.0**-7).astype(np.float32)[None, :]
+    wq, s, b = O.quantize(syn.bf16_bits(w))
+    assert syn.bf16_to_f32(s)[0, 0] == 2.0**-7
+    assert syn.unpack_codes(wq)[0, 5] == 2
+
+
+def test_quantize_positive_extreme_uses_negative_scale():
+    """|max| >= |min| puts the edge at the max: scale < 0 and bias = max."""
+    vals = np.linspace(-0.05, 0.0625, 64).astype(np.float32)
+    vals[-1] = 0.0625
+    wq, s, b = O.quantize(syn.bf16_bits(vals[None, :]))
+    assert syn.bf16_to_f32(s)[0, 0] < 0
+    assert syn.bf16_to_f32(b)[0, 0] == syn.bf16_to_f32(syn.bf16_bits(np.float32(0.0625)))
+    assert syn.unpack_codes(wq)[0, -1] == 0          # the edge itself is code 0
+    # a tie |min| == |max| also takes the max as the edge
+    vals = np.zeros(64, np.float32)
+    vals[0], vals[1] = -0.5, 0.5
+    _, s2, b2 = O.quantize(syn.bf16_bits(vals[None, :]))
+    assert syn.bf16_to_f32(s2)[0, 0] < 0 and syn.bf16_to_f32(b2)[0, 0] == 0.5
+
+
+def test_quantize_constant_groups():
+    zero = np.zeros((1, 64), np.uint16)
+    wq, s, b = O.quantize(zero)
+    assert np.all(wq == 0) and b[0, 0] == 0
+    assert s[0, 0] == syn.bf16_bits(np.float32(-1e-7))   # eps with the sign of the max edge
+    const = syn.bf16_bits(np.full((1, 64), 0.01, np.float32))
+    wq, s, b = O.quantize(const)
+    assert np.all(wq == 0) and b[0, 0] == const[0, 0]     # reconstructs exactly as the bias
+    neg = syn.bf16_bits(np.full((1, 64), -0.25, np.float32))
+    wq, s, b = O.quantize(neg)
+    assert np.all(syn.unpack_codes(wq) == 0) and syn.bf16_to_f32(b)[0, 0] == -0.25
+
+
+def test_quantize_error_bound_random():
+    """Every interior code (1..14) reconstructs within half a step plus the bf16 rounding
+    of scale and bias. Codes 0 and 15 are excluded: the edge rule re-derives the scale
+    from the larger-magnitude extreme, so the far extreme may clip at 15."""
+    w = syn.quantize_input(64, 256, seed=3)
+    wq, s, b = O.quantize(w)
+    codes = syn.unpack_codes(wq).astype(np.float64).reshape(64, 4, 64)
+    sf = syn.bf16_to_f32(s).astype(np.float64)[..., None]
+    bf = syn.bf16_to_f32(b).astype(np.float64)[..., None]
+    x = syn.bf16_to_f32(w).astype(np.float64).reshape(64, 4, 64)
+    err = np.abs(codes * sf + bf - x)
+    bound = 0.5 * np.abs(sf) + 16 * np.abs(sf) * 2.0**-8 + np.abs(bf) * 2.0**-8
+    interior = (codes > 0) & (codes < 15)
+    assert interior.mean() > 0.8
+    assert np.all(err[interior] <= np.broadcast_to(bound, err.shape)[interior])
+
+
+# ---------------------------------------------------------------- dequantize
+
+def test_dequantize_modes_match_exact_arithmetic():
+    rng = np.random.default_rng(4)
+    n, k = 8, 128
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    s = syn.bf16_bits(rng.standard_normal((n, k // 64)).astype(np.float32) * np.float32(0.01))
+    b = syn.bf16_bits(rng.standard_normal((n, k // 64)).astype(np.float32) * np.float32(0.05))
+    codes = syn.unpack_codes(w)
+    for mode in (0, 1):
+        got = O.dequantize(w, s, b, mode=mode)
+        for r in range(n):
+            for c in range(0, k, 7):
+                sv = np.float32(syn.bf16_to_f32(s)[r, c // 64])
+                bv = np.float32(syn.bf16_to_f32(b)[r, c // 64])
+                q = np.float32(codes[r, c])
+                prod = sv * q                              # exact in fp32
+                if mode == 0:
+                    v = np.float32(rne_bf16(float(prod))) + bv
+                else:
+                    v = prod + bv
+                assert got[r, c] == bits_of(rne_bf16(float(v))), (mode, r, c)
+
+
+def test_dequantize_row_gather_and_exact_grid():
+    c = np.tile(np.arange(16), 4)
+    w = syn.pack_codes(np.stack([c, c[::-1]]).astype(np.uint8))
+    s = syn.bf16_bits(np.full((2, 1), 2.0**-7, np.float32))
+    b = syn.bf16_bits(np.full((2, 1), -(2.0**-4), np.float32))
+    out = O.dequantize(w, s, b, rows=np.array([1, 0, 1], np.uint32))
+    expect = ((np.stack([c[::-1], c, c[::-1]]) - 8) * 2.0**-7).astype(np.float32)
+    np.testing.assert_array_equal(syn.bf16_to_f32(out), expect)
+
+
+# ---------------------------------------------------------------- qmatmul
+
+def _rand_q4(n, k, seed):
+    return syn.q4_weights(n, k, seed)
+
+
+def test_qmatmul_one_hot_pins_nibble_order():
+    n, k = 16, 256
+    w, s, b = _rand_q4(n, k, 5)
+    codes = syn.unpack_codes(w)
+    sf, bf = syn.bf16_to_f32(s), syn.bf16_to_f32(b)
+    for j in (0, 1, 7, 8, 63, 64, 130, 255):
+        x = np.zeros((1, k), np.float32)
+        x[0, j] = 1.0
+        xb = syn.bf16_bits(x)
+        expect = sf[:, j // 64].astype(np.float64) * codes[:, j] + bf[:, j // 64]
+        np.testing.assert_array_equal(O.qmatmul_f64(xb, w, s, b)[0], expect)
+        np.testing.assert_array_equal(O.qmatmul_f32_grouped(xb, w, s, b)[0], expect.astype(np.float32))
+        deq = O.dequantize(w, s, b)[:, j]
+        np.testing.assert_array_equal(O.qmatmul_mlx_cpu(xb, w, s, b)[0], deq)
+
+
+def test_qmatmul_exact_integer_case():
+    """x in {-1,0,1}, scale 2^-7, bias -8*scale: every partial sum is exact in fp32."""
+    rng = np.random.default_rng(6)
+    m, n, k = 3, 40, 3840
+    x = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+    codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+    w = syn.pack_codes(codes)
+    s = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+    b = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+    exact = (x.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
+    xb = syn.bf16_bits(x)
+    np.testing.assert_array_equal(O.qmatmul_f64(xb, w, s, b), exact)
+    np.testing.assert_array_equal(O.qmatmul_f32_grouped(xb, w, s, b), exact.astype(np.float32))
+
+
+def test_qmatmul_brute_force_small():
+    rng = np.random.default_rng(7)
+    m, n, k = 3, 5, 192
+    x = syn.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    w, s, b = _rand_q4(n, k, 8)
+    codes = syn.unpack_codes(w).astype(np.float64)
+    sf = np.repeat(syn.bf16_to_f32(s).astype(np.float64), 64, axis=1)
+    bf = np.repeat(syn.bf16_to_f32(b).astype(np.float64), 64, axis=1)
+    ref = syn.bf16_to_f32(x).astype(np.float64) @ (codes * sf + bf).T
+    np.testing.assert_allclose(O.qmatmul_f64(x, w, s, b), ref, rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(O.qmatmul_f32_grouped(x, w, s, b), ref, rtol=1e-4, atol=1e-6)
+
+
+def test_qmatmul_reference_weights_test_on_fixture(fixture_q4):
+    """native/hyperion_mlx/tests/weights_test.cc:101-139 on the tiny artifact's q_proj:
+    x = 0.1 (M=4) against dequantize(f32)+matmul at allclose(rtol=1e-3, atol=1e-2)."""
+    w, s, b = fixture_q4["language_model.model.layers.0.self_attn.q_proj"]
+    k = s.shape[1] * 64
+    x = syn.bf16_bits(np.full((4, k), 0.1, np.float32))
+    wd = O.dequantize(w, s, b, mode=1)
+    ref = syn.bf16_to_f32(x) @ syn.bf16_to_f32(wd).T
+    got = O.qmatmul_f32_grouped(x, w, s, b)
+    np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-2)
+
+
+def test_mlx_cpu_restatement_accumulates_in_bf16():
+    """The MLX CPU restatement (parity unpinned) keeps a bf16 running sum, which the
+    mathematics of bf16 fixes on this input: adding 1.0 to a bf16 sum stalls at 256,
+    because 256 + 1 rounds back to 256 (ties to even)."""
+    k = 3840
+    x = syn.bf16_bits(np.ones((1, k), np.float32))
+    w = syn.pack_codes(np.ones((1, k), np.uint8))
+    s = syn.bf16_bits(np.ones((1, k // 64), np.float32))
+    b = np.zeros((1, k // 64), np.uint16)
+    assert syn.bf16_to_f32(O.qmatmul_mlx_cpu(x, w, s, b))[0, 0] == 256.0
+    assert O.qmatmul_f64(x, w, s, b)[0, 0] == float(k)
+    # on the decode workload its error against the fp64 truth is large (reported
+    # beside the GPU result as the reference-side error), fp32 grouped is tiny
+    x = syn.activations(1, k, seed=9)
+    w, s, b = _rand_q4(64, k, 10)
+    truth = O.qmatmul_f64(x, w, s, b)
+    mlx = syn.bf16_to_f32(O.qmatmul_mlx_cpu(x, w, s, b))
+    assert 1e-3 < syn.sig_rel(mlx, truth) < 0.5
+    assert syn.sig_rel(O.qmatmul_f32_grouped(x, w, s, b), truth) < 1e-5
+
+
+# ---------------------------------------------------------------- gelu / softcap
+
+def test_gelu_chain_constants_and_accuracy():
+    assert O.scale(syn.bf16_bits(np.float32(1.0)), 0.044715) == syn.bf16_bits(np.float32(0.044677734375))
+    assert O.scale(syn.bf16_bits(np.float32(1.0)), 0.7978845608) == syn.bf16_bits(np.float32(0.796875))
+    xs = np.linspace(-6, 6, 2001).astype(np.float32)
+    xb = syn.bf16_bits(xs)
+    xf = syn.bf16_to_f32(xb).astype(np.float64)
+    got = syn.bf16_to_f32(O.gelu_tanh(xb)).astype(np.float64)
+    ref = 0.5 * xf * (1 + np.tanh(math.sqrt(2 / math.pi) * (xf + 0.044715 * xf**3)))
+    assert np.max(np.abs(got - ref)) < 0.05
+    assert O.gelu_tanh(syn.bf16_bits(np.float32(0.0)))[0] == 0
+    big = syn.bf16_bits(np.float32(20.0))
+    assert O.gelu_tanh(big)[0] == big[0]
+    up = syn.bf16_bits(np.full(xs.shape, 2.0, np.float32))
+    np.testing.assert_array_equal(O.gelu_tanh_mul(xb, up), O.scale(O.gelu_tanh(xb), 2.0))
+
+
+def test_softcap_accuracy():
+    xs = np.linspace(-200, 200, 4001).astype(np.float32)
+    xb = syn.bf16_bits(xs)
+    got = syn.bf16_to_f32(O.softcap(xb, 30.0)).astype(np.float64)
+    ref = 30.0 * np.tanh(syn.bf16_to_f32(xb).astype(np.float64) / 30.0)
+    assert np.max(np.abs(got - ref)) <= 0.25       # a few bf16 ulps at |y| ~ 30
+    assert np.all(np.abs(got) <= 30.0)
+
+
+def test_qmatmul_deq_f64_against_dequantize_and_truth():
+    rng = np.random.default_rng(11)
+    m, n, k = 2, 7, 256
+    x = syn.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    w, s, b = _rand_q4(n, k, 12)
+    for mode in (0, 1):
+        deq = syn.bf16_to_f32(O.dequantize(w, s, b, mode=mode)).astype(np.float64)
+        ref = syn.bf16_to_f32(x).astype(np.float64) @ deq.T
+        np.testing.assert_allclose(O.qmatmul_deq_f64(x, w, s, b, mode=mode), ref, rtol=1e-12, atol=1e-14)
+    # exact bf16 weights (2^-7 grid): identical to the undequantized truth
+    s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+    b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+    np.testing.assert_array_equal(O.qmatmul_deq_f64(x, w, s2, b2, mode=0), O.qmatmul_f64(x, w, s2, b2))
