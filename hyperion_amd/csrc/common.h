@@ -43,6 +43,9 @@ class NativeError : public std::runtime_error {
         }                                                                      \
     } while (0)
 
+// Compute units of the current device (queried once per device, then cached).
+uint32_t device_compute_units();
+
 constexpr uint32_t kGroupSize = 64;   // the locked quantization: group 64,
 constexpr uint32_t kBits = 4;         // 4 bits, affine (model.cc:73-74)
 

@@ -21,7 +21,6 @@ struct Q4Matrix {
 enum class Epilogue : int {
     kNone = 0,
     kSoftcap = 1,   // y = softcap(bf16(acc)), forward.cc:154-160
-    kGeluMul = 2,   // y = bf16(gelu_chain(y_in) * bf16(acc)), forward.cc:338-343
 };
 
 // Largest m the decode GEMV handles; larger m goes to the MFMA GEMM.
@@ -35,9 +34,13 @@ void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, ui
                     uint16_t* y, Epilogue epi, float cap_bf16, hipStream_t stream);
 
 // Prefill GEMM on bf16 MFMA: Q4 tiles dequantized in registers, x tiles in LDS.
-// kGeluMul reads y as the gate result and overwrites it.
-void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y,
-                    Epilogue epi, float cap_bf16, hipStream_t stream);
+// Plain bf16 output; epilogues for m > kGemvMaxM run as the elementwise kernels below.
+void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
+
+// h = bf16(gelu_chain(h) * u) over `count` bf16 elements (in place on h).
+void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t stream);
+// y = softcap(y) over `count` bf16 elements (in place).
+void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream);
 
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,

@@ -49,8 +49,6 @@ struct GemmParams {
     uint32_t k;
     uint32_t tiles_n;
     uint32_t tiles_total;
-    int epi;
-    float cap;
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -98,13 +96,24 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     const uint32_t G = k / 64u;
     const size_t row_words = k / 8u;
 
-    // Per-lane weight rows for the wave's two N tiles.
+    // Per-lane weight rows for the wave's two N tiles, clamped into the matrix: every
+    // load is unconditional; columns past n are computed but never stored.
     uint32_t nrow[kNTiles];
-    bool nvalid[kNTiles];
+    size_t wrow[kNTiles];   // row index (clamped)
 #pragma unroll
     for (int t = 0; t < kNTiles; ++t) {
         nrow[t] = n0 + wave * 64u + t * 32u + col;
-        nvalid[t] = nrow[t] < p.n;
+        wrow[t] = min(nrow[t], p.n - 1u);
+    }
+    // X rows this thread stages: rows (tid >> 3) + 32 i, 16-byte column (tid & 7),
+    // clamped likewise (rows past m feed outputs that are never stored).
+    const uint32_t xc16 = tid & 7u;
+    const uint32_t xr0 = tid >> 3;
+    size_t xoff[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) {
+        const uint32_t gm = min(m0 + xr0 + 32u * i, p.m - 1u);
+        xoff[i] = static_cast<size_t>(gm) * k + xc16 * 8u;
     }
 
     f32x16_t acc[kMTiles][kNTiles];
@@ -117,65 +126,44 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 
     uint4 xr[kXLoads];
     uint4 wv[kNTiles];
-    float sv[kNTiles];
-    float bv[kNTiles];
+    uint32_t sraw[kNTiles];
+    uint32_t braw[kNTiles];
 
-    auto load_x = [&](uint32_t g) {
 #pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const uint32_t idx = tid + i * kThreads;
-            const uint32_t row = idx >> 3;
-            const uint32_t c16 = idx & 7u;
-            const uint32_t gm = m0 + row;
-            xr[i] = make_uint4(0u, 0u, 0u, 0u);
-            if (gm < p.m) {
-                xr[i] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(gm) * k + g * 64u + c16 * 8u);
-            }
-        }
-    };
-    auto store_x = [&](int buf) {
+    for (int i = 0; i < kXLoads; ++i) xr[i] = *reinterpret_cast<const uint4*>(p.x + xoff[i]);
 #pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const uint32_t idx = tid + i * kThreads;
-            const uint32_t row = idx >> 3;
-            const uint32_t c16 = idx & 7u;
-            *reinterpret_cast<uint4*>(&xs[buf][row * kLdsStride + c16 * 8u]) = xr[i];
-        }
-    };
-    auto load_w = [&](uint32_t g) {
+    for (int t = 0; t < kNTiles; ++t) {
+        wv[t] = *reinterpret_cast<const uint4*>(p.w + wrow[t] * row_words + half * 4u);
+        sraw[t] = p.s[wrow[t] * G];
+        braw[t] = p.b[wrow[t] * G];
+    }
 #pragma unroll
-        for (int t = 0; t < kNTiles; ++t) {
-            wv[t] = make_uint4(0u, 0u, 0u, 0u);
-            sv[t] = 0.0f;
-            bv[t] = 0.0f;
-            if (nvalid[t]) {
-                const size_t r = nrow[t];
-                wv[t] = *reinterpret_cast<const uint4*>(p.w + r * row_words + g * 8u + half * 4u);
-                sv[t] = bf16_bits_to_f32(p.s[r * G + g]);
-                bv[t] = bf16_bits_to_f32(p.b[r * G + g]);
-            }
-        }
-    };
-
-    load_x(0);
-    load_w(0);
-    store_x(0);
+    for (int i = 0; i < kXLoads; ++i) {
+        *reinterpret_cast<uint4*>(&xs[0][(xr0 + 32u * i) * kLdsStride + xc16 * 8u]) = xr[i];
+    }
     __syncthreads();
 
     for (uint32_t g = 0; g < G; ++g) {
-        const int cur = g & 1;
+        const uint32_t cur = g & 1u;
         bf16x8_t bfr[kNTiles][4];
 #pragma unroll
         for (int t = 0; t < kNTiles; ++t) {
-            const uint32_t words[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                bfr[t][j] = __builtin_bit_cast(bf16x8_t, dequant_word(words[j], sv[t], bv[t]));
-            }
+            const float sv = bf16_bits_to_f32(sraw[t]);
+            const float bv = bf16_bits_to_f32(braw[t]);
+            bfr[t][0] = __builtin_bit_cast(bf16x8_t, dequant_word(wv[t].x, sv, bv));
+            bfr[t][1] = __builtin_bit_cast(bf16x8_t, dequant_word(wv[t].y, sv, bv));
+            bfr[t][2] = __builtin_bit_cast(bf16x8_t, dequant_word(wv[t].z, sv, bv));
+            bfr[t][3] = __builtin_bit_cast(bf16x8_t, dequant_word(wv[t].w, sv, bv));
         }
-        if (g + 1u < G) {
-            load_x(g + 1u);
-            load_w(g + 1u);
+        // Prefetch the next step (the last step re-reads the current group: harmless).
+        const uint32_t gn = min(g + 1u, G - 1u);
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) xr[i] = *reinterpret_cast<const uint4*>(p.x + xoff[i] + gn * 64u);
+#pragma unroll
+        for (int t = 0; t < kNTiles; ++t) {
+            wv[t] = *reinterpret_cast<const uint4*>(p.w + wrow[t] * row_words + gn * 8u + half * 4u);
+            sraw[t] = p.s[wrow[t] * G + gn];
+            braw[t] = p.b[wrow[t] * G + gn];
         }
         const uint16_t* xb = xs[cur];
 #pragma unroll
@@ -191,8 +179,10 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
                 }
             }
         }
-        if (g + 1u < G) {
-            store_x(cur ^ 1);
+        uint16_t* xn = xs[cur ^ 1u];
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            *reinterpret_cast<uint4*>(&xn[(xr0 + 32u * i) * kLdsStride + xc16 * 8u]) = xr[i];
         }
         __syncthreads();
     }
@@ -200,23 +190,18 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     // Epilogue: acc[i][t][v] is Y[m0 + 32i + 8(v/4) + 4*half + v%4][n0 + 64*wave + 32t + col].
 #pragma unroll
     for (int t = 0; t < kNTiles; ++t) {
-        if (!nvalid[t]) continue;
         const uint32_t n = nrow[t];
+        const bool nok = n < p.n;
 #pragma unroll
         for (int i = 0; i < kMTiles; ++i) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t m = m0 + i * 32u + 8u * (v >> 2) + 4u * half + (v & 3);
-                if (m >= p.m) continue;
-                const size_t off = static_cast<size_t>(m) * p.n + n;
-                float out = round_bf16(acc[i][t][v]);
-                if (p.epi == static_cast<int>(Epilogue::kSoftcap)) {
-                    out = softcap_bf16(out, p.cap);
-                } else if (p.epi == static_cast<int>(Epilogue::kGeluMul)) {
-                    const float gate = bf16_bits_to_f32(p.y[off]);
-                    out = round_bf16(gelu_tanh_bf16_chain(gate) * out);
+                if (nok && m < p.m) {
+                    const size_t off = static_cast<size_t>(m) * p.n + n;
+                    const float out = round_bf16(acc[i][t][v]);
+                    p.y[off] = f32_to_bf16_bits(out);
                 }
-                p.y[off] = f32_to_bf16_bits(out);
             }
         }
     }
@@ -224,8 +209,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 
 }  // namespace
 
-void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, Epilogue epi,
-                    float cap_bf16, hipStream_t stream) {
+void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {
     GemmParams p{};
     p.w = w.w;
     p.s = w.scales;
@@ -238,8 +222,6 @@ void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* 
     p.tiles_n = (w.n + kBN - 1u) / kBN;
     const uint32_t tiles_m = (m + kBM - 1u) / kBM;
     p.tiles_total = p.tiles_n * tiles_m;
-    p.epi = static_cast<int>(epi);
-    p.cap = cap_bf16;
     hipLaunchKernelGGL(q4_gemm_kernel, dim3(p.tiles_total), dim3(kThreads), 0, stream, p);
     HYP_HIP_CHECK(hipGetLastError());
 }

@@ -30,7 +30,10 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRowsPerStream = 2;   // rows a wave has in flight per iteration
+#ifndef HYP_GEMV_BLOCKS_PER_CU
+#define HYP_GEMV_BLOCKS_PER_CU 2
+#endif
+constexpr uint32_t kGemvBlocksPerCU = HYP_GEMV_BLOCKS_PER_CU;
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -84,10 +87,9 @@ __device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ x, uint
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (active) {
-                v = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(m) * k + h * 32u + j * 8u);
-            }
+            // h is clamped into the row; inactive lanes zero what they loaded.
+            uint4 v = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(m) * k + h * 32u + j * 8u);
+            if (!active) v = make_uint4(0u, 0u, 0u, 0u);
             xp[m][slot][4 * j + 0] = (v.x & 0xFFFFu) | (v.z << 16);
             xp[m][slot][4 * j + 1] = (v.x >> 16) | (v.z & 0xFFFF0000u);
             xp[m][slot][4 * j + 2] = (v.y & 0xFFFFu) | (v.w << 16);
@@ -124,10 +126,51 @@ __device__ __forceinline__ float half_group_dot(const uint4& wv, const uint32_t*
     return a0 + a1;
 }
 
+// Rows a wave has in flight per iteration: enough bytes in flight to cover HBM
+// latency, within the register budget left by x.
+template <int M, bool DUAL>
+constexpr int rows_per_stream() {
+    return (M * (DUAL ? 2 : 1) <= 2) ? 4 : ((M * (DUAL ? 2 : 1) <= 4) ? 2 : 1);
+}
+
+template <int NW, int RB>
+struct RowRegs {
+    uint4 w[NW][RB][2];
+    uint32_t s[NW][RB][2];
+    uint32_t b[NW][RB][2];
+};
+
+// Loads for rows base+stream*RB .. +RB-1. Indices are clamped into the matrix so every
+// load is unconditional (no exec-masked loads, no forced waits); rows past n are never
+// stored and lanes past the row's half-groups are zeroed at use.
+template <int NW, int RB>
+__device__ __forceinline__ void load_rows(const GemvParams& p, uint32_t first_row, uint32_t h0c, uint32_t h1c,
+                                          RowRegs<NW, RB>& r) {
+    const size_t row_words = p.k / 8u;
+    const uint32_t G = p.k / 64u;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const uint32_t row = min(first_row + rb, p.n - 1u);
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+            const uint32_t* wrow = (q == 0 ? p.w : p.w2) + static_cast<size_t>(row) * row_words;
+            const uint16_t* srow = (q == 0 ? p.s : p.s2) + static_cast<size_t>(row) * G;
+            const uint16_t* brow = (q == 0 ? p.b : p.b2) + static_cast<size_t>(row) * G;
+            r.w[q][rb][0] = *reinterpret_cast<const uint4*>(wrow + h0c * 4u);
+            r.w[q][rb][1] = *reinterpret_cast<const uint4*>(wrow + h1c * 4u);
+            r.s[q][rb][0] = srow[h0c >> 1];
+            r.s[q][rb][1] = srow[h1c >> 1];
+            r.b[q][rb][0] = brow[h0c >> 1];
+            r.b[q][rb][1] = brow[h1c >> 1];
+        }
+    }
+}
+
 template <int M, bool DUAL, int EPI>
 __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
     constexpr int NW = DUAL ? 2 : 1;
-    __shared__ float red[2][kWaves][kRowsPerStream][NW][M];
+    constexpr int RB = rows_per_stream<M, DUAL>();
+    __shared__ float red[2][kWaves][RB][NW][M];
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -136,7 +179,6 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
     const uint32_t stream = wave / S;
     const uint32_t streams = kWaves / S;
     const uint32_t k = p.k;
-    const uint32_t G = k / 64u;
     const uint32_t HG = k / 32u;
     const uint32_t HGs = (HG + S - 1u) / S;
     const uint32_t hbase = split * HGs;
@@ -145,62 +187,51 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
     const uint32_t h1 = h0 + 64u;
     const bool act0 = h0 < hend;
     const bool act1 = h1 < hend;
+    const uint32_t h0c = act0 ? h0 : hbase;
+    const uint32_t h1c = act1 ? h1 : hbase;
 
+    const uint32_t rows_per_iter = streams * RB;
+    const uint32_t stride = gridDim.x * rows_per_iter;
+    uint32_t base = blockIdx.x * rows_per_iter;
+
+    // x first: loads retire in issue order, so x can be consumed while the first
+    // rows are still in flight.
     uint32_t xp[M][2][16];
     float sx[M][2];
-    load_x_half<M>(p.x, k, h0, act0, xp, sx, 0);
-    load_x_half<M>(p.x, k, h1, act1, xp, sx, 1);
+    load_x_half<M>(p.x, k, h0c, act0, xp, sx, 0);
+    load_x_half<M>(p.x, k, h1c, act1, xp, sx, 1);
 
-    const uint32_t rows_per_iter = streams * kRowsPerStream;
-    const size_t row_words = k / 8u;
+    RowRegs<NW, RB> cur;
+    load_rows<NW, RB>(p, base + stream * RB, h0c, h1c, cur);
+
     uint32_t parity = 0;
-    for (uint32_t base = blockIdx.x * rows_per_iter; base < p.n; base += gridDim.x * rows_per_iter) {
-        uint4 wa[NW][kRowsPerStream][2];
-        float sc[NW][kRowsPerStream][2];
-        float bi[NW][kRowsPerStream][2];
-#pragma unroll
-        for (int rb = 0; rb < kRowsPerStream; ++rb) {
-            const uint32_t r = base + stream * kRowsPerStream + rb;
-            const bool rv = r < p.n;
-#pragma unroll
-            for (int q = 0; q < NW; ++q) {
-                const uint32_t* wsrc = q == 0 ? p.w : p.w2;
-                const uint16_t* ssrc = q == 0 ? p.s : p.s2;
-                const uint16_t* bsrc = q == 0 ? p.b : p.b2;
-                const uint32_t* wrow = wsrc + static_cast<size_t>(r) * row_words;
-                const uint16_t* srow = ssrc + static_cast<size_t>(r) * G;
-                const uint16_t* brow = bsrc + static_cast<size_t>(r) * G;
-                wa[q][rb][0] = make_uint4(0u, 0u, 0u, 0u);
-                wa[q][rb][1] = make_uint4(0u, 0u, 0u, 0u);
-                sc[q][rb][0] = sc[q][rb][1] = 0.0f;
-                bi[q][rb][0] = bi[q][rb][1] = 0.0f;
-                if (rv && act0) {
-                    wa[q][rb][0] = *reinterpret_cast<const uint4*>(wrow + h0 * 4u);
-                    sc[q][rb][0] = bf16_bits_to_f32(srow[h0 >> 1]);
-                    bi[q][rb][0] = bf16_bits_to_f32(brow[h0 >> 1]);
-                }
-                if (rv && act1) {
-                    wa[q][rb][1] = *reinterpret_cast<const uint4*>(wrow + h1 * 4u);
-                    sc[q][rb][1] = bf16_bits_to_f32(srow[h1 >> 1]);
-                    bi[q][rb][1] = bf16_bits_to_f32(brow[h1 >> 1]);
-                }
-            }
-        }
+    while (true) {
+        const uint32_t next = base + stride;
+        const bool more = next < p.n;   // uniform across the workgroup
+        RowRegs<NW, RB> nxt;
+        if (more) load_rows<NW, RB>(p, next + stream * RB, h0c, h1c, nxt);
 
-        float tot[NW][kRowsPerStream][M];
+        float tot[NW][RB][M];
 #pragma unroll
         for (int q = 0; q < NW; ++q) {
 #pragma unroll
-            for (int rb = 0; rb < kRowsPerStream; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
+                float sc[2], bi[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const bool act = hh == 0 ? act0 : act1;
+                    sc[hh] = act ? bf16_bits_to_f32(cur.s[q][rb][hh]) : 0.0f;
+                    bi[hh] = act ? bf16_bits_to_f32(cur.b[q][rb][hh]) : 0.0f;
+                }
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     float part = 0.0f;
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        const float acc = half_group_dot(wa[q][rb][hh], xp[m][hh]);
+                        const float acc = half_group_dot(cur.w[q][rb][hh], xp[m][hh]);
                         const float sxv = sx[m][hh];
-                        part = fmaf(sc[q][rb][hh], acc - 128.0f * sxv, part);
-                        part = fmaf(bi[q][rb][hh], sxv, part);
+                        part = fmaf(sc[hh], acc - 128.0f * sxv, part);
+                        part = fmaf(bi[hh], sxv, part);
                     }
                     tot[q][rb][m] = wave_sum(part);
                 }
@@ -212,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
 #pragma unroll
                 for (int q = 0; q < NW; ++q)
 #pragma unroll
-                    for (int rb = 0; rb < kRowsPerStream; ++rb)
+                    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                         for (int m = 0; m < M; ++m) red[parity][wave][rb][q][m] = tot[q][rb][m];
             }
@@ -221,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
 #pragma unroll
                 for (int q = 0; q < NW; ++q)
 #pragma unroll
-                    for (int rb = 0; rb < kRowsPerStream; ++rb)
+                    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
                             float v = 0.0f;
@@ -232,14 +263,14 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
             parity ^= 1u;
         }
 
-        if (split == 0u && lane < static_cast<uint32_t>(kRowsPerStream * M)) {
+        if (split == 0u && lane < static_cast<uint32_t>(RB * M)) {
             // Lane (rb * M + m) stores one output.
 #pragma unroll
-            for (int rb = 0; rb < kRowsPerStream; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     if (lane != static_cast<uint32_t>(rb * M + m)) continue;
-                    const uint32_t r = base + stream * kRowsPerStream + rb;
+                    const uint32_t r = base + stream * RB + rb;
                     if (r >= p.n) continue;
                     float out = round_bf16(tot[0][rb][m]);
                     if constexpr (DUAL) {
@@ -252,17 +283,28 @@ __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
                 }
             }
         }
+        if (!more) break;
+        cur = nxt;
+        base = next;
     }
 }
 
 template <int M>
-void launch_m(const GemvParams& p, bool dual, Epilogue epi, dim3 grid, hipStream_t stream) {
+void launch_m(const GemvParams& p, bool dual, Epilogue epi, uint32_t max_blocks, hipStream_t stream) {
+    const uint32_t streams = kWaves / p.splits;
+    auto grid_for = [&](int rb) {
+        const uint32_t rpi = streams * static_cast<uint32_t>(rb);
+        return dim3(min((p.n + rpi - 1u) / rpi, max_blocks));
+    };
     if (dual) {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, true, 0>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((q4_gemv_kernel<M, true, 0>), grid_for(rows_per_stream<M, true>()), dim3(kThreads), 0,
+                           stream, p);
     } else if (epi == Epilogue::kSoftcap) {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, false, 1>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((q4_gemv_kernel<M, false, 1>), grid_for(rows_per_stream<M, false>()), dim3(kThreads), 0,
+                           stream, p);
     } else {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, false, 0>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((q4_gemv_kernel<M, false, 0>), grid_for(rows_per_stream<M, false>()), dim3(kThreads), 0,
+                           stream, p);
     }
 }
 
@@ -284,15 +326,14 @@ void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, ui
     p.cap = cap_bf16;
     const uint32_t hg = w.k / 32u;
     p.splits = hg <= 128u ? 1u : (hg <= 256u ? 2u : 4u);
-    const uint32_t rows_per_iter = (kWaves / p.splits) * kRowsPerStream;
-    const uint32_t blocks = (w.n + rows_per_iter - 1u) / rows_per_iter;
-    const dim3 grid(blocks);
+    // Persistent grid: kGemvBlocksPerCU workgroups per CU loop over the rows.
+    const uint32_t max_blocks = device_compute_units() * kGemvBlocksPerCU;
     const bool dual = up != nullptr;
     switch (m) {
-        case 1: launch_m<1>(p, dual, epi, grid, stream); break;
-        case 2: launch_m<2>(p, dual, epi, grid, stream); break;
-        case 3: launch_m<3>(p, dual, epi, grid, stream); break;
-        case 4: launch_m<4>(p, dual, epi, grid, stream); break;
+        case 1: launch_m<1>(p, dual, epi, max_blocks, stream); break;
+        case 2: launch_m<2>(p, dual, epi, max_blocks, stream); break;
+        case 3: launch_m<3>(p, dual, epi, max_blocks, stream); break;
+        case 4: launch_m<4>(p, dual, epi, max_blocks, stream); break;
         default: throw NativeError(HYP_STATUS_INTERNAL, "gemv launched with m outside 1..4");
     }
     HYP_HIP_CHECK(hipGetLastError());

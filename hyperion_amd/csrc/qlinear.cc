@@ -5,6 +5,24 @@
 
 #include <utility>
 
+namespace hyperion::hip {
+
+uint32_t device_compute_units() {
+    static thread_local int cached_device = -1;
+    static thread_local uint32_t cached_cus = 0;
+    int dev = 0;
+    HYP_HIP_CHECK(hipGetDevice(&dev));
+    if (dev != cached_device) {
+        int cus = 0;
+        HYP_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        cached_cus = cus > 0 ? static_cast<uint32_t>(cus) : 1u;
+        cached_device = dev;
+    }
+    return cached_cus;
+}
+
+}  // namespace hyperion::hip
+
 namespace hyperion::model {
 
 using hip::NativeError;
@@ -98,8 +116,11 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
     if (m == 0) return;
     if (m <= hip::kGemvMaxM && mat.k <= hip::kGemvMaxK) {
         hip::launch_q4_gemv(mat, nullptr, x, m, y, epi, cap_bf16, stream);
-    } else {
-        hip::launch_q4_gemm(mat, x, m, y, epi, cap_bf16, stream);
+        return;
+    }
+    hip::launch_q4_gemm(mat, x, m, y, stream);
+    if (epi == Epilogue::kSoftcap) {
+        hip::launch_softcap(y, cap_bf16, static_cast<uint64_t>(m) * mat.n, stream);
     }
 }
 
@@ -108,12 +129,21 @@ void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const u
     if (m == 0) return;
     if (m <= hip::kGemvMaxM && gate.mat.k <= hip::kGemvMaxK) {
         hip::launch_q4_gemv(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f, stream);
-    } else {
-        // h <- gate(x); then the up GEMM's epilogue reads each gate value back and
-        // writes gelu(gate) * up in place (same thread reads and writes an element).
-        hip::launch_q4_gemm(gate.mat, x, m, h, Epilogue::kNone, 0.0f, stream);
-        hip::launch_q4_gemm(up.mat, x, m, h, Epilogue::kGeluMul, 0.0f, stream);
+        return;
     }
+    // h <- gate(x); u <- up(x) in a stream-ordered temporary; h <- gelu(h) * u.
+    const size_t bytes = static_cast<size_t>(m) * up.mat.n * sizeof(uint16_t);
+    void* u = nullptr;
+    HYP_HIP_CHECK(hipMallocAsync(&u, bytes, stream));
+    try {
+        hip::launch_q4_gemm(gate.mat, x, m, h, stream);
+        hip::launch_q4_gemm(up.mat, x, m, static_cast<uint16_t*>(u), stream);
+        hip::launch_gelu_mul(h, static_cast<const uint16_t*>(u), static_cast<uint64_t>(m) * up.mat.n, stream);
+    } catch (...) {
+        (void)hipFreeAsync(u, stream);
+        throw;
+    }
+    HYP_HIP_CHECK(hipFreeAsync(u, stream));
 }
 
 }  // namespace hyperion::model

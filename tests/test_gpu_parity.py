@@ -2,8 +2,8 @@
 
 Bars (stated per test):
   * quantize / dequantize: bit-exact (integer and bf16-bit work);
-  * qmatmul: within 1 bf16 ulp of the bf16-rounded fp64 reference (the GEMV against
-    exact dequantization, the MFMA GEMM against its bf16 weights), and
+  * qmatmul: within half a bf16 ulp of the fp64 reference plus 2^-18 * max|ref| (the
+    GEMV against exact dequantization, the MFMA GEMM against its bf16 weights), and
     sig_rel = max|d|/max|ref| <= 1e-2 against the fp64 ground truth;
   * exact-arithmetic inputs (x in {-1,0,1}, scale 2^-7): bit-exact;
   * fused gelu/softcap epilogues: bit-exact against the oracle applied to the
@@ -34,6 +34,19 @@ def ulp_diff(a_bits, b_bits):
         h = h.astype(np.int32)
         return np.where(h & 0x8000, -(h & 0x7FFF), h)
     return np.abs(key(a_bits) - key(b_bits))
+
+
+def assert_within_bf16_rounding(y_bits, truth, what, slack=2.0**-18):
+    """|y - truth| <= half a bf16 ulp of truth + slack * max|truth|: the bf16 output
+    rounding plus an fp32-accumulation allowance (which is relative to the size of the
+    summed terms, so near-zero outputs may be several ulps off in relative terms)."""
+    t = np.asarray(truth, np.float64)
+    y = syn.bf16_to_f32(y_bits).astype(np.float64)
+    tb = syn.bf16_to_f32(syn.bf16_bits(t.astype(np.float32))).astype(np.float64)
+    half_ulp = np.abs(tb) * 2.0**-8 + 1e-40            # bf16: 8 significant bits
+    bound = half_ulp + slack * float(np.max(np.abs(t)))
+    worst = float(np.max(np.abs(y - t) / bound))
+    assert worst <= 1.0, f"{what}: worst error {worst:.2f}x the bf16-rounding bound"
 
 
 def dev(a, stream):
@@ -172,7 +185,7 @@ def test_gemv_decode_config(stream):
     ref_rel = syn.sig_rel(mlx, truth[:, :mlx_rows])
     say(f"  sig_rel gpu={rel:.3e}  mlx-cpu restatement={ref_rel:.3e} (first {mlx_rows} rows)")
     assert rel <= 1e-2
-    assert np.max(ulp_diff(y, syn.bf16_bits(truth.astype(np.float32)))) <= 1
+    assert_within_bf16_rounding(y, truth, "decode")
 
 
 def test_gemv_exact_integer_inputs(stream):
@@ -209,7 +222,7 @@ def test_gemv_layer_projections(stream, m):
         y = run_qmatmul(w, s, b, x, stream)
         truth = O.qmatmul_f64(x, w, s, b)
         assert syn.sig_rel(syn.bf16_to_f32(y), truth) <= 1e-2, name
-        assert np.max(ulp_diff(y, syn.bf16_bits(truth.astype(np.float32)))) <= 1, name
+        assert_within_bf16_rounding(y, truth, name)
 
 
 # ---------------------------------------------------------------- prefill GEMM
@@ -230,7 +243,7 @@ def test_gemm_prefill_projections_sampled(stream, m):
         ref_bf16w = O.qmatmul_deq_f64(xs, w, s, b, mode=1)
         truth = O.qmatmul_f64(xs, w, s, b)
         assert syn.sig_rel(syn.bf16_to_f32(y[rows]), truth) <= 1e-2, name
-        assert np.max(ulp_diff(y[rows], syn.bf16_bits(ref_bf16w.astype(np.float32)))) <= 1, name
+        assert_within_bf16_rounding(y[rows], ref_bf16w, name)
 
 
 def test_gemm_exact_integer_and_ragged_tiles(stream):
