@@ -8,15 +8,25 @@
 
 namespace hyperion::hip {
 
-// A resident Q4/g64 projection in MLX layout: w uint32 [n, k/8], scales and
-// biases bf16 [n, k/64] (native/hyperion_mlx/src/weights.h:18-25).
+// A Q4/g64 projection [n, k]. w/scales/biases: MLX layout, codes uint32 [n, k/8],
+// scales and biases bf16 [n, k/64] (native/hyperion_mlx/src/weights.h:18-25).
+// codes/sb: the tiled resident layout of q4_layout.h (null when not resident).
 struct Q4Matrix {
     const uint32_t* w = nullptr;
     const uint16_t* scales = nullptr;
     const uint16_t* biases = nullptr;
     uint32_t n = 0;
     uint32_t k = 0;
+    const uint4* codes = nullptr;
+    const uint2* sb = nullptr;
 };
+
+// MLX layout -> tiled layout (q4_layout.h), and back. Device pointers; the tiled
+// buffers hold TiledDims::of(n, k).code_bytes() and .sb_bytes().
+void launch_q4_tile(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint32_t n, uint32_t k, uint4* codes,
+                    uint2* sb, hipStream_t stream);
+void launch_q4_untile(const uint4* codes, const uint2* sb, uint32_t n, uint32_t k, uint32_t* w, uint16_t* s,
+                      uint16_t* b, hipStream_t stream);
 
 enum class Epilogue : int {
     kNone = 0,
@@ -28,10 +38,38 @@ constexpr uint32_t kGemvMaxM = 4;
 // Largest k the decode GEMV handles (64 lanes x 2 half-groups x 4 waves x 32).
 constexpr uint32_t kGemvMaxK = 16384;
 
+// Launch shape of the decode GEMV: `rows` consecutive rows per wave (1, 2, 4, or 8
+// for m <= 2), `splits` waves sharing each row's K range (1, 2, 4), `halves`
+// half-groups of 32 codes per lane per row (1 or 2).
+struct GemvConfig {
+    uint32_t rows = 4;
+    uint32_t splits = 1;
+    uint32_t halves = 2;
+};
+
+// The launch shape used for an (m, n, k) problem.
+GemvConfig choose_gemv_config(uint32_t m, uint32_t n, uint32_t k, bool dual);
+
 // Decode GEMV (m <= kGemvMaxM): y[m, n] = x[m, k] . dequant(W)^T.
 // With `up` non-null it is the fused gate/up: y = gelu_chain(x.G^T) * (x.U^T).
 void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m,
                     uint16_t* y, Epilogue epi, float cap_bf16, hipStream_t stream);
+// Same with an explicit launch shape (k must fit: ceil(k/32 / splits) <= 64 * halves).
+void launch_q4_gemv_config(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m,
+                           uint16_t* y, Epilogue epi, float cap_bf16, const GemvConfig& config,
+                           hipStream_t stream);
+
+// Largest m the skinny MFMA kernel handles.
+constexpr uint32_t kSkinnyMaxM = 4;
+
+// Skinny quantized matmul on MFMA (m <= kSkinnyMaxM): y[m, n] = x[m, k] . dequant(W)^T,
+// with `up` the fused gate/up as in launch_q4_gemv. `splits` (1, 2, 4) waves share
+// each 32-row tile; k / 64 >= splits.
+void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
+                      Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream);
+// Splits used for an (n, k) problem, and whether (m, k) fits the kernel's LDS staging.
+uint32_t choose_skinny_splits(uint32_t n, uint32_t k);
+bool skinny_supported(uint32_t m, uint32_t k, bool dual);
 
 // Prefill GEMM on bf16 MFMA: Q4 tiles dequantized in registers, x tiles in LDS.
 // Plain bf16 output; epilogues for m > kGemvMaxM run as the elementwise kernels below.

@@ -5,21 +5,27 @@
 // forward.cc:395,399,409,507 for q/k/v/o, forward.cc:338-343 for the MLP and
 // forward.cc:137-152 for the tied LM head).
 //
-// HBM-bound design (0.5625 B per weight streamed once):
-//  * A wave owns whole rows of W. Lane l reads half-groups (32 codes = 16 B) l and
-//    l+64 of the row, so each dwordx4 load instruction covers 1 KB of contiguous
-//    row bytes. Rows of W are contiguous, so a wave's consecutive rows stream
-//    consecutive memory.
+// HBM-bound design (0.5625 B per weight streamed exactly once):
+//  * A wave owns R consecutive rows of W (R * 1920 contiguous bytes at k = 3840), or
+//    one K-slice of them when S waves split a row. Lane l reads half-groups
+//    (32 codes = 16 B) l and l+64 of its slice, so each dwordx4 load instruction
+//    covers 1 KB of contiguous row bytes.
+//  * Every load of the wave is issued before any arithmetic: x first (it is L2
+//    resident), then the rows in order. Loads retire in issue order, so the math of
+//    row r waits only for row r's bytes while rows r+1.. are still in flight, and a
+//    whole CU's share of W is requested at once. The grid is one wave per R rows
+//    (no persistent loop), thousands of waves, so the tail of one wave's arithmetic
+//    overlaps other waves' loads.
 //  * Codes become bf16 pairs (128+q_a, 128+q_b) with one AND-OR on the packed word
 //    (0x4300 is bf16 128.0 whose ulp is 1, so OR-ing a nibble into the mantissa
-//    adds it exactly) and meet x through v_dot2c_f32_bf16: two MACs per VALU op with
+//    adds it exactly) and meet x through v_dot2_f32_bf16: two MACs per VALU op with
 //    fp32 accumulation. The +128 offset is removed per half-group with the
 //    precomputed sum of x: part = s * (acc - 128*sum(x)) + b * sum(x).
-//  * x lives in registers for the whole kernel, pre-permuted into the pairs the
-//    nibble extraction produces ((x0,x4),(x1,x5),(x2,x6),(x3,x7) per word).
+//  * x lives in registers, pre-permuted into the pairs the nibble extraction
+//    produces ((x0,x4),(x1,x5),(x2,x6),(x3,x7) per word).
 //  * Rows are reduced across the wave with DPP (quad perms, row mirrors,
-//    row_bcast15/31), no LDS. For k > 4096 the row is split across 2 or 4 waves of
-//    the workgroup and the partials meet in LDS.
+//    row_bcast15/31), no LDS. When S > 1 waves share a row, their partials meet
+//    in LDS.
 #include "common.h"
 #include "kernels.h"
 
@@ -30,20 +36,28 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-#ifndef HYP_GEMV_BLOCKS_PER_CU
-#define HYP_GEMV_BLOCKS_PER_CU 2
-#endif
-constexpr uint32_t kGemvBlocksPerCU = HYP_GEMV_BLOCKS_PER_CU;
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// (128 + nibble(shift), 128 + nibble(shift + 16)) as a bf16 pair.
-__device__ __forceinline__ uint32_t code_pair(uint32_t w, int shift) {
-    return ((w >> shift) & 0x000F000Fu) | 0x43004300u;
+// (w & mask) | bits. With mask and bits held in VGPRs (see the kernel), this is one
+// v_and_or_b32; as literals it would split into two VOP2 ops, because GFX9 VOP3
+// encodings take no literal constants and read at most one SGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t bits) {
+    return (w & mask) | bits;
 }
+
+// (128 + nibble(shift), 128 + nibble(shift + 16)) as a bf16 pair: 0x4300 is bf16
+// 128.0, whose ulp is 1, so OR-ing a nibble into the mantissa adds it exactly.
+__device__ __forceinline__ uint32_t code_pair(uint32_t w, int shift, uint32_t mask, uint32_t bits) {
+    return and_or(shift == 0 ? w : (w >> shift), mask, bits);
+}
+
+constexpr uint32_t kNibbleMask = 0x000F000Fu;
+constexpr uint32_t kMagic128 = 0x43004300u;   // bf16 pair (128.0, 128.0)
+constexpr uint32_t kOnePair = 0x3F803F80u;    // bf16 pair (1.0, 1.0)
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_add(float v) {
@@ -77,241 +91,245 @@ struct GemvParams {
     float cap;            // bf16 softcap constant
 };
 
-// Load the lane's x slice for half-group h and permute it into code-pair order.
-template <int M>
-__device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ x, uint32_t k, uint32_t h,
-                                            bool active, uint32_t (&xp)[M][2][16], float (&sx)[M][2],
-                                            int slot) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            // h is clamped into the row; inactive lanes zero what they loaded.
-            uint4 v = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(m) * k + h * 32u + j * 8u);
-            if (!active) v = make_uint4(0u, 0u, 0u, 0u);
-            xp[m][slot][4 * j + 0] = (v.x & 0xFFFFu) | (v.z << 16);
-            xp[m][slot][4 * j + 1] = (v.x >> 16) | (v.z & 0xFFFF0000u);
-            xp[m][slot][4 * j + 2] = (v.y & 0xFFFFu) | (v.w << 16);
-            xp[m][slot][4 * j + 3] = (v.y >> 16) | (v.w & 0xFFFF0000u);
-            sum += bf16_bits_to_f32(v.x & 0xFFFFu) + bf16_bits_to_f32(v.x >> 16);
-            sum += bf16_bits_to_f32(v.y & 0xFFFFu) + bf16_bits_to_f32(v.y >> 16);
-            sum += bf16_bits_to_f32(v.z & 0xFFFFu) + bf16_bits_to_f32(v.z >> 16);
-            sum += bf16_bits_to_f32(v.w & 0xFFFFu) + bf16_bits_to_f32(v.w >> 16);
-        }
-        sx[m][slot] = sum;
-    }
-}
-
 // One half-group (four packed words) against the permuted x of one row m.
-__device__ __forceinline__ float half_group_dot(const uint4& wv, const uint32_t* xp) {
+__device__ __forceinline__ float half_group_dot(const uint4& wv, const uint32_t* xp, uint32_t mask, uint32_t bits) {
     float a0 = 0.0f;
     float a1 = 0.0f;
-    a0 = dot2_bf16(code_pair(wv.x, 0), xp[0], a0);
-    a1 = dot2_bf16(code_pair(wv.x, 4), xp[1], a1);
-    a0 = dot2_bf16(code_pair(wv.x, 8), xp[2], a0);
-    a1 = dot2_bf16(code_pair(wv.x, 12), xp[3], a1);
-    a0 = dot2_bf16(code_pair(wv.y, 0), xp[4], a0);
-    a1 = dot2_bf16(code_pair(wv.y, 4), xp[5], a1);
-    a0 = dot2_bf16(code_pair(wv.y, 8), xp[6], a0);
-    a1 = dot2_bf16(code_pair(wv.y, 12), xp[7], a1);
-    a0 = dot2_bf16(code_pair(wv.z, 0), xp[8], a0);
-    a1 = dot2_bf16(code_pair(wv.z, 4), xp[9], a1);
-    a0 = dot2_bf16(code_pair(wv.z, 8), xp[10], a0);
-    a1 = dot2_bf16(code_pair(wv.z, 12), xp[11], a1);
-    a0 = dot2_bf16(code_pair(wv.w, 0), xp[12], a0);
-    a1 = dot2_bf16(code_pair(wv.w, 4), xp[13], a1);
-    a0 = dot2_bf16(code_pair(wv.w, 8), xp[14], a0);
-    a1 = dot2_bf16(code_pair(wv.w, 12), xp[15], a1);
+    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a0 = dot2_bf16(code_pair(words[i], 0, mask, bits), xp[4 * i + 0], a0);
+        a1 = dot2_bf16(code_pair(words[i], 4, mask, bits), xp[4 * i + 1], a1);
+        a0 = dot2_bf16(code_pair(words[i], 8, mask, bits), xp[4 * i + 2], a0);
+        a1 = dot2_bf16(code_pair(words[i], 12, mask, bits), xp[4 * i + 3], a1);
+    }
     return a0 + a1;
 }
 
-// Rows a wave has in flight per iteration: enough bytes in flight to cover HBM
-// latency, within the register budget left by x.
-template <int M, bool DUAL>
-constexpr int rows_per_stream() {
-    return (M * (DUAL ? 2 : 1) <= 2) ? 4 : ((M * (DUAL ? 2 : 1) <= 4) ? 2 : 1);
-}
-
-template <int NW, int RB>
-struct RowRegs {
-    uint4 w[NW][RB][2];
-    uint32_t s[NW][RB][2];
-    uint32_t b[NW][RB][2];
-};
-
-// Loads for rows base+stream*RB .. +RB-1. Indices are clamped into the matrix so every
-// load is unconditional (no exec-masked loads, no forced waits); rows past n are never
-// stored and lanes past the row's half-groups are zeroed at use.
-template <int NW, int RB>
-__device__ __forceinline__ void load_rows(const GemvParams& p, uint32_t first_row, uint32_t h0c, uint32_t h1c,
-                                          RowRegs<NW, RB>& r) {
-    const size_t row_words = p.k / 8u;
-    const uint32_t G = p.k / 64u;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const uint32_t row = min(first_row + rb, p.n - 1u);
-#pragma unroll
-        for (int q = 0; q < NW; ++q) {
-            const uint32_t* wrow = (q == 0 ? p.w : p.w2) + static_cast<size_t>(row) * row_words;
-            const uint16_t* srow = (q == 0 ? p.s : p.s2) + static_cast<size_t>(row) * G;
-            const uint16_t* brow = (q == 0 ? p.b : p.b2) + static_cast<size_t>(row) * G;
-            r.w[q][rb][0] = *reinterpret_cast<const uint4*>(wrow + h0c * 4u);
-            r.w[q][rb][1] = *reinterpret_cast<const uint4*>(wrow + h1c * 4u);
-            r.s[q][rb][0] = srow[h0c >> 1];
-            r.s[q][rb][1] = srow[h1c >> 1];
-            r.b[q][rb][0] = brow[h0c >> 1];
-            r.b[q][rb][1] = brow[h1c >> 1];
-        }
-    }
-}
-
-template <int M, bool DUAL, int EPI>
+// y[m, row0 .. row0+R) for one wave: R rows (NW matrices) x H half-groups per lane.
+template <int M, int R, int H, bool DUAL, int EPI>
 __global__ __launch_bounds__(kThreads) void q4_gemv_kernel(GemvParams p) {
     constexpr int NW = DUAL ? 2 : 1;
-    constexpr int RB = rows_per_stream<M, DUAL>();
-    __shared__ float red[2][kWaves][RB][NW][M];
+    __shared__ float red[kWaves][NW][R][M];
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t S = p.splits;
     const uint32_t split = wave % S;
-    const uint32_t stream = wave / S;
-    const uint32_t streams = kWaves / S;
+    const uint32_t set = wave / S;
+    const uint32_t row0 = (blockIdx.x * (kWaves / S) + set) * R;
     const uint32_t k = p.k;
     const uint32_t HG = k / 32u;
     const uint32_t HGs = (HG + S - 1u) / S;
     const uint32_t hbase = split * HGs;
     const uint32_t hend = min(HG, hbase + HGs);
-    const uint32_t h0 = hbase + lane;
-    const uint32_t h1 = h0 + 64u;
-    const bool act0 = h0 < hend;
-    const bool act1 = h1 < hend;
-    const uint32_t h0c = act0 ? h0 : hbase;
-    const uint32_t h1c = act1 ? h1 : hbase;
+    bool act[H];
+    uint32_t hc[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        const uint32_t hh = hbase + lane + 64u * h;
+        act[h] = hh < hend;
+        hc[h] = act[h] ? hh : HG - 1u;   // clamped: every load stays inside the row
+    }
 
-    const uint32_t rows_per_iter = streams * RB;
-    const uint32_t stride = gridDim.x * rows_per_iter;
-    uint32_t base = blockIdx.x * rows_per_iter;
+    // x first (L2 resident), then the rows in order.
+    uint32_t xp[H][M][16];
+    float sx[H][M];
+    uint4 xv[H][M][4];
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xv[h][m][j] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + hc[h] * 32u + j * 8u);
 
-    // x first: loads retire in issue order, so x can be consumed while the first
-    // rows are still in flight.
-    uint32_t xp[M][2][16];
-    float sx[M][2];
-    load_x_half<M>(p.x, k, h0c, act0, xp, sx, 0);
-    load_x_half<M>(p.x, k, h1c, act1, xp, sx, 1);
-
-    RowRegs<NW, RB> cur;
-    load_rows<NW, RB>(p, base + stream * RB, h0c, h1c, cur);
-
-    uint32_t parity = 0;
-    while (true) {
-        const uint32_t next = base + stride;
-        const bool more = next < p.n;   // uniform across the workgroup
-        RowRegs<NW, RB> nxt;
-        if (more) load_rows<NW, RB>(p, next + stream * RB, h0c, h1c, nxt);
-
-        float tot[NW][RB][M];
+    const size_t row_words = k / 8u;
+    const uint32_t G = k / 64u;
+    uint4 wv[R][NW][H];
+    uint32_t sr[R][NW][H];
+    uint32_t br[R][NW][H];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = min(row0 + r, p.n - 1u);   // rows past n are loaded, never stored
 #pragma unroll
         for (int q = 0; q < NW; ++q) {
+            const uint32_t* wrow = (q == 0 ? p.w : p.w2) + static_cast<size_t>(row) * row_words;
+            const uint16_t* srow = (q == 0 ? p.s : p.s2) + static_cast<size_t>(row) * G;
+            const uint16_t* brow = (q == 0 ? p.b : p.b2) + static_cast<size_t>(row) * G;
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                float sc[2], bi[2];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const bool act = hh == 0 ? act0 : act1;
-                    sc[hh] = act ? bf16_bits_to_f32(cur.s[q][rb][hh]) : 0.0f;
-                    bi[hh] = act ? bf16_bits_to_f32(cur.b[q][rb][hh]) : 0.0f;
-                }
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    float part = 0.0f;
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const float acc = half_group_dot(cur.w[q][rb][hh], xp[m][hh]);
-                        const float sxv = sx[m][hh];
-                        part = fmaf(sc[hh], acc - 128.0f * sxv, part);
-                        part = fmaf(bi[hh], sxv, part);
-                    }
-                    tot[q][rb][m] = wave_sum(part);
-                }
+            for (int h = 0; h < H; ++h) {
+                wv[r][q][h] = *reinterpret_cast<const uint4*>(wrow + hc[h] * 4u);
+                sr[r][q][h] = srow[hc[h] >> 1];
+                br[r][q][h] = brow[hc[h] >> 1];
             }
         }
+    }
 
-        if (S > 1u) {
-            if (lane == 0u) {
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            // (x0,x4),(x1,x5),(x2,x6),(x3,x7) of each 8-element word, one v_perm_b32 each;
+            // sum(x) through the same dot2 unit against (1, 1).
+            float s0 = 0.0f;
+            float s1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint4 q = xv[h][m][j];
+                if (!act[h]) q = make_uint4(0u, 0u, 0u, 0u);
+                xp[h][m][4 * j + 0] = __builtin_amdgcn_perm(q.z, q.x, 0x05040100u);
+                xp[h][m][4 * j + 1] = __builtin_amdgcn_perm(q.z, q.x, 0x07060302u);
+                xp[h][m][4 * j + 2] = __builtin_amdgcn_perm(q.w, q.y, 0x05040100u);
+                xp[h][m][4 * j + 3] = __builtin_amdgcn_perm(q.w, q.y, 0x07060302u);
+                s0 = dot2_bf16(q.x, kOnePair, s0);
+                s1 = dot2_bf16(q.y, kOnePair, s1);
+                s0 = dot2_bf16(q.z, kOnePair, s0);
+                s1 = dot2_bf16(q.w, kOnePair, s1);
+            }
+            sx[h][m] = s0 + s1;
+        }
+    }
+
+    // Opaque VGPR values, so (w & mask) | bits selects v_and_or_b32 (see and_or).
+    uint32_t mask = kNibbleMask;
+    uint32_t bits = kMagic128;
+    asm volatile("" : "+v"(mask), "+v"(bits));
+
+    float tot[R][NW][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+            float sc[H], bi[H];
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                sc[h] = act[h] ? bf16_bits_to_f32(sr[r][q][h]) : 0.0f;
+                bi[h] = act[h] ? bf16_bits_to_f32(br[r][q][h]) : 0.0f;
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float part = 0.0f;
+#pragma unroll
+                for (int h = 0; h < H; ++h) {
+                    const float acc = half_group_dot(wv[r][q][h], xp[h][m], mask, bits);
+                    part = fmaf(sc[h], acc - 128.0f * sx[h][m], part);
+                    part = fmaf(bi[h], sx[h][m], part);
+                }
+                tot[r][q][m] = wave_sum(part);
+            }
+        }
+    }
+
+    if (S > 1u) {
+        if (lane == 0u) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int q = 0; q < NW; ++q)
 #pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
+                    for (int m = 0; m < M; ++m) red[wave][q][r][m] = tot[r][q][m];
+        }
+        __syncthreads();
+        if (split == 0u) {
 #pragma unroll
-                        for (int m = 0; m < M; ++m) red[parity][wave][rb][q][m] = tot[q][rb][m];
-            }
-            __syncthreads();
-            if (split == 0u) {
+            for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int q = 0; q < NW; ++q)
 #pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                        for (int m = 0; m < M; ++m) {
-                            float v = 0.0f;
-                            for (uint32_t s2 = 0; s2 < S; ++s2) v += red[parity][wave + s2][rb][q][m];
-                            tot[q][rb][m] = v;
-                        }
-            }
-            parity ^= 1u;
-        }
-
-        if (split == 0u && lane < static_cast<uint32_t>(RB * M)) {
-            // Lane (rb * M + m) stores one output.
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    if (lane != static_cast<uint32_t>(rb * M + m)) continue;
-                    const uint32_t r = base + stream * RB + rb;
-                    if (r >= p.n) continue;
-                    float out = round_bf16(tot[0][rb][m]);
-                    if constexpr (DUAL) {
-                        const float up = round_bf16(tot[NW - 1][rb][m]);
-                        out = round_bf16(gelu_tanh_bf16_chain(out) * up);
-                    } else if constexpr (EPI == static_cast<int>(Epilogue::kSoftcap)) {
-                        out = softcap_bf16(out, p.cap);
+                    for (int m = 0; m < M; ++m) {
+                        float v = 0.0f;
+                        for (uint32_t s2 = 0; s2 < S; ++s2) v += red[wave + s2][q][r][m];
+                        tot[r][q][m] = v;
                     }
-                    p.y[static_cast<size_t>(m) * p.n + r] = f32_to_bf16_bits(out);
+        }
+    }
+
+    if (split == 0u && lane < static_cast<uint32_t>(R * M)) {
+        // Lane (r * M + m) stores one output.
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (lane != static_cast<uint32_t>(r * M + m)) continue;
+                const uint32_t row = row0 + r;
+                if (row >= p.n) continue;
+                float out = round_bf16(tot[r][0][m]);
+                if constexpr (DUAL) {
+                    const float up = round_bf16(tot[r][NW - 1][m]);
+                    out = round_bf16(gelu_tanh_bf16_chain(out) * up);
+                } else if constexpr (EPI == static_cast<int>(Epilogue::kSoftcap)) {
+                    out = softcap_bf16(out, p.cap);
                 }
+                p.y[static_cast<size_t>(m) * p.n + row] = f32_to_bf16_bits(out);
             }
         }
-        if (!more) break;
-        cur = nxt;
-        base = next;
+    }
+}
+
+template <int M, int R, int H>
+void launch_mrh(const GemvParams& p, bool dual, Epilogue epi, hipStream_t stream) {
+    const uint32_t rows_per_block = static_cast<uint32_t>(R) * (kWaves / p.splits);
+    const dim3 grid((p.n + rows_per_block - 1u) / rows_per_block);
+    if (dual) {
+        hipLaunchKernelGGL((q4_gemv_kernel<M, R, H, true, 0>), grid, dim3(kThreads), 0, stream, p);
+    } else if (epi == Epilogue::kSoftcap) {
+        hipLaunchKernelGGL((q4_gemv_kernel<M, R, H, false, 1>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((q4_gemv_kernel<M, R, H, false, 0>), grid, dim3(kThreads), 0, stream, p);
+    }
+}
+
+template <int M, int R>
+void launch_mr(const GemvParams& p, uint32_t h, bool dual, Epilogue epi, hipStream_t stream) {
+    if (h == 1u) {
+        launch_mrh<M, R, 1>(p, dual, epi, stream);
+    } else {
+        launch_mrh<M, R, 2>(p, dual, epi, stream);
     }
 }
 
 template <int M>
-void launch_m(const GemvParams& p, bool dual, Epilogue epi, uint32_t max_blocks, hipStream_t stream) {
-    const uint32_t streams = kWaves / p.splits;
-    auto grid_for = [&](int rb) {
-        const uint32_t rpi = streams * static_cast<uint32_t>(rb);
-        return dim3(min((p.n + rpi - 1u) / rpi, max_blocks));
-    };
-    if (dual) {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, true, 0>), grid_for(rows_per_stream<M, true>()), dim3(kThreads), 0,
-                           stream, p);
-    } else if (epi == Epilogue::kSoftcap) {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, false, 1>), grid_for(rows_per_stream<M, false>()), dim3(kThreads), 0,
-                           stream, p);
-    } else {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, false, 0>), grid_for(rows_per_stream<M, false>()), dim3(kThreads), 0,
-                           stream, p);
+void launch_m(const GemvParams& p, const GemvConfig& c, bool dual, Epilogue epi, hipStream_t stream) {
+    switch (c.rows) {
+        case 1: launch_mr<M, 1>(p, c.halves, dual, epi, stream); break;
+        case 2: launch_mr<M, 2>(p, c.halves, dual, epi, stream); break;
+        case 4: launch_mr<M, 4>(p, c.halves, dual, epi, stream); break;
+        case 8:
+            if constexpr (M <= 2) {
+                launch_mr<M, 8>(p, c.halves, dual, epi, stream);
+                break;
+            }
+            [[fallthrough]];
+        default: throw NativeError(HYP_STATUS_INTERNAL, "gemv: unsupported rows per wave");
     }
 }
 
 }  // namespace
 
-void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m,
-                    uint16_t* y, Epilogue epi, float cap_bf16, hipStream_t stream) {
+GemvConfig choose_gemv_config(uint32_t m, uint32_t n, uint32_t k, bool dual) {
+    const uint32_t hg = k / 32u;
+    GemvConfig c{};
+    // Rows per wave: enough bytes in flight per wave, within the registers x leaves.
+    const uint32_t weight_rows = m * (dual ? 2u : 1u);
+    c.rows = weight_rows <= 1u ? 4u : (weight_rows <= 2u ? 4u : 2u);
+    // Waves per row: the fewest whose half-groups fit 2 per lane; more when n is
+    // too small to give every CU several waves.
+    c.splits = hg <= 128u ? 1u : (hg <= 256u ? 2u : 4u);
+    const uint32_t target_waves = device_compute_units() * 8u;
+    while (c.splits < 4u && (n / c.rows) * c.splits < target_waves) c.splits *= 2u;
+    const uint32_t per_split = (hg + c.splits - 1u) / c.splits;
+    c.halves = per_split <= 64u ? 1u : 2u;
+    return c;
+}
+
+void launch_q4_gemv_config(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
+                           Epilogue epi, float cap_bf16, const GemvConfig& c, hipStream_t stream) {
+    const uint32_t hg = w.k / 32u;
+    HYP_REQUIRE(c.splits == 1u || c.splits == 2u || c.splits == 4u, HYP_STATUS_INTERNAL, "gemv: bad split count");
+    HYP_REQUIRE(c.halves == 1u || c.halves == 2u, HYP_STATUS_INTERNAL, "gemv: bad half-groups per lane");
+    HYP_REQUIRE((hg + c.splits - 1u) / c.splits <= 64u * c.halves, HYP_STATUS_INTERNAL,
+                "gemv: k does not fit the split configuration");
     GemvParams p{};
     p.w = w.w;
     p.s = w.scales;
@@ -324,19 +342,21 @@ void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, ui
     p.n = w.n;
     p.k = w.k;
     p.cap = cap_bf16;
-    const uint32_t hg = w.k / 32u;
-    p.splits = hg <= 128u ? 1u : (hg <= 256u ? 2u : 4u);
-    // Persistent grid: kGemvBlocksPerCU workgroups per CU loop over the rows.
-    const uint32_t max_blocks = device_compute_units() * kGemvBlocksPerCU;
+    p.splits = c.splits;
     const bool dual = up != nullptr;
     switch (m) {
-        case 1: launch_m<1>(p, dual, epi, max_blocks, stream); break;
-        case 2: launch_m<2>(p, dual, epi, max_blocks, stream); break;
-        case 3: launch_m<3>(p, dual, epi, max_blocks, stream); break;
-        case 4: launch_m<4>(p, dual, epi, max_blocks, stream); break;
+        case 1: launch_m<1>(p, c, dual, epi, stream); break;
+        case 2: launch_m<2>(p, c, dual, epi, stream); break;
+        case 3: launch_m<3>(p, c, dual, epi, stream); break;
+        case 4: launch_m<4>(p, c, dual, epi, stream); break;
         default: throw NativeError(HYP_STATUS_INTERNAL, "gemv launched with m outside 1..4");
     }
     HYP_HIP_CHECK(hipGetLastError());
+}
+
+void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
+                    Epilogue epi, float cap_bf16, hipStream_t stream) {
+    launch_q4_gemv_config(w, up, x, m, y, epi, cap_bf16, choose_gemv_config(m, w.n, w.k, up != nullptr), stream);
 }
 
 }  // namespace hyperion::hip

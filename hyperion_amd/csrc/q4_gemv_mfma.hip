@@ -1,0 +1,460 @@
+// Skinny quantized matmul (decode, m <= 4 activation rows) on gfx950 MFMA.
+//
+// Replaces mlx::core::quantized_matmul(x, w, scales, biases, transpose=true, 64, 4,
+// "affine") at decode (native/hyperion_mlx/src/weights.h:26-37, called from
+// forward.cc:395,399,409,507 for q/k/v/o, forward.cc:338-343 for the MLP and
+// forward.cc:137-152 for the tied LM head).
+//
+// The op is HBM-bound (0.5625 B per weight, read once), so the design keeps the
+// vector-ALU work per weight far below what the memory stream allows:
+//  * The dot products run on the matrix cores. One v_mfma_f32_16x16x32_bf16 covers
+//    16 weight rows x 32 k: the weights are its B operand (lane j = l % 16 holds row
+//    j), the activations its A operand, and only A rows i < m carry data (rows
+//    i >= m read a copy of x row m-1; their outputs are never stored).
+//  * A packed word (8 codes, lowest k in the lowest nibble) becomes a lane's 8 bf16
+//    B values with 3 shifts and 4 v_and_or_b32: (w >> 4s) & 0x000F000F | 0x43004300
+//    is the bf16 pair (128 + q_s, 128 + q_{s+4}) exactly (bf16 128.0 has ulp 1).
+//    The A values use the same slot order: x is staged in LDS once per workgroup as
+//    (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8-element word, next to the per-group sums
+//    of x that remove the +128 offset.
+//  * The weights are read in the tiled resident layout (q4_layout.h): per 16-row tile
+//    and pair of groups, lane (j, kb = l / 16) loads one contiguous 16-byte entry
+//    holding words 2kb and 2kb+1 of row j for both groups (the wave reads 1 KB of
+//    contiguous bytes per instruction), and lane j one 8-byte entry with both groups'
+//    scale and bias (128 contiguous bytes). A group is 2 MFMAs (words {0,2,4,6}, then
+//    {1,3,5,7}) into a fresh accumulator, after which lane j < 16 applies the group's
+//    bf16 scale and bias:
+//        y[i][j] += s * (acc[i][j] - 128 * sum_g(x_i)) + b * sum_g(x_i).
+//    Every partial product is exact in fp32 and accumulation is fp32. The two groups
+//    of a pair are independent accumulator chains, so the matrix core and the VALU
+//    overlap.
+//  * A wave owns 16 rows and every S-th pair of groups (S waves of a workgroup share
+//    the rows and meet in LDS at the end). Loads go through buffer resources: the
+//    lane's offset is a VGPR, the pair offset a scalar, so addressing costs no VALU.
+//    x is requested first (loads retire in order), then two batches of weights.
+#include "common.h"
+#include "kernels.h"
+#include "q4_layout.h"
+
+namespace hyperion::hip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+constexpr uint32_t kNibbleMask = 0x000F000Fu;
+constexpr uint32_t kMagic128 = 0x43004300u;   // bf16 pair (128.0, 128.0)
+constexpr uint32_t kOnePair = 0x3F803F80u;    // bf16 pair (1.0, 1.0)
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// (w & mask) | bits. With mask and bits held in VGPRs (see the kernel), this is one
+// v_and_or_b32; as literals it would split into two VOP2 ops, because GFX9 VOP3
+// encodings take no literal constants and read at most one SGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t bits) {
+    return (w & mask) | bits;
+}
+
+// The 8 codes of a packed word as MFMA B values (128+q0, 128+q4, 128+q1, 128+q5, ...).
+__device__ __forceinline__ bf16x8_t code_frag(uint32_t w, uint32_t mask, uint32_t bits) {
+    uint4 r;
+    r.x = and_or(w, mask, bits);
+    r.y = and_or(w >> 4, mask, bits);
+    r.z = and_or(w >> 8, mask, bits);
+    r.w = and_or(w >> 12, mask, bits);
+    return __builtin_bit_cast(bf16x8_t, r);
+}
+
+// 128-bit buffer resource over [base, base + bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+struct SkinnyParams {
+    const uint4* codes;    // tiled codes (q4_layout.h)
+    const uint2* sb;       // tiled scales and biases
+    const uint4* codes2;   // fused gate/up: the up projection (same n, k)
+    const uint2* sb2;
+    const uint16_t* x;
+    uint16_t* y;
+    uint32_t n;
+    uint32_t k;
+    uint32_t pairs;       // ceil(k / 128)
+    uint32_t splits;      // waves sharing one 16-row tile: 1, 2 or 4
+    float cap;            // bf16 softcap constant
+};
+
+// One matrix as seen by one lane: buffer resources and the lane's offsets into them.
+struct LaneMatrix {
+    __amdgpu_buffer_rsrc_t codes;
+    __amdgpu_buffer_rsrc_t sb;
+    uint32_t c_off;    // (tile * pairs * 64 + lane) * 16 bytes
+    uint32_t sb_off;   // (tile * pairs * 16 + j) * 8 bytes
+};
+
+// P pairs of groups of one matrix for one lane.
+template <int P>
+struct Batch {
+    uint4 w[P];    // words 2kb, 2kb+1 of the pair's two groups
+    uint2 sb[P];   // (scale | bias << 16) of the pair's two groups
+};
+
+// Pairs first, first + stride, ... (wave-uniform, so the clamp is a scalar op);
+// indices past `last` are clamped to it, so every byte read lies inside the tile.
+template <int P>
+__device__ __forceinline__ void load_batch(const LaneMatrix& lm, uint32_t first, uint32_t stride, uint32_t last,
+                                           Batch<P>& bt) {
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const uint32_t gp = min(first + i * stride, last);
+        bt.w[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(lm.codes, lm.c_off, gp * 1024u, 0));
+        bt.sb[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(lm.sb, lm.sb_off, gp * 128u, 0));
+    }
+}
+
+// y += s * (acc - 128 * sum(x)) + b * sum(x) for one group (acc[m] is D[i = m][j] on
+// lanes j < 16 for m < 4; sxg has the group's sums of x rows 0..3).
+template <int M>
+__device__ __forceinline__ void group_scale(const f32x4_t& acc, uint32_t sbw, const float4& sxg, float (&y)[M]) {
+    const float sc = bf16_bits_to_f32(sbw & 0xFFFFu);
+    const float bi = bf16_bits_to_f32(sbw >> 16);
+    const float sxv[4] = {sxg.x, sxg.y, sxg.z, sxg.w};
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        y[m] = fmaf(sc, fmaf(-128.0f, sxv[m], acc[m]), y[m]);
+        y[m] = fmaf(bi, sxv[m], y[m]);
+    }
+}
+
+// Operands of one pair: the 4 B fragments per matrix (groups g0, g1 x two MFMA
+// steps) and the 4 A fragments they meet.
+template <int NW>
+struct PairOperands {
+    bf16x8_t b[NW][4];
+    uint4 a[4];
+};
+
+template <int NW, int P>
+__device__ __forceinline__ void load_operands(const Batch<P> (&bt)[NW], int i, const uint4* xa, uint32_t g0,
+                                              uint32_t G, uint32_t mask, uint32_t bits, PairOperands<NW>& op) {
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+        op.b[q][0] = code_frag(bt[q].w[i].x, mask, bits);
+        op.b[q][1] = code_frag(bt[q].w[i].y, mask, bits);
+        op.b[q][2] = code_frag(bt[q].w[i].z, mask, bits);
+        op.b[q][3] = code_frag(bt[q].w[i].w, mask, bits);
+    }
+    const uint32_t g1 = min(g0 + 1u, G - 1u);   // an odd group count leaves the last pair half empty
+    op.a[0] = xa[g0 * 8u];
+    op.a[1] = xa[g0 * 8u + 1u];
+    op.a[2] = xa[g1 * 8u];
+    op.a[3] = xa[g1 * 8u + 1u];
+}
+
+// The valid pairs of batch `bt` (its first pair is the wave's pair number `base`),
+// software-pipelined: pair i's MFMAs are issued, then pair i+1's operands are
+// converted and read from LDS while they run, then pair i is scaled.
+template <int M, int NW, int P>
+__device__ __forceinline__ void compute_batch(const Batch<P> (&bt)[NW], uint32_t base, uint32_t cnt,
+                                              uint32_t split, uint32_t S, uint32_t G, const uint4* xa,
+                                              const float4* sx, uint32_t mask, uint32_t bits, float (&y)[NW][M]) {
+    PairOperands<NW> op;
+    load_operands<NW, P>(bt, 0, xa, 2u * (split + base * S), G, mask, bits, op);
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        if (base + i >= cnt) break;   // wave-uniform
+        const uint32_t gp = split + (base + i) * S;
+        const uint32_t g0 = 2u * gp;
+        const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t acc0[NW], acc1[NW];
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+            acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, op.a[0]), op.b[q][0],
+                                                              zero, 0, 0, 0);
+            acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, op.a[2]), op.b[q][2],
+                                                              zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+            acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, op.a[1]), op.b[q][1],
+                                                              acc0[q], 0, 0, 0);
+            acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, op.a[3]), op.b[q][3],
+                                                              acc1[q], 0, 0, 0);
+        }
+        uint2 sbw[NW];
+#pragma unroll
+        for (int q = 0; q < NW; ++q) sbw[q] = bt[q].sb[i];
+        if (i + 1 < P && base + i + 1 < cnt) load_operands<NW, P>(bt, i + 1, xa, 2u * (gp + S), G, mask, bits, op);
+        const float4 sx0 = sx[g0];
+#pragma unroll
+        for (int q = 0; q < NW; ++q) group_scale<M>(acc0[q], sbw[q].x, sx0, y[q]);
+        if (g0 + 1u < G) {
+            const float4 sx1 = sx[g0 + 1u];
+#pragma unroll
+            for (int q = 0; q < NW; ++q) group_scale<M>(acc1[q], sbw[q].y, sx1, y[q]);
+        }
+    }
+}
+
+template <int M, bool DUAL, int EPI, int P>
+__global__ __launch_bounds__(kThreads) void q4_skinny_kernel(SkinnyParams p) {
+    constexpr int NW = DUAL ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) uint4 smem[];
+
+    const uint32_t k = p.k;
+    const uint32_t W = k / 8u;    // packed words per row
+    const uint32_t G = k / 64u;   // groups per row
+    uint4* xs = smem;                                              // [M][W] permuted x
+    float4* sx = reinterpret_cast<float4*>(smem + M * W);          // [G] group sums of x rows 0..3
+    float* red = reinterpret_cast<float*>(sx + G);                 // [kWaves][NW][M][16]
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t S = p.splits;
+    const uint32_t split = wave % S;
+    const uint32_t tile = blockIdx.x * (kWaves / S) + wave / S;
+    const uint32_t j = lane & 15u;
+    const uint32_t kb = lane >> 4;
+    const uint32_t pairs = p.pairs;
+    const uint32_t tiles = (p.n + kTileRows - 1u) / kTileRows;
+    const uint32_t ltile = min(tile, tiles - 1u);   // tiles past the matrix are loaded, never stored
+
+    // This wave's pairs: split, split + S, ... (cnt of them; cnt >= 1 since pairs >= S).
+    const uint32_t cnt = (pairs - split + S - 1u) / S;
+    const uint32_t last = pairs - 1u;
+
+    // x first: the staging below waits only for these loads.
+    const uint32_t xu0 = threadIdx.x;   // first (row, group) unit this thread stages
+    uint4 xv[8];
+    if (xu0 < M * G) {
+        const uint32_t m = xu0 / G;
+        const uint32_t g = xu0 - m * G;
+        const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xv[t] = src[t];
+    }
+
+    const uint32_t c_bytes = tiles * pairs * 1024u;
+    const uint32_t s_bytes = tiles * pairs * 128u;
+    LaneMatrix lm[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+        lm[q].codes = buffer_rsrc(q == 0 ? p.codes : p.codes2, c_bytes);
+        lm[q].sb = buffer_rsrc(q == 0 ? p.sb : p.sb2, s_bytes);
+        lm[q].c_off = (ltile * pairs * 64u + lane) * 16u;
+        lm[q].sb_off = (ltile * pairs * 16u + j) * 8u;
+    }
+
+    // Two batches of weights in flight before the first arithmetic.
+    Batch<P> ba[NW], bb[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split, S, last, ba[q]);
+#pragma unroll
+    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + P * S, S, last, bb[q]);
+
+    // Stage x: each thread permutes whole groups (8 words) and sums them.
+    for (uint32_t u = xu0; u < M * G; u += kThreads) {
+        const uint32_t m = u / G;
+        const uint32_t g = u - m * G;
+        if (u != xu0) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) xv[t] = src[t];
+        }
+        float s0 = 0.0f;
+        float s1 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint4 o;
+            o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
+            o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
+            o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
+            o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
+            xs[m * W + g * 8u + t] = o;
+            s0 = dot2_bf16(xv[t].x, kOnePair, s0);
+            s1 = dot2_bf16(xv[t].y, kOnePair, s1);
+            s0 = dot2_bf16(xv[t].z, kOnePair, s0);
+            s1 = dot2_bf16(xv[t].w, kOnePair, s1);
+        }
+        reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
+    }
+    __syncthreads();
+
+    // Opaque VGPR values, so (w & mask) | bits selects v_and_or_b32 (see and_or).
+    uint32_t mask = kNibbleMask;
+    uint32_t bits = kMagic128;
+    asm volatile("" : "+v"(mask), "+v"(bits));
+
+    const uint32_t arow = min(j, static_cast<uint32_t>(M - 1));   // A row this lane supplies
+    const uint4* xa = xs + arow * W + kb * 2u;
+
+    float y[NW][M];
+#pragma unroll
+    for (int q = 0; q < NW; ++q)
+#pragma unroll
+        for (int m = 0; m < M; ++m) y[q][m] = 0.0f;
+
+    // Ping-pong over two register batches: compute one, refill it two batches ahead.
+    for (uint32_t base = 0; base < cnt; base += 2 * P) {
+        compute_batch<M, NW, P>(ba, base, cnt, split, S, G, xa, sx, mask, bits, y);
+        if (base + 2 * P < cnt) {
+#pragma unroll
+            for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + (base + 2 * P) * S, S, last, ba[q]);
+        }
+        if (base + P >= cnt) break;
+        compute_batch<M, NW, P>(bb, base + P, cnt, split, S, G, xa, sx, mask, bits, y);
+        if (base + 3 * P < cnt) {
+#pragma unroll
+            for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + (base + 3 * P) * S, S, last, bb[q]);
+        }
+    }
+
+    if (S > 1u) {
+        if (kb == 0u) {
+#pragma unroll
+            for (int q = 0; q < NW; ++q)
+#pragma unroll
+                for (int m = 0; m < M; ++m) red[((wave * NW + q) * M + m) * kTileRows + j] = y[q][m];
+        }
+        __syncthreads();
+        if (split == 0u) {
+#pragma unroll
+            for (int q = 0; q < NW; ++q)
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    float v = y[q][m];
+                    for (uint32_t s2 = 1; s2 < S; ++s2)
+                        v += red[(((wave + s2) * NW + q) * M + m) * kTileRows + j];
+                    y[q][m] = v;
+                }
+        }
+    }
+
+    const uint32_t out_row = tile * kTileRows + j;
+    if (split == 0u && kb == 0u && out_row < p.n) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float out = round_bf16(y[0][m]);
+            if constexpr (DUAL) {
+                const float up = round_bf16(y[NW - 1][m]);
+                out = round_bf16(gelu_tanh_bf16_chain(out) * up);
+            } else if constexpr (EPI == static_cast<int>(Epilogue::kSoftcap)) {
+                out = softcap_bf16(out, p.cap);
+            }
+            p.y[static_cast<size_t>(m) * p.n + out_row] = f32_to_bf16_bits(out);
+        }
+    }
+}
+
+size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual) {
+    const size_t W = k / 8u;
+    const size_t G = k / 64u;
+    return m * W * 16u + G * 16u + static_cast<size_t>(kWaves) * (dual ? 2u : 1u) * m * kTileRows * 4u;
+}
+
+size_t max_lds_per_block();
+
+template <int M, bool DUAL, int EPI>
+void launch_skinny_t(const SkinnyParams& p, hipStream_t stream) {
+    constexpr int P = 2;   // pairs per register batch (two batches in flight)
+    auto kernel = q4_skinny_kernel<M, DUAL, EPI, P>;
+    const size_t lds = skinny_lds_bytes(M, p.k, DUAL);
+    if (lds > 65536u) {
+        static thread_local int configured_device = -1;
+        int dev = 0;
+        HYP_HIP_CHECK(hipGetDevice(&dev));
+        if (configured_device != dev) {
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(max_lds_per_block())));
+            configured_device = dev;
+        }
+    }
+    const uint32_t tiles = (p.n + kTileRows - 1u) / kTileRows;
+    const uint32_t tiles_per_block = kWaves / p.splits;
+    const dim3 grid((tiles + tiles_per_block - 1u) / tiles_per_block);
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, stream, p);
+}
+
+template <int M>
+void launch_skinny_m(const SkinnyParams& p, bool dual, Epilogue epi, hipStream_t stream) {
+    if (dual) {
+        launch_skinny_t<M, true, 0>(p, stream);
+    } else if (epi == Epilogue::kSoftcap) {
+        launch_skinny_t<M, false, 1>(p, stream);
+    } else {
+        launch_skinny_t<M, false, 0>(p, stream);
+    }
+}
+
+size_t max_lds_per_block() {
+    static thread_local int cached_device = -1;
+    static thread_local size_t cached = 0;
+    int dev = 0;
+    HYP_HIP_CHECK(hipGetDevice(&dev));
+    if (dev != cached_device) {
+        int v = 0;
+        HYP_HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+        cached = static_cast<size_t>(v);
+        cached_device = dev;
+    }
+    return cached;
+}
+
+}  // namespace
+
+uint32_t choose_skinny_splits(uint32_t n, uint32_t k) {
+    // 4 waves per tile while that stays within 32 waves per CU, else 2 (the fastest
+    // choices measured on the 15360 x 3840 decode and 262144 x 3840 LM-head shapes);
+    // never more splits than group pairs.
+    const TiledDims d = TiledDims::of(n, k);
+    uint32_t s = d.tiles * 4u <= device_compute_units() * 32u ? 4u : 2u;
+    while (s > 1u && d.pairs < s) s /= 2u;
+    return s;
+}
+
+bool skinny_supported(uint32_t m, uint32_t k, bool dual) {
+    return m >= 1u && m <= kSkinnyMaxM && skinny_lds_bytes(m, k, dual) <= max_lds_per_block();
+}
+
+void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
+                      Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream) {
+    const TiledDims d = TiledDims::of(w.n, w.k);
+    HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr && (up == nullptr || (up->codes != nullptr && up->sb != nullptr)),
+                HYP_STATUS_INTERNAL, "skinny: weights are not in the tiled resident layout");
+    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u, HYP_STATUS_INTERNAL, "skinny: bad split count");
+    HYP_REQUIRE(d.pairs >= splits, HYP_STATUS_INTERNAL, "skinny: fewer group pairs than splits");
+    HYP_REQUIRE(skinny_supported(m, w.k, up != nullptr), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
+    HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INTERNAL, "skinny: matrix exceeds 2 GiB of packed codes");
+    SkinnyParams p{};
+    p.codes = w.codes;
+    p.sb = w.sb;
+    p.codes2 = up ? up->codes : nullptr;
+    p.sb2 = up ? up->sb : nullptr;
+    p.x = x;
+    p.y = y;
+    p.n = w.n;
+    p.k = w.k;
+    p.pairs = d.pairs;
+    p.cap = cap_bf16;
+    p.splits = splits;
+    const bool dual = up != nullptr;
+    switch (m) {
+        case 1: launch_skinny_m<1>(p, dual, epi, stream); break;
+        case 2: launch_skinny_m<2>(p, dual, epi, stream); break;
+        case 3: launch_skinny_m<3>(p, dual, epi, stream); break;
+        case 4: launch_skinny_m<4>(p, dual, epi, stream); break;
+        default: throw NativeError(HYP_STATUS_INTERNAL, "skinny launched with m outside 1..4");
+    }
+    HYP_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace hyperion::hip

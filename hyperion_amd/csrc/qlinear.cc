@@ -3,6 +3,8 @@
 // native/hyperion_mlx/src/weights.h:14-17).
 #include "qlinear.h"
 
+#include "q4_layout.h"
+
 #include <utility>
 
 namespace hyperion::hip {
@@ -59,17 +61,21 @@ namespace {
 
 constexpr size_t align256(size_t v) { return (v + 255u) & ~size_t{255u}; }
 
+// One allocation: MLX-layout codes | scales | biases | tiled codes | tiled scales.
 struct Sizes {
-    size_t w, s, off_s, off_b, total;
+    size_t w, s, off_s, off_b, off_codes, off_sb, total;
 };
 
 Sizes sizes_for(uint32_t n, uint32_t k) {
+    const hip::TiledDims d = hip::TiledDims::of(n, k);
     Sizes z{};
     z.w = static_cast<size_t>(n) * (k / 8u) * sizeof(uint32_t);
     z.s = static_cast<size_t>(n) * (k / 64u) * sizeof(uint16_t);
     z.off_s = align256(z.w);
     z.off_b = z.off_s + align256(z.s);
-    z.total = z.off_b + align256(z.s);
+    z.off_codes = z.off_b + align256(z.s);
+    z.off_sb = z.off_codes + align256(d.code_bytes());
+    z.total = z.off_sb + align256(d.sb_bytes());
     return z;
 }
 
@@ -81,9 +87,17 @@ QuantizedLinear make_storage(uint32_t n, uint32_t k, Sizes& z) {
     q.mat.w = reinterpret_cast<const uint32_t*>(base);
     q.mat.scales = reinterpret_cast<const uint16_t*>(base + z.off_s);
     q.mat.biases = reinterpret_cast<const uint16_t*>(base + z.off_b);
+    q.mat.codes = reinterpret_cast<const uint4*>(base + z.off_codes);
+    q.mat.sb = reinterpret_cast<const uint2*>(base + z.off_sb);
     q.mat.n = n;
     q.mat.k = k;
     return q;
+}
+
+// Builds the tiled copy from the MLX-layout copy (stream-ordered).
+void tile(QuantizedLinear& q, hipStream_t stream) {
+    hip::launch_q4_tile(q.mat.w, q.mat.scales, q.mat.biases, q.mat.n, q.mat.k, const_cast<uint4*>(q.mat.codes),
+                        const_cast<uint2*>(q.mat.sb), stream);
 }
 
 }  // namespace
@@ -96,6 +110,8 @@ QuantizedLinear QuantizedLinear::from_host(const uint32_t* w, const uint16_t* sc
     HYP_HIP_CHECK(hipMemcpy(base, w, z.w, hipMemcpyHostToDevice));
     HYP_HIP_CHECK(hipMemcpy(base + z.off_s, scales, z.s, hipMemcpyHostToDevice));
     HYP_HIP_CHECK(hipMemcpy(base + z.off_b, biases, z.s, hipMemcpyHostToDevice));
+    tile(q, nullptr);
+    HYP_HIP_CHECK(hipStreamSynchronize(nullptr));
     return q;
 }
 
@@ -108,12 +124,17 @@ QuantizedLinear QuantizedLinear::from_device(const uint32_t* w, const uint16_t* 
     HYP_HIP_CHECK(hipMemcpyAsync(base, w, z.w, hipMemcpyDeviceToDevice, stream));
     HYP_HIP_CHECK(hipMemcpyAsync(base + z.off_s, scales, z.s, hipMemcpyDeviceToDevice, stream));
     HYP_HIP_CHECK(hipMemcpyAsync(base + z.off_b, biases, z.s, hipMemcpyDeviceToDevice, stream));
+    tile(q, stream);
     return q;
 }
 
 void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream, Epilogue epi,
                             float cap_bf16) const {
     if (m == 0) return;
+    if (hip::skinny_supported(m, mat.k, false)) {
+        hip::launch_q4_skinny(mat, nullptr, x, m, y, epi, cap_bf16, hip::choose_skinny_splits(mat.n, mat.k), stream);
+        return;
+    }
     if (m <= hip::kGemvMaxM && mat.k <= hip::kGemvMaxK) {
         hip::launch_q4_gemv(mat, nullptr, x, m, y, epi, cap_bf16, stream);
         return;
@@ -127,6 +148,11 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
 void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const uint16_t* x, uint32_t m,
                  uint16_t* h, hipStream_t stream) {
     if (m == 0) return;
+    if (hip::skinny_supported(m, gate.mat.k, true)) {
+        hip::launch_q4_skinny(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f,
+                              hip::choose_skinny_splits(gate.mat.n, gate.mat.k), stream);
+        return;
+    }
     if (m <= hip::kGemvMaxM && gate.mat.k <= hip::kGemvMaxK) {
         hip::launch_q4_gemv(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f, stream);
         return;
