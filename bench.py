@@ -1,15 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the Q4/g64 quantized-linear path on one MI355X.
 
-Headline (the `value`): decode GEMV bandwidth on the decode workload
+Headline (`value`): the decode GEMV
   x bf16 [1,3840] . dequant(W [15360,3840] Q4/g64)^T  ->  y bf16 [1,15360]
-measured cold: the timed launches rotate over distinct device copies of the weight
-whose total exceeds the 256 MB Infinity Cache, so every launch streams from HBM.
-A step is one GEMV launch; `value` = algorithmic bytes per launch / mean launch time.
+timed cold: the launches rotate over distinct device copies of W whose total exceeds
+the 256 MB Infinity Cache, so every launch streams its weights from HBM. A step is one
+launch; value = algorithmic bytes per launch / mean launch time, both measured with HIP
+events on the stream the kernel runs on.
 
-Also reported: the prefill GEMM (seven projections of a Gemma-class 12B decoder layer
-at M=2048) in TFLOP/s against the bf16 MFMA peak, and the oracle's restatement of
-MLX's CPU quantized_matmul timed on this host (the CPU baseline).
+Also reported, each on its own workload:
+  quantize    bf16 W [15360,3840] N(0, 0.02^2) with 1% x8 outliers -> Q4/g64 (GB/s)
+  layer       one decoder layer's linear stack (q, k, v, o, fused gate/up + GELU, down)
+              at m = 1 and 4, cold (part of the decode stream below)
+  prefill     the seven projections at m = 512 and 2048 (TFLOP/s vs bf16 MFMA peak)
+  decode      48 layers + tied LM head [262144,3840] with softcap, the hidden state
+              renormalised between layers, m = 1 and 4, replayed from a captured HIP
+              graph (tokens/s and effective HBM GB/s)
+and the oracle's restatement of MLX's CPU quantized_matmul timed on this host's cores
+(cpu_baseline).
 
 Progress goes to stderr; stdout carries exactly one JSON line.
 """
@@ -17,6 +25,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -31,19 +40,26 @@ from hyperion_amd import synthetic as syn  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 DECODE_N, DECODE_K = 15360, 3840
+HIDDEN = syn.HIDDEN
+METRIC = "Q4/g64 qmatmul: decode GB/s (% HBM peak) + prefill TFLOPS (% MFMA peak)"
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def decode_bytes(m, n, k):
-    """Algorithmic bytes of one Q4/g64 GEMV launch: packed codes (0.5 B/weight) +
-    bf16 scale and bias per 64 weights + x + y."""
-    return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * m * k + 2 * m * n
+def q4_bytes(n, k):
+    """Packed codes (0.5 B/weight) + bf16 scale and bias per 64 weights."""
+    return n * k // 2 + 4 * n * (k // 64)
+
+
+def gemv_bytes(m, n, k):
+    """Algorithmic bytes of one launch: the Q4 matrix + x + y (bf16)."""
+    return q4_bytes(n, k) + 2 * m * k + 2 * m * n
 
 
 def time_launches(stream, fn, steps, warmup):
+    """Mean milliseconds per call of fn(i), from HIP events recorded on `stream`."""
     for i in range(warmup):
         fn(i)
     stream.synchronize()
@@ -55,49 +71,57 @@ def time_launches(stream, fn, steps, warmup):
     ms = e0.elapsed_ms(e1)
     e0.close()
     e1.close()
-    return ms
+    return ms / steps
 
 
-def bench_decode(stream, steps, warmup, copies):
-    n, k = DECODE_N, DECODE_K
-    log(f"decode GEMV m=1 n={n} k={k}: generating weights, {copies} device copies")
-    w, s, b = syn.q4_weights(n, k, seed=105)
-    x = syn.activations(1, k, seed=104)
-    base = hy.QWeight.from_host(w, s, b)
+def device_copies(w, s, b, n, k, copies, stream):
+    """`copies` resident projections with the same values in distinct HBM buffers."""
     wd = hy.DeviceArray.from_host(w, stream)
     sd = hy.DeviceArray.from_host(s, stream)
     bd = hy.DeviceArray.from_host(b, stream)
-    qws = [base]
-    for _ in range(copies - 1):
+    out = []
+    for _ in range(copies):
         h = ctypes.c_void_p()
         hy.call("hyp_qweight_create_device", wd.ptr, sd.ptr, bd.ptr, n, k, 64, 4, stream.handle, ctypes.byref(h))
-        qws.append(hy.QWeight(h))
+        out.append(hy.QWeight(h))
     stream.synchronize()
-    xd = hy.DeviceArray.from_host(x, stream)
+    return out
+
+
+def bench_decode_gemv(stream, steps, warmup, copies):
+    n, k = DECODE_N, DECODE_K
+    log(f"decode GEMV m=1 n={n} k={k}: {copies} device copies")
+    w, s, b = syn.q4_weights(n, k, seed=105)
+    qws = device_copies(w, s, b, n, k, copies, stream)
+    xd = hy.DeviceArray.from_host(syn.activations(1, k, seed=104), stream)
     yd = hy.DeviceArray((1, n), np.uint16)
-
-    def cold(i):
-        hy.qmatmul(qws[i % copies], xd, 1, yd, stream)
-
-    def warm(i):
-        hy.qmatmul(base, xd, 1, yd, stream)
-
-    ms_cold = time_launches(stream, cold, steps, warmup)
-    ms_warm = time_launches(stream, warm, steps, warmup)
-    nbytes = decode_bytes(1, n, k)
-    per_cold = ms_cold / steps
-    per_warm = ms_warm / steps
-    log(f"decode cold {per_cold * 1e3:.2f} us/launch = {nbytes / per_cold / 1e6:.0f} GB/s; "
-        f"warm {per_warm * 1e3:.2f} us = {nbytes / per_warm / 1e6:.0f} GB/s")
+    cold = time_launches(stream, lambda i: hy.qmatmul(qws[i % copies], xd, 1, yd, stream), steps, warmup)
+    warm = time_launches(stream, lambda i: hy.qmatmul(qws[0], xd, 1, yd, stream), steps, warmup)
+    nbytes = gemv_bytes(1, n, k)
+    log(f"decode cold {cold * 1e3:.2f} us/launch = {nbytes / cold / 1e6:.0f} GB/s; "
+        f"warm {warm * 1e3:.2f} us = {nbytes / warm / 1e6:.0f} GB/s")
     for q in qws:
         q.close()
-    return {"ms_total": ms_cold, "ms_per_launch": per_cold, "bytes": nbytes,
-            "warm_ms_per_launch": per_warm, "copies": copies,
-            "cold_working_set_bytes": copies * nbytes}
+    return {"ms_per_launch": cold, "warm_ms_per_launch": warm, "bytes": nbytes, "copies": copies}
+
+
+def bench_quantize(stream, steps, warmup, copies=4):
+    n, k = DECODE_N, DECODE_K
+    log(f"quantize/pack n={n} k={k}: {copies} input copies")
+    wb = syn.quantize_input(n, k, seed=101)
+    ins = [hy.DeviceArray.from_host(wb, stream) for _ in range(copies)]
+    wq = hy.DeviceArray((n, k // 8), np.uint32)
+    sq = hy.DeviceArray((n, k // 64), np.uint16)
+    bq = hy.DeviceArray((n, k // 64), np.uint16)
+    ms = time_launches(stream, lambda i: hy.quantize(ins[i % copies], n, k, wq, sq, bq, stream), steps, warmup)
+    nbytes = 2 * n * k + q4_bytes(n, k)
+    log(f"quantize {ms * 1e3:.2f} us = {nbytes / ms / 1e6:.0f} GB/s")
+    return {"workload": f"bf16 [{n},{k}] -> Q4/g64", "us": round(ms * 1e3, 2), "bytes": nbytes,
+            "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def bench_prefill(stream, m, steps, warmup):
-    log(f"prefill GEMM m={m}: seven projections")
+    log(f"prefill m={m}: seven projections")
     per = {}
     total_flops = 0
     total_ms = 0.0
@@ -106,22 +130,84 @@ def bench_prefill(stream, m, steps, warmup):
         qw = hy.QWeight.from_host(w, s, b)
         xd = hy.DeviceArray.from_host(syn.activations(m, k, seed=400 + i), stream)
         yd = hy.DeviceArray((m, n), np.uint16)
-        ms = time_launches(stream, lambda _i: hy.qmatmul(qw, xd, m, yd, stream), steps, warmup) / steps
+        ms = time_launches(stream, lambda _i: hy.qmatmul(qw, xd, m, yd, stream), steps, warmup)
         flops = 2 * m * n * k
-        per[name] = {"n": n, "k": k, "ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1)}
+        per[name] = {"n": n, "k": k, "us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1)}
         total_flops += flops
         total_ms += ms
-        log(f"  {name:5s} n={n:5d} k={k:5d}: {ms:.3f} ms  {flops / ms / 1e9:.0f} TFLOP/s")
+        log(f"  {name:5s} n={n:5d} k={k:5d}: {ms * 1e3:8.1f} us  {flops / ms / 1e9:6.0f} TFLOP/s")
         qw.close()
     tflops = total_flops / total_ms / 1e9
-    log(f"prefill layer m={m}: {total_ms:.3f} ms  {tflops:.0f} TFLOP/s")
-    return {"m": m, "layer_ms": round(total_ms, 4), "tflops": round(tflops, 1),
+    log(f"prefill layer m={m}: {total_ms * 1e3:.1f} us  {tflops:.0f} TFLOP/s")
+    return {"m": m, "layer_us": round(total_ms * 1e3, 1), "tflops": round(tflops, 1),
             "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "per_projection": per}
 
 
+class DecodeModel:
+    """Random-init Q4 weights of a Gemma-class 12B decoder's linear layers (every layer
+    with v_proj) and its tied embedding table, resident in HBM."""
+
+    def __init__(self, layers, stream):
+        self.layers = []
+        t0 = time.perf_counter()
+        for li in range(layers):
+            proj = {}
+            for pi, (name, (n, k)) in enumerate(syn.LAYER_SHAPES.items()):
+                w, s, b = syn.q4_weights(n, k, seed=10_000 + 16 * li + pi)
+                proj[name] = hy.QWeight.from_host(w, s, b)
+            self.layers.append(proj)
+        w, s, b = syn.q4_weights(syn.VOCAB, HIDDEN, seed=9_999)
+        self.embed = hy.QWeight.from_host(w, s, b)
+        self.weight_bytes = layers * sum(q4_bytes(n, k) for n, k in syn.LAYER_SHAPES.values()) + \
+            q4_bytes(syn.VOCAB, HIDDEN)
+        log(f"decode model: {layers} layers + LM head, {self.weight_bytes / 1e9:.2f} GB of Q4 weights "
+            f"({time.perf_counter() - t0:.1f} s to build)")
+
+    def close(self):
+        for proj in self.layers:
+            for q in proj.values():
+                q.close()
+        self.embed.close()
+
+
+def decode_step(model, m, bufs, stream):
+    """One decode step's linear stack: per layer q, k, v from h; o from q's output; the
+    fused gate/up GELU from o's output; down; renormalise into h. Then the tied LM head
+    with softcap 30 on h."""
+    h, q, kv, o, g, logits = bufs
+    for proj in model.layers:
+        hy.qmatmul(proj["q"], h, m, q, stream)
+        hy.qmatmul(proj["k"], h, m, kv, stream)
+        hy.qmatmul(proj["v"], h, m, kv, stream)
+        hy.qmatmul(proj["o"], q, m, o, stream)
+        hy.qmlp_gate_up_gelu(proj["gate"], proj["up"], o, m, g, stream)
+        hy.qmatmul(proj["down"], g, m, h, stream)
+        hy.rms_normalize(h, m, HIDDEN, h, stream)
+    hy.qmatmul(model.embed, h, m, logits, stream, softcap=30.0)
+
+
+def bench_decode_stream(model, m, steps, warmup, stream):
+    h = hy.DeviceArray.from_host(syn.activations(m, HIDDEN, seed=77), stream)
+    bufs = (h, hy.DeviceArray((m, 4096), np.uint16), hy.DeviceArray((m, 2048), np.uint16),
+            hy.DeviceArray((m, HIDDEN), np.uint16), hy.DeviceArray((m, 15360), np.uint16),
+            hy.DeviceArray((m, syn.VOCAB), np.uint16))
+    with hy.Graph.capture(stream) as graph:
+        decode_step(model, m, bufs, stream)
+    ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup)
+    graph.close()
+    act = 2 * m * (len(model.layers) * (HIDDEN * 3 + 4096 * 2 + 2048 * 2 + HIDDEN * 2 + 15360 * 3) + HIDDEN + syn.VOCAB)
+    nbytes = model.weight_bytes + act
+    layers = len(model.layers)
+    out = {"m": m, "ms_per_step": round(ms, 4), "tokens_per_s": round(m / (ms / 1e3), 1),
+           "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+           "bytes_per_step": nbytes, "launches_per_step": 7 * layers + 1}
+    log(f"decode stream m={m}: {ms:.3f} ms/step = {out['tokens_per_s']:.0f} tok/s, {out['gbs']:.0f} GB/s")
+    return out
+
+
 def cpu_baseline(seconds):
-    """The oracle's restatement of MLX's CPU quantized_matmul (bf16 accumulation) on the
-    full decode GEMV, repeated for about `seconds` on one host core."""
+    """The oracle's restatement of MLX's CPU quantized_matmul (bf16 accumulation), on one
+    host core, over a bounded number of full decode GEMVs."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     n, k = DECODE_N, DECODE_K
@@ -135,39 +221,73 @@ def cpu_baseline(seconds):
         if time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
-    gbs = reps * decode_bytes(1, n, k) / dt / 1e9
-    log(f"cpu baseline: {reps} GEMVs in {dt:.1f} s = {gbs:.2f} GB/s (1 core)")
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full decode GEMVs [1,{k}]x[{n},{k}] Q4/g64, bf16-accumulating "
-                      f"restatement of MLX's CPU loop, {dt:.1f} s"}
+    gbs = reps * gemv_bytes(1, n, k) / dt / 1e9
+    log(f"cpu baseline: {reps} GEMVs in {dt:.1f} s = {gbs:.3f} GB/s (1 core)")
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} full decode GEMVs [1,{k}]x[{n},{k}] Q4/g64 in {dt:.1f} s with the oracle's "
+                      f"bf16-accumulating restatement of MLX's CPU quantized_matmul"}
+
+
+def measured_traffic():
+    """HBM bytes per decode-GEMV launch from the committed counter summary, if present."""
+    path = os.path.join(ROOT, "profiles", "decode_gemv_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"```json\s*(\{.*?\})\s*```", open(path).read(), flags=re.S)
+    if not m:
+        return None
+    rec = json.loads(m.group(1))
+    return rec.get("hbm_bytes_per_launch")
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=200, help="timed decode-GEMV launches")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=24, help="distinct weight copies rotated (cold HBM)")
-    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=syn.NUM_LAYERS, help="decoder layers in the decode stream")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only-decode", action="store_true", help="only the headline decode GEMV")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 5 device-to-device copies of 256 MiB (the reference kernel of known "
+                         "traffic for scaling hardware byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs on a single "
+              "MI355X; the multi-GPU sharding of the path is a design, not a measured run)", file=sys.stderr)
         sys.exit(2)
 
     info = hy.runtime_info()
     log(f"{info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units}")
     stream = hy.Stream()
-    dec = bench_decode(stream, args.steps, args.warmup, args.copies)
-    pre = None if args.no_prefill else bench_prefill(stream, 2048, args.prefill_steps, 2)
+    if args.copy_calibration:
+        nbytes = 256 << 20
+        src, dst = hy.DeviceArray((nbytes,), np.uint8), hy.DeviceArray((nbytes,), np.uint8)
+        for _ in range(5):
+            hy.call("hyp_memcpy_dtod", dst.ptr, src.ptr, nbytes, stream.handle)
+        stream.synchronize()
+        log(f"copy calibration: 5 x {nbytes} bytes device-to-device")
+    dec = bench_decode_gemv(stream, args.steps, args.warmup, args.copies)
+    extra = {}
+    if not args.only_decode:
+        extra["quantize"] = bench_quantize(stream, 50, 5)
+        extra["prefill"] = [bench_prefill(stream, m, 10, 2) for m in (512, 2048)]
+        model = DecodeModel(args.layers, stream)
+        streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
+        model.close()
+        extra["decode_stream"] = streams
+        layer_bytes = sum(q4_bytes(n, k) for n, k in syn.LAYER_SHAPES.values())
+        extra["layer"] = [{"m": s["m"], "us_per_layer_in_stream": round(s["ms_per_step"] * 1e3 / (args.layers + 1), 2),
+                           "note": "step time / (layers + 1): a 566 MB LM head is about one layer's worth of bytes",
+                           "layer_weight_bytes": layer_bytes} for s in streams]
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     per = dec["ms_per_launch"]
     gbs = dec["bytes"] / per / 1e6
     line = {
-        "metric": "Q4/g64 qmatmul: decode GB/s (% HBM peak) + prefill TFLOPS (% MFMA peak)",
+        "metric": METRIC,
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -178,16 +298,16 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
+        "data": "synthetic (seeded codes, scales and activations; random-init weights)",
         "config": {"workload": "decode GEMV x[1,3840] . W[15360,3840]^T, MLX affine Q4/g64, cold HBM "
                                f"({dec['copies']} rotated weight copies)",
                    "m": 1, "n": DECODE_N, "k": DECODE_K},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
-        "decode_warm_gbs": round(dec["bytes"] / dec["warm_ms_per_launch"] / 1e6, 1),
-        "prefill": pre,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
+        "decode_gemv_warm_gbs": round(dec["bytes"] / dec["warm_ms_per_launch"] / 1e6, 1),
         "cpu_baseline": cpu,
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
 
 

@@ -41,10 +41,11 @@ EXPORTED = [
     "hyp_stream_create", "hyp_stream_destroy", "hyp_stream_synchronize",
     "hyp_memcpy_htod", "hyp_memcpy_dtoh", "hyp_memcpy_dtod", "hyp_memset_device",
     "hyp_event_create", "hyp_event_destroy", "hyp_event_record", "hyp_event_elapsed_ms",
+    "hyp_graph_capture_begin", "hyp_graph_capture_end", "hyp_graph_launch", "hyp_graph_free",
     "hyp_qweight_create", "hyp_qweight_create_device", "hyp_qweight_free",
     "hyp_qweight_shape", "hyp_qweight_export",
     "hyp_qmatmul", "hyp_qmatmul_ex", "hyp_qmlp_gate_up_gelu",
-    "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed",
+    "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
 ]
@@ -102,6 +103,10 @@ def lib() -> ctypes.CDLL:
         "hyp_event_destroy": [_PP],
         "hyp_event_record": [_P, _P],
         "hyp_event_elapsed_ms": [_P, _P, ctypes.POINTER(ctypes.c_float)],
+        "hyp_graph_capture_begin": [_P],
+        "hyp_graph_capture_end": [_P, _PP],
+        "hyp_graph_launch": [_P, _P],
+        "hyp_graph_free": [_PP],
         "hyp_qweight_create": [_P, _P, _P, _U32, _U32, _U32, _U32, _PP],
         "hyp_qweight_create_device": [_P, _P, _P, _U32, _U32, _U32, _U32, _P, _PP],
         "hyp_qweight_free": [_PP],
@@ -113,6 +118,7 @@ def lib() -> ctypes.CDLL:
         "hyp_quantize_q4g64": [_P, _U32, _U32, _P, _P, _P, _P],
         "hyp_dequantize_q4g64": [_P, _P, _P, _U32, _U32, _P, _U32, ctypes.c_float, _P, _P],
         "hyp_embed": [_P, _P, _U32, _P, _P],
+        "hyp_rms_normalize": [_P, _U32, _U32, ctypes.c_float, _P, _P],
         "hyp_qmodel_load": [ctypes.c_char_p, _U32, _PP],
         "hyp_qmodel_free": [_PP],
         "hyp_qmodel_num_layers": [_P, ctypes.POINTER(_U32)],
@@ -195,6 +201,46 @@ class Event:
             self.close()
         except Exception:
             pass
+
+
+class Graph:
+    """A captured launch sequence: `with Graph.capture(stream) as g: ...`, then g.launch()."""
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+
+    @classmethod
+    def capture(cls, stream: "Stream") -> "_Capture":
+        return _Capture(cls(), stream)
+
+    def launch(self, stream: "Stream") -> None:
+        call("hyp_graph_launch", self._h, stream.handle)
+
+    def close(self) -> None:
+        if self._h:
+            call("hyp_graph_free", ctypes.byref(self._h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _Capture:
+    def __init__(self, graph: Graph, stream: "Stream"):
+        self.graph = graph
+        self.stream = stream
+
+    def __enter__(self) -> Graph:
+        call("hyp_graph_capture_begin", self.stream.handle)
+        return self.graph
+
+    def __exit__(self, exc_type, exc, tb):
+        status = lib().hyp_graph_capture_end(self.stream.handle, ctypes.byref(self.graph._h))
+        if exc_type is None:
+            check(status, "hyp_graph_capture_end")
+        return False
 
 
 class DeviceArray:
@@ -358,3 +404,7 @@ def dequantize(wq: DeviceArray, s: DeviceArray, b: DeviceArray, n_total: int, k:
 
 def embed(table: QWeight, ids: DeviceArray, n_ids: int, out: DeviceArray, stream: Stream) -> None:
     call("hyp_embed", table.handle, ids.ptr, n_ids, out.ptr, stream.handle)
+
+
+def rms_normalize(x: DeviceArray, m: int, k: int, y: DeviceArray, stream: Stream, eps: float = 1e-6) -> None:
+    call("hyp_rms_normalize", x.ptr, m, k, eps, y.ptr, stream.handle)

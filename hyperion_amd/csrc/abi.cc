@@ -26,6 +26,7 @@ constexpr std::uint32_t kQWeightMagic = 0x48505157U;   // "HPQW"
 constexpr std::uint32_t kQModelMagic = 0x4850514DU;    // "HPQM"
 constexpr std::uint32_t kStreamMagic = 0x48505354U;    // "HPST"
 constexpr std::uint32_t kEventMagic = 0x48504556U;     // "HPEV"
+constexpr std::uint32_t kGraphMagic = 0x48504752U;     // "HPGR"
 
 constexpr std::size_t kLastErrorCapacity = 1024;
 thread_local std::array<char, kLastErrorCapacity> g_last_error{};
@@ -108,6 +109,12 @@ struct HypStreamOpaque {
 struct HypEventOpaque {
     std::uint32_t magic = 0;
     hipEvent_t event = nullptr;
+};
+
+struct HypGraphOpaque {
+    std::uint32_t magic = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 namespace {
@@ -313,6 +320,57 @@ HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms) {
     });
 }
 
+HypStatus hyp_graph_capture_begin(HypStream stream) {
+    return abi_call("hyp_graph_capture_begin", [&] {
+        HYP_HIP_CHECK(hipStreamBeginCapture(stream_of(stream), hipStreamCaptureModeThreadLocal));
+    });
+}
+
+HypStatus hyp_graph_capture_end(HypStream stream, HypGraph* out_graph) {
+    return abi_call("hyp_graph_capture_end", [&] {
+        hipStream_t s = stream_of(stream);
+        hipGraph_t graph = nullptr;
+        const hipError_t end = hipStreamEndCapture(s, &graph);
+        REQUIRE_ARG(out_graph != nullptr, "capture end requires a non-null out handle (the capture was ended)");
+        if (end != hipSuccess) {
+            if (graph != nullptr) (void)hipGraphDestroy(graph);
+            HYP_HIP_CHECK(end);
+        }
+        auto h = std::make_unique<HypGraphOpaque>();
+        h->graph = graph;
+        const hipError_t inst = hipGraphInstantiate(&h->exec, graph, nullptr, nullptr, 0);
+        if (inst != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            HYP_HIP_CHECK(inst);
+        }
+        h->magic = kGraphMagic;
+        *out_graph = h.release();
+    });
+}
+
+HypStatus hyp_graph_launch(HypGraph graph, HypStream stream) {
+    return abi_call("hyp_graph_launch", [&] {
+        REQUIRE_ARG(graph != nullptr && graph->magic == kGraphMagic, "graph handle is invalid");
+        HYP_HIP_CHECK(hipGraphLaunch(graph->exec, stream_of(stream)));
+    });
+}
+
+HypStatus hyp_graph_free(HypGraph* graph) {
+    if (graph == nullptr) return fail(HYP_STATUS_INVALID_ARGUMENT, "free requires a non-null handle pointer");
+    if (*graph == nullptr) return ok();
+    if ((*graph)->magic != kGraphMagic) {
+        return fail(HYP_STATUS_INVALID_ARGUMENT, "handle magic mismatch (wrong type, freed, or corrupted)");
+    }
+    const hipError_t e1 = hipGraphExecDestroy((*graph)->exec);
+    const hipError_t e2 = hipGraphDestroy((*graph)->graph);
+    (*graph)->magic = 0;
+    delete *graph;
+    *graph = nullptr;
+    if (e1 != hipSuccess) return fail(HYP_STATUS_INTERNAL, hipGetErrorString(e1));
+    if (e2 != hipSuccess) return fail(HYP_STATUS_INTERNAL, hipGetErrorString(e2));
+    return ok();
+}
+
 HypStatus hyp_qweight_create(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, uint32_t n,
                              uint32_t k, uint32_t group_size, uint32_t bits, HypQWeight* out_weight) {
     return abi_call("hyp_qweight_create", [&] {
@@ -365,11 +423,7 @@ HypStatus hyp_qweight_export(HypQWeight weight, uint32_t* w, uint16_t* scales, u
     return abi_call("hyp_qweight_export", [&] {
         const QuantizedLinear& lin = qweight_ref(weight, "weight");
         REQUIRE_ARG(w != nullptr && scales != nullptr && biases != nullptr, "export requires non-null buffers");
-        const size_t wb = static_cast<size_t>(lin.mat.n) * (lin.mat.k / 8u) * 4u;
-        const size_t sb = static_cast<size_t>(lin.mat.n) * (lin.mat.k / 64u) * 2u;
-        HYP_HIP_CHECK(hipMemcpy(w, lin.mat.w, wb, hipMemcpyDeviceToHost));
-        HYP_HIP_CHECK(hipMemcpy(scales, lin.mat.scales, sb, hipMemcpyDeviceToHost));
-        HYP_HIP_CHECK(hipMemcpy(biases, lin.mat.biases, sb, hipMemcpyDeviceToHost));
+        lin.export_mlx(w, scales, biases);
     });
 }
 
@@ -446,8 +500,17 @@ HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void*
         if (n_ids == 0) return;
         REQUIRE_ARG(ids != nullptr && out != nullptr, "ids and out must be non-null device pointers");
         const float scale = round_to_bf16(std::sqrt(static_cast<float>(t.mat.k)));
-        hyperion::hip::launch_q4_dequantize(t.mat.w, t.mat.scales, t.mat.biases, t.mat.n, t.mat.k, ids, n_ids,
-                                            scale, static_cast<uint16_t*>(out), s);
+        hyperion::hip::launch_q4_dequantize_tiled(t.mat, ids, n_ids, scale, static_cast<uint16_t*>(out), s);
+    });
+}
+
+HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, void* y, HypStream stream) {
+    return abi_call("hyp_rms_normalize", [&] {
+        hipStream_t s = stream_of(stream);
+        REQUIRE_ARG(std::isfinite(eps) && eps >= 0.0f, "eps must be finite and non-negative");
+        if (m == 0 || k == 0) return;
+        REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
+        hyperion::hip::launch_rms_normalize(static_cast<const uint16_t*>(x), m, k, eps, static_cast<uint16_t*>(y), s);
     });
 }
 

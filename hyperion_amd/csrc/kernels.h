@@ -33,56 +33,41 @@ enum class Epilogue : int {
     kSoftcap = 1,   // y = softcap(bf16(acc)), forward.cc:154-160
 };
 
-// Largest m the decode GEMV handles; larger m goes to the MFMA GEMM.
-constexpr uint32_t kGemvMaxM = 4;
-// Largest k the decode GEMV handles (64 lanes x 2 half-groups x 4 waves x 32).
-constexpr uint32_t kGemvMaxK = 16384;
-
-// Launch shape of the decode GEMV: `rows` consecutive rows per wave (1, 2, 4, or 8
-// for m <= 2), `splits` waves sharing each row's K range (1, 2, 4), `halves`
-// half-groups of 32 codes per lane per row (1 or 2).
-struct GemvConfig {
-    uint32_t rows = 4;
-    uint32_t splits = 1;
-    uint32_t halves = 2;
-};
-
-// The launch shape used for an (m, n, k) problem.
-GemvConfig choose_gemv_config(uint32_t m, uint32_t n, uint32_t k, bool dual);
-
-// Decode GEMV (m <= kGemvMaxM): y[m, n] = x[m, k] . dequant(W)^T.
-// With `up` non-null it is the fused gate/up: y = gelu_chain(x.G^T) * (x.U^T).
-void launch_q4_gemv(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m,
-                    uint16_t* y, Epilogue epi, float cap_bf16, hipStream_t stream);
-// Same with an explicit launch shape (k must fit: ceil(k/32 / splits) <= 64 * halves).
-void launch_q4_gemv_config(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m,
-                           uint16_t* y, Epilogue epi, float cap_bf16, const GemvConfig& config,
-                           hipStream_t stream);
-
 // Largest m the skinny MFMA kernel handles.
 constexpr uint32_t kSkinnyMaxM = 4;
 
-// Skinny quantized matmul on MFMA (m <= kSkinnyMaxM): y[m, n] = x[m, k] . dequant(W)^T,
-// with `up` the fused gate/up as in launch_q4_gemv. `splits` (1, 2, 4) waves share
-// each 32-row tile; k / 64 >= splits.
+// Skinny quantized matmul on MFMA (m <= kSkinnyMaxM) over the tiled layout:
+// y[m, n] = x[m, k] . dequant(W)^T. With `up` non-null it is the fused gate/up:
+// y = gelu_chain(x.G^T) * (x.U^T). `splits` (1, 2, 4) waves share each 16-row tile;
+// ceil(k / 128) >= splits.
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream);
 // Splits used for an (n, k) problem, and whether (m, k) fits the kernel's LDS staging.
 uint32_t choose_skinny_splits(uint32_t n, uint32_t k);
 bool skinny_supported(uint32_t m, uint32_t k, bool dual);
 
-// Prefill GEMM on bf16 MFMA: Q4 tiles dequantized in registers, x tiles in LDS.
-// Plain bf16 output; epilogues for m > kGemvMaxM run as the elementwise kernels below.
+// Prefill GEMM on bf16 MFMA over the tiled layout: Q4 codes dequantized in registers,
+// x tiles in LDS. Plain bf16 output; epilogues for larger m run as the elementwise
+// kernels below.
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
+// Same with an explicit workgroup tile: (16 * mt) x (64 * nt), mt in {8, 16}, nt in {2, 4}.
+void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
+                           hipStream_t stream);
 
 // h = bf16(gelu_chain(h) * u) over `count` bf16 elements (in place on h).
 void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t stream);
 // y = softcap(y) over `count` bf16 elements (in place).
 void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream);
+// y[r] = x[r] / sqrt(mean(x[r]^2) + eps) for each of m rows of k bf16 (y may equal x).
+void launch_rms_normalize(const uint16_t* x, uint32_t m, uint32_t k, float eps, uint16_t* y, hipStream_t stream);
 
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,
                         uint16_t* scales, uint16_t* biases, hipStream_t stream);
+
+// The same from the tiled resident layout (the embed table).
+void launch_q4_dequantize_tiled(const Q4Matrix& w, const uint32_t* rows, uint32_t n_rows, float out_scale_bf16,
+                                uint16_t* out, hipStream_t stream);
 
 // mx.dequantize(..., bf16) of gathered rows; out_scale_bf16 != 0 multiplies each
 // value by that bf16 constant with one more rounding.

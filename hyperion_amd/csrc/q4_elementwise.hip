@@ -2,6 +2,8 @@
 // bf16 outputs and these kernels finish them:
 //   gelu_mul: h = bf16(gelu_chain(h) * u)      ForwardPass::mlp, forward.cc:338-343
 //   softcap:  y = bf16(tanh(y / cap) * cap)     ForwardPass::softcap, forward.cc:154-160
+// and the row renormalisation between chained projections:
+//   rms_normalize: y[r] = bf16(x[r] / sqrt(mean(x[r]^2) + eps)), fp32 statistics
 // Eight bf16 per thread (16-byte loads and stores; the pointers are 16-byte aligned).
 #include "common.h"
 #include "kernels.h"
@@ -62,6 +64,28 @@ __global__ __launch_bounds__(kThreads) void softcap_kernel(uint16_t* __restrict_
     }
 }
 
+// One workgroup per row; each thread sums squares over a strided slice, the wave sums
+// meet in LDS, then the row is scaled in place or into y.
+__global__ __launch_bounds__(kThreads) void rms_normalize_kernel(const uint16_t* __restrict__ x,
+                                                                 uint16_t* __restrict__ y, uint32_t k, float eps) {
+    __shared__ float partial[kThreads / 64];
+    const uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * k;
+    uint16_t* yr = y + static_cast<size_t>(blockIdx.x) * k;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < k; i += kThreads) {
+        const float v = bf16_bits_to_f32(xr[i]);
+        ss = fmaf(v, v, ss);
+    }
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((threadIdx.x & 63u) == 0u) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) total += partial[w];
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(k) + eps);
+    for (uint32_t i = threadIdx.x; i < k; i += kThreads) yr[i] = f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) * inv);
+}
+
 dim3 grid_for(uint64_t count) {
     const uint64_t blocks = (count + 8u * kThreads - 1) / (8u * kThreads);
     HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "elementwise: tensor too large");
@@ -79,6 +103,12 @@ void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t
 void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream) {
     if (count == 0) return;
     hipLaunchKernelGGL(softcap_kernel, grid_for(count), dim3(kThreads), 0, stream, y, cap_bf16, count);
+    HYP_HIP_CHECK(hipGetLastError());
+}
+
+void launch_rms_normalize(const uint16_t* x, uint32_t m, uint32_t k, float eps, uint16_t* y, hipStream_t stream) {
+    if (m == 0 || k == 0) return;
+    hipLaunchKernelGGL(rms_normalize_kernel, dim3(m), dim3(kThreads), 0, stream, x, y, k, eps);
     HYP_HIP_CHECK(hipGetLastError());
 }
 

@@ -10,6 +10,7 @@
 // so a wave moves 1 KB of contiguous bf16 per instruction.
 #include "common.h"
 #include "kernels.h"
+#include "q4_layout.h"
 
 namespace hyperion::hip {
 namespace {
@@ -106,6 +107,47 @@ __global__ __launch_bounds__(kThreads) void q4_quantize_kernel(const uint16_t* _
     }
 }
 
+// The 8 bf16 outputs of one packed word: bf16(bf16(s*q) + b), optionally times a bf16
+// constant with one more rounding.
+__device__ __forceinline__ uint4 dequant_word_mlx(uint32_t word, float s, float b, float out_scale) {
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float q = static_cast<float>((word >> (4 * e)) & 0xFu);
+        float val = round_bf16(s * q);   // s*q is exact in fp32; one rounding per MLX op
+        val = round_bf16(val + b);
+        if (out_scale != 0.0f) val = round_bf16(val * out_scale);
+        h[e] = f32_to_bf16_bits(val);
+    }
+    return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+}
+
+// One thread per packed word of an output row, reading the tiled layout (q4_layout.h).
+__global__ __launch_bounds__(kThreads) void q4_dequantize_tiled_kernel(
+    const uint4* __restrict__ codes, const uint2* __restrict__ sb, uint32_t n_total, uint32_t k, uint32_t pairs,
+    const uint32_t* __restrict__ rows, uint32_t n_rows, float out_scale, uint16_t* __restrict__ out) {
+    const uint32_t words_per_row = k / 8u;
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t >= static_cast<uint64_t>(n_rows) * words_per_row) return;
+    const uint32_t i = static_cast<uint32_t>(t / words_per_row);
+    const uint32_t wd = static_cast<uint32_t>(t - static_cast<uint64_t>(i) * words_per_row);
+    const uint32_t r = rows ? rows[i] : i;
+    uint4 res = make_uint4(0u, 0u, 0u, 0u);
+    if (r < n_total) {
+        const uint32_t g = wd / 8u;          // group
+        const uint32_t w8 = wd % 8u;         // word within the group: entry kb = w8 / 2, half w8 % 2
+        const size_t e = static_cast<size_t>(r / kTileRows) * pairs + g / 2u;
+        const uint32_t j = r % kTileRows;
+        const uint4 c = codes[e * 64u + (w8 / 2u) * 16u + j];
+        const uint2 sbv = sb[e * 16u + j];
+        const bool second = (g & 1u) != 0u;
+        const uint32_t word = second ? ((w8 & 1u) ? c.w : c.z) : ((w8 & 1u) ? c.y : c.x);
+        const uint32_t sbw = second ? sbv.y : sbv.x;
+        res = dequant_word_mlx(word, bf16_bits_to_f32(sbw & 0xFFFFu), bf16_bits_to_f32(sbw >> 16), out_scale);
+    }
+    *reinterpret_cast<uint4*>(out + static_cast<size_t>(i) * k + wd * 8u) = res;
+}
+
 // One thread per packed word of an output row: bf16(bf16(s*q) + b), optionally
 // times a bf16 constant.
 __global__ __launch_bounds__(kThreads) void q4_dequantize_kernel(
@@ -124,19 +166,7 @@ __global__ __launch_bounds__(kThreads) void q4_dequantize_kernel(
         const uint32_t word = wq[static_cast<size_t>(r) * words_per_row + j];
         const float s = bf16_bits_to_f32(scales[r * G + (j >> 3)]);
         const float b = bf16_bits_to_f32(biases[r * G + (j >> 3)]);
-        uint32_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float q = static_cast<float>((word >> (4 * e)) & 0xFu);
-            float val = round_bf16(s * q);   // s*q is exact in fp32; one rounding per MLX op
-            val = round_bf16(val + b);
-            if (out_scale != 0.0f) val = round_bf16(val * out_scale);
-            h[e] = f32_to_bf16_bits(val);
-        }
-        res.x = h[0] | (h[1] << 16);
-        res.y = h[2] | (h[3] << 16);
-        res.z = h[4] | (h[5] << 16);
-        res.w = h[6] | (h[7] << 16);
+        res = dequant_word_mlx(word, s, b, out_scale);
     }
     *reinterpret_cast<uint4*>(out + static_cast<size_t>(i) * k + j * 8u) = res;
 }
@@ -161,6 +191,18 @@ void launch_q4_dequantize(const uint32_t* wq, const uint16_t* scales, const uint
     HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "dequantize: output too large");
     hipLaunchKernelGGL(q4_dequantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
                        wq, scales, biases, n_total, k, rows, n_rows, out_scale_bf16, out);
+    HYP_HIP_CHECK(hipGetLastError());
+}
+
+void launch_q4_dequantize_tiled(const Q4Matrix& w, const uint32_t* rows, uint32_t n_rows, float out_scale_bf16,
+                                uint16_t* out, hipStream_t stream) {
+    HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr, HYP_STATUS_INTERNAL,
+                "dequantize: weights are not in the tiled resident layout");
+    const uint64_t threads = static_cast<uint64_t>(n_rows) * (w.k / 8u);
+    const uint64_t blocks = (threads + kThreads - 1) / kThreads;
+    HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "dequantize: output too large");
+    hipLaunchKernelGGL(q4_dequantize_tiled_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
+                       w.codes, w.sb, w.n, w.k, TiledDims::of(w.n, w.k).pairs, rows, n_rows, out_scale_bf16, out);
     HYP_HIP_CHECK(hipGetLastError());
 }
 

@@ -1,6 +1,6 @@
-// QuantizedLinear on HIP: residency and dispatch between the decode GEMV and the
-// prefill MFMA GEMM (the reference leaves this choice to MLX's qmv/qmm routing,
-// native/hyperion_mlx/src/weights.h:14-17).
+// QuantizedLinear on HIP: residency in the tiled layout and dispatch between the
+// skinny decode kernel (m <= 4) and the prefill MFMA GEMM (the reference leaves this
+// choice to MLX's qmv/qmm routing, native/hyperion_mlx/src/weights.h:14-17).
 #include "qlinear.h"
 
 #include "q4_layout.h"
@@ -61,56 +61,54 @@ namespace {
 
 constexpr size_t align256(size_t v) { return (v + 255u) & ~size_t{255u}; }
 
-// One allocation: MLX-layout codes | scales | biases | tiled codes | tiled scales.
-struct Sizes {
-    size_t w, s, off_s, off_b, off_codes, off_sb, total;
+// MLX-layout sizes: codes uint32 [n, k/8], scales and biases bf16 [n, k/64].
+struct MlxSizes {
+    size_t w, s, off_s, off_b, total;
 };
 
-Sizes sizes_for(uint32_t n, uint32_t k) {
-    const hip::TiledDims d = hip::TiledDims::of(n, k);
-    Sizes z{};
+MlxSizes mlx_sizes(uint32_t n, uint32_t k) {
+    MlxSizes z{};
     z.w = static_cast<size_t>(n) * (k / 8u) * sizeof(uint32_t);
     z.s = static_cast<size_t>(n) * (k / 64u) * sizeof(uint16_t);
     z.off_s = align256(z.w);
     z.off_b = z.off_s + align256(z.s);
-    z.off_codes = z.off_b + align256(z.s);
-    z.off_sb = z.off_codes + align256(d.code_bytes());
-    z.total = z.off_sb + align256(d.sb_bytes());
+    z.total = z.off_b + align256(z.s);
     return z;
 }
 
-QuantizedLinear make_storage(uint32_t n, uint32_t k, Sizes& z) {
-    z = sizes_for(n, k);
+// One allocation holding the tiled layout: codes | scales and biases.
+QuantizedLinear make_storage(uint32_t n, uint32_t k) {
+    const hip::TiledDims d = hip::TiledDims::of(n, k);
+    const size_t off_sb = align256(d.code_bytes());
     QuantizedLinear q;
-    q.storage = DeviceBuffer(z.total);
+    q.storage = DeviceBuffer(off_sb + align256(d.sb_bytes()));
     auto* base = static_cast<uint8_t*>(q.storage.data());
-    q.mat.w = reinterpret_cast<const uint32_t*>(base);
-    q.mat.scales = reinterpret_cast<const uint16_t*>(base + z.off_s);
-    q.mat.biases = reinterpret_cast<const uint16_t*>(base + z.off_b);
-    q.mat.codes = reinterpret_cast<const uint4*>(base + z.off_codes);
-    q.mat.sb = reinterpret_cast<const uint2*>(base + z.off_sb);
+    q.mat.codes = reinterpret_cast<const uint4*>(base);
+    q.mat.sb = reinterpret_cast<const uint2*>(base + off_sb);
     q.mat.n = n;
     q.mat.k = k;
     return q;
 }
 
-// Builds the tiled copy from the MLX-layout copy (stream-ordered).
-void tile(QuantizedLinear& q, hipStream_t stream) {
-    hip::launch_q4_tile(q.mat.w, q.mat.scales, q.mat.biases, q.mat.n, q.mat.k, const_cast<uint4*>(q.mat.codes),
-                        const_cast<uint2*>(q.mat.sb), stream);
+void tile_into(QuantizedLinear& q, const uint32_t* w, const uint16_t* s, const uint16_t* b, hipStream_t stream) {
+    hip::launch_q4_tile(w, s, b, q.mat.n, q.mat.k, const_cast<uint4*>(q.mat.codes), const_cast<uint2*>(q.mat.sb),
+                        stream);
 }
 
 }  // namespace
 
 QuantizedLinear QuantizedLinear::from_host(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                            uint32_t n, uint32_t k) {
-    Sizes z{};
-    QuantizedLinear q = make_storage(n, k, z);
-    auto* base = static_cast<uint8_t*>(q.storage.data());
+    QuantizedLinear q = make_storage(n, k);
+    // Upload in MLX layout to a staging buffer, then tile on the device.
+    const MlxSizes z = mlx_sizes(n, k);
+    DeviceBuffer staging(z.total);
+    auto* base = static_cast<uint8_t*>(staging.data());
     HYP_HIP_CHECK(hipMemcpy(base, w, z.w, hipMemcpyHostToDevice));
     HYP_HIP_CHECK(hipMemcpy(base + z.off_s, scales, z.s, hipMemcpyHostToDevice));
     HYP_HIP_CHECK(hipMemcpy(base + z.off_b, biases, z.s, hipMemcpyHostToDevice));
-    tile(q, nullptr);
+    tile_into(q, reinterpret_cast<const uint32_t*>(base), reinterpret_cast<const uint16_t*>(base + z.off_s),
+              reinterpret_cast<const uint16_t*>(base + z.off_b), nullptr);
     HYP_HIP_CHECK(hipStreamSynchronize(nullptr));
     return q;
 }
@@ -118,14 +116,22 @@ QuantizedLinear QuantizedLinear::from_host(const uint32_t* w, const uint16_t* sc
 QuantizedLinear QuantizedLinear::from_device(const uint32_t* w, const uint16_t* scales,
                                              const uint16_t* biases, uint32_t n, uint32_t k,
                                              hipStream_t stream) {
-    Sizes z{};
-    QuantizedLinear q = make_storage(n, k, z);
-    auto* base = static_cast<uint8_t*>(q.storage.data());
-    HYP_HIP_CHECK(hipMemcpyAsync(base, w, z.w, hipMemcpyDeviceToDevice, stream));
-    HYP_HIP_CHECK(hipMemcpyAsync(base + z.off_s, scales, z.s, hipMemcpyDeviceToDevice, stream));
-    HYP_HIP_CHECK(hipMemcpyAsync(base + z.off_b, biases, z.s, hipMemcpyDeviceToDevice, stream));
-    tile(q, stream);
+    QuantizedLinear q = make_storage(n, k);
+    tile_into(q, w, scales, biases, stream);
     return q;
+}
+
+void QuantizedLinear::export_mlx(uint32_t* w, uint16_t* scales, uint16_t* biases) const {
+    const MlxSizes z = mlx_sizes(mat.n, mat.k);
+    DeviceBuffer staging(z.total);
+    auto* base = static_cast<uint8_t*>(staging.data());
+    hip::launch_q4_untile(mat.codes, mat.sb, mat.n, mat.k, reinterpret_cast<uint32_t*>(base),
+                          reinterpret_cast<uint16_t*>(base + z.off_s), reinterpret_cast<uint16_t*>(base + z.off_b),
+                          nullptr);
+    HYP_HIP_CHECK(hipStreamSynchronize(nullptr));
+    HYP_HIP_CHECK(hipMemcpy(w, base, z.w, hipMemcpyDeviceToHost));
+    HYP_HIP_CHECK(hipMemcpy(scales, base + z.off_s, z.s, hipMemcpyDeviceToHost));
+    HYP_HIP_CHECK(hipMemcpy(biases, base + z.off_b, z.s, hipMemcpyDeviceToHost));
 }
 
 void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream, Epilogue epi,
@@ -133,10 +139,6 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
     if (m == 0) return;
     if (hip::skinny_supported(m, mat.k, false)) {
         hip::launch_q4_skinny(mat, nullptr, x, m, y, epi, cap_bf16, hip::choose_skinny_splits(mat.n, mat.k), stream);
-        return;
-    }
-    if (m <= hip::kGemvMaxM && mat.k <= hip::kGemvMaxK) {
-        hip::launch_q4_gemv(mat, nullptr, x, m, y, epi, cap_bf16, stream);
         return;
     }
     hip::launch_q4_gemm(mat, x, m, y, stream);
@@ -151,10 +153,6 @@ void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const u
     if (hip::skinny_supported(m, gate.mat.k, true)) {
         hip::launch_q4_skinny(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f,
                               hip::choose_skinny_splits(gate.mat.n, gate.mat.k), stream);
-        return;
-    }
-    if (m <= hip::kGemvMaxM && gate.mat.k <= hip::kGemvMaxK) {
-        hip::launch_q4_gemv(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f, stream);
         return;
     }
     // h <- gate(x); u <- up(x) in a stream-ordered temporary; h <- gelu(h) * u.

@@ -7,7 +7,8 @@
 //
 // The reference keeps MLX arrays that are lazily mmapped and moved to the GPU on first
 // use (weights_loader.h:70-79). Here every projection is copied to HBM once at load
-// time in MLX layout; the kernels read that layout directly.
+// time and stored in the tiled layout of q4_layout.h, which the kernels read; MLX's
+// layout stays the format at the boundary (upload, export).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -47,16 +48,20 @@ class DeviceBuffer {
 
 // One Q4/g64 projection [out_features = n, in_features = k] resident in HBM.
 struct QuantizedLinear {
-    DeviceBuffer storage;   // w | scales | biases, each 256-byte aligned
-    Q4Matrix mat;
+    DeviceBuffer storage;   // tiled codes | tiled scales and biases, 256-byte aligned
+    Q4Matrix mat;           // codes/sb point into storage; w/scales/biases are null
     int group_size = 64;
     int bits = 4;
 
-    // Copy from host (MLX layout) or from device pointers.
+    // Copy from host (MLX layout, synchronous) or from device pointers (MLX layout;
+    // stream-ordered: the inputs must stay valid until the stream has run the copy).
     static QuantizedLinear from_host(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                      uint32_t n, uint32_t k);
     static QuantizedLinear from_device(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                        uint32_t n, uint32_t k, hipStream_t stream);
+
+    // Copy back to host in MLX layout (synchronous).
+    void export_mlx(uint32_t* w, uint16_t* scales, uint16_t* biases) const;
 
     // y[m, n] = x[m, k] . dequant(W)^T (weights.h:26-37); device pointers.
     void apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream,

@@ -61,6 +61,7 @@ typedef struct HypQWeightOpaque* HypQWeight;   /* magic "HPQW": one resident Q4 
 typedef struct HypQModelOpaque* HypQModel;     /* magic "HPQM": all resident Q4 projections */
 typedef struct HypStreamOpaque* HypStream;     /* a HIP stream (hipStream_t) */
 typedef struct HypEventOpaque* HypEvent;       /* a HIP event (hipEvent_t) */
+typedef struct HypGraphOpaque* HypGraph;       /* magic "HPGR": an instantiated HIP graph */
 
 /* Device and build facts; replaces the Apple platform canary (runtime.mm:223-284). */
 typedef struct HypRuntimeInfo {
@@ -121,6 +122,19 @@ HypStatus hyp_event_destroy(HypEvent* event);
 HypStatus hyp_event_record(HypEvent event, HypStream stream);
 /* Milliseconds between two recorded events; waits for `end` to complete. */
 HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
+
+/* Graph capture of a launch sequence (e.g. one decode step) so it replays without
+ * per-launch host work; the reference has no counterpart (MLX evaluates its lazy graph
+ * at mx::eval, forward.cc:171). Between begin and end, hyp_qmatmul, hyp_qmatmul_ex,
+ * hyp_qmlp_gate_up_gelu with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
+ * hyp_dequantize_q4g64 and hyp_embed on `stream` are recorded instead of run (they
+ * allocate nothing); other calls on that stream are not allowed. The recorded pointers
+ * and handles must stay valid while the graph is used. */
+HypStatus hyp_graph_capture_begin(HypStream stream);
+HypStatus hyp_graph_capture_end(HypStream stream, HypGraph* out_graph);
+/* Enqueue one replay of the graph on stream. */
+HypStatus hyp_graph_launch(HypGraph graph, HypStream stream);
+HypStatus hyp_graph_free(HypGraph* graph);
 
 /* ---- resident Q4 weights (QuantizedLinear, weights.h:18-25; make_proj,
  *      weights_loader.cc:33-45) --------------------------------------------------- */
@@ -184,6 +198,12 @@ HypStatus hyp_dequantize_q4g64(const uint32_t* w, const void* scales, const void
  * by bf16(sqrt(k)). ids are device uint32 < n (out-of-range ids produce zero rows). */
 HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void* out,
                     HypStream stream);
+
+/* y[r] = bf16(x[r] / sqrt(mean(x[r]^2) + eps)) for each of m rows of k bf16 values,
+ * fp32 statistics; y may alias x. The renormalisation of a hidden state between chained
+ * projections: a weightless mx::fast::rms_norm (the reference normalises the decoder
+ * input and branch outputs with it, forward.cc:521-529). eps must be finite and >= 0. */
+HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, void* y, HypStream stream);
 
 /* ---- weight residency (load_model_weights, weights_loader.cc:71-153) ------------ */
 

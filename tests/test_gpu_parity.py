@@ -351,3 +351,95 @@ def test_zero_rows_is_a_noop(stream):
     hy.qmatmul(qw, y, 0, y, stream)
     stream.synchronize()
     assert np.all(y.to_host(stream) == 0)
+
+
+# ---------------------------------------------------------------- tiled layout edge cases
+
+@pytest.mark.parametrize("k", [64, 192, 320])
+def test_odd_group_counts_through_every_path(stream, k):
+    """k/64 odd leaves the last pair of the tiled layout half empty: the skinny kernel
+    (m <= 4), the GEMM (m > 4), export and embed must all ignore the missing group."""
+    n = 40   # not a multiple of 16: the last row tile is partly empty too
+    w, s, b = syn.q4_weights(n, k, seed=900 + k)
+    qw = hy.QWeight.from_host(w, s, b)
+    ew, es, eb = qw.export()
+    assert np.array_equal(ew, w) and np.array_equal(es, s) and np.array_equal(eb, b)
+    for m in (1, 3, 4, 5, 37):
+        say(f"odd groups k={k} m={m}")
+        x = syn.activations(m, k, seed=901 + m)
+        xd = dev(x, stream)
+        yd = hy.DeviceArray((m, n), np.uint16)
+        hy.qmatmul(qw, xd, m, yd, stream)
+        y = yd.to_host(stream)
+        ref = O.qmatmul_deq_f64(x, w, s, b, mode=1) if m > 4 else O.qmatmul_f64(x, w, s, b)
+        assert_within_bf16_rounding(y, ref, f"k={k} m={m}")
+    ids = np.array([0, 39, 17, 16, 15], np.uint32)
+    out = hy.DeviceArray((ids.size, k), np.uint16)
+    hy.embed(qw, dev(ids, stream), ids.size, out, stream)
+    ref = O.scale(O.dequantize(w, s, b, rows=ids, mode=0), float(np.sqrt(np.float32(k))))
+    np.testing.assert_array_equal(out.to_host(stream), ref)
+    qw.close()
+
+
+# ---------------------------------------------------------------- renormalisation
+
+def test_rms_normalize_rows(stream):
+    m, k = 5, 3840
+    x = syn.activations(m, k, seed=950)
+    x[2] = syn.bf16_bits(syn.bf16_to_f32(x[2]) * np.float32(1e3))   # very different row scales
+    x[3] = syn.bf16_bits(syn.bf16_to_f32(x[3]) * np.float32(1e-3))
+    xd = dev(x, stream)
+    yd = hy.DeviceArray((m, k), np.uint16)
+    hy.rms_normalize(xd, m, k, yd, stream, eps=1e-6)
+    got = syn.bf16_to_f32(yd.to_host(stream)).astype(np.float64)
+    xf = syn.bf16_to_f32(x).astype(np.float64)
+    ref = xf / np.sqrt(np.mean(xf * xf, axis=1, keepdims=True) + 1e-6)
+    # one bf16 rounding of the product plus fp32 statistics
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-8 * 1.01 + 1e-30)
+    hy.rms_normalize(xd, m, k, xd, stream, eps=1e-6)   # in place
+    np.testing.assert_array_equal(xd.to_host(stream), yd.to_host(stream))
+
+
+# ---------------------------------------------------------------- graph capture
+
+def test_graph_capture_replays_match_eager(stream):
+    """A captured decode-style chain (GEMV, fused gate/up, GEMV, renormalise, softcap LM
+    head) replayed several times, with eager work and synchronisation between the
+    replays; every replay's outputs equal the eager run's."""
+    k = 256
+    shapes = {"a": (512, k), "gate": (384, k), "up": (384, k), "down": (k, 384), "head": (1000, k)}
+    ws = {name: syn.q4_weights(n, kk, seed=960 + i) for i, (name, (n, kk)) in enumerate(shapes.items())}
+    qws = {name: hy.QWeight.from_host(*v) for name, v in ws.items()}
+    m = 2
+    x0 = syn.activations(m, k, seed=970)
+    h = dev(x0, stream)
+    a = hy.DeviceArray((m, 512), np.uint16)
+    g = hy.DeviceArray((m, 384), np.uint16)
+    logits = hy.DeviceArray((m, 1000), np.uint16)
+
+    def chain():
+        hy.qmatmul(qws["a"], h, m, a, stream)
+        hy.qmlp_gate_up_gelu(qws["gate"], qws["up"], h, m, g, stream)
+        hy.qmatmul(qws["down"], g, m, h, stream)
+        hy.rms_normalize(h, m, k, h, stream)
+        hy.qmatmul(qws["head"], h, m, logits, stream, softcap=30.0)
+
+    chain()
+    eager = (a.to_host(stream), g.to_host(stream), h.to_host(stream), logits.to_host(stream))
+    h.upload(x0, stream)
+    with hy.Graph.capture(stream) as graph:
+        chain()
+    for rep in range(4):
+        h.upload(x0, stream)                       # eager work between replays
+        scratch = hy.DeviceArray((m, 512), np.uint16)
+        hy.qmatmul(qws["a"], h, m, scratch, stream)
+        stream.synchronize()
+        graph.launch(stream)
+        stream.synchronize()
+        got = (a.to_host(stream), g.to_host(stream), h.to_host(stream), logits.to_host(stream))
+        for e, gt, name in zip(eager, got, ("a", "gate/up", "h", "logits")):
+            np.testing.assert_array_equal(gt, e, err_msg=f"replay {rep}: {name}")
+        scratch.close()
+    graph.close()
+    for q in qws.values():
+        q.close()
