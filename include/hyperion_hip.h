@@ -159,9 +159,9 @@ HypStatus hyp_qweight_export(HypQWeight weight, uint32_t* w, uint16_t* scales, u
 /* ---- quantized matmul ---------------------------------------------------------- */
 
 /* y[m, n] = x[m, k] * dequant(W)^T with fp32 accumulation, bf16 out.
- * Replaces QuantizedLinear::apply (weights.h:26-37) for every M: m <= 8 runs the
- * decode GEMV, larger m the MFMA GEMM. x and y are device pointers; m == 0 is a
- * no-op. */
+ * Replaces QuantizedLinear::apply (weights.h:26-37) for every M: m <= 4 runs the
+ * weight-streaming decode kernel, larger m the tiled GEMM (both on bf16 MFMA).
+ * x and y are device pointers; m == 0 is a no-op. */
 HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, HypStream stream);
 
 /* hyp_qmatmul with an epilogue; HYP_EPILOGUE_SOFTCAP with cap > 0 is the tied
