@@ -10,12 +10,11 @@ events on the stream the kernel runs on.
 
 Also reported, each on its own workload:
   quantize    bf16 W [15360,3840] N(0, 0.02^2) with 1% x8 outliers -> Q4/g64 (GB/s)
-  layer       one decoder layer's linear stack (q, k, v, o, fused gate/up + GELU, down)
-              at m = 1 and 4, cold (part of the decode stream below)
   prefill     the seven projections at m = 512 and 2048 (TFLOP/s vs bf16 MFMA peak)
-  decode      48 layers + tied LM head [262144,3840] with softcap, the hidden state
-              renormalised between layers, m = 1 and 4, replayed from a captured HIP
-              graph (tokens/s and effective HBM GB/s)
+  decode      48 layers (grouped q/k/v, o, fused gate/up + GELU, down, renormalise)
+              + tied LM head [262144,3840] with softcap, m = 1 and 4, replayed from a
+              captured HIP graph (tokens/s and effective HBM GB/s), with the LM head
+              timed alone and the per-layer time and rate derived from the two
 and the oracle's restatement of MLX's CPU quantized_matmul timed on this host's cores
 (cpu_baseline).
 
@@ -170,38 +169,56 @@ class DecodeModel:
         self.embed.close()
 
 
-def decode_step(model, m, bufs, stream):
-    """One decode step's linear stack: per layer q, k, v from h; o from q's output; the
-    fused gate/up GELU from o's output; down; renormalise into h. Then the tied LM head
-    with softcap 30 on h."""
-    h, q, kv, o, g, logits = bufs
+def decode_layers(model, m, bufs, stream):
+    """One decode step's layer stack: per layer q, k and v from h in one grouped launch;
+    o from q's output; the fused gate/up GELU from o's output; down; renormalise into h."""
+    h, q, k, v, o, g, _logits = bufs
     for proj in model.layers:
-        hy.qmatmul(proj["q"], h, m, q, stream)
-        hy.qmatmul(proj["k"], h, m, kv, stream)
-        hy.qmatmul(proj["v"], h, m, kv, stream)
+        hy.qmatmul_group([proj["q"], proj["k"], proj["v"]], h, m, [q, k, v], stream)
         hy.qmatmul(proj["o"], q, m, o, stream)
         hy.qmlp_gate_up_gelu(proj["gate"], proj["up"], o, m, g, stream)
         hy.qmatmul(proj["down"], g, m, h, stream)
         hy.rms_normalize(h, m, HIDDEN, h, stream)
-    hy.qmatmul(model.embed, h, m, logits, stream, softcap=30.0)
+
+
+def lm_head(model, m, bufs, stream):
+    """The tied LM head with softcap 30 on h."""
+    hy.qmatmul(model.embed, bufs[0], m, bufs[-1], stream, softcap=30.0)
+
+
+LAUNCHES_PER_LAYER = 5
 
 
 def bench_decode_stream(model, m, steps, warmup, stream):
     h = hy.DeviceArray.from_host(syn.activations(m, HIDDEN, seed=77), stream)
     bufs = (h, hy.DeviceArray((m, 4096), np.uint16), hy.DeviceArray((m, 2048), np.uint16),
-            hy.DeviceArray((m, HIDDEN), np.uint16), hy.DeviceArray((m, 15360), np.uint16),
-            hy.DeviceArray((m, syn.VOCAB), np.uint16))
+            hy.DeviceArray((m, 2048), np.uint16), hy.DeviceArray((m, HIDDEN), np.uint16),
+            hy.DeviceArray((m, 15360), np.uint16), hy.DeviceArray((m, syn.VOCAB), np.uint16))
     with hy.Graph.capture(stream) as graph:
-        decode_step(model, m, bufs, stream)
+        decode_layers(model, m, bufs, stream)
+        lm_head(model, m, bufs, stream)
     ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup)
     graph.close()
-    act = 2 * m * (len(model.layers) * (HIDDEN * 3 + 4096 * 2 + 2048 * 2 + HIDDEN * 2 + 15360 * 3) + HIDDEN + syn.VOCAB)
-    nbytes = model.weight_bytes + act
+    with hy.Graph.capture(stream) as head:
+        lm_head(model, m, bufs, stream)
+    head_ms = time_launches(stream, lambda _i: head.launch(stream), steps, warmup)
+    head.close()
     layers = len(model.layers)
+    act = 2 * m * (layers * (HIDDEN * 3 + 4096 * 2 + 2048 * 2 + HIDDEN * 2 + 15360 * 3) + HIDDEN + syn.VOCAB)
+    nbytes = model.weight_bytes + act
+    head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + syn.VOCAB)
+    layer_bytes = (nbytes - head_bytes) / max(layers, 1)
+    layer_us = (ms - head_ms) * 1e3 / max(layers, 1)
     out = {"m": m, "ms_per_step": round(ms, 4), "tokens_per_s": round(m / (ms / 1e3), 1),
            "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-           "bytes_per_step": nbytes, "launches_per_step": 7 * layers + 1}
-    log(f"decode stream m={m}: {ms:.3f} ms/step = {out['tokens_per_s']:.0f} tok/s, {out['gbs']:.0f} GB/s")
+           "bytes_per_step": nbytes, "launches_per_step": LAUNCHES_PER_LAYER * layers + 1,
+           "lm_head_us": round(head_ms * 1e3, 1),
+           "lm_head_gbs": round(head_bytes / head_ms / 1e6, 1),
+           "layer_us": round(layer_us, 2),
+           "layer_gbs": round(layer_bytes / layer_us / 1e3, 1)}
+    log(f"decode stream m={m}: {ms:.3f} ms/step = {out['tokens_per_s']:.0f} tok/s, {out['gbs']:.0f} GB/s; "
+        f"LM head {out['lm_head_us']} us ({out['lm_head_gbs']} GB/s), layer {out['layer_us']} us "
+        f"({out['layer_gbs']} GB/s)")
     return out
 
 
@@ -278,10 +295,6 @@ def main():
         streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
         extra["decode_stream"] = streams
-        layer_bytes = sum(q4_bytes(n, k) for n, k in syn.LAYER_SHAPES.values())
-        extra["layer"] = [{"m": s["m"], "us_per_layer_in_stream": round(s["ms_per_step"] * 1e3 / (args.layers + 1), 2),
-                           "note": "step time / (layers + 1): a 566 MB LM head is about one layer's worth of bytes",
-                           "layer_weight_bytes": layer_bytes} for s in streams]
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     per = dec["ms_per_launch"]

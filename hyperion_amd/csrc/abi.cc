@@ -451,6 +451,26 @@ HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, Hyp
     return hyp_qmatmul_ex(weight, x, m, y, HYP_EPILOGUE_NONE, 0.0f, stream);
 }
 
+HypStatus hyp_qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
+                            void* const* ys, HypStream stream) {
+    return abi_call("hyp_qmatmul_group", [&] {
+        REQUIRE_ARG(weights != nullptr && ys != nullptr, "weights and ys must be non-null arrays");
+        REQUIRE_ARG(count >= 1u && count <= HYP_QMATMUL_GROUP_MAX, "count must be 1..HYP_QMATMUL_GROUP_MAX");
+        const QuantizedLinear* lins[HYP_QMATMUL_GROUP_MAX];
+        uint16_t* outs[HYP_QMATMUL_GROUP_MAX];
+        for (uint32_t i = 0; i < count; ++i) {
+            lins[i] = &qweight_ref(weights[i], "weights[i]");
+            REQUIRE_ARG(lins[i]->mat.k == lins[0]->mat.k, "grouped weights must share k");
+            outs[i] = static_cast<uint16_t*>(ys[i]);
+        }
+        hipStream_t s = stream_of(stream);
+        if (m == 0) return;
+        REQUIRE_ARG(x != nullptr, "x must be a non-null device pointer");
+        for (uint32_t i = 0; i < count; ++i) REQUIRE_ARG(outs[i] != nullptr, "ys[i] must be non-null device pointers");
+        hyperion::model::apply_group(lins, outs, count, static_cast<const uint16_t*>(x), m, s);
+    });
+}
+
 HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, uint32_t m, void* h,
                                 HypStream stream) {
     return abi_call("hyp_qmlp_gate_up_gelu", [&] {

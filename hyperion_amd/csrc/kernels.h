@@ -33,24 +33,31 @@ enum class Epilogue : int {
     kSoftcap = 1,   // y = softcap(bf16(acc)), forward.cc:154-160
 };
 
-// Largest m the skinny MFMA kernel handles.
+// Largest m the skinny MFMA kernel handles, and the most projections one grouped
+// launch covers.
 constexpr uint32_t kSkinnyMaxM = 4;
+constexpr uint32_t kSkinnyMaxGroup = 3;
 
 // Skinny quantized matmul on MFMA (m <= kSkinnyMaxM) over the tiled layout:
 // y[m, n] = x[m, k] . dequant(W)^T. With `up` non-null it is the fused gate/up:
-// y = gelu_chain(x.G^T) * (x.U^T). `splits` (1, 2, 4) waves share each 16-row tile;
-// ceil(k / 128) >= splits.
+// y = gelu_chain(x.G^T) * (x.U^T). `splits` waves share each 16-row tile (1, 2, 4;
+// 8 or 16 for the plain form; 0 chooses); ceil(k / 128) >= splits.
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream);
-// Splits used for an (n, k) problem, and whether (m, k) fits the kernel's LDS staging.
-uint32_t choose_skinny_splits(uint32_t n, uint32_t k);
+// One launch over `count` projections that share x (and k), e.g. q, k and v:
+// ys[i][m, n_i] = x . dequant(W_i)^T.
+void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                            uint32_t m, hipStream_t stream);
+// Splits for `tiles` 16-row tiles and `pairs` group pairs (wide: the plain form, which
+// allows 8 and 16), and whether (m, k) fits the kernel's LDS staging.
+uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, bool wide);
 bool skinny_supported(uint32_t m, uint32_t k, bool dual);
 
 // Prefill GEMM on bf16 MFMA over the tiled layout: Q4 codes dequantized in registers,
 // x tiles in LDS. Plain bf16 output; epilogues for larger m run as the elementwise
 // kernels below.
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
-// Same with an explicit workgroup tile: (16 * mt) x (64 * nt), mt in {8, 16}, nt in {2, 4}.
+// Same with an explicit workgroup tile: (16 * mt) x (64 * nt), mt in {8, 16}, nt = 2.
 void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
                            hipStream_t stream);
 

@@ -28,12 +28,12 @@
 //    XCD's L2.
 #include "common.h"
 #include "kernels.h"
+#include "q4_dequant.h"
 #include "q4_layout.h"
 
 namespace hyperion::hip {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
@@ -53,30 +53,9 @@ struct GemmParams {
     uint32_t row_tiles;   // ceil(n / 16)
     uint32_t tiles_n;     // workgroup tiles along n
     uint32_t tiles_total;
+    uint32_t code_bytes;
+    uint32_t sb_bytes;
 };
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-// 8 codes of one packed word -> 8 bf16 values bf16(s*q + b), in k order.
-__device__ __forceinline__ bf16x8_t dequant_word(uint32_t word, float s, float b) {
-    uint32_t lo = word & 0x0F0F0F0Fu;          // codes 0,2,4,6 in bytes 0..3
-    uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;   // codes 1,3,5,7
-    // Opaque to the optimizer, so each byte converts with v_cvt_f32_ubyte{0..3} instead
-    // of being re-extracted from the word with v_bfe_u32 first.
-    asm volatile("" : "+v"(lo), "+v"(hi));
-    uint4 r;
-    r.x = pack_bf16x2(fmaf(s, static_cast<float>(lo & 0xFFu), b), fmaf(s, static_cast<float>(hi & 0xFFu), b));
-    r.y = pack_bf16x2(fmaf(s, static_cast<float>((lo >> 8) & 0xFFu), b),
-                      fmaf(s, static_cast<float>((hi >> 8) & 0xFFu), b));
-    r.z = pack_bf16x2(fmaf(s, static_cast<float>((lo >> 16) & 0xFFu), b),
-                      fmaf(s, static_cast<float>((hi >> 16) & 0xFFu), b));
-    r.w = pack_bf16x2(fmaf(s, static_cast<float>(lo >> 24), b), fmaf(s, static_cast<float>(hi >> 24), b));
-    return __builtin_bit_cast(bf16x8_t, r);
-}
 
 // Raw weights of one pair for one lane: NT code entries and NT scale entries.
 template <int NT>
@@ -98,16 +77,16 @@ __device__ __forceinline__ void dequant_step(const BRaw<NT>& raw, bf16x8_t (&b)[
     }
 }
 
+// Raw weights of pair `pair` for this lane: the 16-byte code entry and 8-byte scale
+// entry of each of its NT column tiles (offsets set up once, the pair is a scalar offset).
 template <int NT>
-__device__ __forceinline__ void load_b(const GemmParams& p, uint32_t tile16_0, uint32_t pair, uint32_t lane,
+__device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t sr,
+                                       const uint32_t (&c_off)[NT], const uint32_t (&s_off)[NT], uint32_t pair,
                                        BRaw<NT>& raw) {
-    const uint32_t j = lane & 15u;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t t16 = min(tile16_0 + nt, p.row_tiles - 1u);   // tiles past n: loaded, never stored
-        const size_t e = static_cast<size_t>(t16) * p.pairs + pair;
-        raw.c[nt] = p.codes[e * 64u + lane];
-        raw.sb[nt] = p.sb[e * 16u + j];
+        raw.c[nt] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(cr, c_off[nt], pair * 1024u, 0));
+        raw.sb[nt] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(sr, s_off[nt], pair * 128u, 0));
     }
 }
 
@@ -149,7 +128,7 @@ __device__ __forceinline__ void mfma_step(const uint8_t* xb, uint32_t lane, cons
     }
 }
 
-template <int MT, int NT>
+template <int MT, int NT, bool ODD>
 __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     constexpr int BM = 16 * MT;
     constexpr int kTileBytes = BM * kRowBytes;
@@ -179,26 +158,47 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     // X staging: load t of wave w covers tile rows 4 (w kXLoads + t) .. +3; lane l fills
     // LDS chunk (l % 16) of row r = 4 (w kXLoads + t) + l / 16 with the row's logical
     // chunk (l % 16) ^ (r % 16). kXLoads is a multiple of 4, so r % 16 = (4 t + l / 16)
-    // % 16. Rows past m lie past the end of the buffer resource (m * k * 2 bytes) and
-    // load zeros; so do chunks past k (an odd group count), given offset 2^31.
+    // % 16. Each load's lane offset is set up once; the pair is a scalar offset. Rows past
+    // m get an offset past the buffer resource (m * k * 2 bytes) and load zeros; so do the
+    // chunks past k of an odd group count (ODD: the last pair's second group).
     static_assert(kXLoads % 4 == 0, "swizzle period");
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.x), static_cast<short>(0), static_cast<int>(p.m * k * 2u), 0x00020000);
     const uint32_t lh = lane >> 4;
-    const uint32_t xbase = (m0 + 4u * wave * kXLoads + lh) * k * 2u;   // byte offset of the t = 0 row
+    uint32_t xoff[kXLoads];
     uint32_t xchunk[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) xchunk[t] = (lane & 15u) ^ ((4u * t + lh) & 15u);
+#pragma unroll
+    for (int t = 0; t < kXLoads; ++t) {
+        const uint32_t row = m0 + 4u * (wave * kXLoads + t) + lh;
+        xoff[t] = row < p.m ? row * k * 2u + xchunk[t % 4] * 16u : 0x80000000u;
+    }
     auto load_x = [&](uint32_t pair, uint8_t* buf) {
 #pragma unroll
         for (int t = 0; t < kXLoads; ++t) {
-            const uint32_t kk = pair * kPairK + xchunk[t % 4] * 8u;
-            const uint32_t off = kk < k ? xbase + t * 8u * k + kk * 2u : 0x80000000u;
+            uint32_t off = xoff[t];
+            if (ODD && pair * kPairK + xchunk[t % 4] * 8u >= k) off = 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 xr, (__attribute__((address_space(3))) void*)(buf + (wave * kXLoads + t) * 1024u), 16,
-                static_cast<int>(off), 0, 0, 0);
+                static_cast<int>(off), static_cast<int>(pair * kPairK * 2u), 0, 0);
         }
     };
+
+    // Weights: column tile (tile16_0 + nt), clamped to the last tile (columns past n are
+    // computed, never stored).
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint4*>(p.codes), static_cast<short>(0), static_cast<int>(p.code_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint2*>(p.sb), static_cast<short>(0), static_cast<int>(p.sb_bytes), 0x00020000);
+    uint32_t c_off[NT];
+    uint32_t s_off[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t t16 = min(tile16_0 + nt, p.row_tiles - 1u);
+        c_off[nt] = (t16 * pairs * 64u + lane) * 16u;
+        s_off[nt] = (t16 * pairs * 16u + (lane & 15u)) * 8u;
+    }
 
     f32x4_t acc[MT][NT];
 #pragma unroll
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 
     BRaw<NT> braw, bnext;
     load_x(0u, xs);
-    load_b<NT>(p, tile16_0, 0u, lane, braw);
+    load_b<NT>(cr, sr, c_off, s_off, 0u, braw);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
         const uint8_t* xb = xs + (pair & 1u) * kTileBytes;
         const uint32_t pn = min(pair + 1u, pairs - 1u);
         load_x(pn, xs + ((pair + 1u) & 1u) * kTileBytes);
-        load_b<NT>(p, tile16_0, pn, lane, bnext);
+        load_b<NT>(cr, sr, c_off, s_off, pn, bnext);
 
         dequant_step<NT, 1>(braw, b1);
         mfma_step<MT, NT, 0>(xb, lane, b0, acc);
@@ -237,20 +237,48 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
         __syncthreads();
     }
 
-    // acc[mt][nt][r] is Y[m0 + 16 mt + 4 kb + r][n0 + 16 NT wave + 16 nt + j].
-    const uint32_t j = lane & 15u;
-    const uint32_t kb = lane >> 4;
+    // Epilogue: the workgroup's (16 MT) x (64 NT) tile goes through LDS (rows of
+    // 128 NT bytes plus 32 bytes of padding, so the four row groups a write touches hit
+    // distinct banks) and leaves as 16-byte row segments. acc[mt][nt][r] is tile element
+    // (16 mt + 4 kb + r, 16 NT wave + 16 nt + j).
+    constexpr uint32_t kOutRow = 128u * NT + 32u;
+    static_assert(BM * kOutRow <= 2u * kTileBytes, "output staging exceeds the X buffers");
+    __syncthreads();
+    {
+        const uint32_t j = lane & 15u;
+        const uint32_t kb = lane >> 4;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t n = (tile16_0 + nt) * 16u + j;
-        if (n >= p.n) continue;
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t m = m0 + mt * 16u + kb * 4u + r;
-                if (m < p.m) p.y[static_cast<size_t>(m) * p.n + n] = f32_to_bf16_bits(acc[mt][nt][r]);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = mt * 16u + kb * 4u + r;
+                    const uint32_t col = (wave * NT + nt) * 16u + j;
+                    *reinterpret_cast<uint16_t*>(xs + row * kOutRow + col * 2u) = f32_to_bf16_bits(acc[mt][nt][r]);
+                }
+    }
+    __syncthreads();
+    constexpr uint32_t kCols = 64u * NT;
+    constexpr uint32_t kChunks = kCols / 8u;                  // 16-byte chunks per row
+    constexpr uint32_t kRowsPerPass = kThreads / kChunks;
+    const uint32_t ch = threadIdx.x % kChunks;
+    const uint32_t col0 = n0 + ch * 8u;
+    if ((p.n & 7u) == 0u) {
+        for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
+            const uint32_t row = m0 + r;
+            if (row < p.m && col0 < p.n)
+                *reinterpret_cast<uint4*>(p.y + static_cast<size_t>(row) * p.n + col0) =
+                    *reinterpret_cast<const uint4*>(xs + r * kOutRow + ch * 16u);
+        }
+    } else {
+        for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
+            const uint32_t row = m0 + r;
+            if (row >= p.m) continue;
+            for (uint32_t c = 0; c < 8u; ++c)
+                if (col0 + c < p.n)
+                    p.y[static_cast<size_t>(row) * p.n + col0 + c] =
+                        *reinterpret_cast<const uint16_t*>(xs + r * kOutRow + ch * 16u + c * 2u);
         }
     }
 }
@@ -271,7 +299,8 @@ size_t max_lds_per_block() {
 
 template <int MT, int NT>
 void launch_t(GemmParams p, hipStream_t stream) {
-    auto kernel = q4_gemm_kernel<MT, NT>;
+    const bool odd = ((p.k / 64u) & 1u) != 0u;
+    auto kernel = odd ? q4_gemm_kernel<MT, NT, true> : q4_gemm_kernel<MT, NT, false>;
     const size_t lds = 2u * 16u * MT * kRowBytes;
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
     if (lds > 65536u) {
@@ -279,7 +308,9 @@ void launch_t(GemmParams p, hipStream_t stream) {
         int dev = 0;
         HYP_HIP_CHECK(hipGetDevice(&dev));
         if (configured_device != dev) {
-            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(q4_gemm_kernel<MT, NT, true>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(q4_gemm_kernel<MT, NT, false>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
             configured_device = dev;
         }
@@ -309,12 +340,11 @@ void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uin
     p.k = w.k;
     p.pairs = d.pairs;
     p.row_tiles = d.tiles;
-    if (mt == 16u && nt == 4u) {
-        launch_t<16, 4>(p, stream);
-    } else if (mt == 16u && nt == 2u) {
+    HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT, "gemm: weights of 2 GiB or more");
+    p.code_bytes = static_cast<uint32_t>(d.code_bytes());
+    p.sb_bytes = static_cast<uint32_t>(d.sb_bytes());
+    if (mt == 16u && nt == 2u) {
         launch_t<16, 2>(p, stream);
-    } else if (mt == 8u && nt == 4u) {
-        launch_t<8, 4>(p, stream);
     } else if (mt == 8u && nt == 2u) {
         launch_t<8, 2>(p, stream);
     } else {

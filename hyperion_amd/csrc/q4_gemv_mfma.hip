@@ -43,8 +43,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr uint32_t kMaxSegments = 3;   // projections sharing x in one grouped launch
 
 constexpr uint32_t kNibbleMask = 0x000F000Fu;
 constexpr uint32_t kMagic128 = 0x43004300u;   // bf16 pair (128.0, 128.0)
@@ -78,17 +77,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
                                              static_cast<int>(bytes), 0x00020000);
 }
 
+// One projection of a (possibly grouped) launch: its 16-row tiles are global tiles
+// [tile_begin, tile_begin + ceil(n / 16)).
+struct SkinnySegment {
+    const uint4* codes;   // tiled codes (q4_layout.h)
+    const uint2* sb;      // tiled scales and biases
+    uint16_t* y;          // [m, n]
+    uint32_t n;
+    uint32_t tile_begin;
+};
+
 struct SkinnyParams {
-    const uint4* codes;    // tiled codes (q4_layout.h)
-    const uint2* sb;       // tiled scales and biases
-    const uint4* codes2;   // fused gate/up: the up projection (same n, k)
+    SkinnySegment seg[kMaxSegments];   // segments past nseg are unused
+    const uint4* codes2;               // fused gate/up: the up projection (same n, k as seg[0])
     const uint2* sb2;
     const uint16_t* x;
-    uint16_t* y;
-    uint32_t n;
+    uint32_t nseg;
     uint32_t k;
     uint32_t pairs;       // ceil(k / 128)
-    uint32_t splits;      // waves sharing one 16-row tile: 1, 2 or 4
+    uint32_t splits;      // waves sharing one 16-row tile (divides the workgroup's waves)
     float cap;            // bf16 softcap constant
 };
 
@@ -204,9 +211,10 @@ __device__ __forceinline__ void compute_batch(const Batch<P> (&bt)[NW], uint32_t
     }
 }
 
-template <int M, bool DUAL, int EPI, int P>
-__global__ __launch_bounds__(kThreads) void q4_skinny_kernel(SkinnyParams p) {
+template <int M, bool DUAL, int EPI, int P, int NWAVE>
+__global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     constexpr int NW = DUAL ? 2 : 1;
+    constexpr uint32_t kThreads = 64u * NWAVE;
     extern __shared__ __attribute__((aligned(16))) uint4 smem[];
 
     const uint32_t k = p.k;
@@ -214,17 +222,26 @@ __global__ __launch_bounds__(kThreads) void q4_skinny_kernel(SkinnyParams p) {
     const uint32_t G = k / 64u;   // groups per row
     uint4* xs = smem;                                              // [M][W] permuted x
     float4* sx = reinterpret_cast<float4*>(smem + M * W);          // [G] group sums of x rows 0..3
-    float* red = reinterpret_cast<float*>(sx + G);                 // [kWaves][NW][M][16]
+    float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][NW][M][16]
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t S = p.splits;
     const uint32_t split = wave % S;
-    const uint32_t tile = blockIdx.x * (kWaves / S) + wave / S;
+    const uint32_t gtile = blockIdx.x * (NWAVE / S) + wave / S;   // tile over all segments
     const uint32_t j = lane & 15u;
     const uint32_t kb = lane >> 4;
     const uint32_t pairs = p.pairs;
-    const uint32_t tiles = (p.n + kTileRows - 1u) / kTileRows;
+
+    // This wave's segment (wave-uniform selects, no indexed parameter access).
+    const bool in1 = p.nseg > 1u && gtile >= p.seg[1].tile_begin;
+    const bool in2 = p.nseg > 2u && gtile >= p.seg[2].tile_begin;
+    const uint4* seg_codes = in2 ? p.seg[2].codes : (in1 ? p.seg[1].codes : p.seg[0].codes);
+    const uint2* seg_sb = in2 ? p.seg[2].sb : (in1 ? p.seg[1].sb : p.seg[0].sb);
+    uint16_t* seg_y = in2 ? p.seg[2].y : (in1 ? p.seg[1].y : p.seg[0].y);
+    const uint32_t seg_n = in2 ? p.seg[2].n : (in1 ? p.seg[1].n : p.seg[0].n);
+    const uint32_t tile = gtile - (in2 ? p.seg[2].tile_begin : (in1 ? p.seg[1].tile_begin : 0u));
+    const uint32_t tiles = (seg_n + kTileRows - 1u) / kTileRows;
     const uint32_t ltile = min(tile, tiles - 1u);   // tiles past the matrix are loaded, never stored
 
     // This wave's pairs: split, split + S, ... (cnt of them; cnt >= 1 since pairs >= S).
@@ -247,8 +264,8 @@ __global__ __launch_bounds__(kThreads) void q4_skinny_kernel(SkinnyParams p) {
     LaneMatrix lm[NW];
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-        lm[q].codes = buffer_rsrc(q == 0 ? p.codes : p.codes2, c_bytes);
-        lm[q].sb = buffer_rsrc(q == 0 ? p.sb : p.sb2, s_bytes);
+        lm[q].codes = buffer_rsrc(q == 0 ? seg_codes : p.codes2, c_bytes);
+        lm[q].sb = buffer_rsrc(q == 0 ? seg_sb : p.sb2, s_bytes);
         lm[q].c_off = (ltile * pairs * 64u + lane) * 16u;
         lm[q].sb_off = (ltile * pairs * 16u + j) * 8u;
     }
@@ -339,7 +356,7 @@ __global__ __launch_bounds__(kThreads) void q4_skinny_kernel(SkinnyParams p) {
     }
 
     const uint32_t out_row = tile * kTileRows + j;
-    if (split == 0u && kb == 0u && out_row < p.n) {
+    if (split == 0u && kb == 0u && out_row < seg_n) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             float out = round_bf16(y[0][m]);
@@ -349,24 +366,25 @@ __global__ __launch_bounds__(kThreads) void q4_skinny_kernel(SkinnyParams p) {
             } else if constexpr (EPI == static_cast<int>(Epilogue::kSoftcap)) {
                 out = softcap_bf16(out, p.cap);
             }
-            p.y[static_cast<size_t>(m) * p.n + out_row] = f32_to_bf16_bits(out);
+            seg_y[static_cast<size_t>(m) * seg_n + out_row] = f32_to_bf16_bits(out);
         }
     }
 }
 
-size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual) {
+size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    return m * W * 16u + G * 16u + static_cast<size_t>(kWaves) * (dual ? 2u : 1u) * m * kTileRows * 4u;
+    return m * W * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u;
 }
 
 size_t max_lds_per_block();
 
-template <int M, bool DUAL, int EPI>
-void launch_skinny_t(const SkinnyParams& p, hipStream_t stream) {
+template <int M, bool DUAL, int EPI, int NWAVE>
+void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t stream) {
     constexpr int P = 2;   // pairs per register batch (two batches in flight)
-    auto kernel = q4_skinny_kernel<M, DUAL, EPI, P>;
-    const size_t lds = skinny_lds_bytes(M, p.k, DUAL);
+    auto kernel = q4_skinny_kernel<M, DUAL, EPI, P, NWAVE>;
+    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE);
+    HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "skinny: x staging exceeds the device's LDS");
     if (lds > 65536u) {
         static thread_local int configured_device = -1;
         int dev = 0;
@@ -378,21 +396,37 @@ void launch_skinny_t(const SkinnyParams& p, hipStream_t stream) {
             configured_device = dev;
         }
     }
-    const uint32_t tiles = (p.n + kTileRows - 1u) / kTileRows;
-    const uint32_t tiles_per_block = kWaves / p.splits;
-    const dim3 grid((tiles + tiles_per_block - 1u) / tiles_per_block);
-    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, stream, p);
+    const uint32_t tiles_per_block = NWAVE / p.splits;
+    const dim3 grid((tiles_total + tiles_per_block - 1u) / tiles_per_block);
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * NWAVE), lds, stream, p);
 }
 
+// Workgroups of max(4, splits) waves. The fused gate/up and the softcap head keep 4 (their
+// projections are wide, and the gate/up kernel holds two accumulator sets).
 template <int M>
-void launch_skinny_m(const SkinnyParams& p, bool dual, Epilogue epi, hipStream_t stream) {
+void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, hipStream_t stream) {
     if (dual) {
-        launch_skinny_t<M, true, 0>(p, stream);
+        launch_skinny_t<M, true, 0, 4>(p, tiles_total, stream);
     } else if (epi == Epilogue::kSoftcap) {
-        launch_skinny_t<M, false, 1>(p, stream);
+        launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
+    } else if (p.splits == 16u) {
+        launch_skinny_t<M, false, 0, 16>(p, tiles_total, stream);
+    } else if (p.splits == 8u) {
+        launch_skinny_t<M, false, 0, 8>(p, tiles_total, stream);
     } else {
-        launch_skinny_t<M, false, 0>(p, stream);
+        launch_skinny_t<M, false, 0, 4>(p, tiles_total, stream);
     }
+}
+
+void launch_skinny(SkinnyParams& p, uint32_t tiles_total, uint32_t m, bool dual, Epilogue epi, hipStream_t stream) {
+    switch (m) {
+        case 1: launch_skinny_m<1>(p, tiles_total, dual, epi, stream); break;
+        case 2: launch_skinny_m<2>(p, tiles_total, dual, epi, stream); break;
+        case 3: launch_skinny_m<3>(p, tiles_total, dual, epi, stream); break;
+        case 4: launch_skinny_m<4>(p, tiles_total, dual, epi, stream); break;
+        default: throw NativeError(HYP_STATUS_INTERNAL, "skinny launched with m outside 1..4");
+    }
+    HYP_HIP_CHECK(hipGetLastError());
 }
 
 size_t max_lds_per_block() {
@@ -411,50 +445,79 @@ size_t max_lds_per_block() {
 
 }  // namespace
 
-uint32_t choose_skinny_splits(uint32_t n, uint32_t k) {
-    // 4 waves per tile while that stays within 32 waves per CU, else 2 (the fastest
-    // choices measured on the 15360 x 3840 decode and 262144 x 3840 LM-head shapes);
-    // never more splits than group pairs.
-    const TiledDims d = TiledDims::of(n, k);
-    uint32_t s = d.tiles * 4u <= device_compute_units() * 32u ? 4u : 2u;
-    while (s > 1u && d.pairs < s) s /= 2u;
+uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, bool wide) {
+    // Very wide problems (the 262144-row LM head): 2 waves per tile. Otherwise 4, and for
+    // projections with few row tiles (o, down, k, v; grouped q/k/v) up to 16 while the
+    // grid stays within 16 waves per CU and every wave keeps at least two group pairs.
+    // Never more splits than group pairs.
+    const uint32_t cus = device_compute_units();
+    uint32_t s = 4u;
+    if (tiles * 4u > cus * 32u) {
+        s = 2u;
+    } else if (wide) {
+        while (s < 16u && tiles * s * 2u <= cus * 16u && pairs >= 4u * s) s *= 2u;
+    }
+    while (s > 1u && pairs < s) s /= 2u;
     return s;
 }
 
 bool skinny_supported(uint32_t m, uint32_t k, bool dual) {
-    return m >= 1u && m <= kSkinnyMaxM && skinny_lds_bytes(m, k, dual) <= max_lds_per_block();
+    return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
+           skinny_lds_bytes(m, k, dual, dual ? 4u : 16u) <= max_lds_per_block();
 }
 
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream) {
     const TiledDims d = TiledDims::of(w.n, w.k);
-    HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr && (up == nullptr || (up->codes != nullptr && up->sb != nullptr)),
+    const bool dual = up != nullptr;
+    HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr && (!dual || (up->codes != nullptr && up->sb != nullptr)),
                 HYP_STATUS_INTERNAL, "skinny: weights are not in the tiled resident layout");
-    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u, HYP_STATUS_INTERNAL, "skinny: bad split count");
-    HYP_REQUIRE(d.pairs >= splits, HYP_STATUS_INTERNAL, "skinny: fewer group pairs than splits");
-    HYP_REQUIRE(skinny_supported(m, w.k, up != nullptr), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
+    HYP_REQUIRE(!dual || (up->n == w.n && up->k == w.k), HYP_STATUS_INTERNAL, "skinny: gate and up differ in shape");
+    HYP_REQUIRE(skinny_supported(m, w.k, dual), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
     HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INTERNAL, "skinny: matrix exceeds 2 GiB of packed codes");
+    if (splits == 0u) splits = choose_skinny_splits(d.tiles, d.pairs, !dual && epi == Epilogue::kNone);
+    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u ||
+                    (!dual && epi == Epilogue::kNone && (splits == 8u || splits == 16u)),
+                HYP_STATUS_INTERNAL, "skinny: bad split count");
+    HYP_REQUIRE(d.pairs >= splits, HYP_STATUS_INTERNAL, "skinny: fewer group pairs than splits");
     SkinnyParams p{};
-    p.codes = w.codes;
-    p.sb = w.sb;
-    p.codes2 = up ? up->codes : nullptr;
-    p.sb2 = up ? up->sb : nullptr;
+    p.seg[0] = SkinnySegment{w.codes, w.sb, y, w.n, 0u};
+    p.nseg = 1u;
+    p.codes2 = dual ? up->codes : nullptr;
+    p.sb2 = dual ? up->sb : nullptr;
     p.x = x;
-    p.y = y;
-    p.n = w.n;
     p.k = w.k;
     p.pairs = d.pairs;
     p.cap = cap_bf16;
     p.splits = splits;
-    const bool dual = up != nullptr;
-    switch (m) {
-        case 1: launch_skinny_m<1>(p, dual, epi, stream); break;
-        case 2: launch_skinny_m<2>(p, dual, epi, stream); break;
-        case 3: launch_skinny_m<3>(p, dual, epi, stream); break;
-        case 4: launch_skinny_m<4>(p, dual, epi, stream); break;
-        default: throw NativeError(HYP_STATUS_INTERNAL, "skinny launched with m outside 1..4");
+    launch_skinny(p, d.tiles, m, dual, epi, stream);
+}
+
+void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                            uint32_t m, hipStream_t stream) {
+    HYP_REQUIRE(count >= 1u && count <= kSkinnyMaxGroup, HYP_STATUS_INTERNAL, "skinny: bad group size");
+    const uint32_t k = ws[0]->k;
+    HYP_REQUIRE(skinny_supported(m, k, false), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
+    SkinnyParams p{};
+    uint32_t tiles_total = 0u;
+    for (uint32_t i = 0; i < count; ++i) {
+        const Q4Matrix& w = *ws[i];
+        HYP_REQUIRE(w.k == k, HYP_STATUS_INTERNAL, "skinny: grouped projections differ in k");
+        HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr, HYP_STATUS_INTERNAL,
+                    "skinny: weights are not in the tiled resident layout");
+        const TiledDims d = TiledDims::of(w.n, w.k);
+        HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INTERNAL,
+                    "skinny: matrix exceeds 2 GiB of packed codes");
+        p.seg[i] = SkinnySegment{w.codes, w.sb, ys[i], w.n, tiles_total};
+        tiles_total += d.tiles;
     }
-    HYP_HIP_CHECK(hipGetLastError());
+    p.nseg = count;
+    p.x = x;
+    p.k = k;
+    p.pairs = TiledDims::of(16u, k).pairs;
+    p.cap = 0.0f;
+    p.splits = choose_skinny_splits(tiles_total, p.pairs, true);
+    launch_skinny(p, tiles_total, m, false, Epilogue::kNone, stream);
 }
 
 }  // namespace hyperion::hip

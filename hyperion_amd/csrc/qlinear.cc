@@ -138,7 +138,7 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
                             float cap_bf16) const {
     if (m == 0) return;
     if (hip::skinny_supported(m, mat.k, false)) {
-        hip::launch_q4_skinny(mat, nullptr, x, m, y, epi, cap_bf16, hip::choose_skinny_splits(mat.n, mat.k), stream);
+        hip::launch_q4_skinny(mat, nullptr, x, m, y, epi, cap_bf16, 0u, stream);
         return;
     }
     hip::launch_q4_gemm(mat, x, m, y, stream);
@@ -147,12 +147,23 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
     }
 }
 
+void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                 uint32_t m, hipStream_t stream) {
+    if (m == 0) return;
+    if (hip::skinny_supported(m, linears[0]->mat.k, false)) {
+        const hip::Q4Matrix* mats[hip::kSkinnyMaxGroup];
+        for (uint32_t i = 0; i < count; ++i) mats[i] = &linears[i]->mat;
+        hip::launch_q4_skinny_group(mats, ys, count, x, m, stream);
+        return;
+    }
+    for (uint32_t i = 0; i < count; ++i) hip::launch_q4_gemm(linears[i]->mat, x, m, ys[i], stream);
+}
+
 void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const uint16_t* x, uint32_t m,
                  uint16_t* h, hipStream_t stream) {
     if (m == 0) return;
     if (hip::skinny_supported(m, gate.mat.k, true)) {
-        hip::launch_q4_skinny(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f,
-                              hip::choose_skinny_splits(gate.mat.n, gate.mat.k), stream);
+        hip::launch_q4_skinny(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f, 0u, stream);
         return;
     }
     // h <- gate(x); u <- up(x) in a stream-ordered temporary; h <- gelu(h) * u.

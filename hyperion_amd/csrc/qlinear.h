@@ -72,6 +72,11 @@ struct QuantizedLinear {
 void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const uint16_t* x, uint32_t m,
                  uint16_t* h, hipStream_t stream);
 
+// ys[i] = x . dequant(W_i)^T for up to three projections sharing x and k (the attention
+// q/k/v of one layer, forward.cc:395,399,409): one launch at decode sizes.
+void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                 uint32_t m, hipStream_t stream);
+
 enum class LayerType { Sliding, Full };
 
 struct LayerWeights {

@@ -126,7 +126,7 @@ HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
 /* Graph capture of a launch sequence (e.g. one decode step) so it replays without
  * per-launch host work; the reference has no counterpart (MLX evaluates its lazy graph
  * at mx::eval, forward.cc:171). Between begin and end, hyp_qmatmul, hyp_qmatmul_ex,
- * hyp_qmlp_gate_up_gelu with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
+ * hyp_qmatmul_group, hyp_qmlp_gate_up_gelu with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
  * hyp_dequantize_q4g64 and hyp_embed on `stream` are recorded instead of run (they
  * allocate nothing); other calls on that stream are not allowed. The recorded pointers
  * and handles must stay valid while the graph is used. */
@@ -168,6 +168,15 @@ HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, Hyp
  * LM head + softcap of ForwardPass::lm_head/softcap (forward.cc:137-160). */
 HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y,
                          HypEpilogue epilogue, float cap, HypStream stream);
+
+/* ys[i][m, n_i] = x[m, k] * dequant(W_i)^T for count (1..HYP_QMATMUL_GROUP_MAX) weights
+ * that share k: the q/k/v projections of one attention block, which the reference applies
+ * to the same normed input one after another (forward.cc:395,399,409). At m <= 4 this is
+ * one launch over all of their rows; larger m runs the GEMM per weight. Same results as
+ * count separate hyp_qmatmul calls. */
+#define HYP_QMATMUL_GROUP_MAX 3u
+HypStatus hyp_qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
+                            void* const* ys, HypStream stream);
 
 /* h[m, n] = gelu_tanh(x * dequant(G)^T) * (x * dequant(U)^T), the gate/up half of
  * ForwardPass::mlp (forward.cc:338-343) with gelu_tanh rounded op-by-op in bf16 as

@@ -225,6 +225,76 @@ def test_gemv_layer_projections(stream, m):
         assert_within_bf16_rounding(y, truth, name)
 
 
+def run_group(ws, x, stream):
+    """hyp_qmatmul_group over the weights (MLX tensors) -> list of host outputs."""
+    qws = [hy.QWeight.from_host(*w) for w in ws]
+    m = x.shape[0]
+    xd = dev(x, stream)
+    yds = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
+    hy.qmatmul_group(qws, xd, m, yds, stream)
+    ys = [yd.to_host(stream) for yd in yds]
+    for q in qws:
+        q.close()
+    return ys
+
+
+@pytest.mark.parametrize("m", [1, 4, 5])
+def test_qmatmul_group_qkv(stream, m):
+    """q, k and v of one attention block in one grouped call (one launch at m <= 4,
+    the GEMM per weight above): each output meets the same bars as hyp_qmatmul."""
+    k = 3840
+    ws = [syn.q4_weights(n, k, seed=1200 + i) for i, n in enumerate((4096, 2048, 2048))]
+    x = syn.activations(m, k, seed=1210 + m)
+    ys = run_group(ws, x, stream)
+    for (w, s, b), y, name in zip(ws, ys, ("q", "k", "v")):
+        say(f"group m={m} {name}")
+        if m <= 4:
+            truth = O.qmatmul_f64(x, w, s, b)
+        else:
+            truth = O.qmatmul_deq_f64(x, w, s, b, mode=1)
+        assert syn.sig_rel(syn.bf16_to_f32(y), truth) <= 1e-2, name
+        assert_within_bf16_rounding(y, truth, name)
+
+
+def test_qmatmul_group_ragged_segments(stream):
+    """Segments of 3, 2 and 1 row tiles (n = 40, 24, 8, partly empty last tiles) and an
+    odd group count: workgroups straddle segment boundaries; every output matches the
+    fp64 reference, and nothing is written past a segment's n."""
+    k = 192
+    ws = [syn.q4_weights(n, k, seed=1220 + n) for n in (40, 24, 8)]
+    for m in (1, 2, 3, 4):
+        say(f"ragged group m={m}")
+        x = syn.activations(m, k, seed=1230 + m)
+        qws = [hy.QWeight.from_host(*w) for w in ws]
+        xd = dev(x, stream)
+        # One buffer with a guard band after each output: the kernel must not touch it.
+        sentinel = np.full((m * 64,), 0x7FC1, np.uint16)
+        yds = []
+        for w in ws:
+            buf = np.concatenate([np.zeros(m * w[0].shape[0], np.uint16), sentinel])
+            yds.append(dev(buf, stream))
+        hy.qmatmul_group(qws, xd, m, yds, stream)   # outputs start at each buffer's base
+        for (w, s, b), yd in zip(ws, yds):
+            n = w.shape[0]
+            got = yd.to_host(stream)
+            assert np.array_equal(got[m * n:], sentinel), f"n={n}: write past the output"
+            assert_within_bf16_rounding(got[:m * n].reshape(m, n), O.qmatmul_f64(x, w, s, b), f"n={n} m={m}")
+        for q in qws:
+            q.close()
+
+
+def test_qmatmul_group_rejects_mixed_k(stream):
+    a = hy.QWeight.from_host(*syn.q4_weights(16, 128, seed=1240))
+    b = hy.QWeight.from_host(*syn.q4_weights(16, 192, seed=1241))
+    x = dev(syn.activations(1, 128, seed=1242), stream)
+    ys = [hy.DeviceArray((1, 16), np.uint16) for _ in range(2)]
+    with pytest.raises(hy.HypError) as e:
+        hy.qmatmul_group([a, b], x, 1, ys, stream)
+    assert e.value.status_name == "INVALID_ARGUMENT"
+    a.close()
+    b.close()
+
+
 # ---------------------------------------------------------------- prefill GEMM
 
 @pytest.mark.parametrize("m", [512, 2048])
