@@ -44,7 +44,8 @@ EXPORTED = [
     "hyp_graph_capture_begin", "hyp_graph_capture_end", "hyp_graph_launch", "hyp_graph_free",
     "hyp_qweight_create", "hyp_qweight_create_device", "hyp_qweight_free",
     "hyp_qweight_shape", "hyp_qweight_export",
-    "hyp_qmatmul", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmlp_gate_up_gelu",
+    "hyp_qmatmul", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
+    "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
@@ -115,6 +116,7 @@ def lib() -> ctypes.CDLL:
         "hyp_qmatmul": [_P, _P, _U32, _P, _P],
         "hyp_qmatmul_ex": [_P, _P, _U32, _P, ctypes.c_int, ctypes.c_float, _P],
         "hyp_qmatmul_group": [_P, _U32, _P, _U32, _P, _P],
+        "hyp_qmatmul_group_rmsnorm": [_P, _U32, _P, _U32, ctypes.c_float, _P, _P],
         "hyp_qmlp_gate_up_gelu": [_P, _P, _P, _U32, _P, _P],
         "hyp_quantize_q4g64": [_P, _U32, _U32, _P, _P, _P, _P],
         "hyp_dequantize_q4g64": [_P, _P, _P, _U32, _U32, _P, _U32, ctypes.c_float, _P, _P],
@@ -386,13 +388,17 @@ def qmatmul(w: QWeight, x: DeviceArray, m: int, y: DeviceArray, stream: Stream,
         call("hyp_qmatmul_ex", w.handle, x.ptr, m, y.ptr, EPILOGUE_SOFTCAP, softcap, stream.handle)
 
 
-def qmatmul_group(ws, x: DeviceArray, m: int, ys, stream: Stream) -> None:
-    """ys[i] = x . dequant(ws[i])^T for up to three weights sharing k (one launch at m <= 4)."""
+def qmatmul_group(ws, x: DeviceArray, m: int, ys, stream: Stream, rms_eps: Optional[float] = None) -> None:
+    """ys[i] = x . dequant(ws[i])^T for up to three weights sharing k (one launch at m <= 4);
+    with rms_eps, x is rms-normalised first (hyp_qmatmul_group_rmsnorm)."""
     if len(ws) != len(ys):
         raise ValueError("qmatmul_group: one output per weight")
     handles = (ctypes.c_void_p * len(ws))(*[w.handle for w in ws])
     outs = (ctypes.c_void_p * len(ys))(*[y.ptr for y in ys])
-    call("hyp_qmatmul_group", handles, len(ws), x.ptr, m, outs, stream.handle)
+    if rms_eps is None:
+        call("hyp_qmatmul_group", handles, len(ws), x.ptr, m, outs, stream.handle)
+    else:
+        call("hyp_qmatmul_group_rmsnorm", handles, len(ws), x.ptr, m, rms_eps, outs, stream.handle)
 
 
 def qmlp_gate_up_gelu(gate: QWeight, up: QWeight, x: DeviceArray, m: int, h: DeviceArray,

@@ -451,24 +451,39 @@ HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, Hyp
     return hyp_qmatmul_ex(weight, x, m, y, HYP_EPILOGUE_NONE, 0.0f, stream);
 }
 
+namespace {
+
+void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m, const float* rms_eps,
+                   void* const* ys, HypStream stream) {
+    REQUIRE_ARG(weights != nullptr && ys != nullptr, "weights and ys must be non-null arrays");
+    REQUIRE_ARG(count >= 1u && count <= HYP_QMATMUL_GROUP_MAX, "count must be 1..HYP_QMATMUL_GROUP_MAX");
+    const QuantizedLinear* lins[HYP_QMATMUL_GROUP_MAX];
+    uint16_t* outs[HYP_QMATMUL_GROUP_MAX];
+    for (uint32_t i = 0; i < count; ++i) {
+        lins[i] = &qweight_ref(weights[i], "weights[i]");
+        REQUIRE_ARG(lins[i]->mat.k == lins[0]->mat.k, "grouped weights must share k");
+        outs[i] = static_cast<uint16_t*>(ys[i]);
+    }
+    if (rms_eps != nullptr) REQUIRE_ARG(std::isfinite(*rms_eps) && *rms_eps >= 0.0f, "eps must be finite and >= 0");
+    hipStream_t s = stream_of(stream);
+    if (m == 0) return;
+    REQUIRE_ARG(x != nullptr, "x must be a non-null device pointer");
+    for (uint32_t i = 0; i < count; ++i) REQUIRE_ARG(outs[i] != nullptr, "ys[i] must be non-null device pointers");
+    hyperion::model::apply_group(lins, outs, count, static_cast<const uint16_t*>(x), m, rms_eps, s);
+}
+
+}  // namespace
+
 HypStatus hyp_qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
                             void* const* ys, HypStream stream) {
-    return abi_call("hyp_qmatmul_group", [&] {
-        REQUIRE_ARG(weights != nullptr && ys != nullptr, "weights and ys must be non-null arrays");
-        REQUIRE_ARG(count >= 1u && count <= HYP_QMATMUL_GROUP_MAX, "count must be 1..HYP_QMATMUL_GROUP_MAX");
-        const QuantizedLinear* lins[HYP_QMATMUL_GROUP_MAX];
-        uint16_t* outs[HYP_QMATMUL_GROUP_MAX];
-        for (uint32_t i = 0; i < count; ++i) {
-            lins[i] = &qweight_ref(weights[i], "weights[i]");
-            REQUIRE_ARG(lins[i]->mat.k == lins[0]->mat.k, "grouped weights must share k");
-            outs[i] = static_cast<uint16_t*>(ys[i]);
-        }
-        hipStream_t s = stream_of(stream);
-        if (m == 0) return;
-        REQUIRE_ARG(x != nullptr, "x must be a non-null device pointer");
-        for (uint32_t i = 0; i < count; ++i) REQUIRE_ARG(outs[i] != nullptr, "ys[i] must be non-null device pointers");
-        hyperion::model::apply_group(lins, outs, count, static_cast<const uint16_t*>(x), m, s);
-    });
+    return abi_call("hyp_qmatmul_group",
+                    [&] { qmatmul_group(weights, count, x, m, nullptr, ys, stream); });
+}
+
+HypStatus hyp_qmatmul_group_rmsnorm(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
+                                    float eps, void* const* ys, HypStream stream) {
+    return abi_call("hyp_qmatmul_group_rmsnorm",
+                    [&] { qmatmul_group(weights, count, x, m, &eps, ys, stream); });
 }
 
 HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, uint32_t m, void* h,

@@ -45,13 +45,15 @@ constexpr uint32_t kSkinnyMaxGroup = 3;
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream);
 // One launch over `count` projections that share x (and k), e.g. q, k and v:
-// ys[i][m, n_i] = x . dequant(W_i)^T.
+// ys[i][m, n_i] = x . dequant(W_i)^T. With rms_eps non-null each x row is first
+// rms-normalised (q4_rmsnorm.h; the same bits as launch_rms_normalize) in LDS.
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                            uint32_t m, hipStream_t stream);
-// Splits for `tiles` 16-row tiles and `pairs` group pairs (wide: the plain form, which
-// allows 8 and 16), and whether (m, k) fits the kernel's LDS staging.
-uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, bool wide);
+                            uint32_t m, const float* rms_eps, hipStream_t stream);
+// Splits for `tiles` 16-row tiles, `pairs` group pairs and m rows (wide: the plain form,
+// which allows 8 and 16), and whether (m, k) fits the kernel's LDS staging.
+uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, bool wide);
 bool skinny_supported(uint32_t m, uint32_t k, bool dual);
+bool skinny_norm_supported(uint32_t m, uint32_t k);
 
 // Prefill GEMM on bf16 MFMA over the tiled layout: Q4 codes dequantized in registers,
 // x tiles in LDS. Plain bf16 output; epilogues for larger m run as the elementwise

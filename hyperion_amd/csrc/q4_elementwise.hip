@@ -7,6 +7,7 @@
 // Eight bf16 per thread (16-byte loads and stores; the pointers are 16-byte aligned).
 #include "common.h"
 #include "kernels.h"
+#include "q4_rmsnorm.h"
 
 namespace hyperion::hip {
 namespace {
@@ -106,9 +107,53 @@ void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t str
     HYP_HIP_CHECK(hipGetLastError());
 }
 
+namespace {
+
+// k a multiple of 64: one workgroup per row, a thread per 64-element unit (16-byte loads,
+// the unit kept in registers between the two passes), the summation order of
+// q4_rmsnorm.h - the same bits as the skinny matmul's normalising prologue.
+__global__ __launch_bounds__(kThreads) void rms_normalize_units_kernel(const uint16_t* __restrict__ x,
+                                                                       uint16_t* __restrict__ y, uint32_t k,
+                                                                       float eps) {
+    extern __shared__ float part[];   // [k / 64] unit partials, then the row's inverse
+    const uint32_t units = k / 64u;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(blockIdx.x) * k);
+    uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(blockIdx.x) * k);
+    const uint32_t tid = threadIdx.x;
+    uint4 xv[8];
+    for (uint32_t u = tid; u < units; u += kThreads) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xv[t] = xr[u * 8u + t];
+        part[u] = unit_sumsq(xv);
+    }
+    __syncthreads();
+    if (tid < 64u) {
+        const float ss = row_sumsq(part, units, tid);
+        if (tid == 0u) part[units] = rms_inverse(ss, k, eps);
+    }
+    __syncthreads();
+    const float inv = part[units];
+    for (uint32_t u = tid; u < units; u += kThreads) {
+        if (units > static_cast<uint32_t>(kThreads)) {   // more than one unit per thread: load it again
+#pragma unroll
+            for (int t = 0; t < 8; ++t) xv[t] = xr[u * 8u + t];
+        }
+        normalize_unit(xv, inv);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) yr[u * 8u + t] = xv[t];
+    }
+}
+
+}  // namespace
+
 void launch_rms_normalize(const uint16_t* x, uint32_t m, uint32_t k, float eps, uint16_t* y, hipStream_t stream) {
     if (m == 0 || k == 0) return;
-    hipLaunchKernelGGL(rms_normalize_kernel, dim3(m), dim3(kThreads), 0, stream, x, y, k, eps);
+    if (k % 64u == 0u && k / 64u + 1u <= 16384u) {
+        const size_t lds = (k / 64u + 1u) * sizeof(float);
+        hipLaunchKernelGGL(rms_normalize_units_kernel, dim3(m), dim3(kThreads), lds, stream, x, y, k, eps);
+    } else {
+        hipLaunchKernelGGL(rms_normalize_kernel, dim3(m), dim3(kThreads), 0, stream, x, y, k, eps);
+    }
     HYP_HIP_CHECK(hipGetLastError());
 }
 

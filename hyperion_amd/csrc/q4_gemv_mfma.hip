@@ -35,6 +35,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "q4_layout.h"
+#include "q4_rmsnorm.h"
 
 namespace hyperion::hip {
 namespace {
@@ -97,6 +98,7 @@ struct SkinnyParams {
     uint32_t pairs;       // ceil(k / 128)
     uint32_t splits;      // waves sharing one 16-row tile (divides the workgroup's waves)
     float cap;            // bf16 softcap constant
+    float eps;            // NORM: rms normalisation epsilon
 };
 
 // One matrix as seen by one lane: buffer resources and the lane's offsets into them.
@@ -211,7 +213,9 @@ __device__ __forceinline__ void compute_batch(const Batch<P> (&bt)[NW], uint32_t
     }
 }
 
-template <int M, bool DUAL, int EPI, int P, int NWAVE>
+// NORM: x rows are first rms-normalised (q4_rmsnorm.h) in LDS; the matmul then runs on
+// the normalised rows, which are not written back.
+template <int M, bool DUAL, int EPI, int P, int NWAVE, bool NORM>
 __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     constexpr int NW = DUAL ? 2 : 1;
     constexpr uint32_t kThreads = 64u * NWAVE;
@@ -223,6 +227,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     uint4* xs = smem;                                              // [M][W] permuted x
     float4* sx = reinterpret_cast<float4*>(smem + M * W);          // [G] group sums of x rows 0..3
     float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][NW][M][16]
+    float* part = red + NWAVE * NW * M * kTileRows;                // NORM: [M][G] unit partials, [M] inverses
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -277,15 +282,36 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
     for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + P * S, S, last, bb[q]);
 
+    if constexpr (NORM) {
+        // Per-unit sums of squares, then one wave per row forms its inverse rms.
+        for (uint32_t u = xu0; u < M * G; u += kThreads) {
+            if (u != xu0) {
+                const uint32_t m = u / G;
+                const uint32_t g = u - m * G;
+                const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) xv[t] = src[t];
+            }
+            part[u] = unit_sumsq(xv);
+        }
+        __syncthreads();
+        if (wave < static_cast<uint32_t>(M)) {
+            const float ss = row_sumsq(part + wave * G, G, lane);
+            if (lane == 0u) part[M * G + wave] = rms_inverse(ss, k, p.eps);
+        }
+        __syncthreads();
+    }
+
     // Stage x: each thread permutes whole groups (8 words) and sums them.
     for (uint32_t u = xu0; u < M * G; u += kThreads) {
         const uint32_t m = u / G;
         const uint32_t g = u - m * G;
-        if (u != xu0) {
+        if (u != xu0 || (NORM && M * G > kThreads)) {
             const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
 #pragma unroll
             for (int t = 0; t < 8; ++t) xv[t] = src[t];
         }
+        if constexpr (NORM) normalize_unit(xv, part[M * G + m]);
         float s0 = 0.0f;
         float s1 = 0.0f;
 #pragma unroll
@@ -371,19 +397,20 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     }
 }
 
-size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave) {
+size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool norm = false) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    return m * W * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u;
+    return m * W * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u +
+           (norm ? (m * G + m) * 4u : 0u);
 }
 
 size_t max_lds_per_block();
 
-template <int M, bool DUAL, int EPI, int NWAVE>
+template <int M, bool DUAL, int EPI, int NWAVE, bool NORM = false>
 void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t stream) {
     constexpr int P = 2;   // pairs per register batch (two batches in flight)
-    auto kernel = q4_skinny_kernel<M, DUAL, EPI, P, NWAVE>;
-    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE);
+    auto kernel = q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM>;
+    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM);
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "skinny: x staging exceeds the device's LDS");
     if (lds > 65536u) {
         static thread_local int configured_device = -1;
@@ -401,14 +428,27 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
     hipLaunchKernelGGL(kernel, grid, dim3(64 * NWAVE), lds, stream, p);
 }
 
-// Workgroups of max(4, splits) waves. The fused gate/up and the softcap head keep 4 (their
-// projections are wide, and the gate/up kernel holds two accumulator sets).
+// Workgroups of max(4, splits) waves. The fused gate/up keeps at most 8 and the softcap
+// head 4 (their projections are wide, and the gate/up kernel holds two accumulator sets).
 template <int M>
-void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, hipStream_t stream) {
+void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, bool norm,
+                     hipStream_t stream) {
     if (dual) {
-        launch_skinny_t<M, true, 0, 4>(p, tiles_total, stream);
+        if (p.splits == 8u) {
+            launch_skinny_t<M, true, 0, 8>(p, tiles_total, stream);
+        } else {
+            launch_skinny_t<M, true, 0, 4>(p, tiles_total, stream);
+        }
     } else if (epi == Epilogue::kSoftcap) {
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
+    } else if (norm) {
+        if (p.splits == 16u) {
+            launch_skinny_t<M, false, 0, 16, true>(p, tiles_total, stream);
+        } else if (p.splits == 8u) {
+            launch_skinny_t<M, false, 0, 8, true>(p, tiles_total, stream);
+        } else {
+            launch_skinny_t<M, false, 0, 4, true>(p, tiles_total, stream);
+        }
     } else if (p.splits == 16u) {
         launch_skinny_t<M, false, 0, 16>(p, tiles_total, stream);
     } else if (p.splits == 8u) {
@@ -418,12 +458,13 @@ void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epi
     }
 }
 
-void launch_skinny(SkinnyParams& p, uint32_t tiles_total, uint32_t m, bool dual, Epilogue epi, hipStream_t stream) {
+void launch_skinny(SkinnyParams& p, uint32_t tiles_total, uint32_t m, bool dual, Epilogue epi, bool norm,
+                   hipStream_t stream) {
     switch (m) {
-        case 1: launch_skinny_m<1>(p, tiles_total, dual, epi, stream); break;
-        case 2: launch_skinny_m<2>(p, tiles_total, dual, epi, stream); break;
-        case 3: launch_skinny_m<3>(p, tiles_total, dual, epi, stream); break;
-        case 4: launch_skinny_m<4>(p, tiles_total, dual, epi, stream); break;
+        case 1: launch_skinny_m<1>(p, tiles_total, dual, epi, norm, stream); break;
+        case 2: launch_skinny_m<2>(p, tiles_total, dual, epi, norm, stream); break;
+        case 3: launch_skinny_m<3>(p, tiles_total, dual, epi, norm, stream); break;
+        case 4: launch_skinny_m<4>(p, tiles_total, dual, epi, norm, stream); break;
         default: throw NativeError(HYP_STATUS_INTERNAL, "skinny launched with m outside 1..4");
     }
     HYP_HIP_CHECK(hipGetLastError());
@@ -445,17 +486,21 @@ size_t max_lds_per_block() {
 
 }  // namespace
 
-uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, bool wide) {
-    // Very wide problems (the 262144-row LM head): 2 waves per tile. Otherwise 4, and for
-    // projections with few row tiles (o, down, k, v; grouped q/k/v) up to 16 while the
-    // grid stays within 16 waves per CU and every wave keeps at least two group pairs.
-    // Never more splits than group pairs.
+uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, bool wide) {
+    // Measured on the decode shapes of a 12B layer (MI355X, cold weights):
+    //  * very wide problems (the 262144-row LM head), and wide ones (the 960-tile
+    //    15360 x 3840 projections) at m = 4: 2 waves per tile;
+    //  * otherwise 4, and for projections with few row tiles (o, k, v, grouped q/k/v)
+    //    8 while the grid stays within 16 waves per CU; 16 only when every wave still
+    //    gets at least four group pairs (down, k = 15360).
+    // The fused gate/up uses the same rule without the 8/16 branch, so it accumulates in
+    // the same order as two separate launches. Never more splits than group pairs.
     const uint32_t cus = device_compute_units();
     uint32_t s = 4u;
-    if (tiles * 4u > cus * 32u) {
+    if (tiles * 4u > cus * 32u || (m >= 4u && tiles * 4u > cus * 8u)) {
         s = 2u;
     } else if (wide) {
-        while (s < 16u && tiles * s * 2u <= cus * 16u && pairs >= 4u * s) s *= 2u;
+        while (s < 16u && tiles * s * 2u <= cus * 16u && pairs >= (s < 8u ? 4u : 8u) * s) s *= 2u;
     }
     while (s > 1u && pairs < s) s /= 2u;
     return s;
@@ -463,7 +508,12 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, bool wide) {
 
 bool skinny_supported(uint32_t m, uint32_t k, bool dual) {
     return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
-           skinny_lds_bytes(m, k, dual, dual ? 4u : 16u) <= max_lds_per_block();
+           skinny_lds_bytes(m, k, dual, dual ? 8u : 16u) <= max_lds_per_block();
+}
+
+bool skinny_norm_supported(uint32_t m, uint32_t k) {
+    return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
+           skinny_lds_bytes(m, k, false, 16u, true) <= max_lds_per_block();
 }
 
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
@@ -475,9 +525,9 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
     HYP_REQUIRE(!dual || (up->n == w.n && up->k == w.k), HYP_STATUS_INTERNAL, "skinny: gate and up differ in shape");
     HYP_REQUIRE(skinny_supported(m, w.k, dual), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
     HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INTERNAL, "skinny: matrix exceeds 2 GiB of packed codes");
-    if (splits == 0u) splits = choose_skinny_splits(d.tiles, d.pairs, !dual && epi == Epilogue::kNone);
-    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u ||
-                    (!dual && epi == Epilogue::kNone && (splits == 8u || splits == 16u)),
+    if (splits == 0u) splits = choose_skinny_splits(d.tiles, d.pairs, m, !dual && epi == Epilogue::kNone);
+    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u || (epi == Epilogue::kNone && splits == 8u) ||
+                    (!dual && epi == Epilogue::kNone && splits == 16u),
                 HYP_STATUS_INTERNAL, "skinny: bad split count");
     HYP_REQUIRE(d.pairs >= splits, HYP_STATUS_INTERNAL, "skinny: fewer group pairs than splits");
     SkinnyParams p{};
@@ -490,14 +540,16 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
     p.pairs = d.pairs;
     p.cap = cap_bf16;
     p.splits = splits;
-    launch_skinny(p, d.tiles, m, dual, epi, stream);
+    launch_skinny(p, d.tiles, m, dual, epi, false, stream);
 }
 
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                            uint32_t m, hipStream_t stream) {
+                            uint32_t m, const float* rms_eps, hipStream_t stream) {
     HYP_REQUIRE(count >= 1u && count <= kSkinnyMaxGroup, HYP_STATUS_INTERNAL, "skinny: bad group size");
     const uint32_t k = ws[0]->k;
-    HYP_REQUIRE(skinny_supported(m, k, false), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
+    const bool norm = rms_eps != nullptr;
+    HYP_REQUIRE(norm ? skinny_norm_supported(m, k) : skinny_supported(m, k, false), HYP_STATUS_INTERNAL,
+                "skinny: shape exceeds LDS");
     SkinnyParams p{};
     uint32_t tiles_total = 0u;
     for (uint32_t i = 0; i < count; ++i) {
@@ -516,8 +568,9 @@ void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint
     p.k = k;
     p.pairs = TiledDims::of(16u, k).pairs;
     p.cap = 0.0f;
-    p.splits = choose_skinny_splits(tiles_total, p.pairs, true);
-    launch_skinny(p, tiles_total, m, false, Epilogue::kNone, stream);
+    p.eps = norm ? *rms_eps : 0.0f;
+    p.splits = choose_skinny_splits(tiles_total, p.pairs, m, true);
+    launch_skinny(p, tiles_total, m, false, Epilogue::kNone, norm, stream);
 }
 
 }  // namespace hyperion::hip

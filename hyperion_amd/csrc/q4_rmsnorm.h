@@ -1,0 +1,60 @@
+// Row RMS normalisation shared by the standalone kernel and the normalising prologue of
+// the skinny matmul, so both produce the same bits: y = bf16(x * inv) with
+// inv = 1 / sqrt(ss / k + eps), where ss is summed in one fixed order -
+//   1. per 64-element unit (k ascending), a sequential fp32 fma chain;
+//   2. per row, lane l of one wave adds units l, l + 64, l + 128, ... in that order,
+//      then an xor butterfly over the 64 lanes (offsets 32, 16, ..., 1).
+// A weightless mx::fast::rms_norm (the reference normalises with it around every block,
+// native/hyperion_mlx/src/forward.cc:521-529).
+#pragma once
+
+#include "common.h"
+
+namespace hyperion::hip {
+
+// Sum of squares of one 64-element unit (8 x 16 bytes of bf16, k ascending).
+__device__ __forceinline__ float unit_sumsq(const uint4 (&xv)[8]) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float lo = bf16_bits_to_f32(w[q] & 0xFFFFu);
+            const float hi = bf16_bits_to_f32(w[q] >> 16);
+            ss = fmaf(lo, lo, ss);
+            ss = fmaf(hi, hi, ss);
+        }
+    }
+    return ss;
+}
+
+// Step 2 for one row whose unit partials are part[0 .. units): every lane gets the total.
+__device__ __forceinline__ float row_sumsq(const float* part, uint32_t units, uint32_t lane) {
+    float ss = 0.0f;
+    for (uint32_t i = lane; i < units; i += 64u) ss += part[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    return ss;
+}
+
+__device__ __forceinline__ float rms_inverse(float ss, uint32_t k, float eps) {
+    return 1.0f / sqrtf(ss / static_cast<float>(k) + eps);
+}
+
+// x <- bf16(x * inv) for the 64 values of a unit.
+__device__ __forceinline__ void normalize_unit(uint4 (&xv)[8], float inv) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * inv);
+            const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * inv);
+            w[q] = lo | (hi << 16);
+        }
+        xv[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+}  // namespace hyperion::hip

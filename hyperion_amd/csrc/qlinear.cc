@@ -148,15 +148,31 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
 }
 
 void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                 uint32_t m, hipStream_t stream) {
+                 uint32_t m, const float* rms_eps, hipStream_t stream) {
     if (m == 0) return;
-    if (hip::skinny_supported(m, linears[0]->mat.k, false)) {
+    const uint32_t k = linears[0]->mat.k;
+    if (rms_eps ? hip::skinny_norm_supported(m, k) : hip::skinny_supported(m, k, false)) {
         const hip::Q4Matrix* mats[hip::kSkinnyMaxGroup];
         for (uint32_t i = 0; i < count; ++i) mats[i] = &linears[i]->mat;
-        hip::launch_q4_skinny_group(mats, ys, count, x, m, stream);
+        hip::launch_q4_skinny_group(mats, ys, count, x, m, rms_eps, stream);
         return;
     }
-    for (uint32_t i = 0; i < count; ++i) hip::launch_q4_gemm(linears[i]->mat, x, m, ys[i], stream);
+    if (rms_eps == nullptr) {
+        for (uint32_t i = 0; i < count; ++i) hip::launch_q4_gemm(linears[i]->mat, x, m, ys[i], stream);
+        return;
+    }
+    // The normalised rows in a stream-ordered temporary, then the GEMM per projection.
+    void* xn = nullptr;
+    HYP_HIP_CHECK(hipMallocAsync(&xn, static_cast<size_t>(m) * k * sizeof(uint16_t), stream));
+    try {
+        hip::launch_rms_normalize(x, m, k, *rms_eps, static_cast<uint16_t*>(xn), stream);
+        for (uint32_t i = 0; i < count; ++i)
+            hip::launch_q4_gemm(linears[i]->mat, static_cast<const uint16_t*>(xn), m, ys[i], stream);
+    } catch (...) {
+        (void)hipFreeAsync(xn, stream);
+        throw;
+    }
+    HYP_HIP_CHECK(hipFreeAsync(xn, stream));
 }
 
 void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const uint16_t* x, uint32_t m,

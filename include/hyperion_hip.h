@@ -126,7 +126,7 @@ HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
 /* Graph capture of a launch sequence (e.g. one decode step) so it replays without
  * per-launch host work; the reference has no counterpart (MLX evaluates its lazy graph
  * at mx::eval, forward.cc:171). Between begin and end, hyp_qmatmul, hyp_qmatmul_ex,
- * hyp_qmatmul_group, hyp_qmlp_gate_up_gelu with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
+ * hyp_qmatmul_group, hyp_qmlp_gate_up_gelu and hyp_qmatmul_group_rmsnorm with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
  * hyp_dequantize_q4g64 and hyp_embed on `stream` are recorded instead of run (they
  * allocate nothing); other calls on that stream are not allowed. The recorded pointers
  * and handles must stay valid while the graph is used. */
@@ -177,6 +177,13 @@ HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y,
 #define HYP_QMATMUL_GROUP_MAX 3u
 HypStatus hyp_qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
                             void* const* ys, HypStream stream);
+
+/* hyp_rms_normalize(x, m, k, eps) followed by hyp_qmatmul_group on its output, with the
+ * same results bit for bit: the pre-attention normalisation and q/k/v of one block
+ * (forward.cc:521-529, 395-409). At m <= 4 it is one launch that normalises the rows in
+ * on-chip memory and does not write them back; x is left unchanged either way. */
+HypStatus hyp_qmatmul_group_rmsnorm(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
+                                    float eps, void* const* ys, HypStream stream);
 
 /* h[m, n] = gelu_tanh(x * dequant(G)^T) * (x * dequant(U)^T), the gate/up half of
  * ForwardPass::mlp (forward.cc:338-343) with gelu_tanh rounded op-by-op in bf16 as

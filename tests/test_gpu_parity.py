@@ -340,6 +340,9 @@ def _assert_close_bits(got, ref, what):
 
 @pytest.mark.parametrize("m", [1, 4, 300])
 def test_gate_up_gelu_fused(stream, m):
+    """The fused gate/up (m <= 4: one launch) against the oracle's bf16 GELU chain applied
+    to separate gate and up launches. At m <= 4 the fused kernel splits each tile over as
+    many waves as the separate launches do, so its bf16 gate and up values are the same."""
     n, k = 15360, 3840
     say(f"gate/up gelu m={m}")
     x = syn.activations(m, k, seed=600 + m)
@@ -468,6 +471,49 @@ def test_rms_normalize_rows(stream):
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-8 * 1.01 + 1e-30)
     hy.rms_normalize(xd, m, k, xd, stream, eps=1e-6)   # in place
     np.testing.assert_array_equal(xd.to_host(stream), yd.to_host(stream))
+
+
+@pytest.mark.parametrize("k", [1000, 19200])
+def test_rms_normalize_other_widths(stream, k):
+    """k not a multiple of 64 (the element-wise kernel) and more 64-wide units per row
+    than threads (19200 = 300 units: units loaded twice)."""
+    m = 3
+    x = syn.activations(m, k, seed=960 + k)
+    yd = hy.DeviceArray((m, k), np.uint16)
+    hy.rms_normalize(dev(x, stream), m, k, yd, stream, eps=1e-5)
+    got = syn.bf16_to_f32(yd.to_host(stream)).astype(np.float64)
+    xf = syn.bf16_to_f32(x).astype(np.float64)
+    ref = xf / np.sqrt(np.mean(xf * xf, axis=1, keepdims=True) + 1e-5)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-8 * 1.01 + 1e-30)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5])
+def test_qmatmul_group_rmsnorm_equals_two_calls(stream, m):
+    """hyp_qmatmul_group_rmsnorm == hyp_rms_normalize then hyp_qmatmul_group, bit for bit
+    (one launch with the normalisation in LDS at m <= 4, a temporary above), x unchanged,
+    and within the qmatmul bars of the fp64 product of the normalised rows."""
+    k = 3840
+    ws = [syn.q4_weights(n, k, seed=1250 + i) for i, n in enumerate((4096, 2048, 2048))]
+    qws = [hy.QWeight.from_host(*w) for w in ws]
+    x = syn.activations(m, k, seed=1260 + m)
+    x[0] = syn.bf16_bits(syn.bf16_to_f32(x[0]) * np.float32(37.0))   # rows of different scale
+    xd = dev(x, stream)
+    fused = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
+    hy.qmatmul_group(qws, xd, m, fused, stream, rms_eps=1e-6)
+    np.testing.assert_array_equal(xd.to_host(stream), x)
+    xn = hy.DeviceArray((m, k), np.uint16)
+    hy.rms_normalize(xd, m, k, xn, stream, eps=1e-6)
+    sep = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
+    hy.qmatmul_group(qws, xn, m, sep, stream)
+    xn_host = xn.to_host(stream)
+    for (w, s, b), f, g, name in zip(ws, fused, sep, ("q", "k", "v")):
+        say(f"group rmsnorm m={m} {name}")
+        yf = f.to_host(stream)
+        np.testing.assert_array_equal(yf, g.to_host(stream), err_msg=name)
+        truth = O.qmatmul_f64(xn_host, w, s, b) if m <= 4 else O.qmatmul_deq_f64(xn_host, w, s, b, mode=1)
+        assert_within_bf16_rounding(yf, truth, name)
+    for q in qws:
+        q.close()
 
 
 # ---------------------------------------------------------------- graph capture
