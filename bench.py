@@ -268,6 +268,7 @@ def main():
     ap.add_argument("--layers", type=int, default=syn.NUM_LAYERS, help="decoder layers in the decode stream")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-decode", action="store_true", help="only the headline decode GEMV")
+    ap.add_argument("--only-prefill", action="store_true", help="the headline decode GEMV and the prefill GEMMs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device-to-device copies of 256 MiB (the reference kernel of known "
@@ -290,7 +291,9 @@ def main():
         log(f"copy calibration: 5 x {nbytes} bytes device-to-device")
     dec = bench_decode_gemv(stream, args.steps, args.warmup, args.copies)
     extra = {}
-    if not args.only_decode:
+    if args.only_prefill:
+        extra["prefill"] = [bench_prefill(stream, m, 10, 2) for m in (512, 2048)]
+    elif not args.only_decode:
         extra["quantize"] = bench_quantize(stream, 50, 5)
         extra["prefill"] = [bench_prefill(stream, m, 10, 2) for m in (512, 2048)]
         model = DecodeModel(args.layers, stream)
