@@ -119,11 +119,45 @@ def bench_quantize(stream, steps, warmup, copies=4):
             "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
 
-def bench_prefill(stream, m, steps, warmup):
+def dense_bf16_child(m, steps, warmup):
+    """Child-process mode: hipBLASLt's dense bf16 GEMM (torch.matmul, bf16 weights, no
+    dequantisation) on the seven projection shapes at m rows, timed with torch's events on
+    torch's stream; prints {name: ms} as JSON. torch brings its own HIP runtime, which does
+    not share a process with this library's, hence the separate process."""
+    import torch
+    dev = torch.device("cuda:0")
+    out = {}
+    for name, (n, k) in syn.LAYER_SHAPES.items():
+        x = torch.randn(m, k, device=dev, dtype=torch.bfloat16)
+        wt = torch.randn(k, n, device=dev, dtype=torch.bfloat16)
+        for _ in range(warmup):
+            torch.matmul(x, wt)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch.matmul(x, wt)
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) / steps
+    print(json.dumps(out), flush=True)
+
+
+def dense_bf16_reference(m, steps, warmup):
+    """Runs dense_bf16_child in a child process (called before this process touches the GPU)."""
+    import subprocess
+    res = subprocess.run([sys.executable, os.path.abspath(__file__), "--dense-child", str(m),
+                          "--steps", str(steps), "--warmup", str(warmup)],
+                         capture_output=True, text=True, timeout=600, check=True)
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def bench_prefill(stream, m, steps, warmup, dense=None):
     log(f"prefill m={m}: seven projections")
     per = {}
     total_flops = 0
     total_ms = 0.0
+    dense_ms = 0.0
     for i, (name, (n, k)) in enumerate(syn.LAYER_SHAPES.items()):
         w, s, b = syn.q4_weights(n, k, seed=500 + i)
         qw = hy.QWeight.from_host(w, s, b)
@@ -132,14 +166,26 @@ def bench_prefill(stream, m, steps, warmup):
         ms = time_launches(stream, lambda _i: hy.qmatmul(qw, xd, m, yd, stream), steps, warmup)
         flops = 2 * m * n * k
         per[name] = {"n": n, "k": k, "us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1)}
+        msg = f"  {name:5s} n={n:5d} k={k:5d}: {ms * 1e3:8.1f} us  {flops / ms / 1e9:6.0f} TFLOP/s"
+        if dense is not None:
+            dms = dense[name]
+            dense_ms += dms
+            per[name]["dense_bf16_tflops"] = round(flops / dms / 1e9, 1)
+            msg += f"   (dense bf16 hipBLASLt {flops / dms / 1e9:6.0f} TFLOP/s)"
         total_flops += flops
         total_ms += ms
-        log(f"  {name:5s} n={n:5d} k={k:5d}: {ms * 1e3:8.1f} us  {flops / ms / 1e9:6.0f} TFLOP/s")
+        log(msg)
         qw.close()
     tflops = total_flops / total_ms / 1e9
     log(f"prefill layer m={m}: {total_ms * 1e3:.1f} us  {tflops:.0f} TFLOP/s")
-    return {"m": m, "layer_us": round(total_ms * 1e3, 1), "tflops": round(tflops, 1),
-            "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "per_projection": per}
+    out = {"m": m, "layer_us": round(total_ms * 1e3, 1), "tflops": round(tflops, 1),
+           "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "per_projection": per}
+    if dense is not None:
+        dense = total_flops / dense_ms / 1e9
+        out["dense_bf16_layer_tflops"] = round(dense, 1)
+        out["frac_of_dense_bf16"] = round(tflops / dense, 4)
+        log(f"prefill layer m={m}: dense bf16 hipBLASLt {dense:.0f} TFLOP/s; Q4 GEMM at {tflops / dense:.1%} of it")
+    return out
 
 
 class DecodeModel:
@@ -269,6 +315,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-decode", action="store_true", help="only the headline decode GEMV")
     ap.add_argument("--only-prefill", action="store_true", help="the headline decode GEMV and the prefill GEMMs")
+    ap.add_argument("--dense-ref", action="store_true",
+                    help="also time hipBLASLt's dense bf16 GEMM (torch.matmul) on the prefill shapes")
+    ap.add_argument("--dense-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 5 device-to-device copies of 256 MiB (the reference kernel of known "
@@ -278,6 +327,11 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs on a single "
               "MI355X; the multi-GPU sharding of the path is a design, not a measured run)", file=sys.stderr)
         sys.exit(2)
+    if args.dense_child:
+        dense_bf16_child(args.dense_child, 10, 2)
+        return
+    # The dense reference runs in child processes before this process makes any HIP call.
+    dense = {m: dense_bf16_reference(m, 10, 2) for m in (512, 2048)} if args.dense_ref else {}
 
     info = hy.runtime_info()
     log(f"{info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units}")
@@ -292,10 +346,10 @@ def main():
     dec = bench_decode_gemv(stream, args.steps, args.warmup, args.copies)
     extra = {}
     if args.only_prefill:
-        extra["prefill"] = [bench_prefill(stream, m, 10, 2) for m in (512, 2048)]
+        extra["prefill"] = [bench_prefill(stream, m, 10, 2, dense.get(m)) for m in (512, 2048)]
     elif not args.only_decode:
         extra["quantize"] = bench_quantize(stream, 50, 5)
-        extra["prefill"] = [bench_prefill(stream, m, 10, 2) for m in (512, 2048)]
+        extra["prefill"] = [bench_prefill(stream, m, 10, 2, dense.get(m)) for m in (512, 2048)]
         model = DecodeModel(args.layers, stream)
         streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
