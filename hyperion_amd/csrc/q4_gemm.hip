@@ -283,6 +283,205 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     }
 }
 
+// ---- group-step variant: 256-row tiles, one group (64 k) per iteration ---------------
+//
+// The same scheme with 16 row tiles per wave (each dequantized B fragment feeds 16 MFMAs
+// instead of 8) and 64-k iterations, so two workgroups still fit a CU: X stages of
+// 256 rows x 128 bytes (chunks swizzled by row % 8), double buffered; the raw weights of
+// a group are half of each 16-byte entry (plus its scale word), loaded two groups ahead.
+// k-step s of a group uses word 2 kb + s of the lane's entry, and the A fragments the
+// same k chunk.
+
+constexpr uint32_t kGRowBytes = 128u;   // one group of one X row
+
+template <int NT>
+struct GRaw {
+    uint2 c[NT];       // words 2 kb, 2 kb + 1 of the group
+    uint32_t sb[NT];   // scale | bias << 16 of the group
+};
+
+template <int NT>
+__device__ __forceinline__ void load_graw(__amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t sr,
+                                          const uint32_t (&c_off)[NT], const uint32_t (&s_off)[NT], uint32_t g,
+                                          GRaw<NT>& raw) {
+    const uint32_t pair = g >> 1;
+    const uint32_t h = g & 1u;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        raw.c[nt] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(cr, c_off[nt], pair * 1024u + h * 8u, 0));
+        raw.sb[nt] = __builtin_amdgcn_raw_buffer_load_b32(sr, s_off[nt], pair * 128u + h * 4u, 0);
+    }
+}
+
+template <int NT, int S>
+__device__ __forceinline__ void gdequant(const GRaw<NT>& raw, bf16x8_t (&b)[NT]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const float sc = bf16_bits_to_f32(raw.sb[nt] & 0xFFFFu);
+        const float bi = bf16_bits_to_f32(raw.sb[nt] >> 16);
+        b[nt] = dequant_word(S == 0 ? raw.c[nt].x : raw.c[nt].y, sc, bi);
+    }
+}
+
+template <int MT, int NT, int S>
+__device__ __forceinline__ void gmfma(const uint8_t* xb, uint32_t lane, const bf16x8_t (&b)[NT],
+                                      f32x4_t (&acc)[MT][NT]) {
+    const uint32_t i = lane & 15u;
+    const uint32_t kb = lane >> 4;
+    const uint32_t c = 2u * kb + S;   // this lane's logical k chunk of the group
+    const uint8_t* row = xb + i * kGRowBytes + ((c ^ (i & 7u)) << 4);
+    constexpr int kHalf = MT / 2;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        bf16x8_t a[kHalf];
+#pragma unroll
+        for (int mt = 0; mt < kHalf; ++mt)
+            a[mt] = *reinterpret_cast<const bf16x8_t*>(row + (h * kHalf + mt) * 16u * kGRowBytes);
+#pragma unroll
+        for (int mt = 0; mt < kHalf; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                acc[h * kHalf + mt][nt] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], b[nt], acc[h * kHalf + mt][nt], 0, 0, 0);
+    }
+}
+
+template <int MT, int NT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_g_kernel(GemmParams p) {
+    constexpr uint32_t BM = 16u * MT;
+    constexpr uint32_t kStage = BM * kGRowBytes;
+    constexpr int kXLoads = static_cast<int>(BM / 8u / kWaves);   // 1 KB (8 rows) direct loads per wave
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];   // [2][BM][128 B], reused by the epilogue
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    const uint32_t bid = blockIdx.x;
+    const uint32_t xcd = bid & 7u;
+    const uint32_t slot = bid >> 3;
+    const uint32_t per = p.tiles_total >> 3;
+    const uint32_t rem = p.tiles_total & 7u;
+    const uint32_t tile = xcd * per + min(xcd, rem) + slot;
+    const uint32_t tm = tile / p.tiles_n;
+    const uint32_t tn = tile - tm * p.tiles_n;
+    const uint32_t m0 = tm * BM;
+    const uint32_t n0 = tn * (kWaves * 16u * NT);
+    const uint32_t tile16_0 = n0 / 16u + wave * NT;
+    const uint32_t k = p.k;
+    const uint32_t G = k / 64u;
+
+    // X: load t of wave w fills LDS rows 8 (w kXLoads + t) .. +7; lane l writes physical
+    // chunk l % 8 of row r = 8 (w kXLoads + t) + l / 8 with logical chunk (l % 8) ^ (l / 8).
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.x), static_cast<short>(0), static_cast<int>(p.m * k * 2u), 0x00020000);
+    uint32_t xoff[kXLoads];
+#pragma unroll
+    for (int t = 0; t < kXLoads; ++t) {
+        const uint32_t row = m0 + 8u * (wave * kXLoads + t) + (lane >> 3);
+        const uint32_t chunk = (lane & 7u) ^ (lane >> 3);
+        xoff[t] = row < p.m ? row * k * 2u + chunk * 16u : 0x80000000u;
+    }
+    auto load_x = [&](uint32_t g, uint8_t* buf) {
+#pragma unroll
+        for (int t = 0; t < kXLoads; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)(buf + (wave * kXLoads + t) * 1024u), 16,
+                static_cast<int>(xoff[t]), static_cast<int>(g * 128u), 0, 0);
+    };
+
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint4*>(p.codes), static_cast<short>(0), static_cast<int>(p.code_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint2*>(p.sb), static_cast<short>(0), static_cast<int>(p.sb_bytes), 0x00020000);
+    uint32_t c_off[NT];
+    uint32_t s_off[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t t16 = min(tile16_0 + nt, p.row_tiles - 1u);
+        c_off[nt] = (t16 * p.pairs * 64u + lane) * 16u;
+        s_off[nt] = (t16 * p.pairs * 16u + (lane & 15u)) * 8u;
+    }
+
+    f32x4_t acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    GRaw<NT> r0, r1, r2;
+    load_x(0u, xs);
+    load_graw<NT>(cr, sr, c_off, s_off, 0u, r0);
+    load_graw<NT>(cr, sr, c_off, s_off, min(1u, G - 1u), r1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    bf16x8_t b0[NT], b1[NT];
+    gdequant<NT, 0>(r0, b0);
+
+    // Branch-free loop; past the last group the loads repeat the last group (unused).
+    for (uint32_t g = 0; g < G; ++g) {
+        const uint8_t* xb = xs + (g & 1u) * kStage;
+        load_x(min(g + 1u, G - 1u), xs + ((g + 1u) & 1u) * kStage);
+        __builtin_amdgcn_sched_barrier(0);   // the raw loads below issue after the X loads
+        load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, G - 1u), r2);
+        gdequant<NT, 1>(r0, b1);
+        gmfma<MT, NT, 0>(xb, lane, b0, acc);
+        gdequant<NT, 0>(r1, b0);
+        gmfma<MT, NT, 1>(xb, lane, b1, acc);
+        r0 = r1;
+        r1 = r2;
+        // The next X stage has landed once at most this iteration's 2 NT raw loads remain.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NT) : "memory");
+        __syncthreads();
+    }
+
+    // Epilogue through LDS as in q4_gemm_kernel.
+    constexpr uint32_t kOutRow = 128u * NT + 32u;
+    __syncthreads();
+    {
+        const uint32_t j = lane & 15u;
+        const uint32_t kb = lane >> 4;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = mt * 16u + kb * 4u + r;
+                    const uint32_t col = (wave * NT + nt) * 16u + j;
+                    *reinterpret_cast<uint16_t*>(xs + row * kOutRow + col * 2u) = f32_to_bf16_bits(acc[mt][nt][r]);
+                }
+    }
+    __syncthreads();
+    constexpr uint32_t kChunks = 64u * NT / 8u;
+    constexpr uint32_t kRowsPerPass = kThreads / kChunks;
+    const uint32_t ch = threadIdx.x % kChunks;
+    const uint32_t col0 = n0 + ch * 8u;
+    if ((p.n & 7u) == 0u) {
+        for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
+            const uint32_t row = m0 + r;
+            if (row < p.m && col0 < p.n)
+                *reinterpret_cast<uint4*>(p.y + static_cast<size_t>(row) * p.n + col0) =
+                    *reinterpret_cast<const uint4*>(xs + r * kOutRow + ch * 16u);
+        }
+    } else {
+        for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
+            const uint32_t row = m0 + r;
+            if (row >= p.m) continue;
+            for (uint32_t c = 0; c < 8u; ++c)
+                if (col0 + c < p.n)
+                    p.y[static_cast<size_t>(row) * p.n + col0 + c] =
+                        *reinterpret_cast<const uint16_t*>(xs + r * kOutRow + ch * 16u + c * 2u);
+        }
+    }
+}
+
+template <int MT, int NT>
+constexpr size_t g_lds_bytes() {
+    return 2u * 16u * MT * kGRowBytes > 16u * MT * (128u * NT + 32u) ? 2u * 16u * MT * kGRowBytes
+                                                                     : 16u * MT * (128u * NT + 32u);
+}
+
 size_t max_lds_per_block() {
     static thread_local int cached_device = -1;
     static thread_local size_t cached = 0;
@@ -321,6 +520,27 @@ void launch_t(GemmParams p, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3(p.tiles_total), dim3(kThreads), lds, stream, p);
 }
 
+template <int MT, int NT>
+void launch_g(GemmParams p, hipStream_t stream) {
+    auto kernel = q4_gemm_g_kernel<MT, NT>;
+    constexpr size_t lds = g_lds_bytes<MT, NT>();
+    HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
+    if (lds > 65536u) {
+        static thread_local int configured_device = -1;
+        int dev = 0;
+        HYP_HIP_CHECK(hipGetDevice(&dev));
+        if (configured_device != dev) {
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            configured_device = dev;
+        }
+    }
+    p.tiles_n = (p.n + kWaves * 16u * NT - 1u) / (kWaves * 16u * NT);
+    const uint32_t tiles_m = (p.m + 16u * MT - 1u) / (16u * MT);
+    p.tiles_total = p.tiles_n * tiles_m;
+    hipLaunchKernelGGL(kernel, dim3(p.tiles_total), dim3(kThreads), lds, stream, p);
+}
+
 }  // namespace
 
 void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
@@ -344,7 +564,7 @@ void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uin
     p.code_bytes = static_cast<uint32_t>(d.code_bytes());
     p.sb_bytes = static_cast<uint32_t>(d.sb_bytes());
     if (mt == 16u && nt == 2u) {
-        launch_t<16, 2>(p, stream);
+        launch_g<16, 2>(p, stream);
     } else if (mt == 8u && nt == 2u) {
         launch_t<8, 2>(p, stream);
     } else {
@@ -354,9 +574,13 @@ void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uin
 }
 
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {
-    // 128 x 128 workgroup tiles (wave tile 128 x 32, three waves per SIMD): the fastest
-    // of the four shapes on every projection of the 12B layer at m = 512 and 2048.
-    launch_q4_gemm_config(w, x, m, y, 8u, 2u, stream);
+    // The 256 x 128 group-step kernel halves the dequantization per MFMA but runs two
+    // workgroups per CU; it is faster once its grid holds at least two workgroups per CU
+    // (the 15360-row gate/up at m = 2048: 869 vs 759 TFLOP/s), the 128 x 128 kernel
+    // otherwise (fewer tiles: q, k, v, o, down at 2048, every projection at 512).
+    const uint64_t big_tiles = static_cast<uint64_t>((m + 255u) / 256u) * ((w.n + 127u) / 128u);
+    const bool big = big_tiles >= 2ull * device_compute_units();
+    launch_q4_gemm_config(w, x, m, y, big ? 16u : 8u, 2u, stream);
 }
 
 }  // namespace hyperion::hip

@@ -330,6 +330,32 @@ def test_gemm_exact_integer_and_ragged_tiles(stream):
         np.testing.assert_array_equal(y, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"{m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("n,k", [(8200, 192), (8195, 320), (8200, 3840)])
+def test_gemm_group_step_tiles(stream, n, k):
+    """Grids of >= 2 workgroups per CU select the 256 x 128 group-step kernel: ragged m
+    (2000 rows, the last row tile part-empty), n with a part-empty 16-row tile (8200) or
+    n % 8 != 0 (8195: the element-wise store path), odd group counts (k = 192, 320).
+    Sampled rows against the fp64 product with the kernel's bf16 weights, and all rows
+    exact on integer inputs."""
+    m = 2000
+    say(f"gemm group-step m={m} n={n} k={k}")
+    x = syn.activations(m, k, seed=1300 + k)
+    w, s, b = syn.q4_weights(n, k, seed=1301 + n)
+    y = run_qmatmul(w, s, b, x, stream)
+    rng = np.random.default_rng(n + k)
+    rows = np.sort(rng.choice(m, size=12, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    assert_within_bf16_rounding(y[rows], O.qmatmul_deq_f64(x[rows], w, s, b, mode=1), f"n={n} k={k}")
+    # exact arithmetic over every row and column
+    xi = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+    codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+    s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+    b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+    exact = (xi.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
+    y2 = run_qmatmul(syn.pack_codes(codes), s2, b2, syn.bf16_bits(xi), stream)
+    np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"exact n={n} k={k}")
+
+
 # ---------------------------------------------------------------- fused epilogues
 
 def _assert_close_bits(got, ref, what):
