@@ -10,7 +10,8 @@ events on the stream the kernel runs on.
 
 Also reported, each on its own workload:
   quantize    bf16 W [15360,3840] N(0, 0.02^2) with 1% x8 outliers -> Q4/g64 (GB/s)
-  prefill     the seven projections at m = 512 and 2048 (TFLOP/s vs bf16 MFMA peak)
+  prefill     the seven projections at m = 512 and 2048, q/k/v in one grouped launch
+              (TFLOP/s vs bf16 MFMA peak)
   decode      48 layers (renormalise + q/k/v in one launch, o, fused gate/up + GELU, down)
               + tied LM head [262144,3840] with softcap, m = 1 and 4, replayed from a
               captured HIP graph (tokens/s and effective HBM GB/s), with the LM head
@@ -119,15 +120,24 @@ def bench_quantize(stream, steps, warmup, copies=4):
             "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
 
+# The prefill calls of one layer as the engine makes them: q, k and v in one grouped launch
+# (they share the normed input), then o, gate, up and down.
+PREFILL_CALLS = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate", ("gate",)), ("up", ("up",)),
+                 ("down", ("down",)))
+
+
 def dense_bf16_child(m, steps, warmup):
     """Child-process mode: hipBLASLt's dense bf16 GEMM (torch.matmul, bf16 weights, no
-    dequantisation) on the seven projection shapes at m rows, timed with torch's events on
-    torch's stream; prints {name: ms} as JSON. torch brings its own HIP runtime, which does
-    not share a process with this library's, hence the separate process."""
+    dequantisation) on the layer's prefill calls at m rows (q/k/v as one [8192, 3840]
+    weight), timed with torch's events on torch's stream; prints {call: ms} as JSON. torch
+    brings its own HIP runtime, which does not share a process with this library's, hence
+    the separate process."""
     import torch
     dev = torch.device("cuda:0")
     out = {}
-    for name, (n, k) in syn.LAYER_SHAPES.items():
+    for call_name, projs in PREFILL_CALLS:
+        k = syn.LAYER_SHAPES[projs[0]][1]
+        n = sum(syn.LAYER_SHAPES[p][0] for p in projs)
         x = torch.randn(m, k, device=dev, dtype=torch.bfloat16)
         wt = torch.randn(k, n, device=dev, dtype=torch.bfloat16)
         for _ in range(warmup):
@@ -139,7 +149,7 @@ def dense_bf16_child(m, steps, warmup):
             torch.matmul(x, wt)
         e1.record()
         torch.cuda.synchronize()
-        out[name] = e0.elapsed_time(e1) / steps
+        out[call_name] = e0.elapsed_time(e1) / steps
     print(json.dumps(out), flush=True)
 
 
@@ -153,38 +163,48 @@ def dense_bf16_reference(m, steps, warmup):
 
 
 def bench_prefill(stream, m, steps, warmup, dense=None):
-    log(f"prefill m={m}: seven projections")
+    log(f"prefill m={m}: the layer's calls (q/k/v grouped)")
     per = {}
     total_flops = 0
     total_ms = 0.0
     dense_ms = 0.0
-    for i, (name, (n, k)) in enumerate(syn.LAYER_SHAPES.items()):
-        w, s, b = syn.q4_weights(n, k, seed=500 + i)
-        qw = hy.QWeight.from_host(w, s, b)
-        xd = hy.DeviceArray.from_host(syn.activations(m, k, seed=400 + i), stream)
-        yd = hy.DeviceArray((m, n), np.uint16)
-        ms = time_launches(stream, lambda _i: hy.qmatmul(qw, xd, m, yd, stream), steps, warmup)
-        flops = 2 * m * n * k
-        per[name] = {"n": n, "k": k, "us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1)}
-        msg = f"  {name:5s} n={n:5d} k={k:5d}: {ms * 1e3:8.1f} us  {flops / ms / 1e9:6.0f} TFLOP/s"
+    for ci, (call_name, projs) in enumerate(PREFILL_CALLS):
+        k = syn.LAYER_SHAPES[projs[0]][1]
+        qws, yds = [], []
+        for pi, proj in enumerate(projs):
+            n = syn.LAYER_SHAPES[proj][0]
+            w, s, b = syn.q4_weights(n, k, seed=500 + 8 * ci + pi)
+            qws.append(hy.QWeight.from_host(w, s, b))
+            yds.append(hy.DeviceArray((m, n), np.uint16))
+        xd = hy.DeviceArray.from_host(syn.activations(m, k, seed=400 + ci), stream)
+        if len(qws) == 1:
+            fn = lambda _i: hy.qmatmul(qws[0], xd, m, yds[0], stream)  # noqa: E731
+        else:
+            fn = lambda _i: hy.qmatmul_group(qws, xd, m, yds, stream)  # noqa: E731
+        ms = time_launches(stream, fn, steps, warmup)
+        n_total = sum(syn.LAYER_SHAPES[p][0] for p in projs)
+        flops = 2 * m * n_total * k
+        per[call_name] = {"n": n_total, "k": k, "us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1)}
+        msg = f"  {call_name:5s} n={n_total:5d} k={k:5d}: {ms * 1e3:8.1f} us  {flops / ms / 1e9:6.0f} TFLOP/s"
         if dense is not None:
-            dms = dense[name]
+            dms = dense[call_name]
             dense_ms += dms
-            per[name]["dense_bf16_tflops"] = round(flops / dms / 1e9, 1)
+            per[call_name]["dense_bf16_tflops"] = round(flops / dms / 1e9, 1)
             msg += f"   (dense bf16 hipBLASLt {flops / dms / 1e9:6.0f} TFLOP/s)"
         total_flops += flops
         total_ms += ms
         log(msg)
-        qw.close()
+        for q in qws:
+            q.close()
     tflops = total_flops / total_ms / 1e9
     log(f"prefill layer m={m}: {total_ms * 1e3:.1f} us  {tflops:.0f} TFLOP/s")
     out = {"m": m, "layer_us": round(total_ms * 1e3, 1), "tflops": round(tflops, 1),
-           "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "per_projection": per}
+           "frac_of_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "per_call": per}
     if dense is not None:
-        dense = total_flops / dense_ms / 1e9
-        out["dense_bf16_layer_tflops"] = round(dense, 1)
-        out["frac_of_dense_bf16"] = round(tflops / dense, 4)
-        log(f"prefill layer m={m}: dense bf16 hipBLASLt {dense:.0f} TFLOP/s; Q4 GEMM at {tflops / dense:.1%} of it")
+        dense_tf = total_flops / dense_ms / 1e9
+        out["dense_bf16_layer_tflops"] = round(dense_tf, 1)
+        out["frac_of_dense_bf16"] = round(tflops / dense_tf, 4)
+        log(f"prefill layer m={m}: dense bf16 hipBLASLt {dense_tf:.0f} TFLOP/s; Q4 GEMM at {tflops / dense_tf:.1%} of it")
     return out
 
 

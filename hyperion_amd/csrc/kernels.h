@@ -59,6 +59,10 @@ bool skinny_norm_supported(uint32_t m, uint32_t k);
 // x tiles in LDS. Plain bf16 output; epilogues for larger m run as the elementwise
 // kernels below.
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
+// One launch over `count` (<= 3) projections that share x and k (q, k and v):
+// ys[i][m, n_i] = x . dequant(W_i)^T.
+void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                          uint32_t m, hipStream_t stream);
 // Same with an explicit workgroup tile: (16 * mt) x (64 * nt), nt = 2; mt = 8 is the
 // pair-step kernel (128 x 128), mt = 16 the group-step kernel (256 x 128).
 void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,

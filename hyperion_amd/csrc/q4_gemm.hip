@@ -41,21 +41,62 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kPairK = 128;                 // k per iteration (two groups)
 constexpr int kRowBytes = kPairK * 2;       // one LDS row of an X tile
 
-struct GemmParams {
+// One projection of a (possibly grouped) launch: its workgroup column tiles are the
+// global column tiles [tn_begin, tn_begin + ceil(n / 128)).
+struct GemmSegment {
     const uint4* codes;   // tiled codes (q4_layout.h)
     const uint2* sb;      // tiled scales and biases
-    const uint16_t* x;    // m x k bf16 (m * k * 2 < 2^31 bytes)
-    uint16_t* y;
-    uint32_t m;
+    uint16_t* y;          // [m, n]
     uint32_t n;
-    uint32_t k;
-    uint32_t pairs;       // ceil(k / 128)
     uint32_t row_tiles;   // ceil(n / 16)
-    uint32_t tiles_n;     // workgroup tiles along n
-    uint32_t tiles_total;
     uint32_t code_bytes;
     uint32_t sb_bytes;
+    uint32_t tn_begin;
 };
+
+constexpr uint32_t kMaxGemmSegments = 3;
+
+struct GemmParams {
+    GemmSegment seg[kMaxGemmSegments];   // segments past nseg are unused
+    uint32_t nseg;
+    const uint16_t* x;    // m x k bf16 (m * k * 2 < 2^31 bytes)
+    uint32_t m;
+    uint32_t k;
+    uint32_t pairs;       // ceil(k / 128)
+    uint32_t tiles_n;     // workgroup column tiles over all segments
+    uint32_t tiles_total;
+};
+
+// The segment of global column tile tn (workgroup-uniform selects, no indexed parameter
+// access) and tn's index within it.
+struct SegView {
+    const uint4* codes;
+    const uint2* sb;
+    uint16_t* y;
+    uint32_t n;
+    uint32_t row_tiles;
+    uint32_t code_bytes;
+    uint32_t sb_bytes;
+    uint32_t tn;
+};
+
+__device__ __forceinline__ SegView segment_of(const GemmParams& p, uint32_t tn) {
+    const bool in1 = p.nseg > 1u && tn >= p.seg[1].tn_begin;
+    const bool in2 = p.nseg > 2u && tn >= p.seg[2].tn_begin;
+    const GemmSegment& a = p.seg[0];
+    const GemmSegment& b = p.seg[1];
+    const GemmSegment& c = p.seg[2];
+    SegView v;
+    v.codes = in2 ? c.codes : (in1 ? b.codes : a.codes);
+    v.sb = in2 ? c.sb : (in1 ? b.sb : a.sb);
+    v.y = in2 ? c.y : (in1 ? b.y : a.y);
+    v.n = in2 ? c.n : (in1 ? b.n : a.n);
+    v.row_tiles = in2 ? c.row_tiles : (in1 ? b.row_tiles : a.row_tiles);
+    v.code_bytes = in2 ? c.code_bytes : (in1 ? b.code_bytes : a.code_bytes);
+    v.sb_bytes = in2 ? c.sb_bytes : (in1 ? b.sb_bytes : a.sb_bytes);
+    v.tn = tn - (in2 ? c.tn_begin : (in1 ? b.tn_begin : 0u));
+    return v;
+}
 
 // Raw weights of one pair for one lane: NT code entries and NT scale entries.
 template <int NT>
@@ -147,9 +188,9 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     const uint32_t rem = p.tiles_total & 7u;
     const uint32_t tile = xcd * per + min(xcd, rem) + slot;
     const uint32_t tm = tile / p.tiles_n;
-    const uint32_t tn = tile - tm * p.tiles_n;
+    const SegView sv = segment_of(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
-    const uint32_t n0 = tn * (kWaves * 16u * NT);
+    const uint32_t n0 = sv.tn * (kWaves * 16u * NT);
     const uint32_t tile16_0 = n0 / 16u + wave * NT;
 
     const uint32_t k = p.k;
@@ -188,14 +229,14 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     // Weights: column tile (tile16_0 + nt), clamped to the last tile (columns past n are
     // computed, never stored).
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint4*>(p.codes), static_cast<short>(0), static_cast<int>(p.code_bytes), 0x00020000);
+        const_cast<uint4*>(sv.codes), static_cast<short>(0), static_cast<int>(sv.code_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint2*>(p.sb), static_cast<short>(0), static_cast<int>(p.sb_bytes), 0x00020000);
+        const_cast<uint2*>(sv.sb), static_cast<short>(0), static_cast<int>(sv.sb_bytes), 0x00020000);
     uint32_t c_off[NT];
     uint32_t s_off[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t t16 = min(tile16_0 + nt, p.row_tiles - 1u);
+        const uint32_t t16 = min(tile16_0 + nt, sv.row_tiles - 1u);
         c_off[nt] = (t16 * pairs * 64u + lane) * 16u;
         s_off[nt] = (t16 * pairs * 16u + (lane & 15u)) * 8u;
     }
@@ -264,11 +305,11 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     constexpr uint32_t kRowsPerPass = kThreads / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
     const uint32_t col0 = n0 + ch * 8u;
-    if ((p.n & 7u) == 0u) {
+    if ((sv.n & 7u) == 0u) {
         for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
             const uint32_t row = m0 + r;
-            if (row < p.m && col0 < p.n)
-                *reinterpret_cast<uint4*>(p.y + static_cast<size_t>(row) * p.n + col0) =
+            if (row < p.m && col0 < sv.n)
+                *reinterpret_cast<uint4*>(sv.y + static_cast<size_t>(row) * sv.n + col0) =
                     *reinterpret_cast<const uint4*>(xs + r * kOutRow + ch * 16u);
         }
     } else {
@@ -276,8 +317,8 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
             const uint32_t row = m0 + r;
             if (row >= p.m) continue;
             for (uint32_t c = 0; c < 8u; ++c)
-                if (col0 + c < p.n)
-                    p.y[static_cast<size_t>(row) * p.n + col0 + c] =
+                if (col0 + c < sv.n)
+                    sv.y[static_cast<size_t>(row) * sv.n + col0 + c] =
                         *reinterpret_cast<const uint16_t*>(xs + r * kOutRow + ch * 16u + c * 2u);
         }
     }
@@ -364,9 +405,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t rem = p.tiles_total & 7u;
     const uint32_t tile = xcd * per + min(xcd, rem) + slot;
     const uint32_t tm = tile / p.tiles_n;
-    const uint32_t tn = tile - tm * p.tiles_n;
+    const SegView sv = segment_of(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
-    const uint32_t n0 = tn * (kWaves * 16u * NT);
+    const uint32_t n0 = sv.tn * (kWaves * 16u * NT);
     const uint32_t tile16_0 = n0 / 16u + wave * NT;
     const uint32_t k = p.k;
     const uint32_t G = k / 64u;
@@ -391,14 +432,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint4*>(p.codes), static_cast<short>(0), static_cast<int>(p.code_bytes), 0x00020000);
+        const_cast<uint4*>(sv.codes), static_cast<short>(0), static_cast<int>(sv.code_bytes), 0x00020000);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint2*>(p.sb), static_cast<short>(0), static_cast<int>(p.sb_bytes), 0x00020000);
+        const_cast<uint2*>(sv.sb), static_cast<short>(0), static_cast<int>(sv.sb_bytes), 0x00020000);
     uint32_t c_off[NT];
     uint32_t s_off[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t t16 = min(tile16_0 + nt, p.row_tiles - 1u);
+        const uint32_t t16 = min(tile16_0 + nt, sv.row_tiles - 1u);
         c_off[nt] = (t16 * p.pairs * 64u + lane) * 16u;
         s_off[nt] = (t16 * p.pairs * 16u + (lane & 15u)) * 8u;
     }
@@ -457,11 +498,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     constexpr uint32_t kRowsPerPass = kThreads / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
     const uint32_t col0 = n0 + ch * 8u;
-    if ((p.n & 7u) == 0u) {
+    if ((sv.n & 7u) == 0u) {
         for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
             const uint32_t row = m0 + r;
-            if (row < p.m && col0 < p.n)
-                *reinterpret_cast<uint4*>(p.y + static_cast<size_t>(row) * p.n + col0) =
+            if (row < p.m && col0 < sv.n)
+                *reinterpret_cast<uint4*>(sv.y + static_cast<size_t>(row) * sv.n + col0) =
                     *reinterpret_cast<const uint4*>(xs + r * kOutRow + ch * 16u);
         }
     } else {
@@ -469,8 +510,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             const uint32_t row = m0 + r;
             if (row >= p.m) continue;
             for (uint32_t c = 0; c < 8u; ++c)
-                if (col0 + c < p.n)
-                    p.y[static_cast<size_t>(row) * p.n + col0 + c] =
+                if (col0 + c < sv.n)
+                    sv.y[static_cast<size_t>(row) * sv.n + col0 + c] =
                         *reinterpret_cast<const uint16_t*>(xs + r * kOutRow + ch * 16u + c * 2u);
         }
     }
@@ -514,7 +555,6 @@ void launch_t(GemmParams p, hipStream_t stream) {
             configured_device = dev;
         }
     }
-    p.tiles_n = (p.n + kWaves * 16u * NT - 1u) / (kWaves * 16u * NT);
     const uint32_t tiles_m = (p.m + 16u * MT - 1u) / (16u * MT);
     p.tiles_total = p.tiles_n * tiles_m;
     hipLaunchKernelGGL(kernel, dim3(p.tiles_total), dim3(kThreads), lds, stream, p);
@@ -535,37 +575,46 @@ void launch_g(GemmParams p, hipStream_t stream) {
             configured_device = dev;
         }
     }
-    p.tiles_n = (p.n + kWaves * 16u * NT - 1u) / (kWaves * 16u * NT);
     const uint32_t tiles_m = (p.m + 16u * MT - 1u) / (16u * MT);
     p.tiles_total = p.tiles_n * tiles_m;
     hipLaunchKernelGGL(kernel, dim3(p.tiles_total), dim3(kThreads), lds, stream, p);
 }
 
-}  // namespace
+constexpr uint32_t kTileCols = 128u;   // workgroup tile width of both kernels (NT = 2)
 
-void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
-                           hipStream_t stream) {
-    HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr, HYP_STATUS_INTERNAL,
-                "gemm: weights are not in the tiled resident layout");
-    HYP_REQUIRE(static_cast<uint64_t>(m) * w.k * 2u < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT,
+// Parameters of a grouped launch; tiles_total is set by the launcher of the chosen kernel.
+GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                        uint32_t m) {
+    HYP_REQUIRE(count >= 1u && count <= kMaxGemmSegments, HYP_STATUS_INTERNAL, "gemm: bad group size");
+    const uint32_t k = ws[0]->k;
+    HYP_REQUIRE(static_cast<uint64_t>(m) * k * 2u < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT,
                 "gemm: x is 2 GiB or larger");
-    const TiledDims d = TiledDims::of(w.n, w.k);
     GemmParams p{};
-    p.codes = w.codes;
-    p.sb = w.sb;
+    uint32_t tn = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const Q4Matrix& w = *ws[i];
+        HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr, HYP_STATUS_INTERNAL,
+                    "gemm: weights are not in the tiled resident layout");
+        HYP_REQUIRE(w.k == k, HYP_STATUS_INTERNAL, "gemm: grouped projections differ in k");
+        const TiledDims d = TiledDims::of(w.n, w.k);
+        HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT, "gemm: weights of 2 GiB or more");
+        p.seg[i] = GemmSegment{w.codes, w.sb, ys[i], w.n, d.tiles, static_cast<uint32_t>(d.code_bytes()),
+                               static_cast<uint32_t>(d.sb_bytes()), tn};
+        tn += (w.n + kTileCols - 1u) / kTileCols;
+    }
+    p.nseg = count;
     p.x = x;
-    p.y = y;
     p.m = m;
-    p.n = w.n;
-    p.k = w.k;
-    p.pairs = d.pairs;
-    p.row_tiles = d.tiles;
-    HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT, "gemm: weights of 2 GiB or more");
-    p.code_bytes = static_cast<uint32_t>(d.code_bytes());
-    p.sb_bytes = static_cast<uint32_t>(d.sb_bytes());
-    if (mt == 16u && nt == 2u) {
+    p.k = k;
+    p.pairs = TiledDims::of(16u, k).pairs;
+    p.tiles_n = tn;
+    return p;
+}
+
+void launch_params(GemmParams& p, uint32_t mt, hipStream_t stream) {
+    if (mt == 16u) {
         launch_g<16, 2>(p, stream);
-    } else if (mt == 8u && nt == 2u) {
+    } else if (mt == 8u) {
         launch_t<8, 2>(p, stream);
     } else {
         throw NativeError(HYP_STATUS_INTERNAL, "gemm: unsupported tile shape");
@@ -573,14 +622,36 @@ void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uin
     HYP_HIP_CHECK(hipGetLastError());
 }
 
+// The 256 x 128 group-step kernel halves the dequantization per MFMA but runs two
+// workgroups per CU; it is faster once its grid holds at least two workgroups per CU
+// (the 15360-row gate/up at m = 2048: 869 vs 759 TFLOP/s), the 128 x 128 kernel
+// otherwise (fewer tiles: q, k, v, o, down at 2048, every projection at 512).
+uint32_t choose_mt(const GemmParams& p) {
+    const uint64_t big_tiles = static_cast<uint64_t>((p.m + 255u) / 256u) * p.tiles_n;
+    return big_tiles >= 2ull * device_compute_units() ? 16u : 8u;
+}
+
+}  // namespace
+
+void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
+                           hipStream_t stream) {
+    HYP_REQUIRE(nt == 2u, HYP_STATUS_INTERNAL, "gemm: unsupported tile shape");
+    const Q4Matrix* ws[1] = {&w};
+    uint16_t* ys[1] = {y};
+    GemmParams p = group_params(ws, ys, 1u, x, m);
+    launch_params(p, mt, stream);
+}
+
+void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
+                          uint32_t m, hipStream_t stream) {
+    GemmParams p = group_params(ws, ys, count, x, m);
+    launch_params(p, choose_mt(p), stream);
+}
+
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {
-    // The 256 x 128 group-step kernel halves the dequantization per MFMA but runs two
-    // workgroups per CU; it is faster once its grid holds at least two workgroups per CU
-    // (the 15360-row gate/up at m = 2048: 869 vs 759 TFLOP/s), the 128 x 128 kernel
-    // otherwise (fewer tiles: q, k, v, o, down at 2048, every projection at 512).
-    const uint64_t big_tiles = static_cast<uint64_t>((m + 255u) / 256u) * ((w.n + 127u) / 128u);
-    const bool big = big_tiles >= 2ull * device_compute_units();
-    launch_q4_gemm_config(w, x, m, y, big ? 16u : 8u, 2u, stream);
+    const Q4Matrix* ws[1] = {&w};
+    uint16_t* ys[1] = {y};
+    launch_q4_gemm_group(ws, ys, 1u, x, m, stream);
 }
 
 }  // namespace hyperion::hip

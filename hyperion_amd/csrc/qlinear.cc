@@ -151,23 +151,22 @@ void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uin
                  uint32_t m, const float* rms_eps, hipStream_t stream) {
     if (m == 0) return;
     const uint32_t k = linears[0]->mat.k;
+    const hip::Q4Matrix* mats[hip::kSkinnyMaxGroup];
+    for (uint32_t i = 0; i < count; ++i) mats[i] = &linears[i]->mat;
     if (rms_eps ? hip::skinny_norm_supported(m, k) : hip::skinny_supported(m, k, false)) {
-        const hip::Q4Matrix* mats[hip::kSkinnyMaxGroup];
-        for (uint32_t i = 0; i < count; ++i) mats[i] = &linears[i]->mat;
         hip::launch_q4_skinny_group(mats, ys, count, x, m, rms_eps, stream);
         return;
     }
     if (rms_eps == nullptr) {
-        for (uint32_t i = 0; i < count; ++i) hip::launch_q4_gemm(linears[i]->mat, x, m, ys[i], stream);
+        hip::launch_q4_gemm_group(mats, ys, count, x, m, stream);
         return;
     }
-    // The normalised rows in a stream-ordered temporary, then the GEMM per projection.
+    // The normalised rows in a stream-ordered temporary, then the grouped GEMM.
     void* xn = nullptr;
     HYP_HIP_CHECK(hipMallocAsync(&xn, static_cast<size_t>(m) * k * sizeof(uint16_t), stream));
     try {
         hip::launch_rms_normalize(x, m, k, *rms_eps, static_cast<uint16_t*>(xn), stream);
-        for (uint32_t i = 0; i < count; ++i)
-            hip::launch_q4_gemm(linears[i]->mat, static_cast<const uint16_t*>(xn), m, ys[i], stream);
+        hip::launch_q4_gemm_group(mats, ys, count, static_cast<const uint16_t*>(xn), m, stream);
     } catch (...) {
         (void)hipFreeAsync(xn, stream);
         throw;
