@@ -26,6 +26,8 @@
 //  * Workgroup ids are remapped so each XCD (ids are dealt round-robin over the 8 XCDs)
 //    gets a contiguous run of tiles that share X rows, keeping the X block in that
 //    XCD's L2.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 #include "q4_dequant.h"
@@ -52,6 +54,7 @@ struct GemmSegment {
     uint32_t code_bytes;
     uint32_t sb_bytes;
     uint32_t tn_begin;
+    uint32_t col_begin;   // first column of this segment in the split-k workspace rows
 };
 
 constexpr uint32_t kMaxGemmSegments = 3;
@@ -65,6 +68,12 @@ struct GemmParams {
     uint32_t pairs;       // ceil(k / 128)
     uint32_t tiles_n;     // workgroup column tiles over all segments
     uint32_t tiles_total;
+    // Split k (pair-step kernel): ksplit workgroups share an output tile, each covering
+    // pairs_per_split pairs, and write fp32 partials to partial[ksplit][m][n_total].
+    uint32_t ksplit;
+    uint32_t pairs_per_split;
+    uint32_t n_total;
+    float* partial;
 };
 
 // The segment of global column tile tn (workgroup-uniform selects, no indexed parameter
@@ -77,6 +86,7 @@ struct SegView {
     uint32_t row_tiles;
     uint32_t code_bytes;
     uint32_t sb_bytes;
+    uint32_t col_begin;
     uint32_t tn;
 };
 
@@ -94,6 +104,7 @@ __device__ __forceinline__ SegView segment_of(const GemmParams& p, uint32_t tn) 
     v.row_tiles = in2 ? c.row_tiles : (in1 ? b.row_tiles : a.row_tiles);
     v.code_bytes = in2 ? c.code_bytes : (in1 ? b.code_bytes : a.code_bytes);
     v.sb_bytes = in2 ? c.sb_bytes : (in1 ? b.sb_bytes : a.sb_bytes);
+    v.col_begin = in2 ? c.col_begin : (in1 ? b.col_begin : a.col_begin);
     v.tn = tn - (in2 ? c.tn_begin : (in1 ? b.tn_begin : 0u));
     return v;
 }
@@ -184,9 +195,12 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     const uint32_t bid = blockIdx.x;
     const uint32_t xcd = bid & 7u;
     const uint32_t slot = bid >> 3;
-    const uint32_t per = p.tiles_total >> 3;
-    const uint32_t rem = p.tiles_total & 7u;
-    const uint32_t tile = xcd * per + min(xcd, rem) + slot;
+    const uint32_t ext_total = p.tiles_total * p.ksplit;
+    const uint32_t per = ext_total >> 3;
+    const uint32_t rem = ext_total & 7u;
+    const uint32_t ext = xcd * per + min(xcd, rem) + slot;
+    const uint32_t kz = ext / p.tiles_total;          // this workgroup's k split
+    const uint32_t tile = ext - kz * p.tiles_total;
     const uint32_t tm = tile / p.tiles_n;
     const SegView sv = segment_of(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
@@ -247,9 +261,13 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // This workgroup's pairs [p0, p1) (all of them without split k).
+    const uint32_t p0 = kz * p.pairs_per_split;
+    const uint32_t p1 = min(p0 + p.pairs_per_split, pairs);
+
     BRaw<NT> braw, bnext;
-    load_x(0u, xs);
-    load_b<NT>(cr, sr, c_off, s_off, 0u, braw);
+    load_x(p0, xs);
+    load_b<NT>(cr, sr, c_off, s_off, p0, braw);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
@@ -258,10 +276,10 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 
     // The loop body has no branches (branches split the accumulators' live ranges and
     // cost AGPR copies); the last iteration prefetches its own pair again, harmlessly.
-    for (uint32_t pair = 0; pair < pairs; ++pair) {
-        const uint8_t* xb = xs + (pair & 1u) * kTileBytes;
-        const uint32_t pn = min(pair + 1u, pairs - 1u);
-        load_x(pn, xs + ((pair + 1u) & 1u) * kTileBytes);
+    for (uint32_t pair = p0; pair < p1; ++pair) {
+        const uint8_t* xb = xs + ((pair - p0) & 1u) * kTileBytes;
+        const uint32_t pn = min(pair + 1u, p1 - 1u);
+        load_x(pn, xs + ((pair - p0 + 1u) & 1u) * kTileBytes);
         load_b<NT>(cr, sr, c_off, s_off, pn, bnext);
 
         dequant_step<NT, 1>(braw, b1);
@@ -276,6 +294,26 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+    }
+
+    if (p.ksplit > 1u) {
+        // Split k: fp32 partials, summed by q4_splitk_reduce_kernel.
+        const uint32_t j = lane & 15u;
+        const uint32_t kb = lane >> 4;
+        float* part = p.partial + static_cast<size_t>(kz) * p.m * p.n_total;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t col = n0 + (wave * NT + nt) * 16u + j;
+            if (col >= sv.n) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = m0 + mt * 16u + kb * 4u + r;
+                    if (row < p.m) part[static_cast<size_t>(row) * p.n_total + sv.col_begin + col] = acc[mt][nt][r];
+                }
+        }
+        return;
     }
 
     // Epilogue: the workgroup's (16 MT) x (64 NT) tile goes through LDS (rows of
@@ -523,6 +561,24 @@ constexpr size_t g_lds_bytes() {
                                                                      : 16u * MT * (128u * NT + 32u);
 }
 
+// y_seg[row][col] = bf16(sum over splits z = 0, 1, ... of partial[z][row][col_begin + col]),
+// one thread per element of the m x n_total workspace row block.
+__global__ __launch_bounds__(kThreads) void q4_splitk_reduce_kernel(GemmParams p) {
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(p.m) * p.n_total;
+    if (e >= total) return;
+    const uint32_t row = static_cast<uint32_t>(e / p.n_total);
+    const uint32_t c = static_cast<uint32_t>(e - static_cast<uint64_t>(row) * p.n_total);
+    float sum = 0.0f;
+    for (uint32_t z = 0; z < p.ksplit; ++z) sum += p.partial[z * total + e];
+    const bool in1 = p.nseg > 1u && c >= p.seg[1].col_begin;
+    const bool in2 = p.nseg > 2u && c >= p.seg[2].col_begin;
+    uint16_t* y = in2 ? p.seg[2].y : (in1 ? p.seg[1].y : p.seg[0].y);
+    const uint32_t n = in2 ? p.seg[2].n : (in1 ? p.seg[1].n : p.seg[0].n);
+    const uint32_t c0 = in2 ? p.seg[2].col_begin : (in1 ? p.seg[1].col_begin : 0u);
+    y[static_cast<size_t>(row) * n + (c - c0)] = f32_to_bf16_bits(sum);
+}
+
 size_t max_lds_per_block() {
     static thread_local int cached_device = -1;
     static thread_local size_t cached = 0;
@@ -557,11 +613,12 @@ void launch_t(GemmParams p, hipStream_t stream) {
     }
     const uint32_t tiles_m = (p.m + 16u * MT - 1u) / (16u * MT);
     p.tiles_total = p.tiles_n * tiles_m;
-    hipLaunchKernelGGL(kernel, dim3(p.tiles_total), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL(kernel, dim3(p.tiles_total * p.ksplit), dim3(kThreads), lds, stream, p);
 }
 
 template <int MT, int NT>
 void launch_g(GemmParams p, hipStream_t stream) {
+    HYP_REQUIRE(p.ksplit == 1u, HYP_STATUS_INTERNAL, "gemm: the group-step kernel does not split k");
     auto kernel = q4_gemm_g_kernel<MT, NT>;
     constexpr size_t lds = g_lds_bytes<MT, NT>();
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
@@ -591,6 +648,7 @@ GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t
                 "gemm: x is 2 GiB or larger");
     GemmParams p{};
     uint32_t tn = 0;
+    uint32_t n_total = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const Q4Matrix& w = *ws[i];
         HYP_REQUIRE(w.codes != nullptr && w.sb != nullptr, HYP_STATUS_INTERNAL,
@@ -599,8 +657,9 @@ GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t
         const TiledDims d = TiledDims::of(w.n, w.k);
         HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT, "gemm: weights of 2 GiB or more");
         p.seg[i] = GemmSegment{w.codes, w.sb, ys[i], w.n, d.tiles, static_cast<uint32_t>(d.code_bytes()),
-                               static_cast<uint32_t>(d.sb_bytes()), tn};
+                               static_cast<uint32_t>(d.sb_bytes()), tn, n_total};
         tn += (w.n + kTileCols - 1u) / kTileCols;
+        n_total += w.n;
     }
     p.nseg = count;
     p.x = x;
@@ -608,6 +667,10 @@ GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t
     p.k = k;
     p.pairs = TiledDims::of(16u, k).pairs;
     p.tiles_n = tn;
+    p.ksplit = 1u;
+    p.pairs_per_split = p.pairs;
+    p.n_total = n_total;
+    p.partial = nullptr;
     return p;
 }
 
@@ -631,6 +694,45 @@ uint32_t choose_mt(const GemmParams& p) {
     return big_tiles >= 2ull * device_compute_units() ? 16u : 8u;
 }
 
+// Split k for the pair-step kernel: when its grid has at most one workgroup per CU (two
+// fit), each output tile is shared by up to 4 workgroups of at least 8 pairs each; the
+// fp32 partials go to a stream-ordered workspace and are summed in order. Measured at
+// m = 512: down 191 -> 88 us (4 splits), o 55 -> 42, k 51 -> 35; no gain once the grid
+// holds ~2 workgroups per CU (o and down at m = 2048 get slower).
+uint32_t choose_ksplit(const GemmParams& p) {
+    const uint64_t cus = device_compute_units();
+    const uint64_t tiles = static_cast<uint64_t>((p.m + 127u) / 128u) * p.tiles_n;
+    if (tiles > cus) return 1u;
+    uint32_t s = static_cast<uint32_t>(std::min<uint64_t>(4u, (2u * cus + tiles - 1u) / tiles));
+    while (s > 1u && p.pairs / s < 8u) --s;
+    return s;
+}
+
+void launch_split(GemmParams& p, uint32_t ksplit, hipStream_t stream) {
+    p.ksplit = ksplit;
+    p.pairs_per_split = (p.pairs + ksplit - 1u) / ksplit;
+    p.ksplit = (p.pairs + p.pairs_per_split - 1u) / p.pairs_per_split;   // no empty split
+    if (p.ksplit == 1u) {
+        launch_params(p, 8u, stream);
+        return;
+    }
+    const uint64_t elems = static_cast<uint64_t>(p.m) * p.n_total;
+    void* ws = nullptr;
+    HYP_HIP_CHECK(hipMallocAsync(&ws, elems * p.ksplit * sizeof(float), stream));
+    p.partial = static_cast<float*>(ws);
+    try {
+        launch_params(p, 8u, stream);
+        const uint64_t blocks = (elems + kThreads - 1u) / kThreads;
+        HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
+        hipLaunchKernelGGL(q4_splitk_reduce_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, p);
+        HYP_HIP_CHECK(hipGetLastError());
+    } catch (...) {
+        (void)hipFreeAsync(ws, stream);
+        throw;
+    }
+    HYP_HIP_CHECK(hipFreeAsync(ws, stream));
+}
+
 }  // namespace
 
 void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
@@ -645,7 +747,21 @@ void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uin
 void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
                           uint32_t m, hipStream_t stream) {
     GemmParams p = group_params(ws, ys, count, x, m);
-    launch_params(p, choose_mt(p), stream);
+    const uint32_t mt = choose_mt(p);
+    if (mt == 8u) {
+        launch_split(p, choose_ksplit(p), stream);
+    } else {
+        launch_params(p, mt, stream);
+    }
+}
+
+void launch_q4_gemm_split(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t ksplit,
+                          hipStream_t stream) {
+    HYP_REQUIRE(ksplit >= 1u, HYP_STATUS_INTERNAL, "gemm: bad split count");
+    const Q4Matrix* ws[1] = {&w};
+    uint16_t* ys[1] = {y};
+    GemmParams p = group_params(ws, ys, 1u, x, m);
+    launch_split(p, std::min(ksplit, p.pairs), stream);
 }
 
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {

@@ -330,6 +330,31 @@ def test_gemm_exact_integer_and_ragged_tiles(stream):
         np.testing.assert_array_equal(y, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"{m}x{n}x{k}")
 
 
+def test_gemm_split_k_grouped_and_exact(stream):
+    """Grids of at most one workgroup per CU split k (fp32 partials summed in order): a
+    grouped call (n = 40, 24, 1000: the reduction maps workspace columns back to three
+    outputs) with an odd group count (k = 4160), against the fp64 product with the
+    kernel's bf16 weights; and exact integer inputs (300 x 200 x 4096, 4 splits of 8
+    pairs), bit-exact."""
+    m, k = 200, 4160
+    ws = [syn.q4_weights(n, k, seed=1400 + n) for n in (40, 24, 1000)]
+    x = syn.activations(m, k, seed=1410)
+    say(f"split-k group m={m} k={k}")
+    ys = run_group(ws, x, stream)
+    for (w, s, b), y in zip(ws, ys):
+        assert_within_bf16_rounding(y, O.qmatmul_deq_f64(x, w, s, b, mode=1), f"n={w.shape[0]}")
+    rng = np.random.default_rng(14)
+    m, n, k = 300, 200, 4096
+    say(f"split-k exact m={m} n={n} k={k}")
+    xi = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+    codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+    s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+    b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+    exact = (xi.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
+    y2 = run_qmatmul(syn.pack_codes(codes), s2, b2, syn.bf16_bits(xi), stream)
+    np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)))
+
+
 @pytest.mark.parametrize("n,k", [(8200, 192), (8195, 320), (8200, 3840)])
 def test_gemm_group_step_tiles(stream, n, k):
     """Grids of >= 2 workgroups per CU select the 256 x 128 group-step kernel: ragged m
