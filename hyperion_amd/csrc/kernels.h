@@ -40,8 +40,8 @@ constexpr uint32_t kSkinnyMaxGroup = 3;
 
 // Skinny quantized matmul on MFMA (m <= kSkinnyMaxM) over the tiled layout:
 // y[m, n] = x[m, k] . dequant(W)^T. With `up` non-null it is the fused gate/up:
-// y = gelu_chain(x.G^T) * (x.U^T). `splits` waves share each 16-row tile (1, 2, 4;
-// 8 or 16 for the plain form; 0 chooses); ceil(k / 128) >= splits.
+// y = gelu_chain(x.G^T) * (x.U^T). `splits` waves share each 16-row tile (1, 2, 4, 8
+// or 16; 1, 2 or 4 with the softcap epilogue; 0 chooses); ceil(k / 128) >= splits.
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream);
 // One launch over `count` projections that share x (and k), e.g. q, k and v:
@@ -49,9 +49,14 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
 // rms-normalised (q4_rmsnorm.h; the same bits as launch_rms_normalize) in LDS.
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
                             uint32_t m, const float* rms_eps, hipStream_t stream);
-// Splits for `tiles` 16-row tiles, `pairs` group pairs and m rows (wide: the plain form,
-// which allows 8 and 16), and whether (m, k) fits the kernel's LDS staging.
-uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, bool wide);
+// Splits for `tiles` 16-row tiles, `pairs` group pairs and m rows of one launch form,
+// and whether (m, k) fits the kernel's LDS staging.
+enum class SkinnyForm : int {
+    kPlain = 0,   // one projection or a q/k/v group (optionally normalising)
+    kDual = 1,    // the fused gate/up
+    kHead = 2,    // the softcap LM head
+};
+uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, SkinnyForm form);
 bool skinny_supported(uint32_t m, uint32_t k, bool dual);
 bool skinny_norm_supported(uint32_t m, uint32_t k);
 

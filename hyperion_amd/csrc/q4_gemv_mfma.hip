@@ -28,10 +28,16 @@
 //    Every partial product is exact in fp32 and accumulation is fp32. The two groups
 //    of a pair are independent accumulator chains, so the matrix core and the VALU
 //    overlap.
-//  * A wave owns 16 rows and every S-th pair of groups (S waves of a workgroup share
-//    the rows and meet in LDS at the end). Loads go through buffer resources: the
-//    lane's offset is a VGPR, the pair offset a scalar, so addressing costs no VALU.
-//    x is requested first (loads retire in order), then two batches of weights.
+//  * A wave owns 16 rows and a contiguous range of pairs of groups (S waves of a
+//    workgroup share the rows and meet in LDS at the end). Loads go through buffer
+//    resources with the non-temporal policy (the weights are streamed once): the lane's
+//    offset is a VGPR, the pair offset a scalar, so addressing costs no VALU.
+//  * A compute unit accepts new loads only as fast as earlier ones return, so the order
+//    of issue decides what arrives first. x is requested first by the waves that stage
+//    it, a raw barrier (no memory wait) puts every weight load of the workgroup behind
+//    those requests, and then each wave issues its weights (all of them when they fit in
+//    two register batches). The staging waves publish x through an LDS counter that the
+//    others poll, so no wave waits for another wave's loads to be issued.
 #include "common.h"
 #include "kernels.h"
 #include "q4_layout.h"
@@ -45,6 +51,9 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kMaxSegments = 3;   // projections sharing x in one grouped launch
+constexpr int kSkinnyWaves = 16;        // waves per workgroup (the softcap head uses 4)
+constexpr uint32_t kSkinnyPairsUpFront = 8;   // two batches of 4 pairs: a wave's whole range at once
+constexpr int kSkinnyDualWaves = 8;     // the fused gate/up: two accumulator sets per wave
 
 constexpr uint32_t kNibbleMask = 0x000F000Fu;
 constexpr uint32_t kMagic128 = 0x43004300u;   // bf16 pair (128.0, 128.0)
@@ -88,16 +97,18 @@ struct SkinnySegment {
     uint32_t tile_begin;
 };
 
+// The fields every launch reads before its first load come first (one 64-byte line).
 struct SkinnyParams {
-    SkinnySegment seg[kMaxSegments];   // segments past nseg are unused
-    const uint4* codes2;               // fused gate/up: the up projection (same n, k as seg[0])
-    const uint2* sb2;
     const uint16_t* x;
     uint32_t nseg;
     uint32_t k;
     uint32_t pairs;       // ceil(k / 128)
     uint32_t splits;      // waves sharing one 16-row tile (divides the workgroup's waves)
+    uint32_t split_shift; // log2(splits): splits is a power of two
     float cap;            // bf16 softcap constant
+    SkinnySegment seg[kMaxSegments];   // segments past nseg are unused
+    const uint4* codes2;               // fused gate/up: the up projection (same n, k as seg[0])
+    const uint2* sb2;
     float eps;            // NORM: rms normalisation epsilon
 };
 
@@ -116,17 +127,47 @@ struct Batch {
     uint2 sb[P];   // (scale | bias << 16) of the pair's two groups
 };
 
-// Pairs first, first + stride, ... (wave-uniform, so the clamp is a scalar op);
-// indices past `last` are clamped to it, so every byte read lies inside the tile.
+// Cache policy of the weight loads: non-temporal (each byte is read once per launch).
+constexpr int kStreamPolicy = 2;
+
+// Pairs first, first + 1, ... (wave-uniform, so the clamp is a scalar op); indices past
+// `last` are clamped to it, so every byte read lies inside the tile.
 template <int P>
-__device__ __forceinline__ void load_batch(const LaneMatrix& lm, uint32_t first, uint32_t stride, uint32_t last,
-                                           Batch<P>& bt) {
+__device__ __forceinline__ void load_batch(const LaneMatrix& lm, uint32_t first, uint32_t last, Batch<P>& bt) {
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-        const uint32_t gp = min(first + i * stride, last);
-        bt.w[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(lm.codes, lm.c_off, gp * 1024u, 0));
-        bt.sb[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(lm.sb, lm.sb_off, gp * 128u, 0));
+        const uint32_t gp = min(first + i, last);
+        bt.w[i] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(lm.codes, lm.c_off, gp * 1024u, kStreamPolicy));
+        bt.sb[i] = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(lm.sb, lm.sb_off, gp * 128u, kStreamPolicy));
     }
+}
+
+// The row of staging unit u (units are row-major, G per row), without a division.
+template <int M>
+__device__ __forceinline__ uint32_t unit_row(uint32_t u, uint32_t G) {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int r = 1; r < M; ++r) m += u >= static_cast<uint32_t>(r) * G ? 1u : 0u;
+    return m;
+}
+
+// Spin (bounded) until the LDS counter reaches `target`. The waves that raise it are in
+// the same workgroup and never wait on the polling waves, so the bound is never reached
+// in a correct launch; it only guarantees that every wave terminates.
+__device__ __forceinline__ void wait_counter(const uint32_t* ctr, uint32_t target) {
+    for (uint32_t spin = 0; spin < (1u << 24); ++spin) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// This wave's LDS writes become visible, then the counter is raised once.
+__device__ __forceinline__ void raise_counter(uint32_t* ctr, uint32_t lane) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0u) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // y += s * (acc - 128 * sum(x)) + b * sum(x) for one group (acc[m] is D[i = m][j] on
@@ -173,14 +214,14 @@ __device__ __forceinline__ void load_operands(const Batch<P> (&bt)[NW], int i, c
 // converted and read from LDS while they run, then pair i is scaled.
 template <int M, int NW, int P>
 __device__ __forceinline__ void compute_batch(const Batch<P> (&bt)[NW], uint32_t base, uint32_t cnt,
-                                              uint32_t split, uint32_t S, uint32_t G, const uint4* xa,
-                                              const float4* sx, uint32_t mask, uint32_t bits, float (&y)[NW][M]) {
+                                              uint32_t first, uint32_t G, const uint4* xa, const float4* sx,
+                                              uint32_t mask, uint32_t bits, float (&y)[NW][M]) {
     PairOperands<NW> op;
-    load_operands<NW, P>(bt, 0, xa, 2u * (split + base * S), G, mask, bits, op);
+    load_operands<NW, P>(bt, 0, xa, 2u * (first + base), G, mask, bits, op);
 #pragma unroll
     for (int i = 0; i < P; ++i) {
         if (base + i >= cnt) break;   // wave-uniform
-        const uint32_t gp = split + (base + i) * S;
+        const uint32_t gp = first + base + i;
         const uint32_t g0 = 2u * gp;
         const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
         f32x4_t acc0[NW], acc1[NW];
@@ -201,7 +242,7 @@ __device__ __forceinline__ void compute_batch(const Batch<P> (&bt)[NW], uint32_t
         uint2 sbw[NW];
 #pragma unroll
         for (int q = 0; q < NW; ++q) sbw[q] = bt[q].sb[i];
-        if (i + 1 < P && base + i + 1 < cnt) load_operands<NW, P>(bt, i + 1, xa, 2u * (gp + S), G, mask, bits, op);
+        if (i + 1 < P && base + i + 1 < cnt) load_operands<NW, P>(bt, i + 1, xa, 2u * (gp + 1u), G, mask, bits, op);
         const float4 sx0 = sx[g0];
 #pragma unroll
         for (int q = 0; q < NW; ++q) group_scale<M>(acc0[q], sbw[q].x, sx0, y[q]);
@@ -213,9 +254,47 @@ __device__ __forceinline__ void compute_batch(const Batch<P> (&bt)[NW], uint32_t
     }
 }
 
+// One pair of groups, in order: its B fragments, A fragments from LDS, four MFMAs per
+// matrix, then the two groups' scales. Used where the whole range is in flight, so each
+// pair waits only for its own loads.
+template <int M, int NW>
+__device__ __forceinline__ void compute_pair(const uint4 (&w)[NW], const uint2 (&sbw)[NW], uint32_t gp, uint32_t G,
+                                             const uint4* xa, const float4* sx, uint32_t mask, uint32_t bits,
+                                             float (&y)[NW][M]) {
+    const uint32_t g0 = 2u * gp;
+    const uint32_t g1 = min(g0 + 1u, G - 1u);   // an odd group count leaves the last pair half empty
+    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, xa[g0 * 8u]);
+    const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, xa[g0 * 8u + 1u]);
+    const bf16x8_t a2 = __builtin_bit_cast(bf16x8_t, xa[g1 * 8u]);
+    const bf16x8_t a3 = __builtin_bit_cast(bf16x8_t, xa[g1 * 8u + 1u]);
+    f32x4_t acc0[NW], acc1[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+        acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, code_frag(w[q].x, mask, bits), zero, 0, 0, 0);
+        acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, code_frag(w[q].z, mask, bits), zero, 0, 0, 0);
+        acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, code_frag(w[q].y, mask, bits), acc0[q], 0, 0, 0);
+        acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, code_frag(w[q].w, mask, bits), acc1[q], 0, 0, 0);
+    }
+    const float4 sx0 = sx[g0];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) group_scale<M>(acc0[q], sbw[q].x, sx0, y[q]);
+    if (g0 + 1u < G) {
+        const float4 sx1 = sx[g0 + 1u];
+#pragma unroll
+        for (int q = 0; q < NW; ++q) group_scale<M>(acc1[q], sbw[q].y, sx1, y[q]);
+    }
+}
+
 // NORM: x rows are first rms-normalised (q4_rmsnorm.h) in LDS; the matmul then runs on
 // the normalised rows, which are not written back.
-template <int M, bool DUAL, int EPI, int P, int NWAVE, bool NORM>
+//
+// Staging: thread u < M * G owns the 64-element unit (row u / G, group u % G) while
+// M * G <= threads; the staging waves are the waves holding units (at least M of them
+// with NORM, which forms one row's inverse rms per wave). LDS counters: ctr[0] counts
+// staging waves done with x, ctr[1] staging waves done with the NORM partials.
+// LOOP: a wave's range may exceed two batches (refilled in a loop); otherwise it fits.
+template <int M, bool DUAL, int EPI, int P, int NWAVE, bool NORM, bool LOOP>
 __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     constexpr int NW = DUAL ? 2 : 1;
     constexpr uint32_t kThreads = 64u * NWAVE;
@@ -227,42 +306,72 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     uint4* xs = smem;                                              // [M][W] permuted x
     float4* sx = reinterpret_cast<float4*>(smem + M * W);          // [G] group sums of x rows 0..3
     float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][NW][M][16]
-    float* part = red + NWAVE * NW * M * kTileRows;                // NORM: [M][G] unit partials, [M] inverses
+    uint32_t* ctr = reinterpret_cast<uint32_t*>(red + NWAVE * NW * M * kTileRows);   // [4]
+    float* part = reinterpret_cast<float*>(ctr + 4);               // NORM: [M][G] unit partials, [M] inverses
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Shifts, not divisions: everything up to the first weight load is on the critical path.
     const uint32_t S = p.splits;
-    const uint32_t split = wave % S;
-    const uint32_t gtile = blockIdx.x * (NWAVE / S) + wave / S;   // tile over all segments
+    const uint32_t sh = p.split_shift;
+    const uint32_t split = wave & (S - 1u);
+    const uint32_t gtile = (blockIdx.x << (__builtin_ctz(NWAVE) - sh)) + (wave >> sh);   // tile over all segments
     const uint32_t j = lane & 15u;
     const uint32_t kb = lane >> 4;
     const uint32_t pairs = p.pairs;
 
-    // This wave's segment (wave-uniform selects, no indexed parameter access).
-    const bool in1 = p.nseg > 1u && gtile >= p.seg[1].tile_begin;
-    const bool in2 = p.nseg > 2u && gtile >= p.seg[2].tile_begin;
-    const uint4* seg_codes = in2 ? p.seg[2].codes : (in1 ? p.seg[1].codes : p.seg[0].codes);
-    const uint2* seg_sb = in2 ? p.seg[2].sb : (in1 ? p.seg[1].sb : p.seg[0].sb);
-    uint16_t* seg_y = in2 ? p.seg[2].y : (in1 ? p.seg[1].y : p.seg[0].y);
-    const uint32_t seg_n = in2 ? p.seg[2].n : (in1 ? p.seg[1].n : p.seg[0].n);
-    const uint32_t tile = gtile - (in2 ? p.seg[2].tile_begin : (in1 ? p.seg[1].tile_begin : 0u));
+    // This wave's segment (a wave-uniform branch, no indexed parameter access; a single
+    // projection reads only segment 0).
+    const uint4* seg_codes = p.seg[0].codes;
+    const uint2* seg_sb = p.seg[0].sb;
+    uint16_t* seg_y = p.seg[0].y;
+    uint32_t seg_n = p.seg[0].n;
+    uint32_t tile = gtile;
+    if (p.nseg > 1u) {
+        const bool in1 = gtile >= p.seg[1].tile_begin;
+        const bool in2 = p.nseg > 2u && gtile >= p.seg[2].tile_begin;
+        if (in2) {
+            seg_codes = p.seg[2].codes;
+            seg_sb = p.seg[2].sb;
+            seg_y = p.seg[2].y;
+            seg_n = p.seg[2].n;
+            tile = gtile - p.seg[2].tile_begin;
+        } else if (in1) {
+            seg_codes = p.seg[1].codes;
+            seg_sb = p.seg[1].sb;
+            seg_y = p.seg[1].y;
+            seg_n = p.seg[1].n;
+            tile = gtile - p.seg[1].tile_begin;
+        }
+    }
     const uint32_t tiles = (seg_n + kTileRows - 1u) / kTileRows;
     const uint32_t ltile = min(tile, tiles - 1u);   // tiles past the matrix are loaded, never stored
 
-    // This wave's pairs: split, split + S, ... (cnt of them; cnt >= 1 since pairs >= S).
-    const uint32_t cnt = (pairs - split + S - 1u) / S;
-    const uint32_t last = pairs - 1u;
+    // This wave's pairs: [first, first + cnt), the S ranges as equal as possible
+    // (cnt >= 1 since pairs >= S).
+    const uint32_t per = pairs >> sh;
+    const uint32_t rem = pairs & (S - 1u);
+    const uint32_t first = split * per + min(split, rem);
+    const uint32_t cnt = per + (split < rem ? 1u : 0u);
+    const uint32_t last = first + cnt - 1u;
 
-    // x first: the staging below waits only for these loads.
+    const uint32_t units = M * G;
+    const uint32_t nstage = max((min(units, kThreads) + 63u) / 64u, NORM ? static_cast<uint32_t>(M) : 1u);
+    const bool stager = wave < nstage;
+
+    // x first: thread u's unit is requested before any weight load of the workgroup.
     const uint32_t xu0 = threadIdx.x;   // first (row, group) unit this thread stages
     uint4 xv[8];
-    if (xu0 < M * G) {
-        const uint32_t m = xu0 / G;
+    if (xu0 < units) {
+        const uint32_t m = unit_row<M>(xu0, G);
         const uint32_t g = xu0 - m * G;
         const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
 #pragma unroll
         for (int t = 0; t < 8; ++t) xv[t] = src[t];
     }
+    if (threadIdx.x < 4u) ctr[threadIdx.x] = 0u;
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
+    __builtin_amdgcn_s_barrier();         // no memory wait: only orders the issue
 
     const uint32_t c_bytes = tiles * pairs * 1024u;
     const uint32_t s_bytes = tiles * pairs * 128u;
@@ -278,58 +387,63 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     // Two batches of weights in flight before the first arithmetic.
     Batch<P> ba[NW], bb[NW];
 #pragma unroll
-    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split, S, last, ba[q]);
+    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], first, last, ba[q]);
 #pragma unroll
-    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + P * S, S, last, bb[q]);
+    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], first + P, last, bb[q]);
 
-    if constexpr (NORM) {
-        // Per-unit sums of squares, then one wave per row forms its inverse rms.
-        for (uint32_t u = xu0; u < M * G; u += kThreads) {
-            if (u != xu0) {
-                const uint32_t m = u / G;
-                const uint32_t g = u - m * G;
+    if (stager) {
+        if constexpr (NORM) {
+            // Per-unit sums of squares, then one wave per row forms its inverse rms.
+            for (uint32_t u = xu0; u < units; u += kThreads) {
+                if (u != xu0) {
+                    const uint32_t m = unit_row<M>(u, G);
+                    const uint32_t g = u - m * G;
+                    const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xv[t] = src[t];
+                }
+                part[u] = unit_sumsq(xv);
+            }
+            raise_counter(ctr + 1, lane);
+            wait_counter(ctr + 1, nstage);
+            if (wave < static_cast<uint32_t>(M)) {
+                const float ss = row_sumsq(part + wave * G, G, lane);
+                if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+            }
+            raise_counter(ctr + 2, lane);
+            wait_counter(ctr + 2, nstage);
+        }
+
+        // Stage x: each thread permutes whole groups (8 words) and sums them.
+        for (uint32_t u = xu0; u < units; u += kThreads) {
+            const uint32_t m = unit_row<M>(u, G);
+            const uint32_t g = u - m * G;
+            if (u != xu0 || (NORM && units > kThreads)) {
                 const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
 #pragma unroll
                 for (int t = 0; t < 8; ++t) xv[t] = src[t];
             }
-            part[u] = unit_sumsq(xv);
-        }
-        __syncthreads();
-        if (wave < static_cast<uint32_t>(M)) {
-            const float ss = row_sumsq(part + wave * G, G, lane);
-            if (lane == 0u) part[M * G + wave] = rms_inverse(ss, k, p.eps);
-        }
-        __syncthreads();
-    }
-
-    // Stage x: each thread permutes whole groups (8 words) and sums them.
-    for (uint32_t u = xu0; u < M * G; u += kThreads) {
-        const uint32_t m = u / G;
-        const uint32_t g = u - m * G;
-        if (u != xu0 || (NORM && M * G > kThreads)) {
-            const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+            if constexpr (NORM) normalize_unit(xv, part[units + m]);
+            float s0 = 0.0f;
+            float s1 = 0.0f;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) xv[t] = src[t];
+            for (int t = 0; t < 8; ++t) {
+                uint4 o;
+                o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
+                o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
+                o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
+                o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
+                xs[m * W + g * 8u + t] = o;
+                s0 = dot2_bf16(xv[t].x, kOnePair, s0);
+                s1 = dot2_bf16(xv[t].y, kOnePair, s1);
+                s0 = dot2_bf16(xv[t].z, kOnePair, s0);
+                s1 = dot2_bf16(xv[t].w, kOnePair, s1);
+            }
+            reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
         }
-        if constexpr (NORM) normalize_unit(xv, part[M * G + m]);
-        float s0 = 0.0f;
-        float s1 = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            uint4 o;
-            o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
-            o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
-            o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
-            o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
-            xs[m * W + g * 8u + t] = o;
-            s0 = dot2_bf16(xv[t].x, kOnePair, s0);
-            s1 = dot2_bf16(xv[t].y, kOnePair, s1);
-            s0 = dot2_bf16(xv[t].z, kOnePair, s0);
-            s1 = dot2_bf16(xv[t].w, kOnePair, s1);
-        }
-        reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
+        raise_counter(ctr, lane);
     }
-    __syncthreads();
+    wait_counter(ctr, nstage);
 
     // Opaque VGPR values, so (w & mask) | bits selects v_and_or_b32 (see and_or).
     uint32_t mask = kNibbleMask;
@@ -345,19 +459,36 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
         for (int m = 0; m < M; ++m) y[q][m] = 0.0f;
 
+    if constexpr (!LOOP) {
+        // The whole range is in flight (cnt <= 2P): straight-line code, so each pair waits
+        // only for its own loads (a loop waits for the loads of every iteration).
+#pragma unroll
+        for (int i = 0; i < 2 * P; ++i) {
+            if (static_cast<uint32_t>(i) >= cnt) break;   // wave-uniform
+            uint4 w[NW];
+            uint2 sbw[NW];
+#pragma unroll
+            for (int q = 0; q < NW; ++q) {
+                w[q] = i < P ? ba[q].w[i % P] : bb[q].w[i % P];
+                sbw[q] = i < P ? ba[q].sb[i % P] : bb[q].sb[i % P];
+            }
+            compute_pair<M, NW>(w, sbw, first + i, G, xa, sx, mask, bits, y);
+        }
+    } else {
     // Ping-pong over two register batches: compute one, refill it two batches ahead.
     for (uint32_t base = 0; base < cnt; base += 2 * P) {
-        compute_batch<M, NW, P>(ba, base, cnt, split, S, G, xa, sx, mask, bits, y);
+        compute_batch<M, NW, P>(ba, base, cnt, first, G, xa, sx, mask, bits, y);
         if (base + 2 * P < cnt) {
 #pragma unroll
-            for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + (base + 2 * P) * S, S, last, ba[q]);
+            for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], first + base + 2 * P, last, ba[q]);
         }
         if (base + P >= cnt) break;
-        compute_batch<M, NW, P>(bb, base + P, cnt, split, S, G, xa, sx, mask, bits, y);
+        compute_batch<M, NW, P>(bb, base + P, cnt, first, G, xa, sx, mask, bits, y);
         if (base + 3 * P < cnt) {
 #pragma unroll
-            for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], split + (base + 3 * P) * S, S, last, bb[q]);
+            for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], first + base + 3 * P, last, bb[q]);
         }
+    }
     }
 
     if (S > 1u) {
@@ -400,7 +531,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool norm = false) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    return m * W * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u +
+    return m * W * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u + 16u +
            (norm ? (m * G + m) * 4u : 0u);
 }
 
@@ -408,8 +539,13 @@ size_t max_lds_per_block();
 
 template <int M, bool DUAL, int EPI, int NWAVE, bool NORM = false>
 void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t stream) {
-    constexpr int P = 2;   // pairs per register batch (two batches in flight)
-    auto kernel = q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM>;
+    // Pairs per register batch (two batches in flight): 4, so that a wave's whole range
+    // (at most kSkinnyPairsUpFront pairs) is requested at once; 2 for the fused gate/up,
+    // which holds two matrices' batches, and for the softcap head, whose waves loop.
+    constexpr int P = (DUAL || EPI != 0) ? 2 : 4;
+    const uint32_t per_wave = (p.pairs + p.splits - 1u) / p.splits;
+    auto kernel = per_wave <= 2u * P ? q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false>
+                                     : q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true>;
     const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM);
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "skinny: x staging exceeds the device's LDS");
     if (lds > 65536u) {
@@ -417,9 +553,11 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
         int dev = 0;
         HYP_HIP_CHECK(hipGetDevice(&dev));
         if (configured_device != dev) {
-            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              static_cast<int>(max_lds_per_block())));
+            for (const void* f : {reinterpret_cast<const void*>(q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false>),
+                                  reinterpret_cast<const void*>(q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true>)}) {
+                HYP_HIP_CHECK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  static_cast<int>(max_lds_per_block())));
+            }
             configured_device = dev;
         }
     }
@@ -428,33 +566,24 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
     hipLaunchKernelGGL(kernel, grid, dim3(64 * NWAVE), lds, stream, p);
 }
 
-// Workgroups of max(4, splits) waves. The fused gate/up keeps at most 8 and the softcap
-// head 4 (their projections are wide, and the gate/up kernel holds two accumulator sets).
+// Workgroups of 16 waves (16 / splits row tiles each), so that one workgroup per compute
+// unit stages x once; the fused gate/up uses 8 (its registers) unless 16 waves share a
+// tile, and the softcap head, whose grid is many workgroups per compute unit, 4.
 template <int M>
 void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, bool norm,
                      hipStream_t stream) {
     if (dual) {
-        if (p.splits == 8u) {
-            launch_skinny_t<M, true, 0, 8>(p, tiles_total, stream);
+        if (p.splits > static_cast<uint32_t>(kSkinnyDualWaves)) {
+            launch_skinny_t<M, true, 0, kSkinnyWaves>(p, tiles_total, stream);
         } else {
-            launch_skinny_t<M, true, 0, 4>(p, tiles_total, stream);
+            launch_skinny_t<M, true, 0, kSkinnyDualWaves>(p, tiles_total, stream);
         }
     } else if (epi == Epilogue::kSoftcap) {
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
     } else if (norm) {
-        if (p.splits == 16u) {
-            launch_skinny_t<M, false, 0, 16, true>(p, tiles_total, stream);
-        } else if (p.splits == 8u) {
-            launch_skinny_t<M, false, 0, 8, true>(p, tiles_total, stream);
-        } else {
-            launch_skinny_t<M, false, 0, 4, true>(p, tiles_total, stream);
-        }
-    } else if (p.splits == 16u) {
-        launch_skinny_t<M, false, 0, 16>(p, tiles_total, stream);
-    } else if (p.splits == 8u) {
-        launch_skinny_t<M, false, 0, 8>(p, tiles_total, stream);
+        launch_skinny_t<M, false, 0, kSkinnyWaves, true>(p, tiles_total, stream);
     } else {
-        launch_skinny_t<M, false, 0, 4>(p, tiles_total, stream);
+        launch_skinny_t<M, false, 0, kSkinnyWaves>(p, tiles_total, stream);
     }
 }
 
@@ -486,21 +615,30 @@ size_t max_lds_per_block() {
 
 }  // namespace
 
-uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, bool wide) {
-    // Measured on the decode shapes of a 12B layer (MI355X, cold weights):
-    //  * very wide problems (the 262144-row LM head), and wide ones (the 960-tile
-    //    15360 x 3840 projections) at m = 4: 2 waves per tile;
-    //  * otherwise 4, and for projections with few row tiles (o, k, v, grouped q/k/v)
-    //    8 while the grid stays within 16 waves per CU; 16 only when every wave still
-    //    gets at least four group pairs (down, k = 15360).
-    // The fused gate/up uses the same rule without the 8/16 branch, so it accumulates in
-    // the same order as two separate launches. Never more splits than group pairs.
+uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, SkinnyForm form) {
+    // Measured on the decode shapes of a 12B layer (MI355X, cold weights, every split):
+    //  * plain and grouped launches (16-wave workgroups, S waves share a 16-row tile): the
+    //    smallest power of two that leaves every wave at most kSkinnyPairsUpFront pairs
+    //    (all its loads issued at once), doubled while the grid is short of one workgroup
+    //    per compute unit, up to 16: [15360,3840] 4; q/k/v grouped 8; o, q, k, down 16;
+    //  * the softcap head (262144 rows, 4-wave workgroups, many per compute unit): 1
+    //    (95 vs 100 us at m = 1, 111 vs 123 us at m = 4 with 2);
+    //  * the fused gate/up (two matrices, 2-pair batches): at m = 1 the smallest split that
+    //    keeps every wave's range in its two batches ([15360,3840]: 8, 14.5 us against
+    //    16.8 us at 4); at m >= 2, 2 (17.7 us against 24.2 us at 4 for m = 4).
     const uint32_t cus = device_compute_units();
-    uint32_t s = 4u;
-    if (tiles * 4u > cus * 32u || (m >= 4u && tiles * 4u > cus * 8u)) {
-        s = 2u;
-    } else if (wide) {
-        while (s < 16u && tiles * s * 2u <= cus * 16u && pairs >= (s < 8u ? 4u : 8u) * s) s *= 2u;
+    uint32_t s = 1u;
+    if (form == SkinnyForm::kHead) {
+        s = 1u;
+    } else if (form == SkinnyForm::kDual) {
+        if (m == 1u) {
+            while (s < 16u && pairs > s * (kSkinnyPairsUpFront / 2u)) s *= 2u;
+        } else {
+            s = 2u;
+        }
+    } else {
+        while (s < 16u && pairs > s * kSkinnyPairsUpFront) s *= 2u;
+        while (s < 16u && tiles * s < static_cast<uint32_t>(kSkinnyWaves) * cus * 9u / 10u && pairs >= 2u * s) s *= 2u;
     }
     while (s > 1u && pairs < s) s /= 2u;
     return s;
@@ -508,12 +646,12 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, bool w
 
 bool skinny_supported(uint32_t m, uint32_t k, bool dual) {
     return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
-           skinny_lds_bytes(m, k, dual, dual ? 8u : 16u) <= max_lds_per_block();
+           skinny_lds_bytes(m, k, dual, kSkinnyWaves) <= max_lds_per_block();
 }
 
 bool skinny_norm_supported(uint32_t m, uint32_t k) {
     return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
-           skinny_lds_bytes(m, k, false, 16u, true) <= max_lds_per_block();
+           skinny_lds_bytes(m, k, false, kSkinnyWaves, true) <= max_lds_per_block();
 }
 
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
@@ -525,9 +663,12 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
     HYP_REQUIRE(!dual || (up->n == w.n && up->k == w.k), HYP_STATUS_INTERNAL, "skinny: gate and up differ in shape");
     HYP_REQUIRE(skinny_supported(m, w.k, dual), HYP_STATUS_INTERNAL, "skinny: shape exceeds LDS");
     HYP_REQUIRE(d.code_bytes() < (1ull << 31), HYP_STATUS_INTERNAL, "skinny: matrix exceeds 2 GiB of packed codes");
-    if (splits == 0u) splits = choose_skinny_splits(d.tiles, d.pairs, m, !dual && epi == Epilogue::kNone);
-    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u || (epi == Epilogue::kNone && splits == 8u) ||
-                    (!dual && epi == Epilogue::kNone && splits == 16u),
+    const bool head = epi == Epilogue::kSoftcap;
+    if (splits == 0u) {
+        splits = choose_skinny_splits(d.tiles, d.pairs, m,
+                                      head ? SkinnyForm::kHead : (dual ? SkinnyForm::kDual : SkinnyForm::kPlain));
+    }
+    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u || (!head && (splits == 8u || splits == 16u)),
                 HYP_STATUS_INTERNAL, "skinny: bad split count");
     HYP_REQUIRE(d.pairs >= splits, HYP_STATUS_INTERNAL, "skinny: fewer group pairs than splits");
     SkinnyParams p{};
@@ -540,6 +681,7 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
     p.pairs = d.pairs;
     p.cap = cap_bf16;
     p.splits = splits;
+    p.split_shift = static_cast<uint32_t>(__builtin_ctz(splits));
     launch_skinny(p, d.tiles, m, dual, epi, false, stream);
 }
 
@@ -569,7 +711,8 @@ void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint
     p.pairs = TiledDims::of(16u, k).pairs;
     p.cap = 0.0f;
     p.eps = norm ? *rms_eps : 0.0f;
-    p.splits = choose_skinny_splits(tiles_total, p.pairs, m, true);
+    p.splits = choose_skinny_splits(tiles_total, p.pairs, m, SkinnyForm::kPlain);
+    p.split_shift = static_cast<uint32_t>(__builtin_ctz(p.splits));
     launch_skinny(p, tiles_total, m, false, Epilogue::kNone, norm, stream);
 }
 

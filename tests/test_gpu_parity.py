@@ -383,17 +383,20 @@ def test_gemm_group_step_tiles(stream, n, k):
 
 # ---------------------------------------------------------------- fused epilogues
 
-def _assert_close_bits(got, ref, what):
+def _assert_close_bits(got, ref, what, max_ulp=1):
     d = ulp_diff(got, ref)
-    assert d.max() <= 1, what
+    assert d.max() <= max_ulp, what
     assert np.count_nonzero(d) <= max(1, d.size // 1000), what
 
 
 @pytest.mark.parametrize("m", [1, 4, 300])
 def test_gate_up_gelu_fused(stream, m):
     """The fused gate/up (m <= 4: one launch) against the oracle's bf16 GELU chain applied
-    to separate gate and up launches. At m <= 4 the fused kernel splits each tile over as
-    many waves as the separate launches do, so its bf16 gate and up values are the same."""
+    to separate gate and up launches, and against the chain applied to the fp64 truth.
+    The fused launch may split a tile's k range differently from a separate launch, so its
+    fp32 sums of gate and up are the same terms in another order: a bf16 gate or up value
+    can then round the other way (1 ulp), which the GELU chain and the product carry to at
+    most 2 ulps, in at most 0.1% of the outputs."""
     n, k = 15360, 3840
     say(f"gate/up gelu m={m}")
     x = syn.activations(m, k, seed=600 + m)
@@ -408,7 +411,15 @@ def test_gate_up_gelu_fused(stream, m):
     hy.qmatmul(gate, xd, m, g, stream)
     hy.qmatmul(up, xd, m, u, stream)
     hy.qmlp_gate_up_gelu(gate, up, xd, m, h, stream)
-    _assert_close_bits(h.to_host(stream), O.gelu_tanh_mul(g.to_host(stream), u.to_host(stream)), f"m={m}")
+    hb = h.to_host(stream)
+    _assert_close_bits(hb, O.gelu_tanh_mul(g.to_host(stream), u.to_host(stream)), f"m={m}", max_ulp=2)
+    rows = min(m, 8)
+    g64 = O.qmatmul_f64(x[:rows], gw, gs, gb) if m <= 4 else O.qmatmul_deq_f64(x[:rows], gw, gs, gb, mode=1)
+    u64 = O.qmatmul_f64(x[:rows], uw, us, ub) if m <= 4 else O.qmatmul_deq_f64(x[:rows], uw, us, ub, mode=1)
+    truth = syn.bf16_to_f32(O.gelu_tanh_mul(syn.bf16_bits(g64.astype(np.float32)), syn.bf16_bits(u64.astype(np.float32))))
+    rel = syn.sig_rel(syn.bf16_to_f32(hb[:rows]), truth)
+    say(f"  gate/up gelu m={m}: sig_rel vs the chain on the fp64 gate and up = {rel:.2e} (bound 1e-2)")
+    assert rel <= 1e-2
 
 
 @pytest.mark.parametrize("m", [1, 300])
@@ -422,7 +433,9 @@ def test_lm_head_softcap(stream, m):
     plain = run_qmatmul(w, s, b, x, stream)
     capped = run_qmatmul(w, s, b, x, stream, softcap=30.0)
     assert np.max(np.abs(syn.bf16_to_f32(plain))) > 30.0
-    _assert_close_bits(capped, O.softcap(plain, 30.0), f"m={m}")
+    # The head launch may split k differently from the plain launch (the same terms summed
+    # in another order): a pre-cap logit can round the other way, at most 2 ulps after the cap.
+    _assert_close_bits(capped, O.softcap(plain, 30.0), f"m={m}", max_ulp=2)
 
 
 # ---------------------------------------------------------------- residency (tiny artifact)
