@@ -6,8 +6,8 @@
 // dequantize = mx.dequantize(..., dtype=bfloat16) of gathered rows, the embed path
 //              (native/hyperion_mlx/src/weights_loader.cc:53-69, forward.cc:126-131).
 //
-// Both are one pass over HBM with one thread per packed word (8 codes = 16 B of bf16),
-// so a wave moves 1 KB of contiguous bf16 per instruction.
+// Both are one pass over HBM. Quantize runs one thread per group of 64 (the group's scale
+// is derived once); dequantize one thread per packed word (8 codes = 16 B of bf16).
 #include "common.h"
 #include "kernels.h"
 #include "q4_layout.h"
@@ -17,67 +17,67 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_max(float v) {
-    const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-    return fmaxf(v, o);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_min(float v) {
-    const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-    return fminf(v, o);
-}
-
-// rint((v - bias) / scale) as MLX computes it (IEEE fp32 quotient, then round half to
-// even), evaluated with the group's correctly rounded reciprocal. For |q| < 64,
-// |v*rcp - fl(v/scale)| < 2^-16, so both round to the same integer unless the
-// quotient lies within 2^-15 of a half-integer; only then is the exact division done.
-__device__ __forceinline__ float quant_code(float v, float bias, float scale, float rcp) {
-    const float d = v - bias;
-    float q = d * rcp;
-    const float fr = q - floorf(q);
-    if (fabsf(fr - 0.5f) < 3.0517578125e-05f && fabsf(q) < 64.0f) {
-        q = __fdiv_rn(d, scale);
+// rint((v - bias) / scale) for the 8 values of one packed word, as MLX computes it (IEEE
+// fp32 quotient, round half to even, clamped to 0..15), packed lowest k first. The
+// quotients are formed with the group's correctly rounded reciprocal: fl(fl(d) * fl(1/s))
+// is within 2^-23 relative, so for |q| < 64 within 2^-17, of the IEEE quotient, and both
+// round to the same integer unless a half-integer lies within 2^-17 of the approximate
+// quotient; the exact divisions are done (for all 8) when any approximate quotient lies
+// within 2^-16 of one (twice the bound). Quotients of 64 or more clamp to 15 either way.
+__device__ __forceinline__ uint32_t quant_word(const float (&v)[8], float bias, float scale, float rcp) {
+    float q[8];
+    bool near_tie = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        q[e] = (v[e] - bias) * rcp;
+        const float r = rintf(q[e]);
+        near_tie |= fabsf(q[e] - r) > 0.5f - 1.52587890625e-05f;   // 2^-16
     }
-    q = rintf(q);
-    q = fminf(fmaxf(q, 0.0f), 15.0f);   // NaN (never produced for finite input) -> 0
-    return q;
+    if (near_tie) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = __fdiv_rn(v[e] - bias, scale);
+    }
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float c = fminf(fmaxf(rintf(q[e]), 0.0f), 15.0f);   // NaN (never produced for finite input) -> 0
+        packed |= static_cast<uint32_t>(c) << (4 * e);
+    }
+    return packed;
 }
 
+// One thread per group of 64: it reads the group's 128 contiguous bytes, finds the
+// extremes, derives scale and bias once (zero-point rule, fp32, IEEE division, rint) and
+// writes 8 packed words (32 contiguous bytes) plus a bf16 scale and bias. No cross-lane
+// work and no redundant per-group arithmetic, so the vector ALU work per weight is the
+// quantization itself.
 __global__ __launch_bounds__(kThreads) void q4_quantize_kernel(const uint16_t* __restrict__ w,
                                                                uint32_t* __restrict__ wq,
                                                                uint16_t* __restrict__ scales,
                                                                uint16_t* __restrict__ biases,
-                                                               uint64_t words) {
-    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const bool live = t < words;
-    // Dead lanes of the last wave mirror word 0 so every lane feeds the DPP reductions.
-    const uint64_t src = live ? t : 0u;
-    const uint4 raw = *reinterpret_cast<const uint4*>(w + src * 8u);
-    float v[8];
-    v[0] = bf16_bits_to_f32(raw.x & 0xFFFFu);
-    v[1] = bf16_bits_to_f32(raw.x >> 16);
-    v[2] = bf16_bits_to_f32(raw.y & 0xFFFFu);
-    v[3] = bf16_bits_to_f32(raw.y >> 16);
-    v[4] = bf16_bits_to_f32(raw.z & 0xFFFFu);
-    v[5] = bf16_bits_to_f32(raw.z >> 16);
-    v[6] = bf16_bits_to_f32(raw.w & 0xFFFFu);
-    v[7] = bf16_bits_to_f32(raw.w >> 16);
+                                                               uint64_t groups) {
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (g >= groups) return;
+    // Plain loads: each lane's eight 16-byte loads share its 128-byte lines, which the
+    // non-temporal policy would not keep between them (measured 63 us against 39 us).
+    const uint4* src = reinterpret_cast<const uint4*>(w + g * 64u);
+    uint4 raw[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) raw[t] = src[t];
 
     float w_max = -INFINITY;
     float w_min = INFINITY;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        w_max = fmaxf(w_max, v[e]);
-        w_min = fminf(w_min, v[e]);
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t h[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float lo = bf16_bits_to_f32(h[e] & 0xFFFFu);
+            const float hi = __uint_as_float(h[e] & 0xFFFF0000u);
+            w_max = fmaxf(w_max, fmaxf(lo, hi));
+            w_min = fminf(w_min, fminf(lo, hi));
+        }
     }
-    // The 8 lanes of a group are lanes 8i..8i+7 of the wave.
-    w_max = dpp_max<0xB1>(w_max);
-    w_max = dpp_max<0x4E>(w_max);
-    w_max = dpp_max<0x141>(w_max);
-    w_min = dpp_min<0xB1>(w_min);
-    w_min = dpp_min<0x4E>(w_min);
-    w_min = dpp_min<0x141>(w_min);
 
     // Zero-point ("edge") rule, fp32 with IEEE division.
     const bool mask = fabsf(w_min) > fabsf(w_max);
@@ -93,18 +93,23 @@ __global__ __launch_bounds__(kThreads) void q4_quantize_kernel(const uint16_t* _
     }
     const float rcp = __fdiv_rn(1.0f, scale);
 
-    uint32_t packed = 0;
+    uint32_t packed[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        packed |= static_cast<uint32_t>(quant_code(v[e], bias, scale, rcp)) << (4 * e);
-    }
-    if (live) {
-        wq[t] = packed;
-        if ((t & 7u) == 0u) {
-            scales[t >> 3] = f32_to_bf16_bits(scale);
-            biases[t >> 3] = f32_to_bf16_bits(bias);
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t h[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = bf16_bits_to_f32(h[e] & 0xFFFFu);
+            v[2 * e + 1] = __uint_as_float(h[e] & 0xFFFF0000u);
         }
+        packed[t] = quant_word(v, bias, scale, rcp);
     }
+    uint4* dst = reinterpret_cast<uint4*>(wq + g * 8u);
+    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    scales[g] = f32_to_bf16_bits(scale);
+    biases[g] = f32_to_bf16_bits(bias);
 }
 
 // The 8 bf16 outputs of one packed word: bf16(bf16(s*q) + b), optionally times a bf16
@@ -175,11 +180,11 @@ __global__ __launch_bounds__(kThreads) void q4_dequantize_kernel(
 
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq, uint16_t* scales,
                         uint16_t* biases, hipStream_t stream) {
-    const uint64_t words = static_cast<uint64_t>(n) * (k / 8u);
-    const uint64_t blocks = (words + kThreads - 1) / kThreads;
+    const uint64_t groups = static_cast<uint64_t>(n) * (k / 64u);
+    const uint64_t blocks = (groups + kThreads - 1) / kThreads;
     HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "quantize: matrix too large");
     hipLaunchKernelGGL(q4_quantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream,
-                       w, wq, scales, biases, words);
+                       w, wq, scales, biases, groups);
     HYP_HIP_CHECK(hipGetLastError());
 }
 
