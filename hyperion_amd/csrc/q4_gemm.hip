@@ -439,16 +439,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t bid = blockIdx.x;
     const uint32_t xcd = bid & 7u;
     const uint32_t slot = bid >> 3;
-    const uint32_t per = p.tiles_total >> 3;
-    const uint32_t rem = p.tiles_total & 7u;
-    const uint32_t tile = xcd * per + min(xcd, rem) + slot;
+    const uint32_t ext_total = p.tiles_total * p.ksplit;
+    const uint32_t per = ext_total >> 3;
+    const uint32_t rem = ext_total & 7u;
+    const uint32_t ext = xcd * per + min(xcd, rem) + slot;
+    const uint32_t kz = ext / p.tiles_total;          // this workgroup's k split
+    const uint32_t tile = ext - kz * p.tiles_total;
     const uint32_t tm = tile / p.tiles_n;
     const SegView sv = segment_of(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
     const uint32_t n0 = sv.tn * (kWaves * 16u * NT);
     const uint32_t tile16_0 = n0 / 16u + wave * NT;
     const uint32_t k = p.k;
-    const uint32_t G = k / 64u;
+    // This workgroup's groups [g0, g1): whole pairs of its split (all groups without split k).
+    const uint32_t g0 = 2u * kz * p.pairs_per_split;
+    const uint32_t g1 = min(g0 + 2u * p.pairs_per_split, k / 64u);
 
     // X: load t of wave w fills LDS rows 8 (w kXLoads + t) .. +7; lane l writes physical
     // chunk l % 8 of row r = 8 (w kXLoads + t) + l / 8 with logical chunk (l % 8) ^ (l / 8).
@@ -489,20 +494,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     GRaw<NT> r0, r1, r2;
-    load_x(0u, xs);
-    load_graw<NT>(cr, sr, c_off, s_off, 0u, r0);
-    load_graw<NT>(cr, sr, c_off, s_off, min(1u, G - 1u), r1);
+    load_x(g0, xs);
+    load_graw<NT>(cr, sr, c_off, s_off, g0, r0);
+    load_graw<NT>(cr, sr, c_off, s_off, min(g0 + 1u, g1 - 1u), r1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     bf16x8_t b0[NT], b1[NT];
     gdequant<NT, 0>(r0, b0);
 
     // Branch-free loop; past the last group the loads repeat the last group (unused).
-    for (uint32_t g = 0; g < G; ++g) {
-        const uint8_t* xb = xs + (g & 1u) * kStage;
-        load_x(min(g + 1u, G - 1u), xs + ((g + 1u) & 1u) * kStage);
+    for (uint32_t g = g0; g < g1; ++g) {
+        const uint8_t* xb = xs + ((g - g0) & 1u) * kStage;
+        load_x(min(g + 1u, g1 - 1u), xs + ((g - g0 + 1u) & 1u) * kStage);
         __builtin_amdgcn_sched_barrier(0);   // the raw loads below issue after the X loads
-        load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, G - 1u), r2);
+        load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, g1 - 1u), r2);
         gdequant<NT, 1>(r0, b1);
         gmfma<MT, NT, 0>(xb, lane, b0, acc);
         gdequant<NT, 0>(r1, b0);
@@ -512,6 +517,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         // The next X stage has landed once at most this iteration's 2 NT raw loads remain.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NT) : "memory");
         __syncthreads();
+    }
+
+    if (p.ksplit > 1u) {
+        // Split k: fp32 partials, summed by q4_splitk_reduce_kernel.
+        const uint32_t j = lane & 15u;
+        const uint32_t kb = lane >> 4;
+        float* part = p.partial + static_cast<size_t>(kz) * p.m * p.n_total;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t col = n0 + (wave * NT + nt) * 16u + j;
+            if (col >= sv.n) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = m0 + mt * 16u + kb * 4u + r;
+                    if (row < p.m) part[static_cast<size_t>(row) * p.n_total + sv.col_begin + col] = acc[mt][nt][r];
+                }
+        }
+        return;
     }
 
     // Epilogue through LDS as in q4_gemm_kernel.
@@ -618,7 +643,7 @@ void launch_t(GemmParams p, hipStream_t stream) {
 
 template <int MT, int NT>
 void launch_g(GemmParams p, hipStream_t stream) {
-    HYP_REQUIRE(p.ksplit == 1u, HYP_STATUS_INTERNAL, "gemm: the group-step kernel does not split k");
+
     auto kernel = q4_gemm_g_kernel<MT, NT>;
     constexpr size_t lds = g_lds_bytes<MT, NT>();
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
@@ -634,7 +659,7 @@ void launch_g(GemmParams p, hipStream_t stream) {
     }
     const uint32_t tiles_m = (p.m + 16u * MT - 1u) / (16u * MT);
     p.tiles_total = p.tiles_n * tiles_m;
-    hipLaunchKernelGGL(kernel, dim3(p.tiles_total), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL(kernel, dim3(p.tiles_total * p.ksplit), dim3(kThreads), lds, stream, p);
 }
 
 constexpr uint32_t kTileCols = 128u;   // workgroup tile width of both kernels (NT = 2)
@@ -694,26 +719,38 @@ uint32_t choose_mt(const GemmParams& p) {
     return big_tiles >= 2ull * device_compute_units() ? 16u : 8u;
 }
 
-// Split k for the pair-step kernel: when its grid has at most one workgroup per CU (two
-// fit), each output tile is shared by up to 4 workgroups of at least 8 pairs each; the
-// fp32 partials go to a stream-ordered workspace and are summed in order. Measured at
-// m = 512: down 191 -> 88 us (4 splits), o 55 -> 42, k 51 -> 35; no gain once the grid
-// holds ~2 workgroups per CU (o and down at m = 2048 get slower).
+// Split k for the group-step kernel: a long k (at least 64 pairs) with a grid of fewer
+// than two workgroups per CU. Measured on down at m = 2048 (240 tiles of 256 x 128,
+// k = 15360): 289 us unsplit, 249 with 2 splits, 268 with 3, against 310 for the pair-step
+// kernel; o at m = 2048 (k = 4096) is faster on the pair-step kernel unsplit (82 us).
+uint32_t choose_g_ksplit(const GemmParams& p) {
+    const uint64_t cus = device_compute_units();
+    const uint64_t big_tiles = static_cast<uint64_t>((p.m + 255u) / 256u) * p.tiles_n;
+    if (p.pairs < 64u || big_tiles >= 2u * cus || (p.m + 255u) / 256u < 4u) return 1u;
+    const uint64_t s = (3u * cus + 2u * big_tiles - 1u) / (2u * big_tiles);   // ~1.5 workgroups per CU
+    return static_cast<uint32_t>(std::min<uint64_t>(4u, std::max<uint64_t>(1u, s)));
+}
+
+// Split k for the pair-step kernel: when its grid fills at most 3/4 of the CUs, each
+// output tile is shared by up to 4 workgroups of at least 8 pairs each; the fp32 partials
+// go to a stream-ordered workspace and are summed in order. Measured at m = 512: down
+// 193 -> 88 us (4 splits), o 56 -> 41; q/k/v grouped (256 tiles) 56.5 us unsplit against
+// 59.1 with 2; no gain once the grid holds ~2 workgroups per CU (o and down at m = 2048).
 uint32_t choose_ksplit(const GemmParams& p) {
     const uint64_t cus = device_compute_units();
     const uint64_t tiles = static_cast<uint64_t>((p.m + 127u) / 128u) * p.tiles_n;
-    if (tiles > cus) return 1u;
+    if (tiles * 4u > cus * 3u) return 1u;
     uint32_t s = static_cast<uint32_t>(std::min<uint64_t>(4u, (2u * cus + tiles - 1u) / tiles));
     while (s > 1u && p.pairs / s < 8u) --s;
     return s;
 }
 
-void launch_split(GemmParams& p, uint32_t ksplit, hipStream_t stream) {
+void launch_split(GemmParams& p, uint32_t mt, uint32_t ksplit, hipStream_t stream) {
     p.ksplit = ksplit;
     p.pairs_per_split = (p.pairs + ksplit - 1u) / ksplit;
     p.ksplit = (p.pairs + p.pairs_per_split - 1u) / p.pairs_per_split;   // no empty split
     if (p.ksplit == 1u) {
-        launch_params(p, 8u, stream);
+        launch_params(p, mt, stream);
         return;
     }
     const uint64_t elems = static_cast<uint64_t>(p.m) * p.n_total;
@@ -721,7 +758,7 @@ void launch_split(GemmParams& p, uint32_t ksplit, hipStream_t stream) {
     HYP_HIP_CHECK(hipMallocAsync(&ws, elems * p.ksplit * sizeof(float), stream));
     p.partial = static_cast<float*>(ws);
     try {
-        launch_params(p, 8u, stream);
+        launch_params(p, mt, stream);
         const uint64_t blocks = (elems + kThreads - 1u) / kThreads;
         HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
         hipLaunchKernelGGL(q4_splitk_reduce_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, p);
@@ -748,8 +785,11 @@ void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32
                           uint32_t m, hipStream_t stream) {
     GemmParams p = group_params(ws, ys, count, x, m);
     const uint32_t mt = choose_mt(p);
-    if (mt == 8u) {
-        launch_split(p, choose_ksplit(p), stream);
+    const uint32_t gsplit = mt == 8u ? choose_g_ksplit(p) : 1u;
+    if (gsplit > 1u) {
+        launch_split(p, 16u, gsplit, stream);
+    } else if (mt == 8u) {
+        launch_split(p, 8u, choose_ksplit(p), stream);
     } else {
         launch_params(p, mt, stream);
     }
@@ -761,7 +801,7 @@ void launch_q4_gemm_split(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint
     const Q4Matrix* ws[1] = {&w};
     uint16_t* ys[1] = {y};
     GemmParams p = group_params(ws, ys, 1u, x, m);
-    launch_split(p, std::min(ksplit, p.pairs), stream);
+    launch_split(p, 8u, std::min(ksplit, p.pairs), stream);
 }
 
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {

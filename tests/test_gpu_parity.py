@@ -381,6 +381,32 @@ def test_gemm_group_step_tiles(stream, n, k):
     np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"exact n={n} k={k}")
 
 
+def test_gemm_group_step_split_k(stream):
+    """A long k (129 groups) on a grid short of two workgroups per CU (8 x 3 tiles of
+    256 x 128) runs the group-step kernel with k split 4 ways (34-group ranges, the last
+    of 27 groups ending on a half pair): a grouped call over two segments (n = 100, 200) with ragged
+    m = 2000 against the fp64 product with the kernel's bf16 weights on sampled rows, and
+    every row exact on integer inputs."""
+    m, k = 2000, 8256
+    say(f"gemm group-step split-k m={m} k={k}")
+    ws = [syn.q4_weights(n, k, seed=1500 + n) for n in (100, 200)]
+    x = syn.activations(m, k, seed=1510)
+    ys = run_group(ws, x, stream)
+    rng = np.random.default_rng(k)
+    rows = np.sort(rng.choice(m, size=12, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    for (w, s, b), y in zip(ws, ys):
+        assert_within_bf16_rounding(y[rows], O.qmatmul_deq_f64(x[rows], w, s, b, mode=1), f"n={w.shape[0]}")
+    n = 300
+    xi = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+    codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+    s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+    b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+    exact = (xi.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
+    y2 = run_qmatmul(syn.pack_codes(codes), s2, b2, syn.bf16_bits(xi), stream)
+    np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)), err_msg="exact split-k group-step")
+
+
 # ---------------------------------------------------------------- fused epilogues
 
 def _assert_close_bits(got, ref, what, max_ulp=1):
