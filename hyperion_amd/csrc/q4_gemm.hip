@@ -27,6 +27,8 @@
 //    gets a contiguous run of tiles that share X rows, keeping the X block in that
 //    XCD's L2.
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "kernels.h"
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 //
 // The same scheme with 16 row tiles per wave (each dequantized B fragment feeds 16 MFMAs
 // instead of 8) and 64-k iterations, so two workgroups still fit a CU: X stages of
-// 256 rows x 128 bytes (chunks swizzled by row % 8), double buffered; the raw weights of
+// 256 rows x 128 bytes (chunks swizzled by (row / 2) % 8), double buffered; the raw weights of
 // a group are half of each 16-byte entry (plus its scale word), loaded two groups ahead.
 // k-step s of a group uses word 2 kb + s of the lane's entry, and the A fragments the
 // same k chunk.
@@ -402,26 +404,52 @@ __device__ __forceinline__ void gdequant(const GRaw<NT>& raw, bf16x8_t (&b)[NT])
     }
 }
 
-template <int MT, int NT, int S>
-__device__ __forceinline__ void gmfma(const uint8_t* xb, uint32_t lane, const bf16x8_t (&b)[NT],
-                                      f32x4_t (&acc)[MT][NT]) {
+// Column tile NTI's B fragment of k-step S (gdequant for one tile).
+template <int NT, int S, int NTI>
+__device__ __forceinline__ void gdequant_one(const GRaw<NT>& raw, bf16x8_t (&b)[NT]) {
+    const float sc = bf16_bits_to_f32(raw.sb[NTI] & 0xFFFFu);
+    const float bi = bf16_bits_to_f32(raw.sb[NTI] >> 16);
+    b[NTI] = dequant_word(S == 0 ? raw.c[NTI].x : raw.c[NTI].y, sc, bi);
+}
+
+// f(integral_constant<int, U>) for U in the sequence, in order.
+template <typename F, int... U>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, U...>) {
+    (f(std::integral_constant<int, U>{}), ...);
+}
+
+// A fragments of k-step S, row tiles [Q MT/P, (Q + 1) MT/P), from an X stage. Rows are
+// 128 bytes and the 16 rows one read instruction touches start alternately at bank 0 and
+// bank 32 of the 64, so chunks are swizzled by (row / 2) % 8: the 16 lanes of a cycle
+// then hit 16 distinct 4-bank runs.
+template <int MT, int P, int S, int Q>
+__device__ __forceinline__ void g_read_a(const uint8_t* xb, uint32_t lane, bf16x8_t (&a)[MT / P]) {
     const uint32_t i = lane & 15u;
     const uint32_t kb = lane >> 4;
     const uint32_t c = 2u * kb + S;   // this lane's logical k chunk of the group
-    const uint8_t* row = xb + i * kGRowBytes + ((c ^ (i & 7u)) << 4);
-    constexpr int kHalf = MT / 2;
+    const uint8_t* row = xb + i * kGRowBytes + ((c ^ ((i >> 1) & 7u)) << 4);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        bf16x8_t a[kHalf];
+    for (int mt = 0; mt < MT / P; ++mt)
+        a[mt] = *reinterpret_cast<const bf16x8_t*>(row + (Q * (MT / P) + mt) * 16u * kGRowBytes);
+}
+
+// The MFMAs of one part of a k-step (MT/P row tiles x NT column tiles), with the
+// scheduling hint: the next part's A reads (issued just before) go first, then one MFMA
+// followed by kValu VALU ops (the dequantization of the next k-step) throughout.
+template <int MT, int NT, int P, int Q, int kValu>
+__device__ __forceinline__ void g_mfma_part(const bf16x8_t (&a)[MT / P], const bf16x8_t (&b)[NT],
+                                            f32x4_t (&acc)[MT][NT], bool reads_ahead) {
+    constexpr int kRows = MT / P;
 #pragma unroll
-        for (int mt = 0; mt < kHalf; ++mt)
-            a[mt] = *reinterpret_cast<const bf16x8_t*>(row + (h * kHalf + mt) * 16u * kGRowBytes);
+    for (int mt = 0; mt < kRows; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < kHalf; ++mt)
+        for (int nt = 0; nt < NT; ++nt)
+            acc[Q * kRows + mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], b[nt], acc[Q * kRows + mt][nt], 0, 0, 0);
+    if (reads_ahead) __builtin_amdgcn_sched_group_barrier(0x100, kRows, 0);   // DS read
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-                acc[h * kHalf + mt][nt] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], b[nt], acc[h * kHalf + mt][nt], 0, 0, 0);
+    for (int t = 0; t < kRows * NT; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                 // MFMA
+        if constexpr (kValu > 0) __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);   // VALU
     }
 }
 
@@ -430,6 +458,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     constexpr uint32_t BM = 16u * MT;
     constexpr uint32_t kStage = BM * kGRowBytes;
     constexpr int kXLoads = static_cast<int>(BM / 8u / kWaves);   // 1 KB (8 rows) direct loads per wave
+    static_assert(kXLoads % 2 == 0, "swizzle period");
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];   // [2][BM][128 B], reused by the epilogue
 
     const uint32_t tid = threadIdx.x;
@@ -456,14 +485,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t g1 = min(g0 + 2u * p.pairs_per_split, k / 64u);
 
     // X: load t of wave w fills LDS rows 8 (w kXLoads + t) .. +7; lane l writes physical
-    // chunk l % 8 of row r = 8 (w kXLoads + t) + l / 8 with logical chunk (l % 8) ^ (l / 8).
+    // chunk l % 8 of row r = 8 (w kXLoads + t) + l / 8 with logical chunk
+    // (l % 8) ^ ((r / 2) % 8) = (l % 8) ^ (4 (t % 2) + l / 16) (kXLoads is even).
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.x), static_cast<short>(0), static_cast<int>(p.m * k * 2u), 0x00020000);
     uint32_t xoff[kXLoads];
 #pragma unroll
     for (int t = 0; t < kXLoads; ++t) {
         const uint32_t row = m0 + 8u * (wave * kXLoads + t) + (lane >> 3);
-        const uint32_t chunk = (lane & 7u) ^ (lane >> 3);
+        const uint32_t chunk = (lane & 7u) ^ (4u * (t & 1) + (lane >> 4));
         xoff[t] = row < p.m ? row * k * 2u + chunk * 16u : 0x80000000u;
     }
     auto load_x = [&](uint32_t g, uint8_t* buf) {
@@ -493,31 +523,65 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    GRaw<NT> r0, r1, r2;
+    GRaw<NT> r[3];
     load_x(g0, xs);
-    load_graw<NT>(cr, sr, c_off, s_off, g0, r0);
-    load_graw<NT>(cr, sr, c_off, s_off, min(g0 + 1u, g1 - 1u), r1);
+    load_graw<NT>(cr, sr, c_off, s_off, g0, r[0]);
+    load_graw<NT>(cr, sr, c_off, s_off, min(g0 + 1u, g1 - 1u), r[1]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     bf16x8_t b0[NT], b1[NT];
-    gdequant<NT, 0>(r0, b0);
+    gdequant<NT, 0>(r[0], b0);
 
-    // Branch-free loop; past the last group the loads repeat the last group (unused).
-    for (uint32_t g = g0; g < g1; ++g) {
+    // Each group runs as 2 kParts units (k-step 0 row tiles [0, MT/kParts), then the next
+    // MT/kParts, ..., then k-step 1); a unit's A fragments are read from LDS while the
+    // previous unit's MFMAs run (two register sets), and the dequantization of the next
+    // k-step (or the next group's first) is spread over a k-step's MFMAs. The raw weights
+    // of groups g, g + 1 are in r[s], r[(s + 1) % 3] and those of g + 2 load into
+    // r[(s + 2) % 3] (s = (g - g0) % 3, unrolled, so no register copies wait on loads in
+    // flight). Past the last group the loads repeat the last group (unused).
+    constexpr int kParts = 4;
+    static_assert(NT <= kParts, "one column tile's dequantization per unit");
+    constexpr int kValu = (26 + MT / kParts * NT - 1) / (MT / kParts * NT);   // one tile's dequantization per MFMA
+    bf16x8_t a[2][MT / kParts];
+    g_read_a<MT, kParts, 0, 0>(xs, lane, a[0]);
+    auto group = [&](auto slot, uint32_t g) {
+        constexpr int s = decltype(slot)::value;
         const uint8_t* xb = xs + ((g - g0) & 1u) * kStage;
         load_x(min(g + 1u, g1 - 1u), xs + ((g - g0 + 1u) & 1u) * kStage);
         __builtin_amdgcn_sched_barrier(0);   // the raw loads below issue after the X loads
-        load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, g1 - 1u), r2);
-        gdequant<NT, 1>(r0, b1);
-        gmfma<MT, NT, 0>(xb, lane, b0, acc);
-        gdequant<NT, 0>(r1, b0);
-        gmfma<MT, NT, 1>(xb, lane, b1, acc);
-        r0 = r1;
-        r1 = r2;
-        // The next X stage has landed once at most this iteration's 2 NT raw loads remain.
+        load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, g1 - 1u), r[(s + 2) % 3]);
+        static_for(
+            [&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                constexpr int q = u % kParts;
+                // Each unit is its own scheduling region: the next unit's A reads go out
+                // first, then this unit's MFMAs with one column tile's dequantization.
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (u + 1 < 2 * kParts)
+                    g_read_a<MT, kParts, (u + 1) / kParts, (u + 1) % kParts>(xb, lane, a[(u + 1) & 1]);
+                if constexpr (u < NT) gdequant_one<NT, 1, u>(r[s], b1);
+                if constexpr (u >= kParts && u < kParts + NT) gdequant_one<NT, 0, u - kParts>(r[(s + 1) % 3], b0);
+                constexpr bool deq = u < NT || (u >= kParts && u < kParts + NT);
+                if constexpr (u < kParts)
+                    g_mfma_part<MT, NT, kParts, q, deq ? kValu : 0>(a[u & 1], b0, acc, true);
+                else
+                    g_mfma_part<MT, NT, kParts, q, deq ? kValu : 0>(a[u & 1], b1, acc, u + 1 < 2 * kParts);
+            },
+            std::make_integer_sequence<int, 2 * kParts>{});
+        __builtin_amdgcn_sched_barrier(0);
+        // The next X stage has landed once at most this group's 2 NT raw loads remain.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NT) : "memory");
         __syncthreads();
+        g_read_a<MT, kParts, 0, 0>(xs + ((g - g0 + 1u) & 1u) * kStage, lane, a[0]);
+    };
+    uint32_t g = g0;
+    for (; g + 3u <= g1; g += 3u) {
+        group(std::integral_constant<int, 0>{}, g);
+        group(std::integral_constant<int, 1>{}, g + 1u);
+        group(std::integral_constant<int, 2>{}, g + 2u);
     }
+    if (g < g1) group(std::integral_constant<int, 0>{}, g);
+    if (g + 1u < g1) group(std::integral_constant<int, 1>{}, g + 1u);
 
     if (p.ksplit > 1u) {
         // Split k: fp32 partials, summed by q4_splitk_reduce_kernel.
