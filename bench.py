@@ -290,27 +290,50 @@ def bench_decode_stream(model, m, steps, warmup, stream):
     return out
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds):
-    """The oracle's restatement of MLX's CPU quantized_matmul (bf16 accumulation), on one
-    host core, over a bounded number of full decode GEMVs."""
+    """The oracle's restatement of MLX's CPU quantized_matmul (bf16 accumulation) over a
+    bounded number of full decode GEMVs: on one host core (the reference's CPU stream
+    runs one task), and with output rows over this process's share of cores (OpenMP,
+    OMP_NUM_THREADS or all cores)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     n, k = DECODE_N, DECODE_K
     w, s, b = syn.q4_weights(n, k, seed=105)
     x = syn.activations(1, k, seed=104)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        O.qmatmul_mlx_cpu(x, w, s, b)
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    gbs = reps * gemv_bytes(1, n, k) / dt / 1e9
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+    def timed(fn):
+        reps = 0
+        t0 = time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
+        return reps, dt, reps * gemv_bytes(1, n, k) / dt / 1e9
+
+    what = (f"full decode GEMVs [1,{k}]x[{n},{k}] Q4/g64 with the oracle's bf16-accumulating "
+            f"restatement of MLX's CPU quantized_matmul on {cpu_model()} (nproc {os.cpu_count()})")
+    reps, dt, gbs = timed(lambda: O.qmatmul_mlx_cpu(x, w, s, b))
     log(f"cpu baseline: {reps} GEMVs in {dt:.1f} s = {gbs:.3f} GB/s (1 core)")
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full decode GEMVs [1,{k}]x[{n},{k}] Q4/g64 in {dt:.1f} s with the oracle's "
-                      f"bf16-accumulating restatement of MLX's CPU quantized_matmul"}
+    one = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{reps} {what} in {dt:.1f} s"}
+    reps, dt, gbs = timed(lambda: O.qmatmul_mlx_cpu_mt(x, w, s, b, threads))
+    log(f"cpu baseline: {reps} GEMVs in {dt:.1f} s = {gbs:.3f} GB/s ({threads} threads)")
+    par = {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{reps} {what}, output rows over {threads} OpenMP threads, in {dt:.1f} s"}
+    return one, par
 
 
 def measured_traffic():
@@ -374,7 +397,7 @@ def main():
         streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
         extra["decode_stream"] = streams
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu, cpu_par = (None, None) if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     per = dec["ms_per_launch"]
     gbs = dec["bytes"] / per / 1e6
@@ -398,6 +421,7 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "decode_gemv_warm_gbs": round(dec["bytes"] / dec["warm_ms_per_launch"] / 1e6, 1),
         "cpu_baseline": cpu,
+        "cpu_baseline_parallel": cpu_par,
     }
     line.update(extra)
     print(json.dumps(line), flush=True)

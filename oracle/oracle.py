@@ -38,6 +38,7 @@ def lib():
         L.orc_qmatmul_f32_grouped.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P]
         L.orc_qmatmul_mlx_cpu.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P]
         L.orc_qmatmul_mlx_cpu_rows.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P]
+        L.orc_qmatmul_mlx_cpu_mt.argtypes = [_P, _P, _P, _P, _I, _I, _I, ctypes.c_int, _P]
         L.orc_gelu_tanh_bf16.argtypes = [_P, _I, _P]
         L.orc_gelu_tanh_mul_bf16.argtypes = [_P, _P, _I, _P]
         L.orc_softcap_bf16.argtypes = [_P, _I, ctypes.c_float, _P]
@@ -136,6 +137,14 @@ def qmatmul_mlx_cpu(x, wq, s, b, rows=None) -> np.ndarray:
     n0, n1 = (0, n) if rows is None else rows
     y = np.empty((m, n1 - n0), np.uint16)
     lib().orc_qmatmul_mlx_cpu_rows(_p(x), _p(wq), _p(s), _p(b), m, n0, n1, k, _p(y))
+    return y
+
+
+def qmatmul_mlx_cpu_mt(x, wq, s, b, threads) -> np.ndarray:
+    """qmatmul_mlx_cpu over `threads` OpenMP threads (bit-identical; parity unpinned)."""
+    x, wq, s, b, m, n, k = _mm_args(x, wq, s, b)
+    y = np.empty((m, n), np.uint16)
+    lib().orc_qmatmul_mlx_cpu_mt(_p(x), _p(wq), _p(s), _p(b), m, n, k, int(threads), _p(y))
     return y
 
 

@@ -243,6 +243,25 @@ void orc_qmatmul_mlx_cpu(const uint16_t* x, const uint32_t* wq, const uint16_t* 
     orc_qmatmul_mlx_cpu_rows(x, wq, scales, biases, m, 0, n, k, y);
 }
 
+/* The same loop with output rows dealt over `threads` OpenMP threads in blocks of 64
+ * (each output row is still one sequential bf16 accumulation, so the result is
+ * bit-identical to orc_qmatmul_mlx_cpu). */
+void orc_qmatmul_mlx_cpu_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                            const uint16_t* biases, int64_t m, int64_t n, int64_t k, int threads,
+                            uint16_t* y) {
+    const int64_t blocks = (n + 63) / 64;
+    if (m == 1) {
+#pragma omp parallel for schedule(static) num_threads(threads)
+        for (int64_t bl = 0; bl < blocks; ++bl) {
+            const int64_t r0 = bl * 64;
+            const int64_t r1 = r0 + 64 < n ? r0 + 64 : n;
+            orc_qmatmul_mlx_cpu_rows(x, wq, scales, biases, 1, r0, r1, k, y + r0);
+        }
+        return;
+    }
+    for (int64_t i = 0; i < m; ++i) orc_qmatmul_mlx_cpu_mt(x + i * k, wq, scales, biases, 1, n, k, threads, y + i * n);
+}
+
 /*
  * gelu_pytorch_tanh as the reference composes it (forward.cc:324-336): each MLX op
  * produces a bf16 array, constants are bf16 arrays.

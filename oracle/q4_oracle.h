@@ -89,6 +89,12 @@ void orc_qmatmul_f32_grouped(const uint16_t* x, const uint32_t* wq, const uint16
 void orc_qmatmul_mlx_cpu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                          const uint16_t* biases, int64_t m, int64_t n, int64_t k, uint16_t* y);
 
+/* orc_qmatmul_mlx_cpu with output rows spread over `threads` OpenMP threads
+ * (bit-identical result; the multi-core CPU baseline). */
+void orc_qmatmul_mlx_cpu_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                            const uint16_t* biases, int64_t m, int64_t n, int64_t k, int threads,
+                            uint16_t* y);
+
 /* Rows [n0, n1) only of orc_qmatmul_mlx_cpu (bounded CPU-baseline samples). */
 void orc_qmatmul_mlx_cpu_rows(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, int64_t m, int64_t n0, int64_t n1,

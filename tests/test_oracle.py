@@ -298,6 +298,19 @@ def test_mlx_cpu_restatement_accumulates_in_bf16():
     assert syn.sig_rel(O.qmatmul_f32_grouped(x, w, s, b), truth) < 1e-5
 
 
+def test_mlx_cpu_restatement_threaded_is_identical():
+    """The multi-core CPU baseline deals output rows over threads; each row is still one
+    sequential bf16 accumulation, so its output equals the single-thread loop bit for
+    bit (ragged last block of rows, m = 1 and 3)."""
+    k = 640
+    w, s, b = _rand_q4(203, k, 11)
+    for m in (1, 3):
+        x = syn.activations(m, k, seed=12 + m)
+        one = O.qmatmul_mlx_cpu(x, w, s, b)
+        for threads in (1, 3, 8):
+            np.testing.assert_array_equal(O.qmatmul_mlx_cpu_mt(x, w, s, b, threads), one)
+
+
 # ---------------------------------------------------------------- gelu / softcap
 
 def test_gelu_chain_constants_and_accuracy():
