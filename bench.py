@@ -13,9 +13,10 @@ Also reported, each on its own workload:
   prefill     the seven projections at m = 512 and 2048, q/k/v in one grouped launch
               (TFLOP/s vs bf16 MFMA peak)
   decode      48 layers (renormalise + q/k/v in one launch, o, fused gate/up + GELU, down)
-              + tied LM head [262144,3840] with softcap, m = 1 and 4, replayed from a
-              captured HIP graph (tokens/s and effective HBM GB/s), with the LM head
-              timed alone and the per-layer time and rate derived from the two
+              + tied LM head [262144,3840] with softcap + greedy sampling on the device,
+              m = 1 and 4, replayed from a captured HIP graph (tokens/s and effective
+              HBM GB/s), with the LM head and sampling timed alone and the per-layer time
+              and rate derived from the two
 and the oracle's restatement of MLX's CPU quantized_matmul timed on this host's cores
 (cpu_baseline).
 
@@ -239,7 +240,7 @@ def decode_layers(model, m, bufs, stream):
     """One decode step's layer stack: per layer, h renormalised and multiplied by q, k and
     v in one launch; o from q's output; the fused gate/up GELU from o's output; down
     into h."""
-    h, q, k, v, o, g, _logits = bufs
+    h, q, k, v, o, g = bufs[:6]
     for proj in model.layers:
         hy.qmatmul_group([proj["q"], proj["k"], proj["v"]], h, m, [q, k, v], stream, rms_eps=RMS_EPS)
         hy.qmatmul(proj["o"], q, m, o, stream)
@@ -248,9 +249,11 @@ def decode_layers(model, m, bufs, stream):
 
 
 def lm_head(model, m, bufs, stream):
-    """The last hidden state renormalised, then the tied LM head with softcap 30."""
+    """The last hidden state renormalised, the tied LM head with softcap 30, then greedy
+    sampling of every row on the device (run_epilogue, model.cc:215-228)."""
     hy.rms_normalize(bufs[0], m, HIDDEN, bufs[0], stream, eps=RMS_EPS)
-    hy.qmatmul(model.embed, bufs[0], m, bufs[-1], stream, softcap=30.0)
+    hy.qmatmul(model.embed, bufs[0], m, bufs[-2], stream, softcap=30.0)
+    hy.sample_greedy(bufs[-2], m, syn.VOCAB, bufs[-1], stream)
 
 
 LAUNCHES_PER_LAYER = 4
@@ -261,7 +264,8 @@ def bench_decode_stream(model, m, steps, warmup, stream):
     h = hy.DeviceArray.from_host(syn.activations(m, HIDDEN, seed=77), stream)
     bufs = (h, hy.DeviceArray((m, 4096), np.uint16), hy.DeviceArray((m, 2048), np.uint16),
             hy.DeviceArray((m, 2048), np.uint16), hy.DeviceArray((m, HIDDEN), np.uint16),
-            hy.DeviceArray((m, 15360), np.uint16), hy.DeviceArray((m, syn.VOCAB), np.uint16))
+            hy.DeviceArray((m, 15360), np.uint16), hy.DeviceArray((m, syn.VOCAB), np.uint16),
+            hy.DeviceArray((m, 3), np.uint32))
     with hy.Graph.capture(stream) as graph:
         decode_layers(model, m, bufs, stream)
         lm_head(model, m, bufs, stream)
@@ -272,14 +276,16 @@ def bench_decode_stream(model, m, steps, warmup, stream):
     head_ms = time_launches(stream, lambda _i: head.launch(stream), steps, warmup)
     head.close()
     layers = len(model.layers)
-    act = 2 * m * (layers * (HIDDEN * 3 + 4096 * 2 + 2048 * 2 + HIDDEN * 2 + 15360 * 3) + HIDDEN + syn.VOCAB)
+    # activations: per layer x, q/k/v, o, gate/up, down; then the head's x, logits written
+    # and read back by the sampler, and 12 bytes of sample per row
+    act = 2 * m * (layers * (HIDDEN * 3 + 4096 * 2 + 2048 * 2 + HIDDEN * 2 + 15360 * 3) + HIDDEN + 2 * syn.VOCAB) + 12 * m
     nbytes = model.weight_bytes + act
-    head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + syn.VOCAB)
+    head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + 2 * syn.VOCAB) + 12 * m
     layer_bytes = (nbytes - head_bytes) / max(layers, 1)
     layer_us = (ms - head_ms) * 1e3 / max(layers, 1)
     out = {"m": m, "ms_per_step": round(ms, 4), "tokens_per_s": round(m / (ms / 1e3), 1),
            "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-           "bytes_per_step": nbytes, "launches_per_step": LAUNCHES_PER_LAYER * layers + 2,
+           "bytes_per_step": nbytes, "launches_per_step": LAUNCHES_PER_LAYER * layers + 3,
            "lm_head_us": round(head_ms * 1e3, 1),
            "lm_head_gbs": round(head_bytes / head_ms / 1e6, 1),
            "layer_us": round(layer_us, 2),

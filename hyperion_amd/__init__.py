@@ -47,6 +47,7 @@ EXPORTED = [
     "hyp_qmatmul", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
+    "hyp_sample_greedy",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
 ]
@@ -70,6 +71,15 @@ class RuntimeInfo(ctypes.Structure):
         ("l2_bytes", ctypes.c_uint32),
         ("arch_name", ctypes.c_char * 64),
         ("device_name", ctypes.c_char * 128),
+    ]
+
+
+class GreedySample(ctypes.Structure):
+    """HypGreedySample: ForwardPass::GreedySample (forward.h:104-108)."""
+    _fields_ = [
+        ("token_id", ctypes.c_uint32),
+        ("logit", ctypes.c_float),
+        ("near_tie", ctypes.c_uint32),
     ]
 
 
@@ -122,6 +132,7 @@ def lib() -> ctypes.CDLL:
         "hyp_dequantize_q4g64": [_P, _P, _P, _U32, _U32, _P, _U32, ctypes.c_float, _P, _P],
         "hyp_embed": [_P, _P, _U32, _P, _P],
         "hyp_rms_normalize": [_P, _U32, _U32, ctypes.c_float, _P, _P],
+        "hyp_sample_greedy": [_P, _U32, _U32, _P, _P],
         "hyp_qmodel_load": [ctypes.c_char_p, _U32, _PP],
         "hyp_qmodel_free": [_PP],
         "hyp_qmodel_num_layers": [_P, ctypes.POINTER(_U32)],
@@ -424,3 +435,19 @@ def embed(table: QWeight, ids: DeviceArray, n_ids: int, out: DeviceArray, stream
 
 def rms_normalize(x: DeviceArray, m: int, k: int, y: DeviceArray, stream: Stream, eps: float = 1e-6) -> None:
     call("hyp_rms_normalize", x.ptr, m, k, eps, y.ptr, stream.handle)
+
+
+def sample_greedy(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, stream: Stream,
+                  row_offset: int = 0) -> None:
+    """out[r] = HypGreedySample of logits row row_offset + r, for r < rows (hyp_sample_greedy);
+    out is a device array of at least rows * 12 bytes."""
+    ptr = ctypes.c_void_p((logits.ptr.value or 0) + 2 * row_offset * vocab) if row_offset else logits.ptr
+    call("hyp_sample_greedy", ptr, rows, vocab, out.ptr, stream.handle)
+
+
+def greedy_samples(out: DeviceArray, rows: int, stream: Stream):
+    """The first `rows` HypGreedySample records of a device array, as (token_id, logit,
+    near_tie) tuples (one synchronizing copy of rows * 12 bytes)."""
+    raw = out.to_host(stream).reshape(-1).view(np.uint8)[: rows * ctypes.sizeof(GreedySample)]
+    recs = (GreedySample * rows).from_buffer_copy(raw.tobytes())
+    return [(r.token_id, r.logit, bool(r.near_tie)) for r in recs]

@@ -104,6 +104,10 @@ struct HypQModelOpaque {
 struct HypStreamOpaque {
     std::uint32_t magic = 0;
     hipStream_t stream = nullptr;
+    // Device workspace of the calls that need one (greedy sampling's slice states);
+    // work on one stream is ordered, so its calls never share it concurrently.
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
 };
 
 struct HypEventOpaque {
@@ -218,7 +222,13 @@ HypStatus hyp_stream_create(HypStream* out_stream) {
         REQUIRE_ARG(out_stream != nullptr, "create requires a non-null out handle");
         require_device();
         auto h = std::make_unique<HypStreamOpaque>();
-        HYP_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+        h->workspace_bytes = hyperion::hip::sample_greedy_workspace_bytes();
+        HYP_HIP_CHECK(hipMalloc(&h->workspace, h->workspace_bytes));
+        const hipError_t err = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+        if (err != hipSuccess) {
+            (void)hipFree(h->workspace);
+            HYP_HIP_CHECK(err);
+        }
         h->magic = kStreamMagic;
         *out_stream = h.release();
     });
@@ -230,7 +240,10 @@ HypStatus hyp_stream_destroy(HypStream* stream) {
     if ((*stream)->magic != kStreamMagic) {
         return fail(HYP_STATUS_INVALID_ARGUMENT, "handle magic mismatch (wrong type, freed, or corrupted)");
     }
-    const hipError_t err = hipStreamDestroy((*stream)->stream);
+    hipError_t err = hipStreamDestroy((*stream)->stream);
+    // hipFree waits for the device, so work still queued on the stream finishes first.
+    const hipError_t ferr = hipFree((*stream)->workspace);
+    if (err == hipSuccess) err = ferr;
     (*stream)->magic = 0;
     delete *stream;
     *stream = nullptr;
@@ -546,6 +559,19 @@ HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, vo
         if (m == 0 || k == 0) return;
         REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
         hyperion::hip::launch_rms_normalize(static_cast<const uint16_t*>(x), m, k, eps, static_cast<uint16_t*>(y), s);
+    });
+}
+
+HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, HypGreedySample* out,
+                            HypStream stream) {
+    return abi_call("hyp_sample_greedy", [&] {
+        hipStream_t s = stream_of(stream);
+        if (rows == 0) return;
+        REQUIRE_ARG(out != nullptr, "out must be a non-null device pointer");
+        REQUIRE_ARG(vocab == 0 || logits != nullptr, "logits must be a non-null device pointer");
+        REQUIRE_ARG(static_cast<uint64_t>(rows) * vocab < (1ull << 62), "logits too large");
+        hyperion::hip::launch_sample_greedy(static_cast<const uint16_t*>(logits), rows, vocab, out, stream->workspace,
+                                            stream->workspace_bytes, s);
     });
 }
 

@@ -6,6 +6,8 @@
 
 #include <cstdint>
 
+#include "hyperion_hip.h"
+
 namespace hyperion::hip {
 
 // A Q4/g64 projection [n, k]. w/scales/biases: MLX layout, codes uint32 [n, k/8],
@@ -83,6 +85,13 @@ void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t
 void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream);
 // y[r] = x[r] / sqrt(mean(x[r]^2) + eps) for each of m rows of k bf16 (y may equal x).
 void launch_rms_normalize(const uint16_t* x, uint32_t m, uint32_t k, float eps, uint16_t* y, hipStream_t stream);
+
+// ForwardPass::sample_greedy over each of `rows` rows of `vocab` bf16 logits -> out[row],
+// with slice states in `workspace` (device memory of sample_greedy_workspace_bytes(),
+// used by one stream at a time).
+size_t sample_greedy_workspace_bytes();
+void launch_sample_greedy(const uint16_t* logits, uint32_t rows, uint32_t vocab, HypGreedySample* out,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,

@@ -93,6 +93,13 @@ typedef enum HypEpilogue {
     HYP_EPILOGUE_SOFTCAP = 1        /* y = bf16(bf16(tanh(bf16(y / cap))) * cap), forward.cc:154-160 */
 } HypEpilogue;
 
+/* ForwardPass::GreedySample (forward.h:104-108); near_tie is a bool there. */
+typedef struct HypGreedySample {
+    uint32_t token_id;              /* argmax token */
+    float logit;                    /* the winning logit (bf16 value as fp32) */
+    uint32_t near_tie;              /* 1 when top1 - top2 < 0.5, else 0 */
+} HypGreedySample;
+
 /* ---- errors and runtime ------------------------------------------------------- */
 
 /* Copy the calling thread's last error into buffer (NUL-terminated, truncated).
@@ -108,6 +115,8 @@ HypStatus hyp_runtime_info(HypRuntimeInfo* out);
  * mx::Stream arguments, weights.h:26); a C caller of this engine gets them here. */
 HypStatus hyp_device_alloc(size_t bytes, void** out_ptr);
 HypStatus hyp_device_free(void** ptr);
+/* A non-blocking HIP stream plus a 48 KiB device workspace for the calls that need one
+ * (hyp_sample_greedy). destroy waits for the device before freeing the workspace. */
 HypStatus hyp_stream_create(HypStream* out_stream);
 HypStatus hyp_stream_destroy(HypStream* stream);
 HypStatus hyp_stream_synchronize(HypStream stream);
@@ -220,6 +229,19 @@ HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void*
  * projections: a weightless mx::fast::rms_norm (the reference normalises the decoder
  * input and branch outputs with it, forward.cc:521-529). eps must be finite and >= 0. */
 HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, void* y, HypStream stream);
+
+/* ForwardPass::sample_greedy (forward.cc:162-189) on the device, replacing its host copy
+ * of the logits and the CPU scan: for each of `rows` rows of `vocab` bf16 logits
+ * (row-major, device memory), out[r] (device memory) receives the first index of the
+ * largest value, that value, and whether it leads the largest other value by less than
+ * 0.5. NaN logits are skipped; a row with no value above -inf (or vocab == 0) gives
+ * token 0. The reference samples the last position: pass logits + (m - 1) * vocab and
+ * rows = 1 after the softcap LM head (hyp_qmatmul_ex). Uses a 48 KiB device workspace
+ * owned by the stream (made by hyp_stream_create): a graph captured on a stream keeps
+ * using that stream's workspace, so replay it on that stream (or one whose work is
+ * ordered with it) and only while the stream exists. */
+HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, HypGreedySample* out,
+                            HypStream stream);
 
 /* ---- weight residency (load_model_weights, weights_loader.cc:71-153) ------------ */
 

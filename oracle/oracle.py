@@ -39,6 +39,7 @@ def lib():
         L.orc_qmatmul_mlx_cpu.argtypes = [_P, _P, _P, _P, _I, _I, _I, _P]
         L.orc_qmatmul_mlx_cpu_rows.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P]
         L.orc_qmatmul_mlx_cpu_mt.argtypes = [_P, _P, _P, _P, _I, _I, _I, ctypes.c_int, _P]
+        L.orc_sample_greedy_bf16.argtypes = [_P, _I, _P, _P, _P]
         L.orc_gelu_tanh_bf16.argtypes = [_P, _I, _P]
         L.orc_gelu_tanh_mul_bf16.argtypes = [_P, _P, _I, _P]
         L.orc_softcap_bf16.argtypes = [_P, _I, ctypes.c_float, _P]
@@ -146,6 +147,16 @@ def qmatmul_mlx_cpu_mt(x, wq, s, b, threads) -> np.ndarray:
     y = np.empty((m, n), np.uint16)
     lib().orc_qmatmul_mlx_cpu_mt(_p(x), _p(wq), _p(s), _p(b), m, n, k, int(threads), _p(y))
     return y
+
+
+def sample_greedy(logits):
+    """ForwardPass::sample_greedy of a 1-D bf16 row -> (token_id, logit, near_tie)."""
+    x = _c(logits, np.uint16).reshape(-1)
+    tok = ctypes.c_uint32()
+    val = ctypes.c_float()
+    tie = ctypes.c_int32()
+    lib().orc_sample_greedy_bf16(_p(x), x.size, ctypes.byref(tok), ctypes.byref(val), ctypes.byref(tie))
+    return tok.value, val.value, bool(tie.value)
 
 
 def gelu_tanh(x) -> np.ndarray:

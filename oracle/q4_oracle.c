@@ -314,3 +314,27 @@ void orc_scale_bf16(const uint16_t* x, int64_t n, float c, uint16_t* out) {
         out[i] = orc_bf16_from_f32(orc_f32_from_bf16(x[i]) * cb);
     }
 }
+
+/*
+ * ForwardPass::sample_greedy (forward.cc:162-189): the row converted to fp32, then one
+ * pass in index order keeping top1 (with its index) and top2; near_tie = top1 - top2 < 0.5.
+ */
+void orc_sample_greedy_bf16(const uint16_t* logits, int64_t n, uint32_t* token, float* logit,
+                            int32_t* near_tie) {
+    float top1 = -INFINITY;
+    float top2 = -INFINITY;
+    uint32_t arg = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = orc_f32_from_bf16(logits[i]);
+        if (v > top1) {
+            top2 = top1;
+            top1 = v;
+            arg = (uint32_t)i;
+        } else if (v > top2) {
+            top2 = v;
+        }
+    }
+    *token = arg;
+    *logit = top1;
+    *near_tie = (top1 - top2) < 0.5f ? 1 : 0;
+}

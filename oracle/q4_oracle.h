@@ -18,6 +18,8 @@
  *   gelu_tanh     native/hyperion_mlx/src/forward.cc:324-343
  *   softcap       native/hyperion_mlx/src/forward.cc:154-160
  *   embed scale   native/hyperion_mlx/src/forward.cc:126-131
+ *   greedy sample native/hyperion_mlx/src/forward.cc:162-189 (the reference's own loop,
+ *                 not MLX)
  *
  * Pinning status (what checks each function; see tests/test_oracle.py):
  *   orc_bf16_from_f32       pinned: numpy float32 -> bfloat16 RNE bit patterns computed
@@ -43,6 +45,11 @@
  *   orc_gelu_tanh_mul_bf16  pinned against the closed-form fp64 GELU within the
  *                           rounding the bf16 op chain implies, and special values.
  *   orc_softcap_bf16        pinned likewise against 30*tanh(x/30) in fp64.
+ *   orc_qmatmul_mlx_cpu_mt  pinned to orc_qmatmul_mlx_cpu: bit-identical outputs.
+ *   orc_sample_greedy_bf16  pinned: against the definition computed independently with
+ *                           numpy (first index of the maximum over non-NaN values, the
+ *                           largest other value) on random rows with planted ties, NaN
+ *                           and infinities, and hand cases (empty, all -inf, all NaN).
  */
 #ifndef HYPERION_Q4_ORACLE_H
 #define HYPERION_Q4_ORACLE_H
@@ -88,6 +95,10 @@ void orc_qmatmul_f32_grouped(const uint16_t* x, const uint32_t* wq, const uint16
  * accumulator typed as the input dtype (bf16): every multiply/add rounds to bf16. */
 void orc_qmatmul_mlx_cpu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                          const uint16_t* biases, int64_t m, int64_t n, int64_t k, uint16_t* y);
+
+/* ForwardPass::sample_greedy on one row of n bf16 logits: token, its logit, near_tie. */
+void orc_sample_greedy_bf16(const uint16_t* logits, int64_t n, uint32_t* token, float* logit,
+                            int32_t* near_tie);
 
 /* orc_qmatmul_mlx_cpu with output rows spread over `threads` OpenMP threads
  * (bit-identical result; the multi-core CPU baseline). */

@@ -100,6 +100,10 @@ def test_calls_reject_null_and_foreign_handles():
     assert _status("hyp_stream_synchronize", None) == 1
     assert "explicit stream" in hy.last_error()
     assert _status("hyp_quantize_q4g64", None, 1, 64, None, None, None, hf) == 1
+    assert _status("hyp_sample_greedy", None, 1, 262144, None, None) == 1   # explicit stream
+    assert "explicit stream" in hy.last_error()
+    assert _status("hyp_sample_greedy", None, 1, 262144, None, hf) == 1     # foreign stream handle
+    assert "magic" in hy.last_error()
 
 
 def test_last_error_buffer_contract():

@@ -464,6 +464,100 @@ def test_lm_head_softcap(stream, m):
     _assert_close_bits(capped, O.softcap(plain, 30.0), f"m={m}", max_ulp=2)
 
 
+# ---------------------------------------------------------------- greedy sampling on the device
+
+def _sample_rows(bits2d, stream, rows, vocab, row_offset=0):
+    d = dev(bits2d, stream)
+    out = hy.DeviceArray((max(rows, 1) * 3,), np.uint32)
+    hy.sample_greedy(d, rows, vocab, out, stream, row_offset=row_offset)
+    got = hy.greedy_samples(out, rows, stream)
+    d.close()
+    out.close()
+    return got
+
+
+def _assert_samples_equal(got, want, what):
+    g_tok, g_val, g_tie = got
+    w_tok, w_val, w_tie = want
+    assert (g_tok, g_tie) == (w_tok, w_tie), f"{what}: {got} vs {want}"
+    assert np.float32(g_val).tobytes() == np.float32(w_val).tobytes(), f"{what}: {got} vs {want}"
+
+
+def _planted_logits(rng, rows, vocab):
+    """Random bf16 logits with, per row, one of: a tie at the maximum (the later index
+    must lose), NaN and +-inf entries, a near tie at gap 0.375 or 0.5, or nothing."""
+    v = syn.bf16_bits((rng.standard_normal((rows, vocab)) * 6).astype(np.float32))
+    for r in range(rows):
+        kind = r % 4
+        if vocab < 4:
+            continue
+        i, j = sorted(rng.choice(vocab, 2, replace=False))
+        if kind == 1:
+            v[r, i] = v[r, j] = syn.bf16_bits(np.float32([60.0]))[0]
+        elif kind == 2:
+            v[r, rng.integers(vocab)] = 0x7FC0
+            v[r, rng.integers(vocab)] = 0xFF80
+            v[r, i] = 0x7F80 if r % 8 == 2 else syn.bf16_bits(np.float32([70.0]))[0]
+        elif kind == 3:
+            v[r, j] = syn.bf16_bits(np.float32([64.0]))[0]
+            v[r, i] = syn.bf16_bits(np.float32([63.625 if r % 8 == 3 else 63.5]))[0]
+    return v
+
+
+@pytest.mark.parametrize("vocab", [262144, 262143, 1000, 8, 7, 1])
+def test_sample_greedy_matches_oracle(stream, vocab):
+    """hyp_sample_greedy against the oracle's restatement of forward.cc:162-189, exactly
+    (token, logit bits, near_tie), on 8 rows with planted ties, NaN, infinities and near
+    ties; vocab % 8 != 0 takes the element-wise path; a row offset makes the start
+    unaligned."""
+    rng = np.random.default_rng(vocab)
+    rows = 8
+    say(f"sample_greedy vocab={vocab}")
+    v = _planted_logits(rng, rows, vocab)
+    got = _sample_rows(v, stream, rows, vocab)
+    for r in range(rows):
+        _assert_samples_equal(got[r], O.sample_greedy(v[r]), f"vocab={vocab} row={r}")
+    got = _sample_rows(v, stream, rows - 1, vocab, row_offset=1)
+    for r in range(rows - 1):
+        _assert_samples_equal(got[r], O.sample_greedy(v[r + 1]), f"vocab={vocab} offset row={r + 1}")
+
+
+def test_sample_greedy_degenerate_rows(stream):
+    """All -inf, all NaN and vocab = 0 rows give token 0 with logit -inf and no near tie
+    (the reference's initial values survive the scan); rows = 0 is a no-op."""
+    say("sample_greedy degenerate rows")
+    v = np.stack([np.full(4096, 0xFF80, np.uint16), np.full(4096, 0x7FC0, np.uint16)])
+    for got in _sample_rows(v, stream, 2, 4096):
+        _assert_samples_equal(got, (0, float("-inf"), False), "degenerate")
+    for got in _sample_rows(np.zeros((2, 8), np.uint16), stream, 2, 0):
+        _assert_samples_equal(got, (0, float("-inf"), False), "vocab=0")
+    assert _sample_rows(v, stream, 0, 4096) == []
+
+
+def test_lm_head_softcap_then_device_greedy(stream):
+    """run_epilogue (model.cc:215-228) on the device: the tied head with softcap on m = 3
+    rows of a [32768, 3840] table, then greedy sampling of the last row, equal to the
+    oracle's sampler on that row of the kernel's own logits."""
+    n, k, m = 32768, 3840, 3
+    say("lm head softcap -> device greedy")
+    x = syn.activations(m, k, seed=711)
+    w, s, b = syn.q4_weights(n, k, seed=712)
+    s = syn.bf16_bits(syn.bf16_to_f32(s) * np.float32(64.0))
+    b = syn.bf16_bits(syn.bf16_to_f32(b) * np.float32(64.0))
+    qw = hy.QWeight.from_host(w, s, b)
+    xd = dev(x, stream)
+    yd = hy.DeviceArray((m, n), np.uint16)
+    hy.qmatmul(qw, xd, m, yd, stream, softcap=30.0)
+    out = hy.DeviceArray((3,), np.uint32)
+    hy.sample_greedy(yd, 1, n, out, stream, row_offset=m - 1)
+    got = hy.greedy_samples(out, 1, stream)[0]
+    logits = yd.to_host(stream)
+    _assert_samples_equal(got, O.sample_greedy(logits[m - 1]), "head last row")
+    assert got[1] <= 30.0
+    for a in (qw, xd, yd, out):
+        a.close()
+
+
 # ---------------------------------------------------------------- residency (tiny artifact)
 
 def test_qmodel_fixture_reference_weights_test(stream, fixture_dir):

@@ -351,3 +351,47 @@ def test_qmatmul_deq_f64_against_dequantize_and_truth():
     s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
     b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
     np.testing.assert_array_equal(O.qmatmul_deq_f64(x, w, s2, b2, mode=0), O.qmatmul_f64(x, w, s2, b2))
+
+
+def _greedy_by_definition(row_bits):
+    """ForwardPass::sample_greedy's result from its definition, computed with numpy:
+    the first index of the largest non-NaN value (0 when none exceeds -inf), that value,
+    and whether it leads the largest of the other values by less than 0.5."""
+    v = syn.bf16_to_f32(row_bits.reshape(-1)).astype(np.float32)
+    v = np.where(np.isnan(v), np.float32(-np.inf), v)
+    if v.size == 0 or not (v > -np.inf).any():
+        return 0, float("-inf"), False
+    tok = int(np.argmax(v))
+    top1 = v[tok]
+    rest = np.delete(v, tok)
+    top2 = rest.max() if rest.size else np.float32(-np.inf)
+    return tok, float(top1), bool(np.float32(top1) - np.float32(top2) < np.float32(0.5))
+
+
+def test_sample_greedy_restatement_matches_definition():
+    rng = np.random.default_rng(21)
+    for trial in range(40):
+        n = int(rng.choice([1, 2, 7, 64, 1000, 4099]))
+        v = rng.standard_normal(n).astype(np.float32) * 4
+        bits = syn.bf16_bits(v)
+        if trial % 4 == 1 and n > 3:          # a tie at the maximum, later index
+            j, k2 = sorted(rng.choice(n, 2, replace=False))
+            bits[j] = bits[k2] = syn.bf16_bits(np.float32([50.0]))[0]
+        if trial % 4 == 2 and n > 3:          # NaN and infinities
+            bits[rng.integers(n)] = 0x7FC0
+            bits[rng.integers(n)] = 0xFF80
+            if trial % 8 == 2:
+                bits[rng.integers(n)] = 0x7F80
+        if trial % 4 == 3 and n > 1:          # near tie just under / over 0.5
+            top = int(np.argmax(syn.bf16_to_f32(bits)))
+            other = (top + 1) % n
+            bits[top] = syn.bf16_bits(np.float32([20.0]))[0]
+            bits[other] = syn.bf16_bits(np.float32([19.5 if trial % 8 == 3 else 19.625]))[0]
+        assert O.sample_greedy(bits) == _greedy_by_definition(bits), f"trial {trial}"
+    # hand cases
+    assert O.sample_greedy(np.zeros(0, np.uint16)) == (0, float("-inf"), False)
+    assert O.sample_greedy(np.full(5, 0xFF80, np.uint16)) == (0, float("-inf"), False)
+    assert O.sample_greedy(np.full(5, 0x7FC0, np.uint16)) == (0, float("-inf"), False)
+    assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 3, 2]))) == (1, 3.0, True)
+    assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 2.5, 2]))) == (1, 3.0, False)
+    assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 2.75, 2]))) == (1, 3.0, True)
