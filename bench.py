@@ -296,6 +296,29 @@ def bench_decode_stream(model, m, steps, warmup, stream):
     return out
 
 
+def bench_sample(stream, steps, warmup):
+    """hyp_sample_greedy on rows of vocab 262144 seeded logits N(0, 36): 10 calls captured
+    in one graph, timed per call from graph replays."""
+    out = []
+    for rows in (1, 4):
+        logits = hy.DeviceArray.from_host(
+            syn.bf16_bits((np.random.default_rng(31 + rows).standard_normal((rows, syn.VOCAB)) * 6).astype(np.float32)),
+            stream)
+        res = hy.DeviceArray((rows, 3), np.uint32)
+        with hy.Graph.capture(stream) as graph:
+            for _ in range(10):
+                hy.sample_greedy(logits, rows, syn.VOCAB, res, stream)
+        ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup) / 10
+        graph.close()
+        nbytes = 2 * rows * syn.VOCAB + 12 * rows
+        out.append({"rows": rows, "vocab": syn.VOCAB, "us": round(ms * 1e3, 2),
+                    "gbs": round(nbytes / ms / 1e6, 1)})
+        log(f"greedy sample rows={rows} vocab={syn.VOCAB}: {ms * 1e3:.2f} us per call")
+        logits.close()
+        res.close()
+    return out
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -364,6 +387,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-decode", action="store_true", help="only the headline decode GEMV")
     ap.add_argument("--only-prefill", action="store_true", help="the headline decode GEMV and the prefill GEMMs")
+    ap.add_argument("--only-sample", action="store_true", help="the headline decode GEMV and greedy sampling")
     ap.add_argument("--dense-ref", action="store_true",
                     help="also time hipBLASLt's dense bf16 GEMM (torch.matmul) on the prefill shapes")
     ap.add_argument("--dense-child", type=int, default=0, help=argparse.SUPPRESS)
@@ -396,8 +420,11 @@ def main():
     extra = {}
     if args.only_prefill:
         extra["prefill"] = [bench_prefill(stream, m, 10, 2, dense.get(m)) for m in (512, 2048)]
+    elif args.only_sample:
+        extra["sample_greedy"] = bench_sample(stream, 20, 3)
     elif not args.only_decode:
         extra["quantize"] = bench_quantize(stream, 50, 5)
+        extra["sample_greedy"] = bench_sample(stream, 20, 3)
         extra["prefill"] = [bench_prefill(stream, m, 10, 2, dense.get(m)) for m in (512, 2048)]
         model = DecodeModel(args.layers, stream)
         streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
