@@ -374,6 +374,9 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 // same k chunk.
 
 constexpr uint32_t kGRowBytes = 128u;   // one group of one X row
+// Waves of the group-step kernel's workgroup: each wave owns 16 NT columns, so the
+// workgroup tile is 256 x (16 NT W); the W waves share one X stage.
+constexpr int kGroupWaves = 8;
 
 template <int NT>
 struct GRaw {
@@ -453,11 +456,11 @@ __device__ __forceinline__ void g_mfma_part(const bf16x8_t (&a)[MT / P], const b
     }
 }
 
-template <int MT, int NT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_g_kernel(GemmParams p) {
+template <int MT, int NT, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_g_kernel(GemmParams p) {
     constexpr uint32_t BM = 16u * MT;
     constexpr uint32_t kStage = BM * kGRowBytes;
-    constexpr int kXLoads = static_cast<int>(BM / 8u / kWaves);   // 1 KB (8 rows) direct loads per wave
+    constexpr int kXLoads = static_cast<int>(BM / 8u / W);   // 1 KB (8 rows) direct loads per wave
     static_assert(kXLoads % 2 == 0, "swizzle period");
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];   // [2][BM][128 B], reused by the epilogue
 
@@ -477,7 +480,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t tm = tile / p.tiles_n;
     const SegView sv = segment_of(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
-    const uint32_t n0 = sv.tn * (kWaves * 16u * NT);
+    const uint32_t n0 = sv.tn * (W * 16u * NT);
     const uint32_t tile16_0 = n0 / 16u + wave * NT;
     const uint32_t k = p.k;
     // This workgroup's groups [g0, g1): whole pairs of its split (all groups without split k).
@@ -603,8 +606,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         return;
     }
 
-    // Epilogue through LDS as in q4_gemm_kernel.
-    constexpr uint32_t kOutRow = 128u * NT + 32u;
+    // Epilogue through LDS as in q4_gemm_kernel (rows of 32 NT W bytes plus 32 of padding).
+    constexpr uint32_t kOutRow = 32u * NT * W + 32u;
     __syncthreads();
     {
         const uint32_t j = lane & 15u;
@@ -621,8 +624,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 }
     }
     __syncthreads();
-    constexpr uint32_t kChunks = 64u * NT / 8u;
-    constexpr uint32_t kRowsPerPass = kThreads / kChunks;
+    constexpr uint32_t kChunks = 16u * NT * W / 8u;
+    constexpr uint32_t kRowsPerPass = 64u * W / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
     const uint32_t col0 = n0 + ch * 8u;
     if ((sv.n & 7u) == 0u) {
@@ -644,10 +647,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int W>
 constexpr size_t g_lds_bytes() {
-    return 2u * 16u * MT * kGRowBytes > 16u * MT * (128u * NT + 32u) ? 2u * 16u * MT * kGRowBytes
-                                                                     : 16u * MT * (128u * NT + 32u);
+    return 2u * 16u * MT * kGRowBytes > 16u * MT * (32u * NT * W + 32u) ? 2u * 16u * MT * kGRowBytes
+                                                                         : 16u * MT * (32u * NT * W + 32u);
 }
 
 // y_seg[row][col] = bf16(sum over splits z = 0, 1, ... of partial[z][row][col_begin + col]),
@@ -682,6 +685,18 @@ size_t max_lds_per_block() {
     return cached;
 }
 
+constexpr uint32_t kTileCols = 128u;   // workgroup tile width of the pair-step kernel (NT = 2)
+
+// Column tiles of `tile_cols` columns: each segment's first global tile and the total.
+void retile(GemmParams& p, uint32_t tile_cols) {
+    uint32_t tn = 0;
+    for (uint32_t i = 0; i < p.nseg; ++i) {
+        p.seg[i].tn_begin = tn;
+        tn += (p.seg[i].n + tile_cols - 1u) / tile_cols;
+    }
+    p.tiles_n = tn;
+}
+
 template <int MT, int NT>
 void launch_t(GemmParams p, hipStream_t stream) {
     const bool odd = ((p.k / 64u) & 1u) != 0u;
@@ -705,11 +720,11 @@ void launch_t(GemmParams p, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3(p.tiles_total * p.ksplit), dim3(kThreads), lds, stream, p);
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int W>
 void launch_g(GemmParams p, hipStream_t stream) {
-
-    auto kernel = q4_gemm_g_kernel<MT, NT>;
-    constexpr size_t lds = g_lds_bytes<MT, NT>();
+    retile(p, 16u * NT * W);
+    auto kernel = q4_gemm_g_kernel<MT, NT, W>;
+    constexpr size_t lds = g_lds_bytes<MT, NT, W>();
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
     if (lds > 65536u) {
         static thread_local int configured_device = -1;
@@ -723,10 +738,8 @@ void launch_g(GemmParams p, hipStream_t stream) {
     }
     const uint32_t tiles_m = (p.m + 16u * MT - 1u) / (16u * MT);
     p.tiles_total = p.tiles_n * tiles_m;
-    hipLaunchKernelGGL(kernel, dim3(p.tiles_total * p.ksplit), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL(kernel, dim3(p.tiles_total * p.ksplit), dim3(64 * W), lds, stream, p);
 }
-
-constexpr uint32_t kTileCols = 128u;   // workgroup tile width of both kernels (NT = 2)
 
 // Parameters of a grouped launch; tiles_total is set by the launcher of the chosen kernel.
 GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
@@ -765,7 +778,7 @@ GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t
 
 void launch_params(GemmParams& p, uint32_t mt, hipStream_t stream) {
     if (mt == 16u) {
-        launch_g<16, 2>(p, stream);
+        launch_g<16, 2, kGroupWaves>(p, stream);
     } else if (mt == 8u) {
         launch_t<8, 2>(p, stream);
     } else {
