@@ -70,15 +70,6 @@ void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* 
 // ys[i][m, n_i] = x . dequant(W_i)^T.
 void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
                           uint32_t m, hipStream_t stream);
-// The pair-step kernel with k split `ksplit` ways (fp32 partials in a stream-ordered
-// workspace, summed in order into bf16); ksplit = 1 is the plain launch.
-void launch_q4_gemm_split(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t ksplit,
-                          hipStream_t stream);
-// Same with an explicit workgroup tile: (16 * mt) x (64 * nt), nt = 2; mt = 8 is the
-// pair-step kernel (128 x 128), mt = 16 the group-step kernel (256 x 128).
-void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
-                           hipStream_t stream);
-
 // h = bf16(gelu_chain(h) * u) over `count` bf16 elements (in place on h).
 void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t stream);
 // y = softcap(y) over `count` bf16 elements (in place).

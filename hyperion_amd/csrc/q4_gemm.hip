@@ -778,58 +778,74 @@ GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t
     return p;
 }
 
-void launch_params(GemmParams& p, uint32_t mt, hipStream_t stream) {
-    if (mt == 16u) {
-        launch_g<16, 2, kGroupWaves>(p, stream);
-    } else if (mt == 8u) {
-        launch_t<8, 2>(p, stream);
-    } else {
-        throw NativeError(HYP_STATUS_INTERNAL, "gemm: unsupported tile shape");
+// The three GEMM kernels by workgroup tile.
+enum class GemmKernel : uint32_t {
+    kPair128 = 0,    // q4_gemm_kernel<8, 2>: 128 x 128, pair step, two workgroups per CU
+    kGroup128 = 1,   // q4_gemm_g_kernel<8, 2, 8>: 128 x 256, group step, one per CU
+    kGroup256 = 2,   // q4_gemm_g_kernel<16, 2, 8>: 256 x 256, group step, one per CU
+};
+
+struct GemmChoice {
+    GemmKernel kernel;
+    uint32_t ksplit;
+};
+
+void launch_params(GemmParams& p, GemmKernel kernel, hipStream_t stream) {
+    switch (kernel) {
+        case GemmKernel::kPair128: launch_t<8, 2>(p, stream); break;
+        case GemmKernel::kGroup128: launch_g<8, 2, kGroupWaves>(p, stream); break;
+        case GemmKernel::kGroup256: launch_g<16, 2, kGroupWaves>(p, stream); break;
+        default: throw NativeError(HYP_STATUS_INTERNAL, "gemm: unsupported kernel");
     }
     HYP_HIP_CHECK(hipGetLastError());
 }
 
-// The 256 x 128 group-step kernel halves the dequantization per MFMA but runs two
-// workgroups per CU; it is faster once its grid holds at least two workgroups per CU
-// (the 15360-row gate/up at m = 2048: 869 vs 759 TFLOP/s), the 128 x 128 kernel
-// otherwise (fewer tiles: q, k, v, o, down at 2048, every projection at 512).
-uint32_t choose_mt(const GemmParams& p) {
-    const uint64_t big_tiles = static_cast<uint64_t>((p.m + 255u) / 256u) * p.tiles_n;
-    return big_tiles >= 2ull * device_compute_units() ? 16u : 8u;
+// Workgroups of one k split: (rows / tile rows) x (column tiles over the segments).
+uint64_t gemm_tiles(const GemmParams& p, uint32_t rows, uint32_t cols) {
+    uint64_t tn = 0;
+    for (uint32_t i = 0; i < p.nseg; ++i) tn += (p.seg[i].n + cols - 1u) / cols;
+    return static_cast<uint64_t>((p.m + rows - 1u) / rows) * tn;
 }
 
-// Split k for the group-step kernel: a long k (at least 64 pairs) with a grid of fewer
-// than two workgroups per CU. Measured on down at m = 2048 (240 tiles of 256 x 128,
-// k = 15360): 289 us unsplit, 249 with 2 splits, 268 with 3, against 310 for the pair-step
-// kernel; o at m = 2048 (k = 4096) is faster on the pair-step kernel unsplit (82 us).
-uint32_t choose_g_ksplit(const GemmParams& p) {
-    const uint64_t cus = device_compute_units();
-    const uint64_t big_tiles = static_cast<uint64_t>((p.m + 255u) / 256u) * p.tiles_n;
-    if (p.pairs < 64u || big_tiles >= 2u * cus || (p.m + 255u) / 256u < 4u) return 1u;
-    const uint64_t s = (3u * cus + 2u * big_tiles - 1u) / (2u * big_tiles);   // ~1.5 workgroups per CU
-    return static_cast<uint32_t>(std::min<uint64_t>(4u, std::max<uint64_t>(1u, s)));
-}
-
-// Split k for the pair-step kernel: when its grid fills at most 3/4 of the CUs, each
-// output tile is shared by up to 4 workgroups of at least 8 pairs each; the fp32 partials
-// go to a stream-ordered workspace and are summed in order. Measured at m = 512: down
-// 193 -> 88 us (4 splits), o 56 -> 41; q/k/v grouped (256 tiles) 56.5 us unsplit against
-// 59.1 with 2; no gain once the grid holds ~2 workgroups per CU (o and down at m = 2048).
-uint32_t choose_ksplit(const GemmParams& p) {
-    const uint64_t cus = device_compute_units();
-    const uint64_t tiles = static_cast<uint64_t>((p.m + 127u) / 128u) * p.tiles_n;
-    if (tiles * 4u > cus * 3u) return 1u;
-    uint32_t s = static_cast<uint32_t>(std::min<uint64_t>(4u, (2u * cus + tiles - 1u) / tiles));
-    while (s > 1u && p.pairs / s < 8u) --s;
+// Smallest split (<= 4, at least 6 pairs in each) whose grid of `tiles` x split reaches
+// 90% of the CUs.
+uint32_t fill_split(const GemmParams& p, uint64_t tiles, uint64_t cus) {
+    uint32_t s = 1u;
+    while (s < 4u && tiles * s * 10u < cus * 9u && (p.pairs + s) / (s + 1u) >= 6u) ++s;
     return s;
 }
 
-void launch_split(GemmParams& p, uint32_t mt, uint32_t ksplit, hipStream_t stream) {
+// Kernel and split per call. From a sweep of the seven projections and the grouped q/k/v
+// at m = 512, 1024 and 2048 on seeded random data (all three kernels, 1-4 splits), these
+// rules pick the fastest configuration or one within 5% of it:
+//  * the 256 x 256 kernel when its grid fills 90% of the CUs (gate/up at m >= 1024, the
+//    grouped q/k/v at 2048), or does so split when k is long (down at m = 1024: 4 splits,
+//    125 us against 192 on the pair-step kernel; at 2048: 2 splits, 215 against 226);
+//  * else the 128 x 256 kernel, split to fill the CUs, when that reaches 60% of them
+//    (gate at m = 512: 71 us against 81; o at 2048: 67 against 76);
+//  * else the 128 x 128 pair-step kernel, split likewise (k [2048, 3840] at m = 512, 4
+//    splits: 33 us against 34-36).
+GemmChoice choose_gemm(const GemmParams& p) {
+    const uint64_t cus = device_compute_units();
+    const uint64_t big = gemm_tiles(p, 256u, 256u);
+    if (big * 10u >= cus * 9u) return {GemmKernel::kGroup256, 1u};
+    if (p.pairs >= 64u) {
+        const uint32_t s = fill_split(p, big, cus);
+        if (big * s * 10u >= cus * 9u) return {GemmKernel::kGroup256, s};
+    }
+    const uint64_t mid = gemm_tiles(p, 128u, 256u);
+    const uint32_t s = fill_split(p, mid, cus);
+    if (mid * s * 10u >= cus * 6u) return {GemmKernel::kGroup128, s};
+    const uint64_t pair = gemm_tiles(p, 128u, 128u);
+    return {GemmKernel::kPair128, fill_split(p, pair, cus)};
+}
+
+void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t stream) {
     p.ksplit = ksplit;
     p.pairs_per_split = (p.pairs + ksplit - 1u) / ksplit;
     p.ksplit = (p.pairs + p.pairs_per_split - 1u) / p.pairs_per_split;   // no empty split
     if (p.ksplit == 1u) {
-        launch_params(p, mt, stream);
+        launch_params(p, kernel, stream);
         return;
     }
     const uint64_t elems = static_cast<uint64_t>(p.m) * p.n_total;
@@ -837,7 +853,7 @@ void launch_split(GemmParams& p, uint32_t mt, uint32_t ksplit, hipStream_t strea
     HYP_HIP_CHECK(hipMallocAsync(&ws, elems * p.ksplit * sizeof(float), stream));
     p.partial = static_cast<float*>(ws);
     try {
-        launch_params(p, mt, stream);
+        launch_params(p, kernel, stream);
         const uint64_t blocks = (elems + kThreads - 1u) / kThreads;
         HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
         hipLaunchKernelGGL(q4_splitk_reduce_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, p);
@@ -851,36 +867,11 @@ void launch_split(GemmParams& p, uint32_t mt, uint32_t ksplit, hipStream_t strea
 
 }  // namespace
 
-void launch_q4_gemm_config(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t mt, uint32_t nt,
-                           hipStream_t stream) {
-    HYP_REQUIRE(nt == 2u, HYP_STATUS_INTERNAL, "gemm: unsupported tile shape");
-    const Q4Matrix* ws[1] = {&w};
-    uint16_t* ys[1] = {y};
-    GemmParams p = group_params(ws, ys, 1u, x, m);
-    launch_params(p, mt, stream);
-}
-
 void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
                           uint32_t m, hipStream_t stream) {
     GemmParams p = group_params(ws, ys, count, x, m);
-    const uint32_t mt = choose_mt(p);
-    const uint32_t gsplit = mt == 8u ? choose_g_ksplit(p) : 1u;
-    if (gsplit > 1u) {
-        launch_split(p, 16u, gsplit, stream);
-    } else if (mt == 8u) {
-        launch_split(p, 8u, choose_ksplit(p), stream);
-    } else {
-        launch_params(p, mt, stream);
-    }
-}
-
-void launch_q4_gemm_split(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, uint32_t ksplit,
-                          hipStream_t stream) {
-    HYP_REQUIRE(ksplit >= 1u, HYP_STATUS_INTERNAL, "gemm: bad split count");
-    const Q4Matrix* ws[1] = {&w};
-    uint16_t* ys[1] = {y};
-    GemmParams p = group_params(ws, ys, 1u, x, m);
-    launch_split(p, 8u, std::min(ksplit, p.pairs), stream);
+    const GemmChoice c = choose_gemm(p);
+    launch_split(p, c.kernel, c.ksplit, stream);
 }
 
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {

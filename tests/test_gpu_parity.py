@@ -316,6 +316,25 @@ def test_gemm_prefill_projections_sampled(stream, m):
         assert_within_bf16_rounding(y[rows], ref_bf16w, name)
 
 
+@pytest.mark.parametrize("m", [512, 1024, 2048])
+def test_gemm_grouped_qkv_layer_shapes(stream, m):
+    """The grouped q/k/v call of a layer at prefill sizes ([4096|2048|2048, 3840] in one
+    launch): m = 512 takes the 128 x 256 group-step kernel with 2 k splits, m = 1024 the
+    same unsplit and m = 2048 the 256 x 256 one. Sampled rows against the fp64 product with
+    the kernel's bf16 weights, and sig_rel <= 1e-2 against the fp64 truth."""
+    k = 3840
+    say(f"gemm grouped q/k/v m={m}")
+    ws = [syn.q4_weights(n, k, seed=1600 + i) for i, n in enumerate((4096, 2048, 2048))]
+    x = syn.activations(m, k, seed=1610 + m)
+    ys = run_group(ws, x, stream)
+    rng = np.random.default_rng(m + 7)
+    rows = np.sort(rng.choice(m, size=10, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    for (w, s, b), y in zip(ws, ys):
+        assert_within_bf16_rounding(y[rows], O.qmatmul_deq_f64(x[rows], w, s, b, mode=1), f"n={w.shape[0]}")
+        assert syn.sig_rel(syn.bf16_to_f32(y[rows]), O.qmatmul_f64(x[rows], w, s, b)) <= 1e-2
+
+
 def test_gemm_exact_integer_and_ragged_tiles(stream):
     rng = np.random.default_rng(8)
     for m, n, k in ((300, 200, 512), (257, 33, 64), (5, 1000, 3840), (2048, 40, 128)):
@@ -357,7 +376,7 @@ def test_gemm_split_k_grouped_and_exact(stream):
 
 @pytest.mark.parametrize("n,k", [(8200, 192), (8195, 320), (8200, 3840)])
 def test_gemm_group_step_tiles(stream, n, k):
-    """Grids of >= 2 workgroups per CU select the 256 x 128 group-step kernel: ragged m
+    """Grids of >= 0.9 workgroups per CU in 256 x 256 tiles select the 256-row group-step kernel: ragged m
     (2000 rows, the last row tile part-empty), n with a part-empty 16-row tile (8200) or
     n % 8 != 0 (8195: the element-wise store path), odd group counts (k = 192, 320).
     Sampled rows against the fp64 product with the kernel's bf16 weights, and all rows
@@ -381,15 +400,42 @@ def test_gemm_group_step_tiles(stream, n, k):
     np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"exact n={n} k={k}")
 
 
+@pytest.mark.parametrize("m,n,splits", [(1300, 6000, 1), (700, 3000, 4)])
+def test_gemm_group_step_128_rows(stream, m, n, splits):
+    """Mid-size grids select the 128 x 256 group-step kernel, unsplit (11 x 24 tiles) or
+    with 4 k splits (6 x 12 tiles): ragged m (the last 128-row tile part-empty), n not a
+    multiple of 256, an odd group count (k = 4160: 65 groups, so the last pair is half
+    empty). Sampled rows against the fp64 product with the kernel's bf16 weights, and
+    exact integer inputs on sampled rows including the last row tile."""
+    k = 4160
+    say(f"gemm group-step 128 rows m={m} n={n} k={k} (splits {splits})")
+    x = syn.activations(m, k, seed=1700 + m)
+    w, s, b = syn.q4_weights(n, k, seed=1701 + n)
+    y = run_qmatmul(w, s, b, x, stream)
+    rng = np.random.default_rng(m + n)
+    rows = np.sort(rng.choice(m, size=12, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    assert_within_bf16_rounding(y[rows], O.qmatmul_deq_f64(x[rows], w, s, b, mode=1), f"m={m} n={n}")
+    xi = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
+    codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+    s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
+    b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
+    y2 = run_qmatmul(syn.pack_codes(codes), s2, b2, syn.bf16_bits(xi), stream)
+    check = np.unique(np.concatenate([rows, np.arange(m - 20, m)]))
+    exact = (xi[check].astype(np.float64) @ (codes.astype(np.float64) - 8).T) * 2.0**-7
+    np.testing.assert_array_equal(y2[check], syn.bf16_bits(exact.astype(np.float32)), err_msg=f"exact m={m} n={n}")
+
+
 def test_gemm_group_step_split_k(stream):
-    """A long k (129 groups) on a grid short of two workgroups per CU (8 x 3 tiles of
-    256 x 128) runs the group-step kernel with k split 4 ways (34-group ranges, the last
-    of 27 groups ending on a half pair): a grouped call over two segments (n = 100, 200) with ragged
-    m = 2000 against the fp64 product with the kernel's bf16 weights on sampled rows, and
-    every row exact on integer inputs."""
+    """A long k (129 groups) on a grid short of the CUs (8 x 12 tiles of 256 x 256) runs the
+    256-row group-step kernel with k split 3 ways (22-pair ranges, the last covering 41
+    groups and ending on a half pair): a grouped call over two segments (n = 1000, 2000) with ragged
+    m = 2000, against the fp64 product with the kernel's bf16 weights on sampled rows; and
+    exact integer inputs on one [3000, 8256] matrix, bit-exact on sampled rows including
+    the part-empty last row tile."""
     m, k = 2000, 8256
     say(f"gemm group-step split-k m={m} k={k}")
-    ws = [syn.q4_weights(n, k, seed=1500 + n) for n in (100, 200)]
+    ws = [syn.q4_weights(n, k, seed=1500 + n) for n in (1000, 2000)]
     x = syn.activations(m, k, seed=1510)
     ys = run_group(ws, x, stream)
     rng = np.random.default_rng(k)
@@ -397,14 +443,15 @@ def test_gemm_group_step_split_k(stream):
     rows[0], rows[-1] = 0, m - 1
     for (w, s, b), y in zip(ws, ys):
         assert_within_bf16_rounding(y[rows], O.qmatmul_deq_f64(x[rows], w, s, b, mode=1), f"n={w.shape[0]}")
-    n = 300
+    n = 3000
     xi = rng.integers(-1, 2, size=(m, k)).astype(np.float32)
     codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
     s2 = syn.bf16_bits(np.full((n, k // 64), 2.0**-7, np.float32))
     b2 = syn.bf16_bits(np.full((n, k // 64), -(2.0**-4), np.float32))
-    exact = (xi.astype(np.int64) @ (codes.astype(np.int64) - 8).T) * 2.0**-7
     y2 = run_qmatmul(syn.pack_codes(codes), s2, b2, syn.bf16_bits(xi), stream)
-    np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)), err_msg="exact split-k group-step")
+    check = np.unique(np.concatenate([rows, np.arange(m - 16, m)]))
+    exact = (xi[check].astype(np.float64) @ (codes.astype(np.float64) - 8).T) * 2.0**-7   # integers < 2^17: exact
+    np.testing.assert_array_equal(y2[check], syn.bf16_bits(exact.astype(np.float32)), err_msg="exact split-k group-step")
 
 
 # ---------------------------------------------------------------- fused epilogues
