@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     constexpr uint32_t kRowsPerPass = kThreads / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
     const uint32_t col0 = n0 + ch * 8u;
-    if ((sv.n & 7u) == 0u) {
+    if ((sv.n & 7u) == 0u && (reinterpret_cast<uintptr_t>(sv.y) & 15u) == 0u) {
         for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
             const uint32_t row = m0 + r;
             if (row < p.m && col0 < sv.n)
@@ -630,7 +630,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     constexpr uint32_t kRowsPerPass = 64u * W / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
     const uint32_t col0 = n0 + ch * 8u;
-    if ((sv.n & 7u) == 0u) {
+    if ((sv.n & 7u) == 0u && (reinterpret_cast<uintptr_t>(sv.y) & 15u) == 0u) {
         for (uint32_t r = threadIdx.x / kChunks; r < BM; r += kRowsPerPass) {
             const uint32_t row = m0 + r;
             if (row < p.m && col0 < sv.n)
@@ -653,6 +653,36 @@ template <int MT, int NT, int W>
 constexpr size_t g_lds_bytes() {
     return 2u * 16u * MT * kGRowBytes > 16u * MT * (32u * NT * W + 32u) ? 2u * 16u * MT * kGRowBytes
                                                                          : 16u * MT * (32u * NT * W + 32u);
+}
+
+// The same with 8 consecutive workspace columns per thread (two 16-byte loads per split,
+// one 16-byte store), for grids where every segment's width and first column are
+// multiples of 8 and its output is 16-byte aligned (so 8 columns never straddle two
+// segments and each output row segment is 16-byte aligned).
+__global__ __launch_bounds__(kThreads) void q4_splitk_reduce8_kernel(GemmParams p) {
+    const uint64_t e = (static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x) * 8u;
+    const uint64_t total = static_cast<uint64_t>(p.m) * p.n_total;
+    if (e >= total) return;
+    const uint32_t row = static_cast<uint32_t>(e / p.n_total);
+    const uint32_t c = static_cast<uint32_t>(e - static_cast<uint64_t>(row) * p.n_total);
+    f32x4_t lo = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4_t hi = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t z = 0; z < p.ksplit; ++z) {
+        const f32x4_t* src = reinterpret_cast<const f32x4_t*>(p.partial + z * total + e);
+        lo += src[0];
+        hi += src[1];
+    }
+    const bool in1 = p.nseg > 1u && c >= p.seg[1].col_begin;
+    const bool in2 = p.nseg > 2u && c >= p.seg[2].col_begin;
+    uint16_t* y = in2 ? p.seg[2].y : (in1 ? p.seg[1].y : p.seg[0].y);
+    const uint32_t n = in2 ? p.seg[2].n : (in1 ? p.seg[1].n : p.seg[0].n);
+    const uint32_t c0 = in2 ? p.seg[2].col_begin : (in1 ? p.seg[1].col_begin : 0u);
+    uint4 out;
+    out.x = pack_bf16x2(lo[0], lo[1]);
+    out.y = pack_bf16x2(lo[2], lo[3]);
+    out.z = pack_bf16x2(hi[0], hi[1]);
+    out.w = pack_bf16x2(hi[2], hi[3]);
+    *reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * n + (c - c0)) = out;
 }
 
 // y_seg[row][col] = bf16(sum over splits z = 0, 1, ... of partial[z][row][col_begin + col]),
@@ -854,9 +884,15 @@ void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t
     p.partial = static_cast<float*>(ws);
     try {
         launch_params(p, kernel, stream);
-        const uint64_t blocks = (elems + kThreads - 1u) / kThreads;
+        bool vec = true;
+        for (uint32_t i = 0; i < p.nseg; ++i)
+            vec = vec && p.seg[i].n % 8u == 0u && p.seg[i].col_begin % 8u == 0u &&
+                  (reinterpret_cast<uintptr_t>(p.seg[i].y) & 15u) == 0u;
+        const uint64_t per_thread = vec ? 8u : 1u;
+        const uint64_t blocks = (elems / per_thread + kThreads - 1u) / kThreads;
         HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
-        hipLaunchKernelGGL(q4_splitk_reduce_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL(vec ? q4_splitk_reduce8_kernel : q4_splitk_reduce_kernel, dim3(static_cast<uint32_t>(blocks)),
+                           dim3(kThreads), 0, stream, p);
         HYP_HIP_CHECK(hipGetLastError());
     } catch (...) {
         (void)hipFreeAsync(ws, stream);

@@ -400,13 +400,14 @@ def test_gemm_group_step_tiles(stream, n, k):
     np.testing.assert_array_equal(y2, syn.bf16_bits(exact.astype(np.float32)), err_msg=f"exact n={n} k={k}")
 
 
-@pytest.mark.parametrize("m,n,splits", [(1300, 6000, 1), (700, 3000, 4)])
+@pytest.mark.parametrize("m,n,splits", [(1300, 6000, 1), (700, 2999, 4)])
 def test_gemm_group_step_128_rows(stream, m, n, splits):
     """Mid-size grids select the 128 x 256 group-step kernel, unsplit (11 x 24 tiles) or
-    with 4 k splits (6 x 12 tiles): ragged m (the last 128-row tile part-empty), n not a
-    multiple of 256, an odd group count (k = 4160: 65 groups, so the last pair is half
-    empty). Sampled rows against the fp64 product with the kernel's bf16 weights, and
-    exact integer inputs on sampled rows including the last row tile."""
+    with 4 k splits (6 x 12 tiles; n = 2999 is odd, so the split sums take the
+    element-wise reduction): ragged m (the last 128-row tile part-empty), n not a multiple
+    of 256, an odd group count (k = 4160: 65 groups, so the last pair is half empty).
+    Sampled rows against the fp64 product with the kernel's bf16 weights, and exact
+    integer inputs on sampled rows including the last row tile."""
     k = 4160
     say(f"gemm group-step 128 rows m={m} n={n} k={k} (splits {splits})")
     x = syn.activations(m, k, seed=1700 + m)
@@ -424,6 +425,27 @@ def test_gemm_group_step_128_rows(stream, m, n, splits):
     check = np.unique(np.concatenate([rows, np.arange(m - 20, m)]))
     exact = (xi[check].astype(np.float64) @ (codes.astype(np.float64) - 8).T) * 2.0**-7
     np.testing.assert_array_equal(y2[check], syn.bf16_bits(exact.astype(np.float32)), err_msg=f"exact m={m} n={n}")
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 40, 128), (300, 200, 4096)])
+def test_gemm_output_not_16_byte_aligned(stream, m, n, k):
+    """y one element past a 16-byte boundary: the 16-byte store paths (the tile epilogue,
+    and the 8-column split-k reduction for the 4-split 300 x 200 x 4096 call) fall back
+    to element stores; results equal the aligned call's bit for bit."""
+    import ctypes
+    say(f"gemm unaligned y m={m} n={n} k={k}")
+    x = syn.activations(m, k, seed=1800 + k)
+    w, s, b = syn.q4_weights(n, k, seed=1801 + n)
+    ref = run_qmatmul(w, s, b, x, stream)
+    qw = hy.QWeight.from_host(w, s, b)
+    xd = dev(x, stream)
+    yd = hy.DeviceArray((m * n + 8,), np.uint16)
+    yd.fill_zero(stream)
+    hy.call("hyp_qmatmul", qw.handle, xd.ptr, m, ctypes.c_void_p(yd.ptr.value + 2), stream.handle)
+    got = yd.to_host(stream)
+    assert got[0] == 0 and np.all(got[1 + m * n:] == 0)
+    np.testing.assert_array_equal(got[1:1 + m * n].reshape(m, n), ref)
+    qw.close()
 
 
 def test_gemm_group_step_split_k(stream):
