@@ -303,8 +303,11 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     const uint32_t k = p.k;
     const uint32_t W = k / 8u;    // packed words per row
     const uint32_t G = k / 64u;   // groups per row
-    uint4* xs = smem;                                              // [M][W] permuted x
-    float4* sx = reinterpret_cast<float4*>(smem + M * W);          // [G] group sums of x rows 0..3
+    // x rows in LDS are W + 1 chunks apart: W is a multiple of 16 chunks (256 bytes, all 64
+    // banks), so unpadded the m rows an A read touches would all start on the same bank.
+    const uint32_t WS = W + 1u;
+    uint4* xs = smem;                                              // [M][WS] permuted x
+    float4* sx = reinterpret_cast<float4*>(smem + M * WS);         // [G] group sums of x rows 0..3
     float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][NW][M][16]
     uint32_t* ctr = reinterpret_cast<uint32_t*>(red + NWAVE * NW * M * kTileRows);   // [4]
     float* part = reinterpret_cast<float*>(ctr + 4);               // NORM: [M][G] unit partials, [M] inverses
@@ -433,7 +436,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
                 o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
                 o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
                 o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
-                xs[m * W + g * 8u + t] = o;
+                xs[m * WS + g * 8u + t] = o;
                 s0 = dot2_bf16(xv[t].x, kOnePair, s0);
                 s1 = dot2_bf16(xv[t].y, kOnePair, s1);
                 s0 = dot2_bf16(xv[t].z, kOnePair, s0);
@@ -451,7 +454,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     asm volatile("" : "+v"(mask), "+v"(bits));
 
     const uint32_t arow = min(j, static_cast<uint32_t>(M - 1));   // A row this lane supplies
-    const uint4* xa = xs + arow * W + kb * 2u;
+    const uint4* xa = xs + arow * WS + kb * 2u;
 
     float y[NW][M];
 #pragma unroll
@@ -531,7 +534,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool norm = false) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    return m * W * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u + 16u +
+    return m * (W + 1u) * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u + 16u +
            (norm ? (m * G + m) * 4u : 0u);
 }
 
