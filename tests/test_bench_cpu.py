@@ -1,0 +1,48 @@
+"""bench.py and the entry points on the CPU: the contract pieces that need no GPU."""
+import importlib
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bench():
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    return importlib.import_module("bench")
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr or "single" in r.stderr
+    assert r.stdout == ""
+
+
+def test_algorithmic_work_matches_the_workload_definitions():
+    b = _bench()
+    # decode GEMV [1,3840] x [15360,3840]: nibbles + bf16 scale/bias per 64 + x + y
+    assert b.q4_bytes(15360, 3840) == 29_491_200 + 3_686_400
+    assert b.gemv_bytes(1, 15360, 3840) == 33_216_000
+    # quantize/pack [15360,3840]: bf16 read + Q4 written
+    assert 2 * 15360 * 3840 + b.q4_bytes(15360, 3840) == 151_142_400
+    # prefill: 2 M sum(n k) over the seven projections of a layer
+    from hyperion_amd import synthetic as syn
+    nk = sum(n * k for n, k in syn.LAYER_SHAPES.values())
+    assert nk == 224_133_120                     # weights per layer
+    assert 2 * 2048 * nk == 918_049_259_520      # 9.180e11 flop at M = 2048
+    assert 2 * 512 * nk == 229_512_314_880       # 2.295e11 flop at M = 512
+
+
+def test_roofline_traffic_comes_from_the_committed_counter_summary():
+    b = _bench()
+    assert b.measured_traffic() == 33_388_692
+
+
+def test_entry_points_exist():
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    g = importlib.import_module("__graft_entry__")
+    assert callable(g.build) and callable(g.smoke)
