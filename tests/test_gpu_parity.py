@@ -591,6 +591,18 @@ def test_sample_greedy_matches_oracle(stream, vocab):
         _assert_samples_equal(got[r], O.sample_greedy(v[r + 1]), f"vocab={vocab} offset row={r + 1}")
 
 
+def test_sample_greedy_many_rows(stream):
+    """130 rows run as three passes over the stream's 64-row workspace; every row equals
+    the oracle's scan."""
+    rng = np.random.default_rng(130)
+    rows, vocab = 130, 4104
+    say(f"sample_greedy rows={rows} vocab={vocab}")
+    v = _planted_logits(rng, rows, vocab)
+    got = _sample_rows(v, stream, rows, vocab)
+    for r in range(rows):
+        _assert_samples_equal(got[r], O.sample_greedy(v[r]), f"row={r}")
+
+
 def test_sample_greedy_degenerate_rows(stream):
     """All -inf, all NaN and vocab = 0 rows give token 0 with logit -inf and no near tie
     (the reference's initial values survive the scan); rows = 0 is a no-op."""
