@@ -457,13 +457,20 @@ __device__ __forceinline__ void g_mfma_part(const bf16x8_t (&a)[MT / P], const b
     }
 }
 
+// Groups between barriers of the group-step kernel: its X ring holds 2 of them stages of
+// 16 MT rows x 128 B (128 KB for both tile heights).
+template <int MT>
+constexpr uint32_t g_sync_groups() { return MT >= 16 ? 2u : 4u; }
+
 template <int MT, int NT, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_g_kernel(GemmParams p) {
     constexpr uint32_t BM = 16u * MT;
     constexpr uint32_t kStage = BM * kGRowBytes;
+    constexpr uint32_t kSync = g_sync_groups<MT>();   // groups per barrier; X ring of 2 kSync stages
+    constexpr uint32_t kRing = 2u * kSync - 1u;
     constexpr int kXLoads = static_cast<int>(BM / 8u / W);   // 1 KB (8 rows) direct loads per wave
     static_assert(kXLoads % 2 == 0, "swizzle period");
-    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];   // [2][BM][128 B], reused by the epilogue
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];   // [2 kSync][BM][128 B], reused by the epilogue
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
@@ -529,7 +536,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     GRaw<NT> r[3];
-    load_x(g0, xs);
+#pragma unroll
+    for (uint32_t i = 0; i < kSync; ++i) load_x(min(g0 + i, g1 - 1u), xs + i * kStage);
     load_graw<NT>(cr, sr, c_off, s_off, g0, r[0]);
     load_graw<NT>(cr, sr, c_off, s_off, min(g0 + 1u, g1 - 1u), r[1]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -544,15 +552,22 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // of groups g, g + 1 are in r[s], r[(s + 1) % 3] and those of g + 2 load into
     // r[(s + 2) % 3] (s = (g - g0) % 3, unrolled, so no register copies wait on loads in
     // flight). Past the last group the loads repeat the last group (unused).
+    //
+    // X of group g sits in ring stage (g - g0) % (2 kSync) and is loaded kSync groups ahead;
+    // a barrier ends every kSync-th group. Any kSync consecutive groups hold one barrier,
+    // so a stage is complete and visible (its wave's vmcnt wait, then the barrier) before
+    // its group starts, and every wave has left group g before stage (g - g0) % (2 kSync)
+    // is loaded again for group g + 2 kSync. Fewer barriers let the waves drift apart and
+    // overlap each other's MFMA and dequantization work.
     constexpr int kParts = 4;
     static_assert(NT <= kParts, "one column tile's dequantization per unit");
     constexpr int kValu = (26 + MT / kParts * NT - 1) / (MT / kParts * NT);   // one tile's dequantization per MFMA
     bf16x8_t a[2][MT / kParts];
     g_read_a<MT, kParts, 0, 0>(xs, lane, a[0]);
-    auto group = [&](auto slot, uint32_t g) {
+    auto group = [&](auto slot, auto sync, uint32_t g) {
         constexpr int s = decltype(slot)::value;
-        const uint8_t* xb = xs + ((g - g0) & 1u) * kStage;
-        load_x(min(g + 1u, g1 - 1u), xs + ((g - g0 + 1u) & 1u) * kStage);
+        const uint8_t* xb = xs + ((g - g0) & kRing) * kStage;
+        load_x(min(g + kSync, g1 - 1u), xs + ((g - g0 + kSync) & kRing) * kStage);
         __builtin_amdgcn_sched_barrier(0);   // the raw loads below issue after the X loads
         load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, g1 - 1u), r[(s + 2) % 3]);
         static_for(
@@ -574,19 +589,31 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             },
             std::make_integer_sequence<int, 2 * kParts>{});
         __builtin_amdgcn_sched_barrier(0);
-        // The next X stage has landed once at most this group's 2 NT raw loads remain.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NT) : "memory");
-        __syncthreads();
-        g_read_a<MT, kParts, 0, 0>(xs + ((g - g0 + 1u) & 1u) * kStage, lane, a[0]);
+        if constexpr (decltype(sync)::value) {
+            // The X stages of the next two groups have landed once at most this group's
+            // 2 NT raw loads remain.
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NT) : "memory");
+            __syncthreads();
+        }
+        g_read_a<MT, kParts, 0, 0>(xs + ((g - g0 + 1u) & kRing) * kStage, lane, a[0]);
+    };
+    // Unrolled by 3 kSync groups, so the raw-weight slot and the barrier are compile-time.
+    constexpr int kUnroll = 3 * static_cast<int>(kSync);
+    auto step = [&](auto jc, uint32_t gj) {
+        constexpr int j = decltype(jc)::value;
+        group(std::integral_constant<int, j % 3>{},
+              std::integral_constant<bool, j % static_cast<int>(kSync) == static_cast<int>(kSync) - 1>{}, gj);
     };
     uint32_t g = g0;
-    for (; g + 3u <= g1; g += 3u) {
-        group(std::integral_constant<int, 0>{}, g);
-        group(std::integral_constant<int, 1>{}, g + 1u);
-        group(std::integral_constant<int, 2>{}, g + 2u);
-    }
-    if (g < g1) group(std::integral_constant<int, 0>{}, g);
-    if (g + 1u < g1) group(std::integral_constant<int, 1>{}, g + 1u);
+    for (; g + kUnroll <= g1; g += kUnroll)
+        static_for([&](auto jc) { step(jc, g + decltype(jc)::value); }, std::make_integer_sequence<int, kUnroll>{});
+    static_for(
+        [&](auto jc) {
+            if (g + decltype(jc)::value < g1) step(jc, g + decltype(jc)::value);
+        },
+        std::make_integer_sequence<int, kUnroll - 1>{});
+    // X loads of the last groups may still be in flight; they write LDS the epilogue reuses.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (p.ksplit > 1u) {
         // Split k: fp32 partials, summed by q4_splitk_reduce_kernel.
@@ -651,8 +678,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
 template <int MT, int NT, int W>
 constexpr size_t g_lds_bytes() {
-    return 2u * 16u * MT * kGRowBytes > 16u * MT * (32u * NT * W + 32u) ? 2u * 16u * MT * kGRowBytes
-                                                                         : 16u * MT * (32u * NT * W + 32u);
+    return 2u * g_sync_groups<MT>() * 16u * MT * kGRowBytes > 16u * MT * (32u * NT * W + 32u)
+               ? 2u * g_sync_groups<MT>() * 16u * MT * kGRowBytes
+               : 16u * MT * (32u * NT * W + 32u);
 }
 
 // The same with 8 consecutive workspace columns per thread (two 16-byte loads per split,
