@@ -13,7 +13,8 @@
 //    i >= m read a copy of x row m-1; their outputs are never stored).
 //  * A packed word (8 codes, lowest k in the lowest nibble) becomes a lane's 8 bf16
 //    B values with 3 shifts and 4 v_and_or_b32: (w >> 4s) & 0x000F000F | 0x43004300
-//    is the bf16 pair (128 + q_s, 128 + q_{s+4}) exactly (bf16 128.0 has ulp 1).
+//    is the bf16 pair (128 + q_s, 128 + q_{s+4}) exactly (bf16 128.0 has ulp 1). For
+//    one matrix, two adjacent words share each shift as one 64-bit shift.
 //    The A values use the same slot order: x is staged in LDS once per workgroup as
 //    (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8-element word, next to the per-group sums
 //    of x that remove the +128 offset.
@@ -79,6 +80,45 @@ __device__ __forceinline__ bf16x8_t code_frag(uint32_t w, uint32_t mask, uint32_
     r.z = and_or(w >> 8, mask, bits);
     r.w = and_or(w >> 12, mask, bits);
     return __builtin_bit_cast(bf16x8_t, r);
+}
+
+// code_frag of two adjacent words (lo, hi) with one 64-bit shift per step instead of a
+// 32-bit shift per word (v_lshrrev_b64 runs at full rate on gfx950): the bits of hi that
+// the shift moves into lo's top (bits 20..31 at most) lie outside the mask.
+__device__ __forceinline__ void code_frag2(uint32_t lo, uint32_t hi, uint32_t mask, uint32_t bits, bf16x8_t& f_lo,
+                                           bf16x8_t& f_hi) {
+    const uint64_t v = (static_cast<uint64_t>(hi) << 32) | lo;
+    uint64_t s4, s8, s12;
+    // As plain C++ the compiler narrows each shift back to two 32-bit ones.
+    asm("v_lshrrev_b64 %0, 4, %1" : "=v"(s4) : "v"(v));
+    asm("v_lshrrev_b64 %0, 8, %1" : "=v"(s8) : "v"(v));
+    asm("v_lshrrev_b64 %0, 12, %1" : "=v"(s12) : "v"(v));
+    uint4 a, b;
+    a.x = and_or(lo, mask, bits);
+    a.y = and_or(static_cast<uint32_t>(s4), mask, bits);
+    a.z = and_or(static_cast<uint32_t>(s8), mask, bits);
+    a.w = and_or(static_cast<uint32_t>(s12), mask, bits);
+    b.x = and_or(hi, mask, bits);
+    b.y = and_or(static_cast<uint32_t>(s4 >> 32), mask, bits);
+    b.z = and_or(static_cast<uint32_t>(s8 >> 32), mask, bits);
+    b.w = and_or(static_cast<uint32_t>(s12 >> 32), mask, bits);
+    f_lo = __builtin_bit_cast(bf16x8_t, a);
+    f_hi = __builtin_bit_cast(bf16x8_t, b);
+}
+
+// The four B fragments of one pair's words: 64-bit shifts for a single matrix; the
+// two-matrix (gate/up) form keeps 32-bit shifts, which measured faster there.
+template <int NW>
+__device__ __forceinline__ void pair_frags(const uint4& w, uint32_t mask, uint32_t bits, bf16x8_t (&b)[4]) {
+    if constexpr (NW == 1) {
+        code_frag2(w.x, w.y, mask, bits, b[0], b[1]);
+        code_frag2(w.z, w.w, mask, bits, b[2], b[3]);
+    } else {
+        b[0] = code_frag(w.x, mask, bits);
+        b[1] = code_frag(w.y, mask, bits);
+        b[2] = code_frag(w.z, mask, bits);
+        b[3] = code_frag(w.w, mask, bits);
+    }
 }
 
 // 128-bit buffer resource over [base, base + bytes).
@@ -197,10 +237,7 @@ __device__ __forceinline__ void load_operands(const Batch<P> (&bt)[NW], int i, c
                                               uint32_t G, uint32_t mask, uint32_t bits, PairOperands<NW>& op) {
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-        op.b[q][0] = code_frag(bt[q].w[i].x, mask, bits);
-        op.b[q][1] = code_frag(bt[q].w[i].y, mask, bits);
-        op.b[q][2] = code_frag(bt[q].w[i].z, mask, bits);
-        op.b[q][3] = code_frag(bt[q].w[i].w, mask, bits);
+        pair_frags<NW>(bt[q].w[i], mask, bits, op.b[q]);
     }
     const uint32_t g1 = min(g0 + 1u, G - 1u);   // an odd group count leaves the last pair half empty
     op.a[0] = xa[g0 * 8u];
@@ -271,10 +308,12 @@ __device__ __forceinline__ void compute_pair(const uint4 (&w)[NW], const uint2 (
     f32x4_t acc0[NW], acc1[NW];
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-        acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, code_frag(w[q].x, mask, bits), zero, 0, 0, 0);
-        acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, code_frag(w[q].z, mask, bits), zero, 0, 0, 0);
-        acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, code_frag(w[q].y, mask, bits), acc0[q], 0, 0, 0);
-        acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, code_frag(w[q].w, mask, bits), acc1[q], 0, 0, 0);
+        bf16x8_t b[4];
+        pair_frags<NW>(w[q], mask, bits, b);
+        acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[0], zero, 0, 0, 0);
+        acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[2], zero, 0, 0, 0);
+        acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[1], acc0[q], 0, 0, 0);
+        acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[3], acc1[q], 0, 0, 0);
     }
     const float4 sx0 = sx[g0];
 #pragma unroll
