@@ -15,6 +15,10 @@
 //    B values with 3 shifts and 4 v_and_or_b32: (w >> 4s) & 0x000F000F | 0x43004300
 //    is the bf16 pair (128 + q_s, 128 + q_{s+4}) exactly (bf16 128.0 has ulp 1). For
 //    one matrix, two adjacent words share each shift as one 64-bit shift.
+//  * m = 1, one matrix, whole range in flight: the scale and bias are applied once per
+//    lane for four groups instead of per group, because each 4-row block of the MFMA
+//    output accumulates one group of every two pairs (its A rows read x in that group's
+//    MFMAs and a zero row in the others); the four blocks are added across lanes at the end.
 //    The A values use the same slot order: x is staged in LDS once per workgroup as
 //    (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8-element word, next to the per-group sums
 //    of x that remove the +128 offset.
@@ -172,15 +176,16 @@ constexpr int kStreamPolicy = 2;
 
 // Pairs first, first + 1, ... (wave-uniform, so the clamp is a scalar op); indices past
 // `last` are clamped to it, so every byte read lies inside the tile.
-template <int P>
+template <int P, bool SB = true>
 __device__ __forceinline__ void load_batch(const LaneMatrix& lm, uint32_t first, uint32_t last, Batch<P>& bt) {
 #pragma unroll
     for (int i = 0; i < P; ++i) {
         const uint32_t gp = min(first + i, last);
         bt.w[i] = __builtin_bit_cast(
             uint4, __builtin_amdgcn_raw_buffer_load_b128(lm.codes, lm.c_off, gp * 1024u, kStreamPolicy));
-        bt.sb[i] = __builtin_bit_cast(
-            uint2, __builtin_amdgcn_raw_buffer_load_b64(lm.sb, lm.sb_off, gp * 128u, kStreamPolicy));
+        if constexpr (SB)
+            bt.sb[i] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(lm.sb, lm.sb_off, gp * 128u, kStreamPolicy));
     }
 }
 
@@ -345,8 +350,12 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     // x rows in LDS are W + 1 chunks apart: W is a multiple of 16 chunks (256 bytes, all 64
     // banks), so unpadded the m rows an A read touches would all start on the same bank.
     const uint32_t WS = W + 1u;
+    // One row, one matrix, whole range in flight: lane blocks take one group each (below).
+    constexpr bool kZeroRow = M == 1 && !DUAL;   // as skinny_lds_bytes allocates
+    constexpr bool kLaneGroups = kZeroRow && !LOOP;
     uint4* xs = smem;                                              // [M][WS] permuted x
-    float4* sx = reinterpret_cast<float4*>(smem + M * WS);         // [G] group sums of x rows 0..3
+    uint4* zs = smem + M * WS;                                     // kZeroRow: [WS] zeros
+    float4* sx = reinterpret_cast<float4*>(zs + (kZeroRow ? WS : 0u));   // [G] group sums of x rows 0..3
     float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][NW][M][16]
     uint32_t* ctr = reinterpret_cast<uint32_t*>(red + NWAVE * NW * M * kTileRows);   // [4]
     float* part = reinterpret_cast<float*>(ctr + 4);               // NORM: [M][G] unit partials, [M] inverses
@@ -412,6 +421,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
         for (int t = 0; t < 8; ++t) xv[t] = src[t];
     }
     if (threadIdx.x < 4u) ctr[threadIdx.x] = 0u;
+    if constexpr (kLaneGroups)
+        for (uint32_t t = threadIdx.x; t < WS; t += kThreads) zs[t] = uint4{0u, 0u, 0u, 0u};
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
     __builtin_amdgcn_s_barrier();         // no memory wait: only orders the issue
 
@@ -429,9 +440,20 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     // Two batches of weights in flight before the first arithmetic.
     Batch<P> ba[NW], bb[NW];
 #pragma unroll
-    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], first, last, ba[q]);
+    for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first, last, ba[q]);
 #pragma unroll
-    for (int q = 0; q < NW; ++q) load_batch<P>(lm[q], first + P, last, bb[q]);
+    for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
+    // kLaneGroups: lane block ob = lane / 16 scales group 2 (first + 2 b) + ob of each two
+    // pairs b: one dword of scale and bias per lane and block (past the wave's range the
+    // load reads a neighbour's, or zeros past the buffer; such lanes are masked).
+    const uint32_t ob = lane >> 4;
+    uint32_t sbl[P];
+    if constexpr (kLaneGroups) {
+        const uint32_t off = (ltile * pairs * 16u + (ob >> 1) * 16u + j) * 8u + (ob & 1u) * 4u;
+#pragma unroll
+        for (int b = 0; b < P; ++b)
+            sbl[b] = __builtin_amdgcn_raw_buffer_load_b32(lm[0].sb, off, (first + 2u * b) * 128u, kStreamPolicy);
+    }
 
     if (stager) {
         if constexpr (NORM) {
@@ -501,7 +523,54 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
         for (int m = 0; m < M; ++m) y[q][m] = 0.0f;
 
-    if constexpr (!LOOP) {
+    if constexpr (kLaneGroups) {
+        // m = 1: every A row would carry x row 0, so all four 4-row blocks of an MFMA's
+        // output would hold the same sums. Instead A row block r carries x only in the MFMAs
+        // of group slot r of each two pairs (the other lanes read the zero row), so output
+        // block r accumulates group 2 (first + 2 b) + r alone, and each lane scales one group
+        // per two pairs: 5 VALU per lane where four per-group scalings take 20.
+        const uint32_t ablk = (lane & 15u) >> 2;   // A row block this lane supplies
+        const uint4* src[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) src[r] = (ablk == static_cast<uint32_t>(r) ? xs : zs) + kb * 2u;
+        const float* sxl = reinterpret_cast<const float*>(sx) + (2u * first + ob) * 4u;
+        const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t acc0, acc1;
+#pragma unroll
+        for (int i = 0; i < 2 * P; ++i) {
+            if (static_cast<uint32_t>(i) >= cnt) break;   // wave-uniform
+            const uint4 w = i < P ? ba[0].w[i % P] : bb[0].w[i % P];
+            const uint32_t g0 = 2u * (first + i);
+            const uint32_t g1 = min(g0 + 1u, G - 1u);   // an odd group count leaves the last pair half empty
+            const uint4* pa = src[2 * (i & 1)];
+            const uint4* pb = src[2 * (i & 1) + 1];
+            bf16x8_t b[4];
+            pair_frags<1>(w, mask, bits, b);
+            // The first pair of two starts fresh chains (a literal zero accumulator).
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pa[g0 * 8u]), b[0],
+                                                           (i & 1) == 0 ? zero : acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pb[g1 * 8u]), b[2],
+                                                           (i & 1) == 0 ? zero : acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pa[g0 * 8u + 1u]), b[1], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pb[g1 * 8u + 1u]), b[3], acc1, 0, 0, 0);
+            if ((i & 1) == 1 || static_cast<uint32_t>(i) + 1u >= cnt) {
+                // Two pairs done: acc0 holds blocks 0 and 2 (zero rows elsewhere), acc1 1 and 3.
+                const int bi = i >> 1;
+                const uint32_t g = 2u * (first + 2u * bi) + ob;
+                const bool valid = 2u * bi + (ob >> 1) < cnt && g < G;
+                const float t = acc0[0] + acc1[0];
+                const float sxv = sxl[bi * 16];
+                const float sc = bf16_bits_to_f32(sbl[bi] & 0xFFFFu);
+                const float bs = bf16_bits_to_f32(sbl[bi] >> 16);
+                float yn = fmaf(sc, fmaf(-128.0f, sxv, t), y[0][0]);
+                yn = fmaf(bs, sxv, yn);
+                y[0][0] = valid ? yn : y[0][0];
+            }
+        }
+        // Blocks 0..3 hold the sums over disjoint groups: add lanes j, j + 16, j + 32, j + 48.
+        y[0][0] += __shfl_xor(y[0][0], 16, 64);
+        y[0][0] += __shfl_xor(y[0][0], 32, 64);
+    } else if constexpr (!LOOP) {
         // The whole range is in flight (cnt <= 2P): straight-line code, so each pair waits
         // only for its own loads (a loop waits for the loads of every iteration).
 #pragma unroll
@@ -573,8 +642,9 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool norm = false) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    return m * (W + 1u) * 16u + G * 16u + static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u + 16u +
-           (norm ? (m * G + m) * 4u : 0u);
+    // m = 1 single-matrix kernels keep a zero row beside x (their straight-line form uses it).
+    return (m + (m == 1u && !dual ? 1u : 0u)) * (W + 1u) * 16u + G * 16u +
+           static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u + 16u + (norm ? (m * G + m) * 4u : 0u);
 }
 
 size_t max_lds_per_block();
