@@ -15,10 +15,10 @@
 //    B values with 3 shifts and 4 v_and_or_b32: (w >> 4s) & 0x000F000F | 0x43004300
 //    is the bf16 pair (128 + q_s, 128 + q_{s+4}) exactly (bf16 128.0 has ulp 1). For
 //    one matrix, two adjacent words share each shift as one 64-bit shift.
-//  * m = 1, one matrix, whole range in flight: the scale and bias are applied once per
-//    lane for four groups instead of per group, because each 4-row block of the MFMA
-//    output accumulates one group of every two pairs (its A rows read x in that group's
-//    MFMAs and a zero row in the others); the four blocks are added across lanes at the end.
+//  * One matrix, whole range in flight: the scale and bias are applied once per lane for
+//    four groups instead of per group, because each 4-row block of the MFMA output
+//    accumulates the m rows of one group of every two pairs (its A rows read x in that
+//    group's MFMAs and a zero row in the others); the blocks are added across lanes at the end.
 //    The A values use the same slot order: x is staged in LDS once per workgroup as
 //    (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8-element word, next to the per-group sums
 //    of x that remove the +128 offset.
@@ -123,6 +123,23 @@ __device__ __forceinline__ void pair_frags(const uint4& w, uint32_t mask, uint32
         b[2] = code_frag(w.z, mask, bits);
         b[3] = code_frag(w.w, mask, bits);
     }
+}
+
+// v + the values of lanes l ^ 16, l ^ 32 and l ^ 48, in the same order on all four lanes.
+// With v in both operands, v_permlane32_swap leaves each lane's own value in one register
+// and the value of lane l ^ 32 in the other (v_permlane16_swap likewise for l ^ 16): two
+// VALU swaps instead of LDS permutes. Inline assembly, because the builtins, given equal
+// inputs, compiled to an add of one output register to itself. The s_nop gives the two
+// wait states a permlane swap needs after a VALU write of its operands.
+__device__ __forceinline__ float sum_lane_blocks(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    uint32_t c = u;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(c));
+    v = __builtin_bit_cast(float, u) + __builtin_bit_cast(float, c);
+    u = __builtin_bit_cast(uint32_t, v);
+    c = u;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(u), "+v"(c));
+    return __builtin_bit_cast(float, u) + __builtin_bit_cast(float, c);
 }
 
 // 128-bit buffer resource over [base, base + bytes).
@@ -350,8 +367,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     // x rows in LDS are W + 1 chunks apart: W is a multiple of 16 chunks (256 bytes, all 64
     // banks), so unpadded the m rows an A read touches would all start on the same bank.
     const uint32_t WS = W + 1u;
-    // One row, one matrix, whole range in flight: lane blocks take one group each (below).
-    constexpr bool kZeroRow = M == 1 && !DUAL;   // as skinny_lds_bytes allocates
+    // One matrix, whole range in flight: lane blocks take one group each (below).
+    constexpr bool kZeroRow = !DUAL;   // as skinny_lds_bytes allocates
     constexpr bool kLaneGroups = kZeroRow && !LOOP;
     uint4* xs = smem;                                              // [M][WS] permuted x
     uint4* zs = smem + M * WS;                                     // kZeroRow: [WS] zeros
@@ -524,16 +541,18 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
         for (int m = 0; m < M; ++m) y[q][m] = 0.0f;
 
     if constexpr (kLaneGroups) {
-        // m = 1: every A row would carry x row 0, so all four 4-row blocks of an MFMA's
-        // output would hold the same sums. Instead A row block r carries x only in the MFMAs
-        // of group slot r of each two pairs (the other lanes read the zero row), so output
-        // block r accumulates group 2 (first + 2 b) + r alone, and each lane scales one group
-        // per two pairs: 5 VALU per lane where four per-group scalings take 20.
+        // m <= 4 rows of x fill only A rows 0..m-1 (the rest repeat row m-1), so output
+        // blocks 1..3 (rows 4..15) would carry no new sums. Instead A row block r holds the
+        // m rows only in the MFMAs of group slot r of each two pairs (the other lanes read
+        // the zero row), so output block r accumulates rows 0..m-1 of group
+        // 2 (first + 2 b) + r alone, and each lane scales one group per two pairs: 2 + 4 m
+        // VALU per lane where four per-group scalings take 4 (2 + 3 m).
         const uint32_t ablk = (lane & 15u) >> 2;   // A row block this lane supplies
+        const uint32_t brow = min(lane & 3u, static_cast<uint32_t>(M - 1));   // its x row
         const uint4* src[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) src[r] = (ablk == static_cast<uint32_t>(r) ? xs : zs) + kb * 2u;
-        const float* sxl = reinterpret_cast<const float*>(sx) + (2u * first + ob) * 4u;
+        for (int r = 0; r < 4; ++r) src[r] = (ablk == static_cast<uint32_t>(r) ? xs + brow * WS : zs) + kb * 2u;
+        const float4* sxl = sx + 2u * first + ob;
         const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
         f32x4_t acc0, acc1;
 #pragma unroll
@@ -558,18 +577,22 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
                 const int bi = i >> 1;
                 const uint32_t g = 2u * (first + 2u * bi) + ob;
                 const bool valid = 2u * bi + (ob >> 1) < cnt && g < G;
-                const float t = acc0[0] + acc1[0];
-                const float sxv = sxl[bi * 16];
+                const float4 sx4 = sxl[bi * 4];
+                const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
                 const float sc = bf16_bits_to_f32(sbl[bi] & 0xFFFFu);
                 const float bs = bf16_bits_to_f32(sbl[bi] >> 16);
-                float yn = fmaf(sc, fmaf(-128.0f, sxv, t), y[0][0]);
-                yn = fmaf(bs, sxv, yn);
-                y[0][0] = valid ? yn : y[0][0];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float t = acc0[m] + acc1[m];
+                    float yn = fmaf(sc, fmaf(-128.0f, sxv[m], t), y[0][m]);
+                    yn = fmaf(bs, sxv[m], yn);
+                    y[0][m] = valid ? yn : y[0][m];
+                }
             }
         }
         // Blocks 0..3 hold the sums over disjoint groups: add lanes j, j + 16, j + 32, j + 48.
-        y[0][0] += __shfl_xor(y[0][0], 16, 64);
-        y[0][0] += __shfl_xor(y[0][0], 32, 64);
+#pragma unroll
+        for (int m = 0; m < M; ++m) y[0][m] = sum_lane_blocks(y[0][m]);
     } else if constexpr (!LOOP) {
         // The whole range is in flight (cnt <= 2P): straight-line code, so each pair waits
         // only for its own loads (a loop waits for the loads of every iteration).
@@ -642,8 +665,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool norm = false) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    // m = 1 single-matrix kernels keep a zero row beside x (their straight-line form uses it).
-    return (m + (m == 1u && !dual ? 1u : 0u)) * (W + 1u) * 16u + G * 16u +
+    // Single-matrix kernels keep a zero row beside x (their straight-line form uses it).
+    return (m + (dual ? 0u : 1u)) * (W + 1u) * 16u + G * 16u +
            static_cast<size_t>(nwave) * (dual ? 2u : 1u) * m * kTileRows * 4u + 16u + (norm ? (m * G + m) * 4u : 0u);
 }
 
@@ -733,6 +756,9 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
     //    smallest power of two that leaves every wave at most kSkinnyPairsUpFront pairs
     //    (all its loads issued at once), doubled while the grid is short of one workgroup
     //    per compute unit, up to 16: [15360,3840] 4; q/k/v grouped 8; o, q, k, down 16;
+    //    at m = 4, with the lane-group scaling, o and q run best at 8 (7.45-7.48 us against
+    //    7.89-7.95 at 16: two pairs per wave no longer cover a wave's fixed cost), down at
+    //    16 (14.45 against 16.63 us);
     //  * the softcap head (262144 rows, 4-wave workgroups, many per compute unit): 1
     //    (95 vs 100 us at m = 1, 111 vs 123 us at m = 4 with 2);
     //  * the fused gate/up (two matrices, 2-pair batches): at m = 1 the smallest split that
@@ -750,7 +776,9 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
         }
     } else {
         while (s < 16u && pairs > s * kSkinnyPairsUpFront) s *= 2u;
-        while (s < 16u && tiles * s < static_cast<uint32_t>(kSkinnyWaves) * cus * 9u / 10u && pairs >= 2u * s) s *= 2u;
+        // At m >= 2, 16 splits only where each wave keeps 4 pairs (down), else 8.
+        auto may_double = [&](uint32_t s_) { return pairs >= 2u * s_ && (m == 1u || s_ < 8u || pairs >= 64u); };
+        while (s < 16u && tiles * s < static_cast<uint32_t>(kSkinnyWaves) * cus * 9u / 10u && may_double(s)) s *= 2u;
     }
     while (s > 1u && pairs < s) s /= 2u;
     return s;
