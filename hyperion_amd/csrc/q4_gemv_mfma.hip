@@ -756,9 +756,8 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
     //    smallest power of two that leaves every wave at most kSkinnyPairsUpFront pairs
     //    (all its loads issued at once), doubled while the grid is short of one workgroup
     //    per compute unit, up to 16: [15360,3840] 4; q/k/v grouped 8; o, q, k, down 16;
-    //    at m = 4, with the lane-group scaling, o and q run best at 8 (7.45-7.48 us against
-    //    7.89-7.95 at 16: two pairs per wave no longer cover a wave's fixed cost), down at
-    //    16 (14.45 against 16.63 us);
+    //    at m = 4 o and q measured 8 and 16 within 0.4 us of each other, either way round
+    //    on different boxes;
     //  * the softcap head (262144 rows, 4-wave workgroups, many per compute unit): 1
     //    (95 vs 100 us at m = 1, 111 vs 123 us at m = 4 with 2);
     //  * the fused gate/up (two matrices, 2-pair batches): at m = 1 the smallest split that
@@ -776,9 +775,7 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
         }
     } else {
         while (s < 16u && pairs > s * kSkinnyPairsUpFront) s *= 2u;
-        // At m >= 2, 16 splits only where each wave keeps 4 pairs (down), else 8.
-        auto may_double = [&](uint32_t s_) { return pairs >= 2u * s_ && (m == 1u || s_ < 8u || pairs >= 64u); };
-        while (s < 16u && tiles * s < static_cast<uint32_t>(kSkinnyWaves) * cus * 9u / 10u && may_double(s)) s *= 2u;
+        while (s < 16u && tiles * s < static_cast<uint32_t>(kSkinnyWaves) * cus * 9u / 10u && pairs >= 2u * s) s *= 2u;
     }
     while (s > 1u && pairs < s) s /= 2u;
     return s;
