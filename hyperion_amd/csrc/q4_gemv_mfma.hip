@@ -367,7 +367,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     // x rows in LDS are W + 1 chunks apart: W is a multiple of 16 chunks (256 bytes, all 64
     // banks), so unpadded the m rows an A read touches would all start on the same bank.
     const uint32_t WS = W + 1u;
-    // One matrix, whole range in flight: lane blocks take one group each (below).
+    // Single matrix, whole range in flight: lane blocks take one group each (below). The
+    // fused gate/up form measured slower this way (15.3-15.5 against 14.5 us at m = 1).
     constexpr bool kZeroRow = !DUAL;   // as skinny_lds_bytes allocates
     constexpr bool kLaneGroups = kZeroRow && !LOOP;
     uint4* xs = smem;                                              // [M][WS] permuted x
@@ -454,23 +455,27 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
         lm[q].sb_off = (ltile * pairs * 16u + j) * 8u;
     }
 
+    // kLaneGroups: lane block ob = lane / 16 scales group 2 (first + 2 b) + ob of each two
+    // pairs b: one dword of scale and bias per lane and block (past the wave's range the
+    // load reads a neighbour's, or zeros past the buffer; such lanes are masked). They are
+    // requested before the codes: loads complete in issue order for the wait counters, so
+    // behind the codes the first scaling would wait for every code load of the wave.
+    const uint32_t ob = lane >> 4;
+    uint32_t sbl[NW][P];
+    if constexpr (kLaneGroups) {
+        const uint32_t off = (ltile * pairs * 16u + (ob >> 1) * 16u + j) * 8u + (ob & 1u) * 4u;
+#pragma unroll
+        for (int q = 0; q < NW; ++q)
+#pragma unroll
+            for (int b = 0; b < P; ++b)
+                sbl[q][b] = __builtin_amdgcn_raw_buffer_load_b32(lm[q].sb, off, (first + 2u * b) * 128u, kStreamPolicy);
+    }
     // Two batches of weights in flight before the first arithmetic.
     Batch<P> ba[NW], bb[NW];
 #pragma unroll
     for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first, last, ba[q]);
 #pragma unroll
     for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
-    // kLaneGroups: lane block ob = lane / 16 scales group 2 (first + 2 b) + ob of each two
-    // pairs b: one dword of scale and bias per lane and block (past the wave's range the
-    // load reads a neighbour's, or zeros past the buffer; such lanes are masked).
-    const uint32_t ob = lane >> 4;
-    uint32_t sbl[P];
-    if constexpr (kLaneGroups) {
-        const uint32_t off = (ltile * pairs * 16u + (ob >> 1) * 16u + j) * 8u + (ob & 1u) * 4u;
-#pragma unroll
-        for (int b = 0; b < P; ++b)
-            sbl[b] = __builtin_amdgcn_raw_buffer_load_b32(lm[0].sb, off, (first + 2u * b) * 128u, kStreamPolicy);
-    }
 
     if (stager) {
         if constexpr (NORM) {
@@ -554,24 +559,28 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
         for (int r = 0; r < 4; ++r) src[r] = (ablk == static_cast<uint32_t>(r) ? xs + brow * WS : zs) + kb * 2u;
         const float4* sxl = sx + 2u * first + ob;
         const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4_t acc0, acc1;
+        f32x4_t acc0[NW], acc1[NW];
 #pragma unroll
         for (int i = 0; i < 2 * P; ++i) {
             if (static_cast<uint32_t>(i) >= cnt) break;   // wave-uniform
-            const uint4 w = i < P ? ba[0].w[i % P] : bb[0].w[i % P];
             const uint32_t g0 = 2u * (first + i);
             const uint32_t g1 = min(g0 + 1u, G - 1u);   // an odd group count leaves the last pair half empty
             const uint4* pa = src[2 * (i & 1)];
             const uint4* pb = src[2 * (i & 1) + 1];
-            bf16x8_t b[4];
-            pair_frags<1>(w, mask, bits, b);
-            // The first pair of two starts fresh chains (a literal zero accumulator).
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pa[g0 * 8u]), b[0],
-                                                           (i & 1) == 0 ? zero : acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pb[g1 * 8u]), b[2],
-                                                           (i & 1) == 0 ? zero : acc1, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pa[g0 * 8u + 1u]), b[1], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pb[g1 * 8u + 1u]), b[3], acc1, 0, 0, 0);
+            const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, pa[g0 * 8u]);
+            const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, pa[g0 * 8u + 1u]);
+            const bf16x8_t a2 = __builtin_bit_cast(bf16x8_t, pb[g1 * 8u]);
+            const bf16x8_t a3 = __builtin_bit_cast(bf16x8_t, pb[g1 * 8u + 1u]);
+#pragma unroll
+            for (int q = 0; q < NW; ++q) {
+                bf16x8_t b[4];
+                pair_frags<NW>(i < P ? ba[q].w[i % P] : bb[q].w[i % P], mask, bits, b);
+                // The first pair of two starts fresh chains (a literal zero accumulator).
+                acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[0], (i & 1) == 0 ? zero : acc0[q], 0, 0, 0);
+                acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[2], (i & 1) == 0 ? zero : acc1[q], 0, 0, 0);
+                acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[1], acc0[q], 0, 0, 0);
+                acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[3], acc1[q], 0, 0, 0);
+            }
             if ((i & 1) == 1 || static_cast<uint32_t>(i) + 1u >= cnt) {
                 // Two pairs done: acc0 holds blocks 0 and 2 (zero rows elsewhere), acc1 1 and 3.
                 const int bi = i >> 1;
@@ -579,20 +588,25 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
                 const bool valid = 2u * bi + (ob >> 1) < cnt && g < G;
                 const float4 sx4 = sxl[bi * 4];
                 const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
-                const float sc = bf16_bits_to_f32(sbl[bi] & 0xFFFFu);
-                const float bs = bf16_bits_to_f32(sbl[bi] >> 16);
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float t = acc0[m] + acc1[m];
-                    float yn = fmaf(sc, fmaf(-128.0f, sxv[m], t), y[0][m]);
-                    yn = fmaf(bs, sxv[m], yn);
-                    y[0][m] = valid ? yn : y[0][m];
+                for (int q = 0; q < NW; ++q) {
+                    const float sc = bf16_bits_to_f32(sbl[q][bi] & 0xFFFFu);
+                    const float bs = bf16_bits_to_f32(sbl[q][bi] >> 16);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float t = acc0[q][m] + acc1[q][m];
+                        float yn = fmaf(sc, fmaf(-128.0f, sxv[m], t), y[q][m]);
+                        yn = fmaf(bs, sxv[m], yn);
+                        y[q][m] = valid ? yn : y[q][m];
+                    }
                 }
             }
         }
         // Blocks 0..3 hold the sums over disjoint groups: add lanes j, j + 16, j + 32, j + 48.
 #pragma unroll
-        for (int m = 0; m < M; ++m) y[0][m] = sum_lane_blocks(y[0][m]);
+        for (int q = 0; q < NW; ++q)
+#pragma unroll
+            for (int m = 0; m < M; ++m) y[q][m] = sum_lane_blocks(y[q][m]);
     } else if constexpr (!LOOP) {
         // The whole range is in flight (cnt <= 2P): straight-line code, so each pair waits
         // only for its own loads (a loop waits for the loads of every iteration).
