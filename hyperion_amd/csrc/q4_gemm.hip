@@ -559,7 +559,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // its group starts, and every wave has left group g before stage (g - g0) % (2 kSync)
     // is loaded again for group g + 2 kSync. Fewer barriers let the waves drift apart and
     // overlap each other's MFMA and dequantization work.
-    constexpr int kParts = 4;
+    // Units per k-step: 8 (2 row tiles each) for the 256-row tile, 4 for the 128-row one;
+    // measured on random data, gate at m = 2048 231-234 -> 221-225 us with 8, while the
+    // 128-row kernel ran 1-2% slower with 8.
+    constexpr int kParts = MT >= 16 ? 8 : 4;
     static_assert(NT <= kParts, "one column tile's dequantization per unit");
     constexpr int kValu = (26 + MT / kParts * NT - 1) / (MT / kParts * NT);   // one tile's dequantization per MFMA
     bf16x8_t a[2][MT / kParts];
