@@ -559,10 +559,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // its group starts, and every wave has left group g before stage (g - g0) % (2 kSync)
     // is loaded again for group g + 2 kSync. Fewer barriers let the waves drift apart and
     // overlap each other's MFMA and dequantization work.
-    // Units per k-step: 8 (2 row tiles each) for the 256-row tile, 4 for the 128-row one;
-    // measured on random data, gate at m = 2048 231-234 -> 221-225 us with 8, while the
-    // 128-row kernel ran 1-2% slower with 8.
-    constexpr int kParts = MT >= 16 ? 8 : 4;
+    // Units per k-step: 8 (2 row tiles each) for the 256-row tile, 2 (4 row tiles each)
+    // for the 128-row one. Measured on random data against 4 units: gate at m = 2048
+    // 231-234 -> 221-225 us with 8; gate at m = 512 70.5 -> 67.3 us and o at m = 2048
+    // 72.9 -> 69.3 us with 2 (8 made the 128-row kernel 1-2% slower).
+    constexpr int kParts = MT >= 16 ? 8 : 2;
     static_assert(NT <= kParts, "one column tile's dequantization per unit");
     constexpr int kValu = (26 + MT / kParts * NT - 1) / (MT / kParts * NT);   // one tile's dequantization per MFMA
     bf16x8_t a[2][MT / kParts];
