@@ -36,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 import hyperion_amd as hy  # noqa: E402
+from hyperion_amd import decode_chain as dc  # noqa: E402
 from hyperion_amd import synthetic as syn  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -59,14 +60,27 @@ def gemv_bytes(m, n, k):
     return q4_bytes(n, k) + 2 * m * k + 2 * m * n
 
 
+MALL_BYTES = 256 << 20   # MI355X Infinity Cache
+
+
+def cold_rotation_ok(copies, bytes_per_copy):
+    """True when every reuse of a copy in a rotation over `copies` buffers comes after at
+    least one MALL's worth of other bytes: a launch on copy c is preceded by launches on
+    the other copies - 1 buffers since c was last read."""
+    return (copies - 1) * bytes_per_copy > MALL_BYTES
+
+
 def time_launches(stream, fn, steps, warmup):
-    """Mean milliseconds per call of fn(i), from HIP events recorded on `stream`."""
+    """Mean milliseconds per call of fn(i), from HIP events recorded on `stream`. The
+    index keeps counting from the warm-up into the timed loop (warm-up calls are
+    fn(0..warmup-1), timed calls fn(warmup..warmup+steps-1)), so a rotation over
+    buffers indexed by i % copies never restarts at the buffers the warm-up just read."""
     for i in range(warmup):
         fn(i)
     stream.synchronize()
     e0, e1 = hy.Event(), hy.Event()
     e0.record(stream)
-    for i in range(steps):
+    for i in range(warmup, warmup + steps):
         fn(i)
     e1.record(stream)
     ms = e0.elapsed_ms(e1)
@@ -91,6 +105,9 @@ def device_copies(w, s, b, n, k, copies, stream):
 
 def bench_decode_gemv(stream, steps, warmup, copies):
     n, k = DECODE_N, DECODE_K
+    if not cold_rotation_ok(copies, q4_bytes(n, k)):
+        raise SystemExit(f"--copies {copies}: a rotation over {copies} weight copies re-reads a copy within "
+                         f"{MALL_BYTES >> 20} MiB of other traffic (the MALL would serve it)")
     log(f"decode GEMV m=1 n={n} k={k}: {copies} device copies")
     w, s, b = syn.q4_weights(n, k, seed=105)
     qws = device_copies(w, s, b, n, k, copies, stream)
@@ -108,6 +125,7 @@ def bench_decode_gemv(stream, steps, warmup, copies):
 
 def bench_quantize(stream, steps, warmup, copies=4):
     n, k = DECODE_N, DECODE_K
+    assert cold_rotation_ok(copies, 2 * n * k + q4_bytes(n, k))
     log(f"quantize/pack n={n} k={k}: {copies} input copies")
     wb = syn.quantize_input(n, k, seed=101)
     ins = [hy.DeviceArray.from_host(wb, stream) for _ in range(copies)]
@@ -209,83 +227,25 @@ def bench_prefill(stream, m, steps, warmup, dense=None):
     return out
 
 
-class DecodeModel:
-    """Random-init Q4 weights of a Gemma-class 12B decoder's linear layers (every layer
-    with v_proj) and its tied embedding table, resident in HBM."""
-
-    def __init__(self, layers, stream):
-        self.layers = []
-        t0 = time.perf_counter()
-        for li in range(layers):
-            proj = {}
-            for pi, (name, (n, k)) in enumerate(syn.LAYER_SHAPES.items()):
-                w, s, b = syn.q4_weights(n, k, seed=10_000 + 16 * li + pi)
-                proj[name] = hy.QWeight.from_host(w, s, b)
-            self.layers.append(proj)
-        w, s, b = syn.q4_weights(syn.VOCAB, HIDDEN, seed=9_999)
-        self.embed = hy.QWeight.from_host(w, s, b)
-        self.weight_bytes = layers * sum(q4_bytes(n, k) for n, k in syn.LAYER_SHAPES.values()) + \
-            q4_bytes(syn.VOCAB, HIDDEN)
-        log(f"decode model: {layers} layers + LM head, {self.weight_bytes / 1e9:.2f} GB of Q4 weights "
-            f"({time.perf_counter() - t0:.1f} s to build)")
-
-    def close(self):
-        for proj in self.layers:
-            for q in proj.values():
-                q.close()
-        self.embed.close()
-
-
-def decode_layers(model, m, bufs, stream):
-    """One decode step's layer stack: per layer, h renormalised and multiplied by q, k and
-    v in one launch; o from q's output; the fused gate/up GELU from o's output; down
-    into h."""
-    h, q, k, v, o, g = bufs[:6]
-    for proj in model.layers:
-        hy.qmatmul_group([proj["q"], proj["k"], proj["v"]], h, m, [q, k, v], stream, rms_eps=RMS_EPS)
-        hy.qmatmul(proj["o"], q, m, o, stream)
-        hy.qmlp_gate_up_gelu(proj["gate"], proj["up"], o, m, g, stream)
-        hy.qmatmul(proj["down"], g, m, h, stream)
-
-
-def lm_head(model, m, bufs, stream):
-    """The last hidden state renormalised, the tied LM head with softcap 30, then greedy
-    sampling of every row on the device (run_epilogue, model.cc:215-228)."""
-    hy.rms_normalize(bufs[0], m, HIDDEN, bufs[0], stream, eps=RMS_EPS)
-    hy.qmatmul(model.embed, bufs[0], m, bufs[-2], stream, softcap=30.0)
-    hy.sample_greedy(bufs[-2], m, syn.VOCAB, bufs[-1], stream)
-
-
-LAUNCHES_PER_LAYER = 4
-RMS_EPS = 1e-6
-
-
 def bench_decode_stream(model, m, steps, warmup, stream):
-    h = hy.DeviceArray.from_host(syn.activations(m, HIDDEN, seed=77), stream)
-    bufs = (h, hy.DeviceArray((m, 4096), np.uint16), hy.DeviceArray((m, 2048), np.uint16),
-            hy.DeviceArray((m, 2048), np.uint16), hy.DeviceArray((m, HIDDEN), np.uint16),
-            hy.DeviceArray((m, 15360), np.uint16), hy.DeviceArray((m, syn.VOCAB), np.uint16),
-            hy.DeviceArray((m, 3), np.uint32))
+    b = dc.StepBuffers(hy, m, syn.activations(m, HIDDEN, seed=77), stream)
     with hy.Graph.capture(stream) as graph:
-        decode_layers(model, m, bufs, stream)
-        lm_head(model, m, bufs, stream)
+        dc.decode_step(model, m, b, stream)
     ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup)
     graph.close()
     with hy.Graph.capture(stream) as head:
-        lm_head(model, m, bufs, stream)
+        dc.lm_head(model, m, b, stream)
     head_ms = time_launches(stream, lambda _i: head.launch(stream), steps, warmup)
     head.close()
+    b.close()
     layers = len(model.layers)
-    # activations: per layer x, q/k/v, o, gate/up, down; then the head's x, logits written
-    # and read back by the sampler, and 12 bytes of sample per row
-    act = 2 * m * (layers * (HIDDEN * 3 + 4096 * 2 + 2048 * 2 + HIDDEN * 2 + 15360 * 3) + HIDDEN + 2 * syn.VOCAB) + 12 * m
-    nbytes = model.weight_bytes + act
+    nbytes = model.weight_bytes + dc.step_activation_bytes(layers, m)
     head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + 2 * syn.VOCAB) + 12 * m
     layer_bytes = (nbytes - head_bytes) / max(layers, 1)
     layer_us = (ms - head_ms) * 1e3 / max(layers, 1)
     out = {"m": m, "ms_per_step": round(ms, 4), "tokens_per_s": round(m / (ms / 1e3), 1),
            "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-           "bytes_per_step": nbytes, "launches_per_step": LAUNCHES_PER_LAYER * layers + 3,
+           "bytes_per_step": nbytes, "launches_per_step": dc.LAUNCHES_PER_LAYER * layers + 3,
            "lm_head_us": round(head_ms * 1e3, 1),
            "lm_head_gbs": round(head_bytes / head_ms / 1e6, 1),
            "layer_us": round(layer_us, 2),
@@ -424,14 +384,14 @@ def main():
     elif args.only_sample:
         extra["sample_greedy"] = bench_sample(stream, 20, 3)
     elif args.only_stream:
-        model = DecodeModel(args.layers, stream)
+        model = dc.DecodeModel(hy, args.layers, log)
         extra["decode_stream"] = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
     elif not args.only_decode:
         extra["quantize"] = bench_quantize(stream, 50, 5)
         extra["sample_greedy"] = bench_sample(stream, 20, 3)
         extra["prefill"] = [bench_prefill(stream, m, 10, 2, dense.get(m)) for m in (512, 2048)]
-        model = DecodeModel(args.layers, stream)
+        model = dc.DecodeModel(hy, args.layers, log)
         streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
         extra["decode_stream"] = streams

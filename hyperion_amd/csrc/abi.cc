@@ -136,6 +136,18 @@ hipStream_t stream_of(HypStream s) {
     return s->stream;
 }
 
+// Calls that allocate device memory (stream-ordered temporaries of the m > 4 paths) or
+// clear it with hipMemsetAsync must not be recorded into a graph: a captured
+// allocation or memset node would replay against memory the call no longer owns.
+// Such calls check the stream first and refuse, before anything is enqueued.
+void require_not_capturing(hipStream_t s, const char* what) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    HYP_HIP_CHECK(hipStreamIsCapturing(s, &st));
+    REQUIRE_ARG(st == hipStreamCaptureStatusNone,
+                std::string(what) + " may allocate or clear device memory and cannot be recorded into a graph "
+                                    "(the stream is capturing)");
+}
+
 void validate_quant(std::uint32_t n, std::uint32_t k, std::uint32_t group_size, std::uint32_t bits) {
     if (group_size != 64 || bits != 4) {
         throw NativeError(HYP_STATUS_UNSUPPORTED, "only affine group_size=64 bits=4 is supported (got group_size=" +
@@ -287,6 +299,7 @@ HypStatus hyp_memset_device(void* dst, int value, size_t bytes, HypStream stream
         hipStream_t s = stream_of(stream);
         if (bytes == 0) return;
         REQUIRE_ARG(dst != nullptr, "memset requires a non-null buffer");
+        require_not_capturing(s, "hyp_memset_device");
         HYP_HIP_CHECK(hipMemsetAsync(dst, value, bytes, s));
     });
 }
@@ -456,6 +469,7 @@ HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y, 
         }
         if (m == 0) return;
         REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
+        if (!hyperion::hip::skinny_supported(m, lin.mat.k, false)) require_not_capturing(s, "hyp_qmatmul on the GEMM path");
         lin.apply(static_cast<const uint16_t*>(x), m, static_cast<uint16_t*>(y), s, epi, cap_bf16);
     });
 }
@@ -482,6 +496,9 @@ void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uin
     if (m == 0) return;
     REQUIRE_ARG(x != nullptr, "x must be a non-null device pointer");
     for (uint32_t i = 0; i < count; ++i) REQUIRE_ARG(outs[i] != nullptr, "ys[i] must be non-null device pointers");
+    const uint32_t k = lins[0]->mat.k;
+    if (!(rms_eps != nullptr ? hyperion::hip::skinny_norm_supported(m, k) : hyperion::hip::skinny_supported(m, k, false)))
+        require_not_capturing(s, "hyp_qmatmul_group on the GEMM path");
     hyperion::model::apply_group(lins, outs, count, static_cast<const uint16_t*>(x), m, rms_eps, s);
 }
 
@@ -508,6 +525,7 @@ HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, u
         REQUIRE_ARG(g.mat.n == u.mat.n && g.mat.k == u.mat.k, "gate and up must have the same shape");
         if (m == 0) return;
         REQUIRE_ARG(x != nullptr && h != nullptr, "x and h must be non-null device pointers");
+        if (!hyperion::hip::skinny_supported(m, g.mat.k, true)) require_not_capturing(s, "hyp_qmlp_gate_up_gelu on the GEMM path");
         hyperion::model::mlp_gate_up(g, u, static_cast<const uint16_t*>(x), m, static_cast<uint16_t*>(h), s);
     });
 }

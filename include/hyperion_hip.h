@@ -136,9 +136,12 @@ HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
  * per-launch host work; the reference has no counterpart (MLX evaluates its lazy graph
  * at mx::eval, forward.cc:171). Between begin and end, hyp_qmatmul, hyp_qmatmul_ex,
  * hyp_qmatmul_group, hyp_qmlp_gate_up_gelu and hyp_qmatmul_group_rmsnorm with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
- * hyp_dequantize_q4g64 and hyp_embed on `stream` are recorded instead of run (they
- * allocate nothing); other calls on that stream are not allowed. The recorded pointers
- * and handles must stay valid while the graph is used. */
+ * hyp_dequantize_q4g64, hyp_embed, hyp_sample_greedy and the copies on `stream` are
+ * recorded instead of run (they allocate nothing). Calls that may allocate or clear
+ * memory - the matmul entries on their GEMM path (m > 4) and hyp_memset_device - check
+ * the stream and return INVALID_ARGUMENT while it is capturing, before enqueueing
+ * anything; the capture stays open and usable. The recorded pointers and handles must
+ * stay valid while the graph is used. */
 HypStatus hyp_graph_capture_begin(HypStream stream);
 HypStatus hyp_graph_capture_end(HypStream stream, HypGraph* out_graph);
 /* Enqueue one replay of the graph on stream. */

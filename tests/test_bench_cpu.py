@@ -46,3 +46,45 @@ def test_entry_points_exist():
         sys.path.insert(0, ROOT)
     g = importlib.import_module("__graft_entry__")
     assert callable(g.build) and callable(g.smoke)
+
+
+def test_cold_rotation_never_rereads_a_copy_within_the_mall():
+    """Simulate the bench's index arithmetic: every timed launch on copy c must be
+    separated from the previous read of c (warm-up included) by more than 256 MiB of
+    other weight bytes, for any steps/warmup at the default copy counts."""
+    b = _bench()
+    per_copy = b.q4_bytes(15360, 3840)
+    calls = []
+
+    class _Stream:
+        def synchronize(self):
+            pass
+
+    class _Event:
+        def record(self, _s):
+            pass
+
+        def elapsed_ms(self, _e):
+            return 1.0
+
+        def close(self):
+            pass
+
+    saved = b.hy.Event
+    b.hy.Event = _Event
+    try:
+        for steps, warmup in ((20, 5), (200, 20), (7, 0), (1, 30)):
+            calls.clear()
+            b.time_launches(_Stream(), lambda i: calls.append(i), steps, warmup)
+            copies = 24
+            assert b.cold_rotation_ok(copies, per_copy)
+            last = {}
+            for pos, i in enumerate(calls):
+                c = i % copies
+                if pos >= warmup and c in last:
+                    between = (pos - last[c] - 1) * per_copy
+                    assert between > b.MALL_BYTES, (steps, warmup, pos)
+                last[c] = pos
+    finally:
+        b.hy.Event = saved
+    assert not b.cold_rotation_ok(8, per_copy)   # 7 x 33 MB < 256 MiB: refused
