@@ -151,9 +151,19 @@ def test_lm_head_full_vocab_softcap_and_sampling(model, head_host, stream, m):
     rel = syn.sig_rel(syn.bf16_to_f32(capped[:, rows]), cap_truth)
     say(f"  sampled rows: capped sig_rel {rel:.2e} (bound 1e-2)")
     assert rel <= 1e-2
-    d = ulp_diff(capped, O.softcap(plain, dc.SOFTCAP))
-    say(f"  capped vs oracle softcap of the plain launch: max {d.max()} ulp, {np.count_nonzero(d)} differ")
-    assert d.max() <= 2 and np.count_nonzero(d) <= d.size // 1000
+    # The head launch (one wave per tile) and the plain launch (k split over waves) sum the
+    # same fp32 terms in another order; each is within half a bf16 ulp + 2^-18 max|y| of the
+    # truth, so after the cap they may differ by up to two ulps of the value plus 2^-17 of
+    # the largest logit (near-zero logits can then be many ulps apart in relative terms).
+    ref = O.softcap(plain, dc.SOFTCAP)
+    d = ulp_diff(capped, ref)
+    diff = np.abs(syn.bf16_to_f32(capped).astype(np.float64) - syn.bf16_to_f32(ref))
+    ulp = np.abs(syn.bf16_to_f32(ref)).astype(np.float64) * 2.0**-7 + 1e-40
+    bound = 2.0 * ulp + 2.0**-17 * float(np.max(np.abs(syn.bf16_to_f32(plain))))
+    say(f"  capped vs oracle softcap of the plain launch: {np.count_nonzero(d)} differ, worst "
+        f"{float(np.max(diff / bound)):.2f} of the bound")
+    assert np.all(diff <= bound)
+    assert np.count_nonzero(d) <= d.size // 1000
     out = hy.DeviceArray((m, 3), np.uint32)
     hy.sample_greedy(capped_d, m, syn.VOCAB, out, stream)
     got = hy.greedy_samples(out, m, stream)
