@@ -44,7 +44,7 @@ EXPORTED = [
     "hyp_graph_capture_begin", "hyp_graph_capture_end", "hyp_graph_launch", "hyp_graph_free",
     "hyp_qweight_create", "hyp_qweight_create_device", "hyp_qweight_free",
     "hyp_qweight_shape", "hyp_qweight_export",
-    "hyp_qmatmul", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
+    "hyp_qmatmul", "hyp_qmatmul_noalloc", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
     "hyp_sample_greedy",
@@ -124,6 +124,7 @@ def lib() -> ctypes.CDLL:
         "hyp_qweight_shape": [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32)],
         "hyp_qweight_export": [_P, _P, _P, _P],
         "hyp_qmatmul": [_P, _P, _U32, _P, _P],
+        "hyp_qmatmul_noalloc": [_P, _P, _U32, _P, _P],
         "hyp_qmatmul_ex": [_P, _P, _U32, _P, ctypes.c_int, ctypes.c_float, _P],
         "hyp_qmatmul_group": [_P, _U32, _P, _U32, _P, _P],
         "hyp_qmatmul_group_rmsnorm": [_P, _U32, _P, _U32, ctypes.c_float, _P, _P],

@@ -478,6 +478,16 @@ HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, Hyp
     return hyp_qmatmul_ex(weight, x, m, y, HYP_EPILOGUE_NONE, 0.0f, stream);
 }
 
+HypStatus hyp_qmatmul_noalloc(HypQWeight weight, const void* x, uint32_t m, void* y, HypStream stream) {
+    return abi_call("hyp_qmatmul_noalloc", [&] {
+        const QuantizedLinear& lin = qweight_ref(weight, "weight");
+        hipStream_t s = stream_of(stream);
+        if (m == 0) return;
+        REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
+        lin.apply_noalloc(static_cast<const uint16_t*>(x), m, static_cast<uint16_t*>(y), s);
+    });
+}
+
 namespace {
 
 void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m, const float* rms_eps,

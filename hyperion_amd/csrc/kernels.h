@@ -66,6 +66,10 @@ bool skinny_norm_supported(uint32_t m, uint32_t k);
 // x tiles in LDS. Plain bf16 output; epilogues for larger m run as the elementwise
 // kernels below.
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
+// launch_q4_gemm with the split-k partials in a fixed device scratch array instead of a
+// stream-ordered temporary: allocates nothing (INVALID_ARGUMENT if the call's partials
+// exceed the 64 MiB scratch). Calls on one device share the scratch.
+void launch_q4_gemm_noalloc(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
 // One launch over `count` (<= 3) projections that share x and k (q, k and v):
 // ys[i][m, n_i] = x . dequant(W_i)^T.
 void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,

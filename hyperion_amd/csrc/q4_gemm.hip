@@ -27,6 +27,8 @@
 //    gets a contiguous run of tiles that share X rows, keeping the X block in that
 //    XCD's L2.
 #include <algorithm>
+#include <mutex>
+#include <string>
 #include <type_traits>
 #include <utility>
 
@@ -902,7 +904,16 @@ GemmChoice choose_gemm(const GemmParams& p) {
     return {GemmKernel::kPair128, fill_split(p, pair, cus)};
 }
 
-void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t stream) {
+// Where the split-k partials of one call live: a stream-ordered temporary
+// (hipMallocAsync / hipFreeAsync around the call), or `fixed`, caller-provided device
+// memory of `fixed_bytes` that the call only writes and reads (no allocation).
+struct SplitWorkspace {
+    float* fixed = nullptr;
+    size_t fixed_bytes = 0;
+};
+
+void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t stream,
+                  const SplitWorkspace& wsp = SplitWorkspace{}) {
     p.ksplit = ksplit;
     p.pairs_per_split = (p.pairs + ksplit - 1u) / ksplit;
     p.ksplit = (p.pairs + p.pairs_per_split - 1u) / p.pairs_per_split;   // no empty split
@@ -911,8 +922,18 @@ void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t
         return;
     }
     const uint64_t elems = static_cast<uint64_t>(p.m) * p.n_total;
+    const uint64_t bytes = elems * p.ksplit * sizeof(float);
+    // Every split writes each (row, column) of its partial, so the buffer needs no clearing.
     void* ws = nullptr;
-    HYP_HIP_CHECK(hipMallocAsync(&ws, elems * p.ksplit * sizeof(float), stream));
+    if (wsp.fixed != nullptr) {
+        HYP_REQUIRE(bytes <= wsp.fixed_bytes, HYP_STATUS_INVALID_ARGUMENT,
+                    "gemm: this call splits k " + std::to_string(p.ksplit) + " ways and needs " +
+                        std::to_string(bytes) + " bytes of partial sums; the no-allocation scratch holds " +
+                        std::to_string(wsp.fixed_bytes) + " bytes");
+        ws = wsp.fixed;
+    } else {
+        HYP_HIP_CHECK(hipMallocAsync(&ws, bytes, stream));
+    }
     p.partial = static_cast<float*>(ws);
     try {
         launch_params(p, kernel, stream);
@@ -927,10 +948,38 @@ void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t
                            dim3(kThreads), 0, stream, p);
         HYP_HIP_CHECK(hipGetLastError());
     } catch (...) {
-        (void)hipFreeAsync(ws, stream);
+        if (wsp.fixed == nullptr) (void)hipFreeAsync(ws, stream);
         throw;
     }
-    HYP_HIP_CHECK(hipFreeAsync(ws, stream));
+    if (wsp.fixed == nullptr) HYP_HIP_CHECK(hipFreeAsync(ws, stream));
+}
+
+// The scratch of launch_q4_gemm_noalloc: split-k partials in a file-scope device array,
+// so that path allocates nothing. Each device holds its own copy (64 MiB) from module
+// load until the process ends; every call on one device shares it, so calls that
+// overlap on one device (e.g. on two streams) race.
+constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`. The array's name in host code is only a
+// host-side stand-in, so the device address is looked up once per device (with that
+// device current) and kept; kernels and copies take this pointer, never the name.
+float* noalloc_scratch() {
+    int dev = 0;
+    HYP_HIP_CHECK(hipGetDevice(&dev));
+    HYP_REQUIRE(dev >= 0 && dev < kMaxDevices, HYP_STATUS_UNSUPPORTED, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        HYP_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        HYP_REQUIRE(ptr != nullptr, HYP_STATUS_INTERNAL, "no device address for the no-allocation scratch");
+        g_scratch_ptr[dev] = ptr;
+    }
+    return static_cast<float*>(g_scratch_ptr[dev]);
 }
 
 }  // namespace
@@ -946,6 +995,17 @@ void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* 
     const Q4Matrix* ws[1] = {&w};
     uint16_t* ys[1] = {y};
     launch_q4_gemm_group(ws, ys, 1u, x, m, stream);
+}
+
+void launch_q4_gemm_noalloc(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) {
+    const Q4Matrix* ws[1] = {&w};
+    uint16_t* ys[1] = {y};
+    GemmParams p = group_params(ws, ys, 1u, x, m);
+    const GemmChoice c = choose_gemm(p);   // the same kernel and split as launch_q4_gemm
+    SplitWorkspace wsp;
+    wsp.fixed = noalloc_scratch();
+    wsp.fixed_bytes = kNoAllocScratchBytes;
+    launch_split(p, c.kernel, c.ksplit, stream, wsp);
 }
 
 }  // namespace hyperion::hip

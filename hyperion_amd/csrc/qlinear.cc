@@ -147,6 +147,15 @@ void QuantizedLinear::apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStrea
     }
 }
 
+void QuantizedLinear::apply_noalloc(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) const {
+    if (m == 0) return;
+    if (hip::skinny_supported(m, mat.k, false)) {
+        hip::launch_q4_skinny(mat, nullptr, x, m, y, Epilogue::kNone, 0.0f, 0u, stream);
+        return;
+    }
+    hip::launch_q4_gemm_noalloc(mat, x, m, y, stream);
+}
+
 void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uint32_t count, const uint16_t* x,
                  uint32_t m, const float* rms_eps, hipStream_t stream) {
     if (m == 0) return;

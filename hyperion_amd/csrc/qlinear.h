@@ -66,6 +66,11 @@ struct QuantizedLinear {
     // y[m, n] = x[m, k] . dequant(W)^T (weights.h:26-37); device pointers.
     void apply(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream,
                Epilogue epi = Epilogue::kNone, float cap_bf16 = 0.0f) const;
+
+    // apply() without any allocation: the same kernels and splits, with split-k partials
+    // in the library's fixed device scratch (launch_q4_gemm_noalloc), so the results are
+    // the same bits. Throws INVALID_ARGUMENT when a call's partials exceed the scratch.
+    void apply_noalloc(const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream) const;
 };
 
 // gelu_tanh(gate(x)) * up(x) (forward.cc:338-343 minus the down projection).

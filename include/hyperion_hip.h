@@ -176,6 +176,19 @@ HypStatus hyp_qweight_export(HypQWeight weight, uint32_t* w, uint16_t* scales, u
  * x and y are device pointers; m == 0 is a no-op. */
 HypStatus hyp_qmatmul(HypQWeight weight, const void* x, uint32_t m, void* y, HypStream stream);
 
+/* hyp_qmatmul that allocates nothing: no hipMalloc, hipMallocAsync, hipFree or other
+ * allocating call, on any path. It has no counterpart in the reference; it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation). The kernels and k splits are those of hyp_qmatmul, so the output
+ * is the same bits; where hyp_qmatmul's prefill GEMM (m > 4) splits k, the fp32 partial
+ * sums go to a fixed 64 MiB device scratch array that the library holds on each device
+ * it runs on until the process ends (enough for every projection of a 12B layer at
+ * m <= 2048). A call whose partials would exceed it returns INVALID_ARGUMENT and runs
+ * nothing. All calls on one device share that scratch: calls that overlap on one device
+ * (e.g. on two streams without ordering between them) race; calls on one stream are
+ * ordered and safe. Nothing in the scratch needs clearing between calls. */
+HypStatus hyp_qmatmul_noalloc(HypQWeight weight, const void* x, uint32_t m, void* y, HypStream stream);
+
 /* hyp_qmatmul with an epilogue; HYP_EPILOGUE_SOFTCAP with cap > 0 is the tied
  * LM head + softcap of ForwardPass::lm_head/softcap (forward.cc:137-160). */
 HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y,
