@@ -48,6 +48,7 @@ EXPORTED = [
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
     "hyp_sample_greedy",
+    "hyp_step_program_create", "hyp_step_program_run", "hyp_step_program_check", "hyp_step_program_free",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
 ]
@@ -71,6 +72,24 @@ class RuntimeInfo(ctypes.Structure):
         ("l2_bytes", ctypes.c_uint32),
         ("arch_name", ctypes.c_char * 64),
         ("device_name", ctypes.c_char * 128),
+    ]
+
+
+STEP_QMATMUL = 0
+STEP_QMATMUL_RMSNORM = 1
+STEP_GATE_UP_GELU = 2
+
+
+class StepOp(ctypes.Structure):
+    """HypStepOp: one op of a decode-step program."""
+    _fields_ = [
+        ("kind", ctypes.c_uint32),
+        ("count", ctypes.c_uint32),
+        ("weights", ctypes.c_void_p * 3),
+        ("x", ctypes.c_void_p),
+        ("y", ctypes.c_void_p * 3),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_uint32),
     ]
 
 
@@ -134,6 +153,10 @@ def lib() -> ctypes.CDLL:
         "hyp_embed": [_P, _P, _U32, _P, _P],
         "hyp_rms_normalize": [_P, _U32, _U32, ctypes.c_float, _P, _P],
         "hyp_sample_greedy": [_P, _U32, _U32, _P, _P],
+        "hyp_step_program_create": [_P, _U32, _U32, _U32, _PP],
+        "hyp_step_program_run": [_P, _P],
+        "hyp_step_program_check": [_P],
+        "hyp_step_program_free": [_PP],
         "hyp_qmodel_load": [ctypes.c_char_p, _U32, _PP],
         "hyp_qmodel_free": [_PP],
         "hyp_qmodel_num_layers": [_P, ctypes.POINTER(_U32)],
@@ -384,6 +407,44 @@ class QModel:
     def close(self) -> None:
         if self._h:
             call("hyp_qmodel_free", ctypes.byref(self._h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class StepProgram:
+    """A decode-step program (hyp_step_program_*): ops is a list of (kind, weights, x, ys,
+    eps) with QWeight weights and DeviceArray buffers, all borrowed for the program's life."""
+
+    def __init__(self, ops, m: int, spin_limit: int = 0):
+        arr = (StepOp * len(ops))()
+        self._keep = []
+        for i, (kind, ws, x, ys, eps) in enumerate(ops):
+            o = arr[i]
+            o.kind = kind
+            o.count = len(ws)
+            for q, w in enumerate(ws):
+                o.weights[q] = w.handle.value
+            o.x = x.ptr.value
+            for q, y in enumerate(ys):
+                o.y[q] = y.ptr.value
+            o.eps = eps
+            self._keep.append((ws, x, ys))
+        self._h = ctypes.c_void_p()
+        call("hyp_step_program_create", ctypes.cast(arr, _P), len(ops), m, spin_limit, ctypes.byref(self._h))
+
+    def run(self, stream: "Stream") -> None:
+        call("hyp_step_program_run", self._h, stream.handle)
+
+    def check(self) -> None:
+        call("hyp_step_program_check", self._h)
+
+    def close(self) -> None:
+        if self._h:
+            call("hyp_step_program_free", ctypes.byref(self._h))
 
     def __del__(self):
         try:

@@ -14,6 +14,7 @@
 #include "hyperion_hip.h"
 #include "kernels.h"
 #include "qlinear.h"
+#include "step_program_host.h"
 
 using hyperion::hip::Epilogue;
 using hyperion::hip::NativeError;
@@ -27,6 +28,7 @@ constexpr std::uint32_t kQModelMagic = 0x4850514DU;    // "HPQM"
 constexpr std::uint32_t kStreamMagic = 0x48505354U;    // "HPST"
 constexpr std::uint32_t kEventMagic = 0x48504556U;     // "HPEV"
 constexpr std::uint32_t kGraphMagic = 0x48504752U;     // "HPGR"
+constexpr std::uint32_t kStepProgramMagic = 0x48505350U;   // "HPSP"
 
 constexpr std::size_t kLastErrorCapacity = 1024;
 thread_local std::array<char, kLastErrorCapacity> g_last_error{};
@@ -113,6 +115,11 @@ struct HypStreamOpaque {
 struct HypEventOpaque {
     std::uint32_t magic = 0;
     hipEvent_t event = nullptr;
+};
+
+struct HypStepProgramOpaque {
+    std::uint32_t magic = 0;
+    std::unique_ptr<hyperion::model::StepProgram> program;
 };
 
 struct HypGraphOpaque {
@@ -601,6 +608,64 @@ HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, H
         hyperion::hip::launch_sample_greedy(static_cast<const uint16_t*>(logits), rows, vocab, out, stream->workspace,
                                             stream->workspace_bytes, s);
     });
+}
+
+HypStatus hyp_step_program_create(const HypStepOp* ops, uint32_t n_ops, uint32_t m, uint32_t spin_limit,
+                                  HypStepProgram* out_program) {
+    return abi_call("hyp_step_program_create", [&] {
+        REQUIRE_ARG(out_program != nullptr, "create requires a non-null out handle");
+        REQUIRE_ARG(ops != nullptr && n_ops > 0, "a step program needs at least one op");
+        REQUIRE_ARG(m >= 1u && m <= hyperion::hip::kSkinnyMaxM, "a step program runs m = 1..4 rows");
+        std::vector<hyperion::model::StepOpSpec> specs(n_ops);
+        for (uint32_t i = 0; i < n_ops; ++i) {
+            const HypStepOp& o = ops[i];
+            hyperion::model::StepOpSpec& sp = specs[i];
+            const std::string who = "op " + std::to_string(i) + ": ";
+            switch (o.kind) {
+                case HYP_STEP_QMATMUL: sp.form = hyperion::hip::StepForm::kPlain; break;
+                case HYP_STEP_QMATMUL_RMSNORM: sp.form = hyperion::hip::StepForm::kNorm; break;
+                case HYP_STEP_GATE_UP_GELU: sp.form = hyperion::hip::StepForm::kDual; break;
+                default: throw NativeError(HYP_STATUS_INVALID_ARGUMENT, who + "unknown op kind");
+            }
+            REQUIRE_ARG(o.count >= 1u && o.count <= 3u, who + "count must be 1..3");
+            REQUIRE_ARG(o.reserved == 0u, who + "reserved must be 0");
+            sp.count = o.count;
+            for (uint32_t q = 0; q < o.count; ++q) sp.w[q] = &qweight_ref(o.weights[q], "op weight");
+            sp.x = static_cast<const uint16_t*>(o.x);
+            for (uint32_t q = 0; q < 3u; ++q) sp.y[q] = static_cast<uint16_t*>(o.y[q]);
+            sp.eps = o.eps;
+        }
+        require_device();
+        auto h = std::make_unique<HypStepProgramOpaque>();
+        h->program = std::make_unique<hyperion::model::StepProgram>(specs, m, spin_limit);
+        h->magic = kStepProgramMagic;
+        *out_program = h.release();
+    });
+}
+
+HypStatus hyp_step_program_run(HypStepProgram program, HypStream stream) {
+    return abi_call("hyp_step_program_run", [&] {
+        REQUIRE_ARG(program != nullptr && program->magic == kStepProgramMagic, "step program handle is invalid");
+        hipStream_t s = stream_of(stream);
+        require_not_capturing(s, "hyp_step_program_run (a cooperative launch)");
+        program->program->run(s);
+    });
+}
+
+HypStatus hyp_step_program_check(HypStepProgram program) {
+    return abi_call("hyp_step_program_check", [&] {
+        REQUIRE_ARG(program != nullptr && program->magic == kStepProgramMagic, "step program handle is invalid");
+        const std::uint32_t err = program->program->check();
+        if (err != 0u) {
+            throw NativeError(HYP_STATUS_INTERNAL,
+                              "a step-program run gave up waiting for the other workgroups (error " +
+                                  std::to_string(err) + "); its outputs are undefined and the program was reset");
+        }
+    });
+}
+
+HypStatus hyp_step_program_free(HypStepProgram* program) {
+    return free_handle(program, kStepProgramMagic);
 }
 
 HypStatus hyp_qmodel_load(const char* dir, uint32_t num_layers, HypQModel* out_model) {

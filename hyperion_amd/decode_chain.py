@@ -119,6 +119,19 @@ def lm_head(model: DecodeModel, m: int, b: StepBuffers, stream) -> None:
     hy.sample_greedy(b.logits, m, syn.VOCAB, b.samples, stream)
 
 
+def layer_program(model: DecodeModel, m: int, b: StepBuffers, spin_limit: int = 0):
+    """The layer stack as one decode-step program (hyp_step_program_*): the same four ops
+    per layer as decode_layer, run by one persistent launch with the same output bits."""
+    hy = model.hy
+    ops = []
+    for proj in model.layers:
+        ops.append((hy.STEP_QMATMUL_RMSNORM, [proj["q"], proj["k"], proj["v"]], b.h, [b.q, b.k, b.v], RMS_EPS))
+        ops.append((hy.STEP_QMATMUL, [proj["o"]], b.q, [b.o], 0.0))
+        ops.append((hy.STEP_GATE_UP_GELU, [proj["gate"], proj["up"]], b.o, [b.g], 0.0))
+        ops.append((hy.STEP_QMATMUL, [proj["down"]], b.g, [b.h], 0.0))
+    return hy.StepProgram(ops, m, spin_limit)
+
+
 def decode_step(model: DecodeModel, m: int, b: StepBuffers, stream) -> None:
     decode_layers(model, m, b, stream)
     lm_head(model, m, b, stream)

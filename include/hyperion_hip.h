@@ -259,6 +259,56 @@ HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, vo
 HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, HypGreedySample* out,
                             HypStream stream);
 
+/* ---- decode-step program (the per-token layer loop, forward.cc:558-563, run by
+ *      hyp_decode_block, model.cc:703-718) ------------------------------------------ */
+
+/* An ordered list of decode-size (m <= 4) quantized-linear ops run by ONE launch: a
+ * persistent kernel with one 16-wave workgroup per compute unit walks the ops, and op i
+ * starts only when every workgroup has finished op i - 1 (device-memory arrival counters).
+ * It replaces the per-op launches of a decode step, each of which carries a fixed cost of
+ * several microseconds; the next op's weights stream in while its input is awaited.
+ * Op i may read anything an earlier op wrote and overwrite anything an earlier op read.
+ * Each op gives the same bits as its per-call entry point:
+ *   HYP_STEP_QMATMUL          count 1..3 weights sharing k: hyp_qmatmul / hyp_qmatmul_group
+ *   HYP_STEP_QMATMUL_RMSNORM  the same on rms-normalised x rows: hyp_qmatmul_group_rmsnorm
+ *   HYP_STEP_GATE_UP_GELU     weights[0] gate, weights[1] up, output y[0]:
+ *                             hyp_qmlp_gate_up_gelu */
+typedef struct HypStepProgramOpaque* HypStepProgram;   /* magic "HPSP" */
+
+typedef enum HypStepOpKind {
+    HYP_STEP_QMATMUL = 0,
+    HYP_STEP_QMATMUL_RMSNORM = 1,
+    HYP_STEP_GATE_UP_GELU = 2
+} HypStepOpKind;
+
+typedef struct HypStepOp {
+    uint32_t kind;                  /* HypStepOpKind */
+    uint32_t count;                 /* weights used: 1..3, or 2 for GATE_UP_GELU */
+    HypQWeight weights[3];
+    const void* x;                  /* device bf16 [m, k] */
+    void* y[3];                     /* device bf16 [m, n_i] (GATE_UP_GELU: y[0] only) */
+    float eps;                      /* QMATMUL_RMSNORM */
+    uint32_t reserved;              /* 0 */
+} HypStepOp;
+
+/* Validate the ops for m rows (1..4) and keep a device copy of them. The weights and
+ * buffers are borrowed: they must stay valid while the program is used. An op whose k
+ * needs more than one register-resident range per wave (k > 16384, or k > 8192 for
+ * GATE_UP_GELU), or whose x rows exceed the LDS, is UNSUPPORTED. spin_limit bounds how
+ * long a workgroup polls for the others at an op boundary (0: the default, about 2 s);
+ * a run that exceeds it gives up, leaving its outputs undefined, and the next
+ * hyp_step_program_check reports it. */
+HypStatus hyp_step_program_create(const HypStepOp* ops, uint32_t n_ops, uint32_t m, uint32_t spin_limit,
+                                  HypStepProgram* out_program);
+/* Enqueue one run on stream (one cooperative launch; not recordable into a graph: the
+ * call returns INVALID_ARGUMENT while the stream is capturing). Runs of one program must
+ * be ordered (one stream). */
+HypStatus hyp_step_program_run(HypStepProgram program, HypStream stream);
+/* Wait for the device; INTERNAL if a run since the last check gave up waiting (the
+ * program is then reset and can run again), else OK. */
+HypStatus hyp_step_program_check(HypStepProgram program);
+HypStatus hyp_step_program_free(HypStepProgram* program);
+
 /* ---- weight residency (load_model_weights, weights_loader.cc:71-153) ------------ */
 
 /* Load every *.safetensors shard in dir, resolve the MLX names

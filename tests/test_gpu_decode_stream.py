@@ -263,3 +263,112 @@ def test_capture_refuses_allocating_calls(stream):
     graph.close()
     for a in (qw, up, x1, xm, y1, ym):
         a.close()
+
+
+# ---------------------------------------------------------------- decode-step program
+
+def _zero(arrays, stream):
+    for a in arrays:
+        a.upload(np.zeros(a.shape, a.dtype), stream)
+
+
+def _program_vs_eager(model, layers, m, stream, seed, reps=2):
+    """Run `layers` layers of the model as a step program and as the eager launch sequence
+    from the same input; every buffer must be equal bit for bit, on every run."""
+    h0 = syn.activations(m, syn.HIDDEN, seed=seed)
+    b = dc.StepBuffers(hy, m, h0, stream)
+    for proj in model.layers[:layers]:
+        dc.decode_layer(hy, proj, m, b, stream)
+    eager = {name: getattr(b, name).to_host(stream) for name in ("h", "q", "k", "v", "o", "g")}
+    sub = dc.DecodeModel.__new__(dc.DecodeModel)
+    sub.hy, sub.layers = hy, model.layers[:layers]
+    prog = dc.layer_program(sub, m, b)
+    for rep in range(reps):
+        b.h.upload(h0, stream)
+        _zero((b.q, b.k, b.v, b.o, b.g), stream)
+        say(f"step program: {layers} layers m={m} run {rep}")
+        prog.run(stream)
+        stream.synchronize()
+        prog.check()
+        for name, want in eager.items():
+            np.testing.assert_array_equal(getattr(b, name).to_host(stream), want,
+                                          err_msg=f"{layers} layers m={m} run {rep}: {name}")
+    prog.close()
+    b.close()
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_step_program_two_layers_equals_eager(model, stream, m):
+    _program_vs_eager(model, 2, m, stream, seed=3100 + m)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_step_program_48_layers_equals_eager(model, stream, m):
+    """The whole 48-layer stack (192 ops) in one launch, three runs in a row."""
+    _program_vs_eager(model, syn.NUM_LAYERS, m, stream, seed=3200 + m, reps=3)
+
+
+def test_step_program_ragged_segments_and_odd_groups(stream):
+    """Ops over small ragged shapes: three segments of 3, 2 and 1 row tiles (n = 40, 24, 8,
+    partly empty last tiles), an odd group count (k = 192) and a gate/up pair of n = 40,
+    chained through one buffer; against the per-call entry points, bit for bit."""
+    k = 192
+    ws = [hy.QWeight.from_host(*syn.q4_weights(n, k, seed=3300 + n)) for n in (40, 24, 8)]
+    gate = hy.QWeight.from_host(*syn.q4_weights(40, k, seed=3310))
+    up = hy.QWeight.from_host(*syn.q4_weights(40, k, seed=3311))
+    for m in (1, 2, 3, 4):
+        x0 = syn.activations(m, k, seed=3320 + m)
+        x = dev(x0, stream)
+        ya, yb, yc = (hy.DeviceArray((m, n), np.uint16) for n in (40, 24, 8))
+        g = hy.DeviceArray((m, 40), np.uint16)
+        hy.qmatmul_group(ws, x, m, [ya, yb, yc], stream, rms_eps=1e-6)
+        hy.qmlp_gate_up_gelu(gate, up, x, m, g, stream)
+        hy.qmatmul_group(ws[:2], x, m, [ya, yb], stream)
+        want = [a.to_host(stream) for a in (ya, yb, yc, g)]
+        _zero((ya, yb, yc, g), stream)
+        prog = hy.StepProgram([
+            (hy.STEP_QMATMUL_RMSNORM, ws, x, [ya, yb, yc], 1e-6),
+            (hy.STEP_GATE_UP_GELU, [gate, up], x, [g], 0.0),
+            (hy.STEP_QMATMUL, ws[:2], x, [ya, yb], 0.0),
+        ], m)
+        prog.run(stream)
+        stream.synchronize()
+        prog.check()
+        for got, w, name in zip((ya, yb, yc, g), want, ("a", "b", "c", "gate/up")):
+            np.testing.assert_array_equal(got.to_host(stream), w, err_msg=f"m={m} {name}")
+        prog.close()
+        for a in (x, ya, yb, yc, g):
+            a.close()
+    for q in ws + [gate, up]:
+        q.close()
+
+
+def test_step_program_gives_up_and_recovers(model, stream):
+    """A program whose spin limit is two polls gives up at an op boundary: every
+    workgroup leaves the launch, and check reports INTERNAL and resets it. A program with
+    the default limit then runs the same ops correctly."""
+    m = 1
+    h0 = syn.activations(m, syn.HIDDEN, seed=3400)
+    b = dc.StepBuffers(hy, m, h0, stream)
+    sub = dc.DecodeModel.__new__(dc.DecodeModel)
+    sub.hy, sub.layers = hy, model.layers[:8]
+    for proj in sub.layers:
+        dc.decode_layer(hy, proj, m, b, stream)
+    want = b.h.to_host(stream)
+    b.h.upload(h0, stream)
+    hasty = dc.layer_program(sub, m, b, spin_limit=1)
+    hasty.run(stream)
+    stream.synchronize()
+    with pytest.raises(hy.HypError) as e:
+        hasty.check()
+    assert e.value.status_name == "INTERNAL" and "gave up" in str(e.value)
+    hasty.check()   # reset: nothing pending
+    hasty.close()
+    prog = dc.layer_program(sub, m, b)
+    b.h.upload(h0, stream)
+    prog.run(stream)
+    stream.synchronize()
+    prog.check()
+    np.testing.assert_array_equal(b.h.to_host(stream), want)
+    prog.close()
+    b.close()
