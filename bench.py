@@ -14,9 +14,9 @@ Also reported, each on its own workload:
               (TFLOP/s vs bf16 MFMA peak)
   decode      48 layers (renormalise + q/k/v in one launch, o, fused gate/up + GELU, down)
               + tied LM head [262144,3840] with softcap + greedy sampling on the device,
-              m = 1 and 4, replayed from a captured HIP graph (tokens/s and effective
-              HBM GB/s), with the LM head and sampling timed alone and the per-layer time
-              and rate derived from the two
+              m = 1 and 4, replayed from a captured HIP graph (tokens/s and effective HBM
+              GB/s); the head timed alone (per-layer figures); and the layer stack as one
+              decode-step program launch
 and the oracle's restatement of MLX's CPU quantized_matmul timed on this host's cores
 (cpu_baseline).
 
@@ -228,31 +228,49 @@ def bench_prefill(stream, m, steps, warmup, dense=None):
 
 
 def bench_decode_stream(model, m, steps, warmup, stream):
+    """One decode step at batch m: the 48-layer stack's 192 per-op launches and the head
+    (renormalise, softcap LM head, greedy sampling) replayed from one graph. Also timed: the
+    head alone, from which the per-layer figures are derived, and the same layer stack as
+    one step-program launch followed by the head's graph."""
     b = dc.StepBuffers(hy, m, syn.activations(m, HIDDEN, seed=77), stream)
-    with hy.Graph.capture(stream) as graph:
-        dc.decode_step(model, m, b, stream)
-    ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup)
-    graph.close()
     with hy.Graph.capture(stream) as head:
         dc.lm_head(model, m, b, stream)
     head_ms = time_launches(stream, lambda _i: head.launch(stream), steps, warmup)
+    with hy.Graph.capture(stream) as graph:
+        dc.decode_step(model, m, b, stream)
+    graph_ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup)
+    graph.close()
+    prog = dc.layer_program(model, m, b)
+
+    def step(_i):
+        prog.run(stream)
+        head.launch(stream)
+
+    ms = time_launches(stream, step, steps, warmup)
+    prog.check()
+    prog.close()
     head.close()
     b.close()
     layers = len(model.layers)
     nbytes = model.weight_bytes + dc.step_activation_bytes(layers, m)
     head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + 2 * syn.VOCAB) + 12 * m
     layer_bytes = (nbytes - head_bytes) / max(layers, 1)
-    layer_us = (ms - head_ms) * 1e3 / max(layers, 1)
-    out = {"m": m, "ms_per_step": round(ms, 4), "tokens_per_s": round(m / (ms / 1e3), 1),
-           "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-           "bytes_per_step": nbytes, "launches_per_step": dc.LAUNCHES_PER_LAYER * layers + 3,
-           "lm_head_us": round(head_ms * 1e3, 1),
-           "lm_head_gbs": round(head_bytes / head_ms / 1e6, 1),
-           "layer_us": round(layer_us, 2),
-           "layer_gbs": round(layer_bytes / layer_us / 1e3, 1)}
-    log(f"decode stream m={m}: {ms:.3f} ms/step = {out['tokens_per_s']:.0f} tok/s, {out['gbs']:.0f} GB/s; "
-        f"LM head {out['lm_head_us']} us ({out['lm_head_gbs']} GB/s), layer {out['layer_us']} us "
-        f"({out['layer_gbs']} GB/s)")
+
+    def rates(step_ms):
+        layer_us = (step_ms - head_ms) * 1e3 / max(layers, 1)
+        return {"ms_per_step": round(step_ms, 4), "tokens_per_s": round(m / (step_ms / 1e3), 1),
+                "gbs": round(nbytes / step_ms / 1e6, 1),
+                "frac_of_hbm_peak": round(nbytes / step_ms / 1e6 / HBM_PEAK_GBS, 4),
+                "layer_us": round(layer_us, 2), "layer_gbs": round(layer_bytes / layer_us / 1e3, 1)}
+
+    out = {"m": m, **rates(graph_ms), "bytes_per_step": nbytes,
+           "launches_per_step": dc.LAUNCHES_PER_LAYER * layers + 3,
+           "lm_head_us": round(head_ms * 1e3, 1), "lm_head_gbs": round(head_bytes / head_ms / 1e6, 1),
+           "step_program": {**rates(ms), "launches_per_step": 4}}
+    log(f"decode stream m={m}: per-op launches (graph) {graph_ms:.3f} ms/step = {out['tokens_per_s']:.0f} tok/s, "
+        f"{out['gbs']:.0f} GB/s, layer {out['layer_us']} us ({out['layer_gbs']} GB/s); step program "
+        f"{ms:.3f} ms = {out['step_program']['tokens_per_s']:.0f} tok/s, layer {out['step_program']['layer_us']} us; "
+        f"LM head {out['lm_head_us']} us ({out['lm_head_gbs']} GB/s)")
     return out
 
 

@@ -336,13 +336,14 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
 }
 
 // Workgroups of 16 waves (16 / splits row tiles each), so that one workgroup per compute
-// unit stages x once; the softcap head, whose grid is many workgroups per compute unit,
-// uses 4.
+// unit stages x once; the fused gate/up uses 8 (two workgroups per compute unit, so one
+// streams while the other finishes), and the softcap head, whose grid is many workgroups
+// per compute unit, 4.
 template <int M>
 void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, bool norm,
                      hipStream_t stream) {
     if (dual) {
-        launch_skinny_t<M, true, 0, kSkinnyWaves>(p, tiles_total, stream);
+        launch_skinny_t<M, true, 0, kSkinnyDualWaves>(p, tiles_total, stream);
     } else if (epi == Epilogue::kSoftcap) {
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
     } else if (norm) {
@@ -391,11 +392,12 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
     //  * the softcap head (262144 rows, 4-wave workgroups, many per compute unit): 1
     //    (95 vs 100 us at m = 1, 111 vs 123 us at m = 4 with 2);
     //  * the fused gate/up: the plain rule over its interleaved gate and up tiles (`tiles`
-    //    counts both), at most 8 so that a workgroup holds both halves of a row tile
-    //    ([15360,3840]: 1920 tiles, 4 splits, the same as the plain launch of gate or up).
+    //    counts both), at most 4 so that an 8-wave workgroup holds both halves of a row
+    //    tile ([15360,3840]: 1920 tiles, 4 splits, the same as the plain launch of gate or
+    //    up; 8-wave workgroups measured 14.x us against 16.5 with 16 waves at m = 1).
     (void)m;   // the measured choices did not depend on the row count
     const uint32_t cus = device_compute_units();
-    const uint32_t cap = form == SkinnyForm::kDual ? kSkinnyWaves / 2u : kSkinnyWaves;
+    const uint32_t cap = form == SkinnyForm::kDual ? kSkinnyDualWaves / 2u : kSkinnyWaves;
     uint32_t s = 1u;
     if (form == SkinnyForm::kHead) {
         s = 1u;
@@ -409,7 +411,7 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
 
 bool skinny_supported(uint32_t m, uint32_t k, bool dual) {
     return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
-           skinny_lds_bytes(m, k, dual, kSkinnyWaves) <= max_lds_per_block();
+           skinny_lds_bytes(m, k, dual, dual ? kSkinnyDualWaves : kSkinnyWaves) <= max_lds_per_block();
 }
 
 bool skinny_norm_supported(uint32_t m, uint32_t k) {
@@ -431,7 +433,7 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
         splits = choose_skinny_splits(dual ? 2u * d.tiles : d.tiles, d.pairs, m,
                                       head ? SkinnyForm::kHead : (dual ? SkinnyForm::kDual : SkinnyForm::kPlain));
     }
-    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u || (!head && splits == 8u) || (!head && !dual && splits == 16u),
+    HYP_REQUIRE(splits == 1u || splits == 2u || splits == 4u || (!head && !dual && (splits == 8u || splits == 16u)),
                 HYP_STATUS_INTERNAL, "skinny: bad split count");
     HYP_REQUIRE(d.pairs >= splits, HYP_STATUS_INTERNAL, "skinny: fewer group pairs than splits");
     SkinnyParams p{};

@@ -17,6 +17,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kMaxSegments = 3;   // projections sharing x in one grouped launch
 constexpr int kSkinnyWaves = 16;        // waves per workgroup (the softcap head uses 4)
+constexpr int kSkinnyDualWaves = 8;     // the fused gate/up: two workgroups per compute unit
 constexpr uint32_t kSkinnyPairsUpFront = 8;   // two batches of 4 pairs: a wave's whole range at once
 
 constexpr uint32_t kNibbleMask = 0x000F000Fu;

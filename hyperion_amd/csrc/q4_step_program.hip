@@ -11,9 +11,9 @@
 // weights are already in flight while it is waited for:
 //
 //   for each op i:
+//     arrive for op i - 1 (this workgroup's outputs of op i - 1 are complete)
 //     issue this wave's weight loads for op i (they do not depend on the activations)
-//     arrive for op i - 1 (this workgroup's outputs of op i - 1 are complete), then wait
-//       until every workgroup has arrived for op i - 1
+//     wait until every workgroup has arrived for op i - 1
 //     stage op i's input x into LDS (coherent loads), compute, reduce, store y (coherent)
 //
 // Coherence across the 8 XCDs (each with its own L2): activations cross workgroups only
@@ -82,19 +82,24 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t xr, uint32_t of
         xv[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16u * t, 0, kCoherent));
 }
 
-// Arrive for op `prev` and wait until every workgroup has. Every wave calls it; the
-// caller's stores of op `prev` are complete (the storing waves waited for them). Returns
-// false when the wait gave up (spin limit, or another workgroup's error).
-__device__ __forceinline__ bool arrive_and_wait(uint32_t* sync, uint32_t prev, uint32_t target, uint32_t spin_limit,
-                                                uint32_t* ctl, uint32_t tid, uint32_t lane, uint32_t wave) {
-    // Every wave is past op `prev`. The barrier waits for LDS only (s_waitcnt lgkmcnt(0)
-    // on gfx950), so the next op's weight loads stay in flight; its fences keep the compiler
-    // from moving the arrival above it.
+// Arrive for op `prev`: every wave is past it and the storing waves' outputs are
+// complete. Called before the next op's weight loads are issued, so the arrival (a
+// vector-memory atomic) does not queue behind them in the compute unit's memory pipeline.
+__device__ __forceinline__ void arrive(uint32_t* sync, uint32_t prev, uint32_t tid) {
+    // The barrier waits for LDS only (s_waitcnt lgkmcnt(0) on gfx950); its fences keep the
+    // compiler from moving the arrival above it.
     __syncthreads();
-    uint32_t* ctr = sync + kSyncCounters + prev * kStepSlots * kSyncStride;
     if (tid == 0u)
-        __hip_atomic_fetch_add(ctr + (blockIdx.x % kStepSlots) * kSyncStride, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_fetch_add(sync + kSyncCounters + (prev * kStepSlots + blockIdx.x % kStepSlots) * kSyncStride, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Wait until every workgroup has arrived for op `prev`. Returns false when the wait gave up
+// (spin limit, or another workgroup's error). The polls queue behind this workgroup's
+// weight loads already in flight, so the first one returns about when those have landed.
+__device__ __forceinline__ bool wait_all(uint32_t* sync, uint32_t prev, uint32_t target, uint32_t spin_limit,
+                                         uint32_t* ctl, uint32_t lane, uint32_t wave) {
+    uint32_t* ctr = sync + kSyncCounters + prev * kStepSlots * kSyncStride;
     if (wave == 0u) {
         uint32_t done = 0u;
         for (uint32_t spin = 0;; ++spin) {
@@ -138,10 +143,12 @@ __device__ __forceinline__ void stage_x(ConstStepOp& d, const OpLds& L, bool nor
         }
         __syncthreads();
     }
+    // With at most one unit per thread the rms pass's loads are kept for the staging pass.
+    const bool reload = !norm || units > kThreads;
     for (uint32_t u = tid; u < units; u += kThreads) {
         const uint32_t m = unit_row<M>(u, G);
         const uint32_t g = u - m * G;
-        load_unit(xr, (m * k + g * 64u) * 2u, xv);
+        if (reload) load_unit(xr, (m * k + g * 64u) * 2u, xv);
         if (norm) normalize_unit(xv, L.part[units + m]);
         float s0 = 0.0f;
         float s1 = 0.0f;
@@ -196,14 +203,16 @@ struct BlockLoads {
     uint32_t n;
     uint32_t tile;
     uint32_t gtile;
+    LaneMatrix lm;
 };
 
 // Issue this wave's weight loads of block vb (16 / S row tiles, S waves per tile, as one
-// workgroup of the per-call kernel). A plain op's segment is read by index, so only its
+// workgroup of the per-call kernel); with first_only, only the scales and the first batch
+// of four pairs (the second batch is issued by the caller). A plain op's segment is read by index, so only its
 // fields are live; a gate/up op alternates gate and up tiles (virtual tile 2t is gate
 // tile t, 2t + 1 up tile t).
 __device__ __forceinline__ void issue_block(ConstStepOp& d, bool dual, uint32_t vb, const WaveRange& r,
-                                            BlockLoads& bl) {
+                                            BlockLoads& bl, bool first_only) {
     const uint32_t gtile = (vb << (4u - r.sh)) + (r.wave >> r.sh);
     const uint4* codes;
     const uint2* sb;
@@ -238,7 +247,8 @@ __device__ __forceinline__ void issue_block(ConstStepOp& d, bool dual, uint32_t 
     for (int b = 0; b < 4; ++b)
         bl.sbl[0][b] = __builtin_amdgcn_raw_buffer_load_b32(lm.sb, off, (r.first + 2u * b) * 128u, kStreamPolicy);
     load_batch<4, false>(lm, r.first, r.last, bl.ba);
-    load_batch<4, false>(lm, r.first + 4u, r.last, bl.bb);
+    if (!first_only) load_batch<4, false>(lm, r.first + 4u, r.last, bl.bb);
+    bl.lm = lm;
 }
 
 // Compute a block's loads against the staged x, reduce the splits and store the rows
@@ -298,13 +308,18 @@ __device__ __forceinline__ bool run_op(ConstStepOp& d, uint32_t op, uint32_t* sy
 
     BlockLoads bl;
     const bool have = blockIdx.x < vbs;   // workgroup-uniform
-    if (have) issue_block(d, dual, blockIdx.x, r, bl);
-    if (op > 0u && !arrive_and_wait(sync, op - 1u, target, spin_limit, L.ctl, r.tid, r.lane, r.wave)) return false;
+    // The first batch goes out before the wait and the second after x is staged: every
+    // later vector-memory request of the compute unit (the polls, the x loads) queues behind
+    // the loads already issued, so a deeper prefetch delays the op's start.
+    if (op > 0u) arrive(sync, op - 1u, r.tid);
+    if (have) issue_block(d, dual, blockIdx.x, r, bl, true);
+    if (op > 0u && !wait_all(sync, op - 1u, target, spin_limit, L.ctl, r.lane, r.wave)) return false;
     if (!have) return true;
     stage_x<M>(d, L, norm, k, G, WS, r.tid, r.lane, r.wave);
+    load_batch<4, false>(bl.lm, r.first + 4u, r.last, bl.bb);
     finish_block<M>(bl, dual, L, G, WS, r);
     for (uint32_t vb = blockIdx.x + gridDim.x; vb < vbs; vb += gridDim.x) {
-        issue_block(d, dual, vb, r, bl);
+        issue_block(d, dual, vb, r, bl, false);
         __syncthreads();   // the previous block's reduction and combine areas have been read
         finish_block<M>(bl, dual, L, G, WS, r);
     }

@@ -73,7 +73,7 @@ StepProgram::StepProgram(const std::vector<StepOpSpec>& specs, uint32_t m, uint3
         HYP_REQUIRE(per_wave <= kMaxPairsPerWave, HYP_STATUS_UNSUPPORTED,
                     who + "k = " + std::to_string(k) + " leaves " + std::to_string(per_wave) +
                         " group pairs per wave, more than one launch holds in registers");
-        HYP_REQUIRE(splits >= 1u && splits <= (dual ? hip::kStepWaves / 2u : hip::kStepWaves) && pairs >= splits,
+        HYP_REQUIRE(splits >= 1u && splits <= (dual ? 4u : hip::kStepWaves) && pairs >= splits,
                     HYP_STATUS_INTERNAL, who + "bad split");
         if (s.form == StepForm::kNorm) {
             HYP_REQUIRE(std::isfinite(s.eps) && s.eps >= 0.0f, HYP_STATUS_INVALID_ARGUMENT,

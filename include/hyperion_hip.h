@@ -293,7 +293,7 @@ typedef struct HypStepOp {
 
 /* Validate the ops for m rows (1..4) and keep a device copy of them. The weights and
  * buffers are borrowed: they must stay valid while the program is used. An op whose k
- * needs more than one register-resident range per wave (k > 16384, or k > 8192 for
+ * needs more than one register-resident range per wave (k > 16384, or k > 4096 for
  * GATE_UP_GELU), or whose x rows exceed the LDS, is UNSUPPORTED. spin_limit bounds how
  * long a workgroup polls for the others at an op boundary (0: the default, about 2 s);
  * a run that exceeds it gives up, leaving its outputs undefined, and the next
