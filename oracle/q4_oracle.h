@@ -30,9 +30,12 @@
  *                           holds q=15; sign/zero-point invariants on all groups;
  *                           closed-form cases (exact grids, constant and zero groups).
  *   orc_dequantize_q4g64    pinned where the value is exact (power-of-two scales, bias
- *                           grids) and by the fixture round trip; the choice between
- *                           single and double bf16 rounding is parity unpinned (no
- *                           committed dequantized values exist in the reference).
+ *                           grids) and by the fixture round trip; mode 1 (one rounding)
+ *                           is the correctly rounded value, checked exactly on the decode
+ *                           workload's weights. The choice between single (mode 1) and
+ *                           double (mode 0) bf16 rounding is parity unpinned (no
+ *                           committed dequantized values exist in the reference); the two
+ *                           differ on 38% of those weights.
  *   orc_qmatmul_f64         pinned: closed-form known-answer cases and brute force.
  *   orc_qmatmul_deq_f64     pinned: equals orc_qmatmul_f64 wherever the dequantized
  *                           weights are exact in bf16, and brute force over
@@ -40,11 +43,19 @@
  *   orc_qmatmul_f32_grouped pinned: exact-arithmetic known-answer cases (every partial
  *                           sum representable) and against orc_qmatmul_f64.
  *   orc_qmatmul_mlx_cpu     parity unpinned: restates MLX's scalar CPU loop with
- *                           bf16-typed accumulation; only an MLX import could pin it.
- *                           Used only to report the reference-side error.
- *   orc_gelu_tanh_mul_bf16  pinned against the closed-form fp64 GELU within the
- *                           rounding the bf16 op chain implies, and special values.
- *   orc_softcap_bf16        pinned likewise against 30*tanh(x/30) in fp64.
+ *                           bf16-typed accumulation; only an MLX import could pin that
+ *                           MLX runs this loop. The loop as restated is pinned: its
+ *                           per-element step equals an exact-rational evaluation of
+ *                           dq = bf16(bf16(s*q) + b), sum = bf16(sum + bf16(x*dq)) on
+ *                           small cases, and the bf16 sum stalls at 256 when adding 1.
+ *                           Used only to report the reference-side error and the CPU
+ *                           baseline.
+ *   orc_gelu_tanh_mul_bf16  pinned bit-exactly over all 65,536 bf16 inputs against an
+ *                           exact-arithmetic evaluation of the reference's op order
+ *                           (fp32 result of each op rounded to bf16, tanh from fp64),
+ *                           except the inputs whose tanh lies within 2^-20 of a bf16
+ *                           rounding boundary (counted, under 200).
+ *   orc_softcap_bf16        pinned likewise over all bf16 inputs, caps 30 and 50.
  *   orc_qmatmul_mlx_cpu_mt  pinned to orc_qmatmul_mlx_cpu: bit-identical outputs.
  *   orc_sample_greedy_bf16  pinned: against the definition computed independently with
  *                           numpy (first index of the maximum over non-NaN values, the

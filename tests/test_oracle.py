@@ -395,3 +395,169 @@ def test_sample_greedy_restatement_matches_definition():
     assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 3, 2]))) == (1, 3.0, True)
     assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 2.5, 2]))) == (1, 3.0, False)
     assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 2.75, 2]))) == (1, 3.0, True)
+
+
+# ---------------------------------------------------------------- exhaustive pins of the bf16 op chains
+#
+# Independent restatements of the reference's op chains (forward.cc:154-160 softcap,
+# forward.cc:324-336 gelu_pytorch_tanh, forward.cc:338-343 the gating product), evaluated
+# over all 65,536 bf16 inputs. Each MLX op on bf16 arrays computes in fp32 and rounds the
+# result to bf16; here every op is evaluated exactly in float64 (a product of two bf16
+# values has at most 16 significant bits; a sum of two whose exponents differ by more
+# than 29 rounds to the larger operand in fp32 either way), then rounded to fp32 and to
+# bf16 with an integer round-half-even of the bit pattern. tanh comes from float64;
+# inputs whose float64 tanh lies within 2^-20 (relative) of a bf16 rounding boundary are
+# excluded and counted, since fp32 tanhf may round to the other side there.
+
+def _rne_bf16_of_f32(f32):
+    """float32 array -> bf16 values (as float64), round half to even on the bit pattern."""
+    f = np.atleast_1d(np.asarray(f32, np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    out = (r.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    out[np.isnan(f)] = np.nan
+    return out if np.ndim(f32) else out[0]
+
+
+def _op(v64):
+    """One MLX bf16 op: the exact value, to fp32, to bf16."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        return _rne_bf16_of_f32(np.asarray(v64, np.float64).astype(np.float32))
+
+
+def _near_bf16_boundary(v64, rel=2.0**-20):
+    """True where v64 is within rel of a midpoint between two adjacent bf16 values."""
+    v = np.abs(np.asarray(v64, np.float64))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        e = np.floor(np.log2(np.where(v > 0, v, 1.0)))
+    ulp = np.exp2(np.maximum(e, -126.0) - 7.0)
+    frac = v / ulp - np.floor(v / ulp)
+    return (np.abs(frac - 0.5) * ulp <= rel * np.maximum(v, 1e-300)) & (v > 0)
+
+
+def _all_bf16():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(invalid="ignore"):
+        vals = syn.bf16_to_f32(bits).astype(np.float64)
+    return bits, vals
+
+
+def _cmp_bits(got_bits, want64, keep, what):
+    got = syn.bf16_to_f32(got_bits).astype(np.float64)
+    both_nan = np.isnan(got) & np.isnan(want64)
+    same = (got == want64) & (np.signbit(got) == np.signbit(want64))
+    bad = keep & ~(same | both_nan)
+    assert not bad.any(), f"{what}: {int(bad.sum())} inputs differ, first at bits {np.nonzero(bad)[0][:5]}"
+
+
+def test_gelu_chain_bit_exact_over_all_bf16_inputs():
+    bits, x = _all_bf16()
+    c_coeff = _op(0.044715)        # mx::array(0.044715F, bf16)
+    c_inner = _op(0.7978845608028654)
+    with np.errstate(over="ignore", invalid="ignore"):
+        sq = _op(x * x)                          # square(x)
+        x3 = _op(x * sq)                         # multiply(x, square(x))
+        inner = _op(c_coeff * x3)
+        inner = _op(inner + x)
+        inner = _op(c_inner * inner)
+        t64 = np.tanh(inner)
+        t = _op(t64)
+        half_x = _op(0.5 * x)
+        one_t = _op(1.0 + t)
+        want = _op(half_x * one_t)
+    keep = ~_near_bf16_boundary(t64)
+    excluded = int((~keep).sum())
+    print(f"gelu chain: {excluded} of 65536 inputs excluded (tanh within 2^-20 of a bf16 tie)")
+    assert excluded < 200
+    _cmp_bits(O.gelu_tanh(bits), want, keep, "gelu chain")
+    # the gating product with a second operand, over a sweep of up values
+    rng = np.random.default_rng(5)
+    up_bits = syn.bf16_bits(rng.standard_normal(65536).astype(np.float32))
+    up = syn.bf16_to_f32(up_bits).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want_mul = _op(want * up)
+    _cmp_bits(O.gelu_tanh_mul(bits, up_bits), want_mul, keep, "gelu * up")
+
+
+def test_softcap_bit_exact_over_all_bf16_inputs():
+    bits, x = _all_bf16()
+    for cap in (30.0, 50.0):
+        c = _op(cap)                                   # mx::array(cap, logits dtype)
+        with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+            d = _op(x / c)                             # divide: correctly rounded fp32, then bf16
+            t64 = np.tanh(d)
+            want = _op(_op(t64) * c)
+        keep = ~_near_bf16_boundary(t64)
+        excluded = int((~keep).sum())
+        print(f"softcap {cap}: {excluded} of 65536 inputs excluded")
+        assert excluded < 200
+        _cmp_bits(O.softcap(bits, cap), want, keep, f"softcap {cap}")
+
+
+def test_mlx_cpu_restatement_per_element_step_exact():
+    """The MLX CPU loop's per-element step, restated with exact rationals: dq = bf16(
+    bf16(scale * q) + bias); sum = bf16(sum + bf16(x * dq)), in k order, each op an fp32
+    result rounded to bf16. Small random cases, compared bit for bit."""
+    rng = np.random.default_rng(21)
+
+    def rne32(fr):
+        """Round a rational to float32, half to even (exact)."""
+        return float(np.float32(float(fr))) if fr == Fraction(float(fr)) else _rne_rational_f32(fr)
+
+    def op(fr):
+        return Fraction(rne_bf16(Fraction(rne32(fr))))
+
+    for case in range(6):
+        m, n, k = 2, 3, 128
+        x = syn.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+        codes = rng.integers(0, 16, size=(n, k)).astype(np.uint8)
+        w = syn.pack_codes(codes)
+        s = syn.bf16_bits((np.abs(rng.standard_normal((n, k // 64))) * 0.05).astype(np.float32))
+        b = syn.bf16_bits((-rng.random((n, k // 64)) * 0.4).astype(np.float32))
+        got = O.qmatmul_mlx_cpu(x, w, s, b)
+        xf = [[Fraction(float(v)) for v in row] for row in syn.bf16_to_f32(x)]
+        sf = syn.bf16_to_f32(s)
+        bfv = syn.bf16_to_f32(b)
+        for i in range(m):
+            for r in range(n):
+                acc = Fraction(0)
+                for kk in range(k):
+                    g = kk // 64
+                    dq = op(op(Fraction(float(sf[r, g])) * int(codes[r, kk])) + Fraction(float(bfv[r, g])))
+                    acc = op(acc + op(xf[i][kk] * dq))
+                assert syn.bf16_bits(np.float32(float(acc))) == got[i, r], (case, i, r)
+
+
+def _rne_rational_f32(fr):
+    """Round a rational to the nearest float32 (half to even), exactly."""
+    if fr == 0:
+        return 0.0
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = math.floor(math.log2(a))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 23)
+    return sign * float(round(a / ulp) * ulp)
+
+
+def test_dequantize_modes_mismatch_rate_on_the_decode_weights():
+    """(A) bf16(bf16(s*q) + b) against (B) bf16(fma(s, q, b)) on the decode workload's
+    weights [15360, 3840] (bias = -8 * scale). There s*q + b is exact in fp32 (at most 12
+    significant bits), so (B) is the correctly rounded value: checked exactly on a sample.
+    (A) rounds s*q to 8 bits before the subtraction and differs on a large fraction of
+    values (printed; which one MLX uses is parity unpinned)."""
+    w, s, b = syn.q4_weights(15360, 3840, seed=105)
+    a = O.dequantize(w, s, b, mode=0)
+    bb = O.dequantize(w, s, b, mode=1)
+    rate = float(np.mean(a != bb))
+    print(f"dequantize (A) vs (B): {rate:.4%} of {a.size} values differ")
+    codes = syn.unpack_codes(w[:64])
+    sf = syn.bf16_to_f32(s[:64]).astype(np.float64)
+    bf = syn.bf16_to_f32(b[:64]).astype(np.float64)
+    exact = sf.repeat(64, axis=1) * codes + bf.repeat(64, axis=1)     # exact in float64
+    np.testing.assert_array_equal(bb[:64], syn.bf16_bits(exact.astype(np.float32)))
+    assert 0.2 < rate < 0.6
