@@ -47,7 +47,7 @@ EXPORTED = [
     "hyp_qmatmul", "hyp_qmatmul_noalloc", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
-    "hyp_sample_greedy",
+    "hyp_rope", "hyp_sample_greedy",
     "hyp_step_program_create", "hyp_step_program_run", "hyp_step_program_check", "hyp_step_program_free",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
@@ -90,6 +90,7 @@ class StepOp(ctypes.Structure):
         ("y", ctypes.c_void_p * 3),
         ("eps", ctypes.c_float),
         ("reserved", ctypes.c_uint32),
+        ("norm_weight", ctypes.c_void_p),
     ]
 
 
@@ -146,12 +147,13 @@ def lib() -> ctypes.CDLL:
         "hyp_qmatmul_noalloc": [_P, _P, _U32, _P, _P],
         "hyp_qmatmul_ex": [_P, _P, _U32, _P, ctypes.c_int, ctypes.c_float, _P],
         "hyp_qmatmul_group": [_P, _U32, _P, _U32, _P, _P],
-        "hyp_qmatmul_group_rmsnorm": [_P, _U32, _P, _U32, ctypes.c_float, _P, _P],
+        "hyp_qmatmul_group_rmsnorm": [_P, _U32, _P, _P, _U32, ctypes.c_float, _P, _P],
         "hyp_qmlp_gate_up_gelu": [_P, _P, _P, _U32, _P, _P],
         "hyp_quantize_q4g64": [_P, _U32, _U32, _P, _P, _P, _P],
         "hyp_dequantize_q4g64": [_P, _P, _P, _U32, _U32, _P, _U32, ctypes.c_float, _P, _P],
         "hyp_embed": [_P, _P, _U32, _P, _P],
-        "hyp_rms_normalize": [_P, _U32, _U32, ctypes.c_float, _P, _P],
+        "hyp_rms_normalize": [_P, _P, _U32, _U32, ctypes.c_float, _P, _P],
+        "hyp_rope": [_P, _U32, _U32, _U32, _U32, ctypes.c_float, _U32, _P, _P],
         "hyp_sample_greedy": [_P, _U32, _U32, _P, _P],
         "hyp_step_program_create": [_P, _U32, _U32, _U32, _PP],
         "hyp_step_program_run": [_P, _P],
@@ -417,12 +419,15 @@ class QModel:
 
 class StepProgram:
     """A decode-step program (hyp_step_program_*): ops is a list of (kind, weights, x, ys,
-    eps) with QWeight weights and DeviceArray buffers, all borrowed for the program's life."""
+    eps[, norm_weight]) with QWeight weights and DeviceArray buffers, all borrowed for the
+    program's life."""
 
     def __init__(self, ops, m: int, spin_limit: int = 0):
         arr = (StepOp * len(ops))()
         self._keep = []
-        for i, (kind, ws, x, ys, eps) in enumerate(ops):
+        for i, op in enumerate(ops):
+            kind, ws, x, ys, eps = op[:5]
+            norm_w = op[5] if len(op) > 5 else None
             o = arr[i]
             o.kind = kind
             o.count = len(ws)
@@ -432,7 +437,8 @@ class StepProgram:
             for q, y in enumerate(ys):
                 o.y[q] = y.ptr.value
             o.eps = eps
-            self._keep.append((ws, x, ys))
+            o.norm_weight = norm_w.ptr.value if norm_w is not None else None
+            self._keep.append((ws, x, ys, norm_w))
         self._h = ctypes.c_void_p()
         call("hyp_step_program_create", ctypes.cast(arr, _P), len(ops), m, spin_limit, ctypes.byref(self._h))
 
@@ -461,9 +467,11 @@ def qmatmul(w: QWeight, x: DeviceArray, m: int, y: DeviceArray, stream: Stream,
         call("hyp_qmatmul_ex", w.handle, x.ptr, m, y.ptr, EPILOGUE_SOFTCAP, softcap, stream.handle)
 
 
-def qmatmul_group(ws, x: DeviceArray, m: int, ys, stream: Stream, rms_eps: Optional[float] = None) -> None:
+def qmatmul_group(ws, x: DeviceArray, m: int, ys, stream: Stream, rms_eps: Optional[float] = None,
+                  norm_weight: Optional[DeviceArray] = None) -> None:
     """ys[i] = x . dequant(ws[i])^T for up to three weights sharing k (one launch at m <= 4);
-    with rms_eps, x is rms-normalised first (hyp_qmatmul_group_rmsnorm)."""
+    with rms_eps, x is rms-normalised first, with norm_weight if given
+    (hyp_qmatmul_group_rmsnorm)."""
     if len(ws) != len(ys):
         raise ValueError("qmatmul_group: one output per weight")
     handles = (ctypes.c_void_p * len(ws))(*[w.handle for w in ws])
@@ -471,7 +479,8 @@ def qmatmul_group(ws, x: DeviceArray, m: int, ys, stream: Stream, rms_eps: Optio
     if rms_eps is None:
         call("hyp_qmatmul_group", handles, len(ws), x.ptr, m, outs, stream.handle)
     else:
-        call("hyp_qmatmul_group_rmsnorm", handles, len(ws), x.ptr, m, rms_eps, outs, stream.handle)
+        call("hyp_qmatmul_group_rmsnorm", handles, len(ws), x.ptr, norm_weight.ptr if norm_weight is not None else None,
+             m, rms_eps, outs, stream.handle)
 
 
 def qmlp_gate_up_gelu(gate: QWeight, up: QWeight, x: DeviceArray, m: int, h: DeviceArray,
@@ -495,8 +504,17 @@ def embed(table: QWeight, ids: DeviceArray, n_ids: int, out: DeviceArray, stream
     call("hyp_embed", table.handle, ids.ptr, n_ids, out.ptr, stream.handle)
 
 
-def rms_normalize(x: DeviceArray, m: int, k: int, y: DeviceArray, stream: Stream, eps: float = 1e-6) -> None:
-    call("hyp_rms_normalize", x.ptr, m, k, eps, y.ptr, stream.handle)
+def rms_normalize(x: DeviceArray, m: int, k: int, y: DeviceArray, stream: Stream, eps: float = 1e-6,
+                  weight: Optional[DeviceArray] = None) -> None:
+    """mx::fast::rms_norm over m rows of k (hyp_rms_normalize); weight None is the
+    parameterless form."""
+    call("hyp_rms_normalize", x.ptr, weight.ptr if weight is not None else None, m, k, eps, y.ptr, stream.handle)
+
+
+def rope(x: DeviceArray, rows: int, heads: int, head_dim: int, rotated: int, base: float, offset: int,
+         y: DeviceArray, stream: Stream) -> None:
+    """mx::fast::rope (non-traditional) of x [rows, heads, head_dim] (hyp_rope)."""
+    call("hyp_rope", x.ptr, rows, heads, head_dim, rotated, base, offset, y.ptr, stream.handle)
 
 
 def sample_greedy(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, stream: Stream,

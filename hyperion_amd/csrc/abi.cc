@@ -498,7 +498,7 @@ HypStatus hyp_qmatmul_noalloc(HypQWeight weight, const void* x, uint32_t m, void
 namespace {
 
 void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m, const float* rms_eps,
-                   void* const* ys, HypStream stream) {
+                   const void* norm_weight, void* const* ys, HypStream stream) {
     REQUIRE_ARG(weights != nullptr && ys != nullptr, "weights and ys must be non-null arrays");
     REQUIRE_ARG(count >= 1u && count <= HYP_QMATMUL_GROUP_MAX, "count must be 1..HYP_QMATMUL_GROUP_MAX");
     const QuantizedLinear* lins[HYP_QMATMUL_GROUP_MAX];
@@ -516,7 +516,8 @@ void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uin
     const uint32_t k = lins[0]->mat.k;
     if (!(rms_eps != nullptr ? hyperion::hip::skinny_norm_supported(m, k) : hyperion::hip::skinny_supported(m, k, false)))
         require_not_capturing(s, "hyp_qmatmul_group on the GEMM path");
-    hyperion::model::apply_group(lins, outs, count, static_cast<const uint16_t*>(x), m, rms_eps, s);
+    hyperion::model::apply_group(lins, outs, count, static_cast<const uint16_t*>(x), m, rms_eps,
+                                 static_cast<const uint16_t*>(norm_weight), s);
 }
 
 }  // namespace
@@ -524,13 +525,14 @@ void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uin
 HypStatus hyp_qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
                             void* const* ys, HypStream stream) {
     return abi_call("hyp_qmatmul_group",
-                    [&] { qmatmul_group(weights, count, x, m, nullptr, ys, stream); });
+                    [&] { qmatmul_group(weights, count, x, m, nullptr, nullptr, ys, stream); });
 }
 
-HypStatus hyp_qmatmul_group_rmsnorm(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
-                                    float eps, void* const* ys, HypStream stream) {
+HypStatus hyp_qmatmul_group_rmsnorm(const HypQWeight* weights, uint32_t count, const void* x,
+                                    const void* norm_weight, uint32_t m, float eps, void* const* ys,
+                                    HypStream stream) {
     return abi_call("hyp_qmatmul_group_rmsnorm",
-                    [&] { qmatmul_group(weights, count, x, m, &eps, ys, stream); });
+                    [&] { qmatmul_group(weights, count, x, m, &eps, norm_weight, ys, stream); });
 }
 
 HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, uint32_t m, void* h,
@@ -587,13 +589,33 @@ HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void*
     });
 }
 
-HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, void* y, HypStream stream) {
+HypStatus hyp_rms_normalize(const void* x, const void* weight, uint32_t m, uint32_t k, float eps, void* y,
+                            HypStream stream) {
     return abi_call("hyp_rms_normalize", [&] {
         hipStream_t s = stream_of(stream);
         REQUIRE_ARG(std::isfinite(eps) && eps >= 0.0f, "eps must be finite and non-negative");
         if (m == 0 || k == 0) return;
         REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
-        hyperion::hip::launch_rms_normalize(static_cast<const uint16_t*>(x), m, k, eps, static_cast<uint16_t*>(y), s);
+        REQUIRE_ARG(weight == nullptr || (reinterpret_cast<uintptr_t>(weight) & 15u) == 0u || k % 64u != 0u,
+                    "the weight must be 16-byte aligned");
+        hyperion::hip::launch_rms_normalize(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weight), m, k,
+                                            eps, static_cast<uint16_t*>(y), s);
+    });
+}
+
+HypStatus hyp_rope(const void* x, uint32_t rows, uint32_t heads, uint32_t head_dim, uint32_t rotated_dims, float base,
+                   uint32_t offset, void* y, HypStream stream) {
+    return abi_call("hyp_rope", [&] {
+        hipStream_t s = stream_of(stream);
+        REQUIRE_ARG(head_dim > 0 && head_dim % 2 == 0, "head_dim must be a positive even number");
+        REQUIRE_ARG(rotated_dims % 2 == 0 && rotated_dims <= head_dim, "rotated_dims must be even and <= head_dim");
+        REQUIRE_ARG(std::isfinite(base) && base > 0.0f, "base must be finite and positive");
+        REQUIRE_ARG(static_cast<uint64_t>(offset) + rows <= (1ull << 24),
+                    "positions must stay below 2^24 (exact in fp32)");
+        if (rows == 0 || heads == 0) return;
+        REQUIRE_ARG(x != nullptr && y != nullptr, "x and y must be non-null device pointers");
+        hyperion::hip::launch_rope(static_cast<const uint16_t*>(x), rows, heads, head_dim, rotated_dims, base, offset,
+                                   static_cast<uint16_t*>(y), s);
     });
 }
 
@@ -634,6 +656,7 @@ HypStatus hyp_step_program_create(const HypStepOp* ops, uint32_t n_ops, uint32_t
             sp.x = static_cast<const uint16_t*>(o.x);
             for (uint32_t q = 0; q < 3u; ++q) sp.y[q] = static_cast<uint16_t*>(o.y[q]);
             sp.eps = o.eps;
+            sp.norm_w = static_cast<const uint16_t*>(o.norm_weight);
         }
         require_device();
         auto h = std::make_unique<HypStepProgramOpaque>();

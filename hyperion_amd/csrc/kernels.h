@@ -48,9 +48,10 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream);
 // One launch over `count` projections that share x (and k), e.g. q, k and v:
 // ys[i][m, n_i] = x . dequant(W_i)^T. With rms_eps non-null each x row is first
-// rms-normalised (q4_rmsnorm.h; the same bits as launch_rms_normalize) in LDS.
+// rms-normalised (q4_rmsnorm.h; the same bits as launch_rms_normalize with norm_w) in LDS;
+// norm_w is the norm's bf16 weight [k] or null.
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                            uint32_t m, const float* rms_eps, hipStream_t stream);
+                            uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream);
 // Splits for `tiles` 16-row tiles, `pairs` group pairs and m rows of one launch form,
 // and whether (m, k) fits the kernel's LDS staging.
 enum class SkinnyForm : int {
@@ -78,8 +79,15 @@ void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32
 void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t stream);
 // y = softcap(y) over `count` bf16 elements (in place).
 void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream);
-// y[r] = x[r] / sqrt(mean(x[r]^2) + eps) for each of m rows of k bf16 (y may equal x).
-void launch_rms_normalize(const uint16_t* x, uint32_t m, uint32_t k, float eps, uint16_t* y, hipStream_t stream);
+// y[r] = bf16(w * bf16(x[r] / sqrt(mean(x[r]^2) + eps))) for each of m rows of k bf16,
+// w the bf16 weight [k] or null (then y = bf16(x / ...)); y may equal x.
+void launch_rms_normalize(const uint16_t* x, const uint16_t* w, uint32_t m, uint32_t k, float eps, uint16_t* y,
+                          hipStream_t stream);
+
+// mx::fast::rope (non-traditional) of x [rows, heads, head_dim] at positions offset + r:
+// pairs (i, i + head_dim/2) with i < rotated/2 rotate, the rest are copied (y may equal x).
+void launch_rope(const uint16_t* x, uint32_t rows, uint32_t heads, uint32_t head_dim, uint32_t rotated, float base,
+                 uint32_t offset, uint16_t* y, hipStream_t stream);
 
 // ForwardPass::sample_greedy over each of `rows` rows of `vocab` bf16 logits -> out[row],
 // with slice states in `workspace` (device memory of sample_greedy_workspace_bytes(),

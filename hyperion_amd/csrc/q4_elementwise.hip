@@ -2,8 +2,8 @@
 // bf16 outputs and these kernels finish them:
 //   gelu_mul: h = bf16(gelu_chain(h) * u)      ForwardPass::mlp, forward.cc:338-343
 //   softcap:  y = bf16(tanh(y / cap) * cap)     ForwardPass::softcap, forward.cc:154-160
-// and the row renormalisation between chained projections:
-//   rms_normalize: y[r] = bf16(x[r] / sqrt(mean(x[r]^2) + eps)), fp32 statistics
+// and the row RMS norm (mx::fast::rms_norm with or without its learned weight):
+//   rms_normalize: y[r] = bf16(w * bf16(x[r] / sqrt(mean(x[r]^2) + eps))), fp32 statistics
 // Eight bf16 per thread (16-byte loads and stores; the pointers are 16-byte aligned).
 #include "common.h"
 #include "kernels.h"
@@ -66,8 +66,9 @@ __global__ __launch_bounds__(kThreads) void softcap_kernel(uint16_t* __restrict_
 }
 
 // One workgroup per row; each thread sums squares over a strided slice, the wave sums
-// meet in LDS, then the row is scaled in place or into y.
+// meet in LDS, then the row is scaled in place or into y (k not a multiple of 64).
 __global__ __launch_bounds__(kThreads) void rms_normalize_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w,
                                                                  uint16_t* __restrict__ y, uint32_t k, float eps) {
     __shared__ float partial[kThreads / 64];
     const uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * k;
@@ -82,9 +83,13 @@ __global__ __launch_bounds__(kThreads) void rms_normalize_kernel(const uint16_t*
     __syncthreads();
     float total = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) total += partial[w];
+    for (int wv = 0; wv < kThreads / 64; ++wv) total += partial[wv];
     const float inv = 1.0f / sqrtf(total / static_cast<float>(k) + eps);
-    for (uint32_t i = threadIdx.x; i < k; i += kThreads) yr[i] = f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) * inv);
+    for (uint32_t i = threadIdx.x; i < k; i += kThreads) {
+        float v = round_bf16(bf16_bits_to_f32(xr[i]) * inv);
+        if (w != nullptr) v = bf16_bits_to_f32(w[i]) * v;
+        yr[i] = f32_to_bf16_bits(v);
+    }
 }
 
 dim3 grid_for(uint64_t count) {
@@ -113,12 +118,14 @@ namespace {
 // the unit kept in registers between the two passes), the summation order of
 // q4_rmsnorm.h - the same bits as the skinny matmul's normalising prologue.
 __global__ __launch_bounds__(kThreads) void rms_normalize_units_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ w,
                                                                        uint16_t* __restrict__ y, uint32_t k,
                                                                        float eps) {
     extern __shared__ float part[];   // [k / 64] unit partials, then the row's inverse
     const uint32_t units = k / 64u;
     const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(blockIdx.x) * k);
     uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(blockIdx.x) * k);
+    const uint4* wr = reinterpret_cast<const uint4*>(w);
     const uint32_t tid = threadIdx.x;
     uint4 xv[8];
     for (uint32_t u = tid; u < units; u += kThreads) {
@@ -139,20 +146,69 @@ __global__ __launch_bounds__(kThreads) void rms_normalize_units_kernel(const uin
             for (int t = 0; t < 8; ++t) xv[t] = xr[u * 8u + t];
         }
         normalize_unit(xv, inv);
+        if (wr != nullptr) {
+            uint4 wv[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) wv[t] = wr[u * 8u + t];
+            weight_unit(xv, wv);
+        }
 #pragma unroll
         for (int t = 0; t < 8; ++t) yr[u * 8u + t] = xv[t];
     }
 }
 
+// Short rows (k a multiple of 64, at most 64 units): one wave per row, lane l owning
+// unit l. Each lane has at most one unit, so the order of q4_rmsnorm.h (lane l adds units
+// l, l + 64, ..., then the butterfly) is the same as rms_normalize_units_kernel's: the
+// same bits, for the many head-sized rows of q_norm / k_norm / v_norm.
+__global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ y, uint32_t rows,
+                                                                 uint32_t k, float eps) {
+    const uint32_t row = blockIdx.x * (kThreads / 64u) + (threadIdx.x >> 6);
+    if (row >= rows) return;   // wave-uniform
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t units = k / 64u;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * k);
+    uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * k);
+    uint4 xv[8];
+    float ss = 0.0f;
+    if (lane < units) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xv[t] = xr[lane * 8u + t];
+        ss = unit_sumsq(xv);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float inv = rms_inverse(ss, k, eps);
+    if (lane < units) {
+        normalize_unit(xv, inv);
+        if (w != nullptr) {
+            const uint4* wr = reinterpret_cast<const uint4*>(w);
+            uint4 wv[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) wv[t] = wr[lane * 8u + t];
+            weight_unit(xv, wv);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) yr[lane * 8u + t] = xv[t];
+    }
+}
+
 }  // namespace
 
-void launch_rms_normalize(const uint16_t* x, uint32_t m, uint32_t k, float eps, uint16_t* y, hipStream_t stream) {
+void launch_rms_normalize(const uint16_t* x, const uint16_t* w, uint32_t m, uint32_t k, float eps, uint16_t* y,
+                          hipStream_t stream) {
     if (m == 0 || k == 0) return;
-    if (k % 64u == 0u && k / 64u + 1u <= 16384u) {
+    if (k % 64u == 0u && k <= 64u * 64u) {
+        const uint32_t per_block = kThreads / 64u;
+        hipLaunchKernelGGL(rms_norm_rows_kernel, dim3((m + per_block - 1u) / per_block), dim3(kThreads), 0, stream,
+                           x, w, y, m, k, eps);
+    } else if (k % 64u == 0u && k / 64u + 1u <= 16384u) {
         const size_t lds = (k / 64u + 1u) * sizeof(float);
-        hipLaunchKernelGGL(rms_normalize_units_kernel, dim3(m), dim3(kThreads), lds, stream, x, y, k, eps);
+        hipLaunchKernelGGL(rms_normalize_units_kernel, dim3(m), dim3(kThreads), lds, stream, x, w, y, k, eps);
     } else {
-        hipLaunchKernelGGL(rms_normalize_kernel, dim3(m), dim3(kThreads), 0, stream, x, y, k, eps);
+        hipLaunchKernelGGL(rms_normalize_kernel, dim3(m), dim3(kThreads), 0, stream, x, w, y, k, eps);
     }
     HYP_HIP_CHECK(hipGetLastError());
 }

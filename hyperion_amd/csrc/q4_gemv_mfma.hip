@@ -223,7 +223,16 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
                 for (int t = 0; t < 8; ++t) xv[t] = src[t];
             }
-            if constexpr (NORM) normalize_unit(xv, part[units + m]);
+            if constexpr (NORM) {
+                normalize_unit(xv, part[units + m]);
+                if (p.norm_w != nullptr) {
+                    const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w + g * 64u);
+                    uint4 wv[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
+                    weight_unit(xv, wv);
+                }
+            }
             float s0 = 0.0f;
             float s1 = 0.0f;
 #pragma unroll
@@ -451,7 +460,7 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
 }
 
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                            uint32_t m, const float* rms_eps, hipStream_t stream) {
+                            uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream) {
     HYP_REQUIRE(count >= 1u && count <= kSkinnyMaxGroup, HYP_STATUS_INTERNAL, "skinny: bad group size");
     const uint32_t k = ws[0]->k;
     const bool norm = rms_eps != nullptr;
@@ -476,6 +485,7 @@ void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint
     p.pairs = TiledDims::of(16u, k).pairs;
     p.cap = 0.0f;
     p.eps = norm ? *rms_eps : 0.0f;
+    p.norm_w = norm ? norm_w : nullptr;
     p.splits = choose_skinny_splits(tiles_total, p.pairs, m, SkinnyForm::kPlain);
     p.split_shift = static_cast<uint32_t>(__builtin_ctz(p.splits));
     launch_skinny(p, tiles_total, m, false, Epilogue::kNone, norm, stream);

@@ -4,8 +4,12 @@
 //   1. per 64-element unit (k ascending), a sequential fp32 fma chain;
 //   2. per row, lane l of one wave adds units l, l + 64, l + 128, ... in that order,
 //      then an xor butterfly over the 64 lanes (offsets 32, 16, ..., 1).
-// A weightless mx::fast::rms_norm (the reference normalises with it around every block,
-// native/hyperion_mlx/src/forward.cc:521-529).
+// mx::fast::rms_norm(x, weight, eps) (native/hyperion_mlx/src/forward.cc:23-26): the
+// normalised value is rounded to bf16, then multiplied by the bf16 weight and rounded
+// again, y = bf16(w * bf16(x * inv)); without a weight (v_norm, forward.cc:403-412) y =
+// bf16(x * inv). The reference applies it with weights around every block
+// (input_layernorm, post_attention_layernorm, the feed-forward norms, forward.cc:521-529)
+// and to q and k per head (q_norm, k_norm, forward.cc:400-405).
 #pragma once
 
 #include "common.h"
@@ -54,6 +58,22 @@ __device__ __forceinline__ void normalize_unit(uint4 (&xv)[8], float inv) {
             w[q] = lo | (hi << 16);
         }
         xv[t] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// x <- bf16(w * x) for the 64 values of a unit (the learned scale after normalize_unit).
+__device__ __forceinline__ void weight_unit(uint4 (&xv)[8], const uint4 (&wv)[8]) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        uint32_t x[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+        const uint32_t w[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * bf16_bits_to_f32(x[q] & 0xFFFFu));
+            const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * bf16_bits_to_f32(x[q] >> 16));
+            x[q] = lo | (hi << 16);
+        }
+        xv[t] = make_uint4(x[0], x[1], x[2], x[3]);
     }
 }
 

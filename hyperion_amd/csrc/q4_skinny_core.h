@@ -131,6 +131,7 @@ struct SkinnyParams {
     const uint4* codes2;               // fused gate/up: the up projection (same n, k as seg[0])
     const uint2* sb2;
     float eps;            // NORM: rms normalisation epsilon
+    const uint16_t* norm_w;   // NORM: the norm's learned weight [k] (bf16), or null
 };
 
 // One matrix as seen by one lane: buffer resources and the lane's offsets into them.

@@ -149,7 +149,16 @@ __device__ __forceinline__ void stage_x(ConstStepOp& d, const OpLds& L, bool nor
         const uint32_t m = unit_row<M>(u, G);
         const uint32_t g = u - m * G;
         if (reload) load_unit(xr, (m * k + g * 64u) * 2u, xv);
-        if (norm) normalize_unit(xv, L.part[units + m]);
+        if (norm) {
+            normalize_unit(xv, L.part[units + m]);
+            if (d.norm_w != nullptr) {
+                const uint4* wsrc = reinterpret_cast<const uint4*>(d.norm_w + g * 64u);
+                uint4 wv[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
+                weight_unit(xv, wv);
+            }
+        }
         float s0 = 0.0f;
         float s1 = 0.0f;
 #pragma unroll

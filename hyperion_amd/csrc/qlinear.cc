@@ -157,13 +157,13 @@ void QuantizedLinear::apply_noalloc(const uint16_t* x, uint32_t m, uint16_t* y, 
 }
 
 void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                 uint32_t m, const float* rms_eps, hipStream_t stream) {
+                 uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream) {
     if (m == 0) return;
     const uint32_t k = linears[0]->mat.k;
     const hip::Q4Matrix* mats[hip::kSkinnyMaxGroup];
     for (uint32_t i = 0; i < count; ++i) mats[i] = &linears[i]->mat;
     if (rms_eps ? hip::skinny_norm_supported(m, k) : hip::skinny_supported(m, k, false)) {
-        hip::launch_q4_skinny_group(mats, ys, count, x, m, rms_eps, stream);
+        hip::launch_q4_skinny_group(mats, ys, count, x, m, rms_eps, norm_w, stream);
         return;
     }
     if (rms_eps == nullptr) {
@@ -174,7 +174,7 @@ void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uin
     void* xn = nullptr;
     HYP_HIP_CHECK(hipMallocAsync(&xn, static_cast<size_t>(m) * k * sizeof(uint16_t), stream));
     try {
-        hip::launch_rms_normalize(x, m, k, *rms_eps, static_cast<uint16_t*>(xn), stream);
+        hip::launch_rms_normalize(x, norm_w, m, k, *rms_eps, static_cast<uint16_t*>(xn), stream);
         hip::launch_q4_gemm_group(mats, ys, count, static_cast<const uint16_t*>(xn), m, stream);
     } catch (...) {
         (void)hipFreeAsync(xn, stream);

@@ -79,10 +79,11 @@ void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const u
 
 // ys[i] = x . dequant(W_i)^T for up to three projections sharing x and k (the attention
 // q/k/v of one layer, forward.cc:395,399,409): one launch at decode sizes. With rms_eps
-// non-null, x is first rms-normalised (the same bits as launch_rms_normalize); at decode
+// non-null, x is first rms-normalised with the bf16 weight norm_w [k] (or none, norm_w
+// null; the same bits as launch_rms_normalize); at decode
 // sizes inside the launch, otherwise into a stream-ordered temporary.
 void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                 uint32_t m, const float* rms_eps, hipStream_t stream);
+                 uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream);
 
 enum class LayerType { Sliding, Full };
 

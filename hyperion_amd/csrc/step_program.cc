@@ -91,6 +91,7 @@ StepProgram::StepProgram(const std::vector<StepOpSpec>& specs, uint32_t m, uint3
         const uint32_t tiles_per_block = hip::kStepWaves / splits;
         d.vbs = (tiles_total + tiles_per_block - 1u) / tiles_per_block;
         d.eps = s.form == StepForm::kNorm ? s.eps : 0.0f;
+        d.norm_w = s.form == StepForm::kNorm ? s.norm_w : nullptr;
         const size_t op_lds = hip::step_op_lds_bytes(m, k, s.form);
         HYP_REQUIRE(op_lds <= static_cast<size_t>(max_lds), HYP_STATUS_UNSUPPORTED,
                     who + "x of " + std::to_string(m) + " x " + std::to_string(k) + " exceeds the LDS");

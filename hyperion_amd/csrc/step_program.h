@@ -46,6 +46,8 @@ struct StepOp {
     uint32_t split_shift;
     uint32_t vbs;         // 16-wave blocks of 16 / splits tiles each
     float eps;            // kNorm
+    uint32_t pad;
+    const uint16_t* norm_w;   // kNorm: the norm's bf16 weight [k], or null
 };
 
 // Device synchronisation words of one program (uint32 indices; each on its own 128-byte

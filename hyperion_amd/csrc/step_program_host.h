@@ -19,6 +19,7 @@ struct StepOpSpec {
     const uint16_t* x = nullptr;
     uint16_t* y[hip::kStepMaxSegments] = {};
     float eps = 0.0f;
+    const uint16_t* norm_w = nullptr;           // kNorm: the norm's bf16 weight [k], or null
 };
 
 class StepProgram {

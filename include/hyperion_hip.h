@@ -203,12 +203,15 @@ HypStatus hyp_qmatmul_ex(HypQWeight weight, const void* x, uint32_t m, void* y,
 HypStatus hyp_qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
                             void* const* ys, HypStream stream);
 
-/* hyp_rms_normalize(x, m, k, eps) followed by hyp_qmatmul_group on its output, with the
- * same results bit for bit: the pre-attention normalisation and q/k/v of one block
- * (forward.cc:521-529, 395-409). At m <= 4 it is one launch that normalises the rows in
- * on-chip memory and does not write them back; x is left unchanged either way. */
-HypStatus hyp_qmatmul_group_rmsnorm(const HypQWeight* weights, uint32_t count, const void* x, uint32_t m,
-                                    float eps, void* const* ys, HypStream stream);
+/* hyp_rms_normalize(x, norm_weight, m, k, eps) followed by hyp_qmatmul_group on its
+ * output, with the same results bit for bit: the pre-attention input_layernorm and q/k/v
+ * of one block (forward.cc:521, 395-409). norm_weight is the norm's bf16 weight [k]
+ * (device, 16-byte aligned) or NULL for the weightless form. At m <= 4 it is one launch
+ * that normalises the rows in on-chip memory and does not write them back; x is left
+ * unchanged either way. */
+HypStatus hyp_qmatmul_group_rmsnorm(const HypQWeight* weights, uint32_t count, const void* x,
+                                    const void* norm_weight, uint32_t m, float eps, void* const* ys,
+                                    HypStream stream);
 
 /* h[m, n] = gelu_tanh(x * dequant(G)^T) * (x * dequant(U)^T), the gate/up half of
  * ForwardPass::mlp (forward.cc:338-343) with gelu_tanh rounded op-by-op in bf16 as
@@ -240,11 +243,28 @@ HypStatus hyp_dequantize_q4g64(const uint32_t* w, const void* scales, const void
 HypStatus hyp_embed(HypQWeight table, const uint32_t* ids, uint32_t n_ids, void* out,
                     HypStream stream);
 
-/* y[r] = bf16(x[r] / sqrt(mean(x[r]^2) + eps)) for each of m rows of k bf16 values,
- * fp32 statistics; y may alias x. The renormalisation of a hidden state between chained
- * projections: a weightless mx::fast::rms_norm (the reference normalises the decoder
- * input and branch outputs with it, forward.cc:521-529). eps must be finite and >= 0. */
-HypStatus hyp_rms_normalize(const void* x, uint32_t m, uint32_t k, float eps, void* y, HypStream stream);
+/* mx::fast::rms_norm(x, weight, eps) over rows (forward.cc:23-26): for each of m rows of
+ * k bf16 values, y[r] = bf16(w * bf16(x[r] / sqrt(mean(x[r]^2) + eps))) with fp32
+ * statistics, w the bf16 weight [k] (device, 16-byte aligned when k % 64 == 0); weight ==
+ * NULL is the parameterless form, y[r] = bf16(x[r] / sqrt(...)). The reference applies the
+ * weighted form as input_layernorm, post_attention_layernorm and the feed-forward norms
+ * (forward.cc:521-529) and per head as q_norm and k_norm (rows = tokens x heads, k =
+ * head_dim, forward.cc:400-405), and the weightless one as v_norm (forward.cc:403-412).
+ * y may alias x. eps must be finite and >= 0. */
+HypStatus hyp_rms_normalize(const void* x, const void* weight, uint32_t m, uint32_t k, float eps, void* y,
+                            HypStream stream);
+
+/* mx::fast::rope(x, dims = head_dim, traditional = false, base | freqs, scale = 1, offset)
+ * as Rope::apply does it (rope.cc:16-75) on x [rows, heads, head_dim] bf16 (device), row r
+ * at position offset + r; y may alias x. Pair (i, i + head_dim/2) of every head rotates by
+ * theta = fp32(offset + r) * fp32(base^(-2i / head_dim)) when i < rotated_dims/2, and is
+ * copied otherwise: the local layers' default scheme is rotated_dims = head_dim (256,
+ * base 1e4), the global layers' proportional scheme rotated_dims = 128 of head_dim 512
+ * (base 1e6; its frequencies are base^(2i / head_dim) over the full head_dim, rope.cc:16-33).
+ * inv_freq, cos and sin are computed in double and rounded to fp32; the rotation is fp32
+ * (no fused multiply-add), rounded to bf16. offset + rows must stay below 2^24. */
+HypStatus hyp_rope(const void* x, uint32_t rows, uint32_t heads, uint32_t head_dim, uint32_t rotated_dims, float base,
+                   uint32_t offset, void* y, HypStream stream);
 
 /* ForwardPass::sample_greedy (forward.cc:162-189) on the device, replacing its host copy
  * of the logits and the CPU scan: for each of `rows` rows of `vocab` bf16 logits
@@ -289,6 +309,7 @@ typedef struct HypStepOp {
     void* y[3];                     /* device bf16 [m, n_i] (GATE_UP_GELU: y[0] only) */
     float eps;                      /* QMATMUL_RMSNORM */
     uint32_t reserved;              /* 0 */
+    const void* norm_weight;        /* QMATMUL_RMSNORM: the norm's bf16 weight [k], or NULL */
 } HypStepOp;
 
 /* Validate the ops for m rows (1..4) and keep a device copy of them. The weights and

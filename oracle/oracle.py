@@ -44,6 +44,8 @@ def lib():
         L.orc_gelu_tanh_mul_bf16.argtypes = [_P, _P, _I, _P]
         L.orc_softcap_bf16.argtypes = [_P, _I, ctypes.c_float, _P]
         L.orc_scale_bf16.argtypes = [_P, _I, ctypes.c_float, _P]
+        L.orc_rms_norm_bf16.argtypes = [_P, _P, _I, _I, ctypes.c_float, _P]
+        L.orc_rope_bf16.argtypes = [_P, _I, _I, _I, _I, ctypes.c_double, _I, _P]
         _lib = L
     return _lib
 
@@ -186,4 +188,22 @@ def scale(x, c: float) -> np.ndarray:
     x = _c(x, np.uint16)
     out = np.empty(x.shape, np.uint16)
     lib().orc_scale_bf16(_p(x), x.size, c, _p(out))
+    return out
+
+
+def rms_norm(x, w=None, eps: float = 1e-6) -> np.ndarray:
+    """mx::fast::rms_norm over the rows of x [rows, k] (bf16 bits), w [k] or None."""
+    x = _c(x, np.uint16)
+    rows, k = x.shape
+    out = np.empty_like(x)
+    wp = _p(_c(w, np.uint16)) if w is not None else None
+    lib().orc_rms_norm_bf16(_p(x), wp, rows, k, ctypes.c_float(eps), _p(out))
+    return out
+
+
+def rope(x, rows: int, heads: int, head_dim: int, rotated: int, base: float, offset: int) -> np.ndarray:
+    """mx::fast::rope (non-traditional) of x [rows, heads, head_dim] (bf16 bits)."""
+    x = _c(x, np.uint16).reshape(rows, heads, head_dim)
+    out = np.empty_like(x)
+    lib().orc_rope_bf16(_p(x), rows, heads, head_dim, rotated, ctypes.c_double(base), offset, _p(out))
     return out

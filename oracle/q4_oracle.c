@@ -338,3 +338,103 @@ void orc_sample_greedy_bf16(const uint16_t* logits, int64_t n, uint32_t* token, 
     *logit = top1;
     *near_tie = (top1 - top2) < 0.5f ? 1 : 0;
 }
+
+/*
+ * mx::fast::rms_norm(x, weight, eps) over rows (forward.cc:23-26) with the summation order
+ * of the HIP kernels, so the two agree bit for bit:
+ *   k a multiple of 64: per 64-element unit a sequential fp32 fma chain of squares; lane l
+ *     of 64 adds units l, l + 64, ... in order; then an xor butterfly over the 64 lanes
+ *     (offsets 32, 16, ..., 1; a + b == b + a, so every lane ends with the same total);
+ *   otherwise: thread t of 256 runs an fma chain over elements t, t + 256, ...; a butterfly
+ *     within each wave of 64; the four wave sums added in wave order.
+ * inv = 1 / sqrtf(ss / k + eps); y = bf16(w * bf16(x * inv)), or bf16(x * inv) without w.
+ */
+static float butterfly64(float* v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        float nv[64];
+        for (int l = 0; l < 64; ++l) nv[l] = v[l] + v[l ^ off];
+        for (int l = 0; l < 64; ++l) v[l] = nv[l];
+    }
+    return v[0];
+}
+
+void orc_rms_norm_bf16(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t k, float eps, uint16_t* y) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* xr = x + r * k;
+        uint16_t* yr = y + r * k;
+        float ss;
+        if (k % 64 == 0) {
+            const int64_t units = k / 64;
+            float lanes[64];
+            for (int l = 0; l < 64; ++l) {
+                float acc = 0.0f;
+                for (int64_t u = l; u < units; u += 64) {
+                    float us = 0.0f;
+                    for (int64_t e = 0; e < 64; ++e) {
+                        const float v = orc_f32_from_bf16(xr[u * 64 + e]);
+                        us = fmaf(v, v, us);
+                    }
+                    acc += us;
+                }
+                lanes[l] = acc;
+            }
+            ss = butterfly64(lanes);
+        } else {
+            float waves[4];
+            for (int wv = 0; wv < 4; ++wv) {
+                float lanes[64];
+                for (int l = 0; l < 64; ++l) {
+                    float acc = 0.0f;
+                    for (int64_t i = wv * 64 + l; i < k; i += 256) {
+                        const float v = orc_f32_from_bf16(xr[i]);
+                        acc = fmaf(v, v, acc);
+                    }
+                    lanes[l] = acc;
+                }
+                waves[wv] = butterfly64(lanes);
+            }
+            ss = 0.0f;
+            for (int wv = 0; wv < 4; ++wv) ss += waves[wv];
+        }
+        const float inv = 1.0f / sqrtf(ss / (float)k + eps);
+        for (int64_t i = 0; i < k; ++i) {
+            float v = bf(orc_f32_from_bf16(xr[i]) * inv);
+            if (w != NULL) v = orc_f32_from_bf16(w[i]) * v;
+            yr[i] = orc_bf16_from_f32(v);
+        }
+    }
+}
+
+/*
+ * mx::fast::rope(x, dims = head_dim, traditional = false, base | freqs, scale = 1, offset)
+ * (rope.cc:16-75) on x [rows, heads, head_dim] bf16, row r at position offset + r. Pairs
+ * (i, i + head_dim/2) for i < head_dim/2 rotate by theta = fp32(pos) * inv_freq_i, with
+ * inv_freq_i = fp32(base^(-2i/head_dim)) for i < rotated/2 and 0 above (the proportional
+ * scheme's infinite frequencies: identity). Both are computed in double and rounded to
+ * fp32 once; cos and sin likewise from the fp32 theta. Then, in fp32 without fusion,
+ *   y_i = bf16(x_i c - x_{i+D/2} s),  y_{i+D/2} = bf16(x_i s + x_{i+D/2} c).
+ */
+void orc_rope_bf16(const uint16_t* x, int64_t rows, int64_t heads, int64_t head_dim, int64_t rotated,
+                   double base, int64_t offset, uint16_t* y) {
+    const int64_t half = head_dim / 2;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float pos = (float)(offset + r);
+        for (int64_t i = 0; i < half; ++i) {
+            const float inv = (2 * i < rotated) ? (float)pow(base, -2.0 * (double)i / (double)head_dim) : 0.0f;
+            const float theta = pos * inv;
+            const float c = (float)cos((double)theta);
+            const float sn = (float)sin((double)theta);
+            for (int64_t h = 0; h < heads; ++h) {
+                const int64_t b = (r * heads + h) * head_dim;
+                const float x1 = orc_f32_from_bf16(x[b + i]);
+                const float x2 = orc_f32_from_bf16(x[b + i + half]);
+                const float a1 = x1 * c;
+                const float a2 = x2 * sn;
+                const float b1 = x1 * sn;
+                const float b2 = x2 * c;
+                y[b + i] = orc_bf16_from_f32(a1 - a2);
+                y[b + i + half] = orc_bf16_from_f32(b1 + b2);
+            }
+        }
+    }
+}

@@ -57,6 +57,16 @@
  *                           rounding boundary (counted, under 200).
  *   orc_softcap_bf16        pinned likewise over all bf16 inputs, caps 30 and 50.
  *   orc_qmatmul_mlx_cpu_mt  pinned to orc_qmatmul_mlx_cpu: bit-identical outputs.
+ *   orc_rms_norm_bf16       pinned: against the fp64 closed form within one bf16 rounding
+ *                           (two with a weight) plus fp32 statistics, power-of-two weights
+ *                           exactly, constant rows, and the weightless form equal to a
+ *                           weight of ones. The summation order is the HIP kernels' own:
+ *                           MLX's (its Metal simd reductions) is parity unpinned.
+ *   orc_rope_bf16           pinned: position 0 and the unrotated pairs are the identity;
+ *                           the fp64 rotation of the closed form (theta = pos * base^(-2i/D))
+ *                           within bf16 rounding; the pairs (i, i + D/2) and the rotation's
+ *                           sign checked on one-hot inputs; pair norms preserved. MLX's
+ *                           metal::fast trigonometry is parity unpinned.
  *   orc_sample_greedy_bf16  pinned: against the definition computed independently with
  *                           numpy (first index of the maximum over non-NaN values, the
  *                           largest other value) on random rows with planted ties, NaN
@@ -131,6 +141,12 @@ void orc_softcap_bf16(const uint16_t* x, int64_t n, float cap, uint16_t* out);
 
 /* Elementwise bf16 multiply by a bf16 constant (embed scale). */
 void orc_scale_bf16(const uint16_t* x, int64_t n, float c, uint16_t* out);
+
+/* mx::fast::rms_norm with the HIP kernels' summation order; w may be NULL. */
+void orc_rms_norm_bf16(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t k, float eps, uint16_t* y);
+/* mx::fast::rope, non-traditional, on x [rows, heads, head_dim] at positions offset + r. */
+void orc_rope_bf16(const uint16_t* x, int64_t rows, int64_t heads, int64_t head_dim, int64_t rotated,
+                   double base, int64_t offset, uint16_t* y);
 
 #ifdef __cplusplus
 }

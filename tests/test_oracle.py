@@ -561,3 +561,84 @@ def test_dequantize_modes_mismatch_rate_on_the_decode_weights():
     exact = sf.repeat(64, axis=1) * codes + bf.repeat(64, axis=1)     # exact in float64
     np.testing.assert_array_equal(bb[:64], syn.bf16_bits(exact.astype(np.float32)))
     assert 0.2 < rate < 0.6
+
+
+# ---------------------------------------------------------------- rms norm with weight, rope
+
+def test_rms_norm_oracle_against_closed_form_and_exact_cases():
+    rng = np.random.default_rng(31)
+    for rows, k in ((3, 3840), (5, 256), (2, 1000), (4, 512)):
+        x = syn.bf16_bits((rng.standard_normal((rows, k)) * rng.choice([1e-3, 1.0, 50.0], (rows, 1))).astype(np.float32))
+        w = syn.bf16_bits((1.0 + 0.3 * rng.standard_normal(k)).astype(np.float32))
+        xf = syn.bf16_to_f32(x).astype(np.float64)
+        wf = syn.bf16_to_f32(w).astype(np.float64)
+        inv = 1.0 / np.sqrt(np.mean(xf * xf, axis=1, keepdims=True) + 1e-6)
+        plain = syn.bf16_to_f32(O.rms_norm(x, None, 1e-6)).astype(np.float64)
+        ref = xf * inv
+        assert np.all(np.abs(plain - ref) <= np.abs(ref) * 2.0**-8 * 1.01 + 1e-30), (rows, k)
+        got = syn.bf16_to_f32(O.rms_norm(x, w, 1e-6)).astype(np.float64)
+        refw = wf * ref
+        assert np.all(np.abs(got - refw) <= np.abs(refw) * 2.0**-7 * 1.01 + 1e-30), (rows, k)
+        # the weighted form is the weightless one times w, rounded once more
+        np.testing.assert_array_equal(O.rms_norm(x, w, 1e-6), syn.bf16_bits((syn.bf16_to_f32(O.rms_norm(x, None, 1e-6)) * syn.bf16_to_f32(w)).astype(np.float32)))
+        # a weight of ones changes nothing; a power-of-two weight scales exactly
+        ones = syn.bf16_bits(np.ones(k, np.float32))
+        np.testing.assert_array_equal(O.rms_norm(x, ones, 1e-6), O.rms_norm(x, None, 1e-6))
+        four = syn.bf16_bits(np.full(k, 4.0, np.float32))
+        np.testing.assert_array_equal(syn.bf16_to_f32(O.rms_norm(x, four, 1e-6)), 4.0 * syn.bf16_to_f32(O.rms_norm(x, None, 1e-6)))
+    # a constant row c: inv = 1/sqrt(c^2 + eps); with eps = 0, every output is exactly 1
+    x = syn.bf16_bits(np.full((2, 640), 3.0, np.float32))
+    assert np.all(syn.bf16_to_f32(O.rms_norm(x, None, 0.0)) == 1.0)
+
+
+def _rope_truth(x, heads, d, rotated, base, offset):
+    rows = x.shape[0]
+    xf = syn.bf16_to_f32(x).astype(np.float64).reshape(rows, heads, d)
+    half = d // 2
+    i = np.arange(half)
+    inv = np.where(2 * i < rotated, base ** (-2.0 * i / d), 0.0)
+    pos = (offset + np.arange(rows))[:, None]
+    th = pos * inv[None, :]
+    c, s = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+    x1, x2 = xf[..., :half], xf[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+
+
+def test_rope_oracle_against_closed_form():
+    rng = np.random.default_rng(32)
+    for rows, heads, d, rotated, base, offset in ((4, 3, 256, 256, 1e4, 0), (3, 2, 512, 128, 1e6, 17),
+                                                  (2, 4, 256, 256, 1e4, 4095), (1, 16, 256, 256, 1e4, 100000)):
+        x = syn.bf16_bits(rng.standard_normal((rows, heads * d)).astype(np.float32))
+        got = syn.bf16_to_f32(O.rope(x, rows, heads, d, rotated, base, offset)).astype(np.float64)
+        truth = _rope_truth(x, heads, d, rotated, base, offset)
+        # one bf16 rounding, plus theta's fp32 rounding (|d theta| <= pos * 2^-24)
+        mag = np.abs(syn.bf16_to_f32(x).astype(np.float64).reshape(rows, heads, d))
+        pair = np.sqrt(mag[..., : d // 2] ** 2 + mag[..., d // 2:] ** 2)
+        pair = np.concatenate([pair, pair], axis=-1)
+        pos = (offset + np.arange(rows))[:, None, None]
+        bound = np.abs(truth) * 2.0**-8 * 1.01 + pair * (2.0**-22 + pos * 2.0**-23)
+        assert np.all(np.abs(got - truth) <= bound), (rows, heads, d, rotated, offset)
+        if offset == 0:   # position 0 is the identity
+            np.testing.assert_array_equal(O.rope(x, rows, heads, d, rotated, base, 0)[0], x.reshape(rows, heads, d)[0])
+        if rotated < d:   # pairs past the rotated ones are left as they are
+            xr = x.reshape(rows, heads, d)
+            gr = O.rope(x, rows, heads, d, rotated, base, offset)
+            np.testing.assert_array_equal(gr[..., rotated // 2: d // 2], xr[..., rotated // 2: d // 2])
+            np.testing.assert_array_equal(gr[..., d // 2 + rotated // 2:], xr[..., d // 2 + rotated // 2:])
+
+
+def test_rope_oracle_pairs_and_sign_on_one_hot_inputs():
+    """A one in element i of the first half rotates into (cos, sin) at (i, i + D/2); a one
+    in element i + D/2 into (-sin, cos): this pins the non-traditional pairing and the sign."""
+    d, heads, pos = 256, 1, 7
+    for i in (0, 1, 63, 127):
+        inv = 1e4 ** (-2.0 * i / d)
+        th = np.float32(np.float32(pos) * np.float32(inv))
+        for src, want in ((i, (np.cos(th), np.sin(th))), (i + d // 2, (-np.sin(th), np.cos(th)))):
+            x = np.zeros((1, d), np.float32)
+            x[0, src] = 1.0
+            y = syn.bf16_to_f32(O.rope(syn.bf16_bits(x), 1, heads, d, d, 1e4, pos)).reshape(d)
+            assert y[i] == syn.bf16_to_f32(syn.bf16_bits(np.float32(want[0]))), (i, src)
+            assert y[i + d // 2] == syn.bf16_to_f32(syn.bf16_bits(np.float32(want[1]))), (i, src)
+            others = np.delete(y, [i, i + d // 2])
+            assert not others.any()
