@@ -171,3 +171,30 @@ def test_runtime_info_reports_abi_version():
     assert info.abi_version == 1
     assert st in (0, 5)
     assert _status("hyp_runtime_info", None) == 1
+
+
+def test_step_op_layout_matches_the_header():
+    """HypStepOp: 4 + 4 + 3 pointers + x + 3 pointers + eps + reserved + norm_weight = 80
+    bytes on LP64 (the Rust binding asserts the same size)."""
+    assert ctypes.sizeof(hy.StepOp) == 80
+    assert hy.StepOp.norm_weight.offset == 72
+    src = ('#include <stddef.h>\n#include "hyperion_hip.h"\n'
+           '_Static_assert(sizeof(HypStepOp) == 80, "size");\n'
+           '_Static_assert(offsetof(HypStepOp, norm_weight) == 72, "offset");\nint main(void){return 0;}\n')
+    r = subprocess.run(["gcc", "-std=c11", "-I", os.path.dirname(HEADER), "-x", "c", "-", "-fsyntax-only"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_step_program_create_rejects_bad_arguments_before_the_device():
+    out = ctypes.c_void_p()
+    assert _status("hyp_step_program_create", None, 0, 1, 0, ctypes.byref(out)) == 1
+    ops = (hy.StepOp * 1)()
+    assert _status("hyp_step_program_create", ctypes.cast(ops, ctypes.c_void_p), 1, 5, 0, ctypes.byref(out)) == 1
+    ops[0].kind = 9
+    ops[0].count = 1
+    assert _status("hyp_step_program_create", ctypes.cast(ops, ctypes.c_void_p), 1, 1, 0, ctypes.byref(out)) == 1
+    assert "unknown op kind" in hy.last_error()
+    assert _status("hyp_step_program_free", None) == 1
+    h = ctypes.c_void_p()
+    assert _status("hyp_step_program_free", ctypes.byref(h)) == 0
