@@ -13,10 +13,10 @@ Also reported, each on its own workload:
   prefill     the seven projections at m = 512 and 2048, q/k/v in one grouped launch
               (TFLOP/s vs bf16 MFMA peak)
   decode      48 layers (renormalise + q/k/v in one launch, o, fused gate/up + GELU, down)
-              + tied LM head [262144,3840] with softcap + greedy sampling on the device,
-              m = 1 and 4, replayed from a captured HIP graph (tokens/s and effective HBM
-              GB/s); the head timed alone (per-layer figures); and the layer stack as one
-              decode-step program launch
+              + tied LM head [262144,3840] with softcap + greedy sampling with its top-8
+              sidecar on the device, m = 1 and 4, replayed from a captured HIP graph
+              (tokens/s and effective HBM GB/s); the head timed alone (per-layer figures);
+              and the layer stack as one decode-step program launch
 and the oracle's restatement of MLX's CPU quantized_matmul timed on this host's cores
 (cpu_baseline).
 
@@ -229,7 +229,7 @@ def bench_prefill(stream, m, steps, warmup, dense=None):
 
 def bench_decode_stream(model, m, steps, warmup, stream):
     """One decode step at batch m: the 48-layer stack's 192 per-op launches and the head
-    (renormalise, softcap LM head, greedy sampling) replayed from one graph. Also timed: the
+    (renormalise, softcap LM head, greedy sampling with the top-8 sidecar) replayed from one graph. Also timed: the
     head alone, from which the per-layer figures are derived, and the same layer stack as
     one step-program launch followed by the head's graph."""
     b = dc.StepBuffers(hy, m, syn.activations(m, HIDDEN, seed=77), stream)
@@ -253,7 +253,7 @@ def bench_decode_stream(model, m, steps, warmup, stream):
     b.close()
     layers = len(model.layers)
     nbytes = model.weight_bytes + dc.step_activation_bytes(layers, m)
-    head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + 2 * syn.VOCAB) + 12 * m
+    head_bytes = q4_bytes(syn.VOCAB, HIDDEN) + 2 * m * (HIDDEN + 2 * syn.VOCAB) + 80 * m
     layer_bytes = (nbytes - head_bytes) / max(layers, 1)
 
     def rates(step_ms):
@@ -275,25 +275,27 @@ def bench_decode_stream(model, m, steps, warmup, stream):
 
 
 def bench_sample(stream, steps, warmup):
-    """hyp_sample_greedy on rows of vocab 262144 seeded logits N(0, 36): 10 calls captured
-    in one graph, timed per call from graph replays."""
+    """hyp_sample_greedy and hyp_sample_greedy_topk (the greedy epilogue with its top-8
+    sidecar) on rows of vocab 262144 seeded logits N(0, 36): 10 calls captured in one graph,
+    timed per call from graph replays."""
     out = []
     for rows in (1, 4):
         logits = hy.DeviceArray.from_host(
             syn.bf16_bits((np.random.default_rng(31 + rows).standard_normal((rows, syn.VOCAB)) * 6).astype(np.float32)),
             stream)
-        res = hy.DeviceArray((rows, 3), np.uint32)
-        with hy.Graph.capture(stream) as graph:
-            for _ in range(10):
-                hy.sample_greedy(logits, rows, syn.VOCAB, res, stream)
-        ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup) / 10
-        graph.close()
-        nbytes = 2 * rows * syn.VOCAB + 12 * rows
-        out.append({"rows": rows, "vocab": syn.VOCAB, "us": round(ms * 1e3, 2),
-                    "gbs": round(nbytes / ms / 1e6, 1)})
-        log(f"greedy sample rows={rows} vocab={syn.VOCAB}: {ms * 1e3:.2f} us per call")
+        for name, fn, rec in (("greedy", hy.sample_greedy, 12), ("greedy_topk", hy.sample_greedy_topk, 80)):
+            res = hy.DeviceArray((rows, rec // 4), np.uint32)
+            with hy.Graph.capture(stream) as graph:
+                for _ in range(10):
+                    fn(logits, rows, syn.VOCAB, res, stream)
+            ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup) / 10
+            graph.close()
+            nbytes = 2 * rows * syn.VOCAB + rec * rows
+            out.append({"entry": name, "rows": rows, "vocab": syn.VOCAB, "us": round(ms * 1e3, 2),
+                        "gbs": round(nbytes / ms / 1e6, 1)})
+            log(f"{name} sample rows={rows} vocab={syn.VOCAB}: {ms * 1e3:.2f} us per call")
+            res.close()
         logits.close()
-        res.close()
     return out
 
 

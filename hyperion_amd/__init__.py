@@ -47,7 +47,7 @@ EXPORTED = [
     "hyp_qmatmul", "hyp_qmatmul_noalloc", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
-    "hyp_rope", "hyp_sample_greedy",
+    "hyp_rope", "hyp_sample_greedy", "hyp_sample_greedy_topk",
     "hyp_step_program_create", "hyp_step_program_run", "hyp_step_program_check", "hyp_step_program_free",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
@@ -91,6 +91,22 @@ class StepOp(ctypes.Structure):
         ("eps", ctypes.c_float),
         ("reserved", ctypes.c_uint32),
         ("norm_weight", ctypes.c_void_p),
+    ]
+
+
+TOP_K_LOGPROBS = 8   # HYP_TOP_K_LOGPROBS (hyperion_mlx.h:145)
+
+
+class TopKSample(ctypes.Structure):
+    """HypTopKSample: ForwardPass::StochasticSample (forward.h:125-131) as the greedy
+    epilogue fills it (model.cc:272-288), plus GreedySample's near_tie."""
+    _fields_ = [
+        ("token_id", ctypes.c_uint32),
+        ("logit", ctypes.c_float),
+        ("near_tie", ctypes.c_uint32),
+        ("top_k_count", ctypes.c_uint32),
+        ("top_k_ids", ctypes.c_uint32 * TOP_K_LOGPROBS),
+        ("top_k_logprobs", ctypes.c_float * TOP_K_LOGPROBS),
     ]
 
 
@@ -155,6 +171,7 @@ def lib() -> ctypes.CDLL:
         "hyp_rms_normalize": [_P, _P, _U32, _U32, ctypes.c_float, _P, _P],
         "hyp_rope": [_P, _U32, _U32, _U32, _U32, ctypes.c_float, _U32, _P, _P],
         "hyp_sample_greedy": [_P, _U32, _U32, _P, _P],
+        "hyp_sample_greedy_topk": [_P, _U32, _U32, _P, _P],
         "hyp_step_program_create": [_P, _U32, _U32, _U32, _PP],
         "hyp_step_program_run": [_P, _P],
         "hyp_step_program_check": [_P],
@@ -523,6 +540,27 @@ def sample_greedy(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, 
     out is a device array of at least rows * 12 bytes."""
     ptr = ctypes.c_void_p((logits.ptr.value or 0) + 2 * row_offset * vocab) if row_offset else logits.ptr
     call("hyp_sample_greedy", ptr, rows, vocab, out.ptr, stream.handle)
+
+
+def sample_greedy_topk(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, stream: Stream,
+                       row_offset: int = 0) -> None:
+    """out[r] = HypTopKSample of logits row row_offset + r, for r < rows
+    (hyp_sample_greedy_topk); out is a device array of at least rows * 80 bytes."""
+    ptr = ctypes.c_void_p((logits.ptr.value or 0) + 2 * row_offset * vocab) if row_offset else logits.ptr
+    call("hyp_sample_greedy_topk", ptr, rows, vocab, out.ptr, stream.handle)
+
+
+def topk_samples(out: DeviceArray, rows: int, stream: Stream):
+    """The first `rows` HypTopKSample records of a device array as dicts (one
+    synchronizing copy of rows * 80 bytes); ids/logprobs are numpy arrays of
+    TOP_K_LOGPROBS entries, the values as bit-exact float32."""
+    raw = out.to_host(stream).reshape(-1).view(np.uint8)[: rows * ctypes.sizeof(TopKSample)]
+    recs = np.frombuffer(raw.tobytes(), np.uint32).reshape(rows, ctypes.sizeof(TopKSample) // 4)
+    k = TOP_K_LOGPROBS
+    return [{
+        "token_id": int(r[0]), "logit": r[1:2].view(np.float32)[0], "near_tie": bool(r[2]),
+        "count": int(r[3]), "ids": r[4:4 + k].copy(), "logprobs": r[4 + k:4 + 2 * k].view(np.float32).copy(),
+    } for r in recs]
 
 
 def greedy_samples(out: DeviceArray, rows: int, stream: Stream):

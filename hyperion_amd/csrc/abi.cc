@@ -626,9 +626,26 @@ HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, H
         if (rows == 0) return;
         REQUIRE_ARG(out != nullptr, "out must be a non-null device pointer");
         REQUIRE_ARG(vocab == 0 || logits != nullptr, "logits must be a non-null device pointer");
+        REQUIRE_ARG(vocab <= (1u << 31), "vocab must be at most 2^31");
         REQUIRE_ARG(static_cast<uint64_t>(rows) * vocab < (1ull << 62), "logits too large");
         hyperion::hip::launch_sample_greedy(static_cast<const uint16_t*>(logits), rows, vocab, out, stream->workspace,
                                             stream->workspace_bytes, s);
+    });
+}
+
+static_assert(sizeof(HypTopKSample) == 80, "HypTopKSample is 80 bytes");
+
+HypStatus hyp_sample_greedy_topk(const void* logits, uint32_t rows, uint32_t vocab, HypTopKSample* out,
+                                 HypStream stream) {
+    return abi_call("hyp_sample_greedy_topk", [&] {
+        hipStream_t s = stream_of(stream);
+        if (rows == 0) return;
+        REQUIRE_ARG(out != nullptr, "out must be a non-null device pointer");
+        REQUIRE_ARG(vocab == 0 || logits != nullptr, "logits must be a non-null device pointer");
+        REQUIRE_ARG(vocab <= hyperion::hip::sample_topk_max_vocab(), "vocab must be at most 2^23");
+        REQUIRE_ARG(static_cast<uint64_t>(rows) * vocab < (1ull << 62), "logits too large");
+        hyperion::hip::launch_sample_topk(static_cast<const uint16_t*>(logits), rows, vocab, out, stream->workspace,
+                                          stream->workspace_bytes, s);
     });
 }
 

@@ -96,6 +96,13 @@ size_t sample_greedy_workspace_bytes();
 void launch_sample_greedy(const uint16_t* logits, uint32_t rows, uint32_t vocab, HypGreedySample* out,
                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// The greedy epilogue's top-k sidecar (plus the greedy fields) of each row -> out[row];
+// same workspace as launch_sample_greedy; vocab <= sample_topk_max_vocab() (2^23).
+constexpr uint32_t kHypTopK = HYP_TOP_K_LOGPROBS;
+uint32_t sample_topk_max_vocab();
+void launch_sample_topk(const uint16_t* logits, uint32_t rows, uint32_t vocab, HypTopKSample* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,
                         uint16_t* scales, uint16_t* biases, hipStream_t stream);

@@ -4,8 +4,9 @@ the tied LM head, with the activation chain reduced to plain matmuls between lay
 This is the full-decode weight stream of the benchmark workload (random-init weights of
 the Gemma-class 12B shapes, seeded per projection) as the reference's decode loop drives
 it: the layer loop of ForwardPass::forward (native/hyperion_mlx/src/forward.cc:558-563)
-inside hyp_decode_block (model.cc:703-718), then the epilogue run_epilogue
-(model.cc:215-228: LM head, softcap, greedy sample). Attention, the KV cache and the
+inside hyp_decode_block (model.cc:703-718), then the greedy epilogue with its top-8
+sidecar (run_epilogue_sampled at temperature 0, model.cc:262-288: LM head, softcap, greedy
+sample, the 8 largest logits and their ids). Attention, the KV cache and the
 residual adds are not on the quantized-linear path; between the projections each
 output feeds the next projection directly, and the hidden state is renormalised
 (weightless RMS norm) before each layer's q/k/v, so values stay N(0, 1)-sized over 48
@@ -16,7 +17,8 @@ Per layer, in launch order:
   2. o from q's output                               (hyp_qmatmul)
   3. gelu_tanh(gate(o)) * up(o)                       (hyp_qmlp_gate_up_gelu)
   4. down of that into h                              (hyp_qmatmul)
-then h renormalised, the softcap LM head and greedy sampling of every row.
+then h renormalised, the softcap LM head and greedy sampling of every row with the top-8
+sidecar (hyp_sample_greedy_topk): nothing of the logits leaves the device.
 """
 from __future__ import annotations
 
@@ -90,7 +92,7 @@ class StepBuffers:
         self.o = hy.DeviceArray((m, syn.HIDDEN), np.uint16)
         self.g = hy.DeviceArray((m, 15360), np.uint16)
         self.logits = hy.DeviceArray((m, syn.VOCAB), np.uint16)
-        self.samples = hy.DeviceArray((m, 3), np.uint32)
+        self.samples = hy.DeviceArray((m, 20), np.uint32)   # HypTopKSample, 80 bytes a row
 
     def close(self):
         for a in (self.h, self.q, self.k, self.v, self.o, self.g, self.logits, self.samples):
@@ -112,11 +114,11 @@ def decode_layers(model: DecodeModel, m: int, b: StepBuffers, stream) -> None:
 
 def lm_head(model: DecodeModel, m: int, b: StepBuffers, stream) -> None:
     """The last hidden state renormalised, the tied LM head with softcap 30, then greedy
-    sampling of every row on the device (run_epilogue, model.cc:215-228)."""
+    sampling of every row with its top-8 sidecar on the device (model.cc:262-288)."""
     hy = model.hy
     hy.rms_normalize(b.h, m, syn.HIDDEN, b.h, stream, eps=RMS_EPS)
     hy.qmatmul(model.embed, b.h, m, b.logits, stream, softcap=SOFTCAP)
-    hy.sample_greedy(b.logits, m, syn.VOCAB, b.samples, stream)
+    hy.sample_greedy_topk(b.logits, m, syn.VOCAB, b.samples, stream)
 
 
 def layer_program(model: DecodeModel, m: int, b: StepBuffers, spin_limit: int = 0):
@@ -139,7 +141,7 @@ def decode_step(model: DecodeModel, m: int, b: StepBuffers, stream) -> None:
 
 def step_activation_bytes(layers: int, m: int) -> int:
     """Activation bytes of one step: per layer x, q/k/v, o, gate/up, down read or
-    written; then the head's x, logits written and read back by the sampler, and 12
+    written; then the head's x, logits written and read back by the sampler, and 80
     bytes of sample per row."""
     h = syn.HIDDEN
-    return 2 * m * (layers * (h * 3 + 4096 * 2 + 2048 * 2 + h * 2 + 15360 * 3) + h + 2 * syn.VOCAB) + 12 * m
+    return 2 * m * (layers * (h * 3 + 4096 * 2 + 2048 * 2 + h * 2 + 15360 * 3) + h + 2 * syn.VOCAB) + 80 * m

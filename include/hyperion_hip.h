@@ -100,6 +100,23 @@ typedef struct HypGreedySample {
     uint32_t near_tie;              /* 1 when top1 - top2 < 0.5, else 0 */
 } HypGreedySample;
 
+/* The top-k sidecar's size, HYP_TOP_K_LOGPROBS (hyperion_mlx.h:145). */
+#define HYP_TOP_K_LOGPROBS 8
+
+/* ForwardPass::StochasticSample (forward.h:125-131) as the greedy epilogue fills it
+ * (model.cc:272-288), with GreedySample's near_tie (forward.h:104-108): the greedy token
+ * and logit, and the top_k_count = min(HYP_TOP_K_LOGPROBS, vocab) largest post-softcap
+ * logits (fp32 of the bf16 values; the reference calls them logprobs) with their ids,
+ * descending. Entries past top_k_count are zero. 80 bytes. */
+typedef struct HypTopKSample {
+    uint32_t token_id;
+    float logit;
+    uint32_t near_tie;
+    uint32_t top_k_count;
+    uint32_t top_k_ids[HYP_TOP_K_LOGPROBS];
+    float top_k_logprobs[HYP_TOP_K_LOGPROBS];
+} HypTopKSample;
+
 /* ---- errors and runtime ------------------------------------------------------- */
 
 /* Copy the calling thread's last error into buffer (NUL-terminated, truncated).
@@ -136,7 +153,7 @@ HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
  * per-launch host work; the reference has no counterpart (MLX evaluates its lazy graph
  * at mx::eval, forward.cc:171). Between begin and end, hyp_qmatmul, hyp_qmatmul_ex,
  * hyp_qmatmul_group, hyp_qmlp_gate_up_gelu and hyp_qmatmul_group_rmsnorm with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
- * hyp_dequantize_q4g64, hyp_embed, hyp_sample_greedy and the copies on `stream` are
+ * hyp_dequantize_q4g64, hyp_embed, hyp_sample_greedy, hyp_sample_greedy_topk and the copies on `stream` are
  * recorded instead of run (they allocate nothing). Calls that may allocate or clear
  * memory - the matmul entries on their GEMM path (m > 4) and hyp_memset_device - check
  * the stream and return INVALID_ARGUMENT while it is capturing, before enqueueing
@@ -278,6 +295,18 @@ HypStatus hyp_rope(const void* x, uint32_t rows, uint32_t heads, uint32_t head_d
  * ordered with it) and only while the stream exists. */
 HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, HypGreedySample* out,
                             HypStream stream);
+
+/* The greedy epilogue with its top-k sidecar (model.cc:272-288) on the device, replacing
+ * the host copy of the row and the std::partial_sort there: out[r] (device memory) gets
+ * hyp_sample_greedy's token, logit and near_tie for row r, and its HYP_TOP_K_LOGPROBS
+ * largest values with their ids. partial_sort leaves the order of equal values to the
+ * library, so it is defined here: larger value first (-0 and +0 equal), then the lower
+ * index; NaN after every number, lower index first. Where the largest
+ * HYP_TOP_K_LOGPROBS + 1 values are distinct this is exactly partial_sort's result.
+ * vocab is at most 2^23 (INVALID_ARGUMENT above). Same workspace and capture rules as
+ * hyp_sample_greedy. */
+HypStatus hyp_sample_greedy_topk(const void* logits, uint32_t rows, uint32_t vocab, HypTopKSample* out,
+                                 HypStream stream);
 
 /* ---- decode-step program (the per-token layer loop, forward.cc:558-563, run by
  *      hyp_decode_block, model.cc:703-718) ------------------------------------------ */

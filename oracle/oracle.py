@@ -40,6 +40,8 @@ def lib():
         L.orc_qmatmul_mlx_cpu_rows.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P]
         L.orc_qmatmul_mlx_cpu_mt.argtypes = [_P, _P, _P, _P, _I, _I, _I, ctypes.c_int, _P]
         L.orc_sample_greedy_bf16.argtypes = [_P, _I, _P, _P, _P]
+        L.orc_sample_topk_bf16.restype = ctypes.c_uint32
+        L.orc_sample_topk_bf16.argtypes = [_P, _I, ctypes.c_uint32, _P, _P]
         L.orc_gelu_tanh_bf16.argtypes = [_P, _I, _P]
         L.orc_gelu_tanh_mul_bf16.argtypes = [_P, _P, _I, _P]
         L.orc_softcap_bf16.argtypes = [_P, _I, ctypes.c_float, _P]
@@ -159,6 +161,39 @@ def sample_greedy(logits):
     tie = ctypes.c_int32()
     lib().orc_sample_greedy_bf16(_p(x), x.size, ctypes.byref(tok), ctypes.byref(val), ctypes.byref(tie))
     return tok.value, val.value, bool(tie.value)
+
+
+TOP_K = 8   # HYP_TOP_K_LOGPROBS (hyperion_mlx.h:145)
+
+
+def sample_topk(logits, k: int = TOP_K):
+    """The greedy epilogue's top-k sidecar of a 1-D bf16 row -> (count, ids uint32[k],
+    values float32[k]); order: larger value, then lower index, NaN last."""
+    x = _c(logits, np.uint16).reshape(-1)
+    ids = np.zeros(k, np.uint32)
+    vals = np.zeros(k, np.float32)
+    cnt = lib().orc_sample_topk_bf16(_p(x), x.size, k, _p(ids), _p(vals))
+    return int(cnt), ids, vals
+
+
+_stl = None
+
+
+def stl_partial_sort_topk(p_f32, k: int = TOP_K) -> np.ndarray:
+    """libstdc++ std::partial_sort of the indices by p[a] > p[b] (model.cc:278-288): the
+    first min(k, n) indices."""
+    global _stl
+    if _stl is None:
+        path = os.path.join(os.path.dirname(_LIB_PATH), "libstlsort.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library not built: {path} (run __graft_entry__.build())")
+        _stl = ctypes.CDLL(path)
+        _stl.stl_partial_sort_topk.restype = ctypes.c_uint32
+        _stl.stl_partial_sort_topk.argtypes = [_P, _I, ctypes.c_uint32, _P]
+    p = _c(p_f32, np.float32).reshape(-1)
+    ids = np.zeros(k, np.uint32)
+    cnt = _stl.stl_partial_sort_topk(_p(p), p.size, k, _p(ids))
+    return ids[:cnt]
 
 
 def gelu_tanh(x) -> np.ndarray:

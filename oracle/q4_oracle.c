@@ -340,6 +340,48 @@ void orc_sample_greedy_bf16(const uint16_t* logits, int64_t n, uint32_t* token, 
 }
 
 /*
+ * The top-k sidecar of the greedy epilogue (native/hyperion_mlx/src/model.cc:278-288): the
+ * row converted to fp32, std::partial_sort of the indices by p[a] > p[b], the first
+ * min(k, n) indices and their values. partial_sort leaves the order of equal values to the
+ * library (and NaN breaks its comparator's ordering), so the order is defined here as:
+ * larger value first (-0 == +0, as the comparator sees them), then the lower index; NaN
+ * after every number, lower index first. Where the top k + 1 values are distinct numbers
+ * this is partial_sort's result. Selection: k passes over the row, each taking the first
+ * element in that order among those not yet taken. Returns the count; ids/values beyond
+ * it are zero.
+ */
+static int topk_before(const float* p, int64_t a, int64_t b) {
+    const int na = isnan(p[a]);
+    const int nb = isnan(p[b]);
+    if (na != nb) return nb;                /* a number before NaN */
+    if (!na && p[a] != p[b]) return p[a] > p[b];
+    return a < b;
+}
+
+uint32_t orc_sample_topk_bf16(const uint16_t* logits, int64_t n, uint32_t k, uint32_t* ids, float* values) {
+    const uint32_t count = (int64_t)k < n ? k : (uint32_t)(n < 0 ? 0 : n);
+    float* p = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    for (int64_t i = 0; i < n; ++i) p[i] = orc_f32_from_bf16(logits[i]);
+    for (uint32_t j = 0; j < k; ++j) {
+        ids[j] = 0;
+        values[j] = 0.0f;
+    }
+    for (uint32_t j = 0; j < count; ++j) {
+        int64_t best = -1;
+        for (int64_t i = 0; i < n; ++i) {
+            int taken = 0;
+            for (uint32_t t = 0; t < j; ++t) taken |= (int64_t)ids[t] == i;
+            if (taken) continue;
+            if (best < 0 || topk_before(p, i, best)) best = i;
+        }
+        ids[j] = (uint32_t)best;
+        values[j] = p[best];
+    }
+    free(p);
+    return count;
+}
+
+/*
  * mx::fast::rms_norm(x, weight, eps) over rows (forward.cc:23-26) with the summation order
  * of the HIP kernels, so the two agree bit for bit:
  *   k a multiple of 64: per 64-element unit a sequential fp32 fma chain of squares; lane l

@@ -67,6 +67,12 @@
  *                           within bf16 rounding; the pairs (i, i + D/2) and the rotation's
  *                           sign checked on one-hot inputs; pair norms preserved. MLX's
  *                           metal::fast trigonometry is parity unpinned.
+ *   orc_sample_topk_bf16    pinned: against std::partial_sort with the reference's own
+ *                           comparator (oracle/stl_partial_sort.cc, libstdc++) - the same
+ *                           ids where the top k + 1 values are distinct, the same values
+ *                           always; ties and NaN ordered as stated (partial_sort leaves
+ *                           them unspecified) and checked on hand cases; top-1 and top-2
+ *                           agree with orc_sample_greedy_bf16.
  *   orc_sample_greedy_bf16  pinned: against the definition computed independently with
  *                           numpy (first index of the maximum over non-NaN values, the
  *                           largest other value) on random rows with planted ties, NaN
@@ -120,6 +126,11 @@ void orc_qmatmul_mlx_cpu(const uint16_t* x, const uint32_t* wq, const uint16_t* 
 /* ForwardPass::sample_greedy on one row of n bf16 logits: token, its logit, near_tie. */
 void orc_sample_greedy_bf16(const uint16_t* logits, int64_t n, uint32_t* token, float* logit,
                             int32_t* near_tie);
+
+/* The greedy epilogue's top-k sidecar (model.cc:278-288) of one row of n bf16 logits:
+ * ids/values of the min(k, n) first elements in the order larger value, lower index,
+ * NaN last; returns that count, zero-fills ids/values up to k. */
+uint32_t orc_sample_topk_bf16(const uint16_t* logits, int64_t n, uint32_t k, uint32_t* ids, float* values);
 
 /* orc_qmatmul_mlx_cpu with output rows spread over `threads` OpenMP threads
  * (bit-identical result; the multi-core CPU baseline). */

@@ -186,6 +186,20 @@ def test_step_op_layout_matches_the_header():
     assert r.returncode == 0, r.stderr
 
 
+def test_topk_sample_layout_matches_the_header():
+    """HypTopKSample: token, logit, near_tie, count, 8 ids, 8 values = 80 bytes, and the
+    sidecar size is the reference's HYP_TOP_K_LOGPROBS (8)."""
+    assert ctypes.sizeof(hy.TopKSample) == 80
+    assert hy.TopKSample.top_k_logprobs.offset == 48
+    src = ('#include <stddef.h>\n#include "hyperion_hip.h"\n'
+           '_Static_assert(HYP_TOP_K_LOGPROBS == 8, "k");\n'
+           '_Static_assert(sizeof(HypTopKSample) == 80, "size");\n'
+           '_Static_assert(offsetof(HypTopKSample, top_k_logprobs) == 48, "offset");\nint main(void){return 0;}\n')
+    r = subprocess.run(["gcc", "-std=c11", "-I", os.path.dirname(HEADER), "-x", "c", "-", "-fsyntax-only"],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 def test_step_program_create_rejects_bad_arguments_before_the_device():
     out = ctypes.c_void_p()
     assert _status("hyp_step_program_create", None, 0, 1, 0, ctypes.byref(out)) == 1

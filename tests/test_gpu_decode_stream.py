@@ -131,7 +131,7 @@ def test_lm_head_full_vocab_softcap_and_sampling(model, head_host, stream, m):
     """The tied head [262144, 3840] with softcap 30 at decode batch m (the m >= 2 launches
     take the head kernel's looping form): sampled rows against the fp64 truth, the whole
     row against the oracle's softcap of the plain launch, then device greedy sampling
-    against the oracle's scan of the same capped logits."""
+    and its top-8 sidecar against the oracle on the same capped logits."""
     w, s, b = head_host
     x = syn.activations(m, syn.HIDDEN, seed=900 + m)
     xd = dev(x, stream)
@@ -171,7 +171,14 @@ def test_lm_head_full_vocab_softcap_and_sampling(model, head_host, stream, m):
         want = O.sample_greedy(capped[r])
         assert (got[r][0], got[r][2]) == (want[0], want[2]), f"row {r}: {got[r]} vs {want}"
         assert np.float32(got[r][1]).tobytes() == np.float32(want[1]).tobytes()
-    for a in (xd, capped_d, plain_d, out):
+    topk = hy.DeviceArray((m, 20), np.uint32)
+    hy.sample_greedy_topk(capped_d, m, syn.VOCAB, topk, stream)
+    for r, t in enumerate(hy.topk_samples(topk, m, stream)):
+        cnt, ids, vals = O.sample_topk(capped[r])
+        assert (t["token_id"], t["near_tie"], t["count"]) == (got[r][0], got[r][2], cnt)
+        np.testing.assert_array_equal(t["ids"], ids, err_msg=f"row {r}")
+        np.testing.assert_array_equal(t["logprobs"].view(np.uint32), vals.view(np.uint32))
+    for a in (xd, capped_d, plain_d, out, topk):
         a.close()
 
 

@@ -397,6 +397,113 @@ def test_sample_greedy_restatement_matches_definition():
     assert O.sample_greedy(syn.bf16_bits(np.float32([1, 3, 2.75, 2]))) == (1, 3.0, True)
 
 
+
+# ---------------------------------------------------------------- top-k sidecar of the greedy epilogue
+def _distinct_top_row(rng, n, k=O.TOP_K):
+    """A row whose k + 1 largest values are distinct: normal draws in [-8, 8] plus k + 1
+    distinct planted values above them, at random positions."""
+    bits = syn.bf16_bits(np.clip(rng.standard_normal(n) * 3, -8, 8).astype(np.float32))
+    top = min(n, k + 1)
+    planted = syn.bf16_bits((16.0 + 0.125 * rng.permutation(64)[:top]).astype(np.float32))
+    bits[rng.choice(n, top, replace=False)] = planted
+    return bits
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 100, 4099, 262144])
+def test_topk_equals_partial_sort_where_values_are_distinct(n):
+    """Where the top k + 1 values are distinct, any conforming std::partial_sort gives one
+    answer: libstdc++'s, called with the reference's comparator, is the pin."""
+    rng = np.random.default_rng(n)
+    for trial in range(3):
+        bits = _distinct_top_row(rng, n)
+        p = syn.bf16_to_f32(bits)
+        cnt, ids, vals = O.sample_topk(bits)
+        want = O.stl_partial_sort_topk(p)
+        assert cnt == min(O.TOP_K, n) == want.size
+        np.testing.assert_array_equal(ids[:cnt], want, err_msg=f"n={n} trial {trial}")
+        np.testing.assert_array_equal(vals[:cnt].view(np.uint32), p[want].view(np.uint32))
+        assert not ids[cnt:].any() and not vals[cnt:].any()
+
+
+def test_topk_values_equal_partial_sort_with_ties():
+    """A vocabulary-sized bf16 row of normal logits nearly always has equal values among
+    its top 9 (bf16 keeps 8 significant bits); the values returned are still partial_sort's,
+    and the ids name elements of those values; only which tied ids, and their order, is
+    defined here rather than left to the library."""
+    rng = np.random.default_rng(5)
+    ties_seen = 0
+    for trial in range(8):
+        bits = syn.bf16_bits((rng.standard_normal(262144) * 3).astype(np.float32))
+        p = syn.bf16_to_f32(bits)
+        cnt, ids, vals = O.sample_topk(bits)
+        want = O.stl_partial_sort_topk(p)
+        np.testing.assert_array_equal(vals[:cnt], p[want])
+        np.testing.assert_array_equal(vals[:cnt], p[ids[:cnt]])
+        assert len(set(ids[:cnt].tolist())) == cnt
+        top9 = np.sort(p)[::-1][:9]
+        ties_seen += len(set(top9.tolist())) < 9
+        # the defined order: within a run of equal values the ids ascend, and they are
+        # the lowest indices holding that value
+        for v in set(vals[:cnt].tolist()):
+            sel = ids[:cnt][vals[:cnt] == v]
+            assert list(sel) == sorted(sel)
+            np.testing.assert_array_equal(sel, np.flatnonzero(p == v)[: sel.size])
+    assert ties_seen >= 6
+
+
+def _topk_by_sorting(bits, k=O.TOP_K):
+    """The defined order by a full sort (Python's sorted on a key), for small rows."""
+    p = syn.bf16_to_f32(bits.reshape(-1))
+    order = sorted(range(p.size), key=lambda i: (bool(np.isnan(p[i])), 0.0 if np.isnan(p[i]) else -float(p[i]), i))
+    return order[:k]
+
+
+def test_topk_defined_order_hand_cases():
+    f = lambda xs: syn.bf16_bits(np.float32(xs))
+    nan, inf = float("nan"), float("inf")
+    assert O.sample_topk(np.zeros(0, np.uint16))[0] == 0
+    cnt, ids, vals = O.sample_topk(f([3, 5, 5, 1, 5]), 2)
+    assert (cnt, list(ids)) == (2, [1, 2])
+    cnt, ids, _ = O.sample_topk(f([7.0] * 20))
+    assert list(ids) == list(range(8))
+    cnt, ids, vals = O.sample_topk(np.array([0x8000, 0x0000, 0x8000], np.uint16))   # -0, +0, -0
+    assert (cnt, list(ids[:3])) == (3, [0, 1, 2])
+    assert list(vals[:3].view(np.uint32)) == [0x80000000, 0, 0x80000000]
+    cnt, ids, vals = O.sample_topk(f([nan, 1, nan, -inf]))
+    assert (cnt, list(ids[:4])) == (4, [1, 3, 0, 2]) and not ids[4:].any()
+    cnt, ids, vals = O.sample_topk(f([nan] * 10))
+    assert list(ids) == list(range(8)) and np.isnan(vals).all()
+    cnt, ids, vals = O.sample_topk(f([-inf, 2, inf, -1, inf, 0]))
+    assert list(ids[:6]) == [2, 4, 1, 5, 3, 0]
+    rng = np.random.default_rng(77)
+    for trial in range(30):
+        n = int(rng.integers(1, 300))
+        bits = syn.bf16_bits(rng.integers(-4, 5, n).astype(np.float32))   # many ties
+        bits[rng.random(n) < 0.05] = 0x7FC0
+        bits[rng.random(n) < 0.05] = 0xFF80
+        bits[rng.random(n) < 0.05] = 0x8000
+        cnt, ids, _ = O.sample_topk(bits)
+        assert list(ids[:cnt]) == _topk_by_sorting(bits), f"trial {trial}"
+
+
+def test_topk_head_agrees_with_greedy():
+    """The sidecar's first entry is the greedy token whenever some value exceeds -inf, and
+    its second value is the greedy scan's top2 (the largest other non-NaN value)."""
+    rng = np.random.default_rng(31)
+    for trial in range(40):
+        n = int(rng.choice([2, 9, 1000, 4099]))
+        bits = syn.bf16_bits((rng.standard_normal(n) * 4).astype(np.float32))
+        if trial % 3 == 1:
+            bits[rng.choice(n, 2, replace=False)] = syn.bf16_bits(np.float32([50.0]))[0]
+        if trial % 3 == 2:
+            bits[rng.integers(n)] = 0x7FC0
+            bits[rng.integers(n)] = 0x7F80
+        tok, logit, tie = O.sample_greedy(bits)
+        cnt, ids, vals = O.sample_topk(bits)
+        assert ids[0] == tok and vals[0] == logit
+        top2 = vals[1] if not np.isnan(vals[1]) else np.float32(-np.inf)
+        assert tie == bool(np.float32(logit) - top2 < np.float32(0.5))
+
 # ---------------------------------------------------------------- exhaustive pins of the bf16 op chains
 #
 # Independent restatements of the reference's op chains (forward.cc:154-160 softcap,
