@@ -10,8 +10,9 @@ events on the stream the kernel runs on.
 
 Also reported, each on its own workload:
   quantize    bf16 W [15360,3840] N(0, 0.02^2) with 1% x8 outliers -> Q4/g64 (GB/s)
-  prefill     the seven projections at m = 512 and 2048, q/k/v in one grouped launch
-              (TFLOP/s vs bf16 MFMA peak)
+  prefill     the seven projections at m = 512 and 2048 as the product calls them (q/k/v
+              in one grouped launch, gate/up fused with the GELU gating) (TFLOP/s vs bf16
+              MFMA peak)
   decode      48 layers (renormalise + q/k/v in one launch, o, fused gate/up + GELU, down)
               + tied LM head [262144,3840] with softcap + greedy sampling with its top-8
               sidecar on the device, m = 1 and 4, replayed from a captured HIP graph
@@ -139,10 +140,10 @@ def bench_quantize(stream, steps, warmup, copies=4):
             "gbs": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
 
-# The prefill calls of one layer as the engine makes them: q, k and v in one grouped launch
-# (they share the normed input), then o, gate, up and down.
-PREFILL_CALLS = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate", ("gate",)), ("up", ("up",)),
-                 ("down", ("down",)))
+# The layer's prefill calls as the product makes them: q/k/v in one grouped launch, o, the
+# MLP's gate and up as one fused launch with the GELU gating (hyp_qmlp_gate_up_gelu),
+# down.
+PREFILL_CALLS = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("mlp", ("gate", "up")), ("down", ("down",)))
 
 
 def dense_bf16_child(m, steps, warmup):
@@ -194,9 +195,12 @@ def bench_prefill(stream, m, steps, warmup, dense=None):
             n = syn.LAYER_SHAPES[proj][0]
             w, s, b = syn.q4_weights(n, k, seed=500 + 8 * ci + pi)
             qws.append(hy.QWeight.from_host(w, s, b))
-            yds.append(hy.DeviceArray((m, n), np.uint16))
+            if call_name != "mlp" or pi == 0:
+                yds.append(hy.DeviceArray((m, n), np.uint16))
         xd = hy.DeviceArray.from_host(syn.activations(m, k, seed=400 + ci), stream)
-        if len(qws) == 1:
+        if call_name == "mlp":
+            fn = lambda _i: hy.qmlp_gate_up_gelu(qws[0], qws[1], xd, m, yds[0], stream)  # noqa: E731
+        elif len(qws) == 1:
             fn = lambda _i: hy.qmatmul(qws[0], xd, m, yds[0], stream)  # noqa: E731
         else:
             fn = lambda _i: hy.qmatmul_group(qws, xd, m, yds, stream)  # noqa: E731

@@ -67,6 +67,11 @@ bool skinny_norm_supported(uint32_t m, uint32_t k);
 // x tiles in LDS. Plain bf16 output; epilogues for larger m run as the elementwise
 // kernels below.
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
+// y = bf16(gelu_chain(x . G^T) * (x . U^T)) as one dual GEMM: each wave accumulates a gate
+// tile and the same up tile, the epilogue applies the gating. Same kernel, split and sums
+// as the grouped GEMM of [gate, up], so y is gelu_mul of that launch's outputs bit for bit.
+void launch_q4_gemm_gate_up(const Q4Matrix& gate, const Q4Matrix& up, const uint16_t* x, uint32_t m, uint16_t* y,
+                            hipStream_t stream);
 // launch_q4_gemm with the split-k partials in a fixed device scratch array instead of a
 // stream-ordered temporary: allocates nothing (INVALID_ARGUMENT if the call's partials
 // exceed the 64 MiB scratch). Calls on one device share the scratch.

@@ -78,6 +78,9 @@ struct GemmParams {
     uint32_t pairs_per_split;
     uint32_t n_total;
     float* partial;
+    // Host dispatch only: the launch is a fused gate/up (seg[0] gate with the output,
+    // seg[1] up), run by the DUAL kernels.
+    uint32_t dual;
 };
 
 // The segment of global column tile tn (workgroup-uniform selects, no indexed parameter
@@ -135,14 +138,15 @@ __device__ __forceinline__ void dequant_step(const BRaw<NT>& raw, bf16x8_t (&b)[
 
 // Raw weights of pair `pair` for this lane: the 16-byte code entry and 8-byte scale
 // entry of each of its NT column tiles (offsets set up once, the pair is a scalar offset).
-template <int NT>
-__device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t sr,
-                                       const uint32_t (&c_off)[NT], const uint32_t (&s_off)[NT], uint32_t pair,
-                                       BRaw<NT>& raw) {
+template <int NT, typename R>
+__device__ __forceinline__ void load_b(const R& wr, const uint32_t (&c_off)[NT], const uint32_t (&s_off)[NT],
+                                       uint32_t pair, BRaw<NT>& raw) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        raw.c[nt] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(cr, c_off[nt], pair * 1024u, 0));
-        raw.sb[nt] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(sr, s_off[nt], pair * 128u, 0));
+        raw.c[nt] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(wr.c[nt & 1], c_off[nt], pair * 1024u, 0));
+        raw.sb[nt] = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(wr.s[nt & 1], s_off[nt], pair * 128u, 0));
     }
 }
 
@@ -184,8 +188,157 @@ __device__ __forceinline__ void mfma_step(const uint8_t* xb, uint32_t lane, cons
     }
 }
 
-template <int MT, int NT, bool ODD>
+// The fused MLP gating of one output (forward.cc:338-343 without the down projection):
+// the gate and up sums rounded to bf16 as a separate launch stores them, then
+// bf16(gelu_chain(gate) * up), bit for bit the elementwise gelu_mul pass over them.
+__device__ __forceinline__ uint16_t gated_bits(float gate_sum, float up_sum) {
+    const float g = bf16_bits_to_f32(f32_to_bf16_bits(gate_sum));
+    const float u = bf16_bits_to_f32(f32_to_bf16_bits(up_sum));
+    return f32_to_bf16_bits(gelu_tanh_bf16_chain(g) * u);
+}
+
+// The GELU chain of a bf16 input x is a function of its 16 bits with closed forms outside
+// 2^-10 <= |x| < 8: tanh's argument is then either below 2^-9 in magnitude (1 + t rounds
+// to 1, so the chain gives bf16(x / 2)) or at least 4 in magnitude (t = +-1, so it gives x
+// for finite x >= 8, -0 for finite x <= -8). A DUAL epilogue tabulates the band and the
+// 256 non-finite inputs (+-inf, NaN) in LDS with the chain itself (a few values per
+// thread) and looks outputs up.
+constexpr uint32_t kGeluLo = 0x3A80u;                  // bf16 bits of 2^-10 (magnitude)
+constexpr uint32_t kGeluHi = 0x4100u;                  // bf16 bits of 8
+constexpr uint32_t kGeluSpan = kGeluHi - kGeluLo;      // band values of one sign
+constexpr uint32_t kGeluInf = 0x7F80u;                 // magnitudes from here on: inf, NaN
+constexpr uint32_t kGeluSpecial = 0x8000u - kGeluInf;  // non-finite values of one sign
+constexpr uint32_t kGeluEntries = 2u * kGeluSpan + 2u * kGeluSpecial;
+constexpr uint32_t kGeluTableBytes = kGeluEntries * 2u;
+
+// The bf16 bits tabulated at entry i: the positive band, the negative band, then the
+// non-finite values of each sign.
+__device__ __forceinline__ uint32_t gelu_table_bits(uint32_t i) {
+    if (i < 2u * kGeluSpan) {
+        const uint32_t neg = i >= kGeluSpan ? 1u : 0u;
+        return (neg << 15) | (kGeluLo + i - neg * kGeluSpan);
+    }
+    const uint32_t j = i - 2u * kGeluSpan;
+    const uint32_t neg = j >= kGeluSpecial ? 1u : 0u;
+    return (neg << 15) | (kGeluInf + j - neg * kGeluSpecial);
+}
+
+__device__ __forceinline__ void build_gelu_table(uint16_t* tab, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t i = tid; i < kGeluEntries; i += nthreads)
+        tab[i] = f32_to_bf16_bits(gelu_tanh_bf16_chain(bf16_bits_to_f32(gelu_table_bits(i))));
+}
+
+// gelu_tanh_bf16_chain(x) for a bf16 value x, from the table and the closed forms; the
+// table is read for every x (entry 0 when x is outside it), so no branch is taken.
+__device__ __forceinline__ float gelu_lookup(const uint16_t* tab, float x) {
+    const uint32_t b = __float_as_uint(x) >> 16;
+    const uint32_t a = b & 0x7FFFu;
+    const uint32_t neg = b >> 15;
+    const bool band = a - kGeluLo < kGeluSpan;
+    const bool special = a >= kGeluInf;
+    const uint32_t idx = band ? neg * kGeluSpan + a - kGeluLo
+                              : (special ? 2u * kGeluSpan + neg * kGeluSpecial + a - kGeluInf : 0u);
+    const float tabulated = bf16_bits_to_f32(tab[idx]);
+    const float half = round_bf16(0.5f * x);
+    const float large = neg ? -0.0f : x;
+    return (band || special) ? tabulated : (a < kGeluLo ? half : large);
+}
+
+__device__ __forceinline__ uint16_t gated_bits_table(const uint16_t* tab, float gate_sum, float up_sum) {
+    const uint32_t gu = cvt_pk_bf16(gate_sum, up_sum);   // both rounded by one instruction
+    const float g = __uint_as_float(gu << 16);
+    const float u = __uint_as_float(gu & 0xFFFF0000u);
+    return f32_to_bf16_bits(gelu_lookup(tab, g) * u);
+}
+
+// Buffer resources of column tile nt: in a DUAL launch tile 0 is the gate's, tile 1 the
+// up projection's (seg[1]); otherwise all come from the segment in view.
+struct WeightRsrc {
+    __amdgpu_buffer_rsrc_t c[2];
+    __amdgpu_buffer_rsrc_t s[2];
+};
+
+template <bool DUAL>
+__device__ __forceinline__ WeightRsrc weight_rsrc(const GemmParams& p, const SegView& sv) {
+    WeightRsrc r;
+    r.c[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(sv.codes), static_cast<short>(0),
+                                               static_cast<int>(sv.code_bytes), 0x00020000);
+    r.s[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(sv.sb), static_cast<short>(0),
+                                               static_cast<int>(sv.sb_bytes), 0x00020000);
+    if (DUAL) {
+        r.c[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(p.seg[1].codes), static_cast<short>(0),
+                                                   static_cast<int>(p.seg[1].code_bytes), 0x00020000);
+        r.s[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(p.seg[1].sb), static_cast<short>(0),
+                                                   static_cast<int>(p.seg[1].sb_bytes), 0x00020000);
+    } else {
+        r.c[1] = r.c[0];
+        r.s[1] = r.s[0];
+    }
+    return r;
+}
+
+// The view of a workgroup's column tile tn: in a DUAL launch always the gate's segment
+// (the up projection rides along as column tile 1 of every wave).
+template <bool DUAL>
+__device__ __forceinline__ SegView view_of(const GemmParams& p, uint32_t tn) {
+    SegView sv = segment_of(p, DUAL ? 0u : tn);
+    if (DUAL) sv.tn = tn;
+    return sv;
+}
+
+// Split k: this workgroup's fp32 partials of k split kz, summed by the split-k reduce
+// kernels. acc[mt][nt][r] is (row 16 mt + 4 kb + r, column 16 (kOut wave + nt) + j) of
+// the tile (DUAL: column 16 wave + j of the gate for nt = 0, of up for nt = 1, which sits
+// seg[1].col_begin further along the workspace row).
+template <int MT, int NT, int kOut, bool DUAL>
+__device__ __forceinline__ void store_partials(const GemmParams& p, const SegView& sv, uint32_t kz, uint32_t m0,
+                                               uint32_t n0, uint32_t wave, uint32_t lane,
+                                               const f32x4_t (&acc)[MT][NT]) {
+    const uint32_t j = lane & 15u;
+    const uint32_t kb = lane >> 4;
+    float* part = p.partial + static_cast<size_t>(kz) * p.m * p.n_total;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t col = n0 + (wave * kOut + (DUAL ? 0 : nt)) * 16u + j;
+        const uint32_t base = DUAL && nt == 1 ? p.seg[1].col_begin : sv.col_begin;
+        if (col >= sv.n) continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t row = m0 + mt * 16u + kb * 4u + r;
+                if (row < p.m) part[static_cast<size_t>(row) * p.n_total + base + col] = acc[mt][nt][r];
+            }
+    }
+}
+
+// The tile's bf16 outputs into LDS rows of out_row bytes: column 16 (kOut wave + nt) + j
+// gets bf16(acc[.][nt]); DUAL: column 16 wave + j gets the gated value of acc[.][0] (gate)
+// and acc[.][1] (up), through the GELU table `tab` (built in LDS past the rows).
+template <int MT, int NT, int kOut, bool DUAL>
+__device__ __forceinline__ void stage_out(uint8_t* xs, uint32_t out_row, uint32_t wave, uint32_t lane,
+                                          const f32x4_t (&acc)[MT][NT], const uint16_t* tab) {
+    const uint32_t j = lane & 15u;
+    const uint32_t kb = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kOut; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t row = mt * 16u + kb * 4u + r;
+                const uint32_t col = (wave * kOut + nt) * 16u + j;
+                const uint16_t v =
+                    DUAL ? gated_bits_table(tab, acc[mt][0][r], acc[mt][NT - 1][r])
+                         : f32_to_bf16_bits(acc[mt][nt][r]);
+                *reinterpret_cast<uint16_t*>(xs + row * out_row + col * 2u) = v;
+            }
+}
+
+template <int MT, int NT, bool ODD, bool DUAL>
 __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
+    static_assert(!DUAL || NT == 2, "a dual launch pairs one gate and one up tile per wave");
+    constexpr int kOut = DUAL ? 1 : NT;   // output column tiles per wave
     constexpr int BM = 16 * MT;
     constexpr int kTileBytes = BM * kRowBytes;
     constexpr int kXLoads = BM / 4 / kWaves;   // 1 KB direct loads per wave per X tile
@@ -206,10 +359,10 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     const uint32_t kz = ext / p.tiles_total;          // this workgroup's k split
     const uint32_t tile = ext - kz * p.tiles_total;
     const uint32_t tm = tile / p.tiles_n;
-    const SegView sv = segment_of(p, tile - tm * p.tiles_n);
+    const SegView sv = view_of<DUAL>(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
-    const uint32_t n0 = sv.tn * (kWaves * 16u * NT);
-    const uint32_t tile16_0 = n0 / 16u + wave * NT;
+    const uint32_t n0 = sv.tn * (kWaves * 16u * kOut);
+    const uint32_t tile16_0 = n0 / 16u + wave * kOut;
 
     const uint32_t k = p.k;
     const uint32_t pairs = p.pairs;
@@ -244,17 +397,14 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
         }
     };
 
-    // Weights: column tile (tile16_0 + nt), clamped to the last tile (columns past n are
-    // computed, never stored).
-    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint4*>(sv.codes), static_cast<short>(0), static_cast<int>(sv.code_bytes), 0x00020000);
-    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint2*>(sv.sb), static_cast<short>(0), static_cast<int>(sv.sb_bytes), 0x00020000);
+    // Weights: column tile (tile16_0 + nt) (DUAL: tile tile16_0 of the gate, then of up),
+    // clamped to the last tile (columns past n are computed, never stored).
+    const WeightRsrc wr = weight_rsrc<DUAL>(p, sv);
     uint32_t c_off[NT];
     uint32_t s_off[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t t16 = min(tile16_0 + nt, sv.row_tiles - 1u);
+        const uint32_t t16 = min(tile16_0 + (DUAL ? 0u : static_cast<uint32_t>(nt)), sv.row_tiles - 1u);
         c_off[nt] = (t16 * pairs * 64u + lane) * 16u;
         s_off[nt] = (t16 * pairs * 16u + (lane & 15u)) * 8u;
     }
@@ -271,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
 
     BRaw<NT> braw, bnext;
     load_x(p0, xs);
-    load_b<NT>(cr, sr, c_off, s_off, p0, braw);
+    load_b<NT>(wr, c_off, s_off, p0, braw);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
@@ -284,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
         const uint8_t* xb = xs + ((pair - p0) & 1u) * kTileBytes;
         const uint32_t pn = min(pair + 1u, p1 - 1u);
         load_x(pn, xs + ((pair - p0 + 1u) & 1u) * kTileBytes);
-        load_b<NT>(cr, sr, c_off, s_off, pn, bnext);
+        load_b<NT>(wr, c_off, s_off, pn, bnext);
 
         dequant_step<NT, 1>(braw, b1);
         mfma_step<MT, NT, 0>(xb, lane, b0, acc);
@@ -301,48 +451,27 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmParams p) {
     }
 
     if (p.ksplit > 1u) {
-        // Split k: fp32 partials, summed by q4_splitk_reduce_kernel.
-        const uint32_t j = lane & 15u;
-        const uint32_t kb = lane >> 4;
-        float* part = p.partial + static_cast<size_t>(kz) * p.m * p.n_total;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const uint32_t col = n0 + (wave * NT + nt) * 16u + j;
-            if (col >= sv.n) continue;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t row = m0 + mt * 16u + kb * 4u + r;
-                    if (row < p.m) part[static_cast<size_t>(row) * p.n_total + sv.col_begin + col] = acc[mt][nt][r];
-                }
-        }
+        store_partials<MT, NT, kOut, DUAL>(p, sv, kz, m0, n0, wave, lane, acc);
         return;
     }
 
-    // Epilogue: the workgroup's (16 MT) x (64 NT) tile goes through LDS (rows of
-    // 128 NT bytes plus 32 bytes of padding, so the four row groups a write touches hit
+    // Epilogue: the workgroup's (16 MT) x (64 kOut) tile goes through LDS (rows of
+    // 128 kOut bytes plus 32 bytes of padding, so the four row groups a write touches hit
     // distinct banks) and leaves as 16-byte row segments. acc[mt][nt][r] is tile element
-    // (16 mt + 4 kb + r, 16 NT wave + 16 nt + j).
-    constexpr uint32_t kOutRow = 128u * NT + 32u;
-    static_assert(BM * kOutRow <= 2u * kTileBytes, "output staging exceeds the X buffers");
+    // (16 mt + 4 kb + r, 16 kOut wave + 16 nt + j) (DUAL: nt = 0 gate, 1 up of column
+    // 16 wave + j).
+    constexpr uint32_t kOutRow = 128u * kOut + 32u;
+    static_assert(BM * kOutRow + (DUAL ? kGeluTableBytes : 0u) <= 2u * kTileBytes,
+                  "output staging exceeds the X buffers");
+    uint16_t* tab = reinterpret_cast<uint16_t*>(xs + BM * kOutRow);
     __syncthreads();
-    {
-        const uint32_t j = lane & 15u;
-        const uint32_t kb = lane >> 4;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t row = mt * 16u + kb * 4u + r;
-                    const uint32_t col = (wave * NT + nt) * 16u + j;
-                    *reinterpret_cast<uint16_t*>(xs + row * kOutRow + col * 2u) = f32_to_bf16_bits(acc[mt][nt][r]);
-                }
+    if constexpr (DUAL) {
+        build_gelu_table(tab, tid, kThreads);
+        __syncthreads();
     }
+    stage_out<MT, NT, kOut, DUAL>(xs, kOutRow, wave, lane, acc, tab);
     __syncthreads();
-    constexpr uint32_t kCols = 64u * NT;
+    constexpr uint32_t kCols = 64u * kOut;
     constexpr uint32_t kChunks = kCols / 8u;                  // 16-byte chunks per row
     constexpr uint32_t kRowsPerPass = kThreads / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
@@ -386,16 +515,16 @@ struct GRaw {
     uint32_t sb[NT];   // scale | bias << 16 of the group
 };
 
-template <int NT>
-__device__ __forceinline__ void load_graw(__amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t sr,
-                                          const uint32_t (&c_off)[NT], const uint32_t (&s_off)[NT], uint32_t g,
-                                          GRaw<NT>& raw) {
+template <int NT, typename R>
+__device__ __forceinline__ void load_graw(const R& wr, const uint32_t (&c_off)[NT], const uint32_t (&s_off)[NT],
+                                          uint32_t g, GRaw<NT>& raw) {
     const uint32_t pair = g >> 1;
     const uint32_t h = g & 1u;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        raw.c[nt] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(cr, c_off[nt], pair * 1024u + h * 8u, 0));
-        raw.sb[nt] = __builtin_amdgcn_raw_buffer_load_b32(sr, s_off[nt], pair * 128u + h * 4u, 0);
+        raw.c[nt] = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(wr.c[nt & 1], c_off[nt], pair * 1024u + h * 8u, 0));
+        raw.sb[nt] = __builtin_amdgcn_raw_buffer_load_b32(wr.s[nt & 1], s_off[nt], pair * 128u + h * 4u, 0);
     }
 }
 
@@ -465,7 +594,16 @@ template <int MT>
 constexpr uint32_t g_sync_groups() { return MT >= 16 ? 2u : 4u; }
 
 template <int MT, int NT, int W>
+constexpr size_t g_lds_bytes() {
+    return 2u * g_sync_groups<MT>() * 16u * MT * kGRowBytes > 16u * MT * (32u * NT * W + 32u)
+               ? 2u * g_sync_groups<MT>() * 16u * MT * kGRowBytes
+               : 16u * MT * (32u * NT * W + 32u);
+}
+
+template <int MT, int NT, int W, bool DUAL>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_g_kernel(GemmParams p) {
+    static_assert(!DUAL || NT == 2, "a dual launch pairs one gate and one up tile per wave");
+    constexpr int kOut = DUAL ? 1 : NT;   // output column tiles per wave
     constexpr uint32_t BM = 16u * MT;
     constexpr uint32_t kStage = BM * kGRowBytes;
     constexpr uint32_t kSync = g_sync_groups<MT>();   // groups per barrier; X ring of 2 kSync stages
@@ -488,10 +626,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const uint32_t kz = ext / p.tiles_total;          // this workgroup's k split
     const uint32_t tile = ext - kz * p.tiles_total;
     const uint32_t tm = tile / p.tiles_n;
-    const SegView sv = segment_of(p, tile - tm * p.tiles_n);
+    const SegView sv = view_of<DUAL>(p, tile - tm * p.tiles_n);
     const uint32_t m0 = tm * BM;
-    const uint32_t n0 = sv.tn * (W * 16u * NT);
-    const uint32_t tile16_0 = n0 / 16u + wave * NT;
+    const uint32_t n0 = sv.tn * (W * 16u * kOut);
+    const uint32_t tile16_0 = n0 / 16u + wave * kOut;
     const uint32_t k = p.k;
     // This workgroup's groups [g0, g1): whole pairs of its split (all groups without split k).
     const uint32_t g0 = 2u * kz * p.pairs_per_split;
@@ -518,15 +656,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 static_cast<int>(xoff[t]), static_cast<int>(g * 128u), 0, 0);
     };
 
-    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint4*>(sv.codes), static_cast<short>(0), static_cast<int>(sv.code_bytes), 0x00020000);
-    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint2*>(sv.sb), static_cast<short>(0), static_cast<int>(sv.sb_bytes), 0x00020000);
+    const WeightRsrc wr = weight_rsrc<DUAL>(p, sv);
     uint32_t c_off[NT];
     uint32_t s_off[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t t16 = min(tile16_0 + nt, sv.row_tiles - 1u);
+        const uint32_t t16 = min(tile16_0 + (DUAL ? 0u : static_cast<uint32_t>(nt)), sv.row_tiles - 1u);
         c_off[nt] = (t16 * p.pairs * 64u + lane) * 16u;
         s_off[nt] = (t16 * p.pairs * 16u + (lane & 15u)) * 8u;
     }
@@ -540,8 +675,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     GRaw<NT> r[3];
 #pragma unroll
     for (uint32_t i = 0; i < kSync; ++i) load_x(min(g0 + i, g1 - 1u), xs + i * kStage);
-    load_graw<NT>(cr, sr, c_off, s_off, g0, r[0]);
-    load_graw<NT>(cr, sr, c_off, s_off, min(g0 + 1u, g1 - 1u), r[1]);
+    load_graw<NT>(wr, c_off, s_off, g0, r[0]);
+    load_graw<NT>(wr, c_off, s_off, min(g0 + 1u, g1 - 1u), r[1]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     bf16x8_t b0[NT], b1[NT];
@@ -575,7 +710,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         const uint8_t* xb = xs + ((g - g0) & kRing) * kStage;
         load_x(min(g + kSync, g1 - 1u), xs + ((g - g0 + kSync) & kRing) * kStage);
         __builtin_amdgcn_sched_barrier(0);   // the raw loads below issue after the X loads
-        load_graw<NT>(cr, sr, c_off, s_off, min(g + 2u, g1 - 1u), r[(s + 2) % 3]);
+        load_graw<NT>(wr, c_off, s_off, min(g + 2u, g1 - 1u), r[(s + 2) % 3]);
         static_for(
             [&](auto uc) {
                 constexpr int u = decltype(uc)::value;
@@ -622,44 +757,23 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (p.ksplit > 1u) {
-        // Split k: fp32 partials, summed by q4_splitk_reduce_kernel.
-        const uint32_t j = lane & 15u;
-        const uint32_t kb = lane >> 4;
-        float* part = p.partial + static_cast<size_t>(kz) * p.m * p.n_total;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const uint32_t col = n0 + (wave * NT + nt) * 16u + j;
-            if (col >= sv.n) continue;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t row = m0 + mt * 16u + kb * 4u + r;
-                    if (row < p.m) part[static_cast<size_t>(row) * p.n_total + sv.col_begin + col] = acc[mt][nt][r];
-                }
-        }
+        store_partials<MT, NT, kOut, DUAL>(p, sv, kz, m0, n0, wave, lane, acc);
         return;
     }
 
-    // Epilogue through LDS as in q4_gemm_kernel (rows of 32 NT W bytes plus 32 of padding).
-    constexpr uint32_t kOutRow = 32u * NT * W + 32u;
+    // Epilogue through LDS as in q4_gemm_kernel (rows of 32 kOut W bytes plus 32 of padding).
+    constexpr uint32_t kOutRow = 32u * kOut * W + 32u;
+    static_assert(BM * kOutRow + (DUAL ? kGeluTableBytes : 0u) <= g_lds_bytes<MT, NT, W>(),
+                  "output staging exceeds the LDS");
+    uint16_t* tab = reinterpret_cast<uint16_t*>(xs + BM * kOutRow);
     __syncthreads();
-    {
-        const uint32_t j = lane & 15u;
-        const uint32_t kb = lane >> 4;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t row = mt * 16u + kb * 4u + r;
-                    const uint32_t col = (wave * NT + nt) * 16u + j;
-                    *reinterpret_cast<uint16_t*>(xs + row * kOutRow + col * 2u) = f32_to_bf16_bits(acc[mt][nt][r]);
-                }
+    if constexpr (DUAL) {
+        build_gelu_table(tab, tid, 64u * W);
+        __syncthreads();
     }
+    stage_out<MT, NT, kOut, DUAL>(xs, kOutRow, wave, lane, acc, tab);
     __syncthreads();
-    constexpr uint32_t kChunks = 16u * NT * W / 8u;
+    constexpr uint32_t kChunks = 16u * kOut * W / 8u;
     constexpr uint32_t kRowsPerPass = 64u * W / kChunks;
     const uint32_t ch = threadIdx.x % kChunks;
     const uint32_t col0 = n0 + ch * 8u;
@@ -682,12 +796,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     }
 }
 
-template <int MT, int NT, int W>
-constexpr size_t g_lds_bytes() {
-    return 2u * g_sync_groups<MT>() * 16u * MT * kGRowBytes > 16u * MT * (32u * NT * W + 32u)
-               ? 2u * g_sync_groups<MT>() * 16u * MT * kGRowBytes
-               : 16u * MT * (32u * NT * W + 32u);
-}
 
 // The same with 8 consecutive workspace columns per thread (two 16-byte loads per split,
 // one 16-byte store), for grids where every segment's width and first column are
@@ -737,6 +845,27 @@ __global__ __launch_bounds__(kThreads) void q4_splitk_reduce_kernel(GemmParams p
     y[static_cast<size_t>(row) * n + (c - c0)] = f32_to_bf16_bits(sum);
 }
 
+// The split-k reduce of a DUAL launch: y[row][col] = gated(sum over z of the gate
+// partial at workspace column col, the same of up at column seg[1].col_begin + col), one
+// thread per output, the sums in the order of q4_splitk_reduce_kernel.
+__global__ __launch_bounds__(kThreads) void q4_splitk_reduce_dual_kernel(GemmParams p) {
+    const uint32_t n = p.seg[0].n;
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t outs = static_cast<uint64_t>(p.m) * n;
+    if (e >= outs) return;
+    const uint32_t row = static_cast<uint32_t>(e / n);
+    const uint32_t c = static_cast<uint32_t>(e - static_cast<uint64_t>(row) * n);
+    const uint64_t total = static_cast<uint64_t>(p.m) * p.n_total;
+    const uint64_t at = static_cast<uint64_t>(row) * p.n_total + c;
+    float g = 0.0f;
+    float u = 0.0f;
+    for (uint32_t z = 0; z < p.ksplit; ++z) {
+        g += p.partial[z * total + at];
+        u += p.partial[z * total + at + p.seg[1].col_begin];
+    }
+    p.seg[0].y[static_cast<size_t>(row) * n + c] = gated_bits(g, u);
+}
+
 size_t max_lds_per_block() {
     static thread_local int cached_device = -1;
     static thread_local size_t cached = 0;
@@ -753,8 +882,14 @@ size_t max_lds_per_block() {
 
 constexpr uint32_t kTileCols = 128u;   // workgroup tile width of the pair-step kernel (NT = 2)
 
-// Column tiles of `tile_cols` columns: each segment's first global tile and the total.
+// Column tiles of `tile_cols` output columns: each segment's first global tile and the
+// total (a dual launch tiles the gate's columns only; up rides along).
 void retile(GemmParams& p, uint32_t tile_cols) {
+    if (p.dual != 0u) {
+        p.seg[0].tn_begin = 0u;
+        p.tiles_n = (p.seg[0].n + tile_cols - 1u) / tile_cols;
+        return;
+    }
     uint32_t tn = 0;
     for (uint32_t i = 0; i < p.nseg; ++i) {
         p.seg[i].tn_begin = tn;
@@ -763,10 +898,11 @@ void retile(GemmParams& p, uint32_t tile_cols) {
     p.tiles_n = tn;
 }
 
-template <int MT, int NT>
+template <int MT, int NT, bool DUAL>
 void launch_t(GemmParams p, hipStream_t stream) {
+    retile(p, kWaves * 16u * (DUAL ? 1u : NT));
     const bool odd = ((p.k / 64u) & 1u) != 0u;
-    auto kernel = odd ? q4_gemm_kernel<MT, NT, true> : q4_gemm_kernel<MT, NT, false>;
+    auto kernel = odd ? q4_gemm_kernel<MT, NT, true, DUAL> : q4_gemm_kernel<MT, NT, false, DUAL>;
     const size_t lds = 2u * 16u * MT * kRowBytes;
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
     if (lds > 65536u) {
@@ -774,9 +910,9 @@ void launch_t(GemmParams p, hipStream_t stream) {
         int dev = 0;
         HYP_HIP_CHECK(hipGetDevice(&dev));
         if (configured_device != dev) {
-            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(q4_gemm_kernel<MT, NT, true>),
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(q4_gemm_kernel<MT, NT, true, DUAL>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(q4_gemm_kernel<MT, NT, false>),
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(q4_gemm_kernel<MT, NT, false, DUAL>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
             configured_device = dev;
         }
@@ -786,10 +922,10 @@ void launch_t(GemmParams p, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3(p.tiles_total * p.ksplit), dim3(kThreads), lds, stream, p);
 }
 
-template <int MT, int NT, int W>
+template <int MT, int NT, int W, bool DUAL>
 void launch_g(GemmParams p, hipStream_t stream) {
-    retile(p, 16u * NT * W);
-    auto kernel = q4_gemm_g_kernel<MT, NT, W>;
+    retile(p, 16u * (DUAL ? 1u : NT) * W);
+    auto kernel = q4_gemm_g_kernel<MT, NT, W, DUAL>;
     constexpr size_t lds = g_lds_bytes<MT, NT, W>();
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
     if (lds > 65536u) {
@@ -839,6 +975,7 @@ GemmParams group_params(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t
     p.pairs_per_split = p.pairs;
     p.n_total = n_total;
     p.partial = nullptr;
+    p.dual = 0u;
     return p;
 }
 
@@ -854,12 +991,21 @@ struct GemmChoice {
     uint32_t ksplit;
 };
 
-void launch_params(GemmParams& p, GemmKernel kernel, hipStream_t stream) {
+template <bool DUAL>
+void launch_kernel(GemmParams& p, GemmKernel kernel, hipStream_t stream) {
     switch (kernel) {
-        case GemmKernel::kPair128: launch_t<8, 2>(p, stream); break;
-        case GemmKernel::kGroup128: launch_g<8, 2, kGroupWaves>(p, stream); break;
-        case GemmKernel::kGroup256: launch_g<16, 2, kGroupWaves>(p, stream); break;
+        case GemmKernel::kPair128: launch_t<8, 2, DUAL>(p, stream); break;
+        case GemmKernel::kGroup128: launch_g<8, 2, kGroupWaves, DUAL>(p, stream); break;
+        case GemmKernel::kGroup256: launch_g<16, 2, kGroupWaves, DUAL>(p, stream); break;
         default: throw NativeError(HYP_STATUS_INTERNAL, "gemm: unsupported kernel");
+    }
+}
+
+void launch_params(GemmParams& p, GemmKernel kernel, hipStream_t stream) {
+    if (p.dual != 0u) {
+        launch_kernel<true>(p, kernel, stream);
+    } else {
+        launch_kernel<false>(p, kernel, stream);
     }
     HYP_HIP_CHECK(hipGetLastError());
 }
@@ -937,15 +1083,23 @@ void launch_split(GemmParams& p, GemmKernel kernel, uint32_t ksplit, hipStream_t
     p.partial = static_cast<float*>(ws);
     try {
         launch_params(p, kernel, stream);
-        bool vec = true;
-        for (uint32_t i = 0; i < p.nseg; ++i)
-            vec = vec && p.seg[i].n % 8u == 0u && p.seg[i].col_begin % 8u == 0u &&
-                  (reinterpret_cast<uintptr_t>(p.seg[i].y) & 15u) == 0u;
-        const uint64_t per_thread = vec ? 8u : 1u;
-        const uint64_t blocks = (elems / per_thread + kThreads - 1u) / kThreads;
-        HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
-        hipLaunchKernelGGL(vec ? q4_splitk_reduce8_kernel : q4_splitk_reduce_kernel, dim3(static_cast<uint32_t>(blocks)),
-                           dim3(kThreads), 0, stream, p);
+        if (p.dual != 0u) {
+            const uint64_t outs = static_cast<uint64_t>(p.m) * p.seg[0].n;
+            const uint64_t blocks = (outs + kThreads - 1u) / kThreads;
+            HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
+            hipLaunchKernelGGL(q4_splitk_reduce_dual_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                               stream, p);
+        } else {
+            bool vec = true;
+            for (uint32_t i = 0; i < p.nseg; ++i)
+                vec = vec && p.seg[i].n % 8u == 0u && p.seg[i].col_begin % 8u == 0u &&
+                      (reinterpret_cast<uintptr_t>(p.seg[i].y) & 15u) == 0u;
+            const uint64_t per_thread = vec ? 8u : 1u;
+            const uint64_t blocks = (elems / per_thread + kThreads - 1u) / kThreads;
+            HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "gemm: output too large");
+            hipLaunchKernelGGL(vec ? q4_splitk_reduce8_kernel : q4_splitk_reduce_kernel,
+                               dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, p);
+        }
         HYP_HIP_CHECK(hipGetLastError());
     } catch (...) {
         if (wsp.fixed == nullptr) (void)hipFreeAsync(ws, stream);
@@ -988,6 +1142,17 @@ void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32
                           uint32_t m, hipStream_t stream) {
     GemmParams p = group_params(ws, ys, count, x, m);
     const GemmChoice c = choose_gemm(p);
+    launch_split(p, c.kernel, c.ksplit, stream);
+}
+
+void launch_q4_gemm_gate_up(const Q4Matrix& gate, const Q4Matrix& up, const uint16_t* x, uint32_t m, uint16_t* y,
+                            hipStream_t stream) {
+    HYP_REQUIRE(gate.n == up.n && gate.k == up.k, HYP_STATUS_INVALID_ARGUMENT, "gate and up must have the same shape");
+    const Q4Matrix* ws[2] = {&gate, &up};
+    uint16_t* ys[2] = {y, nullptr};
+    GemmParams p = group_params(ws, ys, 2u, x, m);
+    const GemmChoice c = choose_gemm(p);   // the kernel and split of the grouped gate/up launch
+    p.dual = 1u;
     launch_split(p, c.kernel, c.ksplit, stream);
 }
 

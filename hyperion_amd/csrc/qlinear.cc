@@ -190,19 +190,9 @@ void mlp_gate_up(const QuantizedLinear& gate, const QuantizedLinear& up, const u
         hip::launch_q4_skinny(gate.mat, &up.mat, x, m, h, Epilogue::kNone, 0.0f, 0u, stream);
         return;
     }
-    // h <- gate(x); u <- up(x) in a stream-ordered temporary; h <- gelu(h) * u.
-    const size_t bytes = static_cast<size_t>(m) * up.mat.n * sizeof(uint16_t);
-    void* u = nullptr;
-    HYP_HIP_CHECK(hipMallocAsync(&u, bytes, stream));
-    try {
-        hip::launch_q4_gemm(gate.mat, x, m, h, stream);
-        hip::launch_q4_gemm(up.mat, x, m, static_cast<uint16_t*>(u), stream);
-        hip::launch_gelu_mul(h, static_cast<const uint16_t*>(u), static_cast<uint64_t>(m) * up.mat.n, stream);
-    } catch (...) {
-        (void)hipFreeAsync(u, stream);
-        throw;
-    }
-    HYP_HIP_CHECK(hipFreeAsync(u, stream));
+    // One dual GEMM: each wave accumulates a gate tile and the matching up tile and the
+    // epilogue stores bf16(gelu(gate) * up) (no gate/up temporaries, no elementwise pass).
+    hip::launch_q4_gemm_gate_up(gate.mat, up.mat, x, m, h, stream);
 }
 
 }  // namespace hyperion::model

@@ -486,12 +486,15 @@ def _assert_close_bits(got, ref, what, max_ulp=1):
 
 @pytest.mark.parametrize("m", [1, 4, 300])
 def test_gate_up_gelu_fused(stream, m):
-    """The fused gate/up (m <= 4: one launch) against the oracle's bf16 GELU chain applied
-    to separate gate and up launches, and against the chain applied to the fp64 truth.
-    The fused launch may split a tile's k range differently from a separate launch, so its
-    fp32 sums of gate and up are the same terms in another order: a bf16 gate or up value
-    can then round the other way (1 ulp), which the GELU chain and the product carry to at
-    most 2 ulps, in at most 0.1% of the outputs."""
+    """The fused gate/up against the oracle's bf16 GELU chain applied to gate and up
+    launches, and against the chain applied to the fp64 truth.
+    m <= 4: one decode launch, against separate gate and up launches. It may split a
+    tile's k range differently, so its fp32 sums are the same terms in another order: a
+    bf16 gate or up value can then round the other way (1 ulp), which the GELU chain and
+    the product carry to at most 2 ulps, in at most 0.1% of the outputs here (deep in
+    GELU's negative tail one gate ulp moves the output by many ulps).
+    m > 4: the dual GEMM, against the grouped [gate, up] launch, which makes the same k
+    split and sums: bit-exact."""
     n, k = 15360, 3840
     say(f"gate/up gelu m={m}")
     x = syn.activations(m, k, seed=600 + m)
@@ -503,11 +506,18 @@ def test_gate_up_gelu_fused(stream, m):
     g = hy.DeviceArray((m, n), np.uint16)
     u = hy.DeviceArray((m, n), np.uint16)
     h = hy.DeviceArray((m, n), np.uint16)
-    hy.qmatmul(gate, xd, m, g, stream)
-    hy.qmatmul(up, xd, m, u, stream)
+    if m > 4:
+        hy.qmatmul_group([gate, up], xd, m, [g, u], stream)
+    else:
+        hy.qmatmul(gate, xd, m, g, stream)
+        hy.qmatmul(up, xd, m, u, stream)
     hy.qmlp_gate_up_gelu(gate, up, xd, m, h, stream)
     hb = h.to_host(stream)
-    _assert_close_bits(hb, O.gelu_tanh_mul(g.to_host(stream), u.to_host(stream)), f"m={m}", max_ulp=2)
+    chain = O.gelu_tanh_mul(g.to_host(stream), u.to_host(stream))
+    if m > 4:
+        np.testing.assert_array_equal(hb, chain, err_msg=f"m={m}")
+    else:
+        _assert_close_bits(hb, chain, f"m={m}", max_ulp=2)
     rows = min(m, 8)
     g64 = O.qmatmul_f64(x[:rows], gw, gs, gb) if m <= 4 else O.qmatmul_deq_f64(x[:rows], gw, gs, gb, mode=1)
     u64 = O.qmatmul_f64(x[:rows], uw, us, ub) if m <= 4 else O.qmatmul_deq_f64(x[:rows], uw, us, ub, mode=1)
@@ -515,6 +525,41 @@ def test_gate_up_gelu_fused(stream, m):
     rel = syn.sig_rel(syn.bf16_to_f32(hb[:rows]), truth)
     say(f"  gate/up gelu m={m}: sig_rel vs the chain on the fp64 gate and up = {rel:.2e} (bound 1e-2)")
     assert rel <= 1e-2
+
+
+DUAL_CASES = [
+    # n, k, m: the 256 x 256 group-step kernel; the 128 x 256 one; the pair-step kernel;
+    # the pair-step kernel split 4 ways (the dual split-k reduce); an odd group count; a
+    # ragged n; the smallest GEMM batch
+    (15360, 3840, 2048),
+    (15360, 3840, 512),
+    (15360, 3840, 64),
+    (512, 3840, 64),
+    (384, 192, 40),
+    (1000, 640, 33),
+    (15360, 3840, 5),
+]
+
+
+@pytest.mark.parametrize("n,k,m", DUAL_CASES)
+def test_gate_up_gelu_dual_gemm_equals_grouped_launch(stream, n, k, m):
+    """At m > 4 hyp_qmlp_gate_up_gelu is one dual GEMM (gate and up tiles accumulated by
+    the same wave, the gating in the epilogue). It picks the kernel and k split of the
+    grouped [gate, up] GEMM and sums the same terms in the same order, so its output is
+    the oracle's GELU chain over that launch's gate and up outputs, bit for bit."""
+    say(f"dual gate/up gemm n={n} k={k} m={m}")
+    x = syn.activations(m, k, seed=620 + m)
+    gate = hy.QWeight.from_host(*syn.q4_weights(n, k, seed=621 + n))
+    up = hy.QWeight.from_host(*syn.q4_weights(n, k, seed=622 + n))
+    xd = dev(x, stream)
+    g = hy.DeviceArray((m, n), np.uint16)
+    u = hy.DeviceArray((m, n), np.uint16)
+    h = hy.DeviceArray((m, n), np.uint16)
+    hy.qmatmul_group([gate, up], xd, m, [g, u], stream)
+    hy.qmlp_gate_up_gelu(gate, up, xd, m, h, stream)
+    np.testing.assert_array_equal(h.to_host(stream), O.gelu_tanh_mul(g.to_host(stream), u.to_host(stream)))
+    for a in (gate, up, xd, g, u, h):
+        a.close()
 
 
 @pytest.mark.parametrize("m", [1, 300])

@@ -398,6 +398,24 @@ def test_sample_greedy_restatement_matches_definition():
 
 
 
+
+def test_gelu_chain_closed_forms_outside_the_tabulated_band():
+    """The dual GEMM's epilogue tabulates the GELU chain for 2^-10 <= |x| < 8 and uses
+    closed forms elsewhere: bf16(x / 2) below the band (tanh's argument is under 2^-9, so
+    1 + t rounds to 1), x above it (and +inf), -0 below -8 (t = -1, so 1 + t = 0). Checked
+    here against the oracle's chain for every other finite bf16 input and +inf."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    a = bits & 0x7FFF
+    outside = ((a < 0x3A80) | (a >= 0x4100)) & (a <= 0x7F80) & (bits != 0xFF80)
+    xs = bits[outside]
+    got = O.gelu_tanh(xs)
+    x = syn.bf16_to_f32(xs)
+    small = (xs & 0x7FFF) < 0x3A80
+    want = np.where(small, O.bf16_from_f32((np.float32(0.5) * x).astype(np.float32)),
+                    np.where(x > 0, xs, np.uint16(0x8000)))
+    assert xs.size == 65536 - 2 * (0x4100 - 0x3A80) - 2 * 127 - 1
+    np.testing.assert_array_equal(got, want.astype(np.uint16))
+
 # ---------------------------------------------------------------- top-k sidecar of the greedy epilogue
 def _distinct_top_row(rng, n, k=O.TOP_K):
     """A row whose k + 1 largest values are distinct: normal draws in [-8, 8] plus k + 1
