@@ -372,6 +372,7 @@ def main():
     ap.add_argument("--only-decode", action="store_true", help="only the headline decode GEMV")
     ap.add_argument("--only-prefill", action="store_true", help="the headline decode GEMV and the prefill GEMMs")
     ap.add_argument("--only-sample", action="store_true", help="the headline decode GEMV and greedy sampling")
+    ap.add_argument("--only-quantize", action="store_true", help="the headline decode GEMV and quantize/pack")
     ap.add_argument("--only-stream", action="store_true", help="the headline decode GEMV and the decode stream")
     ap.add_argument("--dense-ref", action="store_true",
                     help="also time hipBLASLt's dense bf16 GEMM (torch.matmul) on the prefill shapes")
@@ -407,6 +408,8 @@ def main():
         extra["prefill"] = [bench_prefill(stream, m, 10, 2, dense.get(m)) for m in (512, 2048)]
     elif args.only_sample:
         extra["sample_greedy"] = bench_sample(stream, 20, 3)
+    elif args.only_quantize:
+        extra["quantize"] = bench_quantize(stream, 50, 5)
     elif args.only_stream:
         model = dc.DecodeModel(hy, args.layers, log)
         extra["decode_stream"] = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]

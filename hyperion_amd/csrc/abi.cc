@@ -556,6 +556,11 @@ HypStatus hyp_quantize_q4g64(const void* w, uint32_t n, uint32_t k, uint32_t* w_
         validate_quant(n, k, 64, 4);
         REQUIRE_ARG(w != nullptr && w_out != nullptr && scales_out != nullptr && biases_out != nullptr,
                     "quantize requires non-null device buffers");
+        REQUIRE_ARG((reinterpret_cast<uintptr_t>(w) & 15u) == 0u && (reinterpret_cast<uintptr_t>(w_out) & 15u) == 0u,
+                    "quantize requires 16-byte aligned w and w_out");
+        REQUIRE_ARG((reinterpret_cast<uintptr_t>(scales_out) & 1u) == 0u &&
+                        (reinterpret_cast<uintptr_t>(biases_out) & 1u) == 0u,
+                    "quantize requires 2-byte aligned scales and biases");
         hyperion::hip::launch_q4_quantize(static_cast<const uint16_t*>(w), n, k, w_out,
                                           static_cast<uint16_t*>(scales_out), static_cast<uint16_t*>(biases_out), s);
     });

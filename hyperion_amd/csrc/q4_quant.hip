@@ -22,28 +22,40 @@ constexpr int kThreads = 256;
 // quotients are formed with the group's correctly rounded reciprocal: fl(fl(d) * fl(1/s))
 // is within 2^-23 relative, so for |q| < 64 within 2^-17, of the IEEE quotient, and both
 // round to the same integer unless a half-integer lies within 2^-17 of the approximate
-// quotient; the exact divisions are done (for all 8) when any approximate quotient lies
-// within 2^-16 of one (twice the bound). Quotients of 64 or more clamp to 15 either way.
+// quotient. Values whose approximate quotient lies within 2^-16 of one (twice the bound)
+// are divided exactly, one by one: bf16 inputs over a scale derived from bf16 extremes
+// make exact half-integer quotients common (about 0.3% of values, 2% of words on
+// N(0, 0.02) weights), so the exact path is kept per value. Quotients of 64 or more clamp
+// to 15 either way.
+__device__ __forceinline__ uint32_t pack_codes(const float (&c)[8]) {
+    // Codes 0, 2, 4, 6 as the bytes of one word and 1, 3, 5, 7 of another (v_cvt_pk_u8_f32,
+    // exact for the integral 0..15), then the odd ones shifted into the high nibbles.
+    const uint32_t lo01 = __builtin_amdgcn_cvt_pk_u8_f32(c[2], 1u, __builtin_amdgcn_cvt_pk_u8_f32(c[0], 0u, 0u));
+    const uint32_t lo23 = __builtin_amdgcn_cvt_pk_u8_f32(c[6], 3u, __builtin_amdgcn_cvt_pk_u8_f32(c[4], 2u, 0u));
+    const uint32_t hi01 = __builtin_amdgcn_cvt_pk_u8_f32(c[3], 1u, __builtin_amdgcn_cvt_pk_u8_f32(c[1], 0u, 0u));
+    const uint32_t hi23 = __builtin_amdgcn_cvt_pk_u8_f32(c[7], 3u, __builtin_amdgcn_cvt_pk_u8_f32(c[5], 2u, 0u));
+    return (lo01 | lo23) | ((hi01 | hi23) << 4);
+}
+
 __device__ __forceinline__ uint32_t quant_word(const float (&v)[8], float bias, float scale, float rcp) {
-    float q[8];
-    bool near_tie = false;
+    constexpr float kNearTie = 0.5f - 1.52587890625e-05f;   // 2^-16 from a half-integer
+    float c[8];
+    float d[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        q[e] = (v[e] - bias) * rcp;
-        const float r = rintf(q[e]);
-        near_tie |= fabsf(q[e] - r) > 0.5f - 1.52587890625e-05f;   // 2^-16
+        const float q = (v[e] - bias) * rcp;
+        const float r = rintf(q);
+        d[e] = fabsf(q - r);
+        c[e] = fminf(fmaxf(r, 0.0f), 15.0f);   // NaN (never produced for finite input) -> 0
     }
-    if (near_tie) {
+    const float dev = fmaxf(fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3])), fmaxf(fmaxf(d[4], d[5]), fmaxf(d[6], d[7])));
+    if (dev > kNearTie) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) q[e] = __fdiv_rn(v[e] - bias, scale);
+        for (int e = 0; e < 8; ++e) {
+            if (d[e] > kNearTie) c[e] = fminf(fmaxf(rintf(__fdiv_rn(v[e] - bias, scale)), 0.0f), 15.0f);
+        }
     }
-    uint32_t packed = 0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float c = fminf(fmaxf(rintf(q[e]), 0.0f), 15.0f);   // NaN (never produced for finite input) -> 0
-        packed |= static_cast<uint32_t>(c) << (4 * e);
-    }
-    return packed;
+    return pack_codes(c);
 }
 
 // One thread per group of 64: it reads the group's 128 contiguous bytes, finds the

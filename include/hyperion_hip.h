@@ -239,7 +239,8 @@ HypStatus hyp_qmlp_gate_up_gelu(HypQWeight gate, HypQWeight up, const void* x, u
 /* ---- quantize / dequantize ----------------------------------------------------- */
 
 /* mx.quantize(w, group_size=64, bits=4, mode="affine") of a bf16 [n, k] device matrix
- * into w_out uint32 [n, k/8], scales_out/biases_out bf16 [n, k/64] (device). */
+ * into w_out uint32 [n, k/8], scales_out/biases_out bf16 [n, k/64] (device). w and w_out
+ * must be 16-byte aligned (INVALID_ARGUMENT otherwise; device allocations are). */
 HypStatus hyp_quantize_q4g64(const void* w, uint32_t n, uint32_t k, uint32_t* w_out,
                              void* scales_out, void* biases_out, HypStream stream);
 

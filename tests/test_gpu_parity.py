@@ -10,6 +10,7 @@ Bars (stated per test):
     kernel's own matmul outputs, allowing a 1-ulp difference on at most 0.1% of
     elements where device tanhf and glibc tanhf round differently.
 """
+import ctypes
 import sys
 
 import numpy as np
@@ -140,6 +141,31 @@ def test_quantize_edge_groups(stream):
     ref = O.quantize(w)
     for gv, rv, name in zip(got, ref, ("packed", "scales", "biases")):
         assert np.array_equal(gv, rv), name
+
+
+@pytest.mark.parametrize("n,k", [(1, 64), (3, 640), (7, 64 * 37), (5, 64 * 52), (257, 128)])
+def test_quantize_ragged_group_counts(stream, n, k):
+    """Group counts that leave a wave (64 groups) or a workgroup (256) partly empty."""
+    say(f"quantize ragged n={n} k={k}")
+    w = syn.quantize_input(n, k, seed=n * 1000 + k)
+    got = _gpu_quantize(w, stream)
+    for gv, rv, name in zip(got, O.quantize(w), ("packed", "scales", "biases")):
+        np.testing.assert_array_equal(gv, rv, err_msg=name)
+
+
+def test_quantize_rejects_misaligned_buffers(stream):
+    n, k = 2, 128
+    wd = dev(syn.quantize_input(n, k, seed=3), stream)
+    wq = hy.DeviceArray((n, k // 8 + 4), np.uint32)
+    sd = hy.DeviceArray((n, k // 64 + 1), np.uint16)
+    bd = hy.DeviceArray((n, k // 64 + 1), np.uint16)
+    shifted = lambda a, by: ctypes.c_void_p(a.ptr.value + by)  # noqa: E731
+    for args in ((shifted(wd, 2), wq.ptr), (wd.ptr, shifted(wq, 4))):
+        with pytest.raises(hy.HypError) as e:
+            hy.call("hyp_quantize_q4g64", args[0], n, k, args[1], sd.ptr, bd.ptr, stream.handle)
+        assert e.value.status_name == "INVALID_ARGUMENT" and "aligned" in str(e.value)
+    for a in (wd, wq, sd, bd):
+        a.close()
 
 
 def test_dequantize_table_bit_exact(stream):
