@@ -69,7 +69,8 @@ bool skinny_norm_supported(uint32_t m, uint32_t k);
 void launch_q4_gemm(const Q4Matrix& w, const uint16_t* x, uint32_t m, uint16_t* y, hipStream_t stream);
 // y = bf16(gelu_chain(x . G^T) * (x . U^T)) as one dual GEMM: each wave accumulates a gate
 // tile and the same up tile, the epilogue applies the gating. Same kernel, split and sums
-// as the grouped GEMM of [gate, up], so y is gelu_mul of that launch's outputs bit for bit.
+// as the grouped GEMM of [gate, up], so y is the GELU chain over that launch's outputs bit
+// for bit.
 void launch_q4_gemm_gate_up(const Q4Matrix& gate, const Q4Matrix& up, const uint16_t* x, uint32_t m, uint16_t* y,
                             hipStream_t stream);
 // launch_q4_gemm with the split-k partials in a fixed device scratch array instead of a
@@ -80,8 +81,6 @@ void launch_q4_gemm_noalloc(const Q4Matrix& w, const uint16_t* x, uint32_t m, ui
 // ys[i][m, n_i] = x . dequant(W_i)^T.
 void launch_q4_gemm_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
                           uint32_t m, hipStream_t stream);
-// h = bf16(gelu_chain(h) * u) over `count` bf16 elements (in place on h).
-void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t stream);
 // y = softcap(y) over `count` bf16 elements (in place).
 void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream);
 // y[r] = bf16(w * bf16(x[r] / sqrt(mean(x[r]^2) + eps))) for each of m rows of k bf16,

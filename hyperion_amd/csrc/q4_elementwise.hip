@@ -1,6 +1,5 @@
-// Elementwise bf16 epilogues for the prefill path (m > 4), where the GEMM writes plain
-// bf16 outputs and these kernels finish them:
-//   gelu_mul: h = bf16(gelu_chain(h) * u)      ForwardPass::mlp, forward.cc:338-343
+// Elementwise bf16 epilogue for the prefill path (m > 4), where the GEMM writes plain
+// bf16 outputs and this kernel finishes them:
 //   softcap:  y = bf16(tanh(y / cap) * cap)     ForwardPass::softcap, forward.cc:154-160
 // and the row RMS norm (mx::fast::rms_norm with or without its learned weight):
 //   rms_normalize: y[r] = bf16(w * bf16(x[r] / sqrt(mean(x[r]^2) + eps))), fp32 statistics
@@ -16,33 +15,6 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
-}
-
-__device__ __forceinline__ float gelu_mul1(float h, float u) { return gelu_tanh_bf16_chain(h) * u; }
-
-// Thread t owns elements [8t, 8t + 8); a full octet moves as 16-byte vectors, the
-// ragged tail element by element.
-__global__ __launch_bounds__(kThreads) void gelu_mul_kernel(uint16_t* __restrict__ h, const uint16_t* __restrict__ u,
-                                                            uint64_t count) {
-    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const uint64_t e0 = t * 8u;
-    if (e0 >= count) return;
-    if (e0 + 8u <= count) {
-        uint4 hv = reinterpret_cast<const uint4*>(h)[t];
-        const uint4 uv = reinterpret_cast<const uint4*>(u)[t];
-        uint32_t* hw = reinterpret_cast<uint32_t*>(&hv);
-        const uint32_t* uw = reinterpret_cast<const uint32_t*>(&uv);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            hw[i] = pack2(gelu_mul1(bf16_bits_to_f32(hw[i] & 0xFFFFu), bf16_bits_to_f32(uw[i] & 0xFFFFu)),
-                          gelu_mul1(bf16_bits_to_f32(hw[i] >> 16), bf16_bits_to_f32(uw[i] >> 16)));
-        }
-        reinterpret_cast<uint4*>(h)[t] = hv;
-    } else {
-        for (uint64_t e = e0; e < count; ++e) {
-            h[e] = f32_to_bf16_bits(gelu_mul1(bf16_bits_to_f32(h[e]), bf16_bits_to_f32(u[e])));
-        }
-    }
 }
 
 __global__ __launch_bounds__(kThreads) void softcap_kernel(uint16_t* __restrict__ y, float cap, uint64_t count) {
@@ -99,12 +71,6 @@ dim3 grid_for(uint64_t count) {
 }
 
 }  // namespace
-
-void launch_gelu_mul(uint16_t* h, const uint16_t* u, uint64_t count, hipStream_t stream) {
-    if (count == 0) return;
-    hipLaunchKernelGGL(gelu_mul_kernel, grid_for(count), dim3(kThreads), 0, stream, h, u, count);
-    HYP_HIP_CHECK(hipGetLastError());
-}
 
 void launch_softcap(uint16_t* y, float cap_bf16, uint64_t count, hipStream_t stream) {
     if (count == 0) return;

@@ -190,7 +190,8 @@ __device__ __forceinline__ void mfma_step(const uint8_t* xb, uint32_t lane, cons
 
 // The fused MLP gating of one output (forward.cc:338-343 without the down projection):
 // the gate and up sums rounded to bf16 as a separate launch stores them, then
-// bf16(gelu_chain(gate) * up), bit for bit the elementwise gelu_mul pass over them.
+// bf16(gelu_chain(gate) * up) (the split-k reduce's form; the GEMM epilogues use the
+// tabulated gated_bits_table, which gives the same bits).
 __device__ __forceinline__ uint16_t gated_bits(float gate_sum, float up_sum) {
     const float g = bf16_bits_to_f32(f32_to_bf16_bits(gate_sum));
     const float u = bf16_bits_to_f32(f32_to_bf16_bits(up_sum));
