@@ -48,6 +48,7 @@ EXPORTED = [
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
     "hyp_rope", "hyp_sample_greedy", "hyp_sample_greedy_topk",
+    "hyp_kv_cache_create", "hyp_kv_cache_free", "hyp_kv_cache_buffers", "hyp_kv_cache_write", "hyp_attention",
     "hyp_step_program_create", "hyp_step_program_run", "hyp_step_program_check", "hyp_step_program_free",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
@@ -172,6 +173,11 @@ def lib() -> ctypes.CDLL:
         "hyp_rope": [_P, _U32, _U32, _U32, _U32, ctypes.c_float, _U32, _P, _P],
         "hyp_sample_greedy": [_P, _U32, _U32, _P, _P],
         "hyp_sample_greedy_topk": [_P, _U32, _U32, _P, _P],
+        "hyp_kv_cache_create": [_U32, _U32, _U32, _PP],
+        "hyp_kv_cache_free": [_PP],
+        "hyp_kv_cache_buffers": [_P, _PP, _PP],
+        "hyp_kv_cache_write": [_P, _P, _P, _U32, _U32, _P],
+        "hyp_attention": [_P, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P],
         "hyp_step_program_create": [_P, _U32, _U32, _U32, _PP],
         "hyp_step_program_run": [_P, _P],
         "hyp_step_program_check": [_P],
@@ -540,6 +546,43 @@ def sample_greedy(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, 
     out is a device array of at least rows * 12 bytes."""
     ptr = ctypes.c_void_p((logits.ptr.value or 0) + 2 * row_offset * vocab) if row_offset else logits.ptr
     call("hyp_sample_greedy", ptr, rows, vocab, out.ptr, stream.handle)
+
+
+class KvCache:
+    """HypKvCache: one layer's K/V cache [capacity, n_kv_heads, head_dim] bf16 on the device
+    (slot = position % capacity)."""
+
+    def __init__(self, capacity: int, n_kv_heads: int, head_dim: int):
+        self.capacity, self.n_kv_heads, self.head_dim = capacity, n_kv_heads, head_dim
+        self.handle = ctypes.c_void_p()
+        call("hyp_kv_cache_create", capacity, n_kv_heads, head_dim, ctypes.byref(self.handle))
+
+    def buffers(self):
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        call("hyp_kv_cache_buffers", self.handle, ctypes.byref(k), ctypes.byref(v))
+        return k, v
+
+    def write(self, k: "DeviceArray", v: "DeviceArray", n: int, pos0: int, stream: "Stream") -> None:
+        call("hyp_kv_cache_write", self.handle, k.ptr, v.ptr, n, pos0, stream.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            call("hyp_kv_cache_free", ctypes.byref(self.handle))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def attention(q: "DeviceArray", k: "DeviceArray", v: "DeviceArray", L: int, n_heads: int, cache: KvCache,
+              offset: int, prefix_len: int, window: int, out: "DeviceArray", stream: "Stream") -> None:
+    """hyp_attention: scale-1 SDPA of q [L, n_heads, d] over the cache's positions
+    [offset - prefix_len, offset) and the chunk k/v [L, n_kv, d]; causal, sliding when
+    window > 0."""
+    call("hyp_attention", q.ptr, k.ptr, v.ptr, L, n_heads, cache.handle, offset, prefix_len, window, out.ptr,
+         stream.handle)
 
 
 def sample_greedy_topk(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, stream: Stream,

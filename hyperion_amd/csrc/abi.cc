@@ -18,6 +18,7 @@
 
 using hyperion::hip::Epilogue;
 using hyperion::hip::NativeError;
+using hyperion::model::DeviceBuffer;
 using hyperion::model::ModelWeights;
 using hyperion::model::QuantizedLinear;
 
@@ -29,6 +30,7 @@ constexpr std::uint32_t kStreamMagic = 0x48505354U;    // "HPST"
 constexpr std::uint32_t kEventMagic = 0x48504556U;     // "HPEV"
 constexpr std::uint32_t kGraphMagic = 0x48504752U;     // "HPGR"
 constexpr std::uint32_t kStepProgramMagic = 0x48505350U;   // "HPSP"
+constexpr std::uint32_t kKvCacheMagic = 0x48504B56U;       // "HPKV"
 
 constexpr std::size_t kLastErrorCapacity = 1024;
 thread_local std::array<char, kLastErrorCapacity> g_last_error{};
@@ -120,6 +122,16 @@ struct HypEventOpaque {
 struct HypStepProgramOpaque {
     std::uint32_t magic = 0;
     std::unique_ptr<hyperion::model::StepProgram> program;
+};
+
+struct HypKvCacheOpaque {
+    std::uint32_t magic = 0;
+    uint32_t capacity = 0;
+    uint32_t num_kv_heads = 0;
+    uint32_t head_dim = 0;
+    DeviceBuffer k;
+    DeviceBuffer v;
+    DeviceBuffer workspace;   // decode attention's split partials
 };
 
 struct HypGraphOpaque {
@@ -651,6 +663,102 @@ HypStatus hyp_sample_greedy_topk(const void* logits, uint32_t rows, uint32_t voc
         REQUIRE_ARG(static_cast<uint64_t>(rows) * vocab < (1ull << 62), "logits too large");
         hyperion::hip::launch_sample_topk(static_cast<const uint16_t*>(logits), rows, vocab, out, stream->workspace,
                                           stream->workspace_bytes, s);
+    });
+}
+
+HypStatus hyp_kv_cache_create(uint32_t capacity, uint32_t num_kv_heads, uint32_t head_dim, HypKvCache* out_cache) {
+    return abi_call("hyp_kv_cache_create", [&] {
+        REQUIRE_ARG(out_cache != nullptr, "create requires a non-null out handle");
+        REQUIRE_ARG(capacity > 0 && num_kv_heads > 0, "capacity and num_kv_heads must be positive");
+        REQUIRE_ARG(head_dim == 64u || head_dim == 128u || head_dim == 256u || head_dim == 512u,
+                    "head_dim must be 64, 128, 256 or 512");
+        REQUIRE_ARG(capacity < (1u << 30), "capacity must be below 2^30 tokens");
+        const uint64_t bytes = static_cast<uint64_t>(capacity) * num_kv_heads * head_dim * 2u;
+        REQUIRE_ARG(bytes < (1ull << 40), "cache too large");
+        require_device();
+        auto c = std::make_unique<HypKvCacheOpaque>();
+        c->capacity = capacity;
+        c->num_kv_heads = num_kv_heads;
+        c->head_dim = head_dim;
+        c->k = DeviceBuffer(bytes);
+        c->v = DeviceBuffer(bytes);
+        c->workspace = DeviceBuffer(hyperion::hip::attention_workspace_bytes(num_kv_heads, head_dim));
+        c->magic = kKvCacheMagic;
+        *out_cache = c.release();
+    });
+}
+
+HypStatus hyp_kv_cache_free(HypKvCache* cache) {
+    return free_handle(cache, kKvCacheMagic);
+}
+
+namespace {
+HypKvCacheOpaque& kv_ref(HypKvCache c) {
+    REQUIRE_ARG(c != nullptr, "kv cache handle is null");
+    REQUIRE_ARG(c->magic == kKvCacheMagic, "kv cache handle magic mismatch (wrong type, freed, or corrupted)");
+    return *c;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0u; }
+}  // namespace
+
+HypStatus hyp_kv_cache_buffers(HypKvCache cache, void** out_k, void** out_v) {
+    return abi_call("hyp_kv_cache_buffers", [&] {
+        HypKvCacheOpaque& c = kv_ref(cache);
+        REQUIRE_ARG(out_k != nullptr && out_v != nullptr, "out pointers must be non-null");
+        *out_k = c.k.data();
+        *out_v = c.v.data();
+    });
+}
+
+HypStatus hyp_kv_cache_write(HypKvCache cache, const void* k, const void* v, uint32_t n_tokens, uint32_t pos0,
+                             HypStream stream) {
+    return abi_call("hyp_kv_cache_write", [&] {
+        hipStream_t s = stream_of(stream);
+        HypKvCacheOpaque& c = kv_ref(cache);
+        if (n_tokens == 0) return;
+        REQUIRE_ARG(k != nullptr && v != nullptr, "k and v must be non-null device pointers");
+        REQUIRE_ARG(aligned16(k) && aligned16(v), "k and v must be 16-byte aligned");
+        REQUIRE_ARG(static_cast<uint64_t>(pos0) + n_tokens < (1ull << 31), "positions must stay below 2^31");
+        hyperion::hip::launch_kv_write(static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                                       static_cast<uint16_t*>(c.k.data()), static_cast<uint16_t*>(c.v.data()), n_tokens,
+                                       pos0, c.capacity, c.num_kv_heads, c.head_dim, s);
+    });
+}
+
+HypStatus hyp_attention(const void* q, const void* k, const void* v, uint32_t L, uint32_t n_heads, HypKvCache cache,
+                        uint32_t offset, uint32_t prefix_len, uint32_t window, void* out, HypStream stream) {
+    return abi_call("hyp_attention", [&] {
+        hipStream_t s = stream_of(stream);
+        HypKvCacheOpaque& c = kv_ref(cache);
+        if (L == 0) return;
+        REQUIRE_ARG(q != nullptr && k != nullptr && v != nullptr && out != nullptr,
+                    "q, k, v and out must be non-null device pointers");
+        REQUIRE_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
+                    "q, k, v and out must be 16-byte aligned");
+        REQUIRE_ARG(n_heads > 0 && n_heads % c.num_kv_heads == 0, "n_heads must be a multiple of the cache's num_kv_heads");
+        REQUIRE_ARG(prefix_len <= offset, "prefix_len must not exceed offset");
+        REQUIRE_ARG(prefix_len <= c.capacity, "prefix_len must not exceed the cache capacity");
+        REQUIRE_ARG(static_cast<uint64_t>(offset) + L < (1ull << 31), "positions must stay below 2^31");
+        REQUIRE_ARG(static_cast<uint64_t>(L) * n_heads * c.head_dim < (1ull << 31), "q too large");
+        hyperion::hip::AttnArgs a{};
+        a.q = static_cast<const uint16_t*>(q);
+        a.k = static_cast<const uint16_t*>(k);
+        a.v = static_cast<const uint16_t*>(v);
+        a.cache_k = static_cast<const uint16_t*>(c.k.data());
+        a.cache_v = static_cast<const uint16_t*>(c.v.data());
+        a.out = static_cast<uint16_t*>(out);
+        a.L = L;
+        a.n_heads = n_heads;
+        a.n_kv_heads = c.num_kv_heads;
+        a.head_dim = c.head_dim;
+        a.cap = c.capacity;
+        a.offset = offset;
+        a.prefix_len = prefix_len;
+        a.window = window;
+        a.workspace = c.workspace.data();
+        a.workspace_bytes = c.workspace.bytes();
+        hyperion::hip::launch_attention(a, s);
     });
 }
 

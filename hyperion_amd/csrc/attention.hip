@@ -1,0 +1,376 @@
+// Attention of the Gemma-4 decoder layer on gfx950: ForwardPass::attention's
+// mx::fast::scaled_dot_product_attention (native/hyperion_mlx/src/forward.cc:376-508) over a
+// KV cache prefix and the current chunk, and the cache writes (LocalKvCache /
+// GlobalKvCache::append, kv_cache.h:33,143).
+//
+// Semantics (the reference's): scale 1.0 (Gemma 4 drops 1/sqrt(d)); query token t of the
+// chunk sits at position offset + t and sees key position p when p <= offset + t and, for
+// a sliding layer, p > offset + t - window (build_mask, forward.cc:345-373); query head h
+// reads kv head h / (H / KVH). Keys are the cache's positions [offset - prefix, offset)
+// (slot p % capacity) followed by the chunk's L positions.
+//
+// One kernel serves prefill and decode, flash-attention style on v_mfma_f32_16x16x32_bf16:
+//  * A workgroup (4 waves) takes a tile of 64 query rows of one kv head - row r is token
+//    r / G, head-in-group r % G (G = H / KVH) - and walks its visible keys in blocks of 32.
+//    A block's K rows and V (transposed, [d][32]) go through LDS; each wave computes its 16
+//    rows' scores S = Q K^T (Q rows read from LDS), masks them, and updates the online
+//    softmax in fp32: m = running row maximum (log2 domain), l = running sum, O = O * 2^(m_old
+//    - m) + P V, with P rounded to bf16 for the PV MFMAs (written to LDS and read back in the
+//    A-operand layout).
+//  * Decode (one row tile per kv head) splits the keys over several workgroups; each writes
+//    its unnormalised O with m and l to a workspace, and attn_combine_kernel merges them.
+//  * LDS rows are padded by 16 bytes so the 16 rows (or keys, or dims) an operand read
+//    touches start on different banks.
+#include <algorithm>
+#include <string>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace hyperion::hip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kAttnThreads = 256;
+constexpr uint32_t kRowsPerTile = 64;   // 4 waves x 16 rows
+constexpr uint32_t kKeyBlock = 32;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnParams {
+    const uint16_t* q;      // [L][H][D]
+    const uint16_t* k;      // [L][KVH][D]: the chunk
+    const uint16_t* v;
+    const uint16_t* ck;     // [cap][KVH][D]: the cache
+    const uint16_t* cv;
+    uint16_t* out;          // [L][H][D]
+    float* part_o;          // split partials: [splits][L * H][D]
+    float* part_ml;         // [splits][L * H][2]
+    uint32_t L, H, KVH, G, cap, offset, prefix, window;
+    uint32_t splits, keys_per_split;
+};
+
+template <uint32_t D>
+struct AttnLds {
+    static constexpr uint32_t kRow = D * 2u + 16u;           // Q and K rows (bytes)
+    static constexpr uint32_t kVtRow = kKeyBlock * 2u + 16u;  // V^T rows
+    static constexpr uint32_t kPRow = kKeyBlock * 2u + 16u;   // P rows
+    static constexpr uint32_t kQ = 0;
+    static constexpr uint32_t kK = kQ + kRowsPerTile * kRow;
+    static constexpr uint32_t kVt = kK + kKeyBlock * kRow;
+    static constexpr uint32_t kP = kVt + D * kVtRow;
+    static constexpr uint32_t kBytes = kP + (kAttnThreads / 64u) * 16u * kPRow;
+};
+
+__device__ __forceinline__ const uint16_t* key_row(const AttnParams& p, const uint16_t* chunk, const uint16_t* cache,
+                                                   uint32_t j, uint32_t hk, uint32_t D) {
+    // Key index j (0 .. prefix + L) -> its row: the cache for the prefix, the chunk after.
+    if (j < p.prefix) {
+        const uint32_t pos = p.offset - p.prefix + j;
+        return cache + (static_cast<size_t>(pos % p.cap) * p.KVH + hk) * D;
+    }
+    return chunk + (static_cast<size_t>(j - p.prefix) * p.KVH + hk) * D;
+}
+
+template <uint32_t D>
+__global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
+    using Lds = AttnLds<D>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    const uint32_t j16 = lane & 15u;
+    const uint32_t kb = lane >> 4;
+    const uint32_t hk = blockIdx.y;
+    const uint32_t split = blockIdx.z;
+    const uint32_t rows = p.L * p.G;                     // query rows of this kv head
+    const uint32_t row0 = blockIdx.x * kRowsPerTile;     // first row of the tile
+    const uint32_t T = p.prefix + p.L;
+
+    // The tile's token range and the keys any of its rows can see, within this split.
+    const uint32_t t_lo = row0 / p.G;
+    const uint32_t t_hi = (min(row0 + kRowsPerTile, rows) - 1u) / p.G;
+    uint32_t j_begin = split * p.keys_per_split;
+    uint32_t j_end = min(j_begin + p.keys_per_split, T);
+    j_end = min(j_end, p.prefix + t_hi + 1u);                 // causal: keys up to the last query
+    if (p.window != 0u) {
+        // keys at positions > offset + t_lo - window, i.e. j > prefix + t_lo - window
+        const int64_t lo = static_cast<int64_t>(p.prefix) + t_lo - p.window + 1;
+        if (lo > static_cast<int64_t>(j_begin)) j_begin = static_cast<uint32_t>(lo);
+    }
+
+    // Q tile -> LDS: thread t copies 16-byte chunks (row = c / (D/8), chunk c % (D/8)).
+    constexpr uint32_t kChunks = D / 8u;
+    for (uint32_t c = tid; c < kRowsPerTile * kChunks; c += kAttnThreads) {
+        const uint32_t r = c / kChunks;
+        const uint32_t ch = c - r * kChunks;
+        const uint32_t gr = row0 + r;
+        uint4 val = make_uint4(0u, 0u, 0u, 0u);
+        if (gr < rows) {
+            const uint32_t t = gr / p.G;
+            const uint32_t h = hk * p.G + (gr - t * p.G);
+            val = *reinterpret_cast<const uint4*>(p.q + (static_cast<size_t>(t) * p.H + h) * D + ch * 8u);
+        }
+        *reinterpret_cast<uint4*>(lds + Lds::kQ + r * Lds::kRow + ch * 16u) = val;
+    }
+
+    // Per lane: rows 4 kb + i (i < 4) of the wave's 16; O tiles of 16 dims.
+    constexpr uint32_t kDTiles = D / 16u;
+    f32x4_t o[kDTiles];
+#pragma unroll
+    for (uint32_t t = 0; t < kDTiles; ++t) o[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[4], l[4];
+    int32_t qpos[4];   // -1: a padding row (never visible)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        m[i] = -__builtin_huge_valf();
+        l[i] = 0.0f;
+        const uint32_t gr = row0 + wave * 16u + 4u * kb + i;
+        qpos[i] = gr < rows ? static_cast<int32_t>(p.offset + gr / p.G) : -1;
+    }
+    const uint8_t* qrow = lds + Lds::kQ + (wave * 16u + j16) * Lds::kRow;   // A operand row (i = j16)
+    uint8_t* prow_w = lds + Lds::kP + wave * 16u * Lds::kPRow;             // this wave's P [16][32]
+
+    for (uint32_t jb = j_begin; jb < j_end; jb += kKeyBlock) {
+        const uint32_t nk = min(kKeyBlock, j_end - jb);
+        __syncthreads();   // the previous block's K/V reads are done (and Q is staged)
+        // K rows -> LDS, V rows -> LDS transposed.
+        for (uint32_t c = tid; c < kKeyBlock * kChunks; c += kAttnThreads) {
+            const uint32_t r = c / kChunks;
+            const uint32_t ch = c - r * kChunks;
+            uint4 kv = make_uint4(0u, 0u, 0u, 0u);
+            uint4 vv = make_uint4(0u, 0u, 0u, 0u);
+            if (r < nk) {
+                kv = *reinterpret_cast<const uint4*>(key_row(p, p.k, p.ck, jb + r, hk, D) + ch * 8u);
+                vv = *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u);
+            }
+            *reinterpret_cast<uint4*>(lds + Lds::kK + r * Lds::kRow + ch * 16u) = kv;
+            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (uint32_t e = 0; e < 4; ++e) {
+                const uint32_t d0 = ch * 8u + 2u * e;
+                *reinterpret_cast<uint16_t*>(lds + Lds::kVt + d0 * Lds::kVtRow + r * 2u) = static_cast<uint16_t>(w[e]);
+                *reinterpret_cast<uint16_t*>(lds + Lds::kVt + (d0 + 1u) * Lds::kVtRow + r * 2u) =
+                    static_cast<uint16_t>(w[e] >> 16);
+            }
+        }
+        __syncthreads();
+
+        // S = Q K^T for the wave's 16 rows x 32 keys (two column tiles of 16 keys).
+        f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll 4
+        for (uint32_t st = 0; st < D / 32u; ++st) {
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(qrow + (st * 32u + kb * 8u) * 2u);
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c) {
+                const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(lds + Lds::kK + (16u * c + j16) * Lds::kRow +
+                                                                      (st * 32u + kb * 8u) * 2u);
+                s[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, s[c], 0, 0, 0);
+            }
+        }
+
+        // Mask, online softmax (log2 domain), P -> LDS as bf16.
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            float sv[2];
+            float bmax = -__builtin_huge_valf();
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c) {
+                const uint32_t key = 16u * c + j16;
+                const int32_t kpos = static_cast<int32_t>(p.offset - p.prefix + jb + key);
+                const bool vis = key < nk && qpos[i] >= 0 && kpos <= qpos[i] &&
+                                 (p.window == 0u || kpos > qpos[i] - static_cast<int32_t>(p.window));
+                sv[c] = vis ? s[c][i] * kLog2e : -__builtin_huge_valf();
+                bmax = fmaxf(bmax, sv[c]);
+            }
+#pragma unroll
+            for (int mask = 1; mask <= 8; mask <<= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, mask, 64));
+            const float m_new = fmaxf(m[i], bmax);
+            const bool any = m_new > -__builtin_huge_valf();
+            const float alpha = any ? exp2f(m[i] - m_new) : 1.0f;   // m[i] = -inf -> 0
+            float psum = 0.0f;
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c) {
+                const float pv = any && sv[c] > -__builtin_huge_valf() ? exp2f(sv[c] - m_new) : 0.0f;
+                psum += pv;
+                *reinterpret_cast<uint16_t*>(prow_w + (4u * kb + i) * Lds::kPRow + (16u * c + j16) * 2u) =
+                    f32_to_bf16_bits(pv);
+            }
+#pragma unroll
+            for (int mask = 1; mask <= 8; mask <<= 1) psum += __shfl_xor(psum, mask, 64);
+            l[i] = l[i] * alpha + psum;
+            m[i] = any ? m_new : m[i];
+#pragma unroll
+            for (uint32_t t = 0; t < kDTiles; ++t) o[t][i] *= alpha;
+        }
+        // P (16 x 32 keys) as the A operand, V^T as B: O += P V.
+        const bf16x8_t pa = *reinterpret_cast<const bf16x8_t*>(prow_w + j16 * Lds::kPRow + kb * 16u);
+#pragma unroll
+        for (uint32_t t = 0; t < kDTiles; ++t) {
+            const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(lds + Lds::kVt + (16u * t + j16) * Lds::kVtRow + kb * 16u);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, o[t], 0, 0, 0);
+        }
+    }
+
+    // Rows 4 kb + i of the wave, dims 16 t + j16.
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t gr = row0 + wave * 16u + 4u * kb + i;
+        if (gr >= rows) continue;
+        const uint32_t t = gr / p.G;
+        const uint32_t h = hk * p.G + (gr - t * p.G);
+        const size_t orow = static_cast<size_t>(t) * p.H + h;   // [L][H] row of the output
+        if (p.splits == 1u) {
+            const float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+#pragma unroll
+            for (uint32_t tt = 0; tt < kDTiles; ++tt) p.out[orow * D + 16u * tt + j16] = f32_to_bf16_bits(o[tt][i] * inv);
+        } else {
+            const size_t prow = static_cast<size_t>(split) * p.L * p.H + orow;
+#pragma unroll
+            for (uint32_t tt = 0; tt < kDTiles; ++tt) p.part_o[prow * D + 16u * tt + j16] = o[tt][i];
+            if (j16 == 0u) {
+                p.part_ml[prow * 2u] = m[i];
+                p.part_ml[prow * 2u + 1u] = l[i];
+            }
+        }
+    }
+}
+
+// Merge the splits of each output row: weights 2^(m_s - max m), sum of l_s, divided sums.
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p, uint32_t D) {
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * kAttnThreads + threadIdx.x;
+    const uint64_t rows = static_cast<uint64_t>(p.L) * p.H;
+    if (e >= rows * D) return;
+    const uint64_t row = e / D;
+    float mx = -__builtin_huge_valf();
+    for (uint32_t s = 0; s < p.splits; ++s) mx = fmaxf(mx, p.part_ml[(s * rows + row) * 2u]);
+    float num = 0.0f;
+    float den = 0.0f;
+    if (mx > -__builtin_huge_valf()) {
+        for (uint32_t s = 0; s < p.splits; ++s) {
+            const float ms = p.part_ml[(s * rows + row) * 2u];
+            if (ms == -__builtin_huge_valf()) continue;
+            const float w = exp2f(ms - mx);
+            den += w * p.part_ml[(s * rows + row) * 2u + 1u];
+            num += w * p.part_o[s * rows * D + e];
+        }
+    }
+    p.out[e] = f32_to_bf16_bits(den > 0.0f ? num / den : 0.0f);
+}
+
+// Tokens pos0 .. pos0 + n - 1 of k/v [n][KVH][D] -> cache slots pos % cap (only the last
+// `cap` of them when n > cap: earlier ones would be overwritten in the same slots).
+__global__ __launch_bounds__(kAttnThreads) void kv_write_kernel(const uint16_t* __restrict__ k,
+                                                               const uint16_t* __restrict__ v, uint16_t* ck,
+                                                               uint16_t* cv, uint32_t n_skip, uint32_t n,
+                                                               uint32_t pos0, uint32_t cap, uint32_t row_elems) {
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * kAttnThreads + threadIdx.x;   // 16-byte chunk
+    const uint32_t per_tok = row_elems / 8u;
+    const uint64_t total = static_cast<uint64_t>(n - n_skip) * per_tok;
+    if (c >= total) return;
+    const uint32_t t = n_skip + static_cast<uint32_t>(c / per_tok);
+    const uint32_t ch = static_cast<uint32_t>(c % per_tok);
+    const uint32_t slot = (pos0 + t) % cap;
+    const size_t src = static_cast<size_t>(t) * row_elems + ch * 8u;
+    const size_t dst = static_cast<size_t>(slot) * row_elems + ch * 8u;
+    *reinterpret_cast<uint4*>(ck + dst) = *reinterpret_cast<const uint4*>(k + src);
+    *reinterpret_cast<uint4*>(cv + dst) = *reinterpret_cast<const uint4*>(v + src);
+}
+
+template <uint32_t D>
+void launch_attn_d(const AttnParams& p, hipStream_t stream) {
+    constexpr size_t lds = AttnLds<D>::kBytes;
+    static_assert(lds <= 160u * 1024u, "attention LDS");
+    if (lds > 65536u) {
+        static thread_local int configured_device = -1;
+        int dev = 0;
+        HYP_HIP_CHECK(hipGetDevice(&dev));
+        if (configured_device != dev) {
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel<D>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            configured_device = dev;
+        }
+    }
+    const uint32_t tiles = (p.L * p.G + kRowsPerTile - 1u) / kRowsPerTile;
+    hipLaunchKernelGGL(attn_kernel<D>, dim3(tiles, p.KVH, p.splits), dim3(kAttnThreads), lds, stream, p);
+    HYP_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim) {
+    // Split partials for decode: at most kAttnMaxSplits splits of one row tile per kv head.
+    const size_t rows = static_cast<size_t>(kRowsPerTile) * n_kv_heads;
+    return kAttnMaxSplits * rows * (static_cast<size_t>(head_dim) * 4u + 8u);
+}
+
+void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_t* cv, uint32_t n, uint32_t pos0,
+                     uint32_t cap, uint32_t n_kv_heads, uint32_t head_dim, hipStream_t stream) {
+    if (n == 0) return;
+    const uint32_t skip = n > cap ? n - cap : 0u;
+    const uint32_t row_elems = n_kv_heads * head_dim;
+    const uint64_t chunks = static_cast<uint64_t>(n - skip) * (row_elems / 8u);
+    const uint64_t blocks = (chunks + kAttnThreads - 1u) / kAttnThreads;
+    HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "kv write: too many tokens");
+    hipLaunchKernelGGL(kv_write_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kAttnThreads), 0, stream, k, v, ck,
+                       cv, skip, n, pos0, cap, row_elems);
+    HYP_HIP_CHECK(hipGetLastError());
+}
+
+uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys) {
+    // One row tile per kv head (decode): split the keys so the grid covers the compute
+    // units, at least 64 keys per split.
+    const uint32_t G = n_heads / n_kv_heads;
+    if (static_cast<uint64_t>(L) * G > kRowsPerTile) return 1u;
+    const uint32_t cus = device_compute_units();
+    uint32_t s = 1u;
+    while (s < kAttnMaxSplits && n_kv_heads * s * 2u <= cus && keys >= 64u * (s * 2u)) s *= 2u;
+    return s;
+}
+
+void launch_attention(const AttnArgs& a, hipStream_t stream) {
+    AttnParams p{};
+    p.q = a.q;
+    p.k = a.k;
+    p.v = a.v;
+    p.ck = a.cache_k;
+    p.cv = a.cache_v;
+    p.out = a.out;
+    p.L = a.L;
+    p.H = a.n_heads;
+    p.KVH = a.n_kv_heads;
+    p.G = a.n_heads / a.n_kv_heads;
+    p.cap = a.cap;
+    p.offset = a.offset;
+    p.prefix = a.prefix_len;
+    p.window = a.window;
+    const uint32_t T = a.prefix_len + a.L;
+    p.splits = attention_splits(a.L, a.n_heads, a.n_kv_heads, T);
+    p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
+    p.splits = std::max(1u, (T + p.keys_per_split - 1u) / p.keys_per_split);   // no empty split
+    if (p.splits > 1u) {
+        HYP_REQUIRE(a.workspace != nullptr &&
+                        a.workspace_bytes >= attention_workspace_bytes(a.n_kv_heads, a.head_dim),
+                    HYP_STATUS_INTERNAL, "attention: split workspace too small");
+        const size_t rows = static_cast<size_t>(a.L) * a.n_heads;
+        p.part_o = static_cast<float*>(a.workspace);
+        p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) +
+                                             static_cast<size_t>(p.splits) * rows * a.head_dim * 4u);
+    }
+    switch (a.head_dim) {
+        case 64: launch_attn_d<64>(p, stream); break;
+        case 128: launch_attn_d<128>(p, stream); break;
+        case 256: launch_attn_d<256>(p, stream); break;
+        case 512: launch_attn_d<512>(p, stream); break;
+        default: throw NativeError(HYP_STATUS_UNSUPPORTED, "attention: head_dim must be 64, 128, 256 or 512");
+    }
+    if (p.splits > 1u) {
+        const uint64_t elems = static_cast<uint64_t>(a.L) * a.n_heads * a.head_dim;
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<uint32_t>((elems + kAttnThreads - 1u) / kAttnThreads)),
+                           dim3(kAttnThreads), 0, stream, p, a.head_dim);
+        HYP_HIP_CHECK(hipGetLastError());
+    }
+}
+
+}  // namespace hyperion::hip

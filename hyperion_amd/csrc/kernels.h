@@ -107,6 +107,27 @@ uint32_t sample_topk_max_vocab();
 void launch_sample_topk(const uint16_t* logits, uint32_t rows, uint32_t vocab, HypTopKSample* out, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 
+// Attention (forward.cc:376-508) over a KV cache prefix and the current chunk; see
+// attention.hip. Decode splits the keys; the partial sums need attention_workspace_bytes.
+constexpr uint32_t kAttnMaxSplits = 32;
+struct AttnArgs {
+    const uint16_t* q;         // [L][n_heads][head_dim]
+    const uint16_t* k;         // [L][n_kv_heads][head_dim] (the chunk)
+    const uint16_t* v;
+    const uint16_t* cache_k;   // [cap][n_kv_heads][head_dim]
+    const uint16_t* cache_v;
+    uint16_t* out;             // [L][n_heads][head_dim]
+    uint32_t L, n_heads, n_kv_heads, head_dim, cap, offset, prefix_len, window;
+    void* workspace;
+    size_t workspace_bytes;
+};
+size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim);
+uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys);
+void launch_attention(const AttnArgs& a, hipStream_t stream);
+// Tokens pos0.. of k/v [n][n_kv_heads][head_dim] into cache slots (pos % cap).
+void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_t* cv, uint32_t n, uint32_t pos0,
+                     uint32_t cap, uint32_t n_kv_heads, uint32_t head_dim, hipStream_t stream);
+
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,
                         uint16_t* scales, uint16_t* biases, hipStream_t stream);

@@ -153,7 +153,8 @@ HypStatus hyp_event_elapsed_ms(HypEvent start, HypEvent end, float* out_ms);
  * per-launch host work; the reference has no counterpart (MLX evaluates its lazy graph
  * at mx::eval, forward.cc:171). Between begin and end, hyp_qmatmul, hyp_qmatmul_ex,
  * hyp_qmatmul_group, hyp_qmlp_gate_up_gelu and hyp_qmatmul_group_rmsnorm with m <= 4, hyp_rms_normalize, hyp_quantize_q4g64,
- * hyp_dequantize_q4g64, hyp_embed, hyp_sample_greedy, hyp_sample_greedy_topk and the copies on `stream` are
+ * hyp_dequantize_q4g64, hyp_embed, hyp_sample_greedy, hyp_sample_greedy_topk, hyp_kv_cache_write,
+ * hyp_attention, hyp_rope and the copies on `stream` are
  * recorded instead of run (they allocate nothing). Calls that may allocate or clear
  * memory - the matmul entries on their GEMM path (m > 4) and hyp_memset_device - check
  * the stream and return INVALID_ARGUMENT while it is capturing, before enqueueing
@@ -308,6 +309,39 @@ HypStatus hyp_sample_greedy(const void* logits, uint32_t rows, uint32_t vocab, H
  * hyp_sample_greedy. */
 HypStatus hyp_sample_greedy_topk(const void* logits, uint32_t rows, uint32_t vocab, HypTopKSample* out,
                                  HypStream stream);
+
+/* ---- attention and the KV caches (forward.cc:376-508, kv_cache.h:33,143) ------------- */
+
+/* One layer's KV cache on the device: K and V [capacity][num_kv_heads][head_dim] bf16, token
+ * position p in slot p % capacity. A sliding layer's ring (LocalKvCache) is a cache of at
+ * least its window; a global layer's cache (GlobalKvCache) is given the context length as
+ * capacity - the reference grows it in 256-token steps, which 288 GB of HBM does not need.
+ * The handle also owns the workspace of decode attention's split keys (fixed size), so
+ * attention on a capturing stream allocates nothing. head_dim: 64, 128, 256 or 512. */
+typedef struct HypKvCacheOpaque* HypKvCache;   /* magic "HPKV" */
+HypStatus hyp_kv_cache_create(uint32_t capacity, uint32_t num_kv_heads, uint32_t head_dim, HypKvCache* out_cache);
+HypStatus hyp_kv_cache_free(HypKvCache* cache);
+/* Device pointers of the cache's K and V tensors (valid until free). */
+HypStatus hyp_kv_cache_buffers(HypKvCache cache, void** out_k, void** out_v);
+/* Write n_tokens of k/v [n_tokens][num_kv_heads][head_dim] (device, bf16) at positions
+ * pos0 .. pos0 + n_tokens - 1 (LocalKvCache::append_committed, GlobalKvCache::append);
+ * when n_tokens > capacity only the last capacity tokens are written (the earlier ones would
+ * be overwritten in the ring). */
+HypStatus hyp_kv_cache_write(HypKvCache cache, const void* k, const void* v, uint32_t n_tokens, uint32_t pos0,
+                             HypStream stream);
+/* mx::fast::scaled_dot_product_attention as ForwardPass::attention calls it: scale 1.0,
+ * the boolean mask of build_mask (forward.cc:345-373: key position p visible to the query
+ * at position offset + t when p <= offset + t and, with window > 0, p > offset + t -
+ * window), grouped-query heads (query head h reads kv head h / (n_heads / num_kv_heads)).
+ * q [L][n_heads][head_dim], the chunk's k/v [L][num_kv_heads][head_dim] (post-norm, k
+ * post-rope), out [L][n_heads][head_dim], all device bf16, 16-byte aligned. The keys are
+ * the cache's positions [offset - prefix_len, offset) followed by the chunk's L positions
+ * [offset, offset + L): call it before hyp_kv_cache_write of the chunk, so a ring's prefix
+ * is read before the chunk overwrites its slots. prefix_len <= offset and <= capacity (a
+ * sliding layer passes min(window, offset), a global one offset). fp32 scores and softmax,
+ * P rounded to bf16 for the P.V products, output rounded to bf16. */
+HypStatus hyp_attention(const void* q, const void* k, const void* v, uint32_t L, uint32_t n_heads, HypKvCache cache,
+                        uint32_t offset, uint32_t prefix_len, uint32_t window, void* out, HypStream stream);
 
 /* ---- decode-step program (the per-token layer loop, forward.cc:558-563, run by
  *      hyp_decode_block, model.cc:703-718) ------------------------------------------ */

@@ -48,6 +48,7 @@ def lib():
         L.orc_scale_bf16.argtypes = [_P, _I, ctypes.c_float, _P]
         L.orc_rms_norm_bf16.argtypes = [_P, _P, _I, _I, ctypes.c_float, _P]
         L.orc_rope_bf16.argtypes = [_P, _I, _I, _I, _I, ctypes.c_double, _I, _P]
+        L.orc_attention_f64.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]
         _lib = L
     return _lib
 
@@ -241,4 +242,21 @@ def rope(x, rows: int, heads: int, head_dim: int, rotated: int, base: float, off
     x = _c(x, np.uint16).reshape(rows, heads, head_dim)
     out = np.empty_like(x)
     lib().orc_rope_bf16(_p(x), rows, heads, head_dim, rotated, ctypes.c_double(base), offset, _p(out))
+    return out
+
+
+def attention_f64(q, k, v, cache_k, cache_v, offset: int, prefix_len: int, window: int) -> np.ndarray:
+    """ForwardPass::attention's SDPA (scale 1, causal + sliding window, GQA) in fp64:
+    q [L, H, D], k/v [L, KVH, D] (the chunk), cache_k/cache_v [cap, KVH, D] (slot = pos % cap,
+    positions [offset - prefix_len, offset) read) -> [L, H, D] float64."""
+    q = _c(q, np.uint16)
+    k = _c(k, np.uint16)
+    v = _c(v, np.uint16)
+    ck = _c(cache_k, np.uint16)
+    cv = _c(cache_v, np.uint16)
+    L, H, D = q.shape
+    KVH = k.shape[1]
+    cap = ck.shape[0]
+    out = np.zeros((L, H, D), np.float64)
+    lib().orc_attention_f64(_p(q), _p(k), _p(v), _p(ck), _p(cv), cap, L, H, KVH, D, offset, prefix_len, window, _p(out))
     return out

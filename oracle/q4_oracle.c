@@ -480,3 +480,63 @@ void orc_rope_bf16(const uint16_t* x, int64_t rows, int64_t heads, int64_t head_
         }
     }
 }
+
+/*
+ * mx::fast::scaled_dot_product_attention as ForwardPass::attention calls it
+ * (native/hyperion_mlx/src/forward.cc:376-508): scale 1.0 (Gemma 4 drops 1/sqrt(d)), a
+ * boolean mask from absolute positions (build_mask, forward.cc:345-373: key k is visible to
+ * query q when k <= q, and for a sliding layer also k > q - window), grouped-query heads
+ * (query head h reads kv head h / (n_heads / n_kv_heads)). In fp64 on the bf16 inputs.
+ * Keys are the cache's prefix positions [offset - prefix_len, offset) (slot = pos % cap)
+ * followed by the chunk's L positions [offset, offset + L). q [L][n_heads][d], k and v
+ * [L][n_kv][d], cache_k and cache_v [cap][n_kv][d]; out [L][n_heads][d].
+ */
+void orc_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* cache_k,
+                       const uint16_t* cache_v, int64_t cap, int64_t L, int64_t n_heads, int64_t n_kv,
+                       int64_t d, int64_t offset, int64_t prefix_len, int64_t window, double* out) {
+    const int64_t group = n_heads / n_kv;
+    const int64_t T = prefix_len + L;
+#pragma omp parallel
+    {
+        double* s = (double*)malloc((size_t)(T > 0 ? T : 1) * sizeof(double));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t th = 0; th < L * n_heads; ++th) {
+            const int64_t t = th / n_heads;
+            const int64_t h = th - t * n_heads;
+            const int64_t qpos = offset + t;
+            const int64_t hk = h / group;
+            const uint16_t* qv = q + (t * n_heads + h) * d;
+            double m = -INFINITY;
+            for (int64_t j = 0; j < T; ++j) {
+                const int64_t kpos = offset - prefix_len + j;
+                const int visible = kpos <= qpos && (window == 0 || kpos > qpos - window);
+                if (!visible) {
+                    s[j] = -INFINITY;
+                    continue;
+                }
+                const uint16_t* kv = j < prefix_len ? cache_k + ((kpos % cap) * n_kv + hk) * d
+                                                    : k + ((kpos - offset) * n_kv + hk) * d;
+                double acc = 0.0;
+                for (int64_t e = 0; e < d; ++e) acc += (double)orc_f32_from_bf16(qv[e]) * (double)orc_f32_from_bf16(kv[e]);
+                s[j] = acc;
+                if (acc > m) m = acc;
+            }
+            double sum = 0.0;
+            for (int64_t j = 0; j < T; ++j) {
+                s[j] = s[j] == -INFINITY ? 0.0 : exp(s[j] - m);
+                sum += s[j];
+            }
+            double* o = out + (t * n_heads + h) * d;
+            for (int64_t e = 0; e < d; ++e) o[e] = 0.0;
+            for (int64_t j = 0; j < T; ++j) {
+                if (s[j] == 0.0) continue;
+                const int64_t kpos = offset - prefix_len + j;
+                const uint16_t* vv = j < prefix_len ? cache_v + ((kpos % cap) * n_kv + hk) * d
+                                                    : v + ((kpos - offset) * n_kv + hk) * d;
+                const double w = s[j] / sum;
+                for (int64_t e = 0; e < d; ++e) o[e] += w * (double)orc_f32_from_bf16(vv[e]);
+            }
+        }
+        free(s);
+    }
+}

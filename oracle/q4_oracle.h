@@ -67,6 +67,10 @@
  *                           within bf16 rounding; the pairs (i, i + D/2) and the rotation's
  *                           sign checked on one-hot inputs; pair norms preserved. MLX's
  *                           metal::fast trigonometry is parity unpinned.
+ *   orc_attention_f64       pinned: the softmax weights of a query sum to one; a single
+ *                           visible key returns its value row; equal keys average the
+ *                           values; the masks against brute-force position tests; GQA head
+ *                           sharing; against numpy's dense fp64 attention on random cases.
  *   orc_sample_topk_bf16    pinned: against std::partial_sort with the reference's own
  *                           comparator (oracle/stl_partial_sort.cc, libstdc++) - the same
  *                           ids where the top k + 1 values are distinct, the same values
@@ -158,6 +162,12 @@ void orc_rms_norm_bf16(const uint16_t* x, const uint16_t* w, int64_t rows, int64
 /* mx::fast::rope, non-traditional, on x [rows, heads, head_dim] at positions offset + r. */
 void orc_rope_bf16(const uint16_t* x, int64_t rows, int64_t heads, int64_t head_dim, int64_t rotated,
                    double base, int64_t offset, uint16_t* y);
+
+/* Scaled dot-product attention of ForwardPass::attention (scale 1, causal + optional
+ * sliding window, grouped-query heads) in fp64 over a cache prefix and a chunk. */
+void orc_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* cache_k,
+                       const uint16_t* cache_v, int64_t cap, int64_t L, int64_t n_heads, int64_t n_kv,
+                       int64_t d, int64_t offset, int64_t prefix_len, int64_t window, double* out);
 
 #ifdef __cplusplus
 }

@@ -767,3 +767,64 @@ def test_rope_oracle_pairs_and_sign_on_one_hot_inputs():
             assert y[i + d // 2] == syn.bf16_to_f32(syn.bf16_bits(np.float32(want[1]))), (i, src)
             others = np.delete(y, [i, i + d // 2])
             assert not others.any()
+
+
+# ---------------------------------------------------------------- attention (scale 1, causal + window, GQA)
+def _attention_dense(q, k, v, ck, cv, offset, prefix_len, window):
+    """The same attention written densely with numpy: gather the key/value rows by position,
+    a [L, T] visibility matrix by broadcasting, scores by einsum, softmax along T."""
+    qf = syn.bf16_to_f32(q).astype(np.float64)
+    L, H, D = qf.shape
+    KVH = k.shape[1]
+    cap = ck.shape[0]
+    pos = np.arange(offset - prefix_len, offset + L)
+    keys = np.concatenate([syn.bf16_to_f32(ck)[(pos[:prefix_len] % cap)], syn.bf16_to_f32(k)], 0).astype(np.float64)
+    vals = np.concatenate([syn.bf16_to_f32(cv)[(pos[:prefix_len] % cap)], syn.bf16_to_f32(v)], 0).astype(np.float64)
+    qpos = offset + np.arange(L)
+    vis = pos[None, :] <= qpos[:, None]
+    if window:
+        vis &= pos[None, :] > qpos[:, None] - window
+    g = H // KVH
+    kh = np.repeat(keys, g, axis=1)          # [T, H, D]
+    vh = np.repeat(vals, g, axis=1)
+    sc = np.einsum("lhd,thd->lht", qf, kh)
+    sc = np.where(vis[:, None, :], sc, -np.inf)
+    sc = sc - sc.max(-1, keepdims=True)
+    p = np.exp(sc)
+    p = p / p.sum(-1, keepdims=True)
+    return np.einsum("lht,thd->lhd", p, vh)
+
+
+@pytest.mark.parametrize("L,H,KVH,D,cap,offset,prefix,window", [
+    (1, 4, 2, 64, 16, 0, 0, 8), (3, 4, 2, 64, 16, 5, 5, 8), (4, 4, 2, 64, 16, 30, 8, 8),   # ring wrapped
+    (1, 8, 1, 128, 64, 40, 40, 0), (6, 8, 1, 128, 64, 10, 10, 0), (20, 4, 2, 64, 16, 0, 0, 8),
+    (5, 16, 8, 32, 12, 100, 10, 11)])
+def test_attention_oracle_matches_dense_numpy(L, H, KVH, D, cap, offset, prefix, window):
+    rng = np.random.default_rng(L * 100 + offset)
+    b = lambda *shape: syn.bf16_bits(rng.standard_normal(shape).astype(np.float32))  # noqa: E731
+    q, k, v, ck, cv = b(L, H, D), b(L, KVH, D), b(L, KVH, D), b(cap, KVH, D), b(cap, KVH, D)
+    got = O.attention_f64(q, k, v, ck, cv, offset, prefix, window)
+    np.testing.assert_allclose(got, _attention_dense(q, k, v, ck, cv, offset, prefix, window), rtol=1e-12, atol=1e-12)
+
+
+def test_attention_oracle_closed_forms():
+    rng = np.random.default_rng(9)
+    b = lambda *shape: syn.bf16_bits(rng.standard_normal(shape).astype(np.float32))  # noqa: E731
+    L, H, KVH, D, cap = 3, 4, 2, 64, 16
+    q, k, v, ck, cv = b(L, H, D), b(L, KVH, D), b(L, KVH, D), b(cap, KVH, D), b(cap, KVH, D)
+    # window 1: each query sees only itself -> its own value row (per kv head)
+    out = O.attention_f64(q, k, v, ck, cv, 7, 7, 1)
+    vf = syn.bf16_to_f32(v).astype(np.float64)
+    np.testing.assert_allclose(out, np.repeat(vf, H // KVH, axis=1), rtol=0, atol=1e-15)
+    # all keys equal -> the mean of the visible values
+    kk = np.repeat(k[:1], L, 0)
+    ckk = np.broadcast_to(k[:1], (cap, KVH, D)).copy()
+    out = O.attention_f64(q, kk, v, ckk, cv, 4, 4, 0)
+    allv = np.concatenate([syn.bf16_to_f32(cv)[np.arange(0, 4) % cap], vf], 0)
+    for t in range(L):
+        mean = allv[: 4 + t + 1].mean(0)
+        np.testing.assert_allclose(out[t], np.repeat(mean, H // KVH, axis=0), rtol=1e-12, atol=1e-12)
+    # values all one -> ones (the weights sum to one)
+    ones = np.full((L, KVH, D), 0x3F80, np.uint16)
+    out = O.attention_f64(q, k, ones, ck, np.full((cap, KVH, D), 0x3F80, np.uint16), 9, 9, 5)
+    np.testing.assert_allclose(out, 1.0, rtol=1e-12)
