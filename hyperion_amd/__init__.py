@@ -49,6 +49,10 @@ EXPORTED = [
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
     "hyp_rope", "hyp_sample_greedy", "hyp_sample_greedy_topk",
     "hyp_kv_cache_create", "hyp_kv_cache_free", "hyp_kv_cache_buffers", "hyp_kv_cache_write", "hyp_attention",
+    "hyp_attention_prepare", "hyp_residual_rms_norm",
+    "hyp_model_create", "hyp_model_free", "hyp_model_load", "hyp_kvstate_create", "hyp_kvstate_free",
+    "hyp_prefill_chunk", "hyp_decode_block", "hyp_prefill_chunk_sampled", "hyp_decode_block_sampled",
+    "hyp_step_result_create", "hyp_step_result_free", "hyp_step_result_fields", "hyp_model_forward_hidden",
     "hyp_step_program_create", "hyp_step_program_run", "hyp_step_program_check", "hyp_step_program_free",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
@@ -120,6 +124,91 @@ class GreedySample(ctypes.Structure):
     ]
 
 
+LAYER_SLIDING = 0   # HypLayerType (hyperion_mlx.h:63-66)
+LAYER_FULL = 1
+GEMMA4_TEXT = 0     # HypTextModelType
+GEMMA4_UNIFIED_TEXT = 1
+
+
+class RopeSpec(ctypes.Structure):
+    """HypRopeSpec (hyperion_mlx.h:75-80)."""
+    _fields_ = [
+        ("theta", ctypes.c_double),
+        ("has_partial_rotary_factor", ctypes.c_int),
+        ("partial_rotary_factor", ctypes.c_float),
+        ("proportional", ctypes.c_int),
+    ]
+
+
+class MoeConfig(ctypes.Structure):
+    _fields_ = [("num_experts", ctypes.c_uint32), ("top_k", ctypes.c_uint32),
+                ("moe_intermediate_size", ctypes.c_uint32)]
+
+
+class GeometryParams(ctypes.Structure):
+    """HypGeometryParams (hyperion_mlx.h:89-116)."""
+    _fields_ = [
+        ("model_type", ctypes.c_int),
+        ("hidden_size", ctypes.c_uint32),
+        ("intermediate_size", ctypes.c_uint32),
+        ("num_hidden_layers", ctypes.c_uint32),
+        ("layer_types", ctypes.POINTER(ctypes.c_int)),
+        ("num_attention_heads", ctypes.c_uint32),
+        ("head_dim_local", ctypes.c_uint32),
+        ("head_dim_global", ctypes.c_uint32),
+        ("num_kv_heads_local", ctypes.c_uint32),
+        ("num_kv_heads_global", ctypes.c_uint32),
+        ("attention_k_eq_v_global", ctypes.c_int),
+        ("num_kv_shared_layers", ctypes.c_uint32),
+        ("sliding_window", ctypes.c_uint32),
+        ("rope_local", RopeSpec),
+        ("rope_global", RopeSpec),
+        ("final_logit_softcapping", ctypes.c_float),
+        ("rms_norm_eps", ctypes.c_float),
+        ("attention_bias", ctypes.c_int),
+        ("vocab_size", ctypes.c_uint32),
+        ("max_position_embeddings", ctypes.c_uint32),
+        ("tie_word_embeddings", ctypes.c_int),
+        ("ple_hidden_per_layer_input", ctypes.c_uint32),
+        ("ple_vocab_per_layer_input", ctypes.c_uint32),
+        ("use_double_wide_mlp", ctypes.c_int),
+        ("has_moe", ctypes.c_int),
+        ("moe", MoeConfig),
+    ]
+
+
+class TokenStream(ctypes.Structure):
+    """HypTokenStream (hyperion_mlx.h:119-123)."""
+    _fields_ = [("tokens", ctypes.POINTER(ctypes.c_uint32)), ("count", ctypes.c_uint32),
+                ("is_prompt", ctypes.c_int)]
+
+
+class SamplingConfig(ctypes.Structure):
+    """HypSamplingConfig (hyperion_mlx.h:134-140)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+                ("min_p", ctypes.c_float), ("seed", ctypes.c_uint64)]
+
+
+class StepResultFields(ctypes.Structure):
+    """HypStepResultFields (hyperion_mlx.h:157-176)."""
+    _fields_ = [
+        ("token_id", ctypes.c_uint32),
+        ("logit", ctypes.c_float),
+        ("peak_mlx_bytes", ctypes.c_uint64),
+        ("active_mlx_bytes", ctypes.c_uint64),
+        ("phys_footprint_bytes", ctypes.c_uint64),
+        ("local_kv_bytes", ctypes.c_uint64),
+        ("global_kv_bytes", ctypes.c_uint64),
+        ("local_kv_eval_ms", ctypes.c_float),
+        ("global_kv_eval_ms", ctypes.c_float),
+        ("governor_state", ctypes.c_int),
+        ("near_tie_events", ctypes.c_uint32),
+        ("top_k_logprob_count", ctypes.c_uint32),
+        ("top_k_logprob_ids", ctypes.c_uint32 * TOP_K_LOGPROBS),
+        ("top_k_logprob_values", ctypes.c_float * TOP_K_LOGPROBS),
+    ]
+
+
 _lib = None
 _P = ctypes.c_void_p
 _PP = ctypes.POINTER(ctypes.c_void_p)
@@ -178,6 +267,22 @@ def lib() -> ctypes.CDLL:
         "hyp_kv_cache_buffers": [_P, _PP, _PP],
         "hyp_kv_cache_write": [_P, _P, _P, _U32, _U32, _P],
         "hyp_attention": [_P, _P, _P, _U32, _U32, _P, _U32, _U32, _U32, _P, _P],
+        "hyp_attention_prepare": [_P, _P, _P, _U32, _U32, _P, _P, _P, ctypes.c_float, _U32, ctypes.c_float, _U32,
+                                  _P],
+        "hyp_residual_rms_norm": [_P, _P, _P, _P, _P, _P, _U32, _U32, ctypes.c_float, _P],
+        "hyp_model_create": [_PP],
+        "hyp_model_free": [_PP],
+        "hyp_model_load": [_P, ctypes.POINTER(GeometryParams), ctypes.c_char_p],
+        "hyp_kvstate_create": [_P, _PP],
+        "hyp_kvstate_free": [_PP],
+        "hyp_prefill_chunk": [_P, _P, ctypes.POINTER(TokenStream), _P],
+        "hyp_decode_block": [_P, _P, _U32, _P],
+        "hyp_prefill_chunk_sampled": [_P, _P, ctypes.POINTER(TokenStream), ctypes.POINTER(SamplingConfig), _P],
+        "hyp_decode_block_sampled": [_P, _P, _U32, ctypes.POINTER(SamplingConfig), _P],
+        "hyp_step_result_create": [_PP],
+        "hyp_step_result_free": [_PP],
+        "hyp_step_result_fields": [_P, ctypes.POINTER(StepResultFields)],
+        "hyp_model_forward_hidden": [_P, _P, ctypes.POINTER(ctypes.c_uint32), _U32, _U32, _P],
         "hyp_step_program_create": [_P, _U32, _U32, _U32, _PP],
         "hyp_step_program_run": [_P, _P],
         "hyp_step_program_check": [_P],
@@ -583,6 +688,168 @@ def attention(q: "DeviceArray", k: "DeviceArray", v: "DeviceArray", L: int, n_he
     window > 0."""
     call("hyp_attention", q.ptr, k.ptr, v.ptr, L, n_heads, cache.handle, offset, prefix_len, window, out.ptr,
          stream.handle)
+
+
+def attention_prepare(q: "DeviceArray", k_raw: "DeviceArray", v_raw: Optional["DeviceArray"], L: int, n_heads: int,
+                      cache: KvCache, q_norm: "DeviceArray", k_norm: "DeviceArray", eps: float, rotated: int,
+                      base: float, offset: int, stream: "Stream") -> None:
+    """hyp_attention_prepare: q <- rope(q_norm(q)) in place; the cache's slots of positions
+    offset.. <- rope(k_norm(k_raw)) and v_norm(v_raw) (v_raw None: of k_raw)."""
+    call("hyp_attention_prepare", q.ptr, k_raw.ptr, None if v_raw is None else v_raw.ptr, L, n_heads, cache.handle,
+         q_norm.ptr, k_norm.ptr, eps, rotated, base, offset, stream.handle)
+
+
+def residual_rms_norm(branch: "DeviceArray", residual: "DeviceArray", post_w: "DeviceArray",
+                      scalar: Optional["DeviceArray"], next_w: Optional["DeviceArray"], nxt: Optional["DeviceArray"],
+                      m: int, hidden: int, eps: float, stream: "Stream") -> None:
+    """hyp_residual_rms_norm: residual <- bf16(residual + rms_norm(branch, post_w)), times the
+    layer scalar when given, then nxt <- rms_norm(residual, next_w) when given."""
+    opt = lambda a: None if a is None else a.ptr  # noqa: E731
+    call("hyp_residual_rms_norm", branch.ptr, residual.ptr, post_w.ptr, opt(scalar), opt(next_w), opt(nxt), m, hidden,
+         eps, stream.handle)
+
+
+def geometry_from_config(cfg: dict):
+    """HypGeometryParams from an mlx-lm config.json's text_config (the reference builds it
+    from hyperion-model's Geometry, crates/hyperion-core/src/geometry_abi.rs). Returns the
+    structure and the layer-type array it points into (keep both alive)."""
+    t = cfg.get("text_config", cfg)
+    kinds = [LAYER_SLIDING if k == "sliding_attention" else LAYER_FULL for k in t["layer_types"]]
+    types = (ctypes.c_int * len(kinds))(*kinds)
+    rp = t["rope_parameters"]
+    sl, fu = rp["sliding_attention"], rp["full_attention"]
+    g = GeometryParams()
+    g.model_type = GEMMA4_UNIFIED_TEXT if t.get("model_type", "").startswith("gemma4_unified") else GEMMA4_TEXT
+    g.hidden_size = t["hidden_size"]
+    g.intermediate_size = t["intermediate_size"]
+    g.num_hidden_layers = t["num_hidden_layers"]
+    g.layer_types = ctypes.cast(types, ctypes.POINTER(ctypes.c_int))
+    g.num_attention_heads = t["num_attention_heads"]
+    g.head_dim_local = t["head_dim"]
+    g.head_dim_global = t.get("global_head_dim", t["head_dim"])
+    g.num_kv_heads_local = t["num_key_value_heads"]
+    g.num_kv_heads_global = t.get("num_global_key_value_heads", t["num_key_value_heads"])
+    g.attention_k_eq_v_global = int(bool(t.get("attention_k_eq_v", True)))
+    g.num_kv_shared_layers = t.get("num_kv_shared_layers", 0) or 0
+    g.sliding_window = t["sliding_window"]
+    g.rope_local = RopeSpec(sl["rope_theta"], 0, 0.0, 0)
+    g.rope_global = RopeSpec(fu["rope_theta"], 1, fu.get("partial_rotary_factor", 1.0),
+                             int(fu.get("rope_type") == "proportional"))
+    g.final_logit_softcapping = t["final_logit_softcapping"]
+    g.rms_norm_eps = t["rms_norm_eps"]
+    g.attention_bias = int(bool(t.get("attention_bias", False)))
+    g.vocab_size = t["vocab_size"]
+    g.max_position_embeddings = t["max_position_embeddings"]
+    g.tie_word_embeddings = int(bool(t.get("tie_word_embeddings", cfg.get("tie_word_embeddings", True))))
+    g.ple_hidden_per_layer_input = t.get("hidden_size_per_layer_input", 0) or 0
+    g.ple_vocab_per_layer_input = t.get("vocab_size_per_layer_input", 0) or 0
+    g.use_double_wide_mlp = int(bool(t.get("use_double_wide_mlp", False)))
+    g.has_moe = int(bool(t.get("enable_moe_block", False)))
+    return g, types
+
+
+class StepResult:
+    """HypStepResult: a reusable per-step result handle."""
+
+    def __init__(self):
+        self.handle = ctypes.c_void_p()
+        call("hyp_step_result_create", ctypes.byref(self.handle))
+
+    def fields(self) -> StepResultFields:
+        f = StepResultFields()
+        call("hyp_step_result_fields", self.handle, ctypes.byref(f))
+        return f
+
+    def close(self) -> None:
+        if self.handle:
+            call("hyp_step_result_free", ctypes.byref(self.handle))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Model:
+    """HypModel loaded from an artifact directory for a geometry (hyp_model_create + load)."""
+
+    def __init__(self, geometry, weights_path: str):
+        self.handle = ctypes.c_void_p()
+        call("hyp_model_create", ctypes.byref(self.handle))
+        self._geometry = geometry
+        try:
+            call("hyp_model_load", self.handle, ctypes.byref(geometry[0] if isinstance(geometry, tuple) else geometry),
+                 weights_path.encode())
+        except Exception:
+            self.close()
+            raise
+        g = geometry[0] if isinstance(geometry, tuple) else geometry
+        self.hidden, self.vocab = g.hidden_size, g.vocab_size
+
+    def kvstate(self) -> "KvState":
+        return KvState(self)
+
+    def close(self) -> None:
+        if self.handle:
+            call("hyp_model_free", ctypes.byref(self.handle))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _sampling(cfg: Optional[SamplingConfig]):
+    return None if cfg is None else ctypes.byref(cfg)
+
+
+class KvState:
+    """HypKvState of a Model: its KV caches and cursor."""
+
+    def __init__(self, model: Model):
+        self.model = model
+        self.handle = ctypes.c_void_p()
+        call("hyp_kvstate_create", model.handle, ctypes.byref(self.handle))
+
+    def prefill(self, tokens, result: StepResult, sampling: Optional[SamplingConfig] = None,
+                sampled: bool = False) -> StepResultFields:
+        ids = np.ascontiguousarray(tokens, dtype=np.uint32)
+        ts = TokenStream(ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), ids.size, 1)
+        if sampled or sampling is not None:
+            call("hyp_prefill_chunk_sampled", self.model.handle, self.handle, ctypes.byref(ts), _sampling(sampling),
+                 result.handle)
+        else:
+            call("hyp_prefill_chunk", self.model.handle, self.handle, ctypes.byref(ts), result.handle)
+        return result.fields()
+
+    def decode(self, n_tokens: int, result: StepResult, sampling: Optional[SamplingConfig] = None,
+               sampled: bool = False) -> StepResultFields:
+        if sampled or sampling is not None:
+            call("hyp_decode_block_sampled", self.model.handle, self.handle, n_tokens, _sampling(sampling),
+                 result.handle)
+        else:
+            call("hyp_decode_block", self.model.handle, self.handle, n_tokens, result.handle)
+        return result.fields()
+
+    def forward_hidden(self, tokens, offset: int) -> np.ndarray:
+        """hyp_model_forward_hidden: the final-normalised hidden rows (bf16 bits [n, hidden])."""
+        ids = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.zeros((ids.size, self.model.hidden), np.uint16)
+        call("hyp_model_forward_hidden", self.model.handle, self.handle,
+             ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), ids.size, offset, out.ctypes.data_as(_P))
+        return out
+
+    def close(self) -> None:
+        if self.handle:
+            call("hyp_kvstate_free", ctypes.byref(self.handle))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def sample_greedy_topk(logits: DeviceArray, rows: int, vocab: int, out: DeviceArray, stream: Stream,

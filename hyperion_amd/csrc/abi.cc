@@ -13,6 +13,7 @@
 
 #include "hyperion_hip.h"
 #include "kernels.h"
+#include "decoder.h"
 #include "qlinear.h"
 #include "step_program_host.h"
 
@@ -692,6 +693,8 @@ HypStatus hyp_kv_cache_free(HypKvCache* cache) {
     return free_handle(cache, kKvCacheMagic);
 }
 
+}  // extern "C"
+
 namespace {
 HypKvCacheOpaque& kv_ref(HypKvCache c) {
     REQUIRE_ARG(c != nullptr, "kv cache handle is null");
@@ -701,6 +704,8 @@ HypKvCacheOpaque& kv_ref(HypKvCache c) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0u; }
 }  // namespace
+
+extern "C" {
 
 HypStatus hyp_kv_cache_buffers(HypKvCache cache, void** out_k, void** out_v) {
     return abi_call("hyp_kv_cache_buffers", [&] {
@@ -732,13 +737,15 @@ HypStatus hyp_attention(const void* q, const void* k, const void* v, uint32_t L,
         hipStream_t s = stream_of(stream);
         HypKvCacheOpaque& c = kv_ref(cache);
         if (L == 0) return;
-        REQUIRE_ARG(q != nullptr && k != nullptr && v != nullptr && out != nullptr,
-                    "q, k, v and out must be non-null device pointers");
+        REQUIRE_ARG(q != nullptr && out != nullptr, "q and out must be non-null device pointers");
+        REQUIRE_ARG((k == nullptr) == (v == nullptr), "k and v must both be device pointers or both NULL");
         REQUIRE_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
                     "q, k, v and out must be 16-byte aligned");
         REQUIRE_ARG(n_heads > 0 && n_heads % c.num_kv_heads == 0, "n_heads must be a multiple of the cache's num_kv_heads");
         REQUIRE_ARG(prefix_len <= offset, "prefix_len must not exceed offset");
         REQUIRE_ARG(prefix_len <= c.capacity, "prefix_len must not exceed the cache capacity");
+        REQUIRE_ARG(k != nullptr || static_cast<uint64_t>(prefix_len) + L <= c.capacity,
+                    "with the chunk read from the cache, prefix_len + L must not exceed the cache capacity");
         REQUIRE_ARG(static_cast<uint64_t>(offset) + L < (1ull << 31), "positions must stay below 2^31");
         REQUIRE_ARG(static_cast<uint64_t>(L) * n_heads * c.head_dim < (1ull << 31), "q too large");
         hyperion::hip::AttnArgs a{};
@@ -759,6 +766,68 @@ HypStatus hyp_attention(const void* q, const void* k, const void* v, uint32_t L,
         a.workspace = c.workspace.data();
         a.workspace_bytes = c.workspace.bytes();
         hyperion::hip::launch_attention(a, s);
+    });
+}
+
+HypStatus hyp_attention_prepare(void* q, const void* k_raw, const void* v_raw, uint32_t L, uint32_t n_heads,
+                                HypKvCache cache, const void* q_norm, const void* k_norm, float eps,
+                                uint32_t rotated_dims, float rope_base, uint32_t offset, HypStream stream) {
+    return abi_call("hyp_attention_prepare", [&] {
+        hipStream_t s = stream_of(stream);
+        HypKvCacheOpaque& c = kv_ref(cache);
+        if (L == 0) return;
+        REQUIRE_ARG(q != nullptr && k_raw != nullptr && q_norm != nullptr && k_norm != nullptr,
+                    "q, k_raw, q_norm and k_norm must be non-null device pointers");
+        REQUIRE_ARG(aligned16(q) && aligned16(k_raw) && aligned16(v_raw) && aligned16(q_norm) && aligned16(k_norm),
+                    "q, k_raw, v_raw, q_norm and k_norm must be 16-byte aligned");
+        REQUIRE_ARG(n_heads > 0 && n_heads % c.num_kv_heads == 0, "n_heads must be a multiple of the cache's num_kv_heads");
+        REQUIRE_ARG(std::isfinite(eps) && eps >= 0.0f, "eps must be finite and >= 0");
+        REQUIRE_ARG(rotated_dims <= c.head_dim && rotated_dims % 2u == 0u, "rotated_dims must be even and <= head_dim");
+        REQUIRE_ARG(std::isfinite(rope_base) && rope_base > 0.0f, "rope_base must be finite and positive");
+        REQUIRE_ARG(static_cast<uint64_t>(offset) + L < (1ull << 24), "positions must stay below 2^24");
+        REQUIRE_ARG(static_cast<uint64_t>(L) * n_heads * c.head_dim < (1ull << 31), "q too large");
+        hyperion::hip::AttnPrepareArgs a{};
+        a.q = static_cast<uint16_t*>(q);
+        a.k_raw = static_cast<const uint16_t*>(k_raw);
+        a.v_raw = static_cast<const uint16_t*>(v_raw);
+        a.q_norm = static_cast<const uint16_t*>(q_norm);
+        a.k_norm = static_cast<const uint16_t*>(k_norm);
+        a.cache_k = static_cast<uint16_t*>(c.k.data());
+        a.cache_v = static_cast<uint16_t*>(c.v.data());
+        a.L = L;
+        a.n_heads = n_heads;
+        a.n_kv_heads = c.num_kv_heads;
+        a.head_dim = c.head_dim;
+        a.rotated = rotated_dims;
+        a.offset = offset;
+        a.cap = c.capacity;
+        a.base = rope_base;
+        a.eps = eps;
+        hyperion::hip::launch_attn_prepare(a, s);
+    });
+}
+
+HypStatus hyp_residual_rms_norm(const void* branch, void* residual, const void* post_weight, const void* scalar,
+                                const void* next_weight, void* next, uint32_t m, uint32_t hidden, float eps,
+                                HypStream stream) {
+    return abi_call("hyp_residual_rms_norm", [&] {
+        hipStream_t s = stream_of(stream);
+        if (m == 0) return;
+        REQUIRE_ARG(branch != nullptr && residual != nullptr && post_weight != nullptr,
+                    "branch, residual and post_weight must be non-null device pointers");
+        REQUIRE_ARG((next_weight == nullptr) == (next == nullptr), "next_weight and next must both be given or both NULL");
+        REQUIRE_ARG(aligned16(branch) && aligned16(residual) && aligned16(post_weight) && aligned16(next_weight) &&
+                        aligned16(next),
+                    "branch, residual, post_weight, next_weight and next must be 16-byte aligned");
+        REQUIRE_ARG(hidden > 0 && hidden % 64u == 0u && hidden <= hyperion::hip::residual_norm_max_hidden(),
+                    "hidden must be a positive multiple of 64, at most 16384");
+        REQUIRE_ARG(std::isfinite(eps) && eps >= 0.0f, "eps must be finite and >= 0");
+        REQUIRE_ARG(static_cast<uint64_t>(m) < (1ull << 31), "too many rows");
+        hyperion::hip::launch_residual_norm(static_cast<const uint16_t*>(branch), static_cast<uint16_t*>(residual),
+                                            static_cast<const uint16_t*>(post_weight),
+                                            static_cast<const uint16_t*>(scalar),
+                                            static_cast<const uint16_t*>(next_weight), static_cast<uint16_t*>(next), m,
+                                            hidden, eps, s);
     });
 }
 
@@ -887,6 +956,214 @@ HypStatus hyp_qmodel_embed(HypQModel model, HypQWeight* out_weight) {
         REQUIRE_ARG(model != nullptr && model->magic == kQModelMagic, "model handle is invalid");
         REQUIRE_ARG(out_weight != nullptr, "requires a non-null out handle");
         *out_weight = model->embed.get();
+    });
+}
+
+}  // extern "C"
+
+// ---- the model, its KV state and the step ABI (model.cc:359-740) ------------------------
+
+constexpr std::uint32_t kModelMagic = 0x48504D44U;        // "HPMD"
+constexpr std::uint32_t kKvStateMagic = 0x48504B53U;      // "HPKS"
+constexpr std::uint32_t kStepResultMagic = 0x48505352U;   // "HPSR"
+
+struct HypModelOpaque {
+    std::uint32_t magic = 0;
+    std::unique_ptr<hyperion::model::Decoder> decoder;   // null until hyp_model_load
+};
+
+struct HypKvStateOpaque {
+    std::uint32_t magic = 0;
+    const HypModelOpaque* model = nullptr;   // the model it was made for (compared, not used)
+    hyperion::model::DecoderState state;
+};
+
+struct HypStepResultOpaque {
+    std::uint32_t magic = 0;
+    HypStepResultFields fields{};
+};
+
+namespace {
+
+hyperion::model::Decoder& loaded(HypModel model) {
+    REQUIRE_ARG(model != nullptr && model->magic == kModelMagic, "model handle is invalid");
+    REQUIRE_ARG(model->decoder != nullptr, "model is not loaded");
+    return *model->decoder;
+}
+
+hyperion::model::DecoderState& state_of(HypModel model, HypKvState kv) {
+    REQUIRE_ARG(kv != nullptr && kv->magic == kKvStateMagic, "kvstate handle is invalid");
+    REQUIRE_ARG(kv->model == model, "kvstate was created for another model");
+    return kv->state;
+}
+
+HypStepResultOpaque& result_of(HypStepResult r) {
+    REQUIRE_ARG(r != nullptr && r->magic == kStepResultMagic, "step-result handle is invalid");
+    return *r;
+}
+
+// validate_sampling_config (model.cc:234-257): NULL or temperature 0 is the greedy path.
+bool sampled_greedy(const HypSamplingConfig* c, uint32_t vocab) {
+    if (c == nullptr || c->temperature == 0.0f) return true;
+    REQUIRE_ARG(!(c->temperature < 0.0f), "sampling temperature must be >= 0 (0 = greedy)");
+    REQUIRE_ARG(c->top_k >= 0, "sampling top_k must be >= 0 (0 = disabled)");
+    REQUIRE_ARG(c->top_k == 0 || static_cast<uint64_t>(c->top_k) <= vocab, "sampling top_k exceeds the vocabulary size");
+    REQUIRE_ARG(std::isnan(c->top_p) || (c->top_p >= 0.0f && c->top_p <= 1.0f),
+                "sampling top_p must be in [0, 1] (0 = disabled)");
+    REQUIRE_ARG(c->min_p >= 0.0f && c->min_p < 1.0f, "sampling min_p must be in [0, 1) (0 = disabled)");
+    throw NativeError(HYP_STATUS_UNSUPPORTED, "sampling with temperature > 0 is not built; use temperature 0");
+}
+
+// write_step_result / write_step_result_sampled (model.cc:310-356).
+void write_result(HypStepResultOpaque& r, const hyperion::model::StepSample& smp,
+                  const hyperion::model::DecoderState& st, bool sidecar) {
+    r.fields = HypStepResultFields{};
+    r.fields.token_id = smp.sample.token_id;
+    r.fields.logit = smp.sample.logit;
+    r.fields.local_kv_bytes = st.local_bytes;
+    r.fields.global_kv_bytes = st.global_bytes;
+    r.fields.governor_state = HYP_GOVERNOR_READY;
+    if (sidecar) {
+        r.fields.top_k_logprob_count = smp.sample.top_k_count;
+        for (uint32_t i = 0; i < smp.sample.top_k_count && i < HYP_TOP_K_LOGPROBS; ++i) {
+            r.fields.top_k_logprob_ids[i] = smp.sample.top_k_ids[i];
+            r.fields.top_k_logprob_values[i] = smp.sample.top_k_logprobs[i];
+        }
+    } else {
+        r.fields.near_tie_events = smp.near_tie_events;
+    }
+}
+
+void check_tokens(const HypTokenStream* tokens) {
+    REQUIRE_ARG(tokens != nullptr, "tokens is null");
+    REQUIRE_ARG(tokens->count != 0, "prefill token count is 0");
+    REQUIRE_ARG(tokens->tokens != nullptr, "tokens->tokens is null");
+}
+
+}  // namespace
+
+extern "C" {
+
+HypStatus hyp_model_create(HypModel* out_model) {
+    return abi_call("hyp_model_create", [&] {
+        REQUIRE_ARG(out_model != nullptr, "create requires a non-null out handle");
+        auto m = std::make_unique<HypModelOpaque>();
+        m->magic = kModelMagic;
+        *out_model = m.release();
+    });
+}
+
+HypStatus hyp_model_free(HypModel* model) {
+    return free_handle(model, kModelMagic);
+}
+
+HypStatus hyp_model_load(HypModel model, const HypGeometryParams* geometry, const char* weights_path) {
+    return abi_call("hyp_model_load", [&] {
+        REQUIRE_ARG(model != nullptr && model->magic == kModelMagic, "model handle is invalid");
+        REQUIRE_ARG(geometry != nullptr, "geometry is null");
+        REQUIRE_ARG(weights_path != nullptr, "weights_path is null");
+        REQUIRE_ARG(model->decoder == nullptr, "model is already loaded");
+        hyperion::model::Geometry geo = hyperion::model::Geometry::from_abi(*geometry);
+        // The artifact is resolved and checked on the host before the first device call.
+        const hyperion::model::ModelManifest manifest(weights_path, geo.num_layers());
+        REQUIRE_ARG(manifest.num_layers() == geo.num_layers(), "the artifact holds fewer layers than the geometry");
+        require_device();
+        model->decoder = std::make_unique<hyperion::model::Decoder>(std::move(geo), manifest.upload());
+    });
+}
+
+HypStatus hyp_kvstate_create(HypModel model, HypKvState* out_kvstate) {
+    return abi_call("hyp_kvstate_create", [&] {
+        REQUIRE_ARG(model != nullptr && model->magic == kModelMagic, "model handle is invalid");
+        REQUIRE_ARG(out_kvstate != nullptr, "out_kvstate is null");
+        REQUIRE_ARG(model->decoder != nullptr, "model is not loaded; cannot allocate KV state");
+        auto kv = std::make_unique<HypKvStateOpaque>();
+        kv->model = model;
+        kv->state = model->decoder->make_state();
+        kv->magic = kKvStateMagic;
+        *out_kvstate = kv.release();
+    });
+}
+
+HypStatus hyp_kvstate_free(HypKvState* kvstate) {
+    return free_handle(kvstate, kKvStateMagic);
+}
+
+HypStatus hyp_prefill_chunk(HypModel model, HypKvState kvstate, const HypTokenStream* tokens,
+                            HypStepResult out_result) {
+    return abi_call("hyp_prefill_chunk", [&] {
+        hyperion::model::Decoder& dec = loaded(model);
+        hyperion::model::DecoderState& st = state_of(model, kvstate);
+        check_tokens(tokens);
+        HypStepResultOpaque& r = result_of(out_result);
+        const auto smp = dec.prefill(st, tokens->tokens, tokens->count);
+        write_result(r, smp, st, false);
+    });
+}
+
+HypStatus hyp_decode_block(HypModel model, HypKvState kvstate, uint32_t n_tokens, HypStepResult out_result) {
+    return abi_call("hyp_decode_block", [&] {
+        hyperion::model::Decoder& dec = loaded(model);
+        hyperion::model::DecoderState& st = state_of(model, kvstate);
+        HypStepResultOpaque& r = result_of(out_result);
+        const auto smp = dec.decode(st, n_tokens);
+        write_result(r, smp, st, false);
+    });
+}
+
+HypStatus hyp_prefill_chunk_sampled(HypModel model, HypKvState kvstate, const HypTokenStream* tokens,
+                                    const HypSamplingConfig* config, HypStepResult out_result) {
+    return abi_call("hyp_prefill_chunk_sampled", [&] {
+        hyperion::model::Decoder& dec = loaded(model);
+        hyperion::model::DecoderState& st = state_of(model, kvstate);
+        check_tokens(tokens);
+        HypStepResultOpaque& r = result_of(out_result);
+        sampled_greedy(config, dec.geometry().vocab);
+        const auto smp = dec.prefill(st, tokens->tokens, tokens->count);
+        write_result(r, smp, st, true);
+    });
+}
+
+HypStatus hyp_decode_block_sampled(HypModel model, HypKvState kvstate, uint32_t n_tokens,
+                                   const HypSamplingConfig* config, HypStepResult out_result) {
+    return abi_call("hyp_decode_block_sampled", [&] {
+        hyperion::model::Decoder& dec = loaded(model);
+        hyperion::model::DecoderState& st = state_of(model, kvstate);
+        HypStepResultOpaque& r = result_of(out_result);
+        sampled_greedy(config, dec.geometry().vocab);
+        const auto smp = dec.decode(st, n_tokens);
+        write_result(r, smp, st, true);
+    });
+}
+
+HypStatus hyp_step_result_create(HypStepResult* out_result) {
+    return abi_call("hyp_step_result_create", [&] {
+        REQUIRE_ARG(out_result != nullptr, "create requires a non-null out handle");
+        auto r = std::make_unique<HypStepResultOpaque>();
+        r->magic = kStepResultMagic;
+        *out_result = r.release();
+    });
+}
+
+HypStatus hyp_step_result_free(HypStepResult* result) {
+    return free_handle(result, kStepResultMagic);
+}
+
+HypStatus hyp_step_result_fields(HypStepResult result, HypStepResultFields* out_fields) {
+    return abi_call("hyp_step_result_fields", [&] {
+        const HypStepResultOpaque& r = result_of(result);
+        REQUIRE_ARG(out_fields != nullptr, "out_fields is null");
+        *out_fields = r.fields;
+    });
+}
+
+HypStatus hyp_model_forward_hidden(HypModel model, HypKvState kvstate, const uint32_t* ids, uint32_t count,
+                                   uint32_t offset, uint16_t* hidden_out) {
+    return abi_call("hyp_model_forward_hidden", [&] {
+        hyperion::model::Decoder& dec = loaded(model);
+        hyperion::model::DecoderState& st = state_of(model, kvstate);
+        REQUIRE_ARG(ids != nullptr && hidden_out != nullptr, "ids and hidden_out must be non-null host pointers");
+        dec.forward_hidden(st, ids, count, offset, hidden_out);
     });
 }
 

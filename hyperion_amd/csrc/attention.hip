@@ -7,7 +7,9 @@
 // chunk sits at position offset + t and sees key position p when p <= offset + t and, for
 // a sliding layer, p > offset + t - window (build_mask, forward.cc:345-373); query head h
 // reads kv head h / (H / KVH). Keys are the cache's positions [offset - prefix, offset)
-// (slot p % capacity) followed by the chunk's L positions.
+// (slot p % capacity) followed by the chunk's L positions, read from the chunk's k/v or,
+// when those are null, from the cache (the decoder appends the chunk first; it sizes its
+// rings to hold prefix + L positions).
 //
 // One kernel serves prefill and decode, flash-attention style on v_mfma_f32_16x16x32_bf16:
 //  * A workgroup (4 waves) takes a tile of 64 query rows of one kv head - row r is token
@@ -40,7 +42,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
     const uint16_t* q;      // [L][H][D]
-    const uint16_t* k;      // [L][KVH][D]: the chunk
+    const uint16_t* k;      // [L][KVH][D]: the chunk, or null when it is in the cache
     const uint16_t* v;
     const uint16_t* ck;     // [cap][KVH][D]: the cache
     const uint16_t* cv;
@@ -65,8 +67,9 @@ struct AttnLds {
 
 __device__ __forceinline__ const uint16_t* key_row(const AttnParams& p, const uint16_t* chunk, const uint16_t* cache,
                                                    uint32_t j, uint32_t hk, uint32_t D) {
-    // Key index j (0 .. prefix + L) -> its row: the cache for the prefix, the chunk after.
-    if (j < p.prefix) {
+    // Key index j (0 .. prefix + L) -> its row: the cache for the prefix, the chunk after
+    // (the cache too when the chunk has already been appended: chunk == null).
+    if (j < p.prefix || chunk == nullptr) {
         const uint32_t pos = p.offset - p.prefix + j;
         return cache + (static_cast<size_t>(pos % p.cap) * p.KVH + hk) * D;
     }

@@ -1,0 +1,431 @@
+// The decoder around the Q4 projections; see decoder.h for what each part replaces.
+#include "decoder.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <utility>
+
+#include "kernels.h"
+
+namespace hyperion::model {
+
+using hip::NativeError;
+
+namespace {
+
+[[noreturn]] void invalid(const std::string& what) { throw NativeError(HYP_STATUS_INVALID_ARGUMENT, what); }
+[[noreturn]] void unsupported(const std::string& what) { throw NativeError(HYP_STATUS_UNSUPPORTED, what); }
+
+float host_round_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+}
+
+RopeParams rope_from_abi(const HypRopeSpec& s) {
+    RopeParams r;
+    r.theta = s.theta;
+    r.has_partial = s.has_partial_rotary_factor != 0;
+    r.partial = s.partial_rotary_factor;
+    r.proportional = s.proportional != 0;
+    return r;
+}
+
+bool attention_head_dim(uint32_t d) { return d == 64u || d == 128u || d == 256u || d == 512u; }
+
+uint16_t* u16(const DeviceBuffer& b) { return static_cast<uint16_t*>(b.data()); }
+
+}  // namespace
+
+Geometry Geometry::from_abi(const HypGeometryParams& p) {
+    // Geometry::from_abi (geometry.cc:23-76).
+    if (p.layer_types == nullptr && p.num_hidden_layers > 0) invalid("layer_types pointer is null");
+    if (p.model_type != HYP_GEMMA4_TEXT && p.model_type != HYP_GEMMA4_UNIFIED_TEXT) {
+        invalid("unknown HypTextModelType");
+    }
+    Geometry g;
+    g.types.reserve(p.num_hidden_layers);
+    for (uint32_t i = 0; i < p.num_hidden_layers; ++i) {
+        if (p.layer_types[i] == HYP_LAYER_SLIDING) {
+            g.types.push_back(LayerType::Sliding);
+        } else if (p.layer_types[i] == HYP_LAYER_FULL) {
+            g.types.push_back(LayerType::Full);
+        } else {
+            invalid("unknown HypLayerType at index " + std::to_string(i));
+        }
+    }
+    g.hidden = p.hidden_size;
+    g.intermediate = p.intermediate_size;
+    g.heads = p.num_attention_heads;
+    g.head_dim_local = p.head_dim_local;
+    g.head_dim_global = p.head_dim_global;
+    g.kv_heads_local = p.num_kv_heads_local;
+    g.kv_heads_global = p.num_kv_heads_global;
+    g.k_eq_v_global = p.attention_k_eq_v_global != 0;
+    g.window = p.sliding_window;
+    g.rope_local = rope_from_abi(p.rope_local);
+    g.rope_global = rope_from_abi(p.rope_global);
+    g.softcap = p.final_logit_softcapping;
+    g.eps = p.rms_norm_eps;
+    g.vocab = p.vocab_size;
+    g.max_positions = p.max_position_embeddings;
+
+    // Geometry::validate (geometry.cc:78-130).
+    if (g.types.empty()) invalid("layer_types is empty");
+    if (g.types.back() != LayerType::Full) invalid("the last layer must be full_attention (Gemma 4 invariant)");
+    if (g.window == 0) invalid("sliding_window must be non-zero");
+    if (p.num_kv_shared_layers > p.num_hidden_layers) invalid("num_kv_shared_layers exceeds num_hidden_layers");
+    if (g.head_dim_local == 0 || g.head_dim_global == 0) {
+        invalid("head_dim_local and head_dim_global must be non-zero");
+    }
+    if (g.heads == 0 || g.kv_heads_local == 0 || g.kv_heads_global == 0) {
+        invalid("attention/KV head counts must be non-zero");
+    }
+    if (g.vocab == 0) invalid("vocab_size must be non-zero");
+    if (g.rope_local.proportional) invalid("sliding rope must be the default (full rotary) scheme");
+    if (g.rope_local.has_partial) invalid("sliding rope must be full rotary (no partial_rotary_factor)");
+    if (!g.rope_global.proportional) invalid("global rope must be the proportional scheme");
+    if (!g.rope_global.has_partial) invalid("global rope must set partial_rotary_factor");
+    if (!(g.rope_local.theta > 0.0) || !(g.rope_global.theta > 0.0)) invalid("rope_theta must be positive");
+    if (p.tie_word_embeddings == 0) {
+        invalid("tie_word_embeddings must be true (lm_head is tied to the embedding table)");
+    }
+    if (p.has_moe != 0 && (p.moe.num_experts == 0 || p.moe.top_k == 0 || p.moe.moe_intermediate_size == 0)) {
+        invalid("moe block requires non-zero num_experts/top_k/moe_intermediate_size");
+    }
+    if (!(g.eps >= 0.0f) || !std::isfinite(g.eps)) invalid("rms_norm_eps must be finite and >= 0");
+    if (!(g.softcap > 0.0f) || !std::isfinite(g.softcap)) invalid("final_logit_softcapping must be finite and > 0");
+    if (g.max_positions == 0) invalid("max_position_embeddings must be non-zero");
+
+    // What this build runs: the dense Gemma 4 text decoder of the tiny fixture and the 12B.
+    if (p.has_moe != 0) unsupported("mixture-of-experts blocks are not built");
+    if (p.ple_hidden_per_layer_input != 0 || p.ple_vocab_per_layer_input != 0) {
+        unsupported("per-layer input embeddings are not built");
+    }
+    if (p.use_double_wide_mlp != 0) unsupported("the double-wide MLP is not built");
+    if (p.num_kv_shared_layers != 0) unsupported("shared KV layers are not built");
+    if (p.attention_bias != 0) unsupported("attention bias is not built");
+    if (!g.k_eq_v_global) unsupported("global layers without attention_k_eq_v are not built");
+    if (!attention_head_dim(g.head_dim_local) || !attention_head_dim(g.head_dim_global)) {
+        unsupported("head dims must be 64, 128, 256 or 512");
+    }
+    if (g.heads % g.kv_heads_local != 0 || g.heads % g.kv_heads_global != 0) {
+        invalid("num_attention_heads must be a multiple of the KV head counts");
+    }
+    if (g.hidden == 0 || g.hidden % 64u != 0 || g.hidden > hip::residual_norm_max_hidden()) {
+        unsupported("hidden_size must be a non-zero multiple of 64, at most 16384");
+    }
+    if (g.intermediate == 0 || g.intermediate % 64u != 0) {
+        unsupported("intermediate_size must be a non-zero multiple of 64");
+    }
+    const uint32_t rotated = g.rotated_dims(LayerType::Full);
+    if (!(g.rope_global.partial > 0.0f) || rotated == 0) invalid("partial_rotary_factor leaves no rotated dims");
+    if (rotated > g.head_dim_global) invalid("partial_rotary_factor must be at most 1");
+    return g;
+}
+
+uint32_t Geometry::rotated_dims(LayerType kind) const noexcept {
+    if (kind == LayerType::Sliding) return head_dim_local;
+    // Rope::Rope (rope.cc:44-49): floor(prf * head_dim) in fp32, rounded down to even.
+    const float r = rope_global.partial * static_cast<float>(head_dim_global);
+    if (!(r >= 0.0f)) return 0;
+    uint32_t rotated = r >= 4294967295.0f ? 0xffffffffu : static_cast<uint32_t>(r);
+    rotated -= rotated % 2u;
+    return rotated;
+}
+
+Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geometry)), w_(std::move(weights)) {
+    const Geometry& g = geo_;
+    if (!w_.has_norms) invalid("the weights artifact is missing norm vectors or layer scalars");
+    if (w_.layers.size() != g.types.size()) {
+        invalid("the artifact holds " + std::to_string(w_.layers.size()) + " layers, the geometry " +
+                std::to_string(g.types.size()));
+    }
+    // The weight schema must agree with the geometry (weights_loader.cc:116-124), and every
+    // tensor with its dims (weights_test.cc:76-82 checks the same on the fixture).
+    if (w_.embed.mat.n != g.vocab || w_.embed.mat.k != g.hidden) invalid("embed_tokens is not [vocab, hidden]");
+    if (w_.final_norm_len != g.hidden) invalid("the final norm is not [hidden]");
+    for (size_t i = 0; i < w_.layers.size(); ++i) {
+        const LayerWeights& lw = w_.layers[i];
+        const std::string at = "layer " + std::to_string(i) + ": ";
+        if (lw.kind != g.types[i]) {
+            invalid(at + "weight schema (" + (lw.kind == LayerType::Sliding ? "sliding" : "global") +
+                    ") disagrees with geometry layer_types");
+        }
+        const bool sliding = lw.kind == LayerType::Sliding;
+        const uint32_t D = sliding ? g.head_dim_local : g.head_dim_global;
+        const uint32_t kvh = sliding ? g.kv_heads_local : g.kv_heads_global;
+        auto shape = [&](const QuantizedLinear& l, uint32_t n, uint32_t k, const char* name) {
+            if (l.mat.n != n || l.mat.k != k) {
+                invalid(at + name + " is [" + std::to_string(l.mat.n) + ", " + std::to_string(l.mat.k) +
+                        "], expected [" + std::to_string(n) + ", " + std::to_string(k) + "]");
+            }
+        };
+        shape(lw.q_proj, g.heads * D, g.hidden, "q_proj");
+        shape(lw.k_proj, kvh * D, g.hidden, "k_proj");
+        if (sliding) shape(*lw.v_proj, kvh * D, g.hidden, "v_proj");
+        shape(lw.o_proj, g.hidden, g.heads * D, "o_proj");
+        shape(lw.gate_proj, g.intermediate, g.hidden, "gate_proj");
+        shape(lw.up_proj, g.intermediate, g.hidden, "up_proj");
+        shape(lw.down_proj, g.hidden, g.intermediate, "down_proj");
+        const uint32_t want[kLayerNorms] = {g.hidden, g.hidden, g.hidden, g.hidden, D, D, 1u};
+        for (int j = 0; j < kLayerNorms; ++j) {
+            if (lw.norm_len[j] != want[j]) invalid(at + "a norm vector or layer_scalar has the wrong length");
+        }
+    }
+
+    embed_scale_ = host_round_bf16(std::sqrt(static_cast<float>(g.hidden)));
+    softcap_ = host_round_bf16(g.softcap);
+    HYP_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+
+    const size_t T = kChunkTokens;
+    const uint32_t dmax = std::max(g.head_dim_local, g.head_dim_global);
+    const uint32_t kvmax = std::max(g.kv_heads_local * g.head_dim_local, g.kv_heads_global * g.head_dim_global);
+    ids_ = DeviceBuffer(T * sizeof(uint32_t));
+    x_ = DeviceBuffer(T * g.hidden * 2u);
+    xn_ = DeviceBuffer(T * g.hidden * 2u);
+    q_ = DeviceBuffer(T * g.heads * dmax * 2u);
+    k_ = DeviceBuffer(T * kvmax * 2u);
+    v_ = DeviceBuffer(T * kvmax * 2u);
+    attn_ = DeviceBuffer(T * g.heads * dmax * 2u);
+    o_ = DeviceBuffer(T * g.hidden * 2u);
+    h_ = DeviceBuffer(T * g.intermediate * 2u);
+    d_ = DeviceBuffer(T * g.hidden * 2u);
+    last_ = DeviceBuffer(static_cast<size_t>(g.hidden) * 2u);
+    logits_ = DeviceBuffer(static_cast<size_t>(g.vocab) * 2u);
+    attn_ws_ = DeviceBuffer(std::max(hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
+                                     hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)));
+    sample_ws_ = DeviceBuffer(hip::sample_greedy_workspace_bytes());
+}
+
+Decoder::~Decoder() {
+    if (stream_ != nullptr) {
+        (void)hipStreamSynchronize(stream_);
+        (void)hipStreamDestroy(stream_);
+    }
+}
+
+DecoderState Decoder::make_state() const {
+    const Geometry& g = geo_;
+    DecoderState st;
+    st.caches.reserve(g.types.size());
+    for (LayerType kind : g.types) {
+        LayerCache c;
+        const bool sliding = kind == LayerType::Sliding;
+        c.head_dim = sliding ? g.head_dim_local : g.head_dim_global;
+        c.kv_heads = sliding ? g.kv_heads_local : g.kv_heads_global;
+        c.cap = sliding ? std::min(g.window + kChunkTokens, g.max_positions) : g.max_positions;
+        const size_t bytes = static_cast<size_t>(c.cap) * c.kv_heads * c.head_dim * 2u;
+        c.k = DeviceBuffer(bytes);
+        c.v = DeviceBuffer(bytes);
+        // Unwritten slots are never read (the masks stop at the committed positions), but
+        // cleared memory keeps a stray read finite.
+        HYP_HIP_CHECK(hipMemsetAsync(c.k.data(), 0, bytes, stream_));
+        HYP_HIP_CHECK(hipMemsetAsync(c.v.data(), 0, bytes, stream_));
+        (sliding ? st.local_bytes : st.global_bytes) += 2u * bytes;
+        st.caches.push_back(std::move(c));
+    }
+    ensure_sample_slots(st, 2);
+    HYP_HIP_CHECK(hipStreamSynchronize(stream_));
+    return st;
+}
+
+void Decoder::ensure_sample_slots(DecoderState& st, uint32_t slots) const {
+    if (st.sample_slots >= slots) return;
+    DeviceBuffer fresh(static_cast<size_t>(slots) * sizeof(HypTopKSample));
+    HYP_HIP_CHECK(hipMemsetAsync(fresh.data(), 0, fresh.bytes(), stream_));
+    if (st.sample_slots > 0) {
+        HYP_HIP_CHECK(hipMemcpyAsync(fresh.data(), st.samples.data(), sizeof(HypTopKSample), hipMemcpyDeviceToDevice,
+                                     stream_));
+    }
+    HYP_HIP_CHECK(hipStreamSynchronize(stream_));
+    st.samples = std::move(fresh);
+    st.sample_slots = slots;
+}
+
+void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset,
+                            uint16_t* final_rows) {
+    const Geometry& g = geo_;
+    hipStream_t s = stream_;
+    uint16_t* x = u16(x_);
+    uint16_t* xn = u16(xn_);
+    const float eps = g.eps;
+    // At decode sizes the q/k/v launch normalises its input rows itself (the same bits as
+    // the standalone norm); above them the input norm is a pass of its own, fused into the
+    // previous layer's closing residual kernel.
+    const bool norm_in_qkv = L <= hip::kSkinnyMaxM && hip::skinny_norm_supported(L, g.hidden);
+
+    // ForwardPass::embed (forward.cc:126-131): gathered rows dequantized, times bf16(sqrt(hidden)).
+    hip::launch_q4_dequantize_tiled(w_.embed.mat, d_ids, L, embed_scale_, x, s);
+    if (!norm_in_qkv) {
+        hip::launch_rms_normalize(x, w_.layers[0].norm(LayerNorm::kInput), L, g.hidden, eps, xn, s);
+    }
+
+    for (size_t i = 0; i < w_.layers.size(); ++i) {
+        const LayerWeights& lw = w_.layers[i];
+        LayerCache& cache = st.caches[i];
+        const bool sliding = lw.kind == LayerType::Sliding;
+        const uint32_t D = cache.head_dim;
+        const uint32_t kvh = cache.kv_heads;
+
+        // q/k/v (forward.cc:395-409; a global layer has no v_proj: K = V).
+        const hip::Q4Matrix* ws[3] = {&lw.q_proj.mat, &lw.k_proj.mat, sliding ? &lw.v_proj->mat : nullptr};
+        uint16_t* ys[3] = {u16(q_), u16(k_), u16(v_)};
+        const uint32_t count = sliding ? 3u : 2u;
+        if (norm_in_qkv) {
+            hip::launch_q4_skinny_group(ws, ys, count, x, L, &eps, lw.norm(LayerNorm::kInput), s);
+        } else if (hip::skinny_supported(L, g.hidden, false)) {
+            hip::launch_q4_skinny_group(ws, ys, count, xn, L, nullptr, nullptr, s);
+        } else {
+            hip::launch_q4_gemm_group(ws, ys, count, xn, L, s);
+        }
+
+        // q_norm / k_norm / v_norm, RoPE, the cache append (forward.cc:400-459).
+        hip::AttnPrepareArgs pa{};
+        pa.q = u16(q_);
+        pa.k_raw = u16(k_);
+        pa.v_raw = sliding ? u16(v_) : nullptr;
+        pa.q_norm = lw.norm(LayerNorm::kQ);
+        pa.k_norm = lw.norm(LayerNorm::kK);
+        pa.cache_k = u16(cache.k);
+        pa.cache_v = u16(cache.v);
+        pa.L = L;
+        pa.n_heads = g.heads;
+        pa.n_kv_heads = kvh;
+        pa.head_dim = D;
+        pa.rotated = g.rotated_dims(lw.kind);
+        pa.offset = offset;
+        pa.cap = cache.cap;
+        pa.base = static_cast<float>(sliding ? g.rope_local.theta : g.rope_global.theta);
+        pa.eps = eps;
+        hip::launch_attn_prepare(pa, s);
+
+        // SDPA over the visible cached prefix and the appended chunk (forward.cc:420-505).
+        hip::AttnArgs aa{};
+        aa.q = u16(q_);
+        aa.k = nullptr;
+        aa.v = nullptr;
+        aa.cache_k = u16(cache.k);
+        aa.cache_v = u16(cache.v);
+        aa.out = u16(attn_);
+        aa.L = L;
+        aa.n_heads = g.heads;
+        aa.n_kv_heads = kvh;
+        aa.head_dim = D;
+        aa.cap = cache.cap;
+        aa.offset = offset;
+        aa.prefix_len = sliding ? std::min(g.window, offset) : offset;
+        aa.window = sliding ? g.window : 0u;
+        aa.workspace = attn_ws_.data();
+        aa.workspace_bytes = attn_ws_.bytes();
+        hip::launch_attention(aa, s);
+
+        // o, then the attention half of the sandwich and the MLP's input norm (forward.cc:518-526).
+        lw.o_proj.apply(u16(attn_), L, u16(o_), s);
+        hip::launch_residual_norm(u16(o_), x, lw.norm(LayerNorm::kPostAttention), nullptr,
+                                  lw.norm(LayerNorm::kPreFeedforward), xn, L, g.hidden, eps, s);
+        // mlp (forward.cc:338-343), the feed-forward half and the layer scalar (:527-539).
+        mlp_gate_up(lw.gate_proj, lw.up_proj, xn, L, u16(h_), s);
+        lw.down_proj.apply(u16(h_), L, u16(d_), s);
+        const uint16_t* next_w =
+            !norm_in_qkv && i + 1 < w_.layers.size() ? w_.layers[i + 1].norm(LayerNorm::kInput) : nullptr;
+        hip::launch_residual_norm(u16(d_), x, lw.norm(LayerNorm::kPostFeedforward), lw.norm(LayerNorm::kScalar),
+                                  next_w, next_w != nullptr ? xn : nullptr, L, g.hidden, eps, s);
+    }
+
+    // final_norm (forward.cc:133-135).
+    const uint16_t* fw = static_cast<const uint16_t*>(w_.final_norm.data());
+    if (final_rows != nullptr) {
+        hip::launch_rms_normalize(x, fw, L, g.hidden, eps, final_rows, s);
+    } else {
+        hip::launch_rms_normalize(x + static_cast<size_t>(L - 1) * g.hidden, fw, 1, g.hidden, eps, u16(last_), s);
+    }
+}
+
+void Decoder::epilogue(HypTopKSample* d_out) {
+    // run_epilogue (model.cc:215-228): tied lm_head + softcap on the last position, then
+    // the greedy pick with its top-k sidecar (model.cc:262-288).
+    w_.embed.apply(u16(last_), 1, u16(logits_), stream_, Epilogue::kSoftcap, softcap_);
+    hip::launch_sample_topk(u16(logits_), 1, geo_.vocab, d_out, sample_ws_.data(), sample_ws_.bytes(), stream_);
+}
+
+void Decoder::forward_hidden(DecoderState& st, const uint32_t* ids, uint32_t count, uint32_t offset,
+                             uint16_t* hidden_out) {
+    const Geometry& g = geo_;
+    if (count == 0) invalid("forward requires at least one token");
+    if (static_cast<uint64_t>(offset) + count > g.max_positions) invalid("positions exceed max_position_embeddings");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ids[i] >= g.vocab) invalid("token id " + std::to_string(ids[i]) + " is outside the vocabulary");
+    }
+    for (uint32_t done = 0; done < count;) {
+        const uint32_t take = std::min(kChunkTokens, count - done);
+        HYP_HIP_CHECK(hipMemcpyAsync(ids_.data(), ids + done, take * sizeof(uint32_t), hipMemcpyHostToDevice, stream_));
+        forward_chunk(st, static_cast<const uint32_t*>(ids_.data()), take, offset + done, u16(o_));
+        HYP_HIP_CHECK(hipMemcpyAsync(hidden_out + static_cast<size_t>(done) * g.hidden, o_.data(),
+                                     static_cast<size_t>(take) * g.hidden * 2u, hipMemcpyDeviceToHost, stream_));
+        HYP_HIP_CHECK(hipStreamSynchronize(stream_));
+        done += take;
+    }
+}
+
+StepSample Decoder::prefill(DecoderState& st, const uint32_t* ids, uint32_t count) {
+    const Geometry& g = geo_;
+    if (st.offset != 0) invalid("prefill requires a fresh (offset 0) KV state");
+    if (count > g.max_positions) invalid("the prompt exceeds max_position_embeddings");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ids[i] >= g.vocab) invalid("token id " + std::to_string(ids[i]) + " is outside the vocabulary");
+    }
+    auto* samples = static_cast<HypTopKSample*>(st.samples.data());
+    for (uint32_t done = 0; done < count;) {
+        const uint32_t take = std::min(kChunkTokens, count - done);
+        HYP_HIP_CHECK(hipMemcpyAsync(ids_.data(), ids + done, take * sizeof(uint32_t), hipMemcpyHostToDevice, stream_));
+        forward_chunk(st, static_cast<const uint32_t*>(ids_.data()), take, done, nullptr);
+        done += take;
+        if (done == count) epilogue(samples);
+        // The ids buffer is reused by the next chunk: its copy waits for this chunk.
+        HYP_HIP_CHECK(hipStreamSynchronize(stream_));
+    }
+    StepSample out;
+    HYP_HIP_CHECK(hipMemcpy(&out.sample, samples, sizeof(HypTopKSample), hipMemcpyDeviceToHost));
+    out.near_tie_events = out.sample.near_tie != 0u ? 1u : 0u;
+    st.offset = count;
+    st.last_token = out.sample.token_id;
+    return out;
+}
+
+StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
+    const Geometry& g = geo_;
+    if (st.offset == 0) invalid("decode requires a populated KV state (prefill first)");
+    if (static_cast<uint64_t>(st.offset) + n_tokens > g.max_positions) {
+        invalid("decoding past max_position_embeddings");
+    }
+    StepSample out;
+    if (n_tokens == 0) return out;
+    ensure_sample_slots(st, n_tokens + 1u);
+    auto* samples = static_cast<HypTopKSample*>(st.samples.data());
+    // Slot 0 holds the last sampled token; step j embeds slot j's token and samples into
+    // slot j + 1, all on the device.
+    for (uint32_t j = 0; j < n_tokens; ++j) {
+        forward_chunk(st, reinterpret_cast<const uint32_t*>(samples + j), 1, st.offset + j, nullptr);
+        epilogue(samples + j + 1);
+    }
+    std::vector<HypTopKSample> host(n_tokens);
+    HYP_HIP_CHECK(hipMemcpyAsync(host.data(), samples + 1, n_tokens * sizeof(HypTopKSample), hipMemcpyDeviceToHost,
+                                 stream_));
+    HYP_HIP_CHECK(hipMemcpyAsync(samples, samples + n_tokens, sizeof(HypTopKSample), hipMemcpyDeviceToDevice, stream_));
+    HYP_HIP_CHECK(hipStreamSynchronize(stream_));
+    for (const HypTopKSample& smp : host) out.near_tie_events += smp.near_tie != 0u ? 1u : 0u;
+    out.sample = host.back();
+    st.offset += n_tokens;
+    st.last_token = out.sample.token_id;
+    return out;
+}
+
+}  // namespace hyperion::model

@@ -1,0 +1,139 @@
+// The decoder around the Q4 projections, device-resident: the model-level half of the
+// reference's native engine re-expressed on HIP buffers and the kernels of this library.
+//
+//   Geometry::from_abi / validate   native/hyperion_mlx/src/geometry.cc:23-130
+//   Decoder (ForwardPass)           forward.cc:95-135 (construction, embed, final_norm),
+//                                   :376-508 (attention), :509-541 (decoder_layer),
+//                                   :543-563 (forward), :137-189 (lm_head, softcap, greedy)
+//   DecoderState (KvState)          kv_cache.h:33 (LocalKvCache), :143 (GlobalKvCache)
+//   prefill / decode_block          model.cc:515-627 (hyp_prefill_chunk), :629-740
+//                                   (hyp_decode_block), :262-301 (the greedy sidecar)
+//
+// Differences of form, not of results:
+//  * every KV cache is allocated once at its final size. A sliding layer's ring holds
+//    window + kChunkTokens positions, so a chunk is appended before its attention and the
+//    window it needs is never overwritten; a global layer's cache holds
+//    max_position_embeddings positions (the reference grows it in 256-token steps; HBM holds
+//    the 12B's 8 global caches at 262144 positions in 4.3 GB).
+//  * the sampled token stays in device memory between decode steps: the next step's embed
+//    gather reads it there, so a decode block makes one host round trip, at its end.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "hyperion_hip.h"
+#include "qlinear.h"
+
+namespace hyperion::model {
+
+// Prefill chunk size (model.cc:574, kPrefillChunkSize).
+constexpr uint32_t kChunkTokens = 2048;
+
+struct RopeParams {
+    double theta = 0.0;
+    bool has_partial = false;
+    float partial = 0.0f;
+    bool proportional = false;
+};
+
+struct Geometry {
+    uint32_t hidden = 0;
+    uint32_t intermediate = 0;
+    std::vector<LayerType> types;
+    uint32_t heads = 0;
+    uint32_t head_dim_local = 0;
+    uint32_t head_dim_global = 0;
+    uint32_t kv_heads_local = 0;
+    uint32_t kv_heads_global = 0;
+    bool k_eq_v_global = true;
+    uint32_t window = 0;
+    RopeParams rope_local;
+    RopeParams rope_global;
+    float softcap = 0.0f;
+    float eps = 0.0f;
+    uint32_t vocab = 0;
+    uint32_t max_positions = 0;
+
+    // Geometry::from_abi + validate (geometry.cc:23-130): INVALID_ARGUMENT for what the
+    // reference rejects, UNSUPPORTED for the variants this build does not run (MoE,
+    // per-layer inputs, double-wide MLP, shared KV layers, attention bias, head dims other
+    // than 64/128/256/512, sizes not a multiple of 64).
+    static Geometry from_abi(const HypGeometryParams& p);
+
+    [[nodiscard]] uint32_t num_layers() const noexcept { return static_cast<uint32_t>(types.size()); }
+    // Rope::Rope (rope.cc:36-56): the proportional scheme rotates floor(prf * head_dim)
+    // rounded down to even dims; the default scheme the whole head.
+    [[nodiscard]] uint32_t rotated_dims(LayerType kind) const noexcept;
+};
+
+struct LayerCache {
+    DeviceBuffer k;   // [cap][kv_heads][head_dim] bf16
+    DeviceBuffer v;
+    uint32_t cap = 0;
+    uint32_t kv_heads = 0;
+    uint32_t head_dim = 0;
+};
+
+// One sequence's KV state (KvState, kv.h) plus its autoregressive cursor (model.cc:606-607).
+struct DecoderState {
+    std::vector<LayerCache> caches;   // one per layer, in layer order
+    uint32_t offset = 0;              // tokens committed
+    uint32_t last_token = 0;
+    DeviceBuffer samples;             // HypTopKSample [sample_slots]: slot 0 = last step's
+    uint32_t sample_slots = 0;
+    uint64_t local_bytes = 0;
+    uint64_t global_bytes = 0;
+};
+
+// One sampled step as the ABI reports it.
+struct StepSample {
+    HypTopKSample sample{};
+    uint32_t near_tie_events = 0;
+};
+
+class Decoder {
+  public:
+    Decoder(Geometry geometry, ModelWeights weights);
+    ~Decoder();
+    Decoder(const Decoder&) = delete;
+    Decoder& operator=(const Decoder&) = delete;
+
+    [[nodiscard]] const Geometry& geometry() const noexcept { return geo_; }
+    [[nodiscard]] hipStream_t stream() const noexcept { return stream_; }
+
+    // build_kv_state (kv.cc) at final sizes.
+    [[nodiscard]] DecoderState make_state() const;
+
+    // ForwardPass::embed + forward over `count` tokens at positions offset.. (host ids),
+    // appending their K/V; the final-normalised hidden rows [count][hidden] bf16 are copied
+    // to the host. Does not move the cursor. Synchronous.
+    void forward_hidden(DecoderState& st, const uint32_t* ids, uint32_t count, uint32_t offset,
+                        uint16_t* hidden_out);
+    // hyp_prefill_chunk: chunked prefill of a fresh state, then the epilogue on the last
+    // position. Synchronous.
+    StepSample prefill(DecoderState& st, const uint32_t* ids, uint32_t count);
+    // hyp_decode_block: n_tokens greedy steps from the cursor. Synchronous.
+    StepSample decode(DecoderState& st, uint32_t n_tokens);
+
+  private:
+    // embed + all layers over L <= kChunkTokens tokens whose ids are in device memory.
+    // final_rows: all L final-normalised rows there; otherwise the last row into last_.
+    void forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset, uint16_t* final_rows);
+    // lm_head + softcap + greedy with the top-k sidecar of last_ into *d_out.
+    void epilogue(HypTopKSample* d_out);
+    void ensure_sample_slots(DecoderState& st, uint32_t slots) const;
+
+    Geometry geo_;
+    ModelWeights w_;
+    hipStream_t stream_ = nullptr;
+    float embed_scale_ = 0.0f;   // bf16(sqrt(hidden)) (forward.cc:103,126-131)
+    float softcap_ = 0.0f;       // bf16(final_logit_softcapping)
+    DeviceBuffer ids_;           // uint32 [kChunkTokens]
+    DeviceBuffer x_, xn_, q_, k_, v_, attn_, o_, h_, d_, last_, logits_;
+    DeviceBuffer attn_ws_, sample_ws_;
+};
+
+}  // namespace hyperion::model

@@ -112,8 +112,8 @@ void launch_sample_topk(const uint16_t* logits, uint32_t rows, uint32_t vocab, H
 constexpr uint32_t kAttnMaxSplits = 32;
 struct AttnArgs {
     const uint16_t* q;         // [L][n_heads][head_dim]
-    const uint16_t* k;         // [L][n_kv_heads][head_dim] (the chunk)
-    const uint16_t* v;
+    const uint16_t* k;         // [L][n_kv_heads][head_dim] (the chunk); null: the chunk is
+    const uint16_t* v;         // already in the cache at positions offset .. offset + L - 1
     const uint16_t* cache_k;   // [cap][n_kv_heads][head_dim]
     const uint16_t* cache_v;
     uint16_t* out;             // [L][n_heads][head_dim]
@@ -127,6 +127,31 @@ void launch_attention(const AttnArgs& a, hipStream_t stream);
 // Tokens pos0.. of k/v [n][n_kv_heads][head_dim] into cache slots (pos % cap).
 void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_t* cv, uint32_t n, uint32_t pos0,
                      uint32_t cap, uint32_t n_kv_heads, uint32_t head_dim, hipStream_t stream);
+
+// q/k/v from their projections to the cache (forward.cc:395-459), see layer_kernels.hip:
+// q <- rope(rms_norm(q, q_norm)) in place; cache K slot <- rope(rms_norm(k_raw, k_norm));
+// cache V slot <- rms_norm(v_raw) (v_raw null: of k_raw). Token t is at position offset + t,
+// slot (offset + t) % cap; when L > cap only the last cap tokens reach the cache.
+struct AttnPrepareArgs {
+    uint16_t* q;
+    const uint16_t* k_raw;
+    const uint16_t* v_raw;
+    const uint16_t* q_norm;
+    const uint16_t* k_norm;
+    uint16_t* cache_k;
+    uint16_t* cache_v;
+    uint32_t L, n_heads, n_kv_heads, head_dim, rotated, offset, cap;
+    float base, eps;
+};
+void launch_attn_prepare(const AttnPrepareArgs& a, hipStream_t stream);
+
+// For each of m rows: residual <- bf16(residual + rms_norm(branch, w_post)); with scalar
+// (device bf16 [1]) residual <- bf16(residual * scalar); with w_next, next <- rms_norm(
+// residual, w_next). hidden a multiple of 64, at most residual_norm_max_hidden().
+uint32_t residual_norm_max_hidden();
+void launch_residual_norm(const uint16_t* branch, uint16_t* residual, const uint16_t* w_post, const uint16_t* scalar,
+                          const uint16_t* w_next, uint16_t* next, uint32_t m, uint32_t hidden, float eps,
+                          hipStream_t stream);
 
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,

@@ -87,6 +87,19 @@ void apply_group(const QuantizedLinear* const* linears, uint16_t* const* ys, uin
 
 enum class LayerType { Sliding, Full };
 
+// The bf16 vectors of a layer (weights_loader.cc:142-148), device-resident: the four
+// sandwich norms [hidden], q_norm and k_norm [head_dim], layer_scalar [1].
+enum class LayerNorm : int {
+    kInput = 0,
+    kPostAttention = 1,
+    kPreFeedforward = 2,
+    kPostFeedforward = 3,
+    kQ = 4,
+    kK = 5,
+    kScalar = 6,
+};
+constexpr int kLayerNorms = 7;
+
 struct LayerWeights {
     QuantizedLinear q_proj;
     QuantizedLinear k_proj;
@@ -96,11 +109,20 @@ struct LayerWeights {
     QuantizedLinear up_proj;
     QuantizedLinear down_proj;
     LayerType kind = LayerType::Sliding;
+    DeviceBuffer norms[kLayerNorms];          // empty when the artifact has none
+    uint32_t norm_len[kLayerNorms] = {};
+
+    [[nodiscard]] const uint16_t* norm(LayerNorm which) const noexcept {
+        return static_cast<const uint16_t*>(norms[static_cast<int>(which)].data());
+    }
 };
 
 struct ModelWeights {
     QuantizedLinear embed;   // tied: also the LM head (forward.cc:137-152)
     std::vector<LayerWeights> layers;
+    DeviceBuffer final_norm;   // [hidden] bf16 (weights_loader.cc:108); empty when absent
+    uint32_t final_norm_len = 0;
+    bool has_norms = false;    // every layer's vectors and the final norm were loaded
 };
 
 // Host phase of load_model_weights: maps every shard, resolves and shape-checks

@@ -78,10 +78,36 @@ QuantizedLinear upload(const ProjPlan& p) {
                                       reinterpret_cast<const uint16_t*>(p.b->file->data(*p.b->info)), p.n, p.k);
 }
 
+// The layer's bf16 vectors, in LayerNorm order (weights_loader.cc:142-148).
+constexpr const char* kNormNames[kLayerNorms] = {
+    "input_layernorm.weight",          "post_attention_layernorm.weight", "pre_feedforward_layernorm.weight",
+    "post_feedforward_layernorm.weight", "self_attn.q_norm.weight",         "self_attn.k_norm.weight",
+    "layer_scalar",
+};
+constexpr const char* kFinalNorm = "language_model.model.norm.weight";
+
+// A 1-D bf16 vector, or null when absent.
+const Located* plan_vector(const NameMap& tensors, const std::string& name) {
+    const auto it = tensors.find(name);
+    if (it == tensors.end()) return nullptr;
+    const TensorInfo& t = *it->second.info;
+    if (t.dtype != "BF16" || t.shape.size() != 1 || t.shape[0] <= 0 || t.shape[0] > 0xffffffffLL) {
+        throw NativeError(HYP_STATUS_INVALID_ARGUMENT, name + ": expected a non-empty 1-D BF16 vector");
+    }
+    return &it->second;
+}
+
 struct LayerPlan {
     ProjPlan proj[7];   // q, k, v, o, gate, up, down
     bool sliding = true;
+    const Located* norm[kLayerNorms] = {};
 };
+
+DeviceBuffer upload_vector(const Located& v) {
+    DeviceBuffer buf(v.info->end - v.info->begin);
+    HYP_HIP_CHECK(hipMemcpy(buf.data(), v.file->data(*v.info), buf.bytes(), hipMemcpyHostToDevice));
+    return buf;
+}
 
 }  // namespace
 
@@ -90,6 +116,8 @@ struct ModelManifest::Impl {
     NameMap tensors;
     ProjPlan embed;
     std::vector<LayerPlan> layers;
+    const Located* final_norm = nullptr;
+    bool has_norms = false;
 };
 
 ModelManifest::ModelManifest(const std::string& dir, uint32_t num_layers) : impl_(std::make_unique<Impl>()) {
@@ -135,8 +163,15 @@ ModelManifest::ModelManifest(const std::string& dir, uint32_t num_layers) : impl
         lp.proj[4] = plan_proj(tensors, layer_tensor(i, "mlp.gate_proj"));
         lp.proj[5] = plan_proj(tensors, layer_tensor(i, "mlp.up_proj"));
         lp.proj[6] = plan_proj(tensors, layer_tensor(i, "mlp.down_proj"));
+        for (int j = 0; j < kLayerNorms; ++j) lp.norm[j] = plan_vector(tensors, layer_tensor(i, kNormNames[j]));
         impl_->layers.push_back(lp);
     }
+    impl_->final_norm = plan_vector(tensors, kFinalNorm);
+    bool all = impl_->final_norm != nullptr;
+    for (const LayerPlan& lp : impl_->layers) {
+        for (const Located* v : lp.norm) all = all && v != nullptr;
+    }
+    impl_->has_norms = all;
 }
 
 ModelManifest::~ModelManifest() = default;
@@ -157,8 +192,18 @@ ModelWeights ModelManifest::upload() const {
         lw.up_proj = hyperion::model::upload(lp.proj[5]);
         lw.down_proj = hyperion::model::upload(lp.proj[6]);
         lw.kind = lp.sliding ? LayerType::Sliding : LayerType::Full;
+        for (int j = 0; j < kLayerNorms; ++j) {
+            if (lp.norm[j] == nullptr) continue;
+            lw.norms[j] = upload_vector(*lp.norm[j]);
+            lw.norm_len[j] = static_cast<uint32_t>(lp.norm[j]->info->shape[0]);
+        }
         weights.layers.push_back(std::move(lw));
     }
+    if (impl_->final_norm != nullptr) {
+        weights.final_norm = upload_vector(*impl_->final_norm);
+        weights.final_norm_len = static_cast<uint32_t>(impl_->final_norm->info->shape[0]);
+    }
+    weights.has_norms = impl_->has_norms;
     return weights;
 }
 

@@ -95,3 +95,107 @@ def sig_rel(got, ref) -> float:
     md = float(np.max(np.abs(got - ref))) if got.size else 0.0
     mo = float(np.max(np.abs(ref))) if ref.size else 0.0
     return md / mo if mo > 0 else md
+
+
+# Gemma 4 text_config of the 12B (crates/hyperion-model/src/geometry.rs:466-500) with the
+# layer count and context as parameters; the tiny fixture's config.json has the same keys.
+def gemma4_text_config(num_layers: int = 48, vocab: int = VOCAB, max_positions: int = 262144,
+                       layer_types=None) -> dict:
+    if layer_types is None:   # five sliding layers, then a global one
+        layer_types = ["full_attention" if (i + 1) % 6 == 0 else "sliding_attention" for i in range(num_layers)]
+    return {
+        "model_type": "gemma4_unified_text", "hidden_size": HIDDEN, "intermediate_size": 15360,
+        "num_hidden_layers": num_layers, "layer_types": list(layer_types), "num_attention_heads": 16,
+        "head_dim": 256, "global_head_dim": 512, "num_key_value_heads": 8, "num_global_key_value_heads": 1,
+        "attention_k_eq_v": True, "num_kv_shared_layers": 0, "sliding_window": 1024,
+        "rope_parameters": {"sliding_attention": {"rope_theta": 10000.0, "rope_type": "default"},
+                            "full_attention": {"rope_theta": 1000000.0, "partial_rotary_factor": 0.25,
+                                               "rope_type": "proportional"}},
+        "final_logit_softcapping": 30.0, "rms_norm_eps": 1e-6, "attention_bias": False, "vocab_size": vocab,
+        "max_position_embeddings": max_positions, "tie_word_embeddings": True, "hidden_size_per_layer_input": 0,
+        "vocab_size_per_layer_input": 0, "use_double_wide_mlp": False, "enable_moe_block": False,
+    }
+
+
+def _q4_random(rng, n: int, k: int):
+    """Random Q4/g64 codes whose dequantized rows have std ~ 1/sqrt(k): q ~ U{0..15},
+    scale = bf16(u / (4.61 sqrt(k))) with u ~ U(0.5, 1.5), bias = bf16(-7.5 * scale)."""
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    u = rng.uniform(0.5, 1.5, size=(n, k // 64)).astype(np.float32)
+    s = bf16_bits(u / np.float32(4.61 * np.sqrt(k)))
+    b = bf16_bits(bf16_to_f32(s) * np.float32(-7.5))
+    return w, s, b
+
+
+def write_safetensors(path: str, tensors: dict) -> None:
+    """{name: numpy array} -> one safetensors file (U32 for uint32, BF16 for uint16 bit patterns)."""
+    import json
+    header, offset, blobs = {}, 0, []
+    for name, a in tensors.items():
+        a = np.ascontiguousarray(a)
+        dt = {np.dtype(np.uint32): "U32", np.dtype(np.uint16): "BF16", np.dtype(np.float32): "F32"}[a.dtype]
+        header[name] = {"dtype": dt, "shape": list(a.shape), "data_offsets": [offset, offset + a.nbytes]}
+        offset += a.nbytes
+        blobs.append(a)
+    raw = json.dumps(header).encode()
+    raw += b" " * (-len(raw) % 8)
+    with open(path, "wb") as f:
+        f.write(np.uint64(len(raw)).tobytes())
+        f.write(raw)
+        for a in blobs:
+            a.tofile(f)
+
+
+def write_model(directory: str, text_config: dict, seed: int, branch_gain: float = 1.0,
+                qk_gain: float = 1.0) -> dict:
+    """A random-init Gemma 4 artifact in the mlx-lm layout (config.json + one safetensors
+    shard): Q4/g64 projections of unit-gain rows; input, pre-feedforward and final norm
+    weights bf16(1 + 0.1 N(0,1)); the post-attention and post-feedforward norms (the
+    branches added to the residual stream) around branch_gain; q_norm and k_norm around
+    qk_gain * head_dim^-1/4 (so the scale-1 attention scores have a standard deviation of
+    about qk_gain^2); layer scalars bf16(U(0.6, 1.0)). Returns the tensors written."""
+    import json
+    import os
+    t = text_config
+    rng = np.random.default_rng(seed)
+    hidden, inter, heads = t["hidden_size"], t["intermediate_size"], t["num_attention_heads"]
+    P = "language_model.model."
+    out = {}
+
+    def proj(name, n, k):
+        w, s, b = _q4_random(rng, n, k)
+        out[name + ".weight"], out[name + ".scales"], out[name + ".biases"] = w, s, b
+
+    def vec(name, n, around=1.0, spread=0.1):
+        out[name] = bf16_bits(np.float32(around) + np.float32(spread) * rng.standard_normal(n).astype(np.float32))
+
+    proj(P + "embed_tokens", t["vocab_size"], hidden)
+    for i, kind in enumerate(t["layer_types"]):
+        sliding = kind == "sliding_attention"
+        d = t["head_dim"] if sliding else t.get("global_head_dim", t["head_dim"])
+        kvh = t["num_key_value_heads"] if sliding else t.get("num_global_key_value_heads", t["num_key_value_heads"])
+        a = f"{P}layers.{i}.self_attn."
+        proj(a + "q_proj", heads * d, hidden)
+        proj(a + "k_proj", kvh * d, hidden)
+        if sliding:
+            proj(a + "v_proj", kvh * d, hidden)
+        proj(a + "o_proj", hidden, heads * d)
+        qk = qk_gain * d ** -0.25
+        vec(a + "q_norm.weight", d, qk, 0.1 * qk)
+        vec(a + "k_norm.weight", d, qk, 0.1 * qk)
+        m = f"{P}layers.{i}."
+        proj(m + "mlp.gate_proj", inter, hidden)
+        proj(m + "mlp.up_proj", inter, hidden)
+        proj(m + "mlp.down_proj", hidden, inter)
+        for norm in ("input_layernorm", "pre_feedforward_layernorm"):
+            vec(m + norm + ".weight", hidden)
+        for norm in ("post_attention_layernorm", "post_feedforward_layernorm"):
+            vec(m + norm + ".weight", hidden, branch_gain, 0.1 * branch_gain)
+        out[m + "layer_scalar"] = bf16_bits(rng.uniform(0.6, 1.0, size=1).astype(np.float32))
+    vec(P + "norm.weight", hidden)
+    os.makedirs(directory, exist_ok=True)
+    write_safetensors(os.path.join(directory, "model.safetensors"), out)
+    with open(os.path.join(directory, "config.json"), "w") as f:
+        json.dump({"model_type": "gemma4_unified", "tie_word_embeddings": True,
+                   "quantization": {"group_size": 64, "bits": 4, "mode": "affine"}, "text_config": t}, f)
+    return out

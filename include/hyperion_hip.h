@@ -343,6 +343,171 @@ HypStatus hyp_kv_cache_write(HypKvCache cache, const void* k, const void* v, uin
 HypStatus hyp_attention(const void* q, const void* k, const void* v, uint32_t L, uint32_t n_heads, HypKvCache cache,
                         uint32_t offset, uint32_t prefix_len, uint32_t window, void* out, HypStream stream);
 
+/* ---- the rest of a decoder layer (forward.cc:395-459, 518-539) ---------------------- */
+
+/* From the q/k/v projections to the cache append, one launch (forward.cc:400-459): for
+ * token t of the chunk (position offset + t, cache slot (offset + t) % capacity),
+ *   q[t][h]        <- rope(rms_norm(q[t][h], q_norm))            in place, every head h;
+ *   cache K[slot]  <- rope(rms_norm(k_raw[t][j], k_norm))        every kv head j;
+ *   cache V[slot]  <- rms_norm(v_raw[t][j]) without a weight     (v_norm; v_raw NULL reads
+ *                                                                 k_raw: the K = V layers).
+ * q [L][n_heads][head_dim], k_raw / v_raw [L][num_kv_heads][head_dim], q_norm / k_norm bf16
+ * [head_dim], all device memory, 16-byte aligned; rope as hyp_rope with rotated_dims and
+ * rope_base. The bits are those of hyp_rms_normalize, hyp_rope and hyp_kv_cache_write in
+ * sequence. Then hyp_attention(q, NULL, NULL, L, ...) reads the chunk from the cache, which
+ * needs prefix_len + L <= capacity. */
+HypStatus hyp_attention_prepare(void* q, const void* k_raw, const void* v_raw, uint32_t L, uint32_t n_heads,
+                                HypKvCache cache, const void* q_norm, const void* k_norm, float eps,
+                                uint32_t rotated_dims, float rope_base, uint32_t offset, HypStream stream);
+
+/* The Gemma sandwich closing a block (ForwardPass::decoder_layer, forward.cc:518-539), one
+ * launch over m rows of hidden bf16 (device, 16-byte aligned):
+ *   residual <- bf16(residual + rms_norm(branch, post_weight));
+ *   residual <- bf16(residual * scalar[0])          when scalar (device bf16 [1]) is non-NULL
+ *                                                   (the layer_scalar after the MLP half);
+ *   next     <- rms_norm(residual, next_weight)     when next_weight is non-NULL (the next
+ *                                                   block's input norm; next [m][hidden]).
+ * Each norm has the bits of hyp_rms_normalize. hidden: a multiple of 64, at most 16384. */
+HypStatus hyp_residual_rms_norm(const void* branch, void* residual, const void* post_weight, const void* scalar,
+                                const void* next_weight, void* next, uint32_t m, uint32_t hidden, float eps,
+                                HypStream stream);
+
+/* ---- the model, its KV state and the step ABI (hyperion_mlx.h:50-248) -------------------
+ * The reference's model-level entry points over this library's kernels: hyp_model_load
+ * makes the projections, norm vectors and layer scalars resident; hyp_prefill_chunk and
+ * hyp_decode_block run embed -> layers -> final norm -> softcap LM head -> greedy sample
+ * on the device (ForwardPass::forward, forward.cc:543-563; model.cc:515-740). The types
+ * below have the reference's names and layouts. Each call is synchronous and runs on the
+ * model's own HIP stream; one thread drives a model and its states. Differences: no
+ * governor (governor_state is always READY and peak/active bytes are 0; every cache is
+ * allocated at its final size by hyp_kvstate_create, so there is nothing to admit),
+ * token ids >= vocab_size are rejected, and sampling with temperature > 0 is UNSUPPORTED. */
+typedef struct HypModelOpaque* HypModel;             /* magic "HPMD" */
+typedef struct HypKvStateOpaque* HypKvState;         /* magic "HPKS" */
+typedef struct HypStepResultOpaque* HypStepResult;   /* magic "HPSR" */
+
+typedef enum HypTextModelType { HYP_GEMMA4_TEXT = 0, HYP_GEMMA4_UNIFIED_TEXT = 1 } HypTextModelType;
+typedef enum HypLayerType { HYP_LAYER_SLIDING = 0, HYP_LAYER_FULL = 1 } HypLayerType;
+typedef enum HypGovernorState {
+    HYP_GOVERNOR_READY = 0,
+    HYP_GOVERNOR_SOFT_PAUSED = 1,
+    HYP_GOVERNOR_HARD_REJECT = 2
+} HypGovernorState;
+
+/* hyperion_mlx.h:75-80. */
+typedef struct HypRopeSpec {
+    double theta;
+    int has_partial_rotary_factor;
+    float partial_rotary_factor;
+    int proportional;
+} HypRopeSpec;
+
+typedef struct HypMoeConfig {
+    uint32_t num_experts;
+    uint32_t top_k;
+    uint32_t moe_intermediate_size;
+} HypMoeConfig;
+
+/* hyperion_mlx.h:89-116, validated as Geometry::validate does (geometry.cc:78-130). */
+typedef struct HypGeometryParams {
+    HypTextModelType model_type;
+    uint32_t hidden_size;
+    uint32_t intermediate_size;
+    uint32_t num_hidden_layers;
+    const HypLayerType* layer_types;
+    uint32_t num_attention_heads;
+    uint32_t head_dim_local;
+    uint32_t head_dim_global;
+    uint32_t num_kv_heads_local;
+    uint32_t num_kv_heads_global;
+    int attention_k_eq_v_global;
+    uint32_t num_kv_shared_layers;
+    uint32_t sliding_window;
+    HypRopeSpec rope_local;
+    HypRopeSpec rope_global;
+    float final_logit_softcapping;
+    float rms_norm_eps;
+    int attention_bias;
+    uint32_t vocab_size;
+    uint32_t max_position_embeddings;
+    int tie_word_embeddings;
+    uint32_t ple_hidden_per_layer_input;
+    uint32_t ple_vocab_per_layer_input;
+    int use_double_wide_mlp;
+    int has_moe;
+    HypMoeConfig moe;
+} HypGeometryParams;
+
+/* hyperion_mlx.h:119-123. */
+typedef struct HypTokenStream {
+    const uint32_t* tokens;
+    uint32_t count;
+    int is_prompt;
+} HypTokenStream;
+
+/* hyperion_mlx.h:134-140. */
+typedef struct HypSamplingConfig {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    uint64_t seed;
+} HypSamplingConfig;
+
+/* hyperion_mlx.h:157-176. */
+typedef struct {
+    uint32_t token_id;
+    float logit;
+    uint64_t peak_mlx_bytes;
+    uint64_t active_mlx_bytes;
+    uint64_t phys_footprint_bytes;
+    uint64_t local_kv_bytes;
+    uint64_t global_kv_bytes;
+    float local_kv_eval_ms;
+    float global_kv_eval_ms;
+    HypGovernorState governor_state;
+    uint32_t near_tie_events;
+    uint32_t top_k_logprob_count;
+    uint32_t top_k_logprob_ids[HYP_TOP_K_LOGPROBS];
+    float top_k_logprob_values[HYP_TOP_K_LOGPROBS];
+} HypStepResultFields;
+
+HypStatus hyp_model_create(HypModel* out_model);
+HypStatus hyp_model_free(HypModel* model);
+/* Load the artifact in weights_path (the hyp_qmodel_load rules, plus the norm vectors
+ * input_layernorm, post_attention_layernorm, pre_feedforward_layernorm,
+ * post_feedforward_layernorm, self_attn.q_norm, self_attn.k_norm, layer_scalar and the
+ * final language_model.model.norm) for `geometry`, on the current device. A loaded model
+ * rejects a second load; a missing directory is NOT_FOUND. */
+HypStatus hyp_model_load(HypModel model, const HypGeometryParams* geometry, const char* weights_path);
+/* One LocalKvCache ring of sliding_window + 2048 positions per sliding layer and one
+ * GlobalKvCache of max_position_embeddings positions per global layer (kv.cc). */
+HypStatus hyp_kvstate_create(HypModel model, HypKvState* out_kvstate);
+HypStatus hyp_kvstate_free(HypKvState* kvstate);
+/* Prefill a fresh state with tokens->count tokens in 2048-token chunks; the result holds
+ * the greedy token after the last one (top_k_logprob_count 0). */
+HypStatus hyp_prefill_chunk(HypModel model, HypKvState kvstate, const HypTokenStream* tokens,
+                            HypStepResult out_result);
+/* n_tokens greedy steps from the state's last token; the result holds the last step's
+ * token and the number of steps whose top-2 gap was < 0.5. */
+HypStatus hyp_decode_block(HypModel model, HypKvState kvstate, uint32_t n_tokens, HypStepResult out_result);
+/* The same with a sampling config: NULL or temperature 0 is the greedy path plus the
+ * top-k sidecar (near_tie_events 0, as model.cc:262-288 reports it); temperature > 0 is
+ * UNSUPPORTED; a malformed config is INVALID_ARGUMENT (model.cc:234-257). */
+HypStatus hyp_prefill_chunk_sampled(HypModel model, HypKvState kvstate, const HypTokenStream* tokens,
+                                    const HypSamplingConfig* config, HypStepResult out_result);
+HypStatus hyp_decode_block_sampled(HypModel model, HypKvState kvstate, uint32_t n_tokens,
+                                   const HypSamplingConfig* config, HypStepResult out_result);
+HypStatus hyp_step_result_create(HypStepResult* out_result);
+HypStatus hyp_step_result_free(HypStepResult* result);
+HypStatus hyp_step_result_fields(HypStepResult result, HypStepResultFields* out_fields);
+/* ForwardPass::embed + forward (forward.cc:126-131, 543-563) as forward_test.cc drives it:
+ * `count` host token ids at positions offset .. offset + count - 1, their K/V appended to
+ * the state's caches, and the final-normalised hidden rows copied to hidden_out (host, bf16
+ * [count][hidden_size]). The state's cursor does not move. */
+HypStatus hyp_model_forward_hidden(HypModel model, HypKvState kvstate, const uint32_t* ids, uint32_t count,
+                                   uint32_t offset, uint16_t* hidden_out);
+
 /* ---- decode-step program (the per-token layer loop, forward.cc:558-563, run by
  *      hyp_decode_block, model.cc:703-718) ------------------------------------------ */
 

@@ -260,3 +260,141 @@ def attention_f64(q, k, v, cache_k, cache_v, offset: int, prefix_len: int, windo
     out = np.zeros((L, H, D), np.float64)
     lib().orc_attention_f64(_p(q), _p(k), _p(v), _p(ck), _p(cv), cap, L, H, KVH, D, offset, prefix_len, window, _p(out))
     return out
+
+
+def add_bf16(a, b) -> np.ndarray:
+    """mx::add of two bf16 arrays: the fp32 sum rounded to bf16."""
+    return bf16_from_f32(f32_from_bf16(a) + f32_from_bf16(b))
+
+
+def mul_bf16(a, b) -> np.ndarray:
+    """mx::multiply of two bf16 arrays (b broadcast): the fp32 product rounded to bf16."""
+    return bf16_from_f32(f32_from_bf16(a) * f32_from_bf16(b))
+
+
+class DecoderOracle:
+    """ForwardPass (native/hyperion_mlx/src/forward.cc) restated over this module's pinned
+    primitives, every MLX op's bf16 result rounded where the reference's graph rounds it:
+
+      embed           forward.cc:126-131   dequantize (double rounding) x bf16(sqrt(hidden))
+      decoder_layer   forward.cc:509-541   the sandwich norms, the residual adds, layer_scalar
+      attention       forward.cc:376-508   q/k/v projections (fp64 products rounded to bf16),
+                                           q_norm/k_norm (weighted), v_norm (weightless, of
+                                           k_raw on K = V layers), RoPE on q and k, SDPA at
+                                           scale 1 over the cached prefix and the chunk
+                                           (attention_f64, rounded to bf16), o_proj
+      mlp             forward.cc:338-343   gate/up, the GELU chain times up, down
+      forward         forward.cc:543-563   every layer at one offset, then final_norm
+      lm_head/epilogue forward.cc:137-189, model.cc:215-228: tied head, softcap, greedy
+
+    `tensors` maps the artifact's mlx-lm names to arrays (uint32 codes, bf16 bits as
+    uint16). Caches are linear per layer (position p in row p); the masks alone bound a
+    sliding layer's window, which is what the reference's ring read returns.
+
+    weights="exact" multiplies by the exactly dequantized weights at every size;
+    weights="per_m" follows the device path's documented weight semantics - exact below
+    five rows (the decode kernel), each weight rounded once to bf16 from five rows on (the
+    prefill GEMM) - so that a comparison with the device isolates everything else.
+    """
+
+    PREFIX = "language_model.model."
+
+    def __init__(self, tensors: dict, text_config: dict, weights: str = "exact"):
+        assert weights in ("exact", "per_m")
+        self.weights = weights
+        t = text_config
+        self.T = tensors
+        self.hidden = t["hidden_size"]
+        self.heads = t["num_attention_heads"]
+        self.kinds = ["sliding" if k == "sliding_attention" else "full" for k in t["layer_types"]]
+        self.d_local, self.d_global = t["head_dim"], t.get("global_head_dim", t["head_dim"])
+        self.kv_local = t["num_key_value_heads"]
+        self.kv_global = t.get("num_global_key_value_heads", self.kv_local)
+        self.window = t["sliding_window"]
+        rp = t["rope_parameters"]
+        self.theta_local = rp["sliding_attention"]["rope_theta"]
+        self.theta_global = rp["full_attention"]["rope_theta"]
+        prf = np.float32(rp["full_attention"].get("partial_rotary_factor", 1.0))
+        rotated = int(np.float32(prf * np.float32(self.d_global)))   # rope.cc:44-49
+        self.rotated_global = rotated - rotated % 2
+        self.eps = t["rms_norm_eps"]
+        self.softcap_cap = t["final_logit_softcapping"]
+        self.vocab = t["vocab_size"]
+        self.max_pos = t["max_position_embeddings"]
+        self.caches = []
+        for kind in self.kinds:
+            d, kvh = (self.d_local, self.kv_local) if kind == "sliding" else (self.d_global, self.kv_global)
+            self.caches.append((np.zeros((self.max_pos, kvh, d), np.uint16), np.zeros((self.max_pos, kvh, d), np.uint16)))
+
+    def _t(self, name):
+        return self.T[self.PREFIX + name]
+
+    def _proj(self, x, base):
+        wq, s, b = (self._t(base + suffix) for suffix in (".weight", ".scales", ".biases"))
+        if self.weights == "per_m" and x.shape[0] > 4:
+            return bf16_from_f32(qmatmul_deq_f64(x, wq, s, b, mode=1).astype(np.float32))
+        return bf16_from_f32(qmatmul_f64(x, wq, s, b).astype(np.float32))
+
+    def embed(self, ids):
+        base = "embed_tokens"
+        rows = dequantize(self._t(base + ".weight"), self._t(base + ".scales"), self._t(base + ".biases"),
+                          rows=np.asarray(ids, np.uint32), mode=0)
+        return scale(rows, float(np.sqrt(np.float32(self.hidden))))
+
+    def layer(self, x, i, offset):
+        L = x.shape[0]
+        pre = f"layers.{i}."
+        sliding = self.kinds[i] == "sliding"
+        d, kvh = (self.d_local, self.kv_local) if sliding else (self.d_global, self.kv_global)
+        rotated = d if sliding else self.rotated_global
+        theta = self.theta_local if sliding else self.theta_global
+        h = rms_norm(x, self._t(pre + "input_layernorm.weight"), self.eps)
+        q = self._proj(h, pre + "self_attn.q_proj")
+        k_raw = self._proj(h, pre + "self_attn.k_proj")
+        v_raw = self._proj(h, pre + "self_attn.v_proj") if sliding else k_raw
+        q = rms_norm(q.reshape(L * self.heads, d), self._t(pre + "self_attn.q_norm.weight"), self.eps)
+        k = rms_norm(k_raw.reshape(L * kvh, d), self._t(pre + "self_attn.k_norm.weight"), self.eps)
+        v = rms_norm(v_raw.reshape(L * kvh, d), None, self.eps).reshape(L, kvh, d)
+        q = rope(q, L, self.heads, d, rotated, theta, offset)
+        k = rope(k, L, kvh, d, rotated, theta, offset)
+        ck, cv = self.caches[i]
+        prefix = min(self.window, offset) if sliding else offset
+        att = attention_f64(q, k, v, ck, cv, offset, prefix, self.window if sliding else 0)
+        ck[offset:offset + L] = k
+        cv[offset:offset + L] = v
+        att = bf16_from_f32(att.astype(np.float32)).reshape(L, self.heads * d)
+        o = self._proj(att, pre + "self_attn.o_proj")
+        x = add_bf16(x, rms_norm(o, self._t(pre + "post_attention_layernorm.weight"), self.eps))
+        h = rms_norm(x, self._t(pre + "pre_feedforward_layernorm.weight"), self.eps)
+        gu = gelu_tanh_mul(self._proj(h, pre + "mlp.gate_proj"), self._proj(h, pre + "mlp.up_proj"))
+        dn = self._proj(gu, pre + "mlp.down_proj")
+        x = add_bf16(x, rms_norm(dn, self._t(pre + "post_feedforward_layernorm.weight"), self.eps))
+        return mul_bf16(x, self._t(pre + "layer_scalar"))
+
+    def forward(self, ids, offset: int):
+        """Final-normalised hidden rows [L, hidden] (bf16 bits); appends the K/V."""
+        x = self.embed(ids)
+        for i in range(len(self.kinds)):
+            x = self.layer(x, i, offset)
+        return rms_norm(x, self._t("norm.weight"), self.eps)
+
+    def logits(self, last_row):
+        """Tied LM head + softcap of one final-normalised row (bf16 bits [vocab])."""
+        return softcap(self._proj(last_row.reshape(1, -1), "embed_tokens"), self.softcap_cap).reshape(-1)
+
+    def greedy(self, ids, n_decode: int):
+        """hyp_prefill_chunk then n_decode single-token steps: [(token, logit, top1 - top2)]."""
+        steps = []
+        h = self.forward(ids, 0)
+        pos = len(ids)
+        for j in range(n_decode + 1):
+            lg = self.logits(h[-1])
+            f = f32_from_bf16(lg).astype(np.float64)
+            order = np.argsort(-f, kind="stable")
+            tok = int(order[0])
+            steps.append((tok, float(f[tok]), float(f[order[0]] - f[order[1]]) if f.size > 1 else np.inf))
+            if j == n_decode:
+                break
+            h = self.forward([tok], pos)
+            pos += 1
+        return steps

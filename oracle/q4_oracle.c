@@ -139,6 +139,9 @@ void orc_dequantize_q4g64(const uint32_t* wq, const uint16_t* scales, const uint
 void orc_qmatmul_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                      const uint16_t* biases, int64_t m, int64_t n, int64_t k, double* y) {
     const int64_t groups = k / GROUP;
+    /* Each output is one thread's sequential sum: the result does not depend on the
+     * thread count. */
+#pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < n; ++r) {
         const uint32_t* wr = wq + r * (k / 8);
         for (int64_t i = 0; i < m; ++i) {
@@ -160,26 +163,27 @@ void orc_qmatmul_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scal
 void orc_qmatmul_deq_f64(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                          const uint16_t* biases, int64_t m, int64_t n, int64_t k, int mode,
                          double* y) {
-    double* row = (double*)malloc((size_t)k * sizeof(double));
-    uint16_t* deq = (uint16_t*)malloc((size_t)k * sizeof(uint16_t));
-    if (row == NULL || deq == NULL) {
+    /* Rows in parallel; each output is one thread's sequential sum (thread-count independent). */
+#pragma omp parallel
+    {
+        double* row = (double*)malloc((size_t)k * sizeof(double));
+        uint16_t* deq = (uint16_t*)malloc((size_t)k * sizeof(uint16_t));
+        if (row == NULL || deq == NULL) abort();   /* a checker must not return partial output */
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n; ++r) {
+            const uint32_t id = (uint32_t)r;
+            orc_dequantize_q4g64(wq, scales, biases, &id, 1, k, mode, deq);
+            for (int64_t kk = 0; kk < k; ++kk) row[kk] = orc_f32_from_bf16(deq[kk]);
+            for (int64_t i = 0; i < m; ++i) {
+                const uint16_t* xr = x + i * k;
+                double acc = 0.0;
+                for (int64_t kk = 0; kk < k; ++kk) acc += (double)orc_f32_from_bf16(xr[kk]) * row[kk];
+                y[i * n + r] = acc;
+            }
+        }
         free(row);
         free(deq);
-        return;
     }
-    for (int64_t r = 0; r < n; ++r) {
-        const uint32_t id = (uint32_t)r;
-        orc_dequantize_q4g64(wq, scales, biases, &id, 1, k, mode, deq);
-        for (int64_t kk = 0; kk < k; ++kk) row[kk] = orc_f32_from_bf16(deq[kk]);
-        for (int64_t i = 0; i < m; ++i) {
-            const uint16_t* xr = x + i * k;
-            double acc = 0.0;
-            for (int64_t kk = 0; kk < k; ++kk) acc += (double)orc_f32_from_bf16(xr[kk]) * row[kk];
-            y[i * n + r] = acc;
-        }
-    }
-    free(row);
-    free(deq);
 }
 
 void orc_qmatmul_f32_grouped(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

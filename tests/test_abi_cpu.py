@@ -212,3 +212,129 @@ def test_step_program_create_rejects_bad_arguments_before_the_device():
     assert _status("hyp_step_program_free", None) == 1
     h = ctypes.c_void_p()
     assert _status("hyp_step_program_free", ctypes.byref(h)) == 0
+
+
+# ---- the model-level ABI (hyperion_mlx.h:50-248) -------------------------------------------
+
+REF_HEADER = "/root/reference/native/hyperion_mlx/include/hyperion_mlx.h"
+MODEL_STRUCTS = {
+    "HypRopeSpec": ["theta", "has_partial_rotary_factor", "partial_rotary_factor", "proportional"],
+    "HypGeometryParams": ["model_type", "hidden_size", "intermediate_size", "num_hidden_layers", "layer_types",
+                          "num_attention_heads", "head_dim_local", "head_dim_global", "num_kv_heads_local",
+                          "num_kv_heads_global", "attention_k_eq_v_global", "num_kv_shared_layers", "sliding_window",
+                          "rope_local", "rope_global", "final_logit_softcapping", "rms_norm_eps", "attention_bias",
+                          "vocab_size", "max_position_embeddings", "tie_word_embeddings",
+                          "ple_hidden_per_layer_input", "ple_vocab_per_layer_input", "use_double_wide_mlp", "has_moe",
+                          "moe"],
+    "HypTokenStream": ["tokens", "count", "is_prompt"],
+    "HypSamplingConfig": ["temperature", "top_k", "top_p", "min_p", "seed"],
+    "HypStepResultFields": ["token_id", "logit", "peak_mlx_bytes", "active_mlx_bytes", "phys_footprint_bytes",
+                            "local_kv_bytes", "global_kv_bytes", "local_kv_eval_ms", "global_kv_eval_ms",
+                            "governor_state", "near_tie_events", "top_k_logprob_count", "top_k_logprob_ids",
+                            "top_k_logprob_values"],
+}
+
+
+def _layout(header_dir, include):
+    """sizeof and every field offset of the model-level structs, compiled with gcc."""
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{include}"', 'int main(void) {']
+    for s, fields in MODEL_STRUCTS.items():
+        lines.append(f'printf("{s} %zu\\n", sizeof({s}));')
+        for f in fields:
+            lines.append(f'printf("{s}.{f} %zu\\n", offsetof({s}, {f}));')
+    lines.append('return 0; }')
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        exe = os.path.join(d, "layout")
+        r = subprocess.run(["gcc", "-std=c11", "-I", header_dir, "-x", "c", "-", "-o", exe], input="\n".join(lines),
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    return dict(line.rsplit(" ", 1) for line in out.split("\n") if line)
+
+
+def test_model_structs_match_the_binding():
+    got = _layout(os.path.dirname(HEADER), "hyperion_hip.h")
+    py = {"HypRopeSpec": hy.RopeSpec, "HypGeometryParams": hy.GeometryParams, "HypTokenStream": hy.TokenStream,
+          "HypSamplingConfig": hy.SamplingConfig, "HypStepResultFields": hy.StepResultFields}
+    for s, cls in py.items():
+        assert int(got[s]) == ctypes.sizeof(cls), s
+        for f in MODEL_STRUCTS[s]:
+            assert int(got[f"{s}.{f}"]) == getattr(cls, f).offset, f"{s}.{f}"
+
+
+@pytest.mark.skipif(not os.path.exists(REF_HEADER), reason="the reference's header is not present")
+def test_model_structs_match_the_reference_header():
+    """The drop-in claim: the same sizes and field offsets as hyperion_mlx.h."""
+    mine = _layout(os.path.dirname(HEADER), "hyperion_hip.h")
+    ref = _layout(os.path.dirname(REF_HEADER), "hyperion_mlx.h")
+    assert mine == ref
+
+
+def _tiny_geometry(fixture_dir, **overrides):
+    with open(os.path.join(fixture_dir, "config.json")) as f:
+        cfg = json.load(f)
+    g, types = hy.geometry_from_config(cfg)
+    for k, v in overrides.items():
+        setattr(g, k, v)
+    return g, types
+
+
+def test_model_lifecycle_and_validation_before_the_device(fixture_dir, tmp_path):
+    m = ctypes.c_void_p()
+    assert _status("hyp_model_create", None) == 1
+    assert _status("hyp_model_create", ctypes.byref(m)) == 0
+    g, types = _tiny_geometry(fixture_dir)
+    assert _status("hyp_model_load", m, None, fixture_dir.encode()) == 1
+    assert _status("hyp_model_load", m, ctypes.byref(g), None) == 1
+    # Geometry::validate (geometry.cc:78-130) before any file or device access
+    bad_types = (ctypes.c_int * 6)(*([hy.LAYER_SLIDING] * 6))
+    g2, _ = _tiny_geometry(fixture_dir)
+    g2.layer_types = ctypes.cast(bad_types, ctypes.POINTER(ctypes.c_int))
+    assert _status("hyp_model_load", m, ctypes.byref(g2), fixture_dir.encode()) == 1
+    assert "full_attention" in hy.last_error()
+    for field, value, status in (("sliding_window", 0, 1), ("vocab_size", 0, 1), ("tie_word_embeddings", 0, 1),
+                                 ("has_moe", 1, 1), ("use_double_wide_mlp", 1, 5), ("attention_bias", 1, 5),
+                                 ("head_dim_local", 96, 5), ("num_kv_shared_layers", 2, 5)):
+        gb, _ = _tiny_geometry(fixture_dir, **{field: value})
+        assert _status("hyp_model_load", m, ctypes.byref(gb), fixture_dir.encode()) == status, field
+    gm, _ = _tiny_geometry(fixture_dir, has_moe=1)
+    gm.moe = hy.MoeConfig(4, 2, 64)
+    assert _status("hyp_model_load", m, ctypes.byref(gm), fixture_dir.encode()) == 5
+    # the artifact: missing directory, too few layers
+    assert _status("hyp_model_load", m, ctypes.byref(g), str(tmp_path / "nope").encode()) == 2
+    types7 = (ctypes.c_int * 7)(*([hy.LAYER_SLIDING] * 6 + [hy.LAYER_FULL]))
+    g7, _ = _tiny_geometry(fixture_dir)
+    g7.num_hidden_layers = 7
+    g7.layer_types = ctypes.cast(types7, ctypes.POINTER(ctypes.c_int))
+    assert _status("hyp_model_load", m, ctypes.byref(g7), fixture_dir.encode()) == 1
+    # a valid load reaches the device check last
+    st = _status("hyp_model_load", m, ctypes.byref(g), fixture_dir.encode())
+    assert st in (0, 5)
+    if st == 5:
+        kv = ctypes.c_void_p()
+        assert _status("hyp_kvstate_create", m, ctypes.byref(kv)) == 1
+        assert "not loaded" in hy.last_error()
+    assert _status("hyp_model_free", ctypes.byref(m)) == 0 and not m.value
+    assert _status("hyp_model_free", ctypes.byref(m)) == 0
+
+
+def test_step_result_lifecycle():
+    r = ctypes.c_void_p()
+    assert _status("hyp_step_result_create", ctypes.byref(r)) == 0
+    f = hy.StepResultFields()
+    f.token_id = 99
+    assert _status("hyp_step_result_fields", r, ctypes.byref(f)) == 0
+    assert f.token_id == 0 and f.top_k_logprob_count == 0
+    assert _status("hyp_step_result_fields", r, None) == 1
+    assert _status("hyp_step_result_fields", None, ctypes.byref(f)) == 1
+    # a handle of another type is refused by magic
+    m = ctypes.c_void_p()
+    assert _status("hyp_model_create", ctypes.byref(m)) == 0
+    assert _status("hyp_step_result_fields", m, ctypes.byref(f)) == 1
+    assert _status("hyp_step_result_free", ctypes.byref(m)) == 1
+    assert _status("hyp_model_free", ctypes.byref(m)) == 0
+    assert _status("hyp_step_result_free", ctypes.byref(r)) == 0 and not r.value
+    ts = hy.TokenStream(None, 0, 1)
+    assert _status("hyp_prefill_chunk", None, None, ctypes.byref(ts), None) == 1
+    assert _status("hyp_decode_block", None, None, 1, None) == 1

@@ -828,3 +828,115 @@ def test_attention_oracle_closed_forms():
     ones = np.full((L, KVH, D), 0x3F80, np.uint16)
     out = O.attention_f64(q, k, ones, ck, np.full((cap, KVH, D), 0x3F80, np.uint16), 9, 9, 5)
     np.testing.assert_allclose(out, 1.0, rtol=1e-12)
+
+
+# ---- the decoder restatement (DecoderOracle) ---------------------------------------------
+
+def _tiny_dims_model(tmp_path, seed=3, layer_types=None):
+    import json
+    cfg = {
+        "model_type": "gemma4_unified_text", "hidden_size": 128, "intermediate_size": 256,
+        "layer_types": layer_types or ["sliding_attention"] * 2 + ["full_attention"], "num_attention_heads": 4,
+        "head_dim": 64, "global_head_dim": 128, "num_key_value_heads": 2, "num_global_key_value_heads": 1,
+        "attention_k_eq_v": True, "sliding_window": 8,
+        "rope_parameters": {"sliding_attention": {"rope_theta": 10000.0},
+                            "full_attention": {"rope_theta": 1e6, "partial_rotary_factor": 0.25,
+                                               "rope_type": "proportional"}},
+        "final_logit_softcapping": 30.0, "rms_norm_eps": 1e-6, "vocab_size": 64, "max_position_embeddings": 64,
+    }
+    cfg["num_hidden_layers"] = len(cfg["layer_types"])
+    T = syn.write_model(str(tmp_path), cfg, seed)
+    return dict(T), json.loads(json.dumps(cfg))
+
+
+def _zero_proj(T, base):
+    T[base + ".weight"] = np.zeros_like(T[base + ".weight"])
+    T[base + ".scales"] = np.zeros_like(T[base + ".scales"])
+    T[base + ".biases"] = np.zeros_like(T[base + ".biases"])
+
+
+def test_decoder_oracle_residual_wiring_closed_form(tmp_path):
+    """With every o_proj and down_proj zero, each branch's rms_norm of a zero row is zero
+    (0 * 1/sqrt(eps)), so the residual stream is the embedding times the layer scalars,
+    rounded after each product (forward.cc:518-539), and the output its final norm."""
+    T, cfg = _tiny_dims_model(tmp_path)
+    P = "language_model.model."
+    for i in range(cfg["num_hidden_layers"]):
+        _zero_proj(T, f"{P}layers.{i}.self_attn.o_proj")
+        _zero_proj(T, f"{P}layers.{i}.mlp.down_proj")
+    ids = [3, 17, 60, 0, 41]
+    got = O.DecoderOracle(T, cfg).forward(ids, 0)
+    # closed form, numpy only: dequantized rows (double rounding, as the embed oracle),
+    # times bf16(sqrt(128)), times each bf16 scalar, then the weighted RMS norm in fp64.
+    e = P + "embed_tokens"
+    codes = syn.unpack_codes(T[e + ".weight"][ids]).astype(np.float32)
+    s = np.repeat(syn.bf16_to_f32(T[e + ".scales"][ids]), 64, axis=1)
+    b = np.repeat(syn.bf16_to_f32(T[e + ".biases"][ids]), 64, axis=1)
+    x = syn.bf16_to_f32(syn.bf16_bits(syn.bf16_to_f32(syn.bf16_bits(s * codes)) + b))
+    x = syn.bf16_to_f32(syn.bf16_bits(x * syn.bf16_to_f32(syn.bf16_bits(np.float32(np.sqrt(np.float32(128)))))))
+    for i in range(cfg["num_hidden_layers"]):
+        x = syn.bf16_to_f32(syn.bf16_bits(x * syn.bf16_to_f32(T[f"{P}layers.{i}.layer_scalar"])[0]))
+    xd = x.astype(np.float64)
+    inv = 1.0 / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-6)
+    ref = syn.bf16_to_f32(T[P + "norm.weight"]).astype(np.float64) * syn.bf16_to_f32(syn.bf16_bits(
+        (xd * inv).astype(np.float32))).astype(np.float64)
+    # the norm's fp32 statistics against fp64: within one bf16 rounding of each product
+    np.testing.assert_allclose(syn.bf16_to_f32(got), ref, rtol=2 ** -7, atol=0)
+
+
+def test_decoder_oracle_single_token_attention_is_v(tmp_path):
+    """At offset 0 a single token's only visible key is itself, so SDPA returns V: the layer
+    must equal the same layer with the attention replaced by V = v_norm(v_proj(x)) on
+    sliding layers and v_norm(k_proj(x)) on global (K = V) layers, kv head h // G for query
+    head h (forward.cc:403-412, :497-505). q, k, RoPE and the scores drop out."""
+    T, cfg = _tiny_dims_model(tmp_path, seed=4)
+    P = "language_model.model."
+    D = O.DecoderOracle(T, cfg)
+    x = D.embed([9])
+    for i, kind in enumerate(D.kinds):
+        got = D.layer(x.copy(), i, 0)
+        pre = f"layers.{i}."
+        sliding = kind == "sliding"
+        d, kvh = (D.d_local, D.kv_local) if sliding else (D.d_global, D.kv_global)
+        h = O.rms_norm(x, T[P + pre + "input_layernorm.weight"])
+        src = "self_attn.v_proj" if sliding else "self_attn.k_proj"
+        raw = D._proj(h, pre + src).reshape(kvh, d)
+        v = O.rms_norm(raw, None)
+        att = v[np.arange(D.heads) // (D.heads // kvh)].reshape(1, -1)
+        o = D._proj(att, pre + "self_attn.o_proj")
+        y = O.add_bf16(x, O.rms_norm(o, T[P + pre + "post_attention_layernorm.weight"]))
+        hh = O.rms_norm(y, T[P + pre + "pre_feedforward_layernorm.weight"])
+        gu = O.gelu_tanh_mul(D._proj(hh, pre + "mlp.gate_proj"), D._proj(hh, pre + "mlp.up_proj"))
+        dn = D._proj(gu, pre + "mlp.down_proj")
+        y = O.add_bf16(y, O.rms_norm(dn, T[P + pre + "post_feedforward_layernorm.weight"]))
+        y = O.mul_bf16(y, T[P + pre + "layer_scalar"])
+        np.testing.assert_array_equal(got, y, err_msg=f"layer {i} ({kind})")
+        x = got
+
+
+def test_decoder_oracle_chunking_invariance(tmp_path):
+    """Prefix then continuation equals one shot, bit for bit (the invariant of
+    forward_test.cc:412-482, exact here because every op of the oracle is row-wise): the
+    caches, positions, prefix lengths and windows are threaded consistently; the window (8)
+    is crossed."""
+    T, cfg = _tiny_dims_model(tmp_path, seed=5)
+    ids = [(7 * i + 3) % 64 for i in range(21)]
+    whole = O.DecoderOracle(T, cfg).forward(ids, 0)
+    D = O.DecoderOracle(T, cfg)
+    parts = [D.forward(ids[:12], 0), D.forward(ids[12:13], 12), D.forward(ids[13:], 13)]
+    np.testing.assert_array_equal(np.concatenate(parts), whole)
+
+
+def test_decoder_oracle_window_hides_old_tokens(tmp_path):
+    """On a sliding layer (window 8) a token 8 or more positions before the query is
+    invisible to it (build_mask, forward.cc:365-371), while one inside the window is seen."""
+    T, cfg = _tiny_dims_model(tmp_path, seed=6, layer_types=["sliding_attention", "full_attention"])
+    D = O.DecoderOracle(T, cfg)
+    a = [(5 * i + 1) % 64 for i in range(12)]
+    b = list(a)
+    b[3] = (b[3] + 1) % 64          # position 3 < 11 - 8 + 1: outside the last query's window
+    xa, xb = D.embed(a), D.embed(b)
+    Da, Db = O.DecoderOracle(T, cfg), O.DecoderOracle(T, cfg)
+    ya, yb = Da.layer(xa, 0, 0), Db.layer(xb, 0, 0)
+    np.testing.assert_array_equal(ya[11], yb[11])
+    assert not np.array_equal(ya[4], yb[4])   # position 4 still sees position 3
