@@ -278,6 +278,76 @@ def bench_decode_stream(model, m, steps, warmup, stream):
     return out
 
 
+def artifact_dir(min_free_bytes):
+    """A scratch directory with room for a synthetic artifact (memory-backed if possible)."""
+    import shutil
+    import tempfile
+    for base in ("/dev/shm", tempfile.gettempdir()):
+        try:
+            if os.path.isdir(base) and shutil.disk_usage(base).free >= min_free_bytes:
+                return tempfile.mkdtemp(prefix="hyp_bench_", dir=base)
+        except OSError:
+            continue
+    return None
+
+
+def bench_model_decode(prompt_len, n_decode, layers):
+    """The product's model-level path on a synthetic 12B artifact (48 layers, tied LM head
+    [262144,3840], 6.6 GB of Q4/g64; the layers' codes are zero, their scales, biases, norms
+    and the embedding random, so every byte is still streamed): hyp_model_load,
+    hyp_prefill_chunk of a
+    prompt_len-token prompt (2048-token chunks), then hyp_decode_block of n_decode greedy
+    tokens in one call - embed, every layer's norms, q/k/v, RoPE, KV cache append,
+    attention over the cached context, o, MLP and residual sandwich, final norm, softcap
+    LM head and greedy sampling, all on the device, one host round trip per call."""
+    import shutil
+    cfg = syn.gemma4_text_config(num_layers=layers, max_positions=max(8192, prompt_len + n_decode + 16))
+    d = artifact_dir(8 << 30)
+    if d is None:
+        log("model decode: no scratch directory with 8 GB free; skipped")
+        return None
+    try:
+        t0 = time.time()
+        syn.write_model(d, cfg, seed=21, branch_gain=0.5, qk_gain=0.7, share_layers=True, zero_layer_codes=True)
+        t1 = time.time()
+        model = hy.Model(hy.geometry_from_config(cfg), d)
+        t2 = time.time()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    log(f"model decode: artifact written in {t1 - t0:.1f} s, loaded in {t2 - t1:.1f} s")
+    prompt = np.random.default_rng(22).integers(0, cfg["vocab_size"], size=prompt_len).astype(np.uint32)
+    res = hy.StepResult()
+    warm = model.kvstate()
+    warm.prefill(prompt[:64], res)
+    warm.decode(4, res)
+    warm.close()
+    st = model.kvstate()
+    t0 = time.perf_counter()
+    st.prefill(prompt, res)
+    prefill_s = time.perf_counter() - t0
+    st.decode(2, res)
+    t0 = time.perf_counter()
+    f = st.decode(n_decode, res)
+    decode_s = time.perf_counter() - t0
+    st.close()
+    res.close()
+    model.close()
+    n_global = cfg["layer_types"].count("full_attention")
+    sl = ((4096, 3840), (2048, 3840), (2048, 3840), (3840, 4096), (15360, 3840), (15360, 3840), (3840, 15360))
+    gl = ((8192, 3840), (512, 3840), (3840, 8192), (15360, 3840), (15360, 3840), (3840, 15360))
+    weight_bytes = (layers - n_global) * sum(q4_bytes(n, k) for n, k in sl) + \
+        n_global * sum(q4_bytes(n, k) for n, k in gl) + q4_bytes(syn.VOCAB, HIDDEN)
+    ms = decode_s * 1e3 / n_decode
+    out = {"layers": layers, "prompt_tokens": prompt_len, "decode_tokens": n_decode,
+           "prefill_tokens_per_s": round(prompt_len / prefill_s, 1), "prefill_s": round(prefill_s, 4),
+           "decode_ms_per_token": round(ms, 4), "decode_tokens_per_s": round(1e3 / ms, 1),
+           "weight_bytes": weight_bytes, "weight_stream_gbs": round(weight_bytes / ms / 1e6, 1),
+           "last_token": int(f.token_id)}
+    log(f"model decode: prefill {prompt_len} tokens {prefill_s * 1e3:.1f} ms ({out['prefill_tokens_per_s']:.0f} tok/s); "
+        f"decode {ms:.3f} ms/token = {out['decode_tokens_per_s']:.0f} tok/s from context {prompt_len + 2}")
+    return out
+
+
 def bench_sample(stream, steps, warmup):
     """hyp_sample_greedy and hyp_sample_greedy_topk (the greedy epilogue with its top-8
     sidecar) on rows of vocab 262144 seeded logits N(0, 36): 10 calls captured in one graph,
@@ -374,6 +444,9 @@ def main():
     ap.add_argument("--only-sample", action="store_true", help="the headline decode GEMV and greedy sampling")
     ap.add_argument("--only-quantize", action="store_true", help="the headline decode GEMV and quantize/pack")
     ap.add_argument("--only-stream", action="store_true", help="the headline decode GEMV and the decode stream")
+    ap.add_argument("--only-model", action="store_true",
+                    help="the headline decode GEMV and the model-level prefill + decode")
+    ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the model-level run")
     ap.add_argument("--dense-ref", action="store_true",
                     help="also time hipBLASLt's dense bf16 GEMM (torch.matmul) on the prefill shapes")
     ap.add_argument("--dense-child", type=int, default=0, help=argparse.SUPPRESS)
@@ -414,6 +487,8 @@ def main():
         model = dc.DecodeModel(hy, args.layers, log)
         extra["decode_stream"] = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
+    elif args.only_model:
+        extra["model_decode"] = bench_model_decode(args.prompt, 32, args.layers)
     elif not args.only_decode:
         extra["quantize"] = bench_quantize(stream, 50, 5)
         extra["sample_greedy"] = bench_sample(stream, 20, 3)

@@ -51,7 +51,19 @@ struct AttnParams {
     float* part_ml;         // [splits][L * H][2]
     uint32_t L, H, KVH, G, cap, offset, prefix, window;
     uint32_t splits, keys_per_split;
+    const uint32_t* pos;    // non-null: offset = *pos, read on the device (graph replays)
 };
+
+// Graph-replay form: the position comes from device memory, the prefix and the split
+// length follow from it as the host computes them (prefix = min(window, offset) with a
+// window, offset without; keys split evenly in whole key blocks over the fixed grid).
+__device__ __forceinline__ void resolve_position(AttnParams& p) {
+    if (p.pos == nullptr) return;
+    p.offset = *p.pos;
+    p.prefix = p.window != 0u ? min(p.window, p.offset) : p.offset;
+    const uint32_t T = p.prefix + p.L;
+    p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
+}
 
 template <uint32_t D>
 struct AttnLds {
@@ -78,6 +90,7 @@ __device__ __forceinline__ const uint16_t* key_row(const AttnParams& p, const ui
 
 template <uint32_t D>
 __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
+    resolve_position(p);
     using Lds = AttnLds<D>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t tid = threadIdx.x;
@@ -240,26 +253,255 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
     }
 }
 
-// Merge the splits of each output row: weights 2^(m_s - max m), sum of l_s, divided sums.
-__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p, uint32_t D) {
-    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * kAttnThreads + threadIdx.x;
-    const uint64_t rows = static_cast<uint64_t>(p.L) * p.H;
-    if (e >= rows * D) return;
-    const uint64_t row = e / D;
-    float mx = -__builtin_huge_valf();
-    for (uint32_t s = 0; s < p.splits; ++s) mx = fmaxf(mx, p.part_ml[(s * rows + row) * 2u]);
-    float num = 0.0f;
-    float den = 0.0f;
-    if (mx > -__builtin_huge_valf()) {
-        for (uint32_t s = 0; s < p.splits; ++s) {
-            const float ms = p.part_ml[(s * rows + row) * 2u];
-            if (ms == -__builtin_huge_valf()) continue;
-            const float w = exp2f(ms - mx);
-            den += w * p.part_ml[(s * rows + row) * 2u + 1u];
-            num += w * p.part_o[s * rows * D + e];
+// Decode form (at most 16 query rows per kv head: L * G <= 16, a single MFMA row tile).
+// Each wave is an independent split of the keys, with nothing shared across waves:
+//  * Q stays in registers as the A operand of S = Q K^T for the whole kernel;
+//  * K rows load straight from memory into the B operand (lane (j, kb) holds key j's dims
+//    8kb .. 8kb + 7 of a 32-dim step: 16 contiguous bytes of the row);
+//  * V rows load coalesced and go through the wave's own LDS transposed ([d][32 keys]); a
+//    lane writes its 8 values in an order rotated by its lane index, which spreads the
+//    16-bit writes of a wave over the banks;
+//  * the online softmax, P in bf16 and the P.V products are those of attn_kernel.
+// Every split writes its unnormalised rows with (m, l); attn_combine_kernel merges them.
+template <uint32_t D>
+struct DecodeLds {
+    static constexpr uint32_t kVtRow = kKeyBlock * 2u + 16u;
+    static constexpr uint32_t kPRow = kKeyBlock * 2u + 16u;
+    static constexpr uint32_t kVt = 0;
+    static constexpr uint32_t kP = kVt + D * kVtRow;
+    static constexpr uint32_t kWave = kP + 16u * kPRow;
+    static constexpr uint32_t kWaves = D <= 256u ? 4u : 2u;
+    static constexpr uint32_t kBytes = kWaves * kWave;
+};
+
+template <uint32_t D>
+__global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel(AttnParams p) {
+    resolve_position(p);
+    using Lds = DecodeLds<D>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t split = blockIdx.x * Lds::kWaves + wave;
+    if (split >= p.splits) return;   // no workgroup barrier below: waves are independent
+    const uint32_t hk = blockIdx.y;
+    const uint32_t j16 = lane & 15u;
+    const uint32_t kb = lane >> 4;
+    const uint32_t rows = p.L * p.G;   // <= 16
+    const uint32_t T = p.prefix + p.L;
+    uint8_t* my = lds + wave * Lds::kWave;
+
+    constexpr uint32_t kSteps = D / 32u;
+    constexpr uint32_t kDTiles = D / 16u;
+    bf16x8_t qa[kSteps];
+    {
+        const bool valid = j16 < rows;
+        const uint32_t t = valid ? j16 / p.G : 0u;
+        const uint32_t h = hk * p.G + (j16 - t * p.G);
+        const uint16_t* src = p.q + (static_cast<size_t>(t) * p.H + h) * D + kb * 8u;
+#pragma unroll
+        for (uint32_t st = 0; st < kSteps; ++st) {
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (valid) v = *reinterpret_cast<const uint4*>(src + st * 32u);
+            qa[st] = __builtin_bit_cast(bf16x8_t, v);
         }
     }
-    p.out[e] = f32_to_bf16_bits(den > 0.0f ? num / den : 0.0f);
+    uint32_t j_begin = split * p.keys_per_split;
+    const uint32_t j_end = min(j_begin + p.keys_per_split, T);
+    if (p.window != 0u) {   // keys at positions > offset - window (the first token's bound)
+        const int64_t lo = static_cast<int64_t>(p.prefix) - p.window + 1;
+        if (lo > static_cast<int64_t>(j_begin)) j_begin = static_cast<uint32_t>(lo);
+    }
+
+    f32x4_t o[kDTiles];
+#pragma unroll
+    for (uint32_t t = 0; t < kDTiles; ++t) o[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[4], l[4];
+    int32_t qpos[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        m[i] = -__builtin_huge_valf();
+        l[i] = 0.0f;
+        const uint32_t r = 4u * kb + i;
+        qpos[i] = r < rows ? static_cast<int32_t>(p.offset + r / p.G) : -1;
+    }
+
+    // Per 16-key column tile c: K rows into the B operands, V rows (coalesced, lane cidx takes
+    // chunk cidx % (D/8) of key cidx / (D/8)) into registers, every load of the tile issued
+    // before its first use; with D <= 256 both tiles' loads are issued together.
+    constexpr uint32_t kChunks = D / 8u;
+    constexpr uint32_t kVPer = 16u * kChunks / 64u;   // V chunks per lane per 16-key tile
+    constexpr uint32_t kTilesUpFront = D <= 256u ? 2u : 1u;
+    for (uint32_t jb = j_begin; jb < j_end; jb += kKeyBlock) {
+        const uint32_t nk = min(kKeyBlock, j_end - jb);
+        f32x4_t sc[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+        for (uint32_t c0 = 0; c0 < 2u; c0 += kTilesUpFront) {
+            uint4 kr[kTilesUpFront][kSteps];
+            uint4 vr[kTilesUpFront][kVPer];
+#pragma unroll
+            for (uint32_t u = 0; u < kTilesUpFront; ++u) {
+                const uint32_t c = c0 + u;
+                const uint32_t key = 16u * c + j16;
+                const uint16_t* row = key < nk ? key_row(p, p.k, p.ck, jb + key, hk, D) + kb * 8u : nullptr;
+#pragma unroll
+                for (uint32_t st = 0; st < kSteps; ++st) {
+                    kr[u][st] = row != nullptr ? *reinterpret_cast<const uint4*>(row + st * 32u)
+                                               : make_uint4(0u, 0u, 0u, 0u);
+                }
+#pragma unroll
+                for (uint32_t it = 0; it < kVPer; ++it) {
+                    const uint32_t cidx = lane + 64u * it;
+                    const uint32_t r = 16u * c + cidx / kChunks;
+                    const uint32_t ch = cidx % kChunks;
+                    vr[u][it] = r < nk ? *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u)
+                                       : make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kTilesUpFront; ++u) {
+                const uint32_t c = c0 + u;
+                // V^T into LDS: 8 values per chunk in an order rotated by the lane.
+#pragma unroll
+                for (uint32_t it = 0; it < kVPer; ++it) {
+                    const uint32_t cidx = lane + 64u * it;
+                    const uint32_t r = 16u * c + cidx / kChunks;
+                    const uint32_t ch = cidx % kChunks;
+                    const uint4 vv = vr[u][it];
+                    uint8_t* col = my + Lds::kVt + (ch * 8u) * Lds::kVtRow + r * 2u;
+#pragma unroll
+                    for (uint32_t s2 = 0; s2 < 8u; ++s2) {
+                        const uint32_t e = (s2 + lane) & 7u;
+                        const uint32_t d01 = (e & 2u) ? vv.y : vv.x;
+                        const uint32_t d23 = (e & 2u) ? vv.w : vv.z;
+                        const uint32_t dw = (e & 4u) ? d23 : d01;
+                        *reinterpret_cast<uint16_t*>(col + e * Lds::kVtRow) =
+                            static_cast<uint16_t>((e & 1u) ? (dw >> 16) : (dw & 0xFFFFu));
+                    }
+                }
+                // S for this tile's 16 keys.
+#pragma unroll
+                for (uint32_t st = 0; st < kSteps; ++st) {
+                    sc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], __builtin_bit_cast(bf16x8_t, kr[u][st]),
+                                                                    sc[c], 0, 0, 0);
+                }
+            }
+        }
+        // Mask, online softmax (log2 domain), P -> LDS as bf16.
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            float sv[2];
+            float bmax = -__builtin_huge_valf();
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c) {
+                const uint32_t key = 16u * c + j16;
+                const int32_t kpos = static_cast<int32_t>(p.offset - p.prefix + jb + key);
+                const bool vis = key < nk && qpos[i] >= 0 && kpos <= qpos[i] &&
+                                 (p.window == 0u || kpos > qpos[i] - static_cast<int32_t>(p.window));
+                sv[c] = vis ? sc[c][i] * kLog2e : -__builtin_huge_valf();
+                bmax = fmaxf(bmax, sv[c]);
+            }
+#pragma unroll
+            for (int mask = 1; mask <= 8; mask <<= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, mask, 64));
+            const float m_new = fmaxf(m[i], bmax);
+            const bool any = m_new > -__builtin_huge_valf();
+            const float alpha = any ? exp2f(m[i] - m_new) : 1.0f;
+            float psum = 0.0f;
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c) {
+                const float pv = any && sv[c] > -__builtin_huge_valf() ? exp2f(sv[c] - m_new) : 0.0f;
+                psum += pv;
+                *reinterpret_cast<uint16_t*>(my + Lds::kP + (4u * kb + i) * Lds::kPRow + (16u * c + j16) * 2u) =
+                    f32_to_bf16_bits(pv);
+            }
+#pragma unroll
+            for (int mask = 1; mask <= 8; mask <<= 1) psum += __shfl_xor(psum, mask, 64);
+            l[i] = l[i] * alpha + psum;
+            m[i] = any ? m_new : m[i];
+#pragma unroll
+            for (uint32_t t = 0; t < kDTiles; ++t) o[t][i] *= alpha;
+        }
+        // O += P V.
+        const bf16x8_t pa = *reinterpret_cast<const bf16x8_t*>(my + Lds::kP + j16 * Lds::kPRow + kb * 16u);
+#pragma unroll
+        for (uint32_t t = 0; t < kDTiles; ++t) {
+            const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(my + Lds::kVt + (16u * t + j16) * Lds::kVtRow + kb * 16u);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, o[t], 0, 0, 0);
+        }
+    }
+
+    // Rows 4 kb + i, dims 16 t + j16.
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t r = 4u * kb + i;
+        if (r >= rows) continue;
+        const uint32_t t = r / p.G;
+        const uint32_t h = hk * p.G + (r - t * p.G);
+        const size_t orow = static_cast<size_t>(t) * p.H + h;
+        if (p.splits == 1u) {
+            const float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+#pragma unroll
+            for (uint32_t tt = 0; tt < kDTiles; ++tt) p.out[orow * D + 16u * tt + j16] = f32_to_bf16_bits(o[tt][i] * inv);
+        } else {
+            const size_t prow = static_cast<size_t>(split) * p.L * p.H + orow;
+#pragma unroll
+            for (uint32_t tt = 0; tt < kDTiles; ++tt) p.part_o[prow * D + 16u * tt + j16] = o[tt][i];
+            if (j16 == 0u) {
+                p.part_ml[prow * 2u] = m[i];
+                p.part_ml[prow * 2u + 1u] = l[i];
+            }
+        }
+    }
+}
+
+// Merge the splits of each output row: weights 2^(m_s - max m), sum of l_s, divided sums.
+// One wave per row: lane s holds split s's (m, l); each lane then owns D/64 consecutive
+// dims and sums the splits' partial rows in split order (independent loads, pipelined).
+template <uint32_t D>
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint64_t rows = static_cast<uint64_t>(p.L) * p.H;
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * (kAttnThreads / 64u) + wave;
+    if (row >= rows) return;   // wave-uniform
+    float ms = -__builtin_huge_valf();
+    float ls = 0.0f;
+    if (lane < p.splits) {
+        ms = p.part_ml[(lane * rows + row) * 2u];
+        ls = p.part_ml[(lane * rows + row) * 2u + 1u];
+    }
+    float mx = ms;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float w = ms == -__builtin_huge_valf() || mx == -__builtin_huge_valf() ? 0.0f : exp2f(ms - mx);
+    constexpr uint32_t kPer = D / 64u;
+    constexpr uint32_t kBatch = 8u;   // splits whose partial rows are loaded together
+    float num[kPer];
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; ++e) num[e] = 0.0f;
+    float den = 0.0f;
+    for (uint32_t s0 = 0; s0 < p.splits; s0 += kBatch) {
+        float part[kBatch][kPer];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t sp = s0 + u;
+            const float* o = p.part_o + (sp * rows + row) * D + lane * kPer;
+#pragma unroll
+            for (uint32_t e = 0; e < kPer; ++e) part[u][e] = sp < p.splits ? o[e] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t sp = s0 + u;
+            const float ws = __shfl(w, static_cast<int>(sp & 63u), 64);
+            const float lw = __shfl(ls, static_cast<int>(sp & 63u), 64);
+            if (sp >= p.splits || ws == 0.0f) continue;   // uniform: past the splits, or an empty split
+            den += ws * lw;
+#pragma unroll
+            for (uint32_t e = 0; e < kPer; ++e) num[e] += ws * part[u][e];
+        }
+    }
+    uint16_t* out = p.out + row * D + lane * kPer;
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; ++e) out[e] = f32_to_bf16_bits(den > 0.0f ? num[e] / den : 0.0f);
 }
 
 // Tokens pos0 .. pos0 + n - 1 of k/v [n][KVH][D] -> cache slots pos % cap (only the last
@@ -279,6 +521,26 @@ __global__ __launch_bounds__(kAttnThreads) void kv_write_kernel(const uint16_t* 
     const size_t dst = static_cast<size_t>(slot) * row_elems + ch * 8u;
     *reinterpret_cast<uint4*>(ck + dst) = *reinterpret_cast<const uint4*>(k + src);
     *reinterpret_cast<uint4*>(cv + dst) = *reinterpret_cast<const uint4*>(v + src);
+}
+
+template <uint32_t D>
+void launch_decode_d(const AttnParams& p, hipStream_t stream) {
+    using Lds = DecodeLds<D>;
+    constexpr size_t lds = Lds::kBytes;
+    static_assert(lds <= 160u * 1024u, "decode attention LDS");
+    if (lds > 65536u) {
+        static thread_local int configured_device = -1;
+        int dev = 0;
+        HYP_HIP_CHECK(hipGetDevice(&dev));
+        if (configured_device != dev) {
+            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attn_decode_kernel<D>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            configured_device = dev;
+        }
+    }
+    const dim3 grid((p.splits + Lds::kWaves - 1u) / Lds::kWaves, p.KVH);
+    hipLaunchKernelGGL(attn_decode_kernel<D>, grid, dim3(Lds::kWaves * 64u), lds, stream, p);
+    HYP_HIP_CHECK(hipGetLastError());
 }
 
 template <uint32_t D>
@@ -321,7 +583,15 @@ void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_
     HYP_HIP_CHECK(hipGetLastError());
 }
 
+// The decode form's splits: one wave per block of 32 keys (each wave then makes a single
+// round trip to memory for its keys), within kAttnMaxSplits.
+uint32_t decode_splits(uint32_t n_kv_heads, uint32_t keys) {
+    (void)n_kv_heads;
+    return std::max(1u, std::min(kAttnMaxSplits, (keys + kKeyBlock - 1u) / kKeyBlock));
+}
+
 uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys) {
+    if (static_cast<uint64_t>(L) * (n_heads / n_kv_heads) <= 16u) return decode_splits(n_kv_heads, keys);
     // One row tile per kv head (decode): split the keys so the grid covers the compute
     // units, at least 64 keys per split.
     const uint32_t G = n_heads / n_kv_heads;
@@ -349,9 +619,17 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
     p.prefix = a.prefix_len;
     p.window = a.window;
     const uint32_t T = a.prefix_len + a.L;
-    p.splits = attention_splits(a.L, a.n_heads, a.n_kv_heads, T);
-    p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
-    p.splits = std::max(1u, (T + p.keys_per_split - 1u) / p.keys_per_split);   // no empty split
+    p.pos = a.pos;
+    if (a.pos != nullptr) {
+        // A grid fixed for every position the captured launch will see (the kernel
+        // derives its key ranges from *pos; splits past the keys write empty partials).
+        p.splits = std::max(1u, std::min(a.fixed_splits, kAttnMaxSplits));
+        p.keys_per_split = kKeyBlock;
+    } else {
+        p.splits = attention_splits(a.L, a.n_heads, a.n_kv_heads, T);
+        p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
+        p.splits = std::max(1u, (T + p.keys_per_split - 1u) / p.keys_per_split);   // no empty split
+    }
     if (p.splits > 1u) {
         HYP_REQUIRE(a.workspace != nullptr &&
                         a.workspace_bytes >= attention_workspace_bytes(a.n_kv_heads, a.head_dim),
@@ -361,17 +639,23 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
         p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) +
                                              static_cast<size_t>(p.splits) * rows * a.head_dim * 4u);
     }
+    const bool decode = static_cast<uint64_t>(a.L) * p.G <= 16u;
     switch (a.head_dim) {
-        case 64: launch_attn_d<64>(p, stream); break;
-        case 128: launch_attn_d<128>(p, stream); break;
-        case 256: launch_attn_d<256>(p, stream); break;
-        case 512: launch_attn_d<512>(p, stream); break;
+        case 64: decode ? launch_decode_d<64>(p, stream) : launch_attn_d<64>(p, stream); break;
+        case 128: decode ? launch_decode_d<128>(p, stream) : launch_attn_d<128>(p, stream); break;
+        case 256: decode ? launch_decode_d<256>(p, stream) : launch_attn_d<256>(p, stream); break;
+        case 512: decode ? launch_decode_d<512>(p, stream) : launch_attn_d<512>(p, stream); break;
         default: throw NativeError(HYP_STATUS_UNSUPPORTED, "attention: head_dim must be 64, 128, 256 or 512");
     }
     if (p.splits > 1u) {
-        const uint64_t elems = static_cast<uint64_t>(a.L) * a.n_heads * a.head_dim;
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<uint32_t>((elems + kAttnThreads - 1u) / kAttnThreads)),
-                           dim3(kAttnThreads), 0, stream, p, a.head_dim);
+        const uint64_t rows = static_cast<uint64_t>(a.L) * a.n_heads;
+        const dim3 grid(static_cast<uint32_t>((rows + kAttnThreads / 64u - 1u) / (kAttnThreads / 64u)));
+        switch (a.head_dim) {
+            case 64: hipLaunchKernelGGL(attn_combine_kernel<64>, grid, dim3(kAttnThreads), 0, stream, p); break;
+            case 128: hipLaunchKernelGGL(attn_combine_kernel<128>, grid, dim3(kAttnThreads), 0, stream, p); break;
+            case 256: hipLaunchKernelGGL(attn_combine_kernel<256>, grid, dim3(kAttnThreads), 0, stream, p); break;
+            default: hipLaunchKernelGGL(attn_combine_kernel<512>, grid, dim3(kAttnThreads), 0, stream, p); break;
+        }
         HYP_HIP_CHECK(hipGetLastError());
     }
 }

@@ -141,6 +141,19 @@ uint32_t Geometry::rotated_dims(LayerType kind) const noexcept {
     return rotated;
 }
 
+GraphExec::~GraphExec() {
+    if (exec_ != nullptr) (void)hipGraphExecDestroy(exec_);
+}
+
+GraphExec& GraphExec::operator=(GraphExec&& o) noexcept {
+    if (this != &o) {
+        if (exec_ != nullptr) (void)hipGraphExecDestroy(exec_);
+        exec_ = o.exec_;
+        o.exec_ = nullptr;
+    }
+    return *this;
+}
+
 Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geometry)), w_(std::move(weights)) {
     const Geometry& g = geo_;
     if (!w_.has_norms) invalid("the weights artifact is missing norm vectors or layer scalars");
@@ -203,6 +216,17 @@ Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geome
     attn_ws_ = DeviceBuffer(std::max(hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
                                      hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)));
     sample_ws_ = DeviceBuffer(hip::sample_greedy_workspace_bytes());
+    const auto table = [&](uint32_t D, LayerType kind, double theta) {
+        const size_t bytes = static_cast<size_t>(g.max_positions) * (D / 2u) * sizeof(float2);
+        if (bytes > kRopeTableMaxBytes) return DeviceBuffer();
+        DeviceBuffer t(bytes);
+        hip::launch_rope_table(static_cast<float2*>(t.data()), g.max_positions, D, g.rotated_dims(kind),
+                               static_cast<float>(theta), stream_);
+        return t;
+    };
+    rope_local_ = table(g.head_dim_local, LayerType::Sliding, g.rope_local.theta);
+    rope_global_ = table(g.head_dim_global, LayerType::Full, g.rope_global.theta);
+    HYP_HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 Decoder::~Decoder() {
@@ -232,26 +256,38 @@ DecoderState Decoder::make_state() const {
         (sliding ? st.local_bytes : st.global_bytes) += 2u * bytes;
         st.caches.push_back(std::move(c));
     }
-    ensure_sample_slots(st, 2);
+    st.cur = DeviceBuffer(sizeof(HypTopKSample));
+    st.counters = DeviceBuffer(2u * sizeof(uint32_t));
+    HYP_HIP_CHECK(hipMemsetAsync(st.cur.data(), 0, st.cur.bytes(), stream_));
+    HYP_HIP_CHECK(hipMemsetAsync(st.counters.data(), 0, st.counters.bytes(), stream_));
     HYP_HIP_CHECK(hipStreamSynchronize(stream_));
     return st;
 }
 
-void Decoder::ensure_sample_slots(DecoderState& st, uint32_t slots) const {
-    if (st.sample_slots >= slots) return;
-    DeviceBuffer fresh(static_cast<size_t>(slots) * sizeof(HypTopKSample));
-    HYP_HIP_CHECK(hipMemsetAsync(fresh.data(), 0, fresh.bytes(), stream_));
-    if (st.sample_slots > 0) {
-        HYP_HIP_CHECK(hipMemcpyAsync(fresh.data(), st.samples.data(), sizeof(HypTopKSample), hipMemcpyDeviceToDevice,
-                                     stream_));
+void Decoder::capture_step(DecoderState& st) {
+    auto* cur = static_cast<HypTopKSample*>(st.cur.data());
+    auto* counters = static_cast<uint32_t*>(st.counters.data());
+    HYP_HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    hipGraph_t graph = nullptr;
+    try {
+        forward_chunk(st, &cur->token_id, 1, 0, nullptr, counters);
+        epilogue(cur);
+        hip::launch_decode_advance(counters, counters + 1, cur, stream_);
+    } catch (...) {
+        (void)hipStreamEndCapture(stream_, &graph);
+        if (graph != nullptr) (void)hipGraphDestroy(graph);
+        throw;
     }
-    HYP_HIP_CHECK(hipStreamSynchronize(stream_));
-    st.samples = std::move(fresh);
-    st.sample_slots = slots;
+    HYP_HIP_CHECK(hipStreamEndCapture(stream_, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HYP_HIP_CHECK(err);
+    st.step = GraphExec(exec);
 }
 
 void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset,
-                            uint16_t* final_rows) {
+                            uint16_t* final_rows, const uint32_t* d_pos) {
     const Geometry& g = geo_;
     hipStream_t s = stream_;
     uint16_t* x = u16(x_);
@@ -289,6 +325,8 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
 
         // q_norm / k_norm / v_norm, RoPE, the cache append (forward.cc:400-459).
         hip::AttnPrepareArgs pa{};
+        pa.pos = d_pos;
+        pa.rope_cs = static_cast<const float2*>((sliding ? rope_local_ : rope_global_).data());
         pa.q = u16(q_);
         pa.k_raw = u16(k_);
         pa.v_raw = sliding ? u16(v_) : nullptr;
@@ -325,6 +363,12 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
         aa.window = sliding ? g.window : 0u;
         aa.workspace = attn_ws_.data();
         aa.workspace_bytes = attn_ws_.bytes();
+        if (d_pos != nullptr) {
+            // Splits sized for the longest key range the replays can see.
+            const uint32_t max_keys = sliding ? std::min(g.window, g.max_positions) + L : g.max_positions;
+            aa.pos = d_pos;
+            aa.fixed_splits = hip::attention_splits(L, g.heads, kvh, max_keys);
+        }
         hip::launch_attention(aa, s);
 
         // o, then the attention half of the sandwich and the MLP's input norm (forward.cc:518-526).
@@ -382,18 +426,18 @@ StepSample Decoder::prefill(DecoderState& st, const uint32_t* ids, uint32_t coun
     for (uint32_t i = 0; i < count; ++i) {
         if (ids[i] >= g.vocab) invalid("token id " + std::to_string(ids[i]) + " is outside the vocabulary");
     }
-    auto* samples = static_cast<HypTopKSample*>(st.samples.data());
+    auto* cur = static_cast<HypTopKSample*>(st.cur.data());
     for (uint32_t done = 0; done < count;) {
         const uint32_t take = std::min(kChunkTokens, count - done);
         HYP_HIP_CHECK(hipMemcpyAsync(ids_.data(), ids + done, take * sizeof(uint32_t), hipMemcpyHostToDevice, stream_));
         forward_chunk(st, static_cast<const uint32_t*>(ids_.data()), take, done, nullptr);
         done += take;
-        if (done == count) epilogue(samples);
+        if (done == count) epilogue(cur);
         // The ids buffer is reused by the next chunk: its copy waits for this chunk.
         HYP_HIP_CHECK(hipStreamSynchronize(stream_));
     }
     StepSample out;
-    HYP_HIP_CHECK(hipMemcpy(&out.sample, samples, sizeof(HypTopKSample), hipMemcpyDeviceToHost));
+    HYP_HIP_CHECK(hipMemcpy(&out.sample, cur, sizeof(HypTopKSample), hipMemcpyDeviceToHost));
     out.near_tie_events = out.sample.near_tie != 0u ? 1u : 0u;
     st.offset = count;
     st.last_token = out.sample.token_id;
@@ -408,21 +452,19 @@ StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
     }
     StepSample out;
     if (n_tokens == 0) return out;
-    ensure_sample_slots(st, n_tokens + 1u);
-    auto* samples = static_cast<HypTopKSample*>(st.samples.data());
-    // Slot 0 holds the last sampled token; step j embeds slot j's token and samples into
-    // slot j + 1, all on the device.
-    for (uint32_t j = 0; j < n_tokens; ++j) {
-        forward_chunk(st, reinterpret_cast<const uint32_t*>(samples + j), 1, st.offset + j, nullptr);
-        epilogue(samples + j + 1);
-    }
-    std::vector<HypTopKSample> host(n_tokens);
-    HYP_HIP_CHECK(hipMemcpyAsync(host.data(), samples + 1, n_tokens * sizeof(HypTopKSample), hipMemcpyDeviceToHost,
-                                 stream_));
-    HYP_HIP_CHECK(hipMemcpyAsync(samples, samples + n_tokens, sizeof(HypTopKSample), hipMemcpyDeviceToDevice, stream_));
+    if (st.step.get() == nullptr) capture_step(st);
+    // The replays start from the cursor with a cleared near-tie count; each embeds the
+    // token in cur, samples the next one into cur and advances the position.
+    const uint32_t start[2] = {st.offset, 0u};
+    auto* counters = static_cast<uint32_t*>(st.counters.data());
+    HYP_HIP_CHECK(hipMemcpyAsync(counters, start, sizeof(start), hipMemcpyHostToDevice, stream_));
+    for (uint32_t j = 0; j < n_tokens; ++j) HYP_HIP_CHECK(hipGraphLaunch(st.step.get(), stream_));
+    uint32_t end[2] = {0u, 0u};
+    HYP_HIP_CHECK(hipMemcpyAsync(&out.sample, st.cur.data(), sizeof(HypTopKSample), hipMemcpyDeviceToHost, stream_));
+    HYP_HIP_CHECK(hipMemcpyAsync(end, counters, sizeof(end), hipMemcpyDeviceToHost, stream_));
     HYP_HIP_CHECK(hipStreamSynchronize(stream_));
-    for (const HypTopKSample& smp : host) out.near_tie_events += smp.near_tie != 0u ? 1u : 0u;
-    out.sample = host.back();
+    HYP_REQUIRE(end[0] == st.offset + n_tokens, HYP_STATUS_INTERNAL, "decode: the device position did not advance");
+    out.near_tie_events = end[1];
     st.offset += n_tokens;
     st.last_token = out.sample.token_id;
     return out;

@@ -17,6 +17,9 @@
 //    the 12B's 8 global caches at 262144 positions in 4.3 GB).
 //  * the sampled token stays in device memory between decode steps: the next step's embed
 //    gather reads it there, so a decode block makes one host round trip, at its end.
+//  * a decode step is one HIP graph, captured once per state and replayed per token: the
+//    position lives in device memory (the kernels that depend on it read it there and a
+//    last node advances it), so a replay needs no host work beyond its launch.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -77,13 +80,30 @@ struct LayerCache {
     uint32_t head_dim = 0;
 };
 
+// An instantiated HIP graph, destroyed with its owner.
+class GraphExec {
+  public:
+    GraphExec() = default;
+    explicit GraphExec(hipGraphExec_t exec) : exec_(exec) {}
+    ~GraphExec();
+    GraphExec(const GraphExec&) = delete;
+    GraphExec& operator=(const GraphExec&) = delete;
+    GraphExec(GraphExec&& o) noexcept : exec_(o.exec_) { o.exec_ = nullptr; }
+    GraphExec& operator=(GraphExec&& o) noexcept;
+    [[nodiscard]] hipGraphExec_t get() const noexcept { return exec_; }
+
+  private:
+    hipGraphExec_t exec_ = nullptr;
+};
+
 // One sequence's KV state (KvState, kv.h) plus its autoregressive cursor (model.cc:606-607).
 struct DecoderState {
     std::vector<LayerCache> caches;   // one per layer, in layer order
     uint32_t offset = 0;              // tokens committed
     uint32_t last_token = 0;
-    DeviceBuffer samples;             // HypTopKSample [sample_slots]: slot 0 = last step's
-    uint32_t sample_slots = 0;
+    DeviceBuffer cur;                 // HypTopKSample: the last sampled token, on the device
+    DeviceBuffer counters;            // uint32 [2]: the device-side position and near-tie count
+    GraphExec step;                   // one decode step, captured at the first decode
     uint64_t local_bytes = 0;
     uint64_t global_bytes = 0;
 };
@@ -121,10 +141,15 @@ class Decoder {
   private:
     // embed + all layers over L <= kChunkTokens tokens whose ids are in device memory.
     // final_rows: all L final-normalised rows there; otherwise the last row into last_.
-    void forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset, uint16_t* final_rows);
+    // d_pos non-null (a replayable step): the position is read from *d_pos on the device
+    // and `offset` is unused.
+    void forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset, uint16_t* final_rows,
+                       const uint32_t* d_pos = nullptr);
     // lm_head + softcap + greedy with the top-k sidecar of last_ into *d_out.
     void epilogue(HypTopKSample* d_out);
-    void ensure_sample_slots(DecoderState& st, uint32_t slots) const;
+    // Capture one decode step of `st` (embed cur's token at *pos, every layer, the head,
+    // the sample into cur, pos += 1) as a graph.
+    void capture_step(DecoderState& st);
 
     Geometry geo_;
     ModelWeights w_;
@@ -134,6 +159,12 @@ class Decoder {
     DeviceBuffer ids_;           // uint32 [kChunkTokens]
     DeviceBuffer x_, xn_, q_, k_, v_, attn_, o_, h_, d_, last_, logits_;
     DeviceBuffer attn_ws_, sample_ws_;
+    // RoPE (cos, sin) of every position per layer kind, computed once on the device with
+    // the rope kernel's arithmetic (a 12B at 262144 positions: 0.8 GB); empty when larger
+    // than kRopeTableMaxBytes, then the prepare kernel computes them per token.
+    DeviceBuffer rope_local_, rope_global_;
 };
+
+constexpr size_t kRopeTableMaxBytes = size_t{4} << 30;
 
 }  // namespace hyperion::model

@@ -109,7 +109,7 @@ void launch_sample_topk(const uint16_t* logits, uint32_t rows, uint32_t vocab, H
 
 // Attention (forward.cc:376-508) over a KV cache prefix and the current chunk; see
 // attention.hip. Decode splits the keys; the partial sums need attention_workspace_bytes.
-constexpr uint32_t kAttnMaxSplits = 32;
+constexpr uint32_t kAttnMaxSplits = 64;
 struct AttnArgs {
     const uint16_t* q;         // [L][n_heads][head_dim]
     const uint16_t* k;         // [L][n_kv_heads][head_dim] (the chunk); null: the chunk is
@@ -120,6 +120,11 @@ struct AttnArgs {
     uint32_t L, n_heads, n_kv_heads, head_dim, cap, offset, prefix_len, window;
     void* workspace;
     size_t workspace_bytes;
+    // Graph-replay form: with pos non-null the kernel reads the offset from *pos and takes
+    // prefix_len = min(window, offset) (window > 0) or offset; the keys are split over
+    // fixed_splits workgroups per kv head whatever the offset.
+    const uint32_t* pos = nullptr;
+    uint32_t fixed_splits = 1;
 };
 size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim);
 uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys);
@@ -133,6 +138,9 @@ void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_
 // cache V slot <- rms_norm(v_raw) (v_raw null: of k_raw). Token t is at position offset + t,
 // slot (offset + t) % cap; when L > cap only the last cap tokens reach the cache.
 struct AttnPrepareArgs {
+    const uint32_t* pos = nullptr;   // non-null: the offset is read from *pos on the device
+    const float2* rope_cs = nullptr; // non-null: (cos, sin) [positions][head_dim / 2] from
+                                     // launch_rope_table, instead of computing them
     uint16_t* q;
     const uint16_t* k_raw;
     const uint16_t* v_raw;
@@ -144,6 +152,10 @@ struct AttnPrepareArgs {
     float base, eps;
 };
 void launch_attn_prepare(const AttnPrepareArgs& a, hipStream_t stream);
+// (cos, sin) of every position < positions and pair i < head_dim / 2, with rope_kernel's
+// arithmetic (so a prepare that reads the table gives the bits of one that computes).
+void launch_rope_table(float2* table, uint32_t positions, uint32_t head_dim, uint32_t rotated, float base,
+                       hipStream_t stream);
 
 // For each of m rows: residual <- bf16(residual + rms_norm(branch, w_post)); with scalar
 // (device bf16 [1]) residual <- bf16(residual * scalar); with w_next, next <- rms_norm(
@@ -152,6 +164,9 @@ uint32_t residual_norm_max_hidden();
 void launch_residual_norm(const uint16_t* branch, uint16_t* residual, const uint16_t* w_post, const uint16_t* scalar,
                           const uint16_t* w_next, uint16_t* next, uint32_t m, uint32_t hidden, float eps,
                           hipStream_t stream);
+
+// The end of a replayed decode step: pos[0] += 1, ties[0] += sample->near_tie.
+void launch_decode_advance(uint32_t* pos, uint32_t* ties, const HypTopKSample* sample, hipStream_t stream);
 
 // mx.quantize(w, 64, 4, "affine") of bf16 [n, k].
 void launch_q4_quantize(const uint16_t* w, uint32_t n, uint32_t k, uint32_t* wq,

@@ -3,11 +3,11 @@
 //  * attn_prepare_kernel - ForwardPass::attention from the q/k/v projections to the cache
 //    append (native/hyperion_mlx/src/forward.cc:395-459): q <- rope(q_norm(q)) in place;
 //    K slot <- rope(k_norm(k_raw)); V slot <- v_norm(v_raw), v_raw = k_raw on K = V global
-//    layers (forward.cc:403-412). One workgroup per token: the token's cos/sin table is
-//    computed once into LDS and shared by all its heads; each wave normalises one head at
-//    a time (lane u owns 64-value unit u, the order of q4_rmsnorm.h), stages it in LDS and
-//    rotates pairs (i, i + D/2). Bits: those of rms_norm_rows_kernel followed by
-//    rope_kernel and kv_write_kernel.
+//    layers (forward.cc:403-412). One wave per (token, head): it normalises the head (lane u
+//    owns 64-value unit u, the order of q4_rmsnorm.h), stages it in LDS and rotates pairs
+//    (i, i + D/2) with their (cos, sin) computed in place or read from a table that
+//    rope_table_kernel filled with the same arithmetic. Bits: those of rms_norm_rows_kernel
+//    followed by rope_kernel and kv_write_kernel.
 //
 //  * residual_norm_kernel - the Gemma sandwich around a block (forward.cc:518-529):
 //    residual <- bf16(residual + rms_norm(branch, w_post)), then optionally
@@ -27,6 +27,8 @@ constexpr uint32_t kWaves = kThreads / 64u;
 constexpr uint32_t kMaxHeadDim = 512;
 
 struct PrepareParams {
+    const uint32_t* pos;      // non-null: offset = *pos
+    const float2* rope_cs;    // non-null: (cos, sin) [positions][D/2], rope_table_kernel's values
     uint16_t* q;              // [L][H][D], in place
     const uint16_t* k_raw;    // [L][KVH][D]
     const uint16_t* v_raw;    // [L][KVH][D] or null (K = V: v_norm of k_raw)
@@ -41,14 +43,20 @@ struct PrepareParams {
 
 // Lanes u < D/64 load head `src` unit u and leave bf16(w * bf16(x * inv)) (w null: bf16(x *
 // inv)) in xv; every lane takes part in the butterfly.
+// (All of the head's and the weight's loads are issued before the first use.)
 __device__ __forceinline__ void norm_head(const uint16_t* src, const uint16_t* w, uint32_t D, float eps,
                                           uint32_t lane, uint4 (&xv)[8]) {
     const uint32_t units = D / 64u;
     float ss = 0.0f;
+    uint4 wv[8];
     if (lane < units) {
         const uint4* s4 = reinterpret_cast<const uint4*>(src) + lane * 8u;
+        const uint4* w4 = reinterpret_cast<const uint4*>(w != nullptr ? w : src) + lane * 8u;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xv[t] = s4[t];
+        for (int t = 0; t < 8; ++t) {
+            xv[t] = s4[t];
+            wv[t] = w4[t];
+        }
         ss = unit_sumsq(xv);
     }
 #pragma unroll
@@ -56,93 +64,102 @@ __device__ __forceinline__ void norm_head(const uint16_t* src, const uint16_t* w
     const float inv = rms_inverse(ss, D, eps);
     if (lane < units) {
         normalize_unit(xv, inv);
-        if (w != nullptr) {
-            const uint4* w4 = reinterpret_cast<const uint4*>(w) + lane * 8u;
-            uint4 wv[8];
+        if (w != nullptr) weight_unit(xv, wv);
+    }
+}
+
+// rope_kernel's angle arithmetic: inv_freq in double rounded to fp32, theta in fp32, cos and
+// sin in double rounded to fp32.
+__device__ __forceinline__ float2 rope_angle(uint32_t pos, uint32_t i, uint32_t D, uint32_t rotated, double base) {
+    const float inv = 2u * i < rotated ? static_cast<float>(pow(base, -2.0 * i / static_cast<double>(D))) : 0.0f;
+    const float theta = static_cast<float>(pos) * inv;
+    return make_float2(static_cast<float>(cos(static_cast<double>(theta))),
+                       static_cast<float>(sin(static_cast<double>(theta))));
+}
+
+// Grid (L, ceil((H + KVH) / 4)): wave w of workgroup (t, y) takes head 4y + w of token t
+// (q heads first, then kv heads).
+__global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t head[kWaves][kMaxHeadDim];
+    const uint32_t t = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t D = p.D;
+    const uint32_t half = D / 2u;
+    const uint32_t pos = (p.pos != nullptr ? *p.pos : p.offset) + t;
+    const uint32_t hh = blockIdx.y * kWaves + wave;
+    const bool is_q = hh < p.H;
+    const bool active = hh < p.H + p.KVH && (is_q || t >= p.first_cached);   // wave-uniform
+    const size_t slot = static_cast<size_t>(pos % p.cap);
+    uint16_t* hb = head[wave];
+    uint16_t* dst = nullptr;
+
+    // This lane's pairs i = lane + 64 j: their (cos, sin), looked up or computed.
+    float2 cs[kMaxHeadDim / 128];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) wv[t] = w4[t];
-            weight_unit(xv, wv);
+    for (uint32_t j = 0; j < kMaxHeadDim / 128; ++j) {
+        const uint32_t i = lane + 64u * j;
+        cs[j] = make_float2(1.0f, 0.0f);
+        if (active && i < half) {
+            cs[j] = p.rope_cs != nullptr ? p.rope_cs[static_cast<size_t>(pos) * half + i]
+                                         : rope_angle(pos, i, D, p.rotated, p.base);
+        }
+    }
+    if (active) {
+        uint4 xv[8];
+        const uint16_t* src;
+        const uint16_t* w;
+        if (is_q) {
+            src = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
+            w = p.q_w;
+            dst = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
+        } else {
+            const uint32_t kh = hh - p.H;
+            const size_t row = (static_cast<size_t>(t) * p.KVH + kh) * D;
+            // V: the weightless norm straight into the cache slot.
+            norm_head(p.v_raw != nullptr ? p.v_raw + row : p.k_raw + row, nullptr, D, p.eps, lane, xv);
+            if (lane < D / 64u) {
+                uint4* v4 = reinterpret_cast<uint4*>(p.cache_v + (slot * p.KVH + kh) * D) + lane * 8u;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v4[u] = xv[u];
+            }
+            src = p.k_raw + row;
+            w = p.k_w;
+            dst = p.cache_k + (slot * p.KVH + kh) * D;
+        }
+        norm_head(src, w, D, p.eps, lane, xv);
+        if (lane < D / 64u) {
+            uint4* h4 = reinterpret_cast<uint4*>(hb) + lane * 8u;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) h4[u] = xv[u];
+        }
+    }
+    __syncthreads();   // the staged head is visible to every lane of its wave
+    if (active) {
+#pragma unroll
+        for (uint32_t j = 0; j < kMaxHeadDim / 128; ++j) {
+            const uint32_t i = lane + 64u * j;
+            if (i >= half) break;
+            const float x1 = bf16_bits_to_f32(hb[i]);
+            const float x2 = bf16_bits_to_f32(hb[i + half]);
+            const float a1 = x1 * cs[j].x;
+            const float a2 = x2 * cs[j].y;
+            const float b1 = x1 * cs[j].y;
+            const float b2 = x2 * cs[j].x;
+            dst[i] = f32_to_bf16_bits(a1 - a2);
+            dst[i + half] = f32_to_bf16_bits(b1 + b2);
         }
     }
 }
 
-__global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p) {
-    __shared__ float2 cs[kMaxHeadDim / 2];                        // (cos, sin) per pair
-    __shared__ __attribute__((aligned(16))) uint16_t head[kWaves][kMaxHeadDim];
-    const uint32_t t = blockIdx.x;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63u;
-    const uint32_t wave = tid >> 6;
-    const uint32_t D = p.D;
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(float2* table, uint32_t positions, uint32_t D,
+                                                              uint32_t rotated, double base) {
     const uint32_t half = D / 2u;
-    const uint32_t pos = p.offset + t;
-
-    // rope_kernel's angle arithmetic: inv_freq in double rounded to fp32, theta in fp32,
-    // cos and sin in double rounded to fp32.
-    for (uint32_t i = tid; i < half; i += kThreads) {
-        const float inv = 2u * i < p.rotated ? static_cast<float>(pow(p.base, -2.0 * i / static_cast<double>(D))) : 0.0f;
-        const float theta = static_cast<float>(pos) * inv;
-        cs[i] = make_float2(static_cast<float>(cos(static_cast<double>(theta))),
-                            static_cast<float>(sin(static_cast<double>(theta))));
-    }
-    __syncthreads();
-
-    const bool cached = t >= p.first_cached;   // a chunk longer than the ring keeps its last cap tokens
-    const size_t slot = static_cast<size_t>(pos % p.cap);
-    const uint32_t total = p.H + p.KVH;
-    const uint32_t rounds = (total + kWaves - 1u) / kWaves;
-    uint16_t* hb = head[wave];
-    for (uint32_t r = 0; r < rounds; ++r) {
-        const uint32_t hh = r * kWaves + wave;
-        const bool is_q = hh < p.H;
-        const bool active = hh < total && (is_q || cached);
-        uint16_t* dst = nullptr;
-        uint4 xv[8];
-        if (active) {
-            const uint16_t* src;
-            const uint16_t* w;
-            if (is_q) {
-                src = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
-                w = p.q_w;
-                dst = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
-            } else {
-                const uint32_t kh = hh - p.H;
-                const size_t row = (static_cast<size_t>(t) * p.KVH + kh) * D;
-                // V: the weightless norm straight into the cache slot.
-                norm_head(p.v_raw != nullptr ? p.v_raw + row : p.k_raw + row, nullptr, D, p.eps, lane, xv);
-                if (lane < D / 64u) {
-                    uint4* v4 = reinterpret_cast<uint4*>(p.cache_v + (slot * p.KVH + kh) * D) + lane * 8u;
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) v4[u] = xv[u];
-                }
-                src = p.k_raw + row;
-                w = p.k_w;
-                dst = p.cache_k + (slot * p.KVH + kh) * D;
-            }
-            norm_head(src, w, D, p.eps, lane, xv);
-            if (lane < D / 64u) {
-                uint4* h4 = reinterpret_cast<uint4*>(hb) + lane * 8u;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) h4[u] = xv[u];
-            }
-        }
-        __syncthreads();   // the staged head is visible to every lane of its wave
-        if (active) {
-            for (uint32_t i = lane; i < half; i += 64u) {
-                const float x1 = bf16_bits_to_f32(hb[i]);
-                const float x2 = bf16_bits_to_f32(hb[i + half]);
-                const float c = cs[i].x;
-                const float s = cs[i].y;
-                const float a1 = x1 * c;
-                const float a2 = x2 * s;
-                const float b1 = x1 * s;
-                const float b2 = x2 * c;
-                dst[i] = f32_to_bf16_bits(a1 - a2);
-                dst[i + half] = f32_to_bf16_bits(b1 + b2);
-            }
-        }
-        __syncthreads();   // the rotation has read the staged head before the next round
-    }
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e >= static_cast<uint64_t>(positions) * half) return;
+    const uint32_t pos = static_cast<uint32_t>(e / half);
+    const uint32_t i = static_cast<uint32_t>(e - static_cast<uint64_t>(pos) * half);
+    table[e] = rope_angle(pos, i, D, rotated, base);
 }
 
 // residual and next are [m][hidden]; hidden = 64 * units, units <= kThreads.
@@ -162,9 +179,19 @@ __global__ __launch_bounds__(kThreads) void residual_norm_kernel(const uint16_t*
     const bool mine = tid < units;
 
     uint4 xv[8];
+    uint4 rv[8];
+    uint4 wv[8];
+    uint4 nv[8];
     if (mine) {
+        const uint4* w4 = reinterpret_cast<const uint4*>(w_post) + tid * 8u;
+        const uint4* n4 = reinterpret_cast<const uint4*>(w_next != nullptr ? w_next : w_post) + tid * 8u;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xv[t] = b4[t];
+        for (int t = 0; t < 8; ++t) {   // every load of the row issued before the first use
+            xv[t] = b4[t];
+            rv[t] = r4[t];
+            wv[t] = w4[t];
+            nv[t] = n4[t];
+        }
         part[tid] = unit_sumsq(xv);
     }
     __syncthreads();
@@ -178,15 +205,10 @@ __global__ __launch_bounds__(kThreads) void residual_norm_kernel(const uint16_t*
     float ss2 = 0.0f;
     if (mine) {
         normalize_unit(xv, inv);
-        uint4 wv[8];
-        const uint4* w4 = reinterpret_cast<const uint4*>(w_post) + tid * 8u;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) wv[t] = w4[t];
         weight_unit(xv, wv);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint4 rv = r4[t];
-            const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
             uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -214,24 +236,34 @@ __global__ __launch_bounds__(kThreads) void residual_norm_kernel(const uint16_t*
     __syncthreads();
     if (mine) {
         normalize_unit(xv, part[kThreads]);
-        uint4 wv[8];
-        const uint4* w4 = reinterpret_cast<const uint4*>(w_next) + tid * 8u;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) wv[t] = w4[t];
-        weight_unit(xv, wv);
+        weight_unit(xv, nv);
         uint4* n4 = reinterpret_cast<uint4*>(next + row) + tid * 8u;
 #pragma unroll
         for (int t = 0; t < 8; ++t) n4[t] = xv[t];
     }
 }
 
+__global__ void decode_advance_kernel(uint32_t* pos, uint32_t* ties, const HypTopKSample* sample) {
+    if (threadIdx.x == 0u) {
+        pos[0] += 1u;
+        ties[0] += sample->near_tie != 0u ? 1u : 0u;
+    }
+}
+
 }  // namespace
+
+void launch_decode_advance(uint32_t* pos, uint32_t* ties, const HypTopKSample* sample, hipStream_t stream) {
+    hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, stream, pos, ties, sample);
+    HYP_HIP_CHECK(hipGetLastError());
+}
 
 void launch_attn_prepare(const AttnPrepareArgs& a, hipStream_t stream) {
     if (a.L == 0) return;
     HYP_REQUIRE(a.head_dim % 64u == 0u && a.head_dim <= kMaxHeadDim, HYP_STATUS_UNSUPPORTED,
                 "attention prepare: head_dim must be a multiple of 64, at most 512");
     PrepareParams p{};
+    p.pos = a.pos;
+    p.rope_cs = a.rope_cs;
     p.q = a.q;
     p.k_raw = a.k_raw;
     p.v_raw = a.v_raw;
@@ -249,7 +281,19 @@ void launch_attn_prepare(const AttnPrepareArgs& a, hipStream_t stream) {
     p.first_cached = a.L > a.cap ? a.L - a.cap : 0u;
     p.base = static_cast<double>(a.base);
     p.eps = a.eps;
-    hipLaunchKernelGGL(attn_prepare_kernel, dim3(a.L), dim3(kThreads), 0, stream, p);
+    const uint32_t groups = (a.n_heads + a.n_kv_heads + kWaves - 1u) / kWaves;
+    hipLaunchKernelGGL(attn_prepare_kernel, dim3(a.L, groups), dim3(kThreads), 0, stream, p);
+    HYP_HIP_CHECK(hipGetLastError());
+}
+
+void launch_rope_table(float2* table, uint32_t positions, uint32_t head_dim, uint32_t rotated, float base,
+                       hipStream_t stream) {
+    const uint64_t n = static_cast<uint64_t>(positions) * (head_dim / 2u);
+    if (n == 0) return;
+    const uint64_t blocks = (n + kThreads - 1u) / kThreads;
+    HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "rope table: too large");
+    hipLaunchKernelGGL(rope_table_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, stream, table,
+                       positions, head_dim, rotated, static_cast<double>(base));
     HYP_HIP_CHECK(hipGetLastError());
 }
 

@@ -12,6 +12,8 @@ seeds. Shapes and distributions are the benchmark configurations of this path:
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 # Gemma-class 12B decoder layer projections: name -> (out_features n, in_features k).
@@ -127,8 +129,10 @@ def _q4_random(rng, n: int, k: int):
     return w, s, b
 
 
-def write_safetensors(path: str, tensors: dict) -> None:
-    """{name: numpy array} -> one safetensors file (U32 for uint32, BF16 for uint16 bit patterns)."""
+def write_safetensors(path: str, tensors: dict, holes=()) -> None:
+    """{name: numpy array} -> one safetensors file (U32 for uint32, BF16 for uint16 bit
+    patterns). Tensors named in `holes` are not written: the file keeps a hole there, which
+    reads as zeros (their arrays give only the shape and dtype)."""
     import json
     header, offset, blobs = {}, 0, []
     for name, a in tensors.items():
@@ -136,26 +140,35 @@ def write_safetensors(path: str, tensors: dict) -> None:
         dt = {np.dtype(np.uint32): "U32", np.dtype(np.uint16): "BF16", np.dtype(np.float32): "F32"}[a.dtype]
         header[name] = {"dtype": dt, "shape": list(a.shape), "data_offsets": [offset, offset + a.nbytes]}
         offset += a.nbytes
-        blobs.append(a)
+        blobs.append((name, a))
     raw = json.dumps(header).encode()
     raw += b" " * (-len(raw) % 8)
+    holes = set(holes)
     with open(path, "wb") as f:
         f.write(np.uint64(len(raw)).tobytes())
         f.write(raw)
-        for a in blobs:
-            a.tofile(f)
+        for name, a in blobs:
+            if name in holes:
+                f.seek(a.nbytes, os.SEEK_CUR)
+            else:
+                a.tofile(f)
+        f.truncate(8 + len(raw) + offset)
 
 
 def write_model(directory: str, text_config: dict, seed: int, branch_gain: float = 1.0,
-                qk_gain: float = 1.0) -> dict:
+                qk_gain: float = 1.0, share_layers: bool = False, zero_layer_codes: bool = False) -> dict:
     """A random-init Gemma 4 artifact in the mlx-lm layout (config.json + one safetensors
     shard): Q4/g64 projections of unit-gain rows; input, pre-feedforward and final norm
     weights bf16(1 + 0.1 N(0,1)); the post-attention and post-feedforward norms (the
     branches added to the residual stream) around branch_gain; q_norm and k_norm around
     qk_gain * head_dim^-1/4 (so the scale-1 attention scores have a standard deviation of
-    about qk_gain^2); layer scalars bf16(U(0.6, 1.0)). Returns the tensors written."""
+    about qk_gain^2); layer scalars bf16(U(0.6, 1.0)). share_layers writes the first sliding
+    and the first global layer's arrays again for every later layer of the same kind (a
+    48-layer artifact is then generated at the cost of two layers; each layer still has its
+    own tensors in the file). zero_layer_codes leaves every layer's packed codes as holes in
+    the file (all codes 0: each weight is its group's bias), which keeps a 6.6 GB artifact
+    cheap to write where only the byte traffic matters. Returns the tensors written."""
     import json
-    import os
     t = text_config
     rng = np.random.default_rng(seed)
     hidden, inter, heads = t["hidden_size"], t["intermediate_size"], t["num_attention_heads"]
@@ -170,8 +183,15 @@ def write_model(directory: str, text_config: dict, seed: int, branch_gain: float
         out[name] = bf16_bits(np.float32(around) + np.float32(spread) * rng.standard_normal(n).astype(np.float32))
 
     proj(P + "embed_tokens", t["vocab_size"], hidden)
+    first = {}
     for i, kind in enumerate(t["layer_types"]):
         sliding = kind == "sliding_attention"
+        if share_layers and kind in first:
+            src = f"{P}layers.{first[kind]}."
+            for name in [n for n in out if n.startswith(src)]:
+                out[f"{P}layers.{i}." + name[len(src):]] = out[name]
+            continue
+        first[kind] = i
         d = t["head_dim"] if sliding else t.get("global_head_dim", t["head_dim"])
         kvh = t["num_key_value_heads"] if sliding else t.get("num_global_key_value_heads", t["num_key_value_heads"])
         a = f"{P}layers.{i}.self_attn."
@@ -194,7 +214,10 @@ def write_model(directory: str, text_config: dict, seed: int, branch_gain: float
         out[m + "layer_scalar"] = bf16_bits(rng.uniform(0.6, 1.0, size=1).astype(np.float32))
     vec(P + "norm.weight", hidden)
     os.makedirs(directory, exist_ok=True)
-    write_safetensors(os.path.join(directory, "model.safetensors"), out)
+    holes = [n for n in out if zero_layer_codes and ".layers." in n and n.endswith("_proj.weight")]
+    write_safetensors(os.path.join(directory, "model.safetensors"), out, holes)
+    for n in holes:   # what the file holds there (a read-only view, no memory)
+        out[n] = np.broadcast_to(np.uint32(0), out[n].shape)
     with open(os.path.join(directory, "config.json"), "w") as f:
         json.dump({"model_type": "gemma4_unified", "tie_word_embeddings": True,
                    "quantization": {"group_size": 64, "bits": 4, "mode": "affine"}, "text_config": t}, f)

@@ -416,3 +416,28 @@ def test_residual_rms_norm_bit_exact(stream, m, hidden, scalar, nxt):
         en.close()
     for x in (bd, rd, wpd, wnd, scd, nd, hn):
         x.close()
+
+
+def test_decode_block_equals_single_steps(tmp_path):
+    """hyp_decode_block(n) (n graph replays in one call) ends where n calls of
+    hyp_decode_block(1) end: the same token, logit and near-tie count; two states of one
+    model each keep their own captured step."""
+    cfg = tiny_dims_config(512)
+    syn.write_model(str(tmp_path), cfg, seed=15, branch_gain=BRANCH_GAIN, qk_gain=QK_GAIN)
+    model = hy.Model(hy.geometry_from_config(cfg), str(tmp_path))
+    prompt = np.random.default_rng(10).integers(0, cfg["vocab_size"], size=30).astype(np.uint32)
+    res = hy.StepResult()
+    a, b = model.kvstate(), model.kvstate()
+    a.prefill(prompt, res)
+    b.prefill(prompt, res)
+    fa = a.decode(12, res)
+    ties = 0
+    for _ in range(12):
+        fb = b.decode(1, res)
+        ties += fb.near_tie_events
+    say(f"  block: token {fa.token_id} logit {fa.logit} ties {fa.near_tie_events}; steps: token {fb.token_id} "
+        f"ties {ties}")
+    assert (fa.token_id, fa.logit, fa.near_tie_events) == (fb.token_id, fb.logit, ties)
+    assert a.decode(3, res).token_id == b.decode(3, res).token_id
+    for h in (a, b, res, model):
+        h.close()
