@@ -53,6 +53,7 @@ EXPORTED = [
     "hyp_model_create", "hyp_model_free", "hyp_model_load", "hyp_kvstate_create", "hyp_kvstate_free",
     "hyp_prefill_chunk", "hyp_decode_block", "hyp_prefill_chunk_sampled", "hyp_decode_block_sampled",
     "hyp_step_result_create", "hyp_step_result_free", "hyp_step_result_fields", "hyp_model_forward_hidden",
+    "hyp_geometry_memory", "hyp_model_memory",
     "hyp_step_program_create", "hyp_step_program_run", "hyp_step_program_check", "hyp_step_program_free",
     "hyp_qmodel_load", "hyp_qmodel_free", "hyp_qmodel_num_layers",
     "hyp_qmodel_linear", "hyp_qmodel_embed",
@@ -209,6 +210,13 @@ class StepResultFields(ctypes.Structure):
     ]
 
 
+class MemoryReport(ctypes.Structure):
+    """HypMemoryReport: device bytes of a model and one KV state, quantization-aware."""
+    _fields_ = [(name, ctypes.c_uint64) for name in (
+        "weight_bytes", "norm_bytes", "kv_local_bytes", "kv_global_bytes", "state_bytes", "scratch_bytes",
+        "dense_bf16_weight_bytes")]
+
+
 _lib = None
 _P = ctypes.c_void_p
 _PP = ctypes.POINTER(ctypes.c_void_p)
@@ -283,6 +291,8 @@ def lib() -> ctypes.CDLL:
         "hyp_step_result_free": [_PP],
         "hyp_step_result_fields": [_P, ctypes.POINTER(StepResultFields)],
         "hyp_model_forward_hidden": [_P, _P, ctypes.POINTER(ctypes.c_uint32), _U32, _U32, _P],
+        "hyp_geometry_memory": [ctypes.POINTER(GeometryParams), ctypes.POINTER(MemoryReport)],
+        "hyp_model_memory": [_P, ctypes.POINTER(MemoryReport)],
         "hyp_step_program_create": [_P, _U32, _U32, _U32, _PP],
         "hyp_step_program_run": [_P, _P],
         "hyp_step_program_check": [_P],
@@ -748,6 +758,14 @@ def geometry_from_config(cfg: dict):
     return g, types
 
 
+def geometry_memory(geometry) -> MemoryReport:
+    """hyp_geometry_memory: what loading a model of this geometry and one state allocate."""
+    g = geometry[0] if isinstance(geometry, tuple) else geometry
+    r = MemoryReport()
+    call("hyp_geometry_memory", ctypes.byref(g), ctypes.byref(r))
+    return r
+
+
 class StepResult:
     """HypStepResult: a reusable per-step result handle."""
 
@@ -789,6 +807,11 @@ class Model:
 
     def kvstate(self) -> "KvState":
         return KvState(self)
+
+    def memory(self) -> MemoryReport:
+        r = MemoryReport()
+        call("hyp_model_memory", self.handle, ctypes.byref(r))
+        return r
 
     def close(self) -> None:
         if self.handle:

@@ -1157,6 +1157,33 @@ HypStatus hyp_step_result_fields(HypStepResult result, HypStepResultFields* out_
     });
 }
 
+namespace {
+void fill_report(const hyperion::model::MemoryReport& r, HypMemoryReport* out) {
+    out->weight_bytes = r.weight_bytes;
+    out->norm_bytes = r.norm_bytes;
+    out->kv_local_bytes = r.kv_local_bytes;
+    out->kv_global_bytes = r.kv_global_bytes;
+    out->state_bytes = r.state_bytes;
+    out->scratch_bytes = r.scratch_bytes;
+    out->dense_bf16_weight_bytes = r.dense_bf16_weight_bytes;
+}
+}  // namespace
+
+HypStatus hyp_geometry_memory(const HypGeometryParams* geometry, HypMemoryReport* out) {
+    return abi_call("hyp_geometry_memory", [&] {
+        REQUIRE_ARG(geometry != nullptr && out != nullptr, "geometry and out must be non-null");
+        fill_report(hyperion::model::plan_memory(hyperion::model::Geometry::from_abi(*geometry)), out);
+    });
+}
+
+HypStatus hyp_model_memory(HypModel model, HypMemoryReport* out) {
+    return abi_call("hyp_model_memory", [&] {
+        hyperion::model::Decoder& dec = loaded(model);
+        REQUIRE_ARG(out != nullptr, "out must be non-null");
+        fill_report(dec.memory(), out);
+    });
+}
+
 HypStatus hyp_model_forward_hidden(HypModel model, HypKvState kvstate, const uint32_t* ids, uint32_t count,
                                    uint32_t offset, uint16_t* hidden_out) {
     return abi_call("hyp_model_forward_hidden", [&] {

@@ -454,54 +454,68 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
 }
 
 // Merge the splits of each output row: weights 2^(m_s - max m), sum of l_s, divided sums.
-// One wave per row: lane s holds split s's (m, l); each lane then owns D/64 consecutive
-// dims and sums the splits' partial rows in split order (independent loads, pipelined).
+// One workgroup per row, every load issued at once: each wave reads all (m, l) (lane s
+// holds split s) and the partial rows of splits w, w + 4, ... (lane-owned dims); the four
+// wave sums meet in LDS and are added in wave order.
 template <uint32_t D>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p) {
+    constexpr uint32_t kWaves = kAttnThreads / 64u;
+    constexpr uint32_t kPer = D / 64u;
+    constexpr uint32_t kMaxPerWave = kAttnMaxSplits / kWaves;
+    __shared__ float acc[kWaves][D];
+    __shared__ float dens[kWaves];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint64_t rows = static_cast<uint64_t>(p.L) * p.H;
-    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * (kAttnThreads / 64u) + wave;
-    if (row >= rows) return;   // wave-uniform
+    const uint64_t row = blockIdx.x;
     float ms = -__builtin_huge_valf();
     float ls = 0.0f;
     if (lane < p.splits) {
         ms = p.part_ml[(lane * rows + row) * 2u];
         ls = p.part_ml[(lane * rows + row) * 2u + 1u];
     }
+    float part[kMaxPerWave][kPer];
+#pragma unroll
+    for (uint32_t u = 0; u < kMaxPerWave; ++u) {
+        const uint32_t sp = wave + kWaves * u;
+        const float* o = p.part_o + (sp * rows + row) * D + lane * kPer;
+#pragma unroll
+        for (uint32_t e = 0; e < kPer; ++e) part[u][e] = sp < p.splits ? o[e] : 0.0f;
+    }
     float mx = ms;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     const float w = ms == -__builtin_huge_valf() || mx == -__builtin_huge_valf() ? 0.0f : exp2f(ms - mx);
-    constexpr uint32_t kPer = D / 64u;
-    constexpr uint32_t kBatch = 8u;   // splits whose partial rows are loaded together
     float num[kPer];
 #pragma unroll
     for (uint32_t e = 0; e < kPer; ++e) num[e] = 0.0f;
     float den = 0.0f;
-    for (uint32_t s0 = 0; s0 < p.splits; s0 += kBatch) {
-        float part[kBatch][kPer];
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t sp = s0 + u;
-            const float* o = p.part_o + (sp * rows + row) * D + lane * kPer;
+    for (uint32_t u = 0; u < kMaxPerWave; ++u) {
+        const uint32_t sp = wave + kWaves * u;
+        const float ws = __shfl(w, static_cast<int>(sp), 64);
+        const float lw = __shfl(ls, static_cast<int>(sp), 64);
+        if (sp >= p.splits || ws == 0.0f) continue;   // uniform: past the splits, or an empty split
+        den += ws * lw;
 #pragma unroll
-            for (uint32_t e = 0; e < kPer; ++e) part[u][e] = sp < p.splits ? o[e] : 0.0f;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t sp = s0 + u;
-            const float ws = __shfl(w, static_cast<int>(sp & 63u), 64);
-            const float lw = __shfl(ls, static_cast<int>(sp & 63u), 64);
-            if (sp >= p.splits || ws == 0.0f) continue;   // uniform: past the splits, or an empty split
-            den += ws * lw;
-#pragma unroll
-            for (uint32_t e = 0; e < kPer; ++e) num[e] += ws * part[u][e];
-        }
+        for (uint32_t e = 0; e < kPer; ++e) num[e] += ws * part[u][e];
     }
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; ++e) acc[wave][lane * kPer + e] = num[e];
+    if (lane == 0u) dens[wave] = den;
+    __syncthreads();
+    if (wave != 0u) return;
+    float dt = 0.0f;
+#pragma unroll
+    for (uint32_t wv = 0; wv < kWaves; ++wv) dt += dens[wv];
     uint16_t* out = p.out + row * D + lane * kPer;
 #pragma unroll
-    for (uint32_t e = 0; e < kPer; ++e) out[e] = f32_to_bf16_bits(den > 0.0f ? num[e] / den : 0.0f);
+    for (uint32_t e = 0; e < kPer; ++e) {
+        float v = 0.0f;
+#pragma unroll
+        for (uint32_t wv = 0; wv < kWaves; ++wv) v += acc[wv][lane * kPer + e];
+        out[e] = f32_to_bf16_bits(dt > 0.0f ? v / dt : 0.0f);
+    }
 }
 
 // Tokens pos0 .. pos0 + n - 1 of k/v [n][KVH][D] -> cache slots pos % cap (only the last
@@ -649,7 +663,8 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
     }
     if (p.splits > 1u) {
         const uint64_t rows = static_cast<uint64_t>(a.L) * a.n_heads;
-        const dim3 grid(static_cast<uint32_t>((rows + kAttnThreads / 64u - 1u) / (kAttnThreads / 64u)));
+        HYP_REQUIRE(rows <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "attention: too many rows to combine");
+        const dim3 grid(static_cast<uint32_t>(rows));
         switch (a.head_dim) {
             case 64: hipLaunchKernelGGL(attn_combine_kernel<64>, grid, dim3(kAttnThreads), 0, stream, p); break;
             case 128: hipLaunchKernelGGL(attn_combine_kernel<128>, grid, dim3(kAttnThreads), 0, stream, p); break;

@@ -141,6 +141,94 @@ uint32_t Geometry::rotated_dims(LayerType kind) const noexcept {
     return rotated;
 }
 
+namespace {
+
+// The tiled resident allocation of one [n, k] projection (qlinear.cc make_storage).
+uint64_t q4_resident_bytes(uint64_t n, uint64_t k) {
+    const uint64_t tiles = (n + 15u) / 16u;
+    const uint64_t pairs = (k + 127u) / 128u;
+    const auto a256 = [](uint64_t v) { return (v + 255u) & ~uint64_t{255u}; };
+    return a256(tiles * pairs * 1024u) + a256(tiles * pairs * 128u);
+}
+
+uint32_t cache_capacity(const Geometry& g, LayerType kind) {
+    return kind == LayerType::Sliding ? std::min(g.window + kChunkTokens, g.max_positions) : g.max_positions;
+}
+
+uint64_t rope_table_bytes(const Geometry& g, uint32_t D) {
+    const uint64_t bytes = static_cast<uint64_t>(g.max_positions) * (D / 2u) * sizeof(float2);
+    return bytes > kRopeTableMaxBytes ? 0u : bytes;
+}
+
+}  // namespace
+
+MemoryReport plan_memory(const Geometry& g) {
+    MemoryReport r;
+    const uint64_t H = g.heads;
+    auto proj = [&](uint64_t n, uint64_t k) {
+        r.weight_bytes += q4_resident_bytes(n, k);
+        r.dense_bf16_weight_bytes += 2u * n * k;
+    };
+    proj(g.vocab, g.hidden);   // the embedding, tied as the LM head
+    for (LayerType kind : g.types) {
+        const bool sliding = kind == LayerType::Sliding;
+        const uint64_t D = sliding ? g.head_dim_local : g.head_dim_global;
+        const uint64_t kvh = sliding ? g.kv_heads_local : g.kv_heads_global;
+        proj(H * D, g.hidden);
+        proj(kvh * D, g.hidden);
+        if (sliding) proj(kvh * D, g.hidden);
+        proj(g.hidden, H * D);
+        proj(g.intermediate, g.hidden);
+        proj(g.intermediate, g.hidden);
+        proj(g.hidden, g.intermediate);
+        r.norm_bytes += 2u * (4u * g.hidden + 2u * D + 1u);
+        const uint64_t kv = 2u * static_cast<uint64_t>(cache_capacity(g, kind)) * kvh * D * 2u;
+        (sliding ? r.kv_local_bytes : r.kv_global_bytes) += kv;
+    }
+    r.norm_bytes += 2u * g.hidden;
+    r.state_bytes = sizeof(HypTopKSample) + 2u * sizeof(uint32_t);
+    const uint64_t T = kChunkTokens;
+    const uint64_t dmax = std::max(g.head_dim_local, g.head_dim_global);
+    const uint64_t kvmax = std::max(g.kv_heads_local * g.head_dim_local, g.kv_heads_global * g.head_dim_global);
+    r.scratch_bytes = T * 4u + 4u * T * g.hidden * 2u + 2u * T * H * dmax * 2u + 2u * T * kvmax * 2u +
+                      T * g.intermediate * 2u + static_cast<uint64_t>(g.hidden) * 2u +
+                      static_cast<uint64_t>(g.vocab) * 2u +
+                      std::max(hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
+                               hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)) +
+                      hip::sample_greedy_workspace_bytes() + rope_table_bytes(g, g.head_dim_local) +
+                      rope_table_bytes(g, g.head_dim_global);
+    return r;
+}
+
+MemoryReport Decoder::memory() const {
+    MemoryReport r;
+    auto lin = [&](const QuantizedLinear& q) {
+        r.weight_bytes += q.storage.bytes();
+        r.dense_bf16_weight_bytes += 2u * static_cast<uint64_t>(q.mat.n) * q.mat.k;
+    };
+    lin(w_.embed);
+    for (const LayerWeights& lw : w_.layers) {
+        lin(lw.q_proj);
+        lin(lw.k_proj);
+        if (lw.v_proj) lin(*lw.v_proj);
+        lin(lw.o_proj);
+        lin(lw.gate_proj);
+        lin(lw.up_proj);
+        lin(lw.down_proj);
+        for (const DeviceBuffer& b : lw.norms) r.norm_bytes += b.bytes();
+    }
+    r.norm_bytes += w_.final_norm.bytes();
+    for (const DeviceBuffer* b : {&ids_, &x_, &xn_, &q_, &k_, &v_, &attn_, &o_, &h_, &d_, &last_, &logits_, &attn_ws_,
+                                  &sample_ws_, &rope_local_, &rope_global_}) {
+        r.scratch_bytes += b->bytes();
+    }
+    const MemoryReport planned = plan_memory(geo_);   // a state is not allocated to be counted
+    r.kv_local_bytes = planned.kv_local_bytes;
+    r.kv_global_bytes = planned.kv_global_bytes;
+    r.state_bytes = planned.state_bytes;
+    return r;
+}
+
 GraphExec::~GraphExec() {
     if (exec_ != nullptr) (void)hipGraphExecDestroy(exec_);
 }
@@ -217,8 +305,8 @@ Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geome
                                      hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)));
     sample_ws_ = DeviceBuffer(hip::sample_greedy_workspace_bytes());
     const auto table = [&](uint32_t D, LayerType kind, double theta) {
-        const size_t bytes = static_cast<size_t>(g.max_positions) * (D / 2u) * sizeof(float2);
-        if (bytes > kRopeTableMaxBytes) return DeviceBuffer();
+        const size_t bytes = rope_table_bytes(g, D);
+        if (bytes == 0) return DeviceBuffer();
         DeviceBuffer t(bytes);
         hip::launch_rope_table(static_cast<float2*>(t.data()), g.max_positions, D, g.rotated_dims(kind),
                                static_cast<float>(theta), stream_);
@@ -245,7 +333,7 @@ DecoderState Decoder::make_state() const {
         const bool sliding = kind == LayerType::Sliding;
         c.head_dim = sliding ? g.head_dim_local : g.head_dim_global;
         c.kv_heads = sliding ? g.kv_heads_local : g.kv_heads_global;
-        c.cap = sliding ? std::min(g.window + kChunkTokens, g.max_positions) : g.max_positions;
+        c.cap = cache_capacity(g, kind);
         const size_t bytes = static_cast<size_t>(c.cap) * c.kv_heads * c.head_dim * 2u;
         c.k = DeviceBuffer(bytes);
         c.v = DeviceBuffer(bytes);

@@ -72,6 +72,20 @@ struct Geometry {
     [[nodiscard]] uint32_t rotated_dims(LayerType kind) const noexcept;
 };
 
+// HypMemoryReport's fields (the planned or the allocated device bytes).
+struct MemoryReport {
+    uint64_t weight_bytes = 0;
+    uint64_t norm_bytes = 0;
+    uint64_t kv_local_bytes = 0;
+    uint64_t kv_global_bytes = 0;
+    uint64_t state_bytes = 0;
+    uint64_t scratch_bytes = 0;
+    uint64_t dense_bf16_weight_bytes = 0;
+};
+
+// What a Decoder and one DecoderState allocate for `g`, from the geometry alone.
+MemoryReport plan_memory(const Geometry& g);
+
 struct LayerCache {
     DeviceBuffer k;   // [cap][kv_heads][head_dim] bf16
     DeviceBuffer v;
@@ -137,6 +151,8 @@ class Decoder {
     StepSample prefill(DecoderState& st, const uint32_t* ids, uint32_t count);
     // hyp_decode_block: n_tokens greedy steps from the cursor. Synchronous.
     StepSample decode(DecoderState& st, uint32_t n_tokens);
+    // The allocated buffers, summed (KV and state as make_state allocates them).
+    [[nodiscard]] MemoryReport memory() const;
 
   private:
     // embed + all layers over L <= kChunkTokens tokens whose ids are in device memory.

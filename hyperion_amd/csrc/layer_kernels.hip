@@ -41,30 +41,27 @@ struct PrepareParams {
     float eps;
 };
 
-// Lanes u < D/64 load head `src` unit u and leave bf16(w * bf16(x * inv)) (w null: bf16(x *
-// inv)) in xv; every lane takes part in the butterfly.
-// (All of the head's and the weight's loads are issued before the first use.)
-__device__ __forceinline__ void norm_head(const uint16_t* src, const uint16_t* w, uint32_t D, float eps,
-                                          uint32_t lane, uint4 (&xv)[8]) {
-    const uint32_t units = D / 64u;
-    float ss = 0.0f;
-    uint4 wv[8];
-    if (lane < units) {
+// Lanes u < D/64 hold 64-value unit u of a head (loaded by load_head); norm_loaded leaves
+// bf16(w * bf16(x * inv)) (no weight: bf16(x * inv)) there. Every lane takes part in the
+// butterfly. Loads are separate so a caller can issue all of its loads before any use.
+__device__ __forceinline__ void load_head(const uint16_t* src, uint32_t D, uint32_t lane, uint4 (&xv)[8]) {
+    if (lane < D / 64u) {
         const uint4* s4 = reinterpret_cast<const uint4*>(src) + lane * 8u;
-        const uint4* w4 = reinterpret_cast<const uint4*>(w != nullptr ? w : src) + lane * 8u;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            xv[t] = s4[t];
-            wv[t] = w4[t];
-        }
-        ss = unit_sumsq(xv);
+        for (int t = 0; t < 8; ++t) xv[t] = s4[t];
     }
+}
+
+__device__ __forceinline__ void norm_loaded(uint4 (&xv)[8], const uint4 (*wv)[8], uint32_t D, float eps,
+                                            uint32_t lane) {
+    const uint32_t units = D / 64u;
+    float ss = lane < units ? unit_sumsq(xv) : 0.0f;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
     const float inv = rms_inverse(ss, D, eps);
     if (lane < units) {
         normalize_unit(xv, inv);
-        if (w != nullptr) weight_unit(xv, wv);
+        if (wv != nullptr) weight_unit(xv, *wv);
     }
 }
 
@@ -107,27 +104,29 @@ __global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p)
     }
     if (active) {
         uint4 xv[8];
-        const uint16_t* src;
-        const uint16_t* w;
+        uint4 wv[8];
+        const uint32_t kh = hh - p.H;
+        const size_t kv_row = (static_cast<size_t>(t) * p.KVH + kh) * D;
         if (is_q) {
-            src = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
-            w = p.q_w;
             dst = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
+            load_head(dst, D, lane, xv);
+            load_head(p.q_w, D, lane, wv);
         } else {
-            const uint32_t kh = hh - p.H;
-            const size_t row = (static_cast<size_t>(t) * p.KVH + kh) * D;
-            // V: the weightless norm straight into the cache slot.
-            norm_head(p.v_raw != nullptr ? p.v_raw + row : p.k_raw + row, nullptr, D, p.eps, lane, xv);
+            // V: the weightless norm straight into the cache slot; its loads and K's are
+            // issued together.
+            uint4 vv[8];
+            load_head(p.v_raw != nullptr ? p.v_raw + kv_row : p.k_raw + kv_row, D, lane, vv);
+            load_head(p.k_raw + kv_row, D, lane, xv);
+            load_head(p.k_w, D, lane, wv);
+            norm_loaded(vv, nullptr, D, p.eps, lane);
             if (lane < D / 64u) {
                 uint4* v4 = reinterpret_cast<uint4*>(p.cache_v + (slot * p.KVH + kh) * D) + lane * 8u;
 #pragma unroll
-                for (int u = 0; u < 8; ++u) v4[u] = xv[u];
+                for (int u = 0; u < 8; ++u) v4[u] = vv[u];
             }
-            src = p.k_raw + row;
-            w = p.k_w;
             dst = p.cache_k + (slot * p.KVH + kh) * D;
         }
-        norm_head(src, w, D, p.eps, lane, xv);
+        norm_loaded(xv, &wv, D, p.eps, lane);
         if (lane < D / 64u) {
             uint4* h4 = reinterpret_cast<uint4*>(hb) + lane * 8u;
 #pragma unroll

@@ -501,6 +501,29 @@ HypStatus hyp_decode_block_sampled(HypModel model, HypKvState kvstate, uint32_t 
 HypStatus hyp_step_result_create(HypStepResult* out_result);
 HypStatus hyp_step_result_free(HypStepResult* result);
 HypStatus hyp_step_result_fields(HypStepResult result, HypStepResultFields* out_fields);
+/* Device memory of a model and one of its KV states, counted in the formats this library
+ * keeps resident: the quantization-aware replacement of the governor's weight estimate
+ * (peak_within_budget, governor.cc:601-640), which counts every weight at 2 bytes (bf16) and
+ * so puts the Q4/g64 12B at 24.7 GB instead of the 6.6 GB that is resident. */
+typedef struct HypMemoryReport {
+    uint64_t weight_bytes;              /* the Q4/g64 projections and the tied embedding / LM head
+                                         * in the tiled resident layout (0.5625 B per weight,
+                                         * plus padding to 16 rows and 128 columns) */
+    uint64_t norm_bytes;                /* norm vectors, layer scalars, the final norm (bf16) */
+    uint64_t kv_local_bytes;            /* one state's sliding-layer rings, K and V */
+    uint64_t kv_global_bytes;           /* one state's global-layer caches, K and V */
+    uint64_t state_bytes;               /* one state's sampled token and device counters */
+    uint64_t scratch_bytes;             /* the model's activation buffers for a 2048-token chunk,
+                                         * attention and sampling workspaces, RoPE tables */
+    uint64_t dense_bf16_weight_bytes;   /* the same projections at 2 bytes per weight */
+} HypMemoryReport;
+/* What hyp_model_load and one hyp_kvstate_create allocate for `geometry` (host only: no
+ * artifact, no device). */
+HypStatus hyp_geometry_memory(const HypGeometryParams* geometry, HypMemoryReport* out);
+/* The loaded model's allocations, summed buffer by buffer, with one state's KV as
+ * hyp_kvstate_create allocates it. */
+HypStatus hyp_model_memory(HypModel model, HypMemoryReport* out);
+
 /* ForwardPass::embed + forward (forward.cc:126-131, 543-563) as forward_test.cc drives it:
  * `count` host token ids at positions offset .. offset + count - 1, their K/V appended to
  * the state's caches, and the final-normalised hidden rows copied to hidden_out (host, bf16

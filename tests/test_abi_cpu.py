@@ -338,3 +338,29 @@ def test_step_result_lifecycle():
     ts = hy.TokenStream(None, 0, 1)
     assert _status("hyp_prefill_chunk", None, None, ctypes.byref(ts), None) == 1
     assert _status("hyp_decode_block", None, None, 1, None) == 1
+
+
+def test_geometry_memory_is_quantization_aware():
+    """hyp_geometry_memory on the 12B geometry (geometry.rs:466-500): every projection shape is
+    a multiple of 16 rows and 128 columns, so the tiled Q4/g64 layout holds exactly 0.5625 B
+    per weight - 6.70 GB for 40 sliding and 8 global layers plus the tied 262144 x 3840 table,
+    against the 24.7 GB of governor.cc:601-640's dense bf16 formula (4 h^2 + 3 h i per layer)."""
+    from hyperion_amd import synthetic as syn
+    cfg = syn.gemma4_text_config()
+    g, types = hy.geometry_from_config(cfg)
+    r = hy.geometry_memory((g, types))
+    h, inter, H = 3840, 15360, 16
+    sl = [(H * 256, h), (8 * 256, h), (8 * 256, h), (h, H * 256), (inter, h), (inter, h), (h, inter)]
+    gl = [(H * 512, h), (1 * 512, h), (h, H * 512), (inter, h), (inter, h), (h, inter)]
+    n_gl = cfg["layer_types"].count("full_attention")
+    assert n_gl == 8
+    weights = (262144 * h + 40 * sum(n * k for n, k in sl) + 8 * sum(n * k for n, k in gl))
+    assert r.weight_bytes * 16 == weights * 9          # 0.5625 B per weight, exactly
+    assert r.dense_bf16_weight_bytes == 2 * weights
+    assert r.norm_bytes == 2 * (40 * (4 * h + 2 * 256 + 1) + 8 * (4 * h + 2 * 512 + 1) + h)
+    assert r.kv_local_bytes == 40 * 2 * (1024 + 2048) * 8 * 256 * 2
+    assert r.kv_global_bytes == 8 * 2 * 262144 * 1 * 512 * 2
+    governor_dense = 2 * (262144 * h + 48 * (4 * h * h + 3 * h * inter))
+    assert round(governor_dense / 1e9, 1) == 24.7 and round(r.weight_bytes / 1e9, 2) == 6.70
+    g.layer_types = None
+    assert _status("hyp_geometry_memory", ctypes.byref(g), ctypes.byref(r)) == 1

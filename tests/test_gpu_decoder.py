@@ -441,3 +441,23 @@ def test_decode_block_equals_single_steps(tmp_path):
     assert a.decode(3, res).token_id == b.decode(3, res).token_id
     for h in (a, b, res, model):
         h.close()
+
+
+def test_model_memory_matches_the_geometry_plan(tiny, tmp_path):
+    """hyp_model_memory (the loaded model's buffers, summed) equals hyp_geometry_memory (the
+    plan from the geometry alone), field by field, on the fixture and on 12B-shaped layers."""
+    model, T, cfg = tiny
+    got = model.memory()
+    plan = hy.geometry_memory(hy.geometry_from_config(cfg))
+    for f, _ in hy.MemoryReport._fields_:
+        assert getattr(got, f) == getattr(plan, f), f
+    cfg12 = syn.gemma4_text_config(num_layers=2, vocab=1024, max_positions=2048,
+                                   layer_types=["sliding_attention", "full_attention"])
+    syn.write_model(str(tmp_path), cfg12, seed=16)
+    m12 = hy.Model(hy.geometry_from_config(cfg12), str(tmp_path))
+    got, plan = m12.memory(), hy.geometry_memory(hy.geometry_from_config(cfg12))
+    say(f"  12B-shaped 2 layers: weights {got.weight_bytes} B (dense bf16 {got.dense_bf16_weight_bytes} B), "
+        f"scratch {got.scratch_bytes} B")
+    for f, _ in hy.MemoryReport._fields_:
+        assert getattr(got, f) == getattr(plan, f), f
+    m12.close()
