@@ -18,6 +18,10 @@ Also reported, each on its own workload:
               sidecar on the device, m = 1 and 4, replayed from a captured HIP graph
               (tokens/s and effective HBM GB/s); the head timed alone (per-layer figures);
               and the layer stack as one decode-step program launch
+  model       the whole decoder through the model-level entry points on a synthetic 12B
+              artifact: a 1024-token prefill (tokens/s) and 32 greedy decode tokens from
+              that context (ms per token: norms, RoPE, attention over the KV caches, all
+              projections, LM head and sampling)
 and the oracle's restatement of MLX's CPU quantized_matmul timed on this host's cores
 (cpu_baseline).
 
@@ -291,7 +295,7 @@ def artifact_dir(min_free_bytes):
     return None
 
 
-def bench_model_decode(prompt_len, n_decode, layers):
+def bench_model_decode(prompt_len, n_decode, layers, host_launch=False):
     """The product's model-level path on a synthetic 12B artifact (48 layers, tied LM head
     [262144,3840], 6.6 GB of Q4/g64; the layers' codes are zero, their scales, biases, norms
     and the embedding random, so every byte is still streamed): hyp_model_load,
@@ -299,7 +303,10 @@ def bench_model_decode(prompt_len, n_decode, layers):
     prompt_len-token prompt (2048-token chunks), then hyp_decode_block of n_decode greedy
     tokens in one call - embed, every layer's norms, q/k/v, RoPE, KV cache append,
     attention over the cached context, o, MLP and residual sandwich, final norm, softcap
-    LM head and greedy sampling, all on the device, one host round trip per call."""
+    LM head and greedy sampling, all on the device, one host round trip per call.
+    host_launch: the n_decode tokens go through hyp_model_forward_hidden one at a time instead
+    (every kernel of a decode step but the LM head and the sampler, launched from the host,
+    not replayed from the step's graph), for kernel traces."""
     import shutil
     cfg = syn.gemma4_text_config(num_layers=layers, max_positions=max(8192, prompt_len + n_decode + 16))
     d = artifact_dir(8 << 30)
@@ -325,10 +332,18 @@ def bench_model_decode(prompt_len, n_decode, layers):
     t0 = time.perf_counter()
     st.prefill(prompt, res)
     prefill_s = time.perf_counter() - t0
-    st.decode(2, res)
-    t0 = time.perf_counter()
-    f = st.decode(n_decode, res)
-    decode_s = time.perf_counter() - t0
+    if host_launch:
+        nxt = np.random.default_rng(23).integers(0, cfg["vocab_size"], size=n_decode).astype(np.uint32)
+        t0 = time.perf_counter()
+        for j in range(n_decode):
+            st.forward_hidden(nxt[j:j + 1], prompt_len + j)
+        decode_s = time.perf_counter() - t0
+        f = res.fields()
+    else:
+        st.decode(2, res)
+        t0 = time.perf_counter()
+        f = st.decode(n_decode, res)
+        decode_s = time.perf_counter() - t0
     st.close()
     res.close()
     model.close()
@@ -339,6 +354,7 @@ def bench_model_decode(prompt_len, n_decode, layers):
         n_global * sum(q4_bytes(n, k) for n, k in gl) + q4_bytes(syn.VOCAB, HIDDEN)
     ms = decode_s * 1e3 / n_decode
     out = {"layers": layers, "prompt_tokens": prompt_len, "decode_tokens": n_decode,
+           "decode_launch": "host, hyp_model_forward_hidden (no LM head)" if host_launch else "graph replay",
            "prefill_tokens_per_s": round(prompt_len / prefill_s, 1), "prefill_s": round(prefill_s, 4),
            "decode_ms_per_token": round(ms, 4), "decode_tokens_per_s": round(1e3 / ms, 1),
            "weight_bytes": weight_bytes, "weight_stream_gbs": round(weight_bytes / ms / 1e6, 1),
@@ -447,6 +463,8 @@ def main():
     ap.add_argument("--only-model", action="store_true",
                     help="the headline decode GEMV and the model-level prefill + decode")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens of the model-level run")
+    ap.add_argument("--model-host-launch", action="store_true",
+                    help="model-level decode tokens launched from the host (for kernel traces)")
     ap.add_argument("--dense-ref", action="store_true",
                     help="also time hipBLASLt's dense bf16 GEMM (torch.matmul) on the prefill shapes")
     ap.add_argument("--dense-child", type=int, default=0, help=argparse.SUPPRESS)
@@ -488,7 +506,7 @@ def main():
         extra["decode_stream"] = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
     elif args.only_model:
-        extra["model_decode"] = bench_model_decode(args.prompt, 32, args.layers)
+        extra["model_decode"] = bench_model_decode(args.prompt, 32, args.layers, args.model_host_launch)
     elif not args.only_decode:
         extra["quantize"] = bench_quantize(stream, 50, 5)
         extra["sample_greedy"] = bench_sample(stream, 20, 3)
@@ -497,6 +515,7 @@ def main():
         streams = [bench_decode_stream(model, m, 10, 2, stream) for m in (1, 4)]
         model.close()
         extra["decode_stream"] = streams
+        extra["model_decode"] = bench_model_decode(args.prompt, 32, args.layers)
     cpu, cpu_par = (None, None) if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     per = dec["ms_per_launch"]
