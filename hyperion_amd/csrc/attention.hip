@@ -148,30 +148,53 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
     const uint8_t* qrow = lds + Lds::kQ + (wave * 16u + j16) * Lds::kRow;   // A operand row (i = j16)
     uint8_t* prow_w = lds + Lds::kP + wave * 16u * Lds::kPRow;             // this wave's P [16][32]
 
+    // K and V of a key block: thread tid takes chunks tid + 256 u (key c / (D/8), chunk c %
+    // (D/8): coalesced rows). The next block's chunks are loaded into registers while the
+    // current block computes; staging writes K rows and V^T (8 values per chunk, in an order
+    // rotated by the lane, which spreads a wave's 16-bit writes over the banks).
+    constexpr uint32_t kPer = kKeyBlock * kChunks / kAttnThreads;
+    uint4 kn[kPer];
+    uint4 vn[kPer];
+    const auto fetch = [&](uint32_t jb_) {
+        const uint32_t nk_ = min(kKeyBlock, j_end - jb_);
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            const uint32_t c = tid + kAttnThreads * u;
+            const uint32_t r = c / kChunks;
+            const uint32_t ch = c - r * kChunks;
+            kn[u] = make_uint4(0u, 0u, 0u, 0u);
+            vn[u] = make_uint4(0u, 0u, 0u, 0u);
+            if (r < nk_) {
+                kn[u] = *reinterpret_cast<const uint4*>(key_row(p, p.k, p.ck, jb_ + r, hk, D) + ch * 8u);
+                vn[u] = *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb_ + r, hk, D) + ch * 8u);
+            }
+        }
+    };
+    if (j_begin < j_end) fetch(j_begin);
+
     for (uint32_t jb = j_begin; jb < j_end; jb += kKeyBlock) {
         const uint32_t nk = min(kKeyBlock, j_end - jb);
         __syncthreads();   // the previous block's K/V reads are done (and Q is staged)
-        // K rows -> LDS, V rows -> LDS transposed.
-        for (uint32_t c = tid; c < kKeyBlock * kChunks; c += kAttnThreads) {
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            const uint32_t c = tid + kAttnThreads * u;
             const uint32_t r = c / kChunks;
             const uint32_t ch = c - r * kChunks;
-            uint4 kv = make_uint4(0u, 0u, 0u, 0u);
-            uint4 vv = make_uint4(0u, 0u, 0u, 0u);
-            if (r < nk) {
-                kv = *reinterpret_cast<const uint4*>(key_row(p, p.k, p.ck, jb + r, hk, D) + ch * 8u);
-                vv = *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u);
-            }
-            *reinterpret_cast<uint4*>(lds + Lds::kK + r * Lds::kRow + ch * 16u) = kv;
-            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+            *reinterpret_cast<uint4*>(lds + Lds::kK + r * Lds::kRow + ch * 16u) = kn[u];
+            const uint4 vv = vn[u];
+            uint8_t* col = lds + Lds::kVt + (ch * 8u) * Lds::kVtRow + r * 2u;
 #pragma unroll
-            for (uint32_t e = 0; e < 4; ++e) {
-                const uint32_t d0 = ch * 8u + 2u * e;
-                *reinterpret_cast<uint16_t*>(lds + Lds::kVt + d0 * Lds::kVtRow + r * 2u) = static_cast<uint16_t>(w[e]);
-                *reinterpret_cast<uint16_t*>(lds + Lds::kVt + (d0 + 1u) * Lds::kVtRow + r * 2u) =
-                    static_cast<uint16_t>(w[e] >> 16);
+            for (uint32_t s2 = 0; s2 < 8u; ++s2) {
+                const uint32_t e = (s2 + lane) & 7u;
+                const uint32_t d01 = (e & 2u) ? vv.y : vv.x;
+                const uint32_t d23 = (e & 2u) ? vv.w : vv.z;
+                const uint32_t dw = (e & 4u) ? d23 : d01;
+                *reinterpret_cast<uint16_t*>(col + e * Lds::kVtRow) =
+                    static_cast<uint16_t>((e & 1u) ? (dw >> 16) : (dw & 0xFFFFu));
             }
         }
         __syncthreads();
+        if (jb + kKeyBlock < j_end) fetch(jb + kKeyBlock);   // in flight during this block
 
         // S = Q K^T for the wave's 16 rows x 32 keys (two column tiles of 16 keys).
         f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
