@@ -192,7 +192,7 @@ MemoryReport plan_memory(const Geometry& g) {
     const uint64_t kvmax = std::max(g.kv_heads_local * g.head_dim_local, g.kv_heads_global * g.head_dim_global);
     r.scratch_bytes = T * 4u + 4u * T * g.hidden * 2u + 2u * T * H * dmax * 2u + 2u * T * kvmax * 2u +
                       T * g.intermediate * 2u + static_cast<uint64_t>(g.hidden) * 2u +
-                      static_cast<uint64_t>(g.vocab) * 2u +
+                      uint64_t{hip::kSkinnyMaxM} * g.hidden * 2u + static_cast<uint64_t>(g.vocab) * 2u +
                       std::max(hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
                                hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)) +
                       hip::sample_greedy_workspace_bytes() + rope_table_bytes(g, g.head_dim_local) +
@@ -218,7 +218,7 @@ MemoryReport Decoder::memory() const {
         for (const DeviceBuffer& b : lw.norms) r.norm_bytes += b.bytes();
     }
     r.norm_bytes += w_.final_norm.bytes();
-    for (const DeviceBuffer* b : {&ids_, &x_, &xn_, &q_, &k_, &v_, &attn_, &o_, &h_, &d_, &last_, &logits_, &attn_ws_,
+    for (const DeviceBuffer* b : {&ids_, &x_, &xn_, &xr_, &q_, &k_, &v_, &attn_, &o_, &h_, &d_, &last_, &logits_, &attn_ws_,
                                   &sample_ws_, &rope_local_, &rope_global_}) {
         r.scratch_bytes += b->bytes();
     }
@@ -292,6 +292,7 @@ Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geome
     ids_ = DeviceBuffer(T * sizeof(uint32_t));
     x_ = DeviceBuffer(T * g.hidden * 2u);
     xn_ = DeviceBuffer(T * g.hidden * 2u);
+    xr_ = DeviceBuffer(size_t{hip::kSkinnyMaxM} * g.hidden * 2u);
     q_ = DeviceBuffer(T * g.heads * dmax * 2u);
     k_ = DeviceBuffer(T * kvmax * 2u);
     v_ = DeviceBuffer(T * kvmax * 2u);
@@ -385,6 +386,14 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
     // the standalone norm); above them the input norm is a pass of its own, fused into the
     // previous layer's closing residual kernel.
     const bool norm_in_qkv = L <= hip::kSkinnyMaxM && hip::skinny_norm_supported(L, g.hidden);
+    // And a layer's closing residual update (x + rms(d) * w_post_ff, times the layer
+    // scalar) runs in the prologue of the next layer's q/k/v launch, which writes the
+    // updated stream to the other of two buffers (x_, xr_); the last layer's close is a
+    // residual kernel that also forms the final norm. Same bits as the separate kernels.
+    // (In the fused gate/up's prologue the attention half's close measured slower than its
+    // own kernel: that launch runs about two rounds of workgroups, each paying it.)
+    const bool fuse_residual = norm_in_qkv && hip::skinny_resid_supported(L, g.hidden);
+    uint16_t* other = u16(xr_);   // fuse_residual: the buffer the next prologue writes
 
     // ForwardPass::embed (forward.cc:126-131): gathered rows dequantized, times bf16(sqrt(hidden)).
     hip::launch_q4_dequantize_tiled(w_.embed.mat, d_ids, L, embed_scale_, x, s);
@@ -403,7 +412,13 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
         const hip::Q4Matrix* ws[3] = {&lw.q_proj.mat, &lw.k_proj.mat, sliding ? &lw.v_proj->mat : nullptr};
         uint16_t* ys[3] = {u16(q_), u16(k_), u16(v_)};
         const uint32_t count = sliding ? 3u : 2u;
-        if (norm_in_qkv) {
+        if (fuse_residual && i > 0) {
+            const LayerWeights& prev = w_.layers[i - 1];
+            const hip::SkinnyResidual res{u16(d_), x, other, prev.norm(LayerNorm::kPostFeedforward),
+                                          prev.norm(LayerNorm::kScalar)};
+            hip::launch_q4_skinny_group(ws, ys, count, x, L, &eps, lw.norm(LayerNorm::kInput), s, &res);
+            std::swap(x, other);
+        } else if (norm_in_qkv) {
             hip::launch_q4_skinny_group(ws, ys, count, x, L, &eps, lw.norm(LayerNorm::kInput), s);
         } else if (hip::skinny_supported(L, g.hidden, false)) {
             hip::launch_q4_skinny_group(ws, ys, count, xn, L, nullptr, nullptr, s);
@@ -466,6 +481,19 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
         // mlp (forward.cc:338-343), the feed-forward half and the layer scalar (:527-539).
         mlp_gate_up(lw.gate_proj, lw.up_proj, xn, L, u16(h_), s);
         lw.down_proj.apply(u16(h_), L, u16(d_), s);
+        if (fuse_residual) {
+            if (i + 1 < w_.layers.size()) continue;   // closed by the next layer's q/k/v launch
+            // The last close, with final_norm (forward.cc:133-135) as its next norm.
+            const uint16_t* fw = static_cast<const uint16_t*>(w_.final_norm.data());
+            uint16_t* fin = final_rows != nullptr ? final_rows : (L == 1u ? u16(last_) : nullptr);
+            hip::launch_residual_norm(u16(d_), x, lw.norm(LayerNorm::kPostFeedforward), lw.norm(LayerNorm::kScalar),
+                                      fin != nullptr ? fw : nullptr, fin, L, g.hidden, eps, s);
+            if (fin == nullptr) {
+                hip::launch_rms_normalize(x + static_cast<size_t>(L - 1) * g.hidden, fw, 1, g.hidden, eps,
+                                          u16(last_), s);
+            }
+            return;
+        }
         const uint16_t* next_w =
             !norm_in_qkv && i + 1 < w_.layers.size() ? w_.layers[i + 1].norm(LayerNorm::kInput) : nullptr;
         hip::launch_residual_norm(u16(d_), x, lw.norm(LayerNorm::kPostFeedforward), lw.norm(LayerNorm::kScalar),

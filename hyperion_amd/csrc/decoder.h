@@ -174,6 +174,7 @@ class Decoder {
     float softcap_ = 0.0f;       // bf16(final_logit_softcapping)
     DeviceBuffer ids_;           // uint32 [kChunkTokens]
     DeviceBuffer x_, xn_, q_, k_, v_, attn_, o_, h_, d_, last_, logits_;
+    DeviceBuffer xr_;            // [kSkinnyMaxM][hidden]: the residual stream's second buffer at decode sizes
     DeviceBuffer attn_ws_, sample_ws_;
     // RoPE (cos, sin) of every position per layer kind, computed once on the device with
     // the rope kernel's arithmetic (a 12B at 262144 positions: 0.8 GB); empty when larger

@@ -50,8 +50,21 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
 // ys[i][m, n_i] = x . dequant(W_i)^T. With rms_eps non-null each x row is first
 // rms-normalised (q4_rmsnorm.h; the same bits as launch_rms_normalize with norm_w) in LDS;
 // norm_w is the norm's bf16 weight [k] or null.
+// With res non-null (and rms_eps), the rows normalised are the sandwich's output x =
+// bf16(res->in + rms_norm(res->branch, res->w)) (times *res->scalar when non-null) - the
+// bits of launch_residual_norm - written to res->out by one workgroup; x is unused.
+struct SkinnyResidual {
+    const uint16_t* branch;   // [m][k]
+    const uint16_t* in;       // [m][k], the residual stream
+    uint16_t* out;            // [m][k], the updated residual stream (not `in`)
+    const uint16_t* w;        // [k] the branch's post-norm weight
+    const uint16_t* scalar;   // bf16 [1] or null
+};
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                            uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream);
+                            uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream,
+                            const SkinnyResidual* res = nullptr);
+// Whether launch_q4_skinny_group takes a residual at (m, k): every unit held by one thread.
+bool skinny_resid_supported(uint32_t m, uint32_t k);
 // Splits for `tiles` 16-row tiles, `pairs` group pairs and m rows of one launch form,
 // and whether (m, k) fits the kernel's LDS staging.
 enum class SkinnyForm : int {

@@ -52,8 +52,12 @@
 namespace hyperion::hip {
 namespace {
 
-// NORM: x rows are first rms-normalised (q4_rmsnorm.h) in LDS; the matmul then runs on
+// NORM 1: x rows are first rms-normalised (q4_rmsnorm.h) in LDS; the matmul then runs on
 // the normalised rows, which are not written back.
+// NORM 2: the sandwich close of the previous block first: x = in + rms(branch) * res_w
+// (times res_scalar when given), in residual_norm_kernel's arithmetic, recomputed by every
+// workgroup from the same inputs; workgroup 0 writes x to res_out, and the matmul runs on
+// rms(x) as with NORM 1. ctr[3..5] order the branch's statistics.
 //
 // Staging: thread u < M * G owns the 64-element unit (row u / G, group u % G) while
 // M * G <= threads; the staging waves are the waves holding units (at least M of them
@@ -64,8 +68,11 @@ namespace {
 // (virtual tile 2t is gate tile t, 2t + 1 up tile t), so both halves of a row tile are
 // in one workgroup; each wave computes one matrix exactly as a plain launch does, and the
 // gate tile's waves combine with the up tile's rows in LDS for the GELU epilogue.
-template <int M, bool DUAL, int EPI, int P, int NWAVE, bool NORM, bool LOOP>
-__global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
+template <int M, bool DUAL, int EPI, int P, int NWAVE, int NORM, bool LOOP>
+// NORM 2 is held to 128 registers (four waves per SIMD, two 8-wave workgroups per compute
+// unit), the occupancy of the other forms.
+__global__ __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu(NORM == 2 ? 4 : 1))) void q4_skinny_kernel(
+    SkinnyParams p) {
     constexpr int NW = 1;
     constexpr uint32_t kThreads = 64u * NWAVE;
     extern __shared__ __attribute__((aligned(16))) uint4 smem[];
@@ -82,8 +89,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     uint4* zs = smem + M * WS;                                     // [WS] zeros
     float4* sx = reinterpret_cast<float4*>(zs + WS);               // [G] group sums of x rows 0..3
     float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][M][16]
-    uint32_t* ctr = reinterpret_cast<uint32_t*>(red + NWAVE * M * kTileRows);   // [4]
-    float* part = reinterpret_cast<float*>(ctr + 4);               // NORM: [M][G] unit partials, [M] inverses
+    uint32_t* ctr = reinterpret_cast<uint32_t*>(red + NWAVE * M * kTileRows);   // [8]
+    float* part = reinterpret_cast<float*>(ctr + 8);               // NORM: [M][G] unit partials, [M] inverses
     float* comb = part + (NORM ? M * G + M : 0u);                  // DUAL: [NWAVE / 2][M][16] up rows
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -142,21 +149,156 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     const uint32_t nstage = max((min(units, kThreads) + 63u) / 64u, NORM ? static_cast<uint32_t>(M) : 1u);
     const bool stager = wave < nstage;
 
-    // x first: thread u's unit is requested before any weight load of the workgroup.
+    // x first: thread u's unit is requested before any weight load of the workgroup. With a
+    // residual (NORM 2) the staging waves instead run the whole prologue before issuing
+    // their weight loads, so that the branch, residual and weight units are never live
+    // beside two weight batches (the registers of both would halve the waves per SIMD).
     const uint32_t xu0 = threadIdx.x;   // first (row, group) unit this thread stages
+    constexpr bool resid = NORM == 2;
     uint4 xv[8];
-    if (xu0 < units) {
-        const uint32_t m = unit_row<M>(xu0, G);
-        const uint32_t g = xu0 - m * G;
-        const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+    if constexpr (!resid) {
+        if (xu0 < units) {
+            const uint32_t m = unit_row<M>(xu0, G);
+            const uint32_t g = xu0 - m * G;
+            const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xv[t] = src[t];
+            for (int t = 0; t < 8; ++t) xv[t] = src[t];
+        }
     }
-    if (threadIdx.x < 4u) ctr[threadIdx.x] = 0u;
+    if (threadIdx.x < 8u) ctr[threadIdx.x] = 0u;
     if constexpr (kLaneGroups)
         for (uint32_t t = threadIdx.x; t < WS; t += kThreads) zs[t] = uint4{0u, 0u, 0u, 0u};
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
     __builtin_amdgcn_s_barrier();         // no memory wait: only orders the issue
+
+    auto stage_x = [&]() {
+        if (stager) {
+            if constexpr (NORM) {
+                if constexpr (resid) {
+                    // The branch's norm (phases 3, 4), the residual add, then x's statistics
+                    // below; each row's inverse is formed by one wave, in residual_norm_kernel's
+                    // order. Every unit is held by one thread (checked on the host).
+                    uint4 rv[8];
+                    uint4 wrv[8];
+                    if (xu0 < units) {   // the branch first: its statistics need only it
+                        const uint32_t m = unit_row<M>(xu0, G);
+                        const uint32_t g = xu0 - m * G;
+                        const size_t off = static_cast<size_t>(m) * k + g * 64u;
+                        const uint4* bsrc = reinterpret_cast<const uint4*>(p.res_branch + off);
+                        const uint4* rsrc = reinterpret_cast<const uint4*>(p.res_in + off);
+                        const uint4* wsrc = reinterpret_cast<const uint4*>(p.res_w + g * 64u);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) xv[t] = bsrc[t];
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) rv[t] = rsrc[t];
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) wrv[t] = wsrc[t];
+                    }
+                    if (xu0 < units) part[xu0] = unit_sumsq(xv);
+                    raise_counter(ctr + 3, lane);
+                    wait_counter(ctr + 3, nstage);
+                    if (wave < static_cast<uint32_t>(M)) {
+                        const float ss = row_sumsq(part + wave * G, G, lane);
+                        if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+                    }
+                    raise_counter(ctr + 4, lane);
+                    wait_counter(ctr + 4, nstage);
+                    float ssx = 0.0f;
+                    if (xu0 < units) {
+                        const uint32_t m = unit_row<M>(xu0, G);
+                        const uint32_t g = xu0 - m * G;
+                        normalize_unit(xv, part[units + m]);
+                        weight_unit(xv, wrv);
+                        const float sc = p.res_scalar != nullptr ? bf16_bits_to_f32(*p.res_scalar) : 1.0f;
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
+                            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
+                                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
+                                if (p.res_scalar != nullptr) {
+                                    lo = round_bf16(lo * sc);
+                                    hi = round_bf16(hi * sc);
+                                }
+                                hw[q] = cvt_pk_bf16(lo, hi);
+                            }
+                            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                        }
+                        if (blockIdx.x == 0u) {
+                            uint4* dst = reinterpret_cast<uint4*>(p.res_out + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                            for (int t = 0; t < 8; ++t) dst[t] = xv[t];
+                        }
+                        ssx = unit_sumsq(xv);
+                    }
+                    raise_counter(ctr + 5, lane);   // every wave has read its inverse
+                    wait_counter(ctr + 5, nstage);
+                    if (xu0 < units) part[xu0] = ssx;
+                } else {
+                // Per-unit sums of squares, then one wave per row forms its inverse rms.
+                for (uint32_t u = xu0; u < units; u += kThreads) {
+                    if (u != xu0) {
+                        const uint32_t m = unit_row<M>(u, G);
+                        const uint32_t g = u - m * G;
+                        const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) xv[t] = src[t];
+                    }
+                    part[u] = unit_sumsq(xv);
+                }
+                }
+                raise_counter(ctr + 1, lane);
+                wait_counter(ctr + 1, nstage);
+                if (wave < static_cast<uint32_t>(M)) {
+                    const float ss = row_sumsq(part + wave * G, G, lane);
+                    if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+                }
+                raise_counter(ctr + 2, lane);
+                wait_counter(ctr + 2, nstage);
+            }
+
+            // Stage x: each thread permutes whole groups (8 words) and sums them.
+            for (uint32_t u = xu0; u < units; u += kThreads) {
+                const uint32_t m = unit_row<M>(u, G);
+                const uint32_t g = u - m * G;
+                if (u != xu0 || (NORM && units > kThreads)) {   // never with a residual
+                    const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xv[t] = src[t];
+                }
+                if constexpr (NORM) {
+                    normalize_unit(xv, part[units + m]);
+                    if (p.norm_w != nullptr) {
+                        const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w + g * 64u);
+                        uint4 wv[8];
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
+                        weight_unit(xv, wv);
+                    }
+                }
+                float s0 = 0.0f;
+                float s1 = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    uint4 o;
+                    o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
+                    o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
+                    o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
+                    o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
+                    xs[m * WS + g * 8u + t] = o;
+                    s0 = dot2_bf16(xv[t].x, kOnePair, s0);
+                    s1 = dot2_bf16(xv[t].y, kOnePair, s1);
+                    s0 = dot2_bf16(xv[t].z, kOnePair, s0);
+                    s1 = dot2_bf16(xv[t].w, kOnePair, s1);
+                }
+                reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
+            }
+            raise_counter(ctr, lane);
+        }
+    };
+    if constexpr (resid) stage_x();
 
     const uint32_t c_bytes = tiles * pairs * 1024u;
     const uint32_t s_bytes = tiles * pairs * 128u;
@@ -191,67 +333,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
     for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
 
-    if (stager) {
-        if constexpr (NORM) {
-            // Per-unit sums of squares, then one wave per row forms its inverse rms.
-            for (uint32_t u = xu0; u < units; u += kThreads) {
-                if (u != xu0) {
-                    const uint32_t m = unit_row<M>(u, G);
-                    const uint32_t g = u - m * G;
-                    const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) xv[t] = src[t];
-                }
-                part[u] = unit_sumsq(xv);
-            }
-            raise_counter(ctr + 1, lane);
-            wait_counter(ctr + 1, nstage);
-            if (wave < static_cast<uint32_t>(M)) {
-                const float ss = row_sumsq(part + wave * G, G, lane);
-                if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
-            }
-            raise_counter(ctr + 2, lane);
-            wait_counter(ctr + 2, nstage);
-        }
-
-        // Stage x: each thread permutes whole groups (8 words) and sums them.
-        for (uint32_t u = xu0; u < units; u += kThreads) {
-            const uint32_t m = unit_row<M>(u, G);
-            const uint32_t g = u - m * G;
-            if (u != xu0 || (NORM && units > kThreads)) {
-                const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) xv[t] = src[t];
-            }
-            if constexpr (NORM) {
-                normalize_unit(xv, part[units + m]);
-                if (p.norm_w != nullptr) {
-                    const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w + g * 64u);
-                    uint4 wv[8];
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
-                    weight_unit(xv, wv);
-                }
-            }
-            float s0 = 0.0f;
-            float s1 = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                uint4 o;
-                o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
-                o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
-                o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
-                o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
-                xs[m * WS + g * 8u + t] = o;
-                s0 = dot2_bf16(xv[t].x, kOnePair, s0);
-                s1 = dot2_bf16(xv[t].y, kOnePair, s1);
-                s0 = dot2_bf16(xv[t].z, kOnePair, s0);
-                s1 = dot2_bf16(xv[t].w, kOnePair, s1);
-            }
-            reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
-        }
-        raise_counter(ctr, lane);
-    }
+    if constexpr (!resid) stage_x();
     wait_counter(ctr, nstage);
 
     // Opaque VGPR values, so (w & mask) | bits selects v_and_or_b32 (see and_or).
@@ -309,13 +391,13 @@ size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool 
     const size_t G = k / 64u;
     // x rows and a zero row, group sums, the split reduction, counters, the rms partials,
     // the gate/up combine.
-    return (m + 1u) * (W + 1u) * 16u + G * 16u + static_cast<size_t>(nwave) * m * kTileRows * 4u + 16u +
+    return (m + 1u) * (W + 1u) * 16u + G * 16u + static_cast<size_t>(nwave) * m * kTileRows * 4u + 32u +
            (norm ? (m * G + m) * 4u : 0u) + (dual ? static_cast<size_t>(nwave / 2u) * m * kTileRows * 4u : 0u);
 }
 
 size_t max_lds_per_block();
 
-template <int M, bool DUAL, int EPI, int NWAVE, bool NORM = false>
+template <int M, bool DUAL, int EPI, int NWAVE, int NORM = 0>
 void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t stream) {
     // Pairs per register batch (two batches in flight): 4, so that a wave's whole range
     // (at most kSkinnyPairsUpFront pairs) is requested at once; 2 for the softcap head,
@@ -324,7 +406,7 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
     const uint32_t per_wave = (p.pairs + p.splits - 1u) / p.splits;
     auto kernel = per_wave <= 2u * P ? q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false>
                                      : q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true>;
-    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM);
+    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM != 0);
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "skinny: x staging exceeds the device's LDS");
     if (lds > 65536u) {
         static thread_local int configured_device = -1;
@@ -349,20 +431,22 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
 // streams while the other finishes), and the softcap head, whose grid is many workgroups
 // per compute unit, 4.
 template <int M>
-void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, bool norm,
+void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, int norm,
                      hipStream_t stream) {
     if (dual) {
         launch_skinny_t<M, true, 0, kSkinnyDualWaves>(p, tiles_total, stream);
     } else if (epi == Epilogue::kSoftcap) {
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
-    } else if (norm) {
-        launch_skinny_t<M, false, 0, kSkinnyWaves, true>(p, tiles_total, stream);
+    } else if (norm == 2) {
+        launch_skinny_t<M, false, 0, kSkinnyWaves, 2>(p, tiles_total, stream);
+    } else if (norm == 1) {
+        launch_skinny_t<M, false, 0, kSkinnyWaves, 1>(p, tiles_total, stream);
     } else {
         launch_skinny_t<M, false, 0, kSkinnyWaves>(p, tiles_total, stream);
     }
 }
 
-void launch_skinny(SkinnyParams& p, uint32_t tiles_total, uint32_t m, bool dual, Epilogue epi, bool norm,
+void launch_skinny(SkinnyParams& p, uint32_t tiles_total, uint32_t m, bool dual, Epilogue epi, int norm,
                    hipStream_t stream) {
     switch (m) {
         case 1: launch_skinny_m<1>(p, tiles_total, dual, epi, norm, stream); break;
@@ -428,6 +512,23 @@ bool skinny_norm_supported(uint32_t m, uint32_t k) {
            skinny_lds_bytes(m, k, false, kSkinnyWaves, true) <= max_lds_per_block();
 }
 
+bool skinny_resid_supported(uint32_t m, uint32_t k) {
+    return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u && m * (k / 64u) <= 64u * kSkinnyWaves &&
+           skinny_lds_bytes(m, k, false, kSkinnyWaves, true) <= max_lds_per_block();
+}
+
+namespace {
+void set_residual(SkinnyParams& p, const SkinnyResidual* res) {
+    if (res == nullptr) return;
+    p.res_branch = res->branch;
+    p.res_in = res->in;
+    p.res_out = res->out;
+    p.res_w = res->w;
+    p.res_scalar = res->scalar;
+    p.x = res->in;
+}
+}  // namespace
+
 void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, uint32_t m, uint16_t* y,
                       Epilogue epi, float cap_bf16, uint32_t splits, hipStream_t stream) {
     const TiledDims d = TiledDims::of(w.n, w.k);
@@ -456,14 +557,17 @@ void launch_q4_skinny(const Q4Matrix& w, const Q4Matrix* up, const uint16_t* x, 
     p.cap = cap_bf16;
     p.splits = splits;
     p.split_shift = static_cast<uint32_t>(__builtin_ctz(splits));
-    launch_skinny(p, dual ? 2u * d.tiles : d.tiles, m, dual, epi, false, stream);
+    launch_skinny(p, dual ? 2u * d.tiles : d.tiles, m, dual, epi, 0, stream);
 }
 
 void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint32_t count, const uint16_t* x,
-                            uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream) {
+                            uint32_t m, const float* rms_eps, const uint16_t* norm_w, hipStream_t stream,
+                            const SkinnyResidual* res) {
     HYP_REQUIRE(count >= 1u && count <= kSkinnyMaxGroup, HYP_STATUS_INTERNAL, "skinny: bad group size");
     const uint32_t k = ws[0]->k;
     const bool norm = rms_eps != nullptr;
+    HYP_REQUIRE(res == nullptr || (norm && skinny_resid_supported(m, k)), HYP_STATUS_INTERNAL,
+                "skinny: residual prologue needs the norm and one unit per thread");
     HYP_REQUIRE(norm ? skinny_norm_supported(m, k) : skinny_supported(m, k, false), HYP_STATUS_INTERNAL,
                 "skinny: shape exceeds LDS");
     SkinnyParams p{};
@@ -488,7 +592,8 @@ void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint
     p.norm_w = norm ? norm_w : nullptr;
     p.splits = choose_skinny_splits(tiles_total, p.pairs, m, SkinnyForm::kPlain);
     p.split_shift = static_cast<uint32_t>(__builtin_ctz(p.splits));
-    launch_skinny(p, tiles_total, m, false, Epilogue::kNone, norm, stream);
+    set_residual(p, res);
+    launch_skinny(p, tiles_total, m, false, Epilogue::kNone, res != nullptr ? 2 : (norm ? 1 : 0), stream);
 }
 
 }  // namespace hyperion::hip

@@ -58,24 +58,66 @@ __device__ __forceinline__ uint32_t quant_word(const float (&v)[8], float bias, 
     return pack_codes(c);
 }
 
-// One thread per group of 64: it reads the group's 128 contiguous bytes, finds the
-// extremes, derives scale and bias once (zero-point rule, fp32, IEEE division, rint) and
-// writes 8 packed words (32 contiguous bytes) plus a bf16 scale and bias. No cross-lane
-// work and no redundant per-group arithmetic, so the vector ALU work per weight is the
-// quantization itself.
+// One thread per group of 64: it finds the group's extremes, derives scale and bias once
+// (zero-point rule, fp32, IEEE division, rint) and forms 8 packed words plus a bf16 scale
+// and bias. No cross-lane arithmetic and no redundant per-group work, so the vector ALU
+// work per weight is the quantization itself.
+//
+// Memory: a wave's 64 groups are 8 KB of contiguous input and 2 KB of contiguous codes. The
+// input is read by 8 wave-wide 16-byte loads of 1 KB each (lane-consecutive) into an LDS
+// tile, from which each lane takes its own group's 8 chunks; the codes go back the same way
+// (2 stores of 1 KB). In the tile chunk c of group r sits at r * 8 + (c ^ (r & 7)), so both
+// the lane-consecutive writes and the per-group reads touch 16 distinct 16-byte bank groups
+// per 16 lanes.
+constexpr uint32_t kQuantWaves = kThreads / 64;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t tile_slot(uint32_t r, uint32_t c) { return r * 8u + (c ^ (r & 7u)); }
+
+// Orders one wave's LDS accesses across its lanes: a wave's LDS instructions execute in
+// order, so only the compiler must keep them in program order. Each wave touches only its
+// own tile, so the waves of a workgroup never wait for each other.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __global__ __launch_bounds__(kThreads) void q4_quantize_kernel(const uint16_t* __restrict__ w,
                                                                uint32_t* __restrict__ wq,
                                                                uint16_t* __restrict__ scales,
                                                                uint16_t* __restrict__ biases,
                                                                uint64_t groups) {
-    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (g >= groups) return;
-    // Plain loads: each lane's eight 16-byte loads share its 128-byte lines, which the
-    // non-temporal policy would not keep between them (measured 63 us against 39 us).
-    const uint4* src = reinterpret_cast<const uint4*>(w + g * 64u);
+    __shared__ uint4 tile[kQuantWaves][64 * 8];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * kThreads + wave * 64u;   // this wave's first group
+    const uint64_t left = g0 < groups ? groups - g0 : 0u;                           // groups from g0 on
+    const uint32_t own = static_cast<uint32_t>(left < 64u ? left : 64u);             // this wave's groups
+    const uint64_t g = g0 + lane;
+    const bool live = lane < own;
+    uint4* t4 = tile[wave];
+
+    const uint4* src = reinterpret_cast<const uint4*>(w) + g0 * 8u;
+    if (own == 64u) {   // every load issued before the first LDS write
+        uint4 in[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            in[t] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) +
+                                                                          static_cast<uint32_t>(t) * 64u + lane));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t j = static_cast<uint32_t>(t) * 64u + lane;
+            t4[tile_slot(j >> 3, j & 7u)] = in[t];
+        }
+    } else {   // the last, partial wave
+        for (uint32_t j = lane; j < own * 8u; j += 64u) t4[tile_slot(j >> 3, j & 7u)] = src[j];
+    }
+    wave_lds_sync();
     uint4 raw[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) raw[t] = src[t];
+    for (int t = 0; t < 8; ++t) raw[t] = t4[tile_slot(lane, static_cast<uint32_t>(t))];
+    wave_lds_sync();   // every lane has its chunks: the tile takes the codes next
 
     float w_max = -INFINITY;
     float w_min = INFINITY;
@@ -117,11 +159,19 @@ __global__ __launch_bounds__(kThreads) void q4_quantize_kernel(const uint16_t* _
         }
         packed[t] = quant_word(v, bias, scale, rcp);
     }
-    uint4* dst = reinterpret_cast<uint4*>(wq + g * 8u);
-    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-    scales[g] = f32_to_bf16_bits(scale);
-    biases[g] = f32_to_bf16_bits(bias);
+    t4[2u * lane] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    t4[2u * lane + 1u] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    wave_lds_sync();
+    uint4* dst = reinterpret_cast<uint4*>(wq) + g0 * 2u;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t j = static_cast<uint32_t>(t) * 64u + lane;
+        if (j < own * 2u) __builtin_nontemporal_store(__builtin_bit_cast(u32x4, t4[j]), reinterpret_cast<u32x4*>(dst) + j);
+    }
+    if (live) {
+        scales[g] = f32_to_bf16_bits(scale);
+        biases[g] = f32_to_bf16_bits(bias);
+    }
 }
 
 // The 8 bf16 outputs of one packed word: bf16(bf16(s*q) + b), optionally times a bf16

@@ -132,6 +132,15 @@ struct SkinnyParams {
     const uint2* sb2;
     float eps;            // NORM: rms normalisation epsilon
     const uint16_t* norm_w;   // NORM: the norm's learned weight [k] (bf16), or null
+    // NORM with a residual (the sandwich closing the previous block, forward.cc:518-539):
+    // the rows normalised are x = bf16(res_in + rms_norm(res_branch, res_w)), times
+    // res_scalar (bf16 [1]) when non-null, with the same bits as residual_norm_kernel;
+    // workgroup 0 writes them to res_out (not res_in, which the other workgroups still read).
+    const uint16_t* res_branch;
+    const uint16_t* res_in;
+    uint16_t* res_out;
+    const uint16_t* res_w;
+    const uint16_t* res_scalar;
 };
 
 // One matrix as seen by one lane: buffer resources and the lane's offsets into them.
