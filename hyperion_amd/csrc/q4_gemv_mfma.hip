@@ -69,10 +69,7 @@ namespace {
 // in one workgroup; each wave computes one matrix exactly as a plain launch does, and the
 // gate tile's waves combine with the up tile's rows in LDS for the GELU epilogue.
 template <int M, bool DUAL, int EPI, int P, int NWAVE, int NORM, bool LOOP>
-// NORM 2 is held to 128 registers (four waves per SIMD, two 8-wave workgroups per compute
-// unit), the occupancy of the other forms.
-__global__ __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu(NORM == 2 ? 4 : 1))) void q4_skinny_kernel(
-    SkinnyParams p) {
+__global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     constexpr int NW = 1;
     constexpr uint32_t kThreads = 64u * NWAVE;
     extern __shared__ __attribute__((aligned(16))) uint4 smem[];
@@ -171,135 +168,6 @@ __global__ __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu(NORM
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
     __builtin_amdgcn_s_barrier();         // no memory wait: only orders the issue
 
-    auto stage_x = [&]() {
-        if (stager) {
-            if constexpr (NORM) {
-                if constexpr (resid) {
-                    // The branch's norm (phases 3, 4), the residual add, then x's statistics
-                    // below; each row's inverse is formed by one wave, in residual_norm_kernel's
-                    // order. Every unit is held by one thread (checked on the host).
-                    uint4 rv[8];
-                    uint4 wrv[8];
-                    if (xu0 < units) {   // the branch first: its statistics need only it
-                        const uint32_t m = unit_row<M>(xu0, G);
-                        const uint32_t g = xu0 - m * G;
-                        const size_t off = static_cast<size_t>(m) * k + g * 64u;
-                        const uint4* bsrc = reinterpret_cast<const uint4*>(p.res_branch + off);
-                        const uint4* rsrc = reinterpret_cast<const uint4*>(p.res_in + off);
-                        const uint4* wsrc = reinterpret_cast<const uint4*>(p.res_w + g * 64u);
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) xv[t] = bsrc[t];
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) rv[t] = rsrc[t];
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) wrv[t] = wsrc[t];
-                    }
-                    if (xu0 < units) part[xu0] = unit_sumsq(xv);
-                    raise_counter(ctr + 3, lane);
-                    wait_counter(ctr + 3, nstage);
-                    if (wave < static_cast<uint32_t>(M)) {
-                        const float ss = row_sumsq(part + wave * G, G, lane);
-                        if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
-                    }
-                    raise_counter(ctr + 4, lane);
-                    wait_counter(ctr + 4, nstage);
-                    float ssx = 0.0f;
-                    if (xu0 < units) {
-                        const uint32_t m = unit_row<M>(xu0, G);
-                        const uint32_t g = xu0 - m * G;
-                        normalize_unit(xv, part[units + m]);
-                        weight_unit(xv, wrv);
-                        const float sc = p.res_scalar != nullptr ? bf16_bits_to_f32(*p.res_scalar) : 1.0f;
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) {
-                            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
-                            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
-                                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
-                                if (p.res_scalar != nullptr) {
-                                    lo = round_bf16(lo * sc);
-                                    hi = round_bf16(hi * sc);
-                                }
-                                hw[q] = cvt_pk_bf16(lo, hi);
-                            }
-                            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-                        }
-                        if (blockIdx.x == 0u) {
-                            uint4* dst = reinterpret_cast<uint4*>(p.res_out + static_cast<size_t>(m) * k + g * 64u);
-#pragma unroll
-                            for (int t = 0; t < 8; ++t) dst[t] = xv[t];
-                        }
-                        ssx = unit_sumsq(xv);
-                    }
-                    raise_counter(ctr + 5, lane);   // every wave has read its inverse
-                    wait_counter(ctr + 5, nstage);
-                    if (xu0 < units) part[xu0] = ssx;
-                } else {
-                // Per-unit sums of squares, then one wave per row forms its inverse rms.
-                for (uint32_t u = xu0; u < units; u += kThreads) {
-                    if (u != xu0) {
-                        const uint32_t m = unit_row<M>(u, G);
-                        const uint32_t g = u - m * G;
-                        const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) xv[t] = src[t];
-                    }
-                    part[u] = unit_sumsq(xv);
-                }
-                }
-                raise_counter(ctr + 1, lane);
-                wait_counter(ctr + 1, nstage);
-                if (wave < static_cast<uint32_t>(M)) {
-                    const float ss = row_sumsq(part + wave * G, G, lane);
-                    if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
-                }
-                raise_counter(ctr + 2, lane);
-                wait_counter(ctr + 2, nstage);
-            }
-
-            // Stage x: each thread permutes whole groups (8 words) and sums them.
-            for (uint32_t u = xu0; u < units; u += kThreads) {
-                const uint32_t m = unit_row<M>(u, G);
-                const uint32_t g = u - m * G;
-                if (u != xu0 || (NORM && units > kThreads)) {   // never with a residual
-                    const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) xv[t] = src[t];
-                }
-                if constexpr (NORM) {
-                    normalize_unit(xv, part[units + m]);
-                    if (p.norm_w != nullptr) {
-                        const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w + g * 64u);
-                        uint4 wv[8];
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
-                        weight_unit(xv, wv);
-                    }
-                }
-                float s0 = 0.0f;
-                float s1 = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    uint4 o;
-                    o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
-                    o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
-                    o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
-                    o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
-                    xs[m * WS + g * 8u + t] = o;
-                    s0 = dot2_bf16(xv[t].x, kOnePair, s0);
-                    s1 = dot2_bf16(xv[t].y, kOnePair, s1);
-                    s0 = dot2_bf16(xv[t].z, kOnePair, s0);
-                    s1 = dot2_bf16(xv[t].w, kOnePair, s1);
-                }
-                reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
-            }
-            raise_counter(ctr, lane);
-        }
-    };
-    if constexpr (resid) stage_x();
-
     const uint32_t c_bytes = tiles * pairs * 1024u;
     const uint32_t s_bytes = tiles * pairs * 128u;
     LaneMatrix lm[NW];
@@ -318,22 +186,163 @@ __global__ __launch_bounds__(64 * NWAVE) __attribute__((amdgpu_waves_per_eu(NORM
     // behind the codes the first scaling would wait for every code load of the wave.
     const uint32_t ob = lane >> 4;
     uint32_t sbl[NW][P];
-    if constexpr (kLaneGroups) {
-        const uint32_t off = (ltile * pairs * 16u + (ob >> 1) * 16u + j) * 8u + (ob & 1u) * 4u;
-#pragma unroll
-        for (int q = 0; q < NW; ++q)
-#pragma unroll
-            for (int b = 0; b < P; ++b)
-                sbl[q][b] = __builtin_amdgcn_raw_buffer_load_b32(lm[q].sb, off, (first + 2u * b) * 128u, kStreamPolicy);
-    }
-    // Two batches of weights in flight before the first arithmetic.
     Batch<P> ba[NW], bb[NW];
+    if constexpr (!resid) {
+        if constexpr (kLaneGroups) {
+            const uint32_t off = (ltile * pairs * 16u + (ob >> 1) * 16u + j) * 8u + (ob & 1u) * 4u;
 #pragma unroll
-    for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first, last, ba[q]);
+            for (int q = 0; q < NW; ++q)
 #pragma unroll
-    for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
+                for (int b = 0; b < P; ++b)
+                    sbl[q][b] = __builtin_amdgcn_raw_buffer_load_b32(lm[q].sb, off, (first + 2u * b) * 128u, kStreamPolicy);
+        }
+        // Two batches of weights in flight before the first arithmetic.
+#pragma unroll
+        for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first, last, ba[q]);
+#pragma unroll
+        for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
+    }
 
-    if constexpr (!resid) stage_x();
+    if (stager) {
+        if constexpr (NORM) {
+            if constexpr (resid) {
+                // The branch's norm (phases 3, 4), the residual add, then x's statistics
+                // below; each row's inverse is formed by one wave, in residual_norm_kernel's
+                // order. Every unit is held by one thread (checked on the host).
+                uint4 rv[8];
+                uint4 wrv[8];
+                if (xu0 < units) {   // the branch first: its statistics need only it
+                    const uint32_t m = unit_row<M>(xu0, G);
+                    const uint32_t g = xu0 - m * G;
+                    const size_t off = static_cast<size_t>(m) * k + g * 64u;
+                    const uint4* bsrc = reinterpret_cast<const uint4*>(p.res_branch + off);
+                    const uint4* rsrc = reinterpret_cast<const uint4*>(p.res_in + off);
+                    const uint4* wsrc = reinterpret_cast<const uint4*>(p.res_w + g * 64u);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xv[t] = bsrc[t];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) rv[t] = rsrc[t];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) wrv[t] = wsrc[t];
+                }
+                if (xu0 < units) part[xu0] = unit_sumsq(xv);
+                raise_counter(ctr + 3, lane);
+                wait_counter(ctr + 3, nstage);
+                if (wave < static_cast<uint32_t>(M)) {
+                    const float ss = row_sumsq(part + wave * G, G, lane);
+                    if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+                }
+                raise_counter(ctr + 4, lane);
+                wait_counter(ctr + 4, nstage);
+                float ssx = 0.0f;
+                if (xu0 < units) {
+                    const uint32_t m = unit_row<M>(xu0, G);
+                    const uint32_t g = xu0 - m * G;
+                    normalize_unit(xv, part[units + m]);
+                    weight_unit(xv, wrv);
+                    const float sc = p.res_scalar != nullptr ? bf16_bits_to_f32(*p.res_scalar) : 1.0f;
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
+                        uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
+                            float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
+                            if (p.res_scalar != nullptr) {
+                                lo = round_bf16(lo * sc);
+                                hi = round_bf16(hi * sc);
+                            }
+                            hw[q] = cvt_pk_bf16(lo, hi);
+                        }
+                        xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                    }
+                    if (blockIdx.x == 0u) {
+                        uint4* dst = reinterpret_cast<uint4*>(p.res_out + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) dst[t] = xv[t];
+                    }
+                    ssx = unit_sumsq(xv);
+                }
+                raise_counter(ctr + 5, lane);   // every wave has read its inverse
+                wait_counter(ctr + 5, nstage);
+                if (xu0 < units) part[xu0] = ssx;
+            } else {
+            // Per-unit sums of squares, then one wave per row forms its inverse rms.
+            for (uint32_t u = xu0; u < units; u += kThreads) {
+                if (u != xu0) {
+                    const uint32_t m = unit_row<M>(u, G);
+                    const uint32_t g = u - m * G;
+                    const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xv[t] = src[t];
+                }
+                part[u] = unit_sumsq(xv);
+            }
+            }
+            raise_counter(ctr + 1, lane);
+            wait_counter(ctr + 1, nstage);
+            if (wave < static_cast<uint32_t>(M)) {
+                const float ss = row_sumsq(part + wave * G, G, lane);
+                if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+            }
+            raise_counter(ctr + 2, lane);
+            wait_counter(ctr + 2, nstage);
+        }
+
+        // Stage x: each thread permutes whole groups (8 words) and sums them.
+        for (uint32_t u = xu0; u < units; u += kThreads) {
+            const uint32_t m = unit_row<M>(u, G);
+            const uint32_t g = u - m * G;
+            if (u != xu0 || (NORM && units > kThreads)) {   // never with a residual
+                const uint4* src = reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * k + g * 64u);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) xv[t] = src[t];
+            }
+            if constexpr (NORM) {
+                normalize_unit(xv, part[units + m]);
+                if (p.norm_w != nullptr) {
+                    const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w + g * 64u);
+                    uint4 wv[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
+                    weight_unit(xv, wv);
+                }
+            }
+            float s0 = 0.0f;
+            float s1 = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                uint4 o;
+                o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
+                o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
+                o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
+                o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
+                xs[m * WS + g * 8u + t] = o;
+                s0 = dot2_bf16(xv[t].x, kOnePair, s0);
+                s1 = dot2_bf16(xv[t].y, kOnePair, s1);
+                s0 = dot2_bf16(xv[t].z, kOnePair, s0);
+                s1 = dot2_bf16(xv[t].w, kOnePair, s1);
+            }
+            reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
+        }
+        raise_counter(ctr, lane);
+    }
+    if constexpr (resid) {   // the same loads, after the prologue
+        if constexpr (kLaneGroups) {
+            const uint32_t off = (ltile * pairs * 16u + (ob >> 1) * 16u + j) * 8u + (ob & 1u) * 4u;
+#pragma unroll
+            for (int q = 0; q < NW; ++q)
+#pragma unroll
+                for (int b = 0; b < P; ++b)
+                    sbl[q][b] = __builtin_amdgcn_raw_buffer_load_b32(lm[q].sb, off, (first + 2u * b) * 128u, kStreamPolicy);
+        }
+        // Two batches of weights in flight before the first arithmetic.
+#pragma unroll
+        for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first, last, ba[q]);
+#pragma unroll
+        for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
+    }
     wait_counter(ctr, nstage);
 
     // Opaque VGPR values, so (w & mask) | bits selects v_and_or_b32 (see and_or).
