@@ -28,6 +28,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "q4_rmsnorm.h"
 
 namespace hyperion::hip {
 namespace {
@@ -52,6 +53,17 @@ struct AttnParams {
     uint32_t L, H, KVH, G, cap, offset, prefix, window;
     uint32_t splits, keys_per_split;
     const uint32_t* pos;    // non-null: offset = *pos, read on the device (graph replays)
+    // The decode form with the prepare folded in (L = 1): q is the raw projection; each
+    // wave normalises and rotates its query rows, and the wave whose keys hold the new
+    // token forms its K/V from k_raw/v_raw and writes them to the cache slot.
+    const float2* rope_cs;  // (cos, sin) [positions][D / 2]
+    const uint16_t* q_w;    // [D]
+    const uint16_t* k_w;    // [D]
+    const uint16_t* k_raw;  // [KVH][D]
+    const uint16_t* v_raw;  // [KVH][D], or null: V = v_norm(k_raw)
+    uint16_t* ck_out;       // the cache, written at the new token's slot
+    uint16_t* cv_out;
+    float eps;
 };
 
 // Graph-replay form: the position comes from device memory, the prefix and the split
@@ -290,14 +302,65 @@ template <uint32_t D>
 struct DecodeLds {
     static constexpr uint32_t kVtRow = kKeyBlock * 2u + 16u;
     static constexpr uint32_t kPRow = kKeyBlock * 2u + 16u;
-    static constexpr uint32_t kVt = 0;
+    static constexpr uint32_t kVt = 0;   // also the query rows' staging before the key loop
     static constexpr uint32_t kP = kVt + D * kVtRow;
-    static constexpr uint32_t kWave = kP + 16u * kPRow;
+    static constexpr uint32_t kNew = kP + 16u * kPRow;   // the new token's K and V rows (bf16)
+    static constexpr uint32_t kWave = kNew + 4u * D;
     static constexpr uint32_t kWaves = D <= 256u ? 4u : 2u;
     static constexpr uint32_t kBytes = kWaves * kWave;
 };
 
+// Orders one wave's LDS accesses across its lanes (a wave's LDS instructions execute in
+// order; only the compiler must keep them in program order).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// RoPE of `rows` head rows of D bf16 in LDS (row stride D), in place, with the prepare
+// kernel's arithmetic: lane takes 8 consecutive pairs (i, i + D/2) of row rsub + k * rpi;
+// cs8 holds (cos, sin) of its pairs.
 template <uint32_t D>
+__device__ __forceinline__ void rope_rows_lds(uint16_t* rows_base, uint32_t rows, uint32_t lane, const float2 (&cs8)[8]) {
+    constexpr uint32_t kHalf = D / 2u;
+    constexpr uint32_t kHalfChunks = kHalf / 8u;
+    constexpr uint32_t kRowsPerIter = 64u / kHalfChunks;
+    const uint32_t c = lane % kHalfChunks;
+    for (uint32_t r = lane / kHalfChunks; r < rows; r += kRowsPerIter) {
+        uint4* lo = reinterpret_cast<uint4*>(rows_base + r * D + c * 8u);
+        uint4* hi = reinterpret_cast<uint4*>(rows_base + r * D + kHalf + c * 8u);
+        const uint4 a = *lo;
+        const uint4 b = *hi;
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+        const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+        uint32_t ow[4];
+        uint32_t pw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t o2[2];
+            uint32_t p2[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float x1 = bf16_bits_to_f32((aw[q] >> (16 * h)) & 0xFFFFu);
+                const float x2 = bf16_bits_to_f32((bw[q] >> (16 * h)) & 0xFFFFu);
+                const float2 cs = cs8[2 * q + h];
+                const float a1 = x1 * cs.x;
+                const float a2 = x2 * cs.y;
+                const float b1 = x1 * cs.y;
+                const float b2 = x2 * cs.x;
+                o2[h] = f32_to_bf16_bits(a1 - a2);
+                p2[h] = f32_to_bf16_bits(b1 + b2);
+            }
+            ow[q] = o2[0] | (o2[1] << 16);
+            pw[q] = p2[0] | (p2[1] << 16);
+        }
+        *lo = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        *hi = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    }
+}
+
+template <uint32_t D, bool PREP>
 __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel(AttnParams p) {
     resolve_position(p);
     using Lds = DecodeLds<D>;
@@ -313,10 +376,112 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
     const uint32_t T = p.prefix + p.L;
     uint8_t* my = lds + wave * Lds::kWave;
 
+    uint32_t j_begin = split * p.keys_per_split;
+    const uint32_t j_end = min(j_begin + p.keys_per_split, T);
+    if (p.window != 0u) {   // keys at positions > offset - window (the first token's bound)
+        const int64_t lo = static_cast<int64_t>(p.prefix) - p.window + 1;
+        if (lo > static_cast<int64_t>(j_begin)) j_begin = static_cast<uint32_t>(lo);
+    }
+
     constexpr uint32_t kSteps = D / 32u;
     constexpr uint32_t kDTiles = D / 16u;
     bf16x8_t qa[kSteps];
-    {
+    // PREP: the new token's K and V rows (this wave's keys include it when fresh_key).
+    uint16_t* new_k = reinterpret_cast<uint16_t*>(my + Lds::kNew);
+    uint16_t* new_v = new_k + D;
+    bool fresh_key = false;
+    if constexpr (PREP) {
+        // attn_prepare_kernel's work for one token (L = 1), in its arithmetic: q_norm and
+        // RoPE of this kv head's G query rows, staged in the V^T area; k_norm + RoPE and
+        // v_norm of the new key by the wave whose range holds it.
+        constexpr uint32_t kU = D / 64u;             // 64-value units per head row
+        constexpr uint32_t kHalf = D / 2u;
+        const bool has_keys = j_begin < j_end;       // wave-uniform
+        fresh_key = has_keys && j_begin <= p.prefix && p.prefix < j_end;
+        uint16_t* qs = reinterpret_cast<uint16_t*>(my + Lds::kVt);   // [G][D]
+        const uint32_t pos = p.offset;
+        float2 cs8[8];
+        {
+            const uint32_t c = lane % (kHalf / 8u);
+            const float4* t4 = reinterpret_cast<const float4*>(p.rope_cs + static_cast<size_t>(pos) * kHalf + c * 8u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 v = has_keys ? t4[e] : make_float4(1.0f, 0.0f, 1.0f, 0.0f);
+                cs8[2 * e] = make_float2(v.x, v.y);
+                cs8[2 * e + 1] = make_float2(v.z, v.w);
+            }
+        }
+        if (!has_keys) {
+#pragma unroll
+            for (uint32_t st = 0; st < kSteps; ++st) qa[st] = bf16x8_t{};
+        } else {
+            // One 64-value unit per lane: row r = lane / kU is query row r (r < G), the new
+            // key's K (r == G) or its V (r == G + 1); the host folds only when they fit.
+            const uint32_t u = lane % kU;
+            const uint32_t r = lane / kU;
+            const bool is_q = r < p.G;
+            const bool is_k = fresh_key && r == p.G;
+            const bool is_v = fresh_key && r == p.G + 1u;
+            const size_t slot_row = (static_cast<size_t>(p.offset % p.cap) * p.KVH + hk) * D;
+            const uint16_t* src = nullptr;
+            const uint16_t* w = nullptr;
+            if (is_q) {
+                src = p.q + (static_cast<size_t>(hk) * p.G + r) * D;
+                w = p.q_w;
+            } else if (is_k) {
+                src = p.k_raw + static_cast<size_t>(hk) * D;
+                w = p.k_w;
+            } else if (is_v) {
+                src = (p.v_raw != nullptr ? p.v_raw : p.k_raw) + static_cast<size_t>(hk) * D;
+            }
+            uint4 xv[8];
+            uint4 wv[8];
+            if (src != nullptr) {
+                const uint4* s4 = reinterpret_cast<const uint4*>(src + u * 64u);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) xv[t] = s4[t];
+            }
+            if (w != nullptr) {
+                const uint4* w4 = reinterpret_cast<const uint4*>(w + u * 64u);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) wv[t] = w4[t];
+            }
+            // The prepare's 64-lane butterfly over a row's kU lanes (the rest of its lanes
+            // add zeros there).
+            float ss = src != nullptr ? unit_sumsq(xv) : 0.0f;
+#pragma unroll
+            for (uint32_t off = kU / 2u; off > 0u; off >>= 1) ss += __shfl_xor(ss, static_cast<int>(off), 64);
+            if (src != nullptr) {
+                normalize_unit(xv, rms_inverse(ss, D, p.eps));
+                if (w != nullptr) weight_unit(xv, wv);
+                uint16_t* dst = is_q ? qs + r * D : (is_k ? new_k : new_v);
+                uint4* d4 = reinterpret_cast<uint4*>(dst + u * 64u);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) d4[t] = xv[t];
+                if (is_v) {
+                    uint4* vg = reinterpret_cast<uint4*>(p.cv_out + slot_row + u * 64u);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) vg[t] = xv[t];
+                }
+            }
+            wave_lds_sync();
+            rope_rows_lds<D>(qs, p.G, lane, cs8);
+            if (fresh_key) rope_rows_lds<D>(new_k, 1u, lane, cs8);
+            wave_lds_sync();
+            if (fresh_key && lane < kU) {
+                const uint4* kl = reinterpret_cast<const uint4*>(new_k + lane * 64u);
+                uint4* kg = reinterpret_cast<uint4*>(p.ck_out + slot_row + lane * 64u);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) kg[t] = kl[t];
+            }
+#pragma unroll
+            for (uint32_t st = 0; st < kSteps; ++st) {
+                uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                if (j16 < p.G) v = *reinterpret_cast<const uint4*>(qs + j16 * D + kb * 8u + st * 32u);
+                qa[st] = __builtin_bit_cast(bf16x8_t, v);
+            }
+        }
+    } else {
         const bool valid = j16 < rows;
         const uint32_t t = valid ? j16 / p.G : 0u;
         const uint32_t h = hk * p.G + (j16 - t * p.G);
@@ -327,12 +492,6 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
             if (valid) v = *reinterpret_cast<const uint4*>(src + st * 32u);
             qa[st] = __builtin_bit_cast(bf16x8_t, v);
         }
-    }
-    uint32_t j_begin = split * p.keys_per_split;
-    const uint32_t j_end = min(j_begin + p.keys_per_split, T);
-    if (p.window != 0u) {   // keys at positions > offset - window (the first token's bound)
-        const int64_t lo = static_cast<int64_t>(p.prefix) - p.window + 1;
-        if (lo > static_cast<int64_t>(j_begin)) j_begin = static_cast<uint32_t>(lo);
     }
 
     f32x4_t o[kDTiles];
@@ -366,18 +525,24 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
                 const uint32_t c = c0 + u;
                 const uint32_t key = 16u * c + j16;
                 const uint16_t* row = key < nk ? key_row(p, p.k, p.ck, jb + key, hk, D) + kb * 8u : nullptr;
+                // PREP: the new token's key from this wave's LDS (its cache slot is being
+                // written by this launch).
+                const bool kfresh = PREP && fresh_key && key < nk && jb + key == p.prefix;
 #pragma unroll
                 for (uint32_t st = 0; st < kSteps; ++st) {
-                    kr[u][st] = row != nullptr ? *reinterpret_cast<const uint4*>(row + st * 32u)
-                                               : make_uint4(0u, 0u, 0u, 0u);
+                    kr[u][st] = kfresh ? *reinterpret_cast<const uint4*>(new_k + kb * 8u + st * 32u)
+                                : row != nullptr ? *reinterpret_cast<const uint4*>(row + st * 32u)
+                                                 : make_uint4(0u, 0u, 0u, 0u);
                 }
 #pragma unroll
                 for (uint32_t it = 0; it < kVPer; ++it) {
                     const uint32_t cidx = lane + 64u * it;
                     const uint32_t r = 16u * c + cidx / kChunks;
                     const uint32_t ch = cidx % kChunks;
-                    vr[u][it] = r < nk ? *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u)
-                                       : make_uint4(0u, 0u, 0u, 0u);
+                    const bool vfresh = PREP && fresh_key && r < nk && jb + r == p.prefix;
+                    vr[u][it] = vfresh ? *reinterpret_cast<const uint4*>(new_v + ch * 8u)
+                                : r < nk ? *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u)
+                                         : make_uint4(0u, 0u, 0u, 0u);
                 }
             }
 #pragma unroll
@@ -561,7 +726,7 @@ __global__ __launch_bounds__(kAttnThreads) void kv_write_kernel(const uint16_t* 
 }
 
 template <uint32_t D>
-void launch_decode_d(const AttnParams& p, hipStream_t stream) {
+void launch_decode_d(const AttnParams& p, bool prep, hipStream_t stream) {
     using Lds = DecodeLds<D>;
     constexpr size_t lds = Lds::kBytes;
     static_assert(lds <= 160u * 1024u, "decode attention LDS");
@@ -570,13 +735,17 @@ void launch_decode_d(const AttnParams& p, hipStream_t stream) {
         int dev = 0;
         HYP_HIP_CHECK(hipGetDevice(&dev));
         if (configured_device != dev) {
-            HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attn_decode_kernel<D>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            for (const void* f : {reinterpret_cast<const void*>(attn_decode_kernel<D, false>),
+                                  reinterpret_cast<const void*>(attn_decode_kernel<D, true>)}) {
+                HYP_HIP_CHECK(
+                    hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+            }
             configured_device = dev;
         }
     }
     const dim3 grid((p.splits + Lds::kWaves - 1u) / Lds::kWaves, p.KVH);
-    hipLaunchKernelGGL(attn_decode_kernel<D>, grid, dim3(Lds::kWaves * 64u), lds, stream, p);
+    auto kernel = prep ? attn_decode_kernel<D, true> : attn_decode_kernel<D, false>;
+    hipLaunchKernelGGL(kernel, grid, dim3(Lds::kWaves * 64u), lds, stream, p);
     HYP_HIP_CHECK(hipGetLastError());
 }
 
@@ -618,6 +787,11 @@ void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_
     hipLaunchKernelGGL(kv_write_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kAttnThreads), 0, stream, k, v, ck,
                        cv, skip, n, pos0, cap, row_elems);
     HYP_HIP_CHECK(hipGetLastError());
+}
+
+bool attention_prep_fits(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim) {
+    // The G query rows, K and V of one kv head as 64-value units, one per lane of a wave.
+    return n_kv_heads > 0u && n_heads % n_kv_heads == 0u && (n_heads / n_kv_heads + 2u) * (head_dim / 64u) <= 64u;
 }
 
 // The decode form's splits: one wave per block of 32 keys (each wave then makes a single
@@ -677,11 +851,29 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
                                              static_cast<size_t>(p.splits) * rows * a.head_dim * 4u);
     }
     const bool decode = static_cast<uint64_t>(a.L) * p.G <= 16u;
+    const bool prep = a.prep != nullptr;
+    if (prep) {
+        const AttnPrepareArgs& pa = *a.prep;
+        HYP_REQUIRE(decode && a.L == 1u && a.k == nullptr && a.v == nullptr && pa.rope_cs != nullptr &&
+                        pa.L == 1u && pa.head_dim == a.head_dim && pa.n_heads == a.n_heads &&
+                        pa.n_kv_heads == a.n_kv_heads && pa.cap == a.cap && pa.pos == a.pos &&
+                        (a.pos != nullptr || pa.offset == a.offset) && pa.q == a.q &&
+                        pa.cache_k == a.cache_k && pa.cache_v == a.cache_v && attention_prep_fits(a.n_heads, a.n_kv_heads, a.head_dim),
+                    HYP_STATUS_INTERNAL, "attention: the folded prepare needs one token, the cache form and a RoPE table");
+        p.rope_cs = pa.rope_cs;
+        p.q_w = pa.q_norm;
+        p.k_w = pa.k_norm;
+        p.k_raw = pa.k_raw;
+        p.v_raw = pa.v_raw;
+        p.ck_out = pa.cache_k;
+        p.cv_out = pa.cache_v;
+        p.eps = pa.eps;
+    }
     switch (a.head_dim) {
-        case 64: decode ? launch_decode_d<64>(p, stream) : launch_attn_d<64>(p, stream); break;
-        case 128: decode ? launch_decode_d<128>(p, stream) : launch_attn_d<128>(p, stream); break;
-        case 256: decode ? launch_decode_d<256>(p, stream) : launch_attn_d<256>(p, stream); break;
-        case 512: decode ? launch_decode_d<512>(p, stream) : launch_attn_d<512>(p, stream); break;
+        case 64: decode ? launch_decode_d<64>(p, prep, stream) : launch_attn_d<64>(p, stream); break;
+        case 128: decode ? launch_decode_d<128>(p, prep, stream) : launch_attn_d<128>(p, stream); break;
+        case 256: decode ? launch_decode_d<256>(p, prep, stream) : launch_attn_d<256>(p, stream); break;
+        case 512: decode ? launch_decode_d<512>(p, prep, stream) : launch_attn_d<512>(p, stream); break;
         default: throw NativeError(HYP_STATUS_UNSUPPORTED, "attention: head_dim must be 64, 128, 256 or 512");
     }
     if (p.splits > 1u) {

@@ -446,7 +446,10 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
         pa.cap = cache.cap;
         pa.base = static_cast<float>(sliding ? g.rope_local.theta : g.rope_global.theta);
         pa.eps = eps;
-        hip::launch_attn_prepare(pa, s);
+        // One token (a decode step) with the RoPE table: the attention launch does this
+        // work itself (the same bits), one launch fewer per layer.
+        const bool fold_prepare = L == 1u && pa.rope_cs != nullptr && hip::attention_prep_fits(g.heads, kvh, D);
+        if (!fold_prepare) hip::launch_attn_prepare(pa, s);
 
         // SDPA over the visible cached prefix and the appended chunk (forward.cc:420-505).
         hip::AttnArgs aa{};
@@ -472,6 +475,7 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
             aa.pos = d_pos;
             aa.fixed_splits = hip::attention_splits(L, g.heads, kvh, max_keys);
         }
+        if (fold_prepare) aa.prep = &pa;
         hip::launch_attention(aa, s);
 
         // o, then the attention half of the sandwich and the MLP's input norm (forward.cc:518-526).

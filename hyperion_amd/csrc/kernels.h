@@ -123,6 +123,7 @@ void launch_sample_topk(const uint16_t* logits, uint32_t rows, uint32_t vocab, H
 // Attention (forward.cc:376-508) over a KV cache prefix and the current chunk; see
 // attention.hip. Decode splits the keys; the partial sums need attention_workspace_bytes.
 constexpr uint32_t kAttnMaxSplits = 64;
+struct AttnPrepareArgs;
 struct AttnArgs {
     const uint16_t* q;         // [L][n_heads][head_dim]
     const uint16_t* k;         // [L][n_kv_heads][head_dim] (the chunk); null: the chunk is
@@ -138,9 +139,17 @@ struct AttnArgs {
     // fixed_splits workgroups per kv head whatever the offset.
     const uint32_t* pos = nullptr;
     uint32_t fixed_splits = 1;
+    // With prep non-null (one token, k = v = null, the decode form, a RoPE table): q is the
+    // raw projection (prep->q, not modified) and the launch does launch_attn_prepare's work
+    // itself, with its arithmetic: the query rows normalised and rotated per wave, and the
+    // new token's K/V written to its cache slot by the wave whose keys hold it.
+    const AttnPrepareArgs* prep = nullptr;
 };
 size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim);
 uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys);
+// Whether AttnArgs::prep can fold the prepare for this geometry (the G query rows and the
+// new K and V of one kv head fit one wave as 64-value units: (G + 2) * head_dim / 64 <= 64).
+bool attention_prep_fits(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 void launch_attention(const AttnArgs& a, hipStream_t stream);
 // Tokens pos0.. of k/v [n][n_kv_heads][head_dim] into cache slots (pos % cap).
 void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_t* cv, uint32_t n, uint32_t pos0,
