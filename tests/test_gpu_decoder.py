@@ -418,6 +418,33 @@ def test_residual_rms_norm_bit_exact(stream, m, hidden, scalar, nxt):
         x.close()
 
 
+@pytest.mark.parametrize("prefix", [20, 31, 32, 63, 64])
+def test_folded_prepare_equals_separate(tmp_path, prefix):
+    """A one-token step folds the q/k norms, RoPE and the cache append into the decode
+    attention launch; a two-token step at the same position runs them as their own launch
+    (attn_prepare_kernel) with every other kernel the same per row. Row 0 of the two-token
+    step has the bits of the one-token step, on both layer kinds, with the new key first,
+    last and inside a 32-key block."""
+    cfg = tiny_dims_config(256)
+    T = syn.write_model(str(tmp_path), cfg, seed=16, branch_gain=BRANCH_GAIN, qk_gain=QK_GAIN)
+    model = hy.Model(hy.geometry_from_config(cfg), str(tmp_path))
+    ids = np.random.default_rng(prefix).integers(0, cfg["vocab_size"], size=prefix + 2).astype(np.uint32)
+    say(f"folded prepare: prefix {prefix}")
+    one, two = model.kvstate(), model.kvstate()
+    one.forward_hidden(ids[:prefix], 0)
+    two.forward_hidden(ids[:prefix], 0)
+    a = one.forward_hidden(ids[prefix:prefix + 1], prefix)
+    b = two.forward_hidden(ids[prefix:prefix + 2], prefix)
+    np.testing.assert_array_equal(a[0], b[0])
+    # and the next step reads the folded step's cache entries as the oracle does (the
+    # six-layer stack's bar against the per-size-weight oracle: sig_rel <= 3e-2)
+    nxt = one.forward_hidden(ids[prefix + 1:prefix + 2], prefix + 1)
+    check_hidden(nxt, O.DecoderOracle(T, cfg, weights="per_m").forward(ids[:prefix + 2], 0)[prefix + 1:],
+                 f"step after the folded one, prefix {prefix}", rtol_atol=None)
+    for h in (one, two, model):
+        h.close()
+
+
 def test_decode_block_equals_single_steps(tmp_path):
     """hyp_decode_block(n) (n graph replays in one call) ends where n calls of
     hyp_decode_block(1) end: the same token, logit and near-tie count; two states of one
