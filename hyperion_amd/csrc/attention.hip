@@ -706,6 +706,51 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p
     }
 }
 
+// The chunk form's merge of its key splits (at most kChunkMaxSplits): thread c takes the 8
+// dims ch = c % (D/8) of row c / (D/8), the splits weighted as in attn_combine_kernel
+// (2^(m_s - max m), the sum of l_s, the divided sum).
+constexpr uint32_t kChunkMaxSplits = 2;
+template <uint32_t D>
+__global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnParams p) {
+    constexpr uint32_t kCh = D / 8u;
+    const uint64_t rows = static_cast<uint64_t>(p.L) * p.H;
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * kAttnThreads + threadIdx.x;
+    if (c >= rows * kCh) return;
+    const uint64_t row = c / kCh;
+    const uint32_t ch = static_cast<uint32_t>(c - row * kCh);
+    float ms[kChunkMaxSplits];
+    float ls[kChunkMaxSplits];
+    float4 lo[kChunkMaxSplits];
+    float4 hi[kChunkMaxSplits];
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (uint32_t s = 0; s < kChunkMaxSplits; ++s) {
+        const bool live = s < p.splits;
+        ms[s] = live ? p.part_ml[(s * rows + row) * 2u] : -__builtin_huge_valf();
+        ls[s] = live ? p.part_ml[(s * rows + row) * 2u + 1u] : 0.0f;
+        const float4* o4 = reinterpret_cast<const float4*>(p.part_o + (s * rows + row) * D + ch * 8u);
+        lo[s] = live ? o4[0] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        hi[s] = live ? o4[1] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        mx = fmaxf(mx, ms[s]);
+    }
+    float den = 0.0f;
+    float num[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t s = 0; s < kChunkMaxSplits; ++s) {
+        const float w = ms[s] == -__builtin_huge_valf() || mx == -__builtin_huge_valf() ? 0.0f : exp2f(ms[s] - mx);
+        if (w == 0.0f) continue;
+        den += w * ls[s];
+        const float v[8] = {lo[s].x, lo[s].y, lo[s].z, lo[s].w, hi[s].x, hi[s].y, hi[s].z, hi[s].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) num[e] += w * v[e];
+    }
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16_bits(den > 0.0f ? num[e] / den : 0.0f);
+    *reinterpret_cast<uint4*>(p.out + row * D + ch * 8u) =
+        make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+}
+
 // Tokens pos0 .. pos0 + n - 1 of k/v [n][KVH][D] -> cache slots pos % cap (only the last
 // `cap` of them when n > cap: earlier ones would be overwritten in the same slots).
 __global__ __launch_bounds__(kAttnThreads) void kv_write_kernel(const uint16_t* __restrict__ k,
@@ -770,6 +815,36 @@ void launch_attn_d(const AttnParams& p, hipStream_t stream) {
 
 }  // namespace
 
+namespace {
+
+// The chunk form at most one workgroup per compute unit (a prefill chunk of up to about
+// 1024 tokens on the 12B's layers): one wave per SIMD leaves every LDS and MFMA dependency
+// exposed and the causal tiles' lengths run 1 .. L / 32 blocks. Two key splits give two
+// resident workgroups per compute unit and halve the longest tile; attn_combine_kernel
+// merges them (measured below).
+bool chunk_split_pays(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys) {
+    const uint32_t G = n_heads / n_kv_heads;
+    const uint64_t tiles = (static_cast<uint64_t>(L) * G + kRowsPerTile - 1u) / kRowsPerTile * n_kv_heads;
+    return tiles <= device_compute_units() && keys >= 8u * kKeyBlock;
+}
+
+size_t chunk_split_bytes(uint32_t L, uint32_t n_heads, uint32_t head_dim) {
+    return 2u * static_cast<size_t>(L) * n_heads * (static_cast<size_t>(head_dim) * 4u + 8u);
+}
+
+}  // namespace
+
+size_t attention_chunk_workspace_bytes(uint32_t max_L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim) {
+    // The longest chunk that still splits (its tiles fit the compute units), within max_L,
+    // for MI355X's 256 compute units (a plan needs no device; on a larger part the chunks
+    // this does not cover run unsplit).
+    constexpr uint64_t kPlanComputeUnits = 256;
+    const uint32_t G = n_heads / n_kv_heads;
+    const uint64_t fit = static_cast<uint64_t>(kRowsPerTile) * (kPlanComputeUnits / n_kv_heads) / G;
+    const uint32_t L = static_cast<uint32_t>(std::min<uint64_t>(max_L, fit));
+    return head_dim <= 256u && L > kRowsPerTile / G ? chunk_split_bytes(L, n_heads, head_dim) : 0u;
+}
+
 size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim) {
     // Split partials for decode: at most kAttnMaxSplits splits of one row tile per kv head.
     const size_t rows = static_cast<size_t>(kRowsPerTile) * n_kv_heads;
@@ -806,7 +881,7 @@ uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uin
     // One row tile per kv head (decode): split the keys so the grid covers the compute
     // units, at least 64 keys per split.
     const uint32_t G = n_heads / n_kv_heads;
-    if (static_cast<uint64_t>(L) * G > kRowsPerTile) return 1u;
+    if (static_cast<uint64_t>(L) * G > kRowsPerTile) return chunk_split_pays(L, n_heads, n_kv_heads, keys) ? 2u : 1u;
     const uint32_t cus = device_compute_units();
     uint32_t s = 1u;
     while (s < kAttnMaxSplits && n_kv_heads * s * 2u <= cus && keys >= 64u * (s * 2u)) s *= 2u;
@@ -838,10 +913,23 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
         p.keys_per_split = kKeyBlock;
     } else {
         p.splits = attention_splits(a.L, a.n_heads, a.n_kv_heads, T);
+        const bool chunk = static_cast<uint64_t>(a.L) * p.G > kRowsPerTile;
+        // The chunk form splits only at head_dim <= 256 (at 512 the split measured 199 against
+        // 204 us per 1024-token layer before its merge) and into a workspace that holds it.
+        if (chunk && p.splits > 1u &&
+            (a.head_dim > 256u || a.workspace == nullptr ||
+             a.workspace_bytes < chunk_split_bytes(a.L, a.n_heads, a.head_dim)))
+            p.splits = 1u;
         p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
         p.splits = std::max(1u, (T + p.keys_per_split - 1u) / p.keys_per_split);   // no empty split
     }
-    if (p.splits > 1u) {
+    if (p.splits > 1u && static_cast<uint64_t>(a.L) * p.G > kRowsPerTile) {
+        // chunk form: checked above
+        const size_t rows = static_cast<size_t>(a.L) * a.n_heads;
+        p.part_o = static_cast<float*>(a.workspace);
+        p.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) +
+                                             static_cast<size_t>(p.splits) * rows * a.head_dim * 4u);
+    } else if (p.splits > 1u) {
         HYP_REQUIRE(a.workspace != nullptr &&
                         a.workspace_bytes >= attention_workspace_bytes(a.n_kv_heads, a.head_dim),
                     HYP_STATUS_INTERNAL, "attention: split workspace too small");
@@ -876,7 +964,18 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
         case 512: decode ? launch_decode_d<512>(p, prep, stream) : launch_attn_d<512>(p, stream); break;
         default: throw NativeError(HYP_STATUS_UNSUPPORTED, "attention: head_dim must be 64, 128, 256 or 512");
     }
-    if (p.splits > 1u) {
+    if (p.splits > 1u && static_cast<uint64_t>(a.L) * p.G > kRowsPerTile) {
+        // chunk form: many rows, two splits; a thread per 8 dims of a row
+        const uint64_t threads = static_cast<uint64_t>(a.L) * a.n_heads * (a.head_dim / 8u);
+        const uint64_t blocks = (threads + kAttnThreads - 1u) / kAttnThreads;
+        HYP_REQUIRE(blocks <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "attention: too many rows to merge");
+        switch (a.head_dim) {
+            case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
+            case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
+            default: hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
+        }
+        HYP_HIP_CHECK(hipGetLastError());
+    } else if (p.splits > 1u) {
         const uint64_t rows = static_cast<uint64_t>(a.L) * a.n_heads;
         HYP_REQUIRE(rows <= 0x7fffffffull, HYP_STATUS_INVALID_ARGUMENT, "attention: too many rows to combine");
         const dim3 grid(static_cast<uint32_t>(rows));

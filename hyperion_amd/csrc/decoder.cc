@@ -160,6 +160,16 @@ uint64_t rope_table_bytes(const Geometry& g, uint32_t D) {
     return bytes > kRopeTableMaxBytes ? 0u : bytes;
 }
 
+// The attention split workspace: decode splits, and the chunk form's two key splits up to
+// one prefill chunk, for both layer kinds.
+uint64_t attention_ws_bytes(const Geometry& g) {
+    const uint32_t chunk = std::min(kChunkTokens, g.max_positions);
+    return std::max({hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
+                     hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global),
+                     hip::attention_chunk_workspace_bytes(chunk, g.heads, g.kv_heads_local, g.head_dim_local),
+                     hip::attention_chunk_workspace_bytes(chunk, g.heads, g.kv_heads_global, g.head_dim_global)});
+}
+
 }  // namespace
 
 MemoryReport plan_memory(const Geometry& g) {
@@ -193,8 +203,7 @@ MemoryReport plan_memory(const Geometry& g) {
     r.scratch_bytes = T * 4u + 4u * T * g.hidden * 2u + 2u * T * H * dmax * 2u + 2u * T * kvmax * 2u +
                       T * g.intermediate * 2u + static_cast<uint64_t>(g.hidden) * 2u +
                       uint64_t{hip::kSkinnyMaxM} * g.hidden * 2u + static_cast<uint64_t>(g.vocab) * 2u +
-                      std::max(hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
-                               hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)) +
+                      attention_ws_bytes(g) +
                       hip::sample_greedy_workspace_bytes() + rope_table_bytes(g, g.head_dim_local) +
                       rope_table_bytes(g, g.head_dim_global);
     return r;
@@ -302,8 +311,7 @@ Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geome
     d_ = DeviceBuffer(T * g.hidden * 2u);
     last_ = DeviceBuffer(static_cast<size_t>(g.hidden) * 2u);
     logits_ = DeviceBuffer(static_cast<size_t>(g.vocab) * 2u);
-    attn_ws_ = DeviceBuffer(std::max(hip::attention_workspace_bytes(g.kv_heads_local, g.head_dim_local),
-                                     hip::attention_workspace_bytes(g.kv_heads_global, g.head_dim_global)));
+    attn_ws_ = DeviceBuffer(attention_ws_bytes(g));
     sample_ws_ = DeviceBuffer(hip::sample_greedy_workspace_bytes());
     const auto table = [&](uint32_t D, LayerType kind, double theta) {
         const size_t bytes = rope_table_bytes(g, D);

@@ -146,6 +146,9 @@ struct AttnArgs {
     const AttnPrepareArgs* prep = nullptr;
 };
 size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim);
+// The workspace with which launch_attention also splits the keys of chunks of up to max_L
+// tokens (0 when no such chunk splits); with less it runs those chunks unsplit.
+size_t attention_chunk_workspace_bytes(uint32_t max_L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys);
 // Whether AttnArgs::prep can fold the prepare for this geometry (the G query rows and the
 // new K and V of one kv head fit one wave as 64-value units: (G + 2) * head_dim / 64 <= 64).
