@@ -14,7 +14,7 @@
 // One kernel serves prefill and decode, flash-attention style on v_mfma_f32_16x16x32_bf16:
 //  * A workgroup (4 waves) takes a tile of 64 query rows of one kv head - row r is token
 //    r / G, head-in-group r % G (G = H / KVH) - and walks its visible keys in blocks of 32.
-//    A block's K rows and V (transposed, [d][32]) go through LDS; each wave computes its 16
+//    A block's K rows and V go through LDS (AttnLds); each wave computes its 16
 //    rows' scores S = Q K^T (Q rows read from LDS), masks them, and updates the online
 //    softmax in fp32: m = running row maximum (log2 domain), l = running sum, O = O * 2^(m_old
 //    - m) + P V, with P rounded to bf16 for the PV MFMAs (written to LDS and read back in the
@@ -80,12 +80,17 @@ __device__ __forceinline__ void resolve_position(AttnParams& p) {
 template <uint32_t D>
 struct AttnLds {
     static constexpr uint32_t kRow = D * 2u + 16u;           // Q and K rows (bytes)
-    static constexpr uint32_t kVtRow = kKeyBlock * 2u + 16u;  // V^T rows
+    // V: at head_dim 512 rows as loaded, read by transposing reads; below, transposed on the
+    // way in ([d][32 keys], 16-bit writes in an order rotated by the lane), which measured
+    // faster there (1024-token sliding layer 77 against 112 us; 179 against 203 at 512).
+    static constexpr bool kTrV = D >= 512u;
+    static constexpr uint32_t kVRow = D * 2u + 16u;           // V rows (bytes), kTrV
+    static constexpr uint32_t kVtRow = kKeyBlock * 2u + 16u;  // V^T rows, !kTrV
     static constexpr uint32_t kPRow = kKeyBlock * 2u + 16u;   // P rows
     static constexpr uint32_t kQ = 0;
     static constexpr uint32_t kK = kQ + kRowsPerTile * kRow;
-    static constexpr uint32_t kVt = kK + kKeyBlock * kRow;
-    static constexpr uint32_t kP = kVt + D * kVtRow;
+    static constexpr uint32_t kV = kK + kKeyBlock * kRow;
+    static constexpr uint32_t kP = kV + (kTrV ? kKeyBlock * kVRow : D * kVtRow);
     static constexpr uint32_t kBytes = kP + (kAttnThreads / 64u) * 16u * kPRow;
 };
 
@@ -98,6 +103,21 @@ __device__ __forceinline__ const uint16_t* key_row(const AttnParams& p, const ui
         return cache + (static_cast<size_t>(pos % p.cap) * p.KVH + hk) * D;
     }
     return chunk + (static_cast<size_t>(j - p.prefix) * p.KVH + hk) * D;
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef short short8_t __attribute__((ext_vector_type(8)));
+
+// The B operand (keys 8kb .. 8kb + 7 of one dim per lane) of a 16-dim tile of V rows kept
+// [key][dim] in LDS with `row` bytes between keys: two ds_read_b64_tr_b16, keys 8kb + e
+// then 8kb + 4 + e; p is this lane's address in the first (row 8kb + (j / 4), dims
+// 4 (j % 4) of the tile).
+__device__ __forceinline__ bf16x8_t v_operand_tr(uint8_t* p, uint32_t row) {
+    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<__attribute__((address_space(3))) short4_t*>(reinterpret_cast<uintptr_t>(p)));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<__attribute__((address_space(3))) short4_t*>(reinterpret_cast<uintptr_t>(p + 4u * row)));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 template <uint32_t D>
@@ -162,8 +182,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 
     // K and V of a key block: thread tid takes chunks tid + 256 u (key c / (D/8), chunk c %
     // (D/8): coalesced rows). The next block's chunks are loaded into registers while the
-    // current block computes; staging writes K rows and V^T (8 values per chunk, in an order
-    // rotated by the lane, which spreads a wave's 16-bit writes over the banks).
+    // current block computes; staging writes the K rows as loaded and V as AttnLds says.
     constexpr uint32_t kPer = kKeyBlock * kChunks / kAttnThreads;
     uint4 kn[kPer];
     uint4 vn[kPer];
@@ -193,16 +212,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
             const uint32_t r = c / kChunks;
             const uint32_t ch = c - r * kChunks;
             *reinterpret_cast<uint4*>(lds + Lds::kK + r * Lds::kRow + ch * 16u) = kn[u];
-            const uint4 vv = vn[u];
-            uint8_t* col = lds + Lds::kVt + (ch * 8u) * Lds::kVtRow + r * 2u;
+            if constexpr (Lds::kTrV) {
+                *reinterpret_cast<uint4*>(lds + Lds::kV + r * Lds::kVRow + ch * 16u) = vn[u];
+            } else {
+                const uint4 vv = vn[u];
+                uint8_t* col = lds + Lds::kV + (ch * 8u) * Lds::kVtRow + r * 2u;
 #pragma unroll
-            for (uint32_t s2 = 0; s2 < 8u; ++s2) {
-                const uint32_t e = (s2 + lane) & 7u;
-                const uint32_t d01 = (e & 2u) ? vv.y : vv.x;
-                const uint32_t d23 = (e & 2u) ? vv.w : vv.z;
-                const uint32_t dw = (e & 4u) ? d23 : d01;
-                *reinterpret_cast<uint16_t*>(col + e * Lds::kVtRow) =
-                    static_cast<uint16_t>((e & 1u) ? (dw >> 16) : (dw & 0xFFFFu));
+                for (uint32_t s2 = 0; s2 < 8u; ++s2) {
+                    const uint32_t e = (s2 + lane) & 7u;
+                    const uint32_t d01 = (e & 2u) ? vv.y : vv.x;
+                    const uint32_t d23 = (e & 2u) ? vv.w : vv.z;
+                    const uint32_t dw = (e & 4u) ? d23 : d01;
+                    *reinterpret_cast<uint16_t*>(col + e * Lds::kVtRow) =
+                        static_cast<uint16_t>((e & 1u) ? (dw >> 16) : (dw & 0xFFFFu));
+                }
             }
         }
         __syncthreads();
@@ -257,10 +280,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
         }
         // P (16 x 32 keys) as the A operand, V^T as B: O += P V.
         const bf16x8_t pa = *reinterpret_cast<const bf16x8_t*>(prow_w + j16 * Lds::kPRow + kb * 16u);
+        if constexpr (Lds::kTrV) {
+            uint8_t* vt = lds + Lds::kV + (8u * kb + (j16 >> 2)) * Lds::kVRow + (j16 & 3u) * 8u;
 #pragma unroll
-        for (uint32_t t = 0; t < kDTiles; ++t) {
-            const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(lds + Lds::kVt + (16u * t + j16) * Lds::kVtRow + kb * 16u);
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, o[t], 0, 0, 0);
+            for (uint32_t t = 0; t < kDTiles; ++t) {
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, v_operand_tr(vt + 32u * t, Lds::kVRow), o[t], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (uint32_t t = 0; t < kDTiles; ++t) {
+                const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(lds + Lds::kV + (16u * t + j16) * Lds::kVtRow + kb * 16u);
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, o[t], 0, 0, 0);
+            }
         }
     }
 
@@ -293,17 +324,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 //  * Q stays in registers as the A operand of S = Q K^T for the whole kernel;
 //  * K rows load straight from memory into the B operand (lane (j, kb) holds key j's dims
 //    8kb .. 8kb + 7 of a 32-dim step: 16 contiguous bytes of the row);
-//  * V rows load coalesced and go through the wave's own LDS transposed ([d][32 keys]); a
-//    lane writes its 8 values in an order rotated by its lane index, which spreads the
-//    16-bit writes of a wave over the banks;
+//  * V rows load coalesced into the wave's own LDS as they are ([32 keys][d], 16-byte
+//    writes) and reach the B operand of O += P V by transposing reads (two
+//    ds_read_b64_tr_b16 per 16-dim tile: lane (dim j, kb) takes keys 8kb .. 8kb + 7);
 //  * the online softmax, P in bf16 and the P.V products are those of attn_kernel.
 // Every split writes its unnormalised rows with (m, l); attn_combine_kernel merges them.
 template <uint32_t D>
 struct DecodeLds {
-    static constexpr uint32_t kVtRow = kKeyBlock * 2u + 16u;
+    static constexpr uint32_t kVRow = D * 2u + 16u;   // a V row (bytes), padded by 16
     static constexpr uint32_t kPRow = kKeyBlock * 2u + 16u;
-    static constexpr uint32_t kVt = 0;   // also the query rows' staging before the key loop
-    static constexpr uint32_t kP = kVt + D * kVtRow;
+    static constexpr uint32_t kV = 0;   // [32 keys][kVRow]; also the query rows' staging before the key loop
+    static constexpr uint32_t kP = kV + kKeyBlock * kVRow;
     static constexpr uint32_t kNew = kP + 16u * kPRow;   // the new token's K and V rows (bf16)
     static constexpr uint32_t kWave = kNew + 4u * D;
     static constexpr uint32_t kWaves = D <= 256u ? 4u : 2u;
@@ -392,13 +423,13 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
     bool fresh_key = false;
     if constexpr (PREP) {
         // attn_prepare_kernel's work for one token (L = 1), in its arithmetic: q_norm and
-        // RoPE of this kv head's G query rows, staged in the V^T area; k_norm + RoPE and
+        // RoPE of this kv head's G query rows, staged in the V area; k_norm + RoPE and
         // v_norm of the new key by the wave whose range holds it.
         constexpr uint32_t kU = D / 64u;             // 64-value units per head row
         constexpr uint32_t kHalf = D / 2u;
         const bool has_keys = j_begin < j_end;       // wave-uniform
         fresh_key = has_keys && j_begin <= p.prefix && p.prefix < j_end;
-        uint16_t* qs = reinterpret_cast<uint16_t*>(my + Lds::kVt);   // [G][D]
+        uint16_t* qs = reinterpret_cast<uint16_t*>(my + Lds::kV);   // [G][D]
         const uint32_t pos = p.offset;
         float2 cs8[8];
         {
@@ -548,23 +579,13 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
 #pragma unroll
             for (uint32_t u = 0; u < kTilesUpFront; ++u) {
                 const uint32_t c = c0 + u;
-                // V^T into LDS: 8 values per chunk in an order rotated by the lane.
+                // V rows into LDS as loaded.
 #pragma unroll
                 for (uint32_t it = 0; it < kVPer; ++it) {
                     const uint32_t cidx = lane + 64u * it;
                     const uint32_t r = 16u * c + cidx / kChunks;
                     const uint32_t ch = cidx % kChunks;
-                    const uint4 vv = vr[u][it];
-                    uint8_t* col = my + Lds::kVt + (ch * 8u) * Lds::kVtRow + r * 2u;
-#pragma unroll
-                    for (uint32_t s2 = 0; s2 < 8u; ++s2) {
-                        const uint32_t e = (s2 + lane) & 7u;
-                        const uint32_t d01 = (e & 2u) ? vv.y : vv.x;
-                        const uint32_t d23 = (e & 2u) ? vv.w : vv.z;
-                        const uint32_t dw = (e & 4u) ? d23 : d01;
-                        *reinterpret_cast<uint16_t*>(col + e * Lds::kVtRow) =
-                            static_cast<uint16_t>((e & 1u) ? (dw >> 16) : (dw & 0xFFFFu));
-                    }
+                    *reinterpret_cast<uint4*>(my + Lds::kV + r * Lds::kVRow + ch * 16u) = vr[u][it];
                 }
                 // S for this tile's 16 keys.
 #pragma unroll
@@ -608,12 +629,14 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
 #pragma unroll
             for (uint32_t t = 0; t < kDTiles; ++t) o[t][i] *= alpha;
         }
-        // O += P V.
+        // O += P V: the B operand of dim tile t by transposing reads of the V rows (the
+        // lanes 4e .. 4e + 3 of a 16-lane group address key 8kb + e at dims 16t + 4(j % 4),
+        // and lane j receives V[8kb + e][16t + j] as element e).
         const bf16x8_t pa = *reinterpret_cast<const bf16x8_t*>(my + Lds::kP + j16 * Lds::kPRow + kb * 16u);
+        uint8_t* vt = my + Lds::kV + (8u * kb + (j16 >> 2)) * Lds::kVRow + (j16 & 3u) * 8u;
 #pragma unroll
         for (uint32_t t = 0; t < kDTiles; ++t) {
-            const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(my + Lds::kVt + (16u * t + j16) * Lds::kVtRow + kb * 16u);
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, v_operand_tr(vt + 32u * t, Lds::kVRow), o[t], 0, 0, 0);
         }
     }
 
