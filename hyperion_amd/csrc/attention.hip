@@ -397,7 +397,9 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
     using Lds = DecodeLds<D>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
+    // Wave-uniform (a scalar): the key range, has_keys and fresh_key below follow from it,
+    // and their branches then stay scalar rather than masking lanes around the loads.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t split = blockIdx.x * Lds::kWaves + wave;
     if (split >= p.splits) return;   // no workgroup barrier below: waves are independent
     const uint32_t hk = blockIdx.y;
@@ -417,7 +419,8 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
     constexpr uint32_t kSteps = D / 32u;
     constexpr uint32_t kDTiles = D / 16u;
     bf16x8_t qa[kSteps];
-    // PREP: the new token's K and V rows (this wave's keys include it when fresh_key).
+    // PREP: the new token's K and V rows staged for the RoPE (this wave's keys include it
+    // when fresh_key).
     uint16_t* new_k = reinterpret_cast<uint16_t*>(my + Lds::kNew);
     uint16_t* new_v = new_k + D;
     bool fresh_key = false;
@@ -477,6 +480,29 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
 #pragma unroll
                 for (int t = 0; t < 8; ++t) wv[t] = w4[t];
             }
+            // One dword of every 128-byte line of the first key block's K and V rows, requested
+            // behind this prologue's loads and consumed at its end: their HBM fetch overlaps
+            // the prologue, and the key loop's loads of them hit the cache.
+            uint32_t touch = 0u;
+            asm volatile("" ::: "memory");   // these requests after the prologue's own
+            {
+                constexpr uint32_t kLines = D * 2u / 128u;   // lines per row
+                constexpr uint32_t kTouch = 2u * kKeyBlock * kLines;
+                const uint32_t nk0 = min(kKeyBlock, j_end - j_begin);
+                if (j_begin != p.prefix) {   // (a block that starts at the new key holds only it)
+#pragma unroll
+                    for (uint32_t i = 0; i < kTouch / 64u; ++i) {
+                        const uint32_t li = lane + 64u * i;
+                        const uint32_t half = li / (kKeyBlock * kLines);   // 0: K, 1: V
+                        const uint32_t rest = li - half * kKeyBlock * kLines;
+                        const uint32_t r = rest / kLines;
+                        // past the block or the new key's row (not read before its store): row 0
+                        const uint32_t rr = r < nk0 && j_begin + r != p.prefix ? r : 0u;
+                        const uint16_t* row = key_row(p, nullptr, half == 0u ? p.ck : p.cv, j_begin + rr, hk, D);
+                        touch |= *reinterpret_cast<const uint32_t*>(row + (rest - r * kLines) * 64u);
+                    }
+                }
+            }
             // The prepare's 64-lane butterfly over a row's kU lanes (the rest of its lanes
             // add zeros there).
             float ss = src != nullptr ? unit_sumsq(xv) : 0.0f;
@@ -505,6 +531,11 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
 #pragma unroll
                 for (int t = 0; t < 8; ++t) kg[t] = kl[t];
             }
+            asm volatile("" ::"v"(touch));
+            // The new key's cache slot is written (above, by this wave): once those stores are
+            // complete the key loop's ordinary loads read it (no other wave reads that slot,
+            // and nothing on this compute unit has read it in this launch).
+            __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
             for (uint32_t st = 0; st < kSteps; ++st) {
                 uint4 v = make_uint4(0u, 0u, 0u, 0u);
@@ -556,24 +587,18 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
                 const uint32_t c = c0 + u;
                 const uint32_t key = 16u * c + j16;
                 const uint16_t* row = key < nk ? key_row(p, p.k, p.ck, jb + key, hk, D) + kb * 8u : nullptr;
-                // PREP: the new token's key from this wave's LDS (its cache slot is being
-                // written by this launch).
-                const bool kfresh = PREP && fresh_key && key < nk && jb + key == p.prefix;
 #pragma unroll
                 for (uint32_t st = 0; st < kSteps; ++st) {
-                    kr[u][st] = kfresh ? *reinterpret_cast<const uint4*>(new_k + kb * 8u + st * 32u)
-                                : row != nullptr ? *reinterpret_cast<const uint4*>(row + st * 32u)
-                                                 : make_uint4(0u, 0u, 0u, 0u);
+                    kr[u][st] = row != nullptr ? *reinterpret_cast<const uint4*>(row + st * 32u)
+                                               : make_uint4(0u, 0u, 0u, 0u);
                 }
 #pragma unroll
                 for (uint32_t it = 0; it < kVPer; ++it) {
                     const uint32_t cidx = lane + 64u * it;
                     const uint32_t r = 16u * c + cidx / kChunks;
                     const uint32_t ch = cidx % kChunks;
-                    const bool vfresh = PREP && fresh_key && r < nk && jb + r == p.prefix;
-                    vr[u][it] = vfresh ? *reinterpret_cast<const uint4*>(new_v + ch * 8u)
-                                : r < nk ? *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u)
-                                         : make_uint4(0u, 0u, 0u, 0u);
+                    vr[u][it] = r < nk ? *reinterpret_cast<const uint4*>(key_row(p, p.v, p.cv, jb + r, hk, D) + ch * 8u)
+                                       : make_uint4(0u, 0u, 0u, 0u);
                 }
             }
 #pragma unroll
