@@ -13,7 +13,8 @@
 //    residual <- bf16(residual + rms_norm(branch, w_post)), then optionally
 //    residual <- bf16(residual * layer_scalar), then optionally next <- rms_norm(residual,
 //    w_next) (the following block's input norm). One workgroup per row, thread u owning unit
-//    u; both statistics in the order of q4_rmsnorm.h, so each norm has the bits of
+//    u (one wave, no LDS, for rows of at most 64 units: residual_norm_wave_kernel); both
+//    statistics in the order of q4_rmsnorm.h, so each norm has the bits of
 //    launch_rms_normalize and of the skinny matmul's normalising prologue.
 #include "common.h"
 #include "kernels.h"
@@ -242,6 +243,77 @@ __global__ __launch_bounds__(kThreads) void residual_norm_kernel(const uint16_t*
     }
 }
 
+// residual_norm_kernel for rows of at most 64 units, one wave per row: the unit sums stay
+// in registers and meet in the same 64-lane butterfly (after which every lane holds the
+// bits lane 0 of the block form computes), so there is no LDS round trip or workgroup
+// barrier. The same arithmetic as residual_norm_kernel, bit for bit.
+__global__ __launch_bounds__(64) void residual_norm_wave_kernel(const uint16_t* __restrict__ branch,
+                                                                uint16_t* __restrict__ residual,
+                                                                const uint16_t* __restrict__ w_post,
+                                                                const uint16_t* __restrict__ scalar,
+                                                                const uint16_t* __restrict__ w_next,
+                                                                uint16_t* __restrict__ next, uint32_t hidden, float eps) {
+    const uint32_t units = hidden / 64u;
+    const uint32_t lane = threadIdx.x;
+    const size_t row = static_cast<size_t>(blockIdx.x) * hidden;
+    const uint4* b4 = reinterpret_cast<const uint4*>(branch + row) + lane * 8u;
+    uint4* r4 = reinterpret_cast<uint4*>(residual + row) + lane * 8u;
+    const bool mine = lane < units;
+
+    uint4 xv[8];
+    uint4 rv[8];
+    uint4 wv[8];
+    uint4 nv[8];
+    if (mine) {
+        const uint4* w4 = reinterpret_cast<const uint4*>(w_post) + lane * 8u;
+        const uint4* n4 = reinterpret_cast<const uint4*>(w_next != nullptr ? w_next : w_post) + lane * 8u;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {   // every load of the row issued before the first use
+            xv[t] = b4[t];
+            rv[t] = r4[t];
+            wv[t] = w4[t];
+            nv[t] = n4[t];
+        }
+    }
+    const float sc = scalar != nullptr ? bf16_bits_to_f32(*scalar) : 1.0f;
+    float ss = mine ? unit_sumsq(xv) : 0.0f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    float ss2 = 0.0f;
+    if (mine) {
+        normalize_unit(xv, rms_inverse(ss, hidden, eps));
+        weight_unit(xv, wv);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
+            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
+                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
+                if (scalar != nullptr) {
+                    lo = round_bf16(lo * sc);
+                    hi = round_bf16(hi * sc);
+                }
+                hw[q] = cvt_pk_bf16(lo, hi);
+            }
+            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            r4[t] = xv[t];
+        }
+        if (w_next != nullptr) ss2 = unit_sumsq(xv);
+    }
+    if (w_next == nullptr) return;   // uniform over the launch
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss2 += __shfl_xor(ss2, off, 64);
+    if (mine) {
+        normalize_unit(xv, rms_inverse(ss2, hidden, eps));
+        weight_unit(xv, nv);
+        uint4* n4 = reinterpret_cast<uint4*>(next + row) + lane * 8u;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) n4[t] = xv[t];
+    }
+}
+
 __global__ void decode_advance_kernel(uint32_t* pos, uint32_t* ties, const HypTopKSample* sample) {
     if (threadIdx.x == 0u) {
         pos[0] += 1u;
@@ -304,8 +376,13 @@ void launch_residual_norm(const uint16_t* branch, uint16_t* residual, const uint
     if (m == 0) return;
     HYP_REQUIRE(hidden % 64u == 0u && hidden <= residual_norm_max_hidden(), HYP_STATUS_UNSUPPORTED,
                 "residual norm: hidden must be a multiple of 64, at most 16384");
-    hipLaunchKernelGGL(residual_norm_kernel, dim3(m), dim3(kThreads), 0, stream, branch, residual, w_post, scalar,
-                       w_next, next, hidden, eps);
+    if (hidden <= 64u * 64u) {
+        hipLaunchKernelGGL(residual_norm_wave_kernel, dim3(m), dim3(64), 0, stream, branch, residual, w_post, scalar,
+                           w_next, next, hidden, eps);
+    } else {
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(m), dim3(kThreads), 0, stream, branch, residual, w_post, scalar,
+                           w_next, next, hidden, eps);
+    }
     HYP_HIP_CHECK(hipGetLastError());
 }
 
