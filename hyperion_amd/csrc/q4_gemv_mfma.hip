@@ -446,12 +446,34 @@ void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epi
         launch_skinny_t<M, true, 0, kSkinnyDualWaves>(p, tiles_total, stream);
     } else if (epi == Epilogue::kSoftcap) {
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
-    } else if (norm == 2) {
-        launch_skinny_t<M, false, 0, kSkinnyWaves, 2>(p, tiles_total, stream);
-    } else if (norm == 1) {
-        launch_skinny_t<M, false, 0, kSkinnyWaves, 1>(p, tiles_total, stream);
     } else {
-        launch_skinny_t<M, false, 0, kSkinnyWaves>(p, tiles_total, stream);
+        // 16-wave workgroups run one per compute unit: a grid a little over the compute
+        // units (the 12B's global q/k: 544 tiles x 8 splits = 272 workgroups) would run a
+        // second round for its last few. Then 8-wave workgroups, two per compute unit, at
+        // half the splits (the same workgroup count, each wave twice the pairs, still all
+        // in flight at once) take it in one. Not the plain norm form: at 8 waves it takes
+        // 149-163 VGPRs, one workgroup per compute unit.
+        const uint64_t ts = static_cast<uint64_t>(tiles_total) * p.splits;
+        const uint64_t cus = device_compute_units();
+        const uint32_t half = p.splits / 2u;
+        const bool narrow = norm != 1 && (ts + kSkinnyWaves - 1u) / kSkinnyWaves > cus && half >= 1u &&
+                            (p.pairs + half - 1u) / half <= kSkinnyPairsUpFront &&
+                            (ts / 2u + kSkinnyDualWaves - 1u) / kSkinnyDualWaves <= 2u * cus &&
+                            (norm != 2 || static_cast<uint64_t>(M) * (p.k / 64u) <= 64u * kSkinnyDualWaves);
+        SkinnyParams q = p;
+        if (narrow) {
+            q.splits = half;
+            q.split_shift = static_cast<uint32_t>(__builtin_ctz(half));
+        }
+        if (norm == 2) {
+            narrow ? launch_skinny_t<M, false, 0, kSkinnyDualWaves, 2>(q, tiles_total, stream)
+                   : launch_skinny_t<M, false, 0, kSkinnyWaves, 2>(p, tiles_total, stream);
+        } else if (norm == 1) {
+            launch_skinny_t<M, false, 0, kSkinnyWaves, 1>(p, tiles_total, stream);
+        } else {
+            narrow ? launch_skinny_t<M, false, 0, kSkinnyDualWaves>(q, tiles_total, stream)
+                   : launch_skinny_t<M, false, 0, kSkinnyWaves>(p, tiles_total, stream);
+        }
     }
 }
 
