@@ -3,11 +3,13 @@
 //  * attn_prepare_kernel - ForwardPass::attention from the q/k/v projections to the cache
 //    append (native/hyperion_mlx/src/forward.cc:395-459): q <- rope(q_norm(q)) in place;
 //    K slot <- rope(k_norm(k_raw)); V slot <- v_norm(v_raw), v_raw = k_raw on K = V global
-//    layers (forward.cc:403-412). One wave per (token, head): it normalises the head (lane u
-//    owns 64-value unit u, the order of q4_rmsnorm.h), stages it in LDS and rotates pairs
-//    (i, i + D/2) with their (cos, sin) computed in place or read from a table that
-//    rope_table_kernel filled with the same arithmetic. Bits: those of rms_norm_rows_kernel
-//    followed by rope_kernel and kv_write_kernel.
+//    layers (forward.cc:403-412). A wave takes 64 / (D/64) head rows (q, K or V rows of any
+//    tokens): D/64 lanes normalise a row (lane owns a 64-value unit, the order of
+//    q4_rmsnorm.h), the q and K rows are staged in LDS and their pairs (i, i + D/2) rotated
+//    with (cos, sin) computed in place or read from a table that rope_table_kernel filled
+//    with the same arithmetic (chunks of up to 16 tokens: attn_prepare_head_kernel, one wave
+//    per head). Bits: those of rms_norm_rows_kernel followed by rope_kernel and
+//    kv_write_kernel.
 //
 //  * residual_norm_kernel - the Gemma sandwich around a block (forward.cc:518-529):
 //    residual <- bf16(residual + rms_norm(branch, w_post)), then optionally
@@ -26,6 +28,10 @@ namespace {
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kWaves = kThreads / 64u;
 constexpr uint32_t kMaxHeadDim = 512;
+// Chunks of at most this many tokens take attn_prepare_head_kernel (measured on a 12B global
+// layer, one token: 7.1 us against 11.5 for the packed rows; 1024-token chunks: 20.5 us packed
+// against 37.6).
+constexpr uint32_t kPrepareHeadMaxTokens = 16;
 
 struct PrepareParams {
     const uint32_t* pos;      // non-null: offset = *pos
@@ -75,9 +81,10 @@ __device__ __forceinline__ float2 rope_angle(uint32_t pos, uint32_t i, uint32_t 
                        static_cast<float>(sin(static_cast<double>(theta))));
 }
 
-// Grid (L, ceil((H + KVH) / 4)): wave w of workgroup (t, y) takes head 4y + w of token t
-// (q heads first, then kv heads).
-__global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p) {
+// Short chunks (a decode step: a few dozen rows, which attn_prepare_kernel would give to a
+// few waves): grid (L, ceil((H + KVH) / 4)), wave w of workgroup (t, y) takes head 4y + w
+// of token t (q heads first, then kv heads), all 64 lanes in its RoPE. The same bits.
+__global__ __launch_bounds__(kThreads) void attn_prepare_head_kernel(PrepareParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t head[kWaves][kMaxHeadDim];
     const uint32_t t = blockIdx.x;
     const uint32_t lane = threadIdx.x & 63u;
@@ -149,6 +156,145 @@ __global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p)
             dst[i] = f32_to_bf16_bits(a1 - a2);
             dst[i + half] = f32_to_bf16_bits(b1 + b2);
         }
+    }
+}
+
+// Rows of the flattened [token][H + 2 KVH] space (q heads, then each kv head's K, then its V),
+// D/64 lanes per row, one 64-value unit per lane: a wave takes 64 / (D/64) rows (16 at
+// head_dim 256) instead of one head, so its lanes and loads are all busy (a 1024-token
+// chunk of a 12B sliding layer: 37 us with one wave per head). Per row: the unit sums of
+// squares of q4_rmsnorm.h met in a butterfly over the row's D/64 lanes (a 64-lane butterfly
+// with the other lanes at zero adds the same partial sums in the same order), bf16(x * inv),
+// bf16(w * x), then the RoPE of rope_kernel on the q and K rows. Q rows are
+// normalised and rotated in place, K rows into their cache slot, V rows normalised (no
+// weight) into theirs.
+template <uint32_t D>
+__global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p) {
+    constexpr uint32_t kU = D / 64u;            // lanes (units) per row
+    constexpr uint32_t kR = 64u / kU;           // rows per wave
+    constexpr uint32_t kHalf = D / 2u;
+    constexpr uint32_t kHalfChunks = kHalf / 8u;
+    constexpr uint32_t kRopeRows = 64u / kHalfChunks;   // rows one RoPE pass covers
+    __shared__ __attribute__((aligned(16))) uint16_t stage[kWaves][kR * D];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t per_tok = p.H + 2u * p.KVH;
+    const uint32_t total = p.L * per_tok;   // < 2^31 (checked on the host)
+    const uint32_t row0 = (blockIdx.x * kWaves + wave) * kR;
+    if (row0 >= total) return;   // wave-uniform; no workgroup barrier below
+    const uint32_t base_pos = p.pos != nullptr ? *p.pos : p.offset;
+    uint16_t* sw = stage[wave];
+
+    // Row idx: its token, kind (0 q, 1 K, 2 V), head, and whether it is written.
+    const auto row_of = [&](uint32_t idx, uint32_t& t, uint32_t& kind, uint32_t& hd, bool& active) {
+        const bool live = idx < total;
+        t = live ? idx / per_tok : 0u;
+        const uint32_t hh = live ? idx - t * per_tok : 0u;
+        kind = hh < p.H ? 0u : (hh < p.H + p.KVH ? 1u : 2u);
+        hd = kind == 0u ? hh : (kind == 1u ? hh - p.H : hh - p.H - p.KVH);
+        active = live && (kind == 0u || t >= p.first_cached);
+    };
+    const uint32_t r = lane / kU;
+    const uint32_t u = lane - r * kU;
+    uint32_t t, kind, hd;
+    bool active;
+    row_of(row0 + r, t, kind, hd, active);
+    const size_t kv_row = (static_cast<size_t>(t) * p.KVH + hd) * D;
+    const uint16_t* src = kind == 0u ? p.q + (static_cast<size_t>(t) * p.H + hd) * D
+                          : kind == 1u ? p.k_raw + kv_row
+                                       : (p.v_raw != nullptr ? p.v_raw : p.k_raw) + kv_row;
+    const uint16_t* w = kind == 0u ? p.q_w : (kind == 1u ? p.k_w : nullptr);
+    uint4 xv[8];
+    uint4 wv[8];
+    if (active) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src + u * 64u);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xv[q] = s4[q];
+        if (w != nullptr) {
+            const uint4* w4 = reinterpret_cast<const uint4*>(w + u * 64u);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) wv[q] = w4[q];
+        }
+    }
+    float ss = active ? unit_sumsq(xv) : 0.0f;
+#pragma unroll
+    for (uint32_t off = kU / 2u; off > 0u; off >>= 1) ss += __shfl_xor(ss, static_cast<int>(off), 64);
+    const size_t slot_row = (static_cast<size_t>((base_pos + t) % p.cap) * p.KVH + hd) * D;
+    if (active) {
+        normalize_unit(xv, rms_inverse(ss, D, p.eps));
+        if (w != nullptr) weight_unit(xv, wv);
+        uint4* dst = kind == 2u ? reinterpret_cast<uint4*>(p.cache_v + slot_row + u * 64u)
+                                : reinterpret_cast<uint4*>(sw + r * D + u * 64u);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[q] = xv[q];
+    }
+    // The wave's LDS instructions execute in order: only the compiler must keep the RoPE's
+    // reads after the writes above (and the stores below after the RoPE's writes).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // RoPE of the staged q and K rows: a lane takes 8 consecutive pairs (i, i + D/2).
+    {
+        const uint32_t c = lane % kHalfChunks;
+        for (uint32_t rr = lane / kHalfChunks; rr < kR; rr += kRopeRows) {
+            uint32_t tr, kr, hr;
+            bool ar;
+            row_of(row0 + rr, tr, kr, hr, ar);
+            if (!ar || kr == 2u) continue;
+            const uint32_t pos = base_pos + tr;
+            float2 cs8[8];
+            if (p.rope_cs != nullptr) {
+                const float4* t4 = reinterpret_cast<const float4*>(p.rope_cs + static_cast<size_t>(pos) * kHalf + c * 8u);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float4 v = t4[e];
+                    cs8[2 * e] = make_float2(v.x, v.y);
+                    cs8[2 * e + 1] = make_float2(v.z, v.w);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) cs8[e] = rope_angle(pos, c * 8u + e, D, p.rotated, p.base);
+            }
+            uint4* lo = reinterpret_cast<uint4*>(sw + rr * D + c * 8u);
+            uint4* hi = reinterpret_cast<uint4*>(sw + rr * D + kHalf + c * 8u);
+            const uint4 a = *lo;
+            const uint4 b = *hi;
+            const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+            const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+            uint32_t ow[4];
+            uint32_t pw[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t o2[2];
+                uint32_t p2[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float2 cs = cs8[2 * q + h];
+                    const float x1 = bf16_bits_to_f32((aw[q] >> (16 * h)) & 0xFFFFu);
+                    const float x2 = bf16_bits_to_f32((bw[q] >> (16 * h)) & 0xFFFFu);
+                    const float a1 = x1 * cs.x;
+                    const float a2 = x2 * cs.y;
+                    const float b1 = x1 * cs.y;
+                    const float b2 = x2 * cs.x;
+                    o2[h] = f32_to_bf16_bits(a1 - a2);
+                    p2[h] = f32_to_bf16_bits(b1 + b2);
+                }
+                ow[q] = o2[0] | (o2[1] << 16);
+                pw[q] = p2[0] | (p2[1] << 16);
+            }
+            *lo = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            *hi = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (active && kind != 2u) {
+        uint4* dst = kind == 0u ? reinterpret_cast<uint4*>(p.q + (static_cast<size_t>(t) * p.H + hd) * D + u * 64u)
+                                : reinterpret_cast<uint4*>(p.cache_k + slot_row + u * 64u);
+        const uint4* st4 = reinterpret_cast<const uint4*>(sw + r * D + u * 64u);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[q] = st4[q];
     }
 }
 
@@ -352,8 +498,25 @@ void launch_attn_prepare(const AttnPrepareArgs& a, hipStream_t stream) {
     p.first_cached = a.L > a.cap ? a.L - a.cap : 0u;
     p.base = static_cast<double>(a.base);
     p.eps = a.eps;
-    const uint32_t groups = (a.n_heads + a.n_kv_heads + kWaves - 1u) / kWaves;
-    hipLaunchKernelGGL(attn_prepare_kernel, dim3(a.L, groups), dim3(kThreads), 0, stream, p);
+    if (a.L <= kPrepareHeadMaxTokens) {
+        const uint32_t groups = (a.n_heads + a.n_kv_heads + kWaves - 1u) / kWaves;
+        hipLaunchKernelGGL(attn_prepare_head_kernel, dim3(a.L, groups), dim3(kThreads), 0, stream, p);
+        HYP_HIP_CHECK(hipGetLastError());
+        return;
+    }
+    const uint64_t rows = static_cast<uint64_t>(a.L) * (a.n_heads + 2u * a.n_kv_heads);
+    const uint64_t per_block = static_cast<uint64_t>(kWaves) * (64u / (a.head_dim / 64u));
+    const uint64_t blocks = (rows + per_block - 1u) / per_block;
+    HYP_REQUIRE(rows + per_block < (1ull << 31), HYP_STATUS_INVALID_ARGUMENT, "attention prepare: too many rows");
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    switch (a.head_dim) {
+        case 64: hipLaunchKernelGGL(attn_prepare_kernel<64>, grid, dim3(kThreads), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL(attn_prepare_kernel<128>, grid, dim3(kThreads), 0, stream, p); break;
+        case 256: hipLaunchKernelGGL(attn_prepare_kernel<256>, grid, dim3(kThreads), 0, stream, p); break;
+        case 512: hipLaunchKernelGGL(attn_prepare_kernel<512>, grid, dim3(kThreads), 0, stream, p); break;
+        default:
+            throw NativeError(HYP_STATUS_UNSUPPORTED, "attention prepare: head_dim must be 64, 128, 256 or 512");
+    }
     HYP_HIP_CHECK(hipGetLastError());
 }
 
