@@ -336,6 +336,8 @@ def test_sampled_greedy_sidecar_and_contract(tiny, tmp_path):
     (300, 16, 1, 512, 128, 1e6, 3, True),
     (9, 4, 2, 64, 64, 1e4, 20, False),
     (3, 4, 1, 128, 32, 1e6, 11, True),
+    (40, 4, 2, 64, 64, 1e4, 20, False),    # above 16 tokens: the packed-row form
+    (33, 4, 1, 128, 32, 1e6, 70, True),
 ])
 def test_attention_prepare_bit_exact(stream, L, H, KVH, D, rotated, base, offset, kv_eq):
     """hyp_attention_prepare == hyp_rms_normalize + hyp_rope on q, the same on k, the
