@@ -601,6 +601,10 @@ constexpr size_t g_lds_bytes() {
                : 16u * MT * (32u * NT * W + 32u);
 }
 
+// A DUAL launch keeps its GELU table past the X ring.
+template <int MT, int NT, int W, bool DUAL>
+constexpr size_t g_lds_total() { return g_lds_bytes<MT, NT, W>() + (DUAL ? kGeluTableBytes : 0u); }
+
 template <int MT, int NT, int W, bool DUAL>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void q4_gemm_g_kernel(GemmParams p) {
     static_assert(!DUAL || NT == 2, "a dual launch pairs one gate and one up tile per wave");
@@ -678,6 +682,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     for (uint32_t i = 0; i < kSync; ++i) load_x(min(g0 + i, g1 - 1u), xs + i * kStage);
     load_graw<NT>(wr, c_off, s_off, g0, r[0]);
     load_graw<NT>(wr, c_off, s_off, min(g0 + 1u, g1 - 1u), r[1]);
+    // A DUAL epilogue's GELU table (past the X ring) is computed while the first loads are
+    // in flight, instead of after the last MFMA (256-row tile at m = 2048: 7 chains per
+    // thread per tile, about 4 tiles per compute unit).
+    uint16_t* tab = reinterpret_cast<uint16_t*>(xs + g_lds_bytes<MT, NT, W>());
+    if constexpr (DUAL) {
+        if (p.ksplit == 1u) build_gelu_table(tab, tid, 64u * W);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     bf16x8_t b0[NT], b1[NT];
@@ -764,14 +775,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 
     // Epilogue through LDS as in q4_gemm_kernel (rows of 32 kOut W bytes plus 32 of padding).
     constexpr uint32_t kOutRow = 32u * kOut * W + 32u;
-    static_assert(BM * kOutRow + (DUAL ? kGeluTableBytes : 0u) <= g_lds_bytes<MT, NT, W>(),
-                  "output staging exceeds the LDS");
-    uint16_t* tab = reinterpret_cast<uint16_t*>(xs + BM * kOutRow);
+    static_assert(BM * kOutRow <= g_lds_bytes<MT, NT, W>(), "output staging exceeds the X ring");
     __syncthreads();
-    if constexpr (DUAL) {
-        build_gelu_table(tab, tid, 64u * W);
-        __syncthreads();
-    }
     stage_out<MT, NT, kOut, DUAL>(xs, kOutRow, wave, lane, acc, tab);
     __syncthreads();
     constexpr uint32_t kChunks = 16u * kOut * W / 8u;
@@ -927,7 +932,7 @@ template <int MT, int NT, int W, bool DUAL>
 void launch_g(GemmParams p, hipStream_t stream) {
     retile(p, 16u * (DUAL ? 1u : NT) * W);
     auto kernel = q4_gemm_g_kernel<MT, NT, W, DUAL>;
-    constexpr size_t lds = g_lds_bytes<MT, NT, W>();
+    constexpr size_t lds = g_lds_total<MT, NT, W, DUAL>();
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "gemm: X tiles exceed the device's LDS");
     if (lds > 65536u) {
         static thread_local int configured_device = -1;
