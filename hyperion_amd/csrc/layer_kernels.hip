@@ -15,8 +15,9 @@
 //    residual <- bf16(residual + rms_norm(branch, w_post)), then optionally
 //    residual <- bf16(residual * layer_scalar), then optionally next <- rms_norm(residual,
 //    w_next) (the following block's input norm). One workgroup per row, thread u owning unit
-//    u (one wave, no LDS, for rows of at most 64 units: residual_norm_wave_kernel); both
-//    statistics in the order of q4_rmsnorm.h, so each norm has the bits of
+//    u (one wave, no LDS, for rows of at most 64 units: residual_norm_wave_kernel; from 64
+//    rows on, residual_norm_tiled_kernel, the same lanes' arithmetic behind coalesced
+//    loads and stores through LDS); both statistics in the order of q4_rmsnorm.h, so each norm has the bits of
 //    launch_rms_normalize and of the skinny matmul's normalising prologue.
 #include "common.h"
 #include "kernels.h"
@@ -460,6 +461,158 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(const uint16_t* 
     }
 }
 
+// residual_norm_wave_kernel for many rows (prefill chunks), with the same per-lane
+// arithmetic (lane u owns unit u) but coalesced memory access: the wave kernel's lanes each
+// read 128 contiguous bytes, so every 16-byte load instruction touches 64 cache lines. Here a
+// wave's loads and stores move 1 KB of consecutive bytes per instruction, and the row and
+// the workgroup's two weights pass through LDS tiles in which chunk t of unit u sits at slot
+// 8u + (t ^ (u % 8)) (the lanes reading their units' chunk t hit distinct banks). One row per
+// wave, kTiledRows rows per workgroup.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kTiledRows = 4;
+constexpr uint32_t kResidualTiledMinRows = 64;
+
+__device__ __forceinline__ uint32_t unit_slot(uint32_t u, uint32_t t) { return u * 8u + (t ^ (u & 7u)); }
+
+// Orders one wave's LDS accesses across its lanes (a wave's LDS instructions execute in
+// order; only the compiler must keep them in program order).
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(64 * kTiledRows) void residual_norm_tiled_kernel(
+    const uint16_t* __restrict__ branch, uint16_t* __restrict__ residual, const uint16_t* __restrict__ w_post,
+    const uint16_t* __restrict__ scalar, const uint16_t* __restrict__ w_next, uint16_t* __restrict__ next,
+    uint32_t m, uint32_t hidden, float eps) {
+    __shared__ uint4 wt[2][512];            // w_post, w_next: 64 units x 8 chunks at most
+    __shared__ uint4 rt[kTiledRows][512];   // one row per wave
+    const uint32_t units = hidden / 64u;
+    const uint32_t chunks = units * 8u;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    const uint32_t row = blockIdx.x * kTiledRows + wave;
+    const bool live = row < m;
+    const size_t base = static_cast<size_t>(live ? row : 0u) * hidden;
+    const uint4* b4 = reinterpret_cast<const uint4*>(branch + base);
+    uint4* r4 = reinterpret_cast<uint4*>(residual + base);
+
+    u32x4_t bc[8];   // native vectors: held in registers (uint4 arrays here went to scratch)
+    u32x4_t rc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {   // the row's loads, issued before the weights are staged;
+        // chunks past the row re-read its last one (unused), so no load sits behind a branch
+        const uint32_t c = min(lane + 64u * t, chunks - 1u);
+        bc[t] = *reinterpret_cast<const u32x4_t*>(b4 + c);
+        rc[t] = *reinterpret_cast<const u32x4_t*>(r4 + c);
+    }
+    const uint4* wp4 = reinterpret_cast<const uint4*>(w_post);
+    const uint4* wn4 = reinterpret_cast<const uint4*>(w_next != nullptr ? w_next : w_post);
+#pragma unroll
+    for (uint32_t i = 0; i < 512u / (64u * kTiledRows); ++i) {   // at most 512 chunks
+        const uint32_t c = tid + 64u * kTiledRows * i;
+        if (c < chunks) {
+            wt[0][unit_slot(c >> 3, c & 7u)] = wp4[c];
+            wt[1][unit_slot(c >> 3, c & 7u)] = wn4[c];
+        }
+    }
+    __syncthreads();
+    if (!live) return;   // no workgroup barrier below
+
+    const bool mine = lane < units;
+    uint4* tile = rt[wave];
+    uint4 xv[8];
+    uint4 rv[8];
+    uint4 wv[8];   // w_post, then w_next, read from their tile where used
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {   // lanes past the row write the last chunk's own value again
+        const uint32_t c = min(lane + 64u * t, chunks - 1u);
+        tile[unit_slot(c >> 3, c & 7u)] = __builtin_bit_cast(uint4, bc[t]);
+    }
+    wave_lds_order();
+    if (mine) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xv[t] = tile[unit_slot(lane, t)];
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {   // lanes past the row write the last chunk's own value again
+        const uint32_t c = min(lane + 64u * t, chunks - 1u);
+        tile[unit_slot(c >> 3, c & 7u)] = __builtin_bit_cast(uint4, rc[t]);
+    }
+    wave_lds_order();
+    if (mine) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) rv[t] = tile[unit_slot(lane, t)];
+    }
+
+    // residual_norm_wave_kernel's arithmetic, unit by unit.
+    const float sc = scalar != nullptr ? bf16_bits_to_f32(*scalar) : 1.0f;
+    float ss = mine ? unit_sumsq(xv) : 0.0f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (mine) {
+        normalize_unit(xv, rms_inverse(ss, hidden, eps));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) wv[t] = wt[0][unit_slot(lane, t)];
+        weight_unit(xv, wv);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
+            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
+                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
+                if (scalar != nullptr) {
+                    lo = round_bf16(lo * sc);
+                    hi = round_bf16(hi * sc);
+                }
+                hw[q] = cvt_pk_bf16(lo, hi);
+            }
+            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        }
+    }
+
+    // The new residual out through the tile (after every lane's reads of the row).
+    wave_lds_order();
+    if (mine) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) tile[unit_slot(lane, t)] = xv[t];
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t c = lane + 64u * t;
+        if (c < chunks) r4[c] = tile[unit_slot(c >> 3, c & 7u)];
+    }
+    if (w_next == nullptr) return;   // uniform over the launch
+
+    float ss2 = mine ? unit_sumsq(xv) : 0.0f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss2 += __shfl_xor(ss2, off, 64);
+    if (mine) {
+        normalize_unit(xv, rms_inverse(ss2, hidden, eps));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) wv[t] = wt[1][unit_slot(lane, t)];
+        weight_unit(xv, wv);
+    }
+    wave_lds_order();
+    if (mine) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) tile[unit_slot(lane, t)] = xv[t];
+    }
+    wave_lds_order();
+    uint4* n4 = reinterpret_cast<uint4*>(next + base);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t c = lane + 64u * t;
+        if (c < chunks) n4[c] = tile[unit_slot(c >> 3, c & 7u)];
+    }
+}
+
 __global__ void decode_advance_kernel(uint32_t* pos, uint32_t* ties, const HypTopKSample* sample) {
     if (threadIdx.x == 0u) {
         pos[0] += 1u;
@@ -539,7 +692,11 @@ void launch_residual_norm(const uint16_t* branch, uint16_t* residual, const uint
     if (m == 0) return;
     HYP_REQUIRE(hidden % 64u == 0u && hidden <= residual_norm_max_hidden(), HYP_STATUS_UNSUPPORTED,
                 "residual norm: hidden must be a multiple of 64, at most 16384");
-    if (hidden <= 64u * 64u) {
+    if (hidden <= 64u * 64u && m >= kResidualTiledMinRows) {
+        hipLaunchKernelGGL(residual_norm_tiled_kernel, dim3((m + kTiledRows - 1u) / kTiledRows),
+                           dim3(64u * kTiledRows), 0, stream, branch, residual, w_post, scalar, w_next, next, m,
+                           hidden, eps);
+    } else if (hidden <= 64u * 64u) {
         hipLaunchKernelGGL(residual_norm_wave_kernel, dim3(m), dim3(64), 0, stream, branch, residual, w_post, scalar,
                            w_next, next, hidden, eps);
     } else {

@@ -385,7 +385,10 @@ def test_attention_prepare_bit_exact(stream, L, H, KVH, D, rotated, base, offset
 
 @pytest.mark.parametrize("m,hidden,scalar,nxt", [(1, 3840, False, True), (4, 3840, True, False),
                                                   (300, 3840, True, True), (7, 128, True, True),
-                                                  (2, 16384, False, False)])
+                                                  (2, 16384, False, False),
+                                                  # from 64 rows on: the coalesced tiled form
+                                                  (1024, 3840, False, True), (65, 128, True, False),
+                                                  (130, 4096, True, True)])
 def test_residual_rms_norm_bit_exact(stream, m, hidden, scalar, nxt):
     """hyp_residual_rms_norm == hyp_rms_normalize(branch, w_post), the bf16 add (and layer
     scalar product) of the oracle, then hyp_rms_normalize(residual, w_next)."""
