@@ -133,7 +133,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
     const uint32_t hk = blockIdx.y;
     const uint32_t split = blockIdx.z;
     const uint32_t rows = p.L * p.G;                     // query rows of this kv head
-    const uint32_t row0 = blockIdx.x * kRowsPerTile;     // first row of the tile
+    // Workgroups are dispatched x first, then z: the second key split takes the tiles in
+    // reverse, so its longest causal halves start first, on the compute units the first
+    // split's short tiles free early.
+    const uint32_t tile = (split & 1u) != 0u ? gridDim.x - 1u - blockIdx.x : blockIdx.x;
+    const uint32_t row0 = tile * kRowsPerTile;           // first row of the tile
     const uint32_t T = p.prefix + p.L;
 
     // The tile's token range and the keys any of its rows can see, within this split.
@@ -896,7 +900,7 @@ size_t attention_chunk_workspace_bytes(uint32_t max_L, uint32_t n_heads, uint32_
     const uint32_t G = n_heads / n_kv_heads;
     const uint64_t fit = static_cast<uint64_t>(kRowsPerTile) * (kPlanComputeUnits / n_kv_heads) / G;
     const uint32_t L = static_cast<uint32_t>(std::min<uint64_t>(max_L, fit));
-    return head_dim <= 256u && L > kRowsPerTile / G ? chunk_split_bytes(L, n_heads, head_dim) : 0u;
+    return L > kRowsPerTile / G ? chunk_split_bytes(L, n_heads, head_dim) : 0u;
 }
 
 size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim) {
@@ -968,11 +972,9 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
     } else {
         p.splits = attention_splits(a.L, a.n_heads, a.n_kv_heads, T);
         const bool chunk = static_cast<uint64_t>(a.L) * p.G > kRowsPerTile;
-        // The chunk form splits only at head_dim <= 256 (at 512 the split measured 199 against
-        // 204 us per 1024-token layer before its merge) and into a workspace that holds it.
+        // The chunk form splits into a workspace that holds it.
         if (chunk && p.splits > 1u &&
-            (a.head_dim > 256u || a.workspace == nullptr ||
-             a.workspace_bytes < chunk_split_bytes(a.L, a.n_heads, a.head_dim)))
+            (a.workspace == nullptr || a.workspace_bytes < chunk_split_bytes(a.L, a.n_heads, a.head_dim)))
             p.splits = 1u;
         p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
         p.splits = std::max(1u, (T + p.keys_per_split - 1u) / p.keys_per_split);   // no empty split
@@ -1026,7 +1028,8 @@ void launch_attention(const AttnArgs& a, hipStream_t stream) {
         switch (a.head_dim) {
             case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
             case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
-            default: hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
+            case 256: hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
+            default: hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(blocks), dim3(kAttnThreads), 0, stream, p); break;
         }
         HYP_HIP_CHECK(hipGetLastError());
     } else if (p.splits > 1u) {

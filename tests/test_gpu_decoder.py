@@ -243,6 +243,23 @@ def test_12b_shaped_layers(tmp_path):
     model.close()
 
 
+def test_12b_global_layer_split_chunk(tmp_path):
+    """One 12B-shaped global layer (16 heads of 512, one KV head) over a 300-token prompt:
+    the chunk attention splits its keys in two (75 tiles, 300 keys) and merges them."""
+    cfg = syn.gemma4_text_config(num_layers=1, vocab=1024, max_positions=2048, layer_types=["full_attention"])
+    T = syn.write_model(str(tmp_path), cfg, seed=14, branch_gain=BRANCH_GAIN, qk_gain=QK_GAIN)
+    model = hy.Model(hy.geometry_from_config(cfg), str(tmp_path))
+    prompt = np.random.default_rng(8).integers(0, cfg["vocab_size"], size=300).astype(np.uint32)
+    say("12B global layer: forward_hidden over 300 tokens (split chunk attention)")
+    st = model.kvstate()
+    got = st.forward_hidden(prompt, 0)
+    st.close()
+    per_m = O.DecoderOracle(T, cfg, weights="per_m").forward(prompt, 0)
+    for lo, hi in ((0, 8), (140, 160), (290, 300)):
+        check_hidden(got[lo:hi], per_m[lo:hi], f"rows {lo}..{hi}", rtol_atol=None)
+    model.close()
+
+
 @pytest.mark.parametrize("dims,kind", [("tiny", "full_attention"), ("tiny", "sliding_attention"),
                                        ("12b", "full_attention"), ("12b", "sliding_attention")])
 def test_single_layer_per_element(tmp_path, dims, kind):
