@@ -79,10 +79,13 @@ def time_launches(stream, fn, steps, warmup):
     """Mean milliseconds per call of fn(i), from HIP events recorded on `stream`. The
     index keeps counting from the warm-up into the timed loop (warm-up calls are
     fn(0..warmup-1), timed calls fn(warmup..warmup+steps-1)), so a rotation over
-    buffers indexed by i % copies never restarts at the buffers the warm-up just read."""
+    buffers indexed by i % copies never restarts at the buffers the warm-up just read.
+    The start event is recorded behind the warm-up calls while they are still queued, so
+    the timed region opens on a busy stream (steady state, as in a decode loop) and not on
+    an idle GPU, whose first launch would carry the queue's start-up."""
+    stream.synchronize()
     for i in range(warmup):
         fn(i)
-    stream.synchronize()
     e0, e1 = hy.Event(), hy.Event()
     e0.record(stream)
     for i in range(warmup, warmup + steps):
@@ -123,8 +126,8 @@ def bench_decode_gemv(stream, steps, warmup, copies):
     nbytes = gemv_bytes(1, n, k)
     log(f"decode cold {cold * 1e3:.2f} us/launch = {nbytes / cold / 1e6:.0f} GB/s; "
         f"warm {warm * 1e3:.2f} us = {nbytes / warm / 1e6:.0f} GB/s")
-    for q in qws:
-        q.close()
+    for a in (*qws, xd, yd):
+        a.close()
     return {"ms_per_launch": cold, "warm_ms_per_launch": warm, "bytes": nbytes, "copies": copies}
 
 
@@ -516,6 +519,10 @@ def main():
         model.close()
         extra["decode_stream"] = streams
         extra["model_decode"] = bench_model_decode(args.prompt, 32, args.layers)
+    # Every HIP object this process made is released here, before the interpreter exits:
+    # nothing is left for finalizers or exit handlers to destroy.
+    stream.synchronize()
+    stream.close()
     cpu, cpu_par = (None, None) if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     per = dec["ms_per_launch"]

@@ -19,6 +19,8 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhyperion_hip.so")
+# The same library with a host-side fault hook (hyp_test_fault_after_first_replay), for tests.
+FAULTS_LIB_PATH = os.path.join(_HERE, "libhyperion_hip_faults.so")
 
 HYP_STATUS = {
     0: "OK",
@@ -227,11 +229,17 @@ _SZ = ctypes.c_size_t
 def lib() -> ctypes.CDLL:
     """Load libhyperion_hip.so (raises if it has not been built)."""
     global _lib
-    if _lib is not None:
-        return _lib
-    if not os.path.exists(LIB_PATH):
-        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
-    L = ctypes.CDLL(LIB_PATH)
+    if _lib is None:
+        _lib = load_library(LIB_PATH)
+    return _lib
+
+
+def load_library(path: str) -> ctypes.CDLL:
+    """A ctypes handle of one build of the library (the product, or the test build
+    FAULTS_LIB_PATH) with the signature of every ABI function set."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build()")
+    L = ctypes.CDLL(path)
     sig = {
         "hyp_last_error": [ctypes.c_char_p, _SZ],
         "hyp_runtime_info": [ctypes.POINTER(RuntimeInfo)],
@@ -307,7 +315,6 @@ def lib() -> ctypes.CDLL:
         fn = getattr(L, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
-    _lib = L
     return L
 
 

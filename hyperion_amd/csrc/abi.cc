@@ -994,6 +994,9 @@ hyperion::model::Decoder& loaded(HypModel model) {
 hyperion::model::DecoderState& state_of(HypModel model, HypKvState kv) {
     REQUIRE_ARG(kv != nullptr && kv->magic == kKvStateMagic, "kvstate handle is invalid");
     REQUIRE_ARG(kv->model == model, "kvstate was created for another model");
+    // validate_kvstate (model.cc:149-160): a state consumed by a failed decode is refused.
+    HYP_REQUIRE(!kv->state.consumed, HYP_STATUS_INTERNAL,
+                "KV state is unusable after an internal execution failure; free and recreate it");
     return kv->state;
 }
 

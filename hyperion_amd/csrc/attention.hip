@@ -923,8 +923,12 @@ void launch_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* ck, uint16_
 }
 
 bool attention_prep_fits(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim) {
-    // The G query rows, K and V of one kv head as 64-value units, one per lane of a wave.
-    return n_kv_heads > 0u && n_heads % n_kv_heads == 0u && (n_heads / n_kv_heads + 2u) * (head_dim / 64u) <= 64u;
+    // Only the decode form folds the prepare, and one token takes it when its G query rows fit
+    // the single row tile (G <= 16); the G query rows, K and V of one kv head must also fit
+    // one wave as 64-value units, one per lane.
+    if (n_kv_heads == 0u || n_heads % n_kv_heads != 0u) return false;
+    const uint32_t G = n_heads / n_kv_heads;
+    return G <= 16u && (G + 2u) * (head_dim / 64u) <= 64u;
 }
 
 // The decode form's splits: one wave per block of 32 keys (each wave then makes a single

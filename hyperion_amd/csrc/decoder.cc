@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <stdexcept>
 #include <string>
 #include <utility>
 
@@ -572,6 +573,42 @@ StepSample Decoder::prefill(DecoderState& st, const uint32_t* ids, uint32_t coun
     return out;
 }
 
+namespace {
+
+// Marks a DecoderState consumed unless disarmed: armed once a decode's first replay is
+// enqueued (the replays advance the live KV rows, cursor and token in place), disarmed when
+// the block has completed and `offset` agrees with the device (DirectKvExecutionGuard,
+// model.cc:79-105). On the failure path it also waits for the stream, so that no replay still
+// reads the state's buffers when the caller frees it.
+class ConsumeOnFailure {
+  public:
+    ConsumeOnFailure(DecoderState& st, hipStream_t stream) noexcept : st_(st), stream_(stream) {}
+    ConsumeOnFailure(const ConsumeOnFailure&) = delete;
+    ConsumeOnFailure& operator=(const ConsumeOnFailure&) = delete;
+    ~ConsumeOnFailure() {
+        if (armed_) {
+            st_.consumed = true;
+            (void)hipStreamSynchronize(stream_);
+        }
+    }
+    void arm() noexcept { armed_ = true; }
+    void disarm() noexcept { armed_ = false; }
+
+  private:
+    DecoderState& st_;
+    hipStream_t stream_;
+    bool armed_ = false;
+};
+
+#ifdef HYP_TEST_FAULTS
+// Test builds only (libhyperion_hip_faults.so): a one-shot host-side throw right after a
+// decode's first replay is enqueued, as the reference's test build injects a failure into its
+// forward (test_fault.cc, forward.cc:564-566). No GPU work is affected.
+thread_local bool g_fault_after_first_replay = false;
+#endif
+
+}  // namespace
+
 StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
     const Geometry& g = geo_;
     if (st.offset == 0) invalid("decode requires a populated KV state (prefill first)");
@@ -586,7 +623,17 @@ StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
     const uint32_t start[2] = {st.offset, 0u};
     auto* counters = static_cast<uint32_t*>(st.counters.data());
     HYP_HIP_CHECK(hipMemcpyAsync(counters, start, sizeof(start), hipMemcpyHostToDevice, stream_));
-    for (uint32_t j = 0; j < n_tokens; ++j) HYP_HIP_CHECK(hipGraphLaunch(st.step.get(), stream_));
+    ConsumeOnFailure guard(st, stream_);
+    guard.arm();
+    for (uint32_t j = 0; j < n_tokens; ++j) {
+        HYP_HIP_CHECK(hipGraphLaunch(st.step.get(), stream_));
+#ifdef HYP_TEST_FAULTS
+        if (g_fault_after_first_replay) {
+            g_fault_after_first_replay = false;
+            throw std::runtime_error("injected failure after the first decode replay");
+        }
+#endif
+    }
     uint32_t end[2] = {0u, 0u};
     HYP_HIP_CHECK(hipMemcpyAsync(&out.sample, st.cur.data(), sizeof(HypTopKSample), hipMemcpyDeviceToHost, stream_));
     HYP_HIP_CHECK(hipMemcpyAsync(end, counters, sizeof(end), hipMemcpyDeviceToHost, stream_));
@@ -595,7 +642,14 @@ StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
     out.near_tie_events = end[1];
     st.offset += n_tokens;
     st.last_token = out.sample.token_id;
+    guard.disarm();
     return out;
 }
 
 }  // namespace hyperion::model
+
+#ifdef HYP_TEST_FAULTS
+extern "C" void hyp_test_fault_after_first_replay(void) {
+    hyperion::model::g_fault_after_first_replay = true;
+}
+#endif

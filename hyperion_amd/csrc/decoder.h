@@ -120,6 +120,10 @@ struct DecoderState {
     GraphExec step;                   // one decode step, captured at the first decode
     uint64_t local_bytes = 0;
     uint64_t global_bytes = 0;
+    // Set when a decode failed after its first replay was enqueued: the KV rows, the device
+    // cursor and the sampled token may have moved past `offset`, so the state is consumed and
+    // every later step on it is refused until it is freed (model.cc:79-105, :155).
+    bool consumed = false;
 };
 
 // One sampled step as the ABI reports it.

@@ -150,8 +150,9 @@ size_t attention_workspace_bytes(uint32_t n_kv_heads, uint32_t head_dim);
 // tokens (0 when no such chunk splits); with less it runs those chunks unsplit.
 size_t attention_chunk_workspace_bytes(uint32_t max_L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 uint32_t attention_splits(uint32_t L, uint32_t n_heads, uint32_t n_kv_heads, uint32_t keys);
-// Whether AttnArgs::prep can fold the prepare for this geometry (the G query rows and the
-// new K and V of one kv head fit one wave as 64-value units: (G + 2) * head_dim / 64 <= 64).
+// Whether AttnArgs::prep can fold the prepare for this geometry: one token runs the decode
+// form (G <= 16 query rows per kv head) and the G query rows and the new K and V of one kv
+// head fit one wave as 64-value units ((G + 2) * head_dim / 64 <= 64).
 bool attention_prep_fits(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 void launch_attention(const AttnArgs& a, hipStream_t stream);
 // Tokens pos0.. of k/v [n][n_kv_heads][head_dim] into cache slots (pos % cap).

@@ -247,7 +247,9 @@ HypStatus hyp_quantize_q4g64(const void* w, uint32_t n, uint32_t k, uint32_t* w_
 
 /* mx.dequantize(..., dtype=bfloat16) of rows rows[0..n_rows) (rows == NULL: rows
  * 0..n_rows) of a Q4 matrix of k columns into out bf16 [n_rows, k]; each value is
- * bf16(bf16(scale*q) + bias). If out_scale != 0 the result is further multiplied
+ * bf16(scale*q + bias), one rounding as MLX's dequantize (weights_loader.cc:60-69; the
+ * reference's 12B embed golden, forward_12b_test.cc:218, fits only this rounding).
+ * If out_scale != 0 the result is further multiplied
  * by bf16(out_scale) and rounded (the embed scale, forward.cc:126-131). Row ids
  * are device uint32; the kernel never reads outside the table: an id >= n_total
  * yields a row of zeros (mx::take would raise; ids are not visible to the host

@@ -87,7 +87,9 @@ def quantize(w_bf16: np.ndarray):
     return wq, s, b
 
 
-def dequantize(wq, s, b, rows=None, mode: int = 0) -> np.ndarray:
+def dequantize(wq, s, b, rows=None, mode: int = 1) -> np.ndarray:
+    """mx.dequantize to bf16 bits; mode 1 (default) is MLX's single rounding bf16(s*q + b),
+    mode 0 the op-composed bf16(bf16(s*q) + b) kept for comparison."""
     wq = _c(wq, np.uint32)
     s = _c(s, np.uint16)
     b = _c(b, np.uint16)
@@ -338,7 +340,7 @@ class DecoderOracle:
     def embed(self, ids):
         base = "embed_tokens"
         rows = dequantize(self._t(base + ".weight"), self._t(base + ".scales"), self._t(base + ".biases"),
-                          rows=np.asarray(ids, np.uint32), mode=0)
+                          rows=np.asarray(ids, np.uint32))
         return scale(rows, float(np.sqrt(np.float32(self.hidden))))
 
     def layer(self, x, i, offset):

@@ -29,13 +29,14 @@
  *                           fixture's (q, scale, bias) bit-exactly on every group that
  *                           holds q=15; sign/zero-point invariants on all groups;
  *                           closed-form cases (exact grids, constant and zero groups).
- *   orc_dequantize_q4g64    pinned where the value is exact (power-of-two scales, bias
- *                           grids) and by the fixture round trip; mode 1 (one rounding)
- *                           is the correctly rounded value, checked exactly on the decode
- *                           workload's weights. The choice between single (mode 1) and
- *                           double (mode 0) bf16 rounding is parity unpinned (no
- *                           committed dequantized values exist in the reference); the two
- *                           differ on 38% of those weights.
+ *   orc_dequantize_q4g64    pinned: mode 1 (one rounding, bf16(s*q + b)) is MLX's - the
+ *                           reference's 12B embed golden (12b_hidden_golden.safetensors
+ *                           'embed', forward_12b_test.cc:218) fits it in all 600 groups and
+ *                           the op-composed mode 0 alone in none; mode 1 reproduces that
+ *                           golden bit for bit from the Q4 rows recovered from it
+ *                           (tests/test_golden_embed.py). Also exact values (power-of-two
+ *                           scales, bias grids) and the fixture round trip. Mode 0 is kept
+ *                           only to show the difference (38% of the decode weights).
  *   orc_qmatmul_f64         pinned: closed-form known-answer cases and brute force.
  *   orc_qmatmul_deq_f64     pinned: equals orc_qmatmul_f64 wherever the dequantized
  *                           weights are exact in bf16, and brute force over
@@ -102,8 +103,8 @@ void orc_quantize_q4g64(const uint16_t* w, int64_t n, int64_t k,
                         uint32_t* wq, uint16_t* scales, uint16_t* biases);
 
 /* mx.dequantize(..., dtype=bfloat16) of rows `rows[0..n_rows)` (rows==NULL: 0..n_rows).
- * mode 0: bf16(bf16(s*q) + b)  (op-composed, one rounding per MLX op)
- * mode 1: bf16(s*q + b)        (fp32 math, single rounding to bf16) */
+ * mode 1: bf16(s*q + b)        (fp32 math, single rounding to bf16: MLX's dequantize)
+ * mode 0: bf16(bf16(s*q) + b)  (op-composed, one rounding per op; not MLX's) */
 void orc_dequantize_q4g64(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
                           const uint32_t* rows, int64_t n_rows, int64_t k, int mode,
                           uint16_t* out);

@@ -103,7 +103,7 @@ def test_quantize_reproduces_reference_fixture(stream, fixture_dir):
     (codes, scale, bias) on every group holding code 15, and equals the oracle on all."""
     total = exact = 0
     for name, (w, s, b) in st_reader.q4_tensors(fixture_dir).items():
-        wd = O.dequantize(w, s, b, mode=0)
+        wd = O.dequantize(w, s, b)
         gw, gs, gb = _gpu_quantize(wd, stream)
         ow, os_, ob = O.quantize(wd)
         assert np.array_equal(gw, ow) and np.array_equal(gs, os_) and np.array_equal(gb, ob), name
@@ -176,7 +176,7 @@ def test_dequantize_table_bit_exact(stream):
     out = hy.DeviceArray((n, k), np.uint16)
     hy.dequantize(wd, sd, bd, n, k, None, n, out, stream)
     got = out.to_host(stream)
-    ref = O.dequantize(w, s, b, mode=0)
+    ref = O.dequantize(w, s, b)
     assert np.count_nonzero(got != ref) == 0
 
 
@@ -190,9 +190,30 @@ def test_dequantize_gather_scale_and_out_of_range(stream):
     hy.dequantize(wd, sd, bd, n, k, idd, ids.size, out, stream, out_scale=float(np.sqrt(k)))
     got = out.to_host(stream)
     valid = ids < n
-    ref = O.scale(O.dequantize(w, s, b, rows=ids[valid], mode=0), float(np.sqrt(np.float32(k))))
+    ref = O.scale(O.dequantize(w, s, b, rows=ids[valid]), float(np.sqrt(np.float32(k))))
     np.testing.assert_array_equal(got[valid], ref)
     assert np.all(got[~valid] == 0)
+
+
+def test_embed_reproduces_the_reference_12b_golden(stream):
+    """hyp_embed and hyp_dequantize_q4g64 return the bits of the reference's own 12B embed
+    golden (forward_12b_test.cc:218) from the Q4 rows recovered from it (tests/embed_fit.py):
+    MLX's single-rounded dequantize times bf16(sqrt(3840)), bit for bit."""
+    import embed_fit
+    _, e = embed_fit.load()
+    w, s, b = embed_fit.fitted_rows(e)
+    n, k = w.shape[0], w.shape[1] * 8
+    ids = np.array([3, 0, 9, 1, 2, 4, 5, 6, 7, 8], np.uint32)
+    say(f"12B embed golden: {n} rows k={k}")
+    qw = hy.QWeight.from_host(w, s, b)
+    out = hy.DeviceArray((ids.size, k), np.uint16)
+    hy.embed(qw, dev(ids, stream), ids.size, out, stream)
+    np.testing.assert_array_equal(out.to_host(stream), e[ids])
+    qw.close()
+    wd, sd, bd = dev(w, stream), dev(s, stream), dev(b, stream)
+    out2 = hy.DeviceArray((n, k), np.uint16)
+    hy.dequantize(wd, sd, bd, n, k, None, n, out2, stream, out_scale=float(np.sqrt(np.float32(k))))
+    np.testing.assert_array_equal(out2.to_host(stream), e)
 
 
 # ---------------------------------------------------------------- decode GEMV
@@ -745,7 +766,7 @@ def test_qmodel_fixture_reference_weights_test(stream, fixture_dir):
     out = hy.DeviceArray((ids.size, 128), np.uint16)
     hy.embed(emb, dev(ids, stream), ids.size, out, stream)
     w, s, b = tensors["language_model.model.embed_tokens"]
-    ref = O.scale(O.dequantize(w, s, b, rows=ids, mode=0), float(np.sqrt(np.float32(128))))
+    ref = O.scale(O.dequantize(w, s, b, rows=ids), float(np.sqrt(np.float32(128))))
     np.testing.assert_array_equal(out.to_host(stream), ref)
     with pytest.raises(hy.HypError):
         hy.call("hyp_qweight_free", __import__("ctypes").byref(emb.handle))
@@ -785,7 +806,7 @@ def test_odd_group_counts_through_every_path(stream, k):
     ids = np.array([0, 39, 17, 16, 15], np.uint32)
     out = hy.DeviceArray((ids.size, k), np.uint16)
     hy.embed(qw, dev(ids, stream), ids.size, out, stream)
-    ref = O.scale(O.dequantize(w, s, b, rows=ids, mode=0), float(np.sqrt(np.float32(k))))
+    ref = O.scale(O.dequantize(w, s, b, rows=ids), float(np.sqrt(np.float32(k))))
     np.testing.assert_array_equal(out.to_host(stream), ref)
     qw.close()
 

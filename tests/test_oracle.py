@@ -233,7 +233,9 @@ def test_qmatmul_one_hot_pins_nibble_order():
         expect = sf[:, j // 64].astype(np.float64) * codes[:, j] + bf[:, j // 64]
         np.testing.assert_array_equal(O.qmatmul_f64(xb, w, s, b)[0], expect)
         np.testing.assert_array_equal(O.qmatmul_f32_grouped(xb, w, s, b)[0], expect.astype(np.float32))
-        deq = O.dequantize(w, s, b)[:, j]
+        # the CPU-loop restatement rounds after every bf16 op, so its one-hot row is the
+        # op-composed dequantize (mode 0), not the single-rounded one of MLX's dequantize
+        deq = O.dequantize(w, s, b, mode=0)[:, j]
         np.testing.assert_array_equal(O.qmatmul_mlx_cpu(xb, w, s, b)[0], deq)
 
 
@@ -674,7 +676,8 @@ def test_dequantize_modes_mismatch_rate_on_the_decode_weights():
     weights [15360, 3840] (bias = -8 * scale). There s*q + b is exact in fp32 (at most 12
     significant bits), so (B) is the correctly rounded value: checked exactly on a sample.
     (A) rounds s*q to 8 bits before the subtraction and differs on a large fraction of
-    values (printed; which one MLX uses is parity unpinned)."""
+    values (printed). MLX's is (B): tests/test_golden_embed.py decides it on the reference's
+    12B embed golden."""
     w, s, b = syn.q4_weights(15360, 3840, seed=105)
     a = O.dequantize(w, s, b, mode=0)
     bb = O.dequantize(w, s, b, mode=1)
@@ -866,13 +869,14 @@ def test_decoder_oracle_residual_wiring_closed_form(tmp_path):
         _zero_proj(T, f"{P}layers.{i}.mlp.down_proj")
     ids = [3, 17, 60, 0, 41]
     got = O.DecoderOracle(T, cfg).forward(ids, 0)
-    # closed form, numpy only: dequantized rows (double rounding, as the embed oracle),
-    # times bf16(sqrt(128)), times each bf16 scalar, then the weighted RMS norm in fp64.
+    # closed form, numpy only: dequantized rows (one rounding of s*q + b, as MLX's
+    # dequantize), times bf16(sqrt(128)), times each bf16 scalar, then the weighted RMS norm
+    # in fp64.
     e = P + "embed_tokens"
     codes = syn.unpack_codes(T[e + ".weight"][ids]).astype(np.float32)
     s = np.repeat(syn.bf16_to_f32(T[e + ".scales"][ids]), 64, axis=1)
     b = np.repeat(syn.bf16_to_f32(T[e + ".biases"][ids]), 64, axis=1)
-    x = syn.bf16_to_f32(syn.bf16_bits(syn.bf16_to_f32(syn.bf16_bits(s * codes)) + b))
+    x = syn.bf16_to_f32(syn.bf16_bits(s * codes + b))
     x = syn.bf16_to_f32(syn.bf16_bits(x * syn.bf16_to_f32(syn.bf16_bits(np.float32(np.sqrt(np.float32(128)))))))
     for i in range(cfg["num_hidden_layers"]):
         x = syn.bf16_to_f32(syn.bf16_bits(x * syn.bf16_to_f32(T[f"{P}layers.{i}.layer_scalar"])[0]))
