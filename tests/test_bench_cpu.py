@@ -37,8 +37,17 @@ def test_algorithmic_work_matches_the_workload_definitions():
 
 
 def test_roofline_traffic_comes_from_the_committed_counter_summary():
+    """roofline.traffic is the committed record's scaled FETCH_SIZE + WRITE_SIZE, which lies
+    within 5% above the algorithmic bytes (every weight byte read once)."""
+    import json
+    import re
     b = _bench()
-    assert b.measured_traffic() == 33_428_523
+    text = open(os.path.join(ROOT, "profiles", "decode_gemv_traffic.md")).read()
+    rec = json.loads(re.search(r"```json\s*(\{.*?\})\s*```", text, flags=re.S).group(1))
+    assert b.measured_traffic() == rec["hbm_bytes_per_launch"]
+    assert rec["hbm_bytes_per_launch"] == rec["hbm_read_bytes_per_launch"] + rec["hbm_write_bytes_per_launch"]
+    assert rec["algorithmic_bytes_per_launch"] == b.gemv_bytes(1, 15360, 3840)
+    assert 1.0 <= rec["hbm_bytes_per_launch"] / rec["algorithmic_bytes_per_launch"] <= 1.05
 
 
 def test_entry_points_exist():
