@@ -485,13 +485,19 @@ HypStatus hyp_model_load(HypModel model, const HypGeometryParams* geometry, cons
 /* One LocalKvCache ring of sliding_window + 2048 positions per sliding layer and one
  * GlobalKvCache of max_position_embeddings positions per global layer (kv.cc). */
 HypStatus hyp_kvstate_create(HypModel model, HypKvState* out_kvstate);
+/* Frees the state; valid after a step returned HYP_STATUS_INTERNAL (hyperion_mlx.h:192-194). */
 HypStatus hyp_kvstate_free(HypKvState* kvstate);
 /* Prefill a fresh state with tokens->count tokens in 2048-token chunks; the result holds
- * the greedy token after the last one (top_k_logprob_count 0). */
+ * the greedy token after the last one (top_k_logprob_count 0). A state consumed by a failed
+ * decode returns HYP_STATUS_INTERNAL until it is freed (hyperion_mlx.h:196-198). A failed
+ * prefill leaves the state reusable: the next prefill rewrites every position it reads. */
 HypStatus hyp_prefill_chunk(HypModel model, HypKvState kvstate, const HypTokenStream* tokens,
                             HypStepResult out_result);
 /* n_tokens greedy steps from the state's last token; the result holds the last step's
- * token and the number of steps whose top-2 gap was < 0.5. */
+ * token and the number of steps whose top-2 gap was < 0.5. A decode that fails after its
+ * first step is enqueued consumes the state: it and every later prefill or decode on that
+ * state return HYP_STATUS_INTERNAL until it is freed and recreated (hyperion_mlx.h:204-208,
+ * DirectKvExecutionGuard model.cc:79-105). */
 HypStatus hyp_decode_block(HypModel model, HypKvState kvstate, uint32_t n_tokens, HypStepResult out_result);
 /* The same with a sampling config: NULL or temperature 0 is the greedy path plus the
  * top-k sidecar (near_tie_events 0, as model.cc:262-288 reports it); temperature > 0 is
