@@ -1,6 +1,6 @@
 """Which bf16 rounding MLX's dequantize uses, recovered from the reference's 12B embed golden.
 
-The golden (`tests/golden/gemma4-12b-embed/embed.safetensors`, copied from the reference's
+The golden (`tests/golden/gemma4-12b-hidden/golden.safetensors`, copied from the reference's
 `native/hyperion_mlx/tests/fixtures/12b_hidden_golden.safetensors`) holds MLX's
 `ForwardPass::embed` of ten prompt tokens on the real 12B (forward.cc:126-131,
 weights_loader.cc:52-69): e = bf16(d * 62) for every element, where d is the bf16 output of
@@ -27,8 +27,8 @@ import numpy as np
 
 import st_reader
 
-GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gemma4-12b-embed",
-                      "embed.safetensors")
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gemma4-12b-hidden",
+                      "golden.safetensors")
 HIDDEN = 3840
 EMBED_SCALE = np.float32(62.0)   # bf16(sqrt(3840)): 61.97 rounds to 62 with 8 significant bits
 

@@ -148,3 +148,51 @@ def test_q_k_v_prep_of_a_global_layer(stream):
     np.testing.assert_array_equal(vo.to_host(stream), O.rms_norm(kh, None, 1e-6))
     for a in (qw, kw, x, q, kr, qn, kn, qo, ko, vo):
         a.close()
+
+
+# ---- MLX's own 12B keys and values (the reference's hidden golden) ------------------------
+
+@pytest.mark.parametrize("layer", [0, 5])
+def test_norms_and_rope_reproduce_the_reference_12b_keys(stream, layer):
+    """The reference's 12B golden keys (k_norm then RoPE at positions 0..9) and, on the global
+    layer, values (v_norm of k_proj), from the golden k_proj output (forward.cc:395-418,
+    forward_12b_test.cc:193-211), with the k_norm weight recovered as the CPU tests do
+    (tests/test_golden_norm_rope.py): hyp_rms_normalize + hyp_rope, and the decoder's own
+    hyp_attention_prepare into a cache, equal the oracle bit for bit, so they reproduce MLX's
+    keys wherever the oracle does (all 5,120 of the global layer, 20,479 of 20,480 on the
+    sliding one) and its values exactly."""
+    import ctypes
+
+    import norm_rope_fit as F
+    from test_golden_norm_rope import resolved_weight
+    g = F.load()
+    D, heads, rot, theta = F.LAYERS[layer]
+    kp = g[f"kproj{layer}"]
+    L = kp.shape[0]
+    w, _ = resolved_weight(g, layer)
+    say(f"12B golden keys: layer {layer}, D={D}, kv heads={heads}")
+    ref = O.rope(O.rms_norm(kp.reshape(-1, D), w, 1e-6), L, heads, D, rot, theta, 0)
+    xd, wd = dev(kp, stream), dev(w, stream)
+    yd = hy.DeviceArray((L, heads, D), np.uint16)
+    hy.rms_normalize(xd, L * heads, D, yd, stream, eps=1e-6, weight=wd)
+    hy.rope(yd, L, heads, D, rot, theta, 0, yd, stream)
+    got = yd.to_host(stream)
+    np.testing.assert_array_equal(got, ref)
+    assert int((got != g[f"k{layer}"]).sum()) <= (1 if layer == 0 else 0)
+    # the decoder's fused prepare: q <- rope(q_norm(q)) and the cache slots <- K, V
+    cache = hy.KvCache(64, heads, D)
+    qd = dev(kp, stream)
+    hy.attention_prepare(qd, xd, None, L, heads, cache, wd, wd, 1e-6, rot, theta, 0, stream)
+    np.testing.assert_array_equal(qd.to_host(stream).reshape(L, heads, D), ref)
+    kbuf, vbuf = cache.buffers()
+    ck = np.zeros((64, heads, D), np.uint16)
+    cv = np.zeros((64, heads, D), np.uint16)
+    hy.call("hyp_memcpy_dtoh", ck.ctypes.data_as(ctypes.c_void_p), kbuf, ck.nbytes, stream.handle)
+    hy.call("hyp_memcpy_dtoh", cv.ctypes.data_as(ctypes.c_void_p), vbuf, cv.nbytes, stream.handle)
+    stream.synchronize()
+    np.testing.assert_array_equal(ck[:L], ref)
+    vn = O.rms_norm(kp.reshape(-1, D), None, 1e-6).reshape(L, heads, D)
+    np.testing.assert_array_equal(cv[:L], vn)
+    if layer == 5:
+        np.testing.assert_array_equal(cv[:L, 0], g["v5"])
+    cache.close()
