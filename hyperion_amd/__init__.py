@@ -49,7 +49,7 @@ EXPORTED = [
     "hyp_qmatmul", "hyp_qmatmul_noalloc", "hyp_qmatmul_ex", "hyp_qmatmul_group", "hyp_qmatmul_group_rmsnorm",
     "hyp_qmlp_gate_up_gelu",
     "hyp_quantize_q4g64", "hyp_dequantize_q4g64", "hyp_embed", "hyp_rms_normalize",
-    "hyp_rope", "hyp_sample_greedy", "hyp_sample_greedy_topk",
+    "hyp_rope", "hyp_sample_greedy", "hyp_sample_greedy_topk", "hyp_sample_stochastic",
     "hyp_kv_cache_create", "hyp_kv_cache_free", "hyp_kv_cache_buffers", "hyp_kv_cache_write", "hyp_attention",
     "hyp_attention_prepare", "hyp_residual_rms_norm",
     "hyp_model_create", "hyp_model_free", "hyp_model_load", "hyp_kvstate_create", "hyp_kvstate_free",
@@ -278,6 +278,7 @@ def load_library(path: str) -> ctypes.CDLL:
         "hyp_rope": [_P, _U32, _U32, _U32, _U32, ctypes.c_float, _U32, _P, _P],
         "hyp_sample_greedy": [_P, _U32, _U32, _P, _P],
         "hyp_sample_greedy_topk": [_P, _U32, _U32, _P, _P],
+        "hyp_sample_stochastic": [_P, _U32, ctypes.POINTER(SamplingConfig), ctypes.c_uint64, _P, _P],
         "hyp_kv_cache_create": [_U32, _U32, _U32, _PP],
         "hyp_kv_cache_free": [_PP],
         "hyp_kv_cache_buffers": [_P, _PP, _PP],
@@ -888,6 +889,16 @@ def sample_greedy_topk(logits: DeviceArray, rows: int, vocab: int, out: DeviceAr
     (hyp_sample_greedy_topk); out is a device array of at least rows * 80 bytes."""
     ptr = ctypes.c_void_p((logits.ptr.value or 0) + 2 * row_offset * vocab) if row_offset else logits.ptr
     call("hyp_sample_greedy_topk", ptr, rows, vocab, out.ptr, stream.handle)
+
+
+def sample_stochastic(logits: DeviceArray, vocab: int, sampling: Optional[SamplingConfig], rng_state: int,
+                      out: DeviceArray, stream: Stream, row_offset: int = 0) -> None:
+    """out[0] = the temperature draw of logits row row_offset with the top-k sidecar
+    (hyp_sample_stochastic): ForwardPass::sample_stochastic (forward.cc:191-322) with the RNG
+    state rng_state; sampling None or temperature 0 is the greedy result."""
+    ptr = ctypes.c_void_p((logits.ptr.value or 0) + 2 * row_offset * vocab) if row_offset else logits.ptr
+    call("hyp_sample_stochastic", ptr, vocab, _sampling(sampling), rng_state & 0xFFFFFFFFFFFFFFFF, out.ptr,
+         stream.handle)
 
 
 def topk_samples(out: DeviceArray, rows: int, stream: Stream):

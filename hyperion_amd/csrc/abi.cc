@@ -15,6 +15,7 @@
 #include "kernels.h"
 #include "decoder.h"
 #include "qlinear.h"
+#include "sampling.h"
 #include "step_program_host.h"
 
 using hyperion::hip::Epilogue;
@@ -109,10 +110,15 @@ struct HypQModelOpaque {
 struct HypStreamOpaque {
     std::uint32_t magic = 0;
     hipStream_t stream = nullptr;
-    // Device workspace of the calls that need one (greedy sampling's slice states);
-    // work on one stream is ordered, so its calls never share it concurrently.
+    // Device workspace of the calls that need one (greedy sampling's slice states, then the
+    // temperature draw's bins and parameters from stoch_workspace_offset); work on one
+    // stream is ordered, so its calls never share it concurrently.
     void* workspace = nullptr;
-    size_t workspace_bytes = 0;
+    size_t workspace_bytes = 0;   // the greedy part
+    size_t stoch_workspace_offset = 0;
+    [[nodiscard]] void* stoch_workspace() const noexcept {
+        return static_cast<uint8_t*>(workspace) + stoch_workspace_offset;
+    }
 };
 
 struct HypEventOpaque {
@@ -255,8 +261,16 @@ HypStatus hyp_stream_create(HypStream* out_stream) {
         require_device();
         auto h = std::make_unique<HypStreamOpaque>();
         h->workspace_bytes = hyperion::hip::sample_greedy_workspace_bytes();
-        HYP_HIP_CHECK(hipMalloc(&h->workspace, h->workspace_bytes));
-        const hipError_t err = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+        h->stoch_workspace_offset = (h->workspace_bytes + 255u) / 256u * 256u;
+        const size_t bytes = h->stoch_workspace_offset + hyperion::hip::sample_stochastic_workspace_bytes();
+        HYP_HIP_CHECK(hipMalloc(&h->workspace, bytes));
+        hipError_t err = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+        if (err == hipSuccess) {
+            // The draw's bins start (and stay, between calls) zero.
+            hyperion::hip::init_sample_stochastic_workspace(h->stoch_workspace(), h->stream);
+            err = hipStreamSynchronize(h->stream);
+            if (err != hipSuccess) (void)hipStreamDestroy(h->stream);
+        }
         if (err != hipSuccess) {
             (void)hipFree(h->workspace);
             HYP_HIP_CHECK(err);
@@ -667,6 +681,25 @@ HypStatus hyp_sample_greedy_topk(const void* logits, uint32_t rows, uint32_t voc
     });
 }
 
+HypStatus hyp_sample_stochastic(const void* logits, uint32_t vocab, const HypSamplingConfig* config,
+                                uint64_t rng_state, HypTopKSample* out, HypStream stream) {
+    return abi_call("hyp_sample_stochastic", [&] {
+        hipStream_t s = stream_of(stream);
+        REQUIRE_ARG(out != nullptr, "out must be a non-null device pointer");
+        REQUIRE_ARG(vocab == 0 || logits != nullptr, "logits must be a non-null device pointer");
+        REQUIRE_ARG(vocab <= hyperion::hip::sample_topk_max_vocab(), "vocab must be at most 2^23");
+        const bool greedy = hyperion::model::sampling_is_greedy(config, vocab);
+        const auto* l = static_cast<const uint16_t*>(logits);
+        hyperion::hip::launch_sample_topk(l, 1, vocab, out, stream->workspace, stream->workspace_bytes, s);
+        if (greedy) return;
+        const hyperion::hip::SampleParams p = hyperion::model::sampling_params(*config);
+        hyperion::hip::launch_sample_params(stream->stoch_workspace(), p.inv_temp, p.top_p, p.min_p, p.top_k,
+                                            hyperion::model::sampling_uniform(rng_state), s);
+        hyperion::hip::launch_sample_stochastic(l, vocab, stream->stoch_workspace(),
+                                                hyperion::hip::sample_stochastic_workspace_bytes(), out, s);
+    });
+}
+
 HypStatus hyp_kv_cache_create(uint32_t capacity, uint32_t num_kv_heads, uint32_t head_dim, HypKvCache* out_cache) {
     return abi_call("hyp_kv_cache_create", [&] {
         REQUIRE_ARG(out_cache != nullptr, "create requires a non-null out handle");
@@ -1005,18 +1038,6 @@ HypStepResultOpaque& result_of(HypStepResult r) {
     return *r;
 }
 
-// validate_sampling_config (model.cc:234-257): NULL or temperature 0 is the greedy path.
-bool sampled_greedy(const HypSamplingConfig* c, uint32_t vocab) {
-    if (c == nullptr || c->temperature == 0.0f) return true;
-    REQUIRE_ARG(!(c->temperature < 0.0f), "sampling temperature must be >= 0 (0 = greedy)");
-    REQUIRE_ARG(c->top_k >= 0, "sampling top_k must be >= 0 (0 = disabled)");
-    REQUIRE_ARG(c->top_k == 0 || static_cast<uint64_t>(c->top_k) <= vocab, "sampling top_k exceeds the vocabulary size");
-    REQUIRE_ARG(std::isnan(c->top_p) || (c->top_p >= 0.0f && c->top_p <= 1.0f),
-                "sampling top_p must be in [0, 1] (0 = disabled)");
-    REQUIRE_ARG(c->min_p >= 0.0f && c->min_p < 1.0f, "sampling min_p must be in [0, 1) (0 = disabled)");
-    throw NativeError(HYP_STATUS_UNSUPPORTED, "sampling with temperature > 0 is not built; use temperature 0");
-}
-
 // write_step_result / write_step_result_sampled (model.cc:310-356).
 void write_result(HypStepResultOpaque& r, const hyperion::model::StepSample& smp,
                   const hyperion::model::DecoderState& st, bool sidecar) {
@@ -1121,8 +1142,8 @@ HypStatus hyp_prefill_chunk_sampled(HypModel model, HypKvState kvstate, const Hy
         hyperion::model::DecoderState& st = state_of(model, kvstate);
         check_tokens(tokens);
         HypStepResultOpaque& r = result_of(out_result);
-        sampled_greedy(config, dec.geometry().vocab);
-        const auto smp = dec.prefill(st, tokens->tokens, tokens->count);
+        const bool greedy = hyperion::model::sampling_is_greedy(config, dec.geometry().vocab);
+        const auto smp = dec.prefill(st, tokens->tokens, tokens->count, greedy ? nullptr : config);
         write_result(r, smp, st, true);
     });
 }
@@ -1133,8 +1154,8 @@ HypStatus hyp_decode_block_sampled(HypModel model, HypKvState kvstate, uint32_t 
         hyperion::model::Decoder& dec = loaded(model);
         hyperion::model::DecoderState& st = state_of(model, kvstate);
         HypStepResultOpaque& r = result_of(out_result);
-        sampled_greedy(config, dec.geometry().vocab);
-        const auto smp = dec.decode(st, n_tokens);
+        const bool greedy = hyperion::model::sampling_is_greedy(config, dec.geometry().vocab);
+        const auto smp = dec.decode(st, n_tokens, greedy ? nullptr : config);
         write_result(r, smp, st, true);
     });
 }

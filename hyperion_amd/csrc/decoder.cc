@@ -9,6 +9,7 @@
 #include <utility>
 
 #include "kernels.h"
+#include "sampling.h"
 
 namespace hyperion::model {
 
@@ -205,7 +206,8 @@ MemoryReport plan_memory(const Geometry& g) {
                       T * g.intermediate * 2u + static_cast<uint64_t>(g.hidden) * 2u +
                       uint64_t{hip::kSkinnyMaxM} * g.hidden * 2u + static_cast<uint64_t>(g.vocab) * 2u +
                       attention_ws_bytes(g) +
-                      hip::sample_greedy_workspace_bytes() + rope_table_bytes(g, g.head_dim_local) +
+                      hip::sample_greedy_workspace_bytes() + hip::sample_stochastic_workspace_bytes() +
+                      rope_table_bytes(g, g.head_dim_local) +
                       rope_table_bytes(g, g.head_dim_global);
     return r;
 }
@@ -229,7 +231,7 @@ MemoryReport Decoder::memory() const {
     }
     r.norm_bytes += w_.final_norm.bytes();
     for (const DeviceBuffer* b : {&ids_, &x_, &xn_, &xr_, &q_, &k_, &v_, &attn_, &o_, &h_, &d_, &last_, &logits_, &attn_ws_,
-                                  &sample_ws_, &rope_local_, &rope_global_}) {
+                                  &sample_ws_, &stoch_ws_, &rope_local_, &rope_global_}) {
         r.scratch_bytes += b->bytes();
     }
     const MemoryReport planned = plan_memory(geo_);   // a state is not allocated to be counted
@@ -314,6 +316,8 @@ Decoder::Decoder(Geometry geometry, ModelWeights weights) : geo_(std::move(geome
     logits_ = DeviceBuffer(static_cast<size_t>(g.vocab) * 2u);
     attn_ws_ = DeviceBuffer(attention_ws_bytes(g));
     sample_ws_ = DeviceBuffer(hip::sample_greedy_workspace_bytes());
+    stoch_ws_ = DeviceBuffer(hip::sample_stochastic_workspace_bytes());
+    hip::init_sample_stochastic_workspace(stoch_ws_.data(), stream_);
     const auto table = [&](uint32_t D, LayerType kind, double theta) {
         const size_t bytes = rope_table_bytes(g, D);
         if (bytes == 0) return DeviceBuffer();
@@ -362,14 +366,14 @@ DecoderState Decoder::make_state() const {
     return st;
 }
 
-void Decoder::capture_step(DecoderState& st) {
+GraphExec Decoder::capture_step(DecoderState& st, bool draw) {
     auto* cur = static_cast<HypTopKSample*>(st.cur.data());
     auto* counters = static_cast<uint32_t*>(st.counters.data());
     HYP_HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
     hipGraph_t graph = nullptr;
     try {
         forward_chunk(st, &cur->token_id, 1, 0, nullptr, counters);
-        epilogue(cur);
+        epilogue(cur, draw);
         hip::launch_decode_advance(counters, counters + 1, cur, stream_);
     } catch (...) {
         (void)hipStreamEndCapture(stream_, &graph);
@@ -381,7 +385,7 @@ void Decoder::capture_step(DecoderState& st) {
     const hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     HYP_HIP_CHECK(err);
-    st.step = GraphExec(exec);
+    return GraphExec(exec);
 }
 
 void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset,
@@ -522,11 +526,16 @@ void Decoder::forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L,
     }
 }
 
-void Decoder::epilogue(HypTopKSample* d_out) {
+void Decoder::epilogue(HypTopKSample* d_out, bool draw) {
     // run_epilogue (model.cc:215-228): tied lm_head + softcap on the last position, then
-    // the greedy pick with its top-k sidecar (model.cc:262-288).
+    // the greedy pick with its top-k sidecar (model.cc:262-288). The sampled epilogue
+    // (model.cc:262-301) keeps that sidecar of the pre-filter logits (forward.cc:303-319) and
+    // replaces the token with the draw.
     w_.embed.apply(u16(last_), 1, u16(logits_), stream_, Epilogue::kSoftcap, softcap_);
     hip::launch_sample_topk(u16(logits_), 1, geo_.vocab, d_out, sample_ws_.data(), sample_ws_.bytes(), stream_);
+    if (draw) {
+        hip::launch_sample_stochastic(u16(logits_), geo_.vocab, stoch_ws_.data(), stoch_ws_.bytes(), d_out, stream_);
+    }
 }
 
 void Decoder::forward_hidden(DecoderState& st, const uint32_t* ids, uint32_t count, uint32_t offset,
@@ -548,7 +557,8 @@ void Decoder::forward_hidden(DecoderState& st, const uint32_t* ids, uint32_t cou
     }
 }
 
-StepSample Decoder::prefill(DecoderState& st, const uint32_t* ids, uint32_t count) {
+StepSample Decoder::prefill(DecoderState& st, const uint32_t* ids, uint32_t count,
+                            const HypSamplingConfig* sampling) {
     const Geometry& g = geo_;
     if (st.offset != 0) invalid("prefill requires a fresh (offset 0) KV state");
     if (count > g.max_positions) invalid("the prompt exceeds max_position_embeddings");
@@ -561,7 +571,15 @@ StepSample Decoder::prefill(DecoderState& st, const uint32_t* ids, uint32_t coun
         HYP_HIP_CHECK(hipMemcpyAsync(ids_.data(), ids + done, take * sizeof(uint32_t), hipMemcpyHostToDevice, stream_));
         forward_chunk(st, static_cast<const uint32_t*>(ids_.data()), take, done, nullptr);
         done += take;
-        if (done == count) epilogue(cur);
+        if (done == count) {
+            if (sampling != nullptr) {
+                // The prefill's draw uses the request seed itself (model.cc:840-841).
+                const hip::SampleParams p = sampling_params(*sampling);
+                hip::launch_sample_params(stoch_ws_.data(), p.inv_temp, p.top_p, p.min_p, p.top_k,
+                                          sampling_uniform(sampling->seed), stream_);
+            }
+            epilogue(cur, sampling != nullptr);
+        }
         // The ids buffer is reused by the next chunk: its copy waits for this chunk.
         HYP_HIP_CHECK(hipStreamSynchronize(stream_));
     }
@@ -609,7 +627,7 @@ thread_local bool g_fault_after_first_replay = false;
 
 }  // namespace
 
-StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
+StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens, const HypSamplingConfig* sampling) {
     const Geometry& g = geo_;
     if (st.offset == 0) invalid("decode requires a populated KV state (prefill first)");
     if (static_cast<uint64_t>(st.offset) + n_tokens > g.max_positions) {
@@ -617,7 +635,23 @@ StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
     }
     StepSample out;
     if (n_tokens == 0) return out;
-    if (st.step.get() == nullptr) capture_step(st);
+    GraphExec& graph = sampling != nullptr ? st.sampled_step : st.step;
+    if (graph.get() == nullptr) graph = capture_step(st, sampling != nullptr);
+    // The draws' parameters: per block of up to kMaxSampledSteps replays, the config and
+    // the uniform of each step's RNG state (the state starts at the seed every call and
+    // advances per step, model.cc:926-944). Each block's copy is queued before its replays;
+    // the host blocks stay alive until the stream has been synchronised below.
+    std::vector<hip::SampleParams> blocks;
+    if (sampling != nullptr) {
+        blocks.resize((n_tokens + hip::kMaxSampledSteps - 1u) / hip::kMaxSampledSteps, sampling_params(*sampling));
+        uint64_t state = sampling->seed;
+        for (uint32_t j = 0; j < n_tokens; ++j) {
+            hip::SampleParams& b = blocks[j / hip::kMaxSampledSteps];
+            b.uniform[b.n_uniform++] = sampling_uniform(state);
+            state = advance_sampling_state(state);
+        }
+    }
+    hip::SampleParams* d_params = hip::sample_stochastic_params(stoch_ws_.data());
     // The replays start from the cursor with a cleared near-tie count; each embeds the
     // token in cur, samples the next one into cur and advances the position.
     const uint32_t start[2] = {st.offset, 0u};
@@ -626,7 +660,11 @@ StepSample Decoder::decode(DecoderState& st, uint32_t n_tokens) {
     ConsumeOnFailure guard(st, stream_);
     guard.arm();
     for (uint32_t j = 0; j < n_tokens; ++j) {
-        HYP_HIP_CHECK(hipGraphLaunch(st.step.get(), stream_));
+        if (sampling != nullptr && j % hip::kMaxSampledSteps == 0u) {
+            HYP_HIP_CHECK(hipMemcpyAsync(d_params, &blocks[j / hip::kMaxSampledSteps], sizeof(hip::SampleParams),
+                                         hipMemcpyHostToDevice, stream_));
+        }
+        HYP_HIP_CHECK(hipGraphLaunch(graph.get(), stream_));
 #ifdef HYP_TEST_FAULTS
         if (g_fault_after_first_replay) {
             g_fault_after_first_replay = false;

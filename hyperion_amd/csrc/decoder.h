@@ -118,6 +118,7 @@ struct DecoderState {
     DeviceBuffer cur;                 // HypTopKSample: the last sampled token, on the device
     DeviceBuffer counters;            // uint32 [2]: the device-side position and near-tie count
     GraphExec step;                   // one decode step, captured at the first decode
+    GraphExec sampled_step;           // the same with the temperature draw, at the first sampled decode
     uint64_t local_bytes = 0;
     uint64_t global_bytes = 0;
     // Set when a decode failed after its first replay was enqueued: the KV rows, the device
@@ -151,10 +152,15 @@ class Decoder {
     void forward_hidden(DecoderState& st, const uint32_t* ids, uint32_t count, uint32_t offset,
                         uint16_t* hidden_out);
     // hyp_prefill_chunk: chunked prefill of a fresh state, then the epilogue on the last
-    // position. Synchronous.
-    StepSample prefill(DecoderState& st, const uint32_t* ids, uint32_t count);
-    // hyp_decode_block: n_tokens greedy steps from the cursor. Synchronous.
-    StepSample decode(DecoderState& st, uint32_t n_tokens);
+    // position. With `sampling` (a validated config with temperature > 0:
+    // hyp_prefill_chunk_sampled) the token is drawn with the config's seed (model.cc:841).
+    // Synchronous.
+    StepSample prefill(DecoderState& st, const uint32_t* ids, uint32_t count,
+                       const HypSamplingConfig* sampling = nullptr);
+    // hyp_decode_block: n_tokens greedy steps from the cursor; with `sampling`
+    // (hyp_decode_block_sampled) each step draws, the RNG state starting from the config's
+    // seed and advancing per step (model.cc:924-944). Synchronous.
+    StepSample decode(DecoderState& st, uint32_t n_tokens, const HypSamplingConfig* sampling = nullptr);
     // The allocated buffers, summed (KV and state as make_state allocates them).
     [[nodiscard]] MemoryReport memory() const;
 
@@ -165,11 +171,12 @@ class Decoder {
     // and `offset` is unused.
     void forward_chunk(DecoderState& st, const uint32_t* d_ids, uint32_t L, uint32_t offset, uint16_t* final_rows,
                        const uint32_t* d_pos = nullptr);
-    // lm_head + softcap + greedy with the top-k sidecar of last_ into *d_out.
-    void epilogue(HypTopKSample* d_out);
+    // lm_head + softcap + greedy with the top-k sidecar of last_ into *d_out; with `draw`
+    // the temperature draw (the parameters in stoch_ws_) then replaces the token and logit.
+    void epilogue(HypTopKSample* d_out, bool draw = false);
     // Capture one decode step of `st` (embed cur's token at *pos, every layer, the head,
-    // the sample into cur, pos += 1) as a graph.
-    void capture_step(DecoderState& st);
+    // the sample into cur, pos += 1) as a graph; `draw`: the sampled epilogue.
+    GraphExec capture_step(DecoderState& st, bool draw);
 
     Geometry geo_;
     ModelWeights w_;
@@ -180,6 +187,7 @@ class Decoder {
     DeviceBuffer x_, xn_, q_, k_, v_, attn_, o_, h_, d_, last_, logits_;
     DeviceBuffer xr_;            // [kSkinnyMaxM][hidden]: the residual stream's second buffer at decode sizes
     DeviceBuffer attn_ws_, sample_ws_;
+    DeviceBuffer stoch_ws_;      // the temperature draw's bins (zero between draws) and SampleParams
     // RoPE (cos, sin) of every position per layer kind, computed once on the device with
     // the rope kernel's arithmetic (a 12B at 262144 positions: 0.8 GB); empty when larger
     // than kRopeTableMaxBytes, then the prepare kernel computes them per token.

@@ -120,6 +120,35 @@ uint32_t sample_topk_max_vocab();
 void launch_sample_topk(const uint16_t* logits, uint32_t rows, uint32_t vocab, HypTopKSample* out, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 
+// Temperature sampling of one row (ForwardPass::sample_stochastic, forward.cc:192-310), the
+// filters and draw on the device. Its parameters live in device memory so that a captured
+// decode step can sample with the configuration and uniforms the host writes before the
+// replays: each launch draws with uniform[min(step, n_uniform - 1)] and advances step.
+constexpr uint32_t kMaxSampledSteps = 256;
+struct SampleParams {
+    float inv_temp;   // 1 / temperature (fp32)
+    float top_p;      // (0, 1]: nucleus; otherwise off
+    float min_p;      // (0, 1): min-p; otherwise off
+    int32_t top_k;    // (0, vocab): top-k; otherwise off
+    uint32_t n_uniform;
+    uint32_t step;
+    float uniform[kMaxSampledSteps];   // std::generate_canonical<float> of std::mt19937_64, per step
+};
+// Device workspace of launch_sample_stochastic (256-byte aligned): 65536 value bins and a flag
+// word, zero between launches (init_sample_stochastic_workspace clears a new workspace once;
+// every launch leaves them zero), the decision of the cut, and the SampleParams.
+size_t sample_stochastic_workspace_bytes();
+void init_sample_stochastic_workspace(void* workspace, hipStream_t stream);
+SampleParams* sample_stochastic_params(void* workspace);
+// Write a one-draw SampleParams (uniform[0] = canon) into the workspace, as a kernel (its
+// values travel as kernel arguments, so a captured call keeps them).
+void launch_sample_params(void* workspace, float inv_temp, float top_p, float min_p, int32_t top_k, float canon,
+                          hipStream_t stream);
+// out->token_id, logit and near_tie (0) of the draw with the workspace's SampleParams; the
+// top-k sidecar is launch_sample_topk's. vocab is at most 2^23.
+void launch_sample_stochastic(const uint16_t* logits, uint32_t vocab, void* workspace, size_t workspace_bytes,
+                              HypTopKSample* out, hipStream_t stream);
+
 // Attention (forward.cc:376-508) over a KV cache prefix and the current chunk; see
 // attention.hip. Decode splits the keys; the partial sums need attention_workspace_bytes.
 constexpr uint32_t kAttnMaxSplits = 64;

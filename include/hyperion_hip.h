@@ -132,8 +132,9 @@ HypStatus hyp_runtime_info(HypRuntimeInfo* out);
  * mx::Stream arguments, weights.h:26); a C caller of this engine gets them here. */
 HypStatus hyp_device_alloc(size_t bytes, void** out_ptr);
 HypStatus hyp_device_free(void** ptr);
-/* A non-blocking HIP stream plus a 48 KiB device workspace for the calls that need one
- * (hyp_sample_greedy). destroy waits for the device before freeing the workspace. */
+/* A non-blocking HIP stream plus a 306 KiB device workspace for the calls that need one
+ * (hyp_sample_greedy, hyp_sample_greedy_topk, hyp_sample_stochastic). destroy waits for the
+ * device before freeing the workspace. */
 HypStatus hyp_stream_create(HypStream* out_stream);
 HypStatus hyp_stream_destroy(HypStream* stream);
 HypStatus hyp_stream_synchronize(HypStream stream);
@@ -383,7 +384,8 @@ HypStatus hyp_residual_rms_norm(const void* branch, void* residual, const void* 
  * model's own HIP stream; one thread drives a model and its states. Differences: no
  * governor (governor_state is always READY and peak/active bytes are 0; every cache is
  * allocated at its final size by hyp_kvstate_create, so there is nothing to admit),
- * token ids >= vocab_size are rejected, and sampling with temperature > 0 is UNSUPPORTED. */
+ * token ids >= vocab_size are rejected, and the temperature draw fixes the orders the
+ * reference leaves to its library (hyp_sample_stochastic). */
 typedef struct HypModelOpaque* HypModel;             /* magic "HPMD" */
 typedef struct HypKvStateOpaque* HypKvState;         /* magic "HPKS" */
 typedef struct HypStepResultOpaque* HypStepResult;   /* magic "HPSR" */
@@ -499,13 +501,39 @@ HypStatus hyp_prefill_chunk(HypModel model, HypKvState kvstate, const HypTokenSt
  * state return HYP_STATUS_INTERNAL until it is freed and recreated (hyperion_mlx.h:204-208,
  * DirectKvExecutionGuard model.cc:79-105). */
 HypStatus hyp_decode_block(HypModel model, HypKvState kvstate, uint32_t n_tokens, HypStepResult out_result);
-/* The same with a sampling config: NULL or temperature 0 is the greedy path plus the
- * top-k sidecar (near_tie_events 0, as model.cc:262-288 reports it); temperature > 0 is
- * UNSUPPORTED; a malformed config is INVALID_ARGUMENT (model.cc:234-257). */
+/* The same with a sampling config (hyperion_mlx.h:210-231, model.cc:743-960): NULL or
+ * temperature 0 is the greedy path plus the top-k sidecar (near_tie_events 0, as
+ * model.cc:262-288 reports it); a malformed config is INVALID_ARGUMENT (model.cc:234-257);
+ * temperature > 0 draws each token as hyp_sample_stochastic does, on the device, with the
+ * top-k sidecar of the pre-filter logits. The prefill draws with the RNG state config->seed
+ * (model.cc:841); a decode block starts every call from config->seed and advances the state
+ * per step as state * 6364136223846793005 + 1442695040888963407 (model.cc:926-944), so the
+ * same seed and prompt give the same tokens. */
 HypStatus hyp_prefill_chunk_sampled(HypModel model, HypKvState kvstate, const HypTokenStream* tokens,
                                     const HypSamplingConfig* config, HypStepResult out_result);
 HypStatus hyp_decode_block_sampled(HypModel model, HypKvState kvstate, uint32_t n_tokens,
                                    const HypSamplingConfig* config, HypStepResult out_result);
+
+/* ForwardPass::sample_stochastic (forward.cc:191-322) of one row of vocab bf16 logits
+ * (device memory) into *out (device memory, 80 bytes), replacing the host copy of the row,
+ * the host softmax, sorts and draw: config (host memory) is validated as
+ * validate_sampling_config does (model.cc:234-257; INVALID_ARGUMENT); NULL or temperature 0
+ * gives hyp_sample_greedy_topk's result. Otherwise t = logit * (1/temperature), the softmax
+ * of t, the top-p nucleus, min-p and top-k filters (each as the reference applies it) and a
+ * draw u = sz * U, where U = std::generate_canonical<float, 24> of std::mt19937_64 seeded with
+ * rng_state (what std::uniform_real_distribution<float>(0, sz) draws under libstdc++) and sz
+ * the kept total: the first index whose running sum of the kept exp(t - max t) reaches u;
+ * token_id, logit (its pre-filter value), near_tie 0, and the top-k sidecar of the
+ * pre-filter logits. The reference leaves the order of equal probabilities and of its fp32
+ * sums to its library (a statistical bar, hyperion_mlx.h:125-133); here they are fixed:
+ * equal values are kept lowest index first, and the sums run in the kernels' fixed order,
+ * so the result is a deterministic function of (logits, config, rng_state). A +inf or NaN
+ * scaled logit makes the reference's draw total NaN and its draw the last index; so here.
+ * With no finite scaled logit (and no such value) it draws index 0, as the reference's zero
+ * total does. vocab is at most 2^23. Uses the stream's workspace (hyp_sample_greedy's
+ * capture rules; a captured call keeps its rng_state). */
+HypStatus hyp_sample_stochastic(const void* logits, uint32_t vocab, const HypSamplingConfig* config,
+                                uint64_t rng_state, HypTopKSample* out, HypStream stream);
 HypStatus hyp_step_result_create(HypStepResult* out_result);
 HypStatus hyp_step_result_free(HypStepResult* result);
 HypStatus hyp_step_result_fields(HypStepResult result, HypStepResultFields* out_fields);

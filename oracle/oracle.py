@@ -49,6 +49,10 @@ def lib():
         L.orc_rms_norm_bf16.argtypes = [_P, _P, _I, _I, ctypes.c_float, _P]
         L.orc_rope_bf16.argtypes = [_P, _I, _I, _I, _I, ctypes.c_double, _I, _P]
         L.orc_attention_f64.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]
+        L.orc_det_exp.restype = ctypes.c_float
+        L.orc_det_exp.argtypes = [ctypes.c_float]
+        L.orc_sample_stochastic_bf16.argtypes = [_P, ctypes.c_uint32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                                 ctypes.c_int32, ctypes.c_float, _P, _P, _P]
         _lib = L
     return _lib
 
@@ -179,24 +183,91 @@ def sample_topk(logits, k: int = TOP_K):
     return int(cnt), ids, vals
 
 
+def det_exp(x: float) -> float:
+    """exp(x), x <= 0, as the sampling kernels compute it."""
+    return float(lib().orc_det_exp(float(x)))
+
+
+def sample_stochastic(logits, temperature: float, top_k: int = 0, top_p: float = 0.0, min_p: float = 0.0,
+                      canon: float = 0.5):
+    """ForwardPass::sample_stochastic's draw of a 1-D bf16 row with the HIP kernels' defined
+    orders -> (token_id, logit, kept): kept is the size of the kept prefix (value
+    descending, index ascending), 0 for a row drawn without weights. canon: the uniform in
+    [0, 1) (canonical(state) for an RNG state)."""
+    x = _c(logits, np.uint16).reshape(-1)
+    with np.errstate(over="ignore", divide="ignore"):
+        inv_temp = np.float32(1.0) / np.float32(temperature)
+    tok = ctypes.c_uint32()
+    val = ctypes.c_float()
+    kept = ctypes.c_uint32()
+    lib().orc_sample_stochastic_bf16(_p(x), x.size, float(inv_temp), float(top_p), float(min_p), int(top_k),
+                                     float(canon), ctypes.byref(tok), ctypes.byref(val), ctypes.byref(kept))
+    return tok.value, val.value, kept.value
+
+
 _stl = None
 
 
-def stl_partial_sort_topk(p_f32, k: int = TOP_K) -> np.ndarray:
-    """libstdc++ std::partial_sort of the indices by p[a] > p[b] (model.cc:278-288): the
-    first min(k, n) indices."""
+def stl():
+    """oracle/libstlsort.so: the reference's standard-library calls (libstdc++)."""
     global _stl
     if _stl is None:
         path = os.path.join(os.path.dirname(_LIB_PATH), "libstlsort.so")
         if not os.path.exists(path):
             raise RuntimeError(f"oracle library not built: {path} (run __graft_entry__.build())")
-        _stl = ctypes.CDLL(path)
-        _stl.stl_partial_sort_topk.restype = ctypes.c_uint32
-        _stl.stl_partial_sort_topk.argtypes = [_P, _I, ctypes.c_uint32, _P]
+        S = ctypes.CDLL(path)
+        S.stl_partial_sort_topk.restype = ctypes.c_uint32
+        S.stl_partial_sort_topk.argtypes = [_P, _I, ctypes.c_uint32, _P]
+        S.stl_canonical_mt19937_64.restype = ctypes.c_float
+        S.stl_canonical_mt19937_64.argtypes = [ctypes.c_uint64]
+        S.stl_uniform_real_mt19937_64.restype = ctypes.c_float
+        S.stl_uniform_real_mt19937_64.argtypes = [ctypes.c_uint64, ctypes.c_float]
+        S.stl_mt19937_64_nth.restype = ctypes.c_uint64
+        S.stl_mt19937_64_nth.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        S.stl_sample_stochastic.restype = ctypes.c_uint32
+        S.stl_sample_stochastic.argtypes = [_P, ctypes.c_uint32, ctypes.c_float, ctypes.c_int32, ctypes.c_float,
+                                            ctypes.c_float, ctypes.c_uint64, _P, _P]
+        _stl = S
+    return _stl
+
+
+def stl_partial_sort_topk(p_f32, k: int = TOP_K) -> np.ndarray:
+    """libstdc++ std::partial_sort of the indices by p[a] > p[b] (model.cc:278-288): the
+    first min(k, n) indices."""
     p = _c(p_f32, np.float32).reshape(-1)
     ids = np.zeros(k, np.uint32)
-    cnt = _stl.stl_partial_sort_topk(_p(p), p.size, k, _p(ids))
+    cnt = stl().stl_partial_sort_topk(_p(p), p.size, k, _p(ids))
     return ids[:cnt]
+
+
+def canonical(state: int) -> float:
+    """std::generate_canonical<float, 24> of std::mt19937_64(state) (libstdc++)."""
+    return float(stl().stl_canonical_mt19937_64(state & 0xFFFFFFFFFFFFFFFF))
+
+
+def stl_uniform_real(state: int, b: float) -> float:
+    """std::uniform_real_distribution<float>(0, b) drawn once from std::mt19937_64(state)."""
+    return float(stl().stl_uniform_real_mt19937_64(state & 0xFFFFFFFFFFFFFFFF, b))
+
+
+def mt19937_64_nth(seed: int, n: int) -> int:
+    return int(stl().stl_mt19937_64_nth(seed & 0xFFFFFFFFFFFFFFFF, n))
+
+
+def advance_rng(state: int) -> int:
+    """The per-step RNG state advance of the sampled decode loop (model.cc:944)."""
+    return (state * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
+
+
+def stl_sample_stochastic(logits_f32, temperature: float, top_k: int = 0, top_p: float = 0.0, min_p: float = 0.0,
+                          rng_state: int = 0):
+    """The reference's host sampler restated over libstdc++ -> (token, kept mask bool[n], u)."""
+    x = _c(logits_f32, np.float32).reshape(-1)
+    kept = np.zeros(x.size, np.uint8)
+    u = ctypes.c_float()
+    tok = stl().stl_sample_stochastic(_p(x), x.size, float(temperature), int(top_k), float(top_p), float(min_p),
+                                      rng_state & 0xFFFFFFFFFFFFFFFF, _p(kept), ctypes.byref(u))
+    return int(tok), kept.astype(bool), u.value
 
 
 def gelu_tanh(x) -> np.ndarray:

@@ -404,6 +404,262 @@ static float butterfly64(float* v) {
     return v[0];
 }
 
+/* ---- temperature sampling: ForwardPass::sample_stochastic (forward.cc:191-301) ----------
+ *
+ * The reference scales the fp32 logits by 1/temperature, takes the softmax, masks the tokens
+ * outside the top-p nucleus (probability descending), below min_p times the largest
+ * probability and outside the top-k (logit descending), then draws u from
+ * uniform_real_distribution<float>(0, sz) and returns the first index whose running sum of
+ * kept exp(t - max) reaches u (forward.cc:225-301). Its sort tie order and host summation
+ * order are not fixed by its contract (hyperion_mlx.h:125-133: a statistical bar), so this
+ * restates the defined algorithm of the HIP kernels, which fixes them:
+ *   - 65536 bins over the bf16 value (bin 0 = largest, -0 as +0; -inf, +inf, NaN no bin);
+ *     every filter keeps a prefix of (value descending, index ascending);
+ *   - exp is st_exp below (the same fp32 operations as the device);
+ *   - z = 16 waves (in order) of a 64-lane xor butterfly of per-lane sequential sums over 64
+ *     bins; running sums over bins and tokens: a sequential sum within each of 1024 chunks
+ *     added to the sequential exclusive prefix of the chunk totals;
+ *   - rows whose scaled logits hold +inf or NaN draw the last index, rows with no finite
+ *     scaled logit (and none of those) draw index 0 - what the reference's arithmetic gives.
+ * canon is the uniform in [0, 1) (std::generate_canonical<float> of std::mt19937_64 seeded
+ * with the request's RNG state; u = sz * canon). */
+#define ST_BINS 65536u
+#define ST_NOBIN ST_BINS
+#define ST_THREADS 1024u
+#define ST_PER 64u
+#define ST_NONE 0xFFFFFFFFu
+
+static uint32_t st_bin_of(uint16_t h) {
+    uint32_t b = h;
+    if (b == 0x8000u) b = 0u;
+    if ((b & 0x7F80u) == 0x7F80u) return ST_NOBIN;
+    const uint32_t ok = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+    return 0xFFFFu - ok;
+}
+
+static float st_bin_value(uint32_t d) {
+    const uint32_t ok = 0xFFFFu - d;
+    const uint32_t b = (ok & 0x8000u) ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
+    return orc_f32_from_bf16((uint16_t)b);
+}
+
+/* exp(x), x <= 0: Cody-Waite reduction by ln 2 (ln 2 split as 0.693145751953125 +
+ * 1.42860677e-06), the degree-7 Taylor polynomial of exp on |r| <= 0.35 in Horner form,
+ * times 2^k; 0 at or below -86 (results stay normal numbers). Unfused fp32 operations. */
+float orc_det_exp(float x) {
+    if (!(x > -86.0f)) return 0.0f;
+    const float kf = rintf(x * 1.44269502f);
+    const float r = (x - kf * 0.693145751953125f) - kf * 1.42860677e-06f;
+    float p = 1.98412701e-04f;
+    p = p * r + 1.38888892e-03f;
+    p = p * r + 8.33333377e-03f;
+    p = p * r + 4.16666679e-02f;
+    p = p * r + 1.66666672e-01f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    const int k = (int)kf;
+    uint32_t e = (uint32_t)(k + 127) << 23;
+    float scale;
+    memcpy(&scale, &e, 4);
+    return p * scale;
+}
+
+static float st_weight(uint32_t d, float inv_temp, float max_t) {
+    return orc_det_exp(st_bin_value(d) * inv_temp - max_t);
+}
+
+static void st_prefix_f(float* a) {   /* exclusive, sequential; a[ST_THREADS] = total */
+    float run = 0.0f;
+    for (uint32_t j = 0; j < ST_THREADS; ++j) {
+        const float v = a[j];
+        a[j] = run;
+        run = run + v;
+    }
+    a[ST_THREADS] = run;
+}
+
+static void st_prefix_u(uint32_t* a) {
+    uint32_t run = 0u;
+    for (uint32_t j = 0; j < ST_THREADS; ++j) {
+        const uint32_t v = a[j];
+        a[j] = run;
+        run = run + v;
+    }
+    a[ST_THREADS] = run;
+}
+
+void orc_sample_stochastic_bf16(const uint16_t* logits, uint32_t vocab, float inv_temp, float top_p, float min_p,
+                                int32_t top_k, float canon, uint32_t* token, float* logit, uint32_t* kept) {
+    uint32_t* cnt = (uint32_t*)calloc(ST_BINS, sizeof(uint32_t));
+    int inf_nan = 0, neg_inf = 0;
+    for (uint32_t i = 0; i < vocab; ++i) {
+        const uint32_t d = st_bin_of(logits[i]);
+        if (d < ST_BINS) cnt[d] += 1u;
+        else if (logits[i] == 0xFF80u) neg_inf = 1;
+        else inf_nan = 1;
+    }
+    uint32_t top = ST_NOBIN;
+    for (uint32_t d = 0; d < ST_BINS && top == ST_NOBIN; ++d) {
+        if (cnt[d] != 0u) top = d;
+    }
+    const float max_t = top != ST_NOBIN ? st_bin_value(top) * inv_temp : 0.0f;
+    int mode = 0;   /* 0 kept, 1 index 0, 2 the last index */
+    if (inf_nan || (neg_inf && inv_temp == 0.0f) || isnan(inv_temp) || isnan(max_t) || max_t == INFINITY) {
+        mode = 2;
+    } else if (top == ST_NOBIN || max_t == -INFINITY) {
+        mode = 1;
+    }
+    if (mode != 0 || vocab == 0u) {
+        const uint32_t arg = mode == 2 && vocab != 0u ? vocab - 1u : 0u;
+        *token = arg;
+        *logit = vocab != 0u ? orc_f32_from_bf16(logits[arg]) : -INFINITY;
+        if (kept) *kept = 0u;
+        free(cnt);
+        return;
+    }
+
+    /* z: per lane (thread) a sequential sum over its 64 bins, a butterfly per wave, the
+     * 16 wave sums in order. */
+    float z = 0.0f;
+    for (uint32_t w = 0; w < ST_THREADS / 64u; ++w) {
+        float lanes[64];
+        for (uint32_t l = 0; l < 64u; ++l) {
+            const uint32_t d0 = (w * 64u + l) * ST_PER;
+            float zl = 0.0f;
+            for (uint32_t d = d0; d < d0 + ST_PER; ++d) {
+                if (cnt[d] != 0u) zl = zl + (float)cnt[d] * st_weight(d, inv_temp, max_t);
+            }
+            lanes[l] = zl;
+        }
+        z = z + butterfly64(lanes);
+    }
+
+    float fs[ST_THREADS + 1];
+    uint32_t us[ST_THREADS + 1];
+    for (uint32_t t = 0; t < ST_THREADS; ++t) {
+        float pl = 0.0f;
+        uint32_t tl = 0u;
+        for (uint32_t d = t * ST_PER; d < (t + 1u) * ST_PER; ++d) {
+            if (cnt[d] != 0u) pl = pl + (float)cnt[d] * (st_weight(d, inv_temp, max_t) / z);
+            tl += cnt[d];
+        }
+        fs[t] = pl;
+        us[t] = tl;
+    }
+    st_prefix_f(fs);
+    st_prefix_u(us);
+    const uint32_t total = us[ST_THREADS];
+
+    /* top-p: per thread the first bin where its running mass reaches top_p, the smallest
+     * count t within that bin by bisection; the lowest position over threads. */
+    uint32_t np = total;
+    if (top_p > 0.0f && top_p <= 1.0f) {
+        uint32_t best = ST_NONE;
+        for (uint32_t t = 0; t < ST_THREADS; ++t) {
+            const float start = fs[t];
+            float part = 0.0f;
+            uint32_t seen = us[t];
+            uint32_t cand = ST_NONE;
+            for (uint32_t d = t * ST_PER; d < (t + 1u) * ST_PER && cand == ST_NONE; ++d) {
+                const uint32_t c = cnt[d];
+                if (c == 0u) continue;
+                const float p = st_weight(d, inv_temp, max_t) / z;
+                const float cb = start + part;
+                if (cb + (float)c * p >= top_p) {
+                    uint32_t lo = 1u, hi = c;
+                    while (lo < hi) {
+                        const uint32_t mid = (lo + hi) >> 1;
+                        if (cb + (float)mid * p >= top_p) hi = mid; else lo = mid + 1u;
+                    }
+                    cand = seen + lo;
+                }
+                part = part + (float)c * p;
+                seen += c;
+            }
+            if (cand < best) best = cand;
+        }
+        if (best != ST_NONE) np = best;
+    }
+    /* min-p: the tokens whose probability is at least min_p * (1 / z). */
+    uint32_t nm = total;
+    if (min_p > 0.0f && min_p < 1.0f) {
+        const float thr = min_p * (1.0f / z);
+        nm = 0u;
+        for (uint32_t d = 0; d < ST_BINS; ++d) {
+            if (cnt[d] != 0u && st_weight(d, inv_temp, max_t) / z >= thr) nm += cnt[d];
+        }
+    }
+    const uint32_t nk = top_k > 0 && (uint32_t)top_k < vocab ? (uint32_t)top_k : total;
+    uint32_t n = np < nm ? np : nm;
+    if (nk < n) n = nk;
+    if (total < n) n = total;
+    uint32_t cut_bin = 0u, cut_count = 0u, seen = 0u;
+    for (uint32_t d = 0; d < ST_BINS; ++d) {
+        if (seen + cnt[d] >= n && cnt[d] != 0u) {
+            cut_bin = d;
+            cut_count = n - seen;
+            break;
+        }
+        seen += cnt[d];
+    }
+    free(cnt);
+    if (kept) *kept = n;
+
+    /* The draw: chunk t of ceil(vocab / 1024) tokens; the cut bin's ranks before each chunk;
+     * kept weights summed per chunk, then the exclusive prefix over chunks. */
+    const uint32_t chunk = (vocab + ST_THREADS - 1u) / ST_THREADS;
+    uint32_t rank0[ST_THREADS + 1];
+    for (uint32_t t = 0; t < ST_THREADS; ++t) {
+        const uint32_t b = t * chunk < vocab ? t * chunk : vocab;
+        const uint32_t e = b + chunk < vocab ? b + chunk : vocab;
+        uint32_t c = 0u;
+        for (uint32_t i = b; i < e; ++i) c += st_bin_of(logits[i]) == cut_bin ? 1u : 0u;
+        rank0[t] = c;
+    }
+    st_prefix_u(rank0);
+#define ST_KEPT(d, rank) ((d) < cut_bin || ((d) == cut_bin && (rank)++ < cut_count))
+    for (uint32_t t = 0; t < ST_THREADS; ++t) {
+        const uint32_t b = t * chunk < vocab ? t * chunk : vocab;
+        const uint32_t e = b + chunk < vocab ? b + chunk : vocab;
+        float sum = 0.0f;
+        uint32_t rank = rank0[t];
+        for (uint32_t i = b; i < e; ++i) {
+            const uint32_t d = st_bin_of(logits[i]);
+            if (ST_KEPT(d, rank)) sum = sum + orc_det_exp(orc_f32_from_bf16(logits[i]) * inv_temp - max_t);
+        }
+        fs[t] = sum;
+    }
+    st_prefix_f(fs);
+    const float sz = fs[ST_THREADS];
+    const float u = sz * canon + 0.0f;
+    uint32_t arg = ST_NONE;
+    if (u <= 0.0f) {
+        arg = 0u;
+    } else {
+        for (uint32_t t = 0; t < ST_THREADS && arg == ST_NONE; ++t) {
+            const uint32_t b = t * chunk < vocab ? t * chunk : vocab;
+            const uint32_t e = b + chunk < vocab ? b + chunk : vocab;
+            const float start = fs[t];
+            float part = 0.0f;
+            uint32_t rank = rank0[t];
+            for (uint32_t i = b; i < e; ++i) {
+                const uint32_t d = st_bin_of(logits[i]);
+                if (!ST_KEPT(d, rank)) continue;
+                part = part + orc_det_exp(orc_f32_from_bf16(logits[i]) * inv_temp - max_t);
+                if (u <= start + part) {
+                    arg = i;
+                    break;
+                }
+            }
+        }
+    }
+#undef ST_KEPT
+    if (arg >= vocab) arg = vocab - 1u;
+    *token = arg;
+    *logit = orc_f32_from_bf16(logits[arg]);
+}
+
 void orc_rms_norm_bf16(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t k, float eps, uint16_t* y) {
     for (int64_t r = 0; r < rows; ++r) {
         const uint16_t* xr = x + r * k;

@@ -78,6 +78,20 @@
  *                           always; ties and NaN ordered as stated (partial_sort leaves
  *                           them unspecified) and checked on hand cases; top-1 and top-2
  *                           agree with orc_sample_greedy_bf16.
+ *   orc_det_exp             pinned: within 2 ulp of the correctly rounded exp over a dense
+ *                           sweep of (-86, 0]; exp(0) = 1 exactly; 0 at and below -86.
+ *   orc_sample_stochastic_bf16
+ *                           pinned against oracle/stl_sample_stochastic.cc, a restatement of
+ *                           the reference's host algorithm (std::exp, std::sort,
+ *                           std::partial_sort, std::mt19937_64 and uniform_real_distribution
+ *                           from libstdc++): the same kept sets wherever no two kept/dropped
+ *                           probabilities tie at a filter's boundary, the same token wherever
+ *                           u is not within rounding of a running-sum boundary; the kept set
+ *                           against a float64 numpy sort; the token frequencies against the
+ *                           filtered softmax by a chi-square test; top_k = 1 and tiny
+ *                           temperatures equal the greedy token; the non-finite rows as the
+ *                           reference's arithmetic gives them. The summation orders are the
+ *                           HIP kernels' own (the reference's are not fixed by its contract).
  *   orc_sample_greedy_bf16  pinned: against the definition computed independently with
  *                           numpy (first index of the maximum over non-NaN values, the
  *                           largest other value) on random rows with planted ties, NaN
@@ -136,6 +150,16 @@ void orc_sample_greedy_bf16(const uint16_t* logits, int64_t n, uint32_t* token, 
  * ids/values of the min(k, n) first elements in the order larger value, lower index,
  * NaN last; returns that count, zero-fills ids/values up to k. */
 uint32_t orc_sample_topk_bf16(const uint16_t* logits, int64_t n, uint32_t k, uint32_t* ids, float* values);
+
+/* exp(x) for x <= 0 as the sampling kernels compute it (0 at or below -86). */
+float orc_det_exp(float x);
+
+/* ForwardPass::sample_stochastic's draw (forward.cc:225-301) over one row of vocab bf16
+ * logits with the defined orders of the HIP kernels: token and its logit; *kept (if non-null)
+ * receives the size of the kept prefix (0 for rows drawn without weights). canon is the
+ * uniform in [0, 1) the draw scales by the kept total. */
+void orc_sample_stochastic_bf16(const uint16_t* logits, uint32_t vocab, float inv_temp, float top_p, float min_p,
+                                int32_t top_k, float canon, uint32_t* token, float* logit, uint32_t* kept);
 
 /* orc_qmatmul_mlx_cpu with output rows spread over `threads` OpenMP threads
  * (bit-identical result; the multi-core CPU baseline). */

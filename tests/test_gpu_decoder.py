@@ -393,8 +393,9 @@ def test_wide_query_groups_decode(tmp_path):
 
 def test_sampled_greedy_sidecar_and_contract(tiny, tmp_path):
     """hyp_*_sampled at temperature 0 is the greedy path plus the top-k sidecar
-    (model.cc:262-301); temperature > 0 is UNSUPPORTED; malformed configs, decode before
-    prefill, a second prefill and a foreign state are rejected."""
+    (model.cc:262-301); temperature > 0 draws (its parity is tests/test_gpu_sampling.py's);
+    malformed configs, decode before prefill, a second prefill and a foreign state are
+    rejected."""
     model, T, cfg = tiny
     st = model.kvstate()
     res = hy.StepResult()
@@ -411,8 +412,10 @@ def test_sampled_greedy_sidecar_and_contract(tiny, tmp_path):
     assert e.value.status_name == "INVALID_ARGUMENT"
     f2 = st.decode(2, res, sampling=hy.SamplingConfig(0.0, 0, 0.0, 0.0, 7))
     assert f2.top_k_logprob_count == hy.TOP_K_LOGPROBS
-    for bad, status in ((hy.SamplingConfig(0.7, 0, 0.0, 0.0, 1), "UNSUPPORTED"),
-                        (hy.SamplingConfig(-1.0, 0, 0.0, 0.0, 1), "INVALID_ARGUMENT"),
+    f3 = st.decode(1, res, sampling=hy.SamplingConfig(0.7, 0, 0.0, 0.0, 1))
+    assert f3.token_id < cfg["vocab_size"] and f3.top_k_logprob_count == hy.TOP_K_LOGPROBS
+    assert f3.near_tie_events == 0
+    for bad, status in ((hy.SamplingConfig(-1.0, 0, 0.0, 0.0, 1), "INVALID_ARGUMENT"),
                         (hy.SamplingConfig(0.7, cfg["vocab_size"] + 1, 0.0, 0.0, 1), "INVALID_ARGUMENT"),
                         (hy.SamplingConfig(0.7, 0, 1.5, 0.0, 1), "INVALID_ARGUMENT"),
                         (hy.SamplingConfig(0.7, 0, 0.0, 1.0, 1), "INVALID_ARGUMENT")):
