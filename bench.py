@@ -417,6 +417,20 @@ def bench_sample(stream, steps, warmup):
                         "gbs": round(nbytes / ms / 1e6, 1)})
             log(f"{name} sample rows={rows} vocab={syn.VOCAB}: {ms * 1e3:.2f} us per call")
             res.close()
+        if rows == 1:
+            # the temperature draw (hyp_sample_stochastic) with the top-8 sidecar, one row
+            cfg = hy.SamplingConfig(temperature=0.8, top_k=64, top_p=0.95, min_p=0.05, seed=7)
+            res = hy.DeviceArray((1, 20), np.uint32)
+            with hy.Graph.capture(stream) as graph:
+                for j in range(10):
+                    hy.sample_stochastic(logits, syn.VOCAB, cfg, 7 + j, res, stream)
+            ms = time_launches(stream, lambda _i: graph.launch(stream), steps, warmup) / 10
+            graph.close()
+            out.append({"entry": "stochastic", "rows": 1, "vocab": syn.VOCAB, "us": round(ms * 1e3, 2),
+                        "gbs": round((2 * syn.VOCAB + 80) / ms / 1e6, 1),
+                        "config": "temperature 0.8, top_k 64, top_p 0.95, min_p 0.05"})
+            log(f"stochastic sample rows=1 vocab={syn.VOCAB}: {ms * 1e3:.2f} us per call")
+            res.close()
         logits.close()
     return out
 
