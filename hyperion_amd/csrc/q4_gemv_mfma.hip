@@ -39,15 +39,18 @@
 //    offset is a VGPR, the pair offset a scalar, so addressing costs no VALU.
 //  * A compute unit accepts new loads only as fast as earlier ones return, so the order
 //    of issue decides what arrives first. x is requested first by the waves that stage
-//    it, a raw barrier (no memory wait) puts every weight load of the workgroup behind
-//    those requests, and then each wave issues its weights (all of them when they fit in
-//    two register batches). The staging waves publish x through an LDS counter that the
-//    others poll, so no wave waits for another wave's loads to be issued.
+//    it, then each wave issues its weights (all of them when they fit in two register
+//    batches). In 16-wave workgroups a raw barrier (no memory wait) puts every weight load
+//    of the workgroup behind the x requests and the staging waves publish x through an LDS
+//    counter that the others poll; in smaller workgroups no wave waits before issuing its
+//    weights, and x is published by a barrier the staging waves reach once it is staged.
 #include "common.h"
 #include "kernels.h"
 #include "q4_layout.h"
 #include "q4_rmsnorm.h"
 #include "q4_skinny_core.h"
+
+#include <algorithm>
 
 namespace hyperion::hip {
 namespace {
@@ -146,8 +149,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     const uint32_t nstage = max((min(units, kThreads) + 63u) / 64u, NORM ? static_cast<uint32_t>(M) : 1u);
     const bool stager = wave < nstage;
 
-    // x first: thread u's unit is requested before any weight load of the workgroup. With a
-    // residual (NORM 2) the staging waves instead run the whole prologue before issuing
+    // x first: thread u's unit is requested before its wave's weight loads (with the early
+    // barrier below, before every weight load of the workgroup). With a residual (NORM 2) the staging waves instead run the whole prologue before issuing
     // their weight loads, so that the branch, residual and weight units are never live
     // beside two weight batches (the registers of both would halve the waves per SIMD).
     const uint32_t xu0 = threadIdx.x;   // first (row, group) unit this thread stages
@@ -165,8 +168,21 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     if (threadIdx.x < 8u) ctr[threadIdx.x] = 0u;
     if constexpr (kLaneGroups)
         for (uint32_t t = threadIdx.x; t < WS; t += kThreads) zs[t] = uint4{0u, 0u, 0u, 0u};
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
-    __builtin_amdgcn_s_barrier();         // no memory wait: only orders the issue
+    // Two ways to publish x. 16-wave workgroups (one per compute unit) and the normalising
+    // forms: a raw barrier (no memory wait) right after the x requests puts every weight load
+    // of the workgroup behind them and orders the clearing of the LDS counters, through which
+    // the staging waves then publish x (and the rms statistics) without blocking the others.
+    // Smaller workgroups: no barrier before the weight loads; the staging waves publish x by
+    // arriving at a barrier after staging it, the other waves once their loads are issued.
+    // Measured (cold weights, one process): [15360,3840] in 8-wave workgroups 7.69 against
+    // 7.95 us, o [3840,4096] in 4-wave workgroups 4.30 against 4.63 us, the fused gate/up
+    // 13.74 against 14.39 us; in 16-wave workgroups the early barrier, 8.17 against 8.65 us
+    // (the late barrier waits for the last of 16 waves to issue its loads).
+    constexpr bool kEarly = NORM != 0 || NWAVE >= 16;
+    if constexpr (kEarly) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
+        __builtin_amdgcn_s_barrier();
+    }
 
     const uint32_t c_bytes = tiles * pairs * 1024u;
     const uint32_t s_bytes = tiles * pairs * 128u;
@@ -326,7 +342,7 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
             }
             reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
         }
-        raise_counter(ctr, lane);
+        if constexpr (kEarly) raise_counter(ctr, lane);
     }
     if constexpr (resid) {   // the same loads, after the prologue
         if constexpr (kLaneGroups) {
@@ -343,7 +359,13 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
         for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
     }
-    wait_counter(ctr, nstage);
+    if constexpr (kEarly) {
+        wait_counter(ctr, nstage);
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // x, its sums and the zero row
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
 
     // Opaque VGPR values, so (w & mask) | bits selects v_and_or_b32 (see and_or).
     uint32_t mask = kNibbleMask;
@@ -435,10 +457,34 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
     hipLaunchKernelGGL(kernel, grid, dim3(64 * NWAVE), lds, stream, p);
 }
 
-// Workgroups of 16 waves (16 / splits row tiles each), so that one workgroup per compute
-// unit stages x once; the fused gate/up uses 8 (two workgroups per compute unit, so one
-// streams while the other finishes), and the softcap head, whose grid is many workgroups
-// per compute unit, 4.
+// Waves per workgroup of a plain or normalising launch of `ts` = tiles x splits waves (the
+// fused gate/up runs 8-wave workgroups, the softcap head 4). Measured on the decode shapes of
+// a 12B layer (MI355X, cold weights, every waves x splits pair with the splits of
+// choose_skinny_splits fixed): a workgroup holds the fewest waves that keep the grid at about
+// one workgroup per compute unit or more - [15360,3840] at m = 1 8 waves (7.69 us against
+// 8.17 with 16), o [3840,4096] 4 (4.30 against 5.76 with 16 waves at 16 splits), the
+// normalised q/k/v 8 (7.71 against 9.04; its 16-wave form spills); 16 when the splits need
+// them (down [3840,15360], 16 splits) and for a plain launch of m >= 2 rows whose grid fills
+// the compute units with 16-wave workgroups ([15360,3840] at m = 4: 9.07 against 9.36 us),
+// which stage x once per compute unit.
+uint32_t choose_skinny_waves(uint32_t tiles_total, uint32_t splits, uint32_t m, uint32_t k, int norm) {
+    const uint64_t ts = static_cast<uint64_t>(tiles_total) * splits;
+    const uint64_t cus = device_compute_units();
+    uint32_t w;
+    if (splits >= 16u) {
+        w = 16u;
+    } else if (norm == 0 && m >= 2u && ts >= 16u * cus * 9u / 10u) {
+        w = 16u;
+    } else if (ts >= 8u * cus * 9u / 10u || norm != 0) {
+        w = std::max(splits, 8u);
+    } else {
+        w = std::max(splits, 4u);
+    }
+    // A residual prologue holds every (row, group) unit in one thread.
+    if (norm == 2 && static_cast<uint64_t>(m) * (k / 64u) > 64u * w) w = 16u;
+    return w;
+}
+
 template <int M>
 void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epilogue epi, int norm,
                      hipStream_t stream) {
@@ -447,32 +493,19 @@ void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epi
     } else if (epi == Epilogue::kSoftcap) {
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
     } else {
-        // 16-wave workgroups run one per compute unit: a grid a little over the compute
-        // units (the 12B's global q/k: 544 tiles x 8 splits = 272 workgroups) would run a
-        // second round for its last few. Then 8-wave workgroups, two per compute unit, at
-        // half the splits (the same workgroup count, each wave twice the pairs, still all
-        // in flight at once) take it in one. Not the plain norm form: at 8 waves it takes
-        // 149-163 VGPRs, one workgroup per compute unit.
-        const uint64_t ts = static_cast<uint64_t>(tiles_total) * p.splits;
-        const uint64_t cus = device_compute_units();
-        const uint32_t half = p.splits / 2u;
-        const bool narrow = norm != 1 && (ts + kSkinnyWaves - 1u) / kSkinnyWaves > cus && half >= 1u &&
-                            (p.pairs + half - 1u) / half <= kSkinnyPairsUpFront &&
-                            (ts / 2u + kSkinnyDualWaves - 1u) / kSkinnyDualWaves <= 2u * cus &&
-                            (norm != 2 || static_cast<uint64_t>(M) * (p.k / 64u) <= 64u * kSkinnyDualWaves);
-        SkinnyParams q = p;
-        if (narrow) {
-            q.splits = half;
-            q.split_shift = static_cast<uint32_t>(__builtin_ctz(half));
-        }
+        const uint32_t w = choose_skinny_waves(tiles_total, p.splits, M, p.k, norm);
         if (norm == 2) {
-            narrow ? launch_skinny_t<M, false, 0, kSkinnyDualWaves, 2>(q, tiles_total, stream)
-                   : launch_skinny_t<M, false, 0, kSkinnyWaves, 2>(p, tiles_total, stream);
+            w == 8u ? launch_skinny_t<M, false, 0, 8, 2>(p, tiles_total, stream)
+                    : launch_skinny_t<M, false, 0, 16, 2>(p, tiles_total, stream);
         } else if (norm == 1) {
-            launch_skinny_t<M, false, 0, kSkinnyWaves, 1>(p, tiles_total, stream);
+            w == 8u ? launch_skinny_t<M, false, 0, 8, 1>(p, tiles_total, stream)
+                    : launch_skinny_t<M, false, 0, 16, 1>(p, tiles_total, stream);
+        } else if (w == 4u) {
+            launch_skinny_t<M, false, 0, 4>(p, tiles_total, stream);
+        } else if (w == 8u) {
+            launch_skinny_t<M, false, 0, 8>(p, tiles_total, stream);
         } else {
-            narrow ? launch_skinny_t<M, false, 0, kSkinnyDualWaves>(q, tiles_total, stream)
-                   : launch_skinny_t<M, false, 0, kSkinnyWaves>(p, tiles_total, stream);
+            launch_skinny_t<M, false, 0, 16>(p, tiles_total, stream);
         }
     }
 }
@@ -506,19 +539,15 @@ size_t max_lds_per_block() {
 }  // namespace
 
 uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, SkinnyForm form) {
-    // Measured on the decode shapes of a 12B layer (MI355X, cold weights, every split):
-    //  * plain and grouped launches (16-wave workgroups, S waves share a 16-row tile): the
-    //    smallest power of two that leaves every wave at most kSkinnyPairsUpFront pairs
-    //    (all its loads issued at once), doubled while the grid is short of one workgroup
-    //    per compute unit, up to 16: [15360,3840] 4; q/k/v grouped 8; o, q, k, down 16;
-    //    at m = 4 o and q measured 8 and 16 within 0.4 us of each other, either way round
-    //    on different boxes;
-    //  * the softcap head (262144 rows, 4-wave workgroups, many per compute unit): 1
-    //    (95 vs 100 us at m = 1, 111 vs 123 us at m = 4 with 2);
-    //  * the fused gate/up: the plain rule over its interleaved gate and up tiles (`tiles`
-    //    counts both), at most 4 so that an 8-wave workgroup holds both halves of a row
-    //    tile ([15360,3840]: 1920 tiles, 4 splits, the same as the plain launch of gate or
-    //    up; 8-wave workgroups measured 14.x us against 16.5 with 16 waves at m = 1).
+    // The fewest splits (a power of two) that leave every wave at most kSkinnyPairsUpFront
+    // pairs, all its loads issued at once; doubled only while the launch has fewer than two
+    // waves per compute unit. Measured on the decode shapes of a 12B layer (MI355X, cold
+    // weights, every waves x splits pair): more splits of a short range cost more in x
+    // staging and the split reduction than the extra waves gain - o [3840,4096] 4 splits in
+    // 4-wave workgroups 4.30 us, 16 splits (16 waves) 5.76 us; [15360,3840] 4 (8 waves)
+    // 7.69 us, 8 splits 9.93 us. The softcap head (262144 rows, 4-wave workgroups, many per
+    // compute unit): 1 (95 vs 100 us at m = 1, 111 vs 123 us at m = 4 with 2). The fused
+    // gate/up: at most 4, so that an 8-wave workgroup holds both halves of a row tile.
     (void)m;   // the measured choices did not depend on the row count
     const uint32_t cus = device_compute_units();
     const uint32_t cap = form == SkinnyForm::kDual ? kSkinnyDualWaves / 2u : kSkinnyWaves;
@@ -527,7 +556,7 @@ uint32_t choose_skinny_splits(uint32_t tiles, uint32_t pairs, uint32_t m, Skinny
         s = 1u;
     } else {
         while (s < cap && pairs > s * kSkinnyPairsUpFront) s *= 2u;
-        while (s < cap && tiles * s < static_cast<uint32_t>(kSkinnyWaves) * cus * 9u / 10u && pairs >= 2u * s) s *= 2u;
+        while (s < cap && tiles * s < 2u * cus && pairs >= 2u * s) s *= 2u;
     }
     while (s > 1u && pairs < s) s /= 2u;
     return s;
