@@ -473,6 +473,12 @@ uint32_t choose_skinny_waves(uint32_t tiles_total, uint32_t splits, uint32_t m, 
     uint32_t w;
     if (splits >= 16u) {
         w = 16u;
+    } else if (norm == 2) {
+        // The residual prologue (run by the staging waves before their own weight loads):
+        // one 16-wave workgroup per compute unit when that covers the grid in one round (the
+        // 12B's sliding q/k/v at 8 splits: 10.8 us against 11.6 in 8-wave workgroups at 4),
+        // else 8-wave workgroups.
+        w = ts >= 16u * cus * 9u / 10u && ts <= 16u * cus ? 16u : std::max(splits, 8u);
     } else if (norm == 0 && m >= 2u && ts >= 16u * cus * 9u / 10u) {
         w = 16u;
     } else if (ts >= 8u * cus * 9u / 10u || norm != 0) {
@@ -651,6 +657,10 @@ void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint
     p.eps = norm ? *rms_eps : 0.0f;
     p.norm_w = norm ? norm_w : nullptr;
     p.splits = choose_skinny_splits(tiles_total, p.pairs, m, SkinnyForm::kPlain);
+    if (res != nullptr && p.splits < 16u && p.pairs >= 2u * p.splits &&
+        static_cast<uint64_t>(tiles_total) * 2u * p.splits <= 16ull * device_compute_units()) {
+        p.splits *= 2u;   // the residual form's 16-wave workgroups (choose_skinny_waves)
+    }
     p.split_shift = static_cast<uint32_t>(__builtin_ctz(p.splits));
     set_residual(p, res);
     launch_skinny(p, tiles_total, m, false, Epilogue::kNone, res != nullptr ? 2 : (norm ? 1 : 0), stream);
