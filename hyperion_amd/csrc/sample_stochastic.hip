@@ -23,22 +23,31 @@
 //    present (every logit -inf, or 1/temperature +inf over negative values) its draw total
 //    is 0, u = 0 and it returns index 0; here too.
 //  * exp is det_exp below, the same float operations as the oracle's restatement, so the two
-//    give the same bits. Sums run in defined orders: z = the sum over 16 waves (in order) of
-//    a 64-lane butterfly of per-lane sums over 64 bins (each bin adding count * e); running
-//    sums over bins and tokens go chunk by chunk (a sequential sum within a thread's chunk,
-//    added to the sequential prefix of the earlier chunks).
+//    give the same bits. Sums run in defined orders. The cut: z = the sum over 16 waves (in
+//    order) of a 64-lane butterfly of per-lane sums over 64 bins (each bin adding count * e);
+//    the running probability mass before each of the 1024 threads' 64-bin ranges is a
+//    Hillis-Steele scan within the wave plus the wave totals of the earlier waves added in
+//    order. The draw: the row is cut into chunks of 256 tokens, a wave each, lane l holding
+//    tokens 4l..4l+3; a lane sums its kept weights in token order, a Hillis-Steele scan over
+//    the 64 lanes gives each lane's running sum before it and the chunk total; the chunk
+//    totals are scanned the same way in groups of 64 chunks, the group totals added in order;
+//    the running sum at a token is chunk start + (lanes before + the lane's sum so far).
 //  * The uniform in [0, 1) is std::generate_canonical<float> of std::mt19937_64 (the host
 //    computes it from the request's RNG state, as the reference's uniform_real_distribution
-//    does under libstdc++), and u = sz * it.
+//    does under libstdc++), and u = sz * it, sz the kept total.
 //
-// Three launches per row: a histogram (per workgroup in LDS, two 16-bit counts per word,
-// then added to the global bins; +inf/NaN and -inf logits set bits of a flag word), one
-// workgroup that reads and clears the bins and decides the cut, one workgroup that sums
-// the kept weights in index order and draws. The top-8 logprob sidecar of the pre-filter
-// logits (forward.cc:303-319) is launch_sample_topk's.
+// Seven launches per row, each of them short: a histogram (per workgroup in LDS, two 16-bit
+// counts per word, then added to the global bins; +inf/NaN and -inf logits set bits of a flag
+// word); one workgroup that reads and clears the bins and decides the cut; then, one wave per
+// chunk, the cut bin's tokens per chunk (only when the cut falls inside a bin: its first
+// tokens in index order are kept), each chunk's kept total, one workgroup scanning the chunk
+// totals, one wave per chunk finding its first token whose running sum reaches u (the lowest
+// over the row by an atomic minimum), and one wave writing the token. The top-8 logprob
+// sidecar of the pre-filter logits (forward.cc:303-319) is launch_sample_topk's.
 //
 // Workspace: bins [65536] uint32 and the flag word (zero between launches: the decision
-// clears them), the decision, the parameters (SampleParams).
+// clears them), the decision, the parameters (SampleParams), per-chunk cut counts and totals,
+// per-group cut counts, per-chunk starts, the draw's result word.
 #include <algorithm>
 #include <cstdint>
 
@@ -52,26 +61,55 @@ constexpr uint32_t kBins = 65536;
 constexpr uint32_t kNoBin = kBins;
 constexpr uint32_t kNone = 0xFFFFFFFFu;                // no position: above every index and count
 constexpr uint32_t kMaxVocab = 1u << 23;
-constexpr uint32_t kThreads = 1024;                    // decide and draw: one workgroup
+constexpr uint32_t kThreads = 1024;                    // the decision and the chunk scan: one workgroup
+constexpr uint32_t kWaves = kThreads / 64u;
 constexpr uint32_t kBinsPerThread = kBins / kThreads;  // 64
 constexpr uint32_t kHistThreads = 1024;
 constexpr uint32_t kHistSpan = 8192;                   // tokens per histogram workgroup (< 2^16)
 constexpr uint32_t kHistLds = kBins / 2u * 4u + 16u;   // 128 KB: two 16-bit counts per word; the flags
+constexpr uint32_t kChunk = 256;                       // tokens per chunk: 4 per lane of one wave
+constexpr uint32_t kMaxChunks = kMaxVocab / kChunk;    // 32768
+constexpr uint32_t kMaxGroups = kMaxChunks / 64u;      // 512 groups of 64 chunks
+constexpr uint32_t kChunkWaves = 4;                    // waves (chunks) per workgroup of the chunk kernels
 constexpr size_t kBinsBytes = (kBins + 64u) * 4u;      // the bins, the flag word at [kBins], padding
 constexpr size_t kDecisionOffset = kBinsBytes;
 constexpr size_t kParamsOffset = kDecisionOffset + 256u;
-constexpr size_t kWorkspaceBytes = kParamsOffset + ((sizeof(SampleParams) + 255u) / 256u) * 256u;
+constexpr size_t kParamsBytes = ((sizeof(SampleParams) + 255u) / 256u) * 256u;
+constexpr size_t kCutCountOffset = kParamsOffset + kParamsBytes;          // uint32 [kMaxChunks]
+constexpr size_t kGroupCountOffset = kCutCountOffset + kMaxChunks * 4u;   // uint32 [kMaxGroups]
+constexpr size_t kTotalOffset = kGroupCountOffset + kMaxGroups * 4u;      // float [kMaxChunks]
+constexpr size_t kStartOffset = kTotalOffset + kMaxChunks * 4u;           // float [kMaxChunks]
+constexpr size_t kResultOffset = kStartOffset + kMaxChunks * 4u;          // uint32 (+ padding)
+constexpr size_t kWorkspaceBytes = kResultOffset + 256u;
 
 enum : uint32_t { kDrawKept = 0u, kDrawFirst = 1u, kDrawLast = 2u };
 enum : uint32_t { kFlagInfNan = 1u, kFlagNegInf = 2u };   // bits of the flag word
 
-// The decision of the second launch, read by the third.
+// The decision of the second launch, read by the later ones.
 struct StochDecision {
     float max_t;         // t of the largest finite value
     uint32_t cut_bin;    // bins < cut_bin are kept whole
     uint32_t cut_count;  // and the first cut_count tokens (index order) of bin cut_bin
     uint32_t mode;       // kDrawKept, or a row drawn without weights: index 0 or the last
+    uint32_t partial;    // cut_count is below the cut bin's token count (ranks are needed)
+    float u;             // the draw's target, sz * uniform (written by the chunk scan)
+    float sz;            // the kept total
 };
+
+struct ChunkArrays {
+    uint32_t* cut_count;   // [chunks] tokens of the cut bin per chunk
+    uint32_t* group_count; // [groups] the same per group of 64 chunks
+    float* total;          // [chunks] kept total per chunk
+    float* start;          // [chunks] running sum before each chunk
+    uint32_t* result;      // the lowest drawn index (atomic minimum)
+};
+
+ChunkArrays chunk_arrays(void* workspace) {
+    uint8_t* b = static_cast<uint8_t*>(workspace);
+    return ChunkArrays{reinterpret_cast<uint32_t*>(b + kCutCountOffset), reinterpret_cast<uint32_t*>(b + kGroupCountOffset),
+                       reinterpret_cast<float*>(b + kTotalOffset), reinterpret_cast<float*>(b + kStartOffset),
+                       reinterpret_cast<uint32_t*>(b + kResultOffset)};
+}
 
 __device__ __forceinline__ uint32_t bin_of(uint32_t b) {
     b &= 0xFFFFu;
@@ -114,6 +152,45 @@ __device__ __forceinline__ float butterfly_sum(float v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, m, 64)));
+    return v;
+}
+
+// Inclusive Hillis-Steele scan over the 64 lanes: in step d (1, 2, 4, ..., 32) lane l >= d
+// adds the value lane l - d held before the step (fp32 addition is commutative, so the
+// operand order does not matter).
+__device__ __forceinline__ float hs_scan(float v, uint32_t lane) {
+#pragma unroll
+    for (uint32_t d = 1; d < 64u; d <<= 1) {
+        const float y = __shfl_up(v, d, 64);
+        if (lane >= d) v = v + y;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t hs_scan_u(uint32_t v, uint32_t lane) {
+#pragma unroll
+    for (uint32_t d = 1; d < 64u; d <<= 1) {
+        const uint32_t y = __shfl_up(v, d, 64);
+        if (lane >= d) v += y;
+    }
+    return v;
+}
+
+// The exclusive value of an inclusive scan: lane l - 1's (0 on lane 0).
+__device__ __forceinline__ float exclusive_of(float incl, uint32_t lane) {
+    const float y = __shfl_up(incl, 1u, 64);
+    return lane == 0u ? 0.0f : y;
+}
+
 __global__ __launch_bounds__(kHistThreads) void stoch_hist_kernel(const uint16_t* __restrict__ logits, uint32_t vocab,
                                                                   uint32_t* __restrict__ bins) {
     extern __shared__ __attribute__((aligned(16))) uint32_t h[];
@@ -140,50 +217,46 @@ __global__ __launch_bounds__(kHistThreads) void stoch_hist_kernel(const uint16_t
     if (tid == 0u && h[kBins / 2u] != 0u) atomicOr(&bins[kBins], h[kBins / 2u]);
 }
 
-// Exclusive prefix of a[0..kThreads) in index order by thread 0 (sequential: the defined
-// order of the float sums); a[kThreads] receives the total.
-template <typename T>
-__device__ __forceinline__ void serial_prefix(T* a, uint32_t tid) {
-    __syncthreads();
-    if (tid == 0u) {
-        T run = T(0);
-        for (uint32_t j = 0; j < kThreads; ++j) {
-            const T v = a[j];
-            a[j] = run;
-            run = run + v;
-        }
-        a[kThreads] = run;
-    }
-    __syncthreads();
-}
+// Each thread owns bins [64 tid, 64 tid + 64) and walks them in order once per pass, in
+// batches of kBinBatch counts whose loads are issued together (the bins stay in the caches
+// between passes; holding all 64 in registers across the passes would spill).
+constexpr uint32_t kBinBatch = 32;
 
-// Each thread owns bins [64 tid, 64 tid + 64) and walks them in order once per pass,
-// reading them from device memory (a pass holds 4 at a time; they are cleared after the last
-// pass for the next row).
 template <typename F>
 __device__ __forceinline__ void for_each_bin(const uint32_t* bins, uint32_t d0, F&& f) {
-    const uint4* b4 = reinterpret_cast<const uint4*>(bins + d0);
-    for (uint32_t q = 0; q < kBinsPerThread / 4u; ++q) {
-        const uint4 v = b4[q];
-        f(d0 + 4u * q, v.x);
-        f(d0 + 4u * q + 1u, v.y);
-        f(d0 + 4u * q + 2u, v.z);
-        f(d0 + 4u * q + 3u, v.w);
+#pragma unroll 1
+    for (uint32_t b0 = 0; b0 < kBinsPerThread; b0 += kBinBatch) {
+        uint32_t c[kBinBatch];
+        const uint4* b4 = reinterpret_cast<const uint4*>(bins + d0 + b0);
+#pragma unroll
+        for (uint32_t q = 0; q < kBinBatch / 4u; ++q) {
+            const uint4 v = b4[q];
+            c[4u * q] = v.x;
+            c[4u * q + 1u] = v.y;
+            c[4u * q + 2u] = v.z;
+            c[4u * q + 3u] = v.w;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBinBatch; ++j) f(d0 + b0 + j, c[j]);
     }
 }
 
 __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __restrict__ bins, uint32_t vocab,
                                                                 const SampleParams* __restrict__ prm,
-                                                                StochDecision* __restrict__ dec) {
-    __shared__ float fs[kThreads + 1];
-    __shared__ uint32_t us[kThreads + 1];
-    __shared__ float wz[kThreads / 64u];
+                                                                StochDecision* __restrict__ dec, ChunkArrays ca) {
+    __shared__ float wf[kWaves];
+    __shared__ uint32_t wu[kWaves];
+    __shared__ float wz[kWaves];
     __shared__ uint32_t red;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
     const uint32_t d0 = tid * kBinsPerThread;
     const float inv_temp = prm->inv_temp;
+
+    // The per-group cut counts start at zero and no token is drawn yet.
+    for (uint32_t g = tid; g < kMaxGroups; g += kThreads) ca.group_count[g] = 0u;
+    if (tid == 0u) *ca.result = kNone;
 
     const uint32_t flags = bins[kBins];
     uint32_t first = kNoBin;
@@ -209,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
     if (mode != kDrawKept) {
         __syncthreads();   // every thread has read the flag word
         if (tid == 0u) {
-            *dec = StochDecision{0.0f, 0u, 0u, mode};
+            *dec = StochDecision{0.0f, 0u, 0u, mode, 0u, 0.0f, 0.0f};
             bins[kBins] = 0u;
         }
         uint4* b4 = reinterpret_cast<uint4*>(bins + d0);
@@ -227,25 +300,39 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
     if (lane == 0u) wz[wave] = zw;
     __syncthreads();
     float z = 0.0f;
-    for (uint32_t w = 0; w < kThreads / 64u; ++w) z = z + wz[w];
+    for (uint32_t w = 0; w < kWaves; ++w) z = z + wz[w];
 
-    // Counts and probability masses before each thread's bins.
+    // Counts and probability masses before each thread's bins: a scan within the wave, the
+    // earlier waves' totals added in order.
     float pl = 0.0f;
     for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
         if (c != 0u) pl = pl + static_cast<float>(c) * (weight(d) / z);
     });
-    fs[tid] = pl;
-    us[tid] = total_l;
-    serial_prefix(fs, tid);
-    serial_prefix(us, tid);
-    const uint32_t total = us[kThreads];
-    const uint32_t before = us[tid];
+    const float pincl = hs_scan(pl, lane);
+    const float pexcl = exclusive_of(pincl, lane);
+    const uint32_t uincl = hs_scan_u(total_l, lane);
+    if (lane == 63u) {
+        wf[wave] = pincl;
+        wu[wave] = uincl;
+    }
+    __syncthreads();
+    float off = 0.0f;
+    uint32_t uoff = 0u;
+    uint32_t total = 0u;
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        if (w < wave) {
+            off = off + wf[w];
+            uoff += wu[w];
+        }
+        total += wu[w];
+    }
+    const float start = off + pexcl;
+    const uint32_t before = uoff + uincl - total_l;
 
     // top-p: the first position (in the order) whose running mass reaches top_p.
     uint32_t np = total;
     const float top_p = prm->top_p;
     if (top_p > 0.0f && top_p <= 1.0f) {   // uniform
-        const float start = fs[tid];
         float part = 0.0f;
         uint32_t seen = before;
         uint32_t cand = kNone;
@@ -296,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
         bool done = false;
         for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
             if (!done && seen + c >= n) {
-                *dec = StochDecision{max_t, d, n - seen, kDrawKept};
+                *dec = StochDecision{max_t, d, n - seen, kDrawKept, n - seen < c ? 1u : 0u, 0.0f, 0.0f};
                 done = true;
             }
             seen += c;
@@ -309,89 +396,181 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
     for (uint32_t q = 0; q < kBinsPerThread / 4u; ++q) b4[q] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-__device__ __forceinline__ float kept_weight(uint32_t d, uint32_t& rank, const StochDecision& dc, float x,
-                                             float inv_temp) {
-    const bool keep = d < dc.cut_bin || (d == dc.cut_bin && rank++ < dc.cut_count);
-    return keep ? det_exp(x * inv_temp - dc.max_t) : -1.0f;
+// Tokens of the cut bin per chunk (and per group of 64 chunks), when the cut falls inside
+// the bin. One wave per chunk.
+__global__ __launch_bounds__(64 * kChunkWaves) void stoch_count_kernel(const uint16_t* __restrict__ logits,
+                                                                       uint32_t vocab,
+                                                                       const StochDecision* __restrict__ dec,
+                                                                       ChunkArrays ca) {
+    const StochDecision dc = *dec;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = blockIdx.x * kChunkWaves + (threadIdx.x >> 6);
+    if (dc.mode != kDrawKept || dc.partial == 0u || c * kChunk >= vocab) return;   // wave-uniform
+    uint32_t n = 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        const uint32_t i = c * kChunk + 4u * lane + k;
+        if (i < vocab && bin_of(logits[i]) == dc.cut_bin) ++n;
+    }
+    n = wave_sum_u(n);
+    if (lane == 0u) {
+        ca.cut_count[c] = n;
+        if (n != 0u) atomicAdd(&ca.group_count[c >> 6], n);
+    }
 }
 
-__global__ __launch_bounds__(kThreads) void stoch_draw_kernel(const uint16_t* __restrict__ logits, uint32_t vocab,
-                                                              SampleParams* __restrict__ prm,
-                                                              const StochDecision* __restrict__ dec,
-                                                              HypTopKSample* __restrict__ out) {
-    __shared__ float fs[kThreads + 1];
-    __shared__ uint32_t us[kThreads + 1];
-    __shared__ uint32_t red;
-    const uint32_t tid = threadIdx.x;
-    const StochDecision dc = *dec;
-    const uint32_t step = prm->step;
-    const uint32_t nu = min(max(prm->n_uniform, 1u), kMaxSampledSteps);
-    const float canon = prm->uniform[min(step, nu - 1u)];
-    const float inv_temp = prm->inv_temp;
-    __syncthreads();
-    if (tid == 0u) prm->step = step + 1u;
-    if (dc.mode != kDrawKept || vocab == 0u) {
-        if (tid == 0u) {
-            const uint32_t arg = dc.mode == kDrawLast && vocab != 0u ? vocab - 1u : 0u;
-            out->token_id = arg;
-            out->logit = vocab != 0u ? __uint_as_float(static_cast<uint32_t>(logits[arg]) << 16) : -__builtin_huge_valf();
-            out->near_tie = 0u;
-        }
-        return;
-    }
-    const uint32_t chunk = (vocab + kThreads - 1u) / kThreads;
-    const uint32_t begin = min(vocab, tid * chunk);
-    const uint32_t end = min(vocab, begin + chunk);
+// One chunk's tokens as one wave sees them: lane l holds tokens 4l..4l+3; kept[k] and the
+// kept weights w[k], and the lane's sum of its kept weights in token order.
+struct ChunkLane {
+    float w[4];
+    bool kept[4];
+    float sum;
+};
 
-    // Ranks of the cut bin's tokens before this chunk.
+__device__ __forceinline__ ChunkLane chunk_lane(const uint16_t* __restrict__ logits, uint32_t vocab, uint32_t c,
+                                                uint32_t lane, const StochDecision& dc, float inv_temp,
+                                                const ChunkArrays& ca) {
+    uint32_t d[4];
+    float x[4];
     uint32_t ncut = 0u;
-    for (uint32_t i = begin; i < end; ++i) ncut += bin_of(logits[i]) == dc.cut_bin ? 1u : 0u;
-    us[tid] = ncut;
-    serial_prefix(us, tid);
-    const uint32_t rank0 = us[tid];
-
-    // Kept weight of the chunk in index order, then the prefix over chunks.
-    float s = 0.0f;
-    uint32_t rank = rank0;
-    for (uint32_t i = begin; i < end; ++i) {
-        const uint32_t bits = logits[i];
-        const float w = kept_weight(bin_of(bits), rank, dc, __uint_as_float(bits << 16), inv_temp);
-        if (w >= 0.0f) s = s + w;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        const uint32_t i = c * kChunk + 4u * lane + k;
+        const uint32_t bits = i < vocab ? logits[i] : 0xFF80u;   // past the row: no token (-inf)
+        d[k] = i < vocab ? bin_of(bits) : kNoBin;
+        x[k] = __uint_as_float(bits << 16);
+        ncut += d[k] == dc.cut_bin ? 1u : 0u;
     }
-    fs[tid] = s;
-    serial_prefix(fs, tid);
-    const float sz = fs[kThreads];
-    const float u = sz * canon + 0.0f;   // uniform_real_distribution<float>(0, sz)
-
-    // The first index whose running sum reaches u.
-    uint32_t cand = kNone;   // above any index
-    if (u <= 0.0f) {
-        cand = 0u;
-    } else {
-        const float start = fs[tid];
-        float part = 0.0f;
-        rank = rank0;
-        for (uint32_t i = begin; i < end; ++i) {
-            const uint32_t bits = logits[i];
-            const float w = kept_weight(bin_of(bits), rank, dc, __uint_as_float(bits << 16), inv_temp);
-            if (w < 0.0f) continue;
-            part = part + w;
-            if (u <= start + part) {
-                cand = i;
-                break;
-            }
-        }
+    // The rank (index order) of this lane's first cut-bin token among the row's cut-bin tokens.
+    uint32_t rank = 0u;
+    if (dc.partial != 0u) {   // uniform
+        const uint32_t g = c >> 6;
+        uint32_t before = 0u;
+        for (uint32_t j = lane; j < g; j += 64u) before += ca.group_count[j];
+        for (uint32_t j = 64u * g + lane; j < c; j += 64u) before += ca.cut_count[j];
+        rank = wave_sum_u(before) + hs_scan_u(ncut, lane) - ncut;
     }
-    if (tid == 0u) red = kNone;
-    __syncthreads();
-    atomicMin(&red, cand);
+    ChunkLane r;
+    r.sum = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        const bool cut = d[k] == dc.cut_bin;
+        r.kept[k] = d[k] < dc.cut_bin || (cut && (dc.partial == 0u || rank < dc.cut_count));
+        rank += cut ? 1u : 0u;
+        r.w[k] = r.kept[k] ? det_exp(x[k] * inv_temp - dc.max_t) : 0.0f;
+        if (r.kept[k]) r.sum = r.sum + r.w[k];
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(64 * kChunkWaves) void stoch_chunk_kernel(const uint16_t* __restrict__ logits,
+                                                                       uint32_t vocab,
+                                                                       const SampleParams* __restrict__ prm,
+                                                                       const StochDecision* __restrict__ dec,
+                                                                       ChunkArrays ca) {
+    const StochDecision dc = *dec;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = blockIdx.x * kChunkWaves + (threadIdx.x >> 6);
+    if (dc.mode != kDrawKept || c * kChunk >= vocab) return;   // wave-uniform
+    const ChunkLane cl = chunk_lane(logits, vocab, c, lane, dc, prm->inv_temp, ca);
+    const float incl = hs_scan(cl.sum, lane);
+    if (lane == 63u) ca.total[c] = incl;
+}
+
+// The running sum before each chunk: groups of 64 chunks scanned by a wave each, the group
+// totals added in order; the kept total sz and u = sz * uniform into the decision.
+__global__ __launch_bounds__(kThreads) void stoch_scan_kernel(uint32_t vocab, SampleParams* __restrict__ prm,
+                                                              StochDecision* __restrict__ dec, ChunkArrays ca) {
+    __shared__ float gt[kMaxGroups];
+    __shared__ float gs[kMaxGroups + 1];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    if (dec->mode != kDrawKept) return;   // uniform
+    const uint32_t chunks = (vocab + kChunk - 1u) / kChunk;
+    const uint32_t groups = (chunks + 63u) / 64u;
+    for (uint32_t g = wave; g < groups; g += kWaves) {
+        const uint32_t c = 64u * g + lane;
+        const float incl = hs_scan(c < chunks ? ca.total[c] : 0.0f, lane);
+        const float excl = exclusive_of(incl, lane);
+        if (c < chunks) ca.start[c] = excl;
+        if (lane == 63u) gt[g] = incl;
+    }
     __syncthreads();
     if (tid == 0u) {
-        const uint32_t arg = red < vocab ? red : vocab - 1u;   // the reference's fallback: the last index
-        out->token_id = arg;
-        out->logit = __uint_as_float(static_cast<uint32_t>(logits[arg]) << 16);
-        out->near_tie = 0u;
+        float run = 0.0f;
+        for (uint32_t g = 0; g < groups; ++g) {
+            gs[g] = run;
+            run = run + gt[g];
+        }
+        gs[groups] = run;
     }
+    __syncthreads();
+    // Each wave adds its own groups' starts (the lanes that wrote them).
+    for (uint32_t g = wave; g < groups; g += kWaves) {
+        const uint32_t c = 64u * g + lane;
+        if (c < chunks) ca.start[c] = gs[g] + ca.start[c];
+    }
+    if (tid == 0u) {
+        const uint32_t step = prm->step;
+        const uint32_t nu = min(max(prm->n_uniform, 1u), kMaxSampledSteps);
+        const float canon = prm->uniform[min(step, nu - 1u)];
+        const float sz = gs[groups];
+        dec->sz = sz;
+        dec->u = sz * canon + 0.0f;   // uniform_real_distribution<float>(0, sz)
+    }
+}
+
+// Each chunk's first kept token whose running sum reaches u; the lowest index over the row.
+__global__ __launch_bounds__(64 * kChunkWaves) void stoch_find_kernel(const uint16_t* __restrict__ logits,
+                                                                      uint32_t vocab,
+                                                                      const SampleParams* __restrict__ prm,
+                                                                      const StochDecision* __restrict__ dec,
+                                                                      ChunkArrays ca) {
+    const StochDecision dc = *dec;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = blockIdx.x * kChunkWaves + (threadIdx.x >> 6);
+    if (dc.mode != kDrawKept || c * kChunk >= vocab) return;   // wave-uniform
+    if (!(dc.u > 0.0f)) {   // u <= 0 (or NaN: no running sum reaches it, the last index)
+        if (c == 0u && lane == 0u && dc.u <= 0.0f) atomicMin(ca.result, 0u);
+        return;
+    }
+    const ChunkLane cl = chunk_lane(logits, vocab, c, lane, dc, prm->inv_temp, ca);
+    const float incl = hs_scan(cl.sum, lane);
+    const float before = exclusive_of(incl, lane);
+    const float sc = ca.start[c];
+    uint32_t cand = kNone;
+    float part = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        if (!cl.kept[k] || cand != kNone) continue;
+        part = part + cl.w[k];
+        if (dc.u <= sc + (before + part)) cand = c * kChunk + 4u * lane + k;
+    }
+    cand = wave_min_u(cand);
+    if (lane == 0u && cand != kNone) atomicMin(ca.result, cand);
+}
+
+// The drawn token (the reference's fallback, the last index, when no running sum reached u)
+// and the next step's uniform.
+__global__ __launch_bounds__(64) void stoch_final_kernel(const uint16_t* __restrict__ logits, uint32_t vocab,
+                                                         SampleParams* __restrict__ prm,
+                                                         const StochDecision* __restrict__ dec, ChunkArrays ca,
+                                                         HypTopKSample* __restrict__ out) {
+    if (threadIdx.x != 0u) return;
+    const StochDecision dc = *dec;
+    prm->step = prm->step + 1u;
+    uint32_t arg;
+    if (dc.mode != kDrawKept || vocab == 0u) {
+        arg = dc.mode == kDrawLast && vocab != 0u ? vocab - 1u : 0u;
+    } else {
+        const uint32_t r = *ca.result;
+        arg = r < vocab ? r : vocab - 1u;
+    }
+    out->token_id = arg;
+    out->logit = vocab != 0u ? __uint_as_float(static_cast<uint32_t>(logits[arg]) << 16) : -__builtin_huge_valf();
+    out->near_tie = 0u;
+    *ca.result = kNone;
 }
 
 }  // namespace
@@ -438,7 +617,9 @@ void launch_sample_stochastic(const uint16_t* logits, uint32_t vocab, void* work
     HYP_REQUIRE(vocab <= kMaxVocab, HYP_STATUS_INVALID_ARGUMENT, "sample_stochastic: vocab must be at most 2^23");
     uint32_t* bins = static_cast<uint32_t*>(workspace);
     auto* dec = reinterpret_cast<StochDecision*>(static_cast<uint8_t*>(workspace) + kDecisionOffset);
+    static_assert(sizeof(StochDecision) <= 256u, "decision slot");
     SampleParams* params = sample_stochastic_params(workspace);
+    const ChunkArrays ca = chunk_arrays(workspace);
     static thread_local int configured_device = -1;
     int dev = 0;
     HYP_HIP_CHECK(hipGetDevice(&dev));
@@ -452,9 +633,23 @@ void launch_sample_stochastic(const uint16_t* logits, uint32_t vocab, void* work
         hipLaunchKernelGGL(stoch_hist_kernel, dim3(groups), dim3(kHistThreads), kHistLds, stream, logits, vocab, bins);
         HYP_HIP_CHECK(hipGetLastError());
     }
-    hipLaunchKernelGGL(stoch_decide_kernel, dim3(1), dim3(kThreads), 0, stream, bins, vocab, params, dec);
+    hipLaunchKernelGGL(stoch_decide_kernel, dim3(1), dim3(kThreads), 0, stream, bins, vocab, params, dec, ca);
     HYP_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(stoch_draw_kernel, dim3(1), dim3(kThreads), 0, stream, logits, vocab, params, dec, out);
+    if (vocab != 0u) {
+        const uint32_t chunks = (vocab + kChunk - 1u) / kChunk;
+        const dim3 grid((chunks + kChunkWaves - 1u) / kChunkWaves);
+        hipLaunchKernelGGL(stoch_count_kernel, grid, dim3(64 * kChunkWaves), 0, stream, logits, vocab, dec, ca);
+        HYP_HIP_CHECK(hipGetLastError());
+        hipLaunchKernelGGL(stoch_chunk_kernel, grid, dim3(64 * kChunkWaves), 0, stream, logits, vocab, params, dec,
+                           ca);
+        HYP_HIP_CHECK(hipGetLastError());
+        hipLaunchKernelGGL(stoch_scan_kernel, dim3(1), dim3(kThreads), 0, stream, vocab, params, dec, ca);
+        HYP_HIP_CHECK(hipGetLastError());
+        hipLaunchKernelGGL(stoch_find_kernel, grid, dim3(64 * kChunkWaves), 0, stream, logits, vocab, params, dec,
+                           ca);
+        HYP_HIP_CHECK(hipGetLastError());
+    }
+    hipLaunchKernelGGL(stoch_final_kernel, dim3(1), dim3(64), 0, stream, logits, vocab, params, dec, ca, out);
     HYP_HIP_CHECK(hipGetLastError());
 }
 

@@ -417,8 +417,13 @@ static float butterfly64(float* v) {
  *     every filter keeps a prefix of (value descending, index ascending);
  *   - exp is st_exp below (the same fp32 operations as the device);
  *   - z = 16 waves (in order) of a 64-lane xor butterfly of per-lane sequential sums over 64
- *     bins; running sums over bins and tokens: a sequential sum within each of 1024 chunks
- *     added to the sequential exclusive prefix of the chunk totals;
+ *     bins; the running mass before each of 1024 threads' 64-bin ranges: a Hillis-Steele
+ *     scan within each wave of 64 threads plus the earlier waves' totals added in order;
+ *   - the draw: chunks of 256 tokens, 4 per lane of a 64-lane wave; a lane's kept weights
+ *     summed in token order, a Hillis-Steele scan over the lanes (the chunk total is its last
+ *     lane), the chunk totals scanned the same way in groups of 64 chunks with the group
+ *     totals added in order; the running sum at a token is chunk start + (lanes before + the
+ *     lane's sum so far), and the token is the lowest index whose running sum reaches u;
  *   - rows whose scaled logits hold +inf or NaN draw the last index, rows with no finite
  *     scaled logit (and none of those) draw index 0 - what the reference's arithmetic gives.
  * canon is the uniform in [0, 1) (std::generate_canonical<float> of std::mt19937_64 seeded
@@ -469,14 +474,28 @@ static float st_weight(uint32_t d, float inv_temp, float max_t) {
     return orc_det_exp(st_bin_value(d) * inv_temp - max_t);
 }
 
-static void st_prefix_f(float* a) {   /* exclusive, sequential; a[ST_THREADS] = total */
-    float run = 0.0f;
-    for (uint32_t j = 0; j < ST_THREADS; ++j) {
-        const float v = a[j];
-        a[j] = run;
-        run = run + v;
+/* Inclusive Hillis-Steele scan of 64 lanes: in step d (1, 2, 4, ..., 32) lane l >= d adds the
+ * value lane l - d held before the step. */
+static void st_hs_scan64(float* v) {
+    for (uint32_t d = 1u; d < 64u; d <<= 1) {
+        float t[64];
+        for (uint32_t l = 0; l < 64u; ++l) t[l] = l >= d ? v[l] + v[l - d] : v[l];
+        memcpy(v, t, sizeof(t));
     }
-    a[ST_THREADS] = run;
+}
+
+/* Exclusive prefix over the 1024 threads' values: the scan within each wave of 64, plus the
+ * earlier waves' totals added in order; a[ST_THREADS] = the total. */
+static void st_prefix_f(float* a) {
+    float off = 0.0f;
+    for (uint32_t w = 0; w < ST_THREADS / 64u; ++w) {
+        float v[64];
+        memcpy(v, a + 64u * w, sizeof(v));
+        st_hs_scan64(v);
+        for (uint32_t l = 0; l < 64u; ++l) a[64u * w + l] = off + (l != 0u ? v[l - 1u] : 0.0f);
+        off = off + v[63];
+    }
+    a[ST_THREADS] = off;
 }
 
 static void st_prefix_u(uint32_t* a) {
@@ -606,55 +625,65 @@ void orc_sample_stochastic_bf16(const uint16_t* logits, uint32_t vocab, float in
     free(cnt);
     if (kept) *kept = n;
 
-    /* The draw: chunk t of ceil(vocab / 1024) tokens; the cut bin's ranks before each chunk;
-     * kept weights summed per chunk, then the exclusive prefix over chunks. */
-    const uint32_t chunk = (vocab + ST_THREADS - 1u) / ST_THREADS;
-    uint32_t rank0[ST_THREADS + 1];
-    for (uint32_t t = 0; t < ST_THREADS; ++t) {
-        const uint32_t b = t * chunk < vocab ? t * chunk : vocab;
-        const uint32_t e = b + chunk < vocab ? b + chunk : vocab;
-        uint32_t c = 0u;
-        for (uint32_t i = b; i < e; ++i) c += st_bin_of(logits[i]) == cut_bin ? 1u : 0u;
-        rank0[t] = c;
+    /* The draw over chunks of 256 tokens (lane l of a chunk: its tokens 4l..4l+3). kept(i):
+     * bin < cut_bin, or the cut bin within its first cut_count tokens in index order. */
+#define ST_CHUNK 256u
+    const uint32_t chunks = (vocab + ST_CHUNK - 1u) / ST_CHUNK;
+    const uint32_t groups = (chunks + 63u) / 64u;
+    float* wt = (float*)malloc(sizeof(float) * (size_t)chunks * ST_CHUNK);   /* kept weight or -1 */
+    uint32_t cut_seen = 0u;
+    for (uint32_t i = 0; i < chunks * ST_CHUNK; ++i) {
+        wt[i] = -1.0f;
+        if (i >= vocab) continue;
+        const uint32_t d = st_bin_of(logits[i]);
+        const int keep = d < cut_bin || (d == cut_bin && cut_seen < cut_count);
+        if (d == cut_bin) cut_seen += 1u;
+        if (keep) wt[i] = orc_det_exp(orc_f32_from_bf16(logits[i]) * inv_temp - max_t);
     }
-    st_prefix_u(rank0);
-#define ST_KEPT(d, rank) ((d) < cut_bin || ((d) == cut_bin && (rank)++ < cut_count))
-    for (uint32_t t = 0; t < ST_THREADS; ++t) {
-        const uint32_t b = t * chunk < vocab ? t * chunk : vocab;
-        const uint32_t e = b + chunk < vocab ? b + chunk : vocab;
-        float sum = 0.0f;
-        uint32_t rank = rank0[t];
-        for (uint32_t i = b; i < e; ++i) {
-            const uint32_t d = st_bin_of(logits[i]);
-            if (ST_KEPT(d, rank)) sum = sum + orc_det_exp(orc_f32_from_bf16(logits[i]) * inv_temp - max_t);
+    float* before = (float*)malloc(sizeof(float) * (size_t)chunks * 64u);   /* lane sums before */
+    float* start = (float*)calloc((size_t)groups * 64u, sizeof(float));
+    for (uint32_t c = 0; c < chunks; ++c) {
+        float v[64];
+        for (uint32_t l = 0; l < 64u; ++l) {
+            float sum = 0.0f;
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const float w = wt[c * ST_CHUNK + 4u * l + k];
+                if (w >= 0.0f) sum = sum + w;
+            }
+            v[l] = sum;
         }
-        fs[t] = sum;
+        st_hs_scan64(v);
+        for (uint32_t l = 0; l < 64u; ++l) before[c * 64u + l] = l != 0u ? v[l - 1u] : 0.0f;
+        start[c] = v[63];   /* the chunk total, replaced by its start below */
     }
-    st_prefix_f(fs);
-    const float sz = fs[ST_THREADS];
+    float run = 0.0f;
+    for (uint32_t g = 0; g < groups; ++g) {
+        float v[64];
+        memcpy(v, start + 64u * g, sizeof(v));   /* chunks past the row hold 0 */
+        st_hs_scan64(v);
+        for (uint32_t l = 0; l < 64u; ++l) start[64u * g + l] = run + (l != 0u ? v[l - 1u] : 0.0f);
+        run = run + v[63];
+    }
+    const float sz = run;
     const float u = sz * canon + 0.0f;
     uint32_t arg = ST_NONE;
     if (u <= 0.0f) {
         arg = 0u;
     } else {
-        for (uint32_t t = 0; t < ST_THREADS && arg == ST_NONE; ++t) {
-            const uint32_t b = t * chunk < vocab ? t * chunk : vocab;
-            const uint32_t e = b + chunk < vocab ? b + chunk : vocab;
-            const float start = fs[t];
+        for (uint32_t i = 0; i < vocab && arg == ST_NONE; ++i) {
+            const float w = wt[i];
+            if (w < 0.0f) continue;
+            const uint32_t c = i / ST_CHUNK, l = (i % ST_CHUNK) / 4u;
             float part = 0.0f;
-            uint32_t rank = rank0[t];
-            for (uint32_t i = b; i < e; ++i) {
-                const uint32_t d = st_bin_of(logits[i]);
-                if (!ST_KEPT(d, rank)) continue;
-                part = part + orc_det_exp(orc_f32_from_bf16(logits[i]) * inv_temp - max_t);
-                if (u <= start + part) {
-                    arg = i;
-                    break;
-                }
-            }
+            for (uint32_t j = c * ST_CHUNK + 4u * l; j <= i; ++j)
+                if (wt[j] >= 0.0f) part = part + wt[j];
+            if (u <= start[c] + (before[c * 64u + l] + part)) arg = i;
         }
     }
-#undef ST_KEPT
+#undef ST_CHUNK
+    free(wt);
+    free(before);
+    free(start);
     if (arg >= vocab) arg = vocab - 1u;
     *token = arg;
     *logit = orc_f32_from_bf16(logits[arg]);
