@@ -23,11 +23,12 @@
 //    present (every logit -inf, or 1/temperature +inf over negative values) its draw total
 //    is 0, u = 0 and it returns index 0; here too.
 //  * exp is det_exp below, the same float operations as the oracle's restatement, so the two
-//    give the same bits. Sums run in defined orders. The cut: z = the sum over 16 waves (in
-//    order) of a 64-lane butterfly of per-lane sums over 64 bins (each bin adding count * e);
-//    the running probability mass before each of the 1024 threads' 64-bin ranges is a
-//    Hillis-Steele scan within the wave plus the wave totals of the earlier waves added in
-//    order. The draw: the row is cut into chunks of 256 tokens, a wave each, lane l holding
+//    give the same bits. Sums run in defined orders. The cut, over 1024 blocks of 64 bins
+//    (wave w of 16 taking blocks 16 i + w): z = the 16 waves' sums in order, each adding in
+//    order the 64-lane butterflies of count * e over its blocks; the probability mass before
+//    a bin = its block's start (the blocks' masses, each a Hillis-Steele scan over its bins,
+//    scanned in block order: within waves of 64 blocks, plus the earlier waves' totals in
+//    order) + the scan of its block's masses before it. The draw: the row is cut into chunks of 256 tokens, a wave each, lane l holding
 //    tokens 4l..4l+3; a lane sums its kept weights in token order, a Hillis-Steele scan over
 //    the 64 lanes gives each lane's running sum before it and the chunk total; the chunk
 //    totals are scanned the same way in groups of 64 chunks, the group totals added in order;
@@ -38,16 +39,17 @@
 //
 // Seven launches per row, each of them short: a histogram (per workgroup in LDS, two 16-bit
 // counts per word, then added to the global bins; +inf/NaN and -inf logits set bits of a flag
-// word); one workgroup that reads and clears the bins and decides the cut; then, one wave per
+// word); one workgroup that reads the bins into LDS, decides the cut and clears them; then, one wave per
 // chunk, the cut bin's tokens per chunk (only when the cut falls inside a bin: its first
 // tokens in index order are kept), each chunk's kept total, one workgroup scanning the chunk
 // totals, one wave per chunk finding its first token whose running sum reaches u (the lowest
 // over the row by an atomic minimum), and one wave writing the token. The top-8 logprob
 // sidecar of the pre-filter logits (forward.cc:303-319) is launch_sample_topk's.
 //
-// Workspace: bins [65536] uint32 and the flag word (zero between launches: the decision
-// clears them), the decision, the parameters (SampleParams), per-chunk cut counts and totals,
-// per-group cut counts, per-chunk starts, the draw's result word.
+// Workspace: bins [65536] uint32, the flag word and the totals of the 1024 blocks of 64 bins
+// (zero between launches: the decision clears them), the decision, the parameters
+// (SampleParams), per-chunk cut counts and totals, per-group cut counts, per-chunk starts,
+// the draw's result word.
 #include <algorithm>
 #include <cstdint>
 
@@ -63,7 +65,6 @@ constexpr uint32_t kNone = 0xFFFFFFFFu;                // no position: above eve
 constexpr uint32_t kMaxVocab = 1u << 23;
 constexpr uint32_t kThreads = 1024;                    // the decision and the chunk scan: one workgroup
 constexpr uint32_t kWaves = kThreads / 64u;
-constexpr uint32_t kBinsPerThread = kBins / kThreads;  // 64
 constexpr uint32_t kHistThreads = 1024;
 constexpr uint32_t kHistSpan = 8192;                   // tokens per histogram workgroup (< 2^16)
 constexpr uint32_t kHistLds = kBins / 2u * 4u + 16u;   // 128 KB: two 16-bit counts per word; the flags
@@ -80,7 +81,8 @@ constexpr size_t kGroupCountOffset = kCutCountOffset + kMaxChunks * 4u;   // uin
 constexpr size_t kTotalOffset = kGroupCountOffset + kMaxGroups * 4u;      // float [kMaxChunks]
 constexpr size_t kStartOffset = kTotalOffset + kMaxChunks * 4u;           // float [kMaxChunks]
 constexpr size_t kResultOffset = kStartOffset + kMaxChunks * 4u;          // uint32 (+ padding)
-constexpr size_t kWorkspaceBytes = kResultOffset + 256u;
+constexpr size_t kBlockTotalOffset = kResultOffset + 256u;                // uint32 [kBins / 64]
+constexpr size_t kWorkspaceBytes = kBlockTotalOffset + (kBins / 64u) * 4u;
 
 enum : uint32_t { kDrawKept = 0u, kDrawFirst = 1u, kDrawLast = 2u };
 enum : uint32_t { kFlagInfNan = 1u, kFlagNegInf = 2u };   // bits of the flag word
@@ -191,10 +193,13 @@ __device__ __forceinline__ float exclusive_of(float incl, uint32_t lane) {
     return lane == 0u ? 0.0f : y;
 }
 
+// Block totals too (blocks of 64 bins): a wave's 64 words cover two blocks, one per half.
 __global__ __launch_bounds__(kHistThreads) void stoch_hist_kernel(const uint16_t* __restrict__ logits, uint32_t vocab,
-                                                                  uint32_t* __restrict__ bins) {
+                                                                  uint32_t* __restrict__ bins,
+                                                                  uint32_t* __restrict__ block_total) {
     extern __shared__ __attribute__((aligned(16))) uint32_t h[];
     const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
     for (uint32_t w = tid; w <= kBins / 2u; w += kHistThreads) h[w] = 0u;   // h[kBins / 2]: the flags
     __syncthreads();
     const uint32_t begin = blockIdx.x * kHistSpan;
@@ -209,65 +214,98 @@ __global__ __launch_bounds__(kHistThreads) void stoch_hist_kernel(const uint16_t
         }
     }
     __syncthreads();
-    for (uint32_t w = tid; w < kBins / 2u; w += kHistThreads) {
+    for (uint32_t w = tid; w < kBins / 2u; w += kHistThreads) {   // w = 64 j + lane: blocks 2j, 2j + 1
         const uint32_t v = h[w];
         if (v & 0xFFFFu) atomicAdd(&bins[2u * w], v & 0xFFFFu);
         if (v >> 16) atomicAdd(&bins[2u * w + 1u], v >> 16);
+        uint32_t t = (v & 0xFFFFu) + (v >> 16);
+        if (__any(t != 0u)) {
+#pragma unroll
+            for (int m = 16; m > 0; m >>= 1) t += __shfl_xor(t, m, 64);   // within each half
+            if ((lane & 31u) == 0u && t != 0u) atomicAdd(&block_total[w >> 5], t);
+        }
     }
     if (tid == 0u && h[kBins / 2u] != 0u) atomicOr(&bins[kBins], h[kBins / 2u]);
 }
 
-// Each thread owns bins [64 tid, 64 tid + 64) and walks them in order once per pass, in
-// batches of kBinBatch counts whose loads are issued together (the bins stay in the caches
-// between passes; holding all 64 in registers across the passes would spill).
-constexpr uint32_t kBinBatch = 32;
+// The decision runs over 1024 blocks of 64 bins, lane l of a wave holding bin 64 b + l of
+// block b; wave w takes blocks 16 i + w (i = 0..63), so the blocks a row's values occupy
+// (usually a few dozen neighbours) spread over all 16 waves. The histogram's block totals
+// give each wave the mask of its non-empty blocks, which are the only ones it reads and
+// visits; their counts go to LDS as 16-bit values (65535 standing for "read the count from
+// device memory", a bin holding 65535 tokens or more).
+constexpr uint32_t kBlocks = kBins / 64u;               // 1024
+constexpr uint32_t kSat = 0xFFFFu;
+constexpr uint32_t kDecideLds = kBins * 2u + 4u * kBlocks * 4u;   // counts, totals, masses, two starts
 
+__device__ __forceinline__ uint32_t block_of(uint32_t i, uint32_t wave) { return kWaves * i + wave; }
+
+// Visit the set bits i of a wave-uniform 64-bit mask in increasing order.
 template <typename F>
-__device__ __forceinline__ void for_each_bin(const uint32_t* bins, uint32_t d0, F&& f) {
-#pragma unroll 1
-    for (uint32_t b0 = 0; b0 < kBinsPerThread; b0 += kBinBatch) {
-        uint32_t c[kBinBatch];
-        const uint4* b4 = reinterpret_cast<const uint4*>(bins + d0 + b0);
-#pragma unroll
-        for (uint32_t q = 0; q < kBinBatch / 4u; ++q) {
-            const uint4 v = b4[q];
-            c[4u * q] = v.x;
-            c[4u * q + 1u] = v.y;
-            c[4u * q + 2u] = v.z;
-            c[4u * q + 3u] = v.w;
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < kBinBatch; ++j) f(d0 + b0 + j, c[j]);
+__device__ __forceinline__ void for_each_block(uint64_t mask, F&& f) {
+    while (mask != 0ull) {
+        const uint32_t i = static_cast<uint32_t>(__builtin_ctzll(mask));
+        mask &= mask - 1ull;
+        f(i);
     }
 }
 
 __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __restrict__ bins, uint32_t vocab,
                                                                 const SampleParams* __restrict__ prm,
-                                                                StochDecision* __restrict__ dec, ChunkArrays ca) {
+                                                                StochDecision* __restrict__ dec, ChunkArrays ca,
+                                                                uint32_t* __restrict__ block_total) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    uint16_t* c16 = reinterpret_cast<uint16_t*>(lds);            // [kBins]
+    uint32_t* btot = lds + kBins / 2u;                           // [kBlocks] tokens per block
+    float* bm = reinterpret_cast<float*>(btot + kBlocks);        // [kBlocks] probability mass per block
+    float* bsm = bm + kBlocks;                                   // [kBlocks] mass before each block
+    uint32_t* bsc = reinterpret_cast<uint32_t*>(bsm + kBlocks);  // [kBlocks] tokens before each block
     __shared__ float wf[kWaves];
     __shared__ uint32_t wu[kWaves];
-    __shared__ float wz[kWaves];
     __shared__ uint32_t red;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
-    const uint32_t d0 = tid * kBinsPerThread;
     const float inv_temp = prm->inv_temp;
 
     // The per-group cut counts start at zero and no token is drawn yet.
     for (uint32_t g = tid; g < kMaxGroups; g += kThreads) ca.group_count[g] = 0u;
-    if (tid == 0u) *ca.result = kNone;
-
+    if (tid == 0u) {
+        *ca.result = kNone;
+        red = kNoBin;
+    }
     const uint32_t flags = bins[kBins];
-    uint32_t first = kNoBin;
-    uint32_t total_l = 0u;
-    for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
-        if (c != 0u && first == kNoBin) first = d;
-        total_l += c;
-    });
-    if (tid == 0u) red = kNoBin;
+    btot[tid] = block_total[tid];   // kThreads == kBlocks
+    bm[tid] = 0.0f;
     __syncthreads();
-    atomicMin(&red, first);
+    const uint64_t active = __ballot(btot[block_of(lane, wave)] != 0u);   // bit i: block 16 i + wave
+
+    // Counts of the non-empty blocks into LDS (a batch of up to 8 blocks' loads in flight),
+    // the first non-empty bin.
+    uint32_t first = kNoBin;
+    {
+        uint64_t rest = active;
+        while (rest != 0ull) {   // uniform
+            uint32_t bi[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; ++j) {
+                bi[j] = rest != 0ull ? static_cast<uint32_t>(__builtin_ctzll(rest)) : 64u;   // 64: none
+                rest &= rest - 1ull;   // 0 stays 0
+            }
+            uint32_t c[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; ++j) c[j] = bi[j] < 64u ? bins[64u * block_of(bi[j], wave) + lane] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; ++j) {
+                if (bi[j] >= 64u) continue;
+                const uint32_t d = 64u * block_of(bi[j], wave) + lane;
+                c16[d] = static_cast<uint16_t>(min(c[j], kSat));
+                if (c[j] != 0u) first = min(first, d);
+            }
+        }
+    }
+    first = wave_min_u(first);
+    if (lane == 0u) atomicMin(&red, first);
     __syncthreads();
     const uint32_t top = red;
     const float max_t = top != kNoBin ? bin_value(top) * inv_temp : 0.0f;
@@ -279,81 +317,99 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
     } else if (top == kNoBin || max_t == -__builtin_huge_valf()) {
         mode = kDrawFirst;
     }
+    auto count_of = [&](uint32_t d) {
+        const uint32_t c = c16[d];
+        return c == kSat ? bins[d] : c;
+    };
+    auto weight = [&](uint32_t d) { return det_exp(bin_value(d) * inv_temp - max_t); };
+    // Clears the non-empty blocks' bins and totals for the next row (each bin by the lane
+    // that read it).
+    auto clear_bins = [&]() {
+        for_each_block(active, [&](uint32_t i) { bins[64u * block_of(i, wave) + lane] = 0u; });
+        block_total[tid] = 0u;
+        if (tid == 0u) bins[kBins] = 0u;
+    };
     if (mode != kDrawKept) {
-        __syncthreads();   // every thread has read the flag word
-        if (tid == 0u) {
-            *dec = StochDecision{0.0f, 0u, 0u, mode, 0u, 0.0f, 0.0f};
-            bins[kBins] = 0u;
-        }
-        uint4* b4 = reinterpret_cast<uint4*>(bins + d0);
-        for (uint32_t q = 0; q < kBinsPerThread / 4u; ++q) b4[q] = make_uint4(0u, 0u, 0u, 0u);
+        if (tid == 0u) *dec = StochDecision{0.0f, 0u, 0u, mode, 0u, 0.0f, 0.0f};
+        clear_bins();
         return;
     }
-    auto weight = [&](uint32_t d) { return det_exp(bin_value(d) * inv_temp - max_t); };
 
-    // z: per-lane sums over the lane's bins, a butterfly per wave, the waves in order.
-    float zl = 0.0f;
-    for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
-        if (c != 0u) zl = zl + static_cast<float>(c) * weight(d);
+    // z: per block a butterfly over its 64 bins of count * e, each wave adding its blocks in
+    // order (an empty block adds 0), the 16 waves' sums in order.
+    float zw = 0.0f;
+    for_each_block(active, [&](uint32_t i) {
+        const uint32_t d = 64u * block_of(i, wave) + lane;
+        const uint32_t c = count_of(d);
+        zw = zw + butterfly_sum(c != 0u ? static_cast<float>(c) * weight(d) : 0.0f);
     });
-    const float zw = butterfly_sum(zl);
-    if (lane == 0u) wz[wave] = zw;
+    if (lane == 0u) wf[wave] = zw;
     __syncthreads();
     float z = 0.0f;
-    for (uint32_t w = 0; w < kWaves; ++w) z = z + wz[w];
+    for (uint32_t w = 0; w < kWaves; ++w) z = z + wf[w];
+    __syncthreads();   // wf is reused below
 
-    // Counts and probability masses before each thread's bins: a scan within the wave, the
-    // earlier waves' totals added in order.
-    float pl = 0.0f;
-    for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
-        if (c != 0u) pl = pl + static_cast<float>(c) * (weight(d) / z);
+    // Each block's probability mass (a scan over its bins, the last lane's value; 0 when empty).
+    auto mass = [&](uint32_t d, uint32_t c) { return c != 0u ? static_cast<float>(c) * (weight(d) / z) : 0.0f; };
+    for_each_block(active, [&](uint32_t i) {
+        const uint32_t b = block_of(i, wave);
+        const uint32_t d = 64u * b + lane;
+        const float m = hs_scan(mass(d, count_of(d)), lane);
+        if (lane == 63u) bm[b] = m;
     });
-    const float pincl = hs_scan(pl, lane);
-    const float pexcl = exclusive_of(pincl, lane);
-    const uint32_t uincl = hs_scan_u(total_l, lane);
-    if (lane == 63u) {
-        wf[wave] = pincl;
-        wu[wave] = uincl;
-    }
     __syncthreads();
-    float off = 0.0f;
-    uint32_t uoff = 0u;
-    uint32_t total = 0u;
-    for (uint32_t w = 0; w < kWaves; ++w) {
-        if (w < wave) {
+    // The mass and the tokens before each block, in block order: wave w scans blocks
+    // 64 w .. 64 w + 63, the earlier waves' totals added in order.
+    {
+        const uint32_t b = 64u * wave + lane;
+        const float incl = hs_scan(bm[b], lane);
+        const float excl = exclusive_of(incl, lane);
+        const uint32_t cnt = btot[b];
+        const uint32_t uincl = hs_scan_u(cnt, lane);
+        if (lane == 63u) {
+            wf[wave] = incl;
+            wu[wave] = uincl;
+        }
+        __syncthreads();
+        float off = 0.0f;
+        uint32_t uoff = 0u;
+        for (uint32_t w = 0; w < wave; ++w) {
             off = off + wf[w];
             uoff += wu[w];
         }
-        total += wu[w];
+        bsm[b] = off + excl;
+        bsc[b] = uoff + uincl - cnt;
     }
-    const float start = off + pexcl;
-    const uint32_t before = uoff + uincl - total_l;
+    uint32_t total = 0u;
+    for (uint32_t w = 0; w < kWaves; ++w) total += wu[w];
+    if (tid == 0u) red = kNone;
+    __syncthreads();
 
     // top-p: the first position (in the order) whose running mass reaches top_p.
     uint32_t np = total;
     const float top_p = prm->top_p;
     if (top_p > 0.0f && top_p <= 1.0f) {   // uniform
-        float part = 0.0f;
-        uint32_t seen = before;
         uint32_t cand = kNone;
-        for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
-            if (c == 0u || cand != kNone) return;
-            const float p = weight(d) / z;
-            const float cb = start + part;
-            if (cb + static_cast<float>(c) * p >= top_p) {
-                uint32_t lo = 1u, hi = c;   // the smallest t in [1, c] with cb + t p >= top_p
-                while (lo < hi) {
-                    const uint32_t mid = (lo + hi) >> 1;
-                    if (cb + static_cast<float>(mid) * p >= top_p) hi = mid; else lo = mid + 1u;
+        for_each_block(active, [&](uint32_t i) {
+            const uint32_t b = block_of(i, wave);
+            const uint32_t d = 64u * b + lane;
+            const uint32_t c = count_of(d);
+            const float cb = bsm[b] + exclusive_of(hs_scan(mass(d, c), lane), lane);
+            const uint32_t seen = bsc[b] + hs_scan_u(c, lane) - c;
+            if (c != 0u) {
+                const float p = weight(d) / z;
+                if (cb + static_cast<float>(c) * p >= top_p) {
+                    uint32_t lo = 1u, hi = c;   // the smallest t in [1, c] with cb + t p >= top_p
+                    while (lo < hi) {
+                        const uint32_t mid = (lo + hi) >> 1;
+                        if (cb + static_cast<float>(mid) * p >= top_p) hi = mid; else lo = mid + 1u;
+                    }
+                    cand = min(cand, seen + lo);
                 }
-                cand = seen + lo;
             }
-            part = part + static_cast<float>(c) * p;
-            seen += c;
         });
-        if (tid == 0u) red = kNone;
-        __syncthreads();
-        atomicMin(&red, cand);
+        cand = wave_min_u(cand);
+        if (lane == 0u) atomicMin(&red, cand);
         __syncthreads();
         if (red != kNone) np = red;
         __syncthreads();   // every thread has read red before it is reused
@@ -364,12 +420,15 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
     if (min_p > 0.0f && min_p < 1.0f) {   // uniform
         const float thr = min_p * (1.0f / z);
         uint32_t kept = 0u;
-        for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
+        for_each_block(active, [&](uint32_t i) {
+            const uint32_t d = 64u * block_of(i, wave) + lane;
+            const uint32_t c = count_of(d);
             if (c != 0u && weight(d) / z >= thr) kept += c;
         });
+        kept = wave_sum_u(kept);
         if (tid == 0u) red = 0u;
         __syncthreads();
-        atomicAdd(&red, kept);
+        if (lane == 0u) atomicAdd(&red, kept);
         __syncthreads();
         nm = red;
     }
@@ -377,23 +436,18 @@ __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(uint32_t* __rest
     const uint32_t nk = top_k > 0 && static_cast<uint32_t>(top_k) < vocab ? static_cast<uint32_t>(top_k) : total;
     const uint32_t n = min(min(np, nm), min(nk, total));   // >= 1: every filter keeps the top token
 
-    // The bin where the first n tokens end (one thread's range holds it).
-    if (before < n && n <= before + total_l) {
-        uint32_t seen = before;
-        bool done = false;
-        for_each_bin(bins, d0, [&](uint32_t d, uint32_t c) {
-            if (!done && seen + c >= n) {
-                *dec = StochDecision{max_t, d, n - seen, kDrawKept, n - seen < c ? 1u : 0u, 0.0f, 0.0f};
-                done = true;
-            }
-            seen += c;
-        });
-    }
-    // Clear this thread's bins for the next row (only this thread reads them; every thread
-    // read the flag word before the barriers above).
-    if (tid == 0u) bins[kBins] = 0u;
-    uint4* b4 = reinterpret_cast<uint4*>(bins + d0);
-    for (uint32_t q = 0; q < kBinsPerThread / 4u; ++q) b4[q] = make_uint4(0u, 0u, 0u, 0u);
+    // The bin where the first n tokens end (one lane of one block holds it).
+    for_each_block(active, [&](uint32_t i) {
+        const uint32_t b = block_of(i, wave);
+        if (!(bsc[b] < n && n <= bsc[b] + btot[b])) return;   // uniform
+        const uint32_t d = 64u * b + lane;
+        const uint32_t c = count_of(d);
+        const uint32_t seen = bsc[b] + hs_scan_u(c, lane) - c;
+        if (c != 0u && seen < n && n <= seen + c) {
+            *dec = StochDecision{max_t, d, n - seen, kDrawKept, n - seen < c ? 1u : 0u, 0.0f, 0.0f};
+        }
+    });
+    clear_bins();
 }
 
 // Tokens of the cut bin per chunk (and per group of 64 chunks), when the cut falls inside
@@ -620,20 +674,26 @@ void launch_sample_stochastic(const uint16_t* logits, uint32_t vocab, void* work
     static_assert(sizeof(StochDecision) <= 256u, "decision slot");
     SampleParams* params = sample_stochastic_params(workspace);
     const ChunkArrays ca = chunk_arrays(workspace);
+    uint32_t* block_total = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + kBlockTotalOffset);
+    static_assert(kThreads == kBins / 64u, "one block total per thread of the decision");
     static thread_local int configured_device = -1;
     int dev = 0;
     HYP_HIP_CHECK(hipGetDevice(&dev));
     if (configured_device != dev) {
         HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(stoch_hist_kernel),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
+        HYP_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(stoch_decide_kernel),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kDecideLds)));
         configured_device = dev;
     }
     if (vocab != 0u) {
         const uint32_t groups = (vocab + kHistSpan - 1u) / kHistSpan;
-        hipLaunchKernelGGL(stoch_hist_kernel, dim3(groups), dim3(kHistThreads), kHistLds, stream, logits, vocab, bins);
+        hipLaunchKernelGGL(stoch_hist_kernel, dim3(groups), dim3(kHistThreads), kHistLds, stream, logits, vocab, bins,
+                           block_total);
         HYP_HIP_CHECK(hipGetLastError());
     }
-    hipLaunchKernelGGL(stoch_decide_kernel, dim3(1), dim3(kThreads), 0, stream, bins, vocab, params, dec, ca);
+    hipLaunchKernelGGL(stoch_decide_kernel, dim3(1), dim3(kThreads), kDecideLds, stream, bins, vocab, params, dec, ca,
+                       block_total);
     HYP_HIP_CHECK(hipGetLastError());
     if (vocab != 0u) {
         const uint32_t chunks = (vocab + kChunk - 1u) / kChunk;
