@@ -873,6 +873,33 @@ def test_qmatmul_group_rmsnorm_equals_two_calls(stream, m):
         q.close()
 
 
+@pytest.mark.parametrize("m,k,ns", [(4, 10240, (512, 256, 256)), (1, 10240, (512, 256, 256)),
+                                    (4, 8192, (256, 64, 64)), (3, 3840, (128, 64, 64))])
+def test_qmatmul_group_rmsnorm_launch_shapes(stream, m, k, ns):
+    """The normalising q/k/v launch in the workgroup shapes its launcher picks for other
+    widths and grids - more (row, group) units than an 8-wave workgroup has threads (m = 4,
+    k = 10240: 640 units), exactly as many (k = 8192), a grid of a few tiles - equals
+    hyp_rms_normalize then hyp_qmatmul_group, bit for bit."""
+    ws = [syn.q4_weights(n, k, seed=1270 + i) for i, n in enumerate(ns)]
+    qws = [hy.QWeight.from_host(*w) for w in ws]
+    x = syn.activations(m, k, seed=1280 + m)
+    xd = dev(x, stream)
+    say(f"group rmsnorm m={m} k={k} n={ns}")
+    fused = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
+    hy.qmatmul_group(qws, xd, m, fused, stream, rms_eps=1e-6)
+    xn = hy.DeviceArray((m, k), np.uint16)
+    hy.rms_normalize(xd, m, k, xn, stream, eps=1e-6)
+    sep = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
+    hy.qmatmul_group(qws, xn, m, sep, stream)
+    xn_host = xn.to_host(stream)
+    for (w, s, b), f, g, name in zip(ws, fused, sep, ("q", "k", "v")):
+        yf = f.to_host(stream)
+        np.testing.assert_array_equal(yf, g.to_host(stream), err_msg=name)
+        assert_within_bf16_rounding(yf, O.qmatmul_f64(xn_host, w, s, b), name)
+    for a in qws + fused + sep + [xd, xn]:
+        a.close()
+
+
 # ---------------------------------------------------------------- graph capture
 
 def test_graph_capture_replays_match_eager(stream):
