@@ -416,9 +416,11 @@ static float butterfly64(float* v) {
  *   - 65536 bins over the bf16 value (bin 0 = largest, -0 as +0; -inf, +inf, NaN no bin);
  *     every filter keeps a prefix of (value descending, index ascending);
  *   - exp is st_exp below (the same fp32 operations as the device);
- *   - z = 16 waves (in order) of a 64-lane xor butterfly of per-lane sequential sums over 64
- *     bins; the running mass before each of 1024 threads' 64-bin ranges: a Hillis-Steele
- *     scan within each wave of 64 threads plus the earlier waves' totals added in order;
+ *   - blocks of 64 bins; z = 16 wave sums in order, wave w adding in order the 64-lane xor
+ *     butterflies of count * e over its blocks 16i + w; the mass before a bin = its block's
+ *     start (the blocks' masses, each a Hillis-Steele scan over its bins, scanned in block
+ *     order: within waves of 64 blocks plus the earlier waves' totals in order) + the scan of
+ *     the block's masses before it;
  *   - the draw: chunks of 256 tokens, 4 per lane of a 64-lane wave; a lane's kept weights
  *     summed in token order, a Hillis-Steele scan over the lanes (the chunk total is its last
  *     lane), the chunk totals scanned the same way in groups of 64 chunks with the group
@@ -538,68 +540,81 @@ void orc_sample_stochastic_bf16(const uint16_t* logits, uint32_t vocab, float in
         return;
     }
 
-    /* z: per lane (thread) a sequential sum over its 64 bins, a butterfly per wave, the
-     * 16 wave sums in order. */
+    /* Blocks of 64 bins (block b = bins 64b .. 64b + 63); wave w of 16 takes blocks 16i + w.
+     * z: per block a butterfly over its bins of count * e, each wave adding its blocks in
+     * order i = 0..63, the 16 wave sums in order. */
+#define ST_BLOCKS (ST_BINS / 64u)
     float z = 0.0f;
     for (uint32_t w = 0; w < ST_THREADS / 64u; ++w) {
-        float lanes[64];
-        for (uint32_t l = 0; l < 64u; ++l) {
-            const uint32_t d0 = (w * 64u + l) * ST_PER;
-            float zl = 0.0f;
-            for (uint32_t d = d0; d < d0 + ST_PER; ++d) {
-                if (cnt[d] != 0u) zl = zl + (float)cnt[d] * st_weight(d, inv_temp, max_t);
+        float zw = 0.0f;
+        for (uint32_t i = 0; i < ST_BLOCKS / 16u; ++i) {
+            const uint32_t b = 16u * i + w;
+            float lanes[64];
+            for (uint32_t l = 0; l < 64u; ++l) {
+                const uint32_t d = 64u * b + l;
+                lanes[l] = cnt[d] != 0u ? (float)cnt[d] * st_weight(d, inv_temp, max_t) : 0.0f;
             }
-            lanes[l] = zl;
+            zw = zw + butterfly64(lanes);
         }
-        z = z + butterfly64(lanes);
+        z = z + zw;
     }
 
-    float fs[ST_THREADS + 1];
-    uint32_t us[ST_THREADS + 1];
-    for (uint32_t t = 0; t < ST_THREADS; ++t) {
-        float pl = 0.0f;
-        uint32_t tl = 0u;
-        for (uint32_t d = t * ST_PER; d < (t + 1u) * ST_PER; ++d) {
-            if (cnt[d] != 0u) pl = pl + (float)cnt[d] * (st_weight(d, inv_temp, max_t) / z);
-            tl += cnt[d];
+    /* Probability mass per bin, c * (e / z); per block a Hillis-Steele scan over its bins
+     * (the block's mass is the last lane's), then the masses and token counts before each
+     * block in block order (st_prefix_f: waves of 64 blocks, offsets added in order). */
+    float* mass = (float*)malloc(sizeof(float) * ST_BINS);
+    float bm[ST_BLOCKS + 1];
+    uint32_t bc[ST_BLOCKS + 1];
+    for (uint32_t b = 0; b < ST_BLOCKS; ++b) {
+        float v[64];
+        uint32_t t = 0u;
+        for (uint32_t l = 0; l < 64u; ++l) {
+            const uint32_t d = 64u * b + l;
+            mass[d] = cnt[d] != 0u ? (float)cnt[d] * (st_weight(d, inv_temp, max_t) / z) : 0.0f;
+            v[l] = mass[d];
+            t += cnt[d];
         }
-        fs[t] = pl;
-        us[t] = tl;
+        st_hs_scan64(v);
+        bm[b] = v[63];
+        bc[b] = t;
     }
-    st_prefix_f(fs);
-    st_prefix_u(us);
-    const uint32_t total = us[ST_THREADS];
+    st_prefix_f(bm);
+    st_prefix_u(bc);
+    const uint32_t total = bc[ST_BLOCKS];
 
-    /* top-p: per thread the first bin where its running mass reaches top_p, the smallest
-     * count t within that bin by bisection; the lowest position over threads. */
+    /* top-p: per non-empty bin, the running mass before it (block start + the scan of the
+     * block's masses before it); where that plus count * p reaches top_p, the smallest count
+     * t that does by bisection; the lowest position over bins. */
     uint32_t np = total;
     if (top_p > 0.0f && top_p <= 1.0f) {
         uint32_t best = ST_NONE;
-        for (uint32_t t = 0; t < ST_THREADS; ++t) {
-            const float start = fs[t];
-            float part = 0.0f;
-            uint32_t seen = us[t];
-            uint32_t cand = ST_NONE;
-            for (uint32_t d = t * ST_PER; d < (t + 1u) * ST_PER && cand == ST_NONE; ++d) {
+        for (uint32_t b = 0; b < ST_BLOCKS; ++b) {
+            float v[64];
+            for (uint32_t l = 0; l < 64u; ++l) v[l] = mass[64u * b + l];
+            st_hs_scan64(v);
+            uint32_t seen = bc[b];
+            for (uint32_t l = 0; l < 64u; ++l) {
+                const uint32_t d = 64u * b + l;
                 const uint32_t c = cnt[d];
-                if (c == 0u) continue;
-                const float p = st_weight(d, inv_temp, max_t) / z;
-                const float cb = start + part;
-                if (cb + (float)c * p >= top_p) {
-                    uint32_t lo = 1u, hi = c;
-                    while (lo < hi) {
-                        const uint32_t mid = (lo + hi) >> 1;
-                        if (cb + (float)mid * p >= top_p) hi = mid; else lo = mid + 1u;
+                const float cb = bm[b] + (l != 0u ? v[l - 1u] : 0.0f);
+                if (c != 0u) {
+                    const float p = st_weight(d, inv_temp, max_t) / z;
+                    if (cb + (float)c * p >= top_p) {
+                        uint32_t lo = 1u, hi = c;
+                        while (lo < hi) {
+                            const uint32_t mid = (lo + hi) >> 1;
+                            if (cb + (float)mid * p >= top_p) hi = mid; else lo = mid + 1u;
+                        }
+                        if (seen + lo < best) best = seen + lo;
                     }
-                    cand = seen + lo;
                 }
-                part = part + (float)c * p;
                 seen += c;
             }
-            if (cand < best) best = cand;
         }
         if (best != ST_NONE) np = best;
     }
+    free(mass);
+#undef ST_BLOCKS
     /* min-p: the tokens whose probability is at least min_p * (1 / z). */
     uint32_t nm = total;
     if (min_p > 0.0f && min_p < 1.0f) {
