@@ -71,8 +71,11 @@ namespace {
 // (virtual tile 2t is gate tile t, 2t + 1 up tile t), so both halves of a row tile are
 // in one workgroup; each wave computes one matrix exactly as a plain launch does, and the
 // gate tile's waves combine with the up tile's rows in LDS for the GELU epilogue.
+// The 8-wave residual form is held to 128 VGPRs (four waves per SIMD): its grids run two
+// workgroups on some compute units (the 12B's global q/k: 272 workgroups), and at more
+// registers the second would wait for the first (13.4 against 17.0 us at 134 VGPRs).
 template <int M, bool DUAL, int EPI, int P, int NWAVE, int NORM, bool LOOP>
-__global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
+__global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q4_skinny_kernel(SkinnyParams p) {
     constexpr int NW = 1;
     constexpr uint32_t kThreads = 64u * NWAVE;
     extern __shared__ __attribute__((aligned(16))) uint4 smem[];
@@ -85,9 +88,14 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     const uint32_t WS = W + 1u;
     // Whole range in flight: lane blocks take one group each (compute_lane_groups).
     constexpr bool kLaneGroups = !LOOP;
+    // NORM: the norm's weight (and with a residual the branch norm's weight) copied into LDS
+    // whole, KW chunks each.
+    const uint32_t KW = NORM ? lds_copy_bytes(2u * k) / 16u : 0u;
     uint4* xs = smem;                                              // [M][WS] permuted x
     uint4* zs = smem + M * WS;                                     // [WS] zeros
-    float4* sx = reinterpret_cast<float4*>(zs + WS);               // [G] group sums of x rows 0..3
+    uint4* nwl = zs + WS;                                          // NORM: [KW] norm weight
+    uint4* rwl = nwl + KW;                                         // NORM 2: [KW] branch norm weight
+    float4* sx = reinterpret_cast<float4*>(rwl + (NORM == 2 ? KW : 0u));   // [G] group sums of x rows 0..3
     float* red = reinterpret_cast<float*>(sx + G);                 // [NWAVE][M][16]
     uint32_t* ctr = reinterpret_cast<uint32_t*>(red + NWAVE * M * kTileRows);   // [8]
     float* part = reinterpret_cast<float*>(ctr + 8);               // NORM: [M][G] unit partials, [M] inverses
@@ -150,12 +158,18 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     const bool stager = wave < nstage;
 
     // x first: thread u's unit is requested before its wave's weight loads (with the early
-    // barrier below, before every weight load of the workgroup). With a residual (NORM 2) the staging waves instead run the whole prologue before issuing
-    // their weight loads, so that the branch, residual and weight units are never live
-    // beside two weight batches (the registers of both would halve the waves per SIMD).
+    // barrier below, before every weight load of the workgroup). With a residual (NORM 2)
+    // the branch and residual units are requested there instead, and the staging waves run
+    // the whole prologue before issuing their weight loads, so that those units are never
+    // live beside two weight batches (the registers of both would halve the waves per
+    // SIMD). The norms' weights (and the layer scalar) are requested there too, by wave 0
+    // straight into LDS: behind the weight loads each would cost the prologue a round trip
+    // through the compute unit's queue of weight requests.
     const uint32_t xu0 = threadIdx.x;   // first (row, group) unit this thread stages
     constexpr bool resid = NORM == 2;
     uint4 xv[8];
+    uint4 rv[8];
+    uint16_t res_sc = 0u;   // NORM 2: the layer scalar (bf16)
     if constexpr (!resid) {
         if (xu0 < units) {
             const uint32_t m = unit_row<M>(xu0, G);
@@ -164,6 +178,23 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) xv[t] = src[t];
         }
+    } else if (stager) {
+        if (xu0 < units) {   // the branch first: its statistics need only it
+            const uint32_t m = unit_row<M>(xu0, G);
+            const uint32_t g = xu0 - m * G;
+            const size_t off = static_cast<size_t>(m) * k + g * 64u;
+            const uint4* bsrc = reinterpret_cast<const uint4*>(p.res_branch + off);
+            const uint4* rsrc = reinterpret_cast<const uint4*>(p.res_in + off);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) xv[t] = bsrc[t];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) rv[t] = rsrc[t];
+        }
+    }
+    if constexpr (resid) {
+        // By every thread, from a valid address either way (the value is used only with a
+        // scalar): outside any branch, nothing consumes it before it is needed.
+        res_sc = *(p.res_scalar != nullptr ? p.res_scalar : p.res_w);
     }
     if (threadIdx.x < 8u) ctr[threadIdx.x] = 0u;
     if constexpr (kLaneGroups)
@@ -179,10 +210,22 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     // 13.74 against 14.39 us; in 16-wave workgroups the early barrier, 8.17 against 8.65 us
     // (the late barrier waits for the last of 16 waves to issue its loads).
     constexpr bool kEarly = NORM != 0 || NWAVE >= 16;
+    if constexpr (NORM) {
+        // After the LDS clearing above, which would otherwise have to wait for these writes.
+        if (wave == 0u) {
+            if (p.norm_w != nullptr) copy_to_lds(p.norm_w, 2u * k, nwl, lane);
+            if constexpr (resid) copy_to_lds(p.res_w, 2u * k, rwl, lane);
+        }
+    }
     if constexpr (kEarly) {
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the counters are cleared
         __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");        // no load of the weights above the barrier
     }
+    // Vector-memory instructions a staging wave issues after the barrier before it reads the
+    // LDS copies: the scale-and-bias loads and two batches (with lane groups), two batches of
+    // codes and scales otherwise; none with a residual.
+    constexpr uint32_t kAfterCopy = resid ? 0u : (kLaneGroups ? 3u * P : 4u * P);
 
     const uint32_t c_bytes = tiles * pairs * 1024u;
     const uint32_t s_bytes = tiles * pairs * 128u;
@@ -225,23 +268,9 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
                 // The branch's norm (phases 3, 4), the residual add, then x's statistics
                 // below; each row's inverse is formed by one wave, in residual_norm_kernel's
                 // order. Every unit is held by one thread (checked on the host).
-                uint4 rv[8];
-                uint4 wrv[8];
-                if (xu0 < units) {   // the branch first: its statistics need only it
-                    const uint32_t m = unit_row<M>(xu0, G);
-                    const uint32_t g = xu0 - m * G;
-                    const size_t off = static_cast<size_t>(m) * k + g * 64u;
-                    const uint4* bsrc = reinterpret_cast<const uint4*>(p.res_branch + off);
-                    const uint4* rsrc = reinterpret_cast<const uint4*>(p.res_in + off);
-                    const uint4* wsrc = reinterpret_cast<const uint4*>(p.res_w + g * 64u);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) xv[t] = bsrc[t];
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) rv[t] = rsrc[t];
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) wrv[t] = wsrc[t];
-                }
                 if (xu0 < units) part[xu0] = unit_sumsq(xv);
+                // Wave 0's copies are in LDS (it has issued no other loads since).
+                if (wave == 0u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfterCopy));
                 raise_counter(ctr + 3, lane);
                 wait_counter(ctr + 3, nstage);
                 if (wave < static_cast<uint32_t>(M)) {
@@ -254,9 +283,12 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
                 if (xu0 < units) {
                     const uint32_t m = unit_row<M>(xu0, G);
                     const uint32_t g = xu0 - m * G;
+                    uint4 wrv[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) wrv[t] = rwl[g * 8u + t];
                     normalize_unit(xv, part[units + m]);
                     weight_unit(xv, wrv);
-                    const float sc = p.res_scalar != nullptr ? bf16_bits_to_f32(*p.res_scalar) : 1.0f;
+                    const float sc = bf16_bits_to_f32(res_sc);
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
                         const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
@@ -295,6 +327,8 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
                 }
                 part[u] = unit_sumsq(xv);
             }
+            // Wave 0's copy is in LDS once no more than the loads issued after it are pending.
+            if (wave == 0u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfterCopy));
             }
             raise_counter(ctr + 1, lane);
             wait_counter(ctr + 1, nstage);
@@ -318,10 +352,9 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
             if constexpr (NORM) {
                 normalize_unit(xv, part[units + m]);
                 if (p.norm_w != nullptr) {
-                    const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w + g * 64u);
                     uint4 wv[8];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) wv[t] = wsrc[t];
+                    for (int t = 0; t < 8; ++t) wv[t] = nwl[g * 8u + t];
                     weight_unit(xv, wv);
                 }
             }
@@ -417,12 +450,13 @@ __global__ __launch_bounds__(64 * NWAVE) void q4_skinny_kernel(SkinnyParams p) {
     }
 }
 
-size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, bool norm = false) {
+size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, int norm = 0) {
     const size_t W = k / 8u;
     const size_t G = k / 64u;
-    // x rows and a zero row, group sums, the split reduction, counters, the rms partials,
-    // the gate/up combine.
-    return (m + 1u) * (W + 1u) * 16u + G * 16u + static_cast<size_t>(nwave) * m * kTileRows * 4u + 32u +
+    // x rows and a zero row, the norms' weights, group sums, the split reduction, counters,
+    // the rms partials, the gate/up combine.
+    const size_t copies = static_cast<size_t>(norm == 2 ? 2 : (norm != 0 ? 1 : 0)) * lds_copy_bytes(2u * k);
+    return (m + 1u) * (W + 1u) * 16u + copies + G * 16u + static_cast<size_t>(nwave) * m * kTileRows * 4u + 32u +
            (norm ? (m * G + m) * 4u : 0u) + (dual ? static_cast<size_t>(nwave / 2u) * m * kTileRows * 4u : 0u);
 }
 
@@ -437,7 +471,7 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
     const uint32_t per_wave = (p.pairs + p.splits - 1u) / p.splits;
     auto kernel = per_wave <= 2u * P ? q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false>
                                      : q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true>;
-    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM != 0);
+    const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM);
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "skinny: x staging exceeds the device's LDS");
     if (lds > 65536u) {
         static thread_local int configured_device = -1;
@@ -475,10 +509,12 @@ uint32_t choose_skinny_waves(uint32_t tiles_total, uint32_t splits, uint32_t m, 
         w = 16u;
     } else if (norm == 2) {
         // The residual prologue (run by the staging waves before their own weight loads):
-        // one 16-wave workgroup per compute unit when that covers the grid in one round (the
-        // 12B's sliding q/k/v at 8 splits: 10.8 us against 11.6 in 8-wave workgroups at 4),
-        // else 8-wave workgroups.
-        w = ts >= 16u * cus * 9u / 10u && ts <= 16u * cus ? 16u : std::max(splits, 8u);
+        // 8-wave workgroups when one round of them covers the grid, else 16-wave ones, which
+        // leave some compute units idle rather than give some two workgroups (the 12B's
+        // sliding q/k/v, 512 tiles at 4 splits: 9.48 us in 8-wave workgroups against 9.56 in
+        // 16-wave ones at 8 splits; its global q/k, 544 tiles: 10.48 us in 136 16-wave
+        // workgroups against 13.15 in 272 8-wave ones).
+        w = ts <= 8u * cus ? std::max(splits, 8u) : 16u;
     } else if (norm == 0 && m >= 2u && ts >= 16u * cus * 9u / 10u) {
         w = 16u;
     } else if (ts >= 8u * cus * 9u / 10u || norm != 0) {
@@ -575,12 +611,12 @@ bool skinny_supported(uint32_t m, uint32_t k, bool dual) {
 
 bool skinny_norm_supported(uint32_t m, uint32_t k) {
     return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u &&
-           skinny_lds_bytes(m, k, false, kSkinnyWaves, true) <= max_lds_per_block();
+           skinny_lds_bytes(m, k, false, kSkinnyWaves, 1) <= max_lds_per_block();
 }
 
 bool skinny_resid_supported(uint32_t m, uint32_t k) {
     return m >= 1u && m <= kSkinnyMaxM && k % 64u == 0u && k > 0u && m * (k / 64u) <= 64u * kSkinnyWaves &&
-           skinny_lds_bytes(m, k, false, kSkinnyWaves, true) <= max_lds_per_block();
+           skinny_lds_bytes(m, k, false, kSkinnyWaves, 2) <= max_lds_per_block();
 }
 
 namespace {
@@ -657,10 +693,6 @@ void launch_q4_skinny_group(const Q4Matrix* const* ws, uint16_t* const* ys, uint
     p.eps = norm ? *rms_eps : 0.0f;
     p.norm_w = norm ? norm_w : nullptr;
     p.splits = choose_skinny_splits(tiles_total, p.pairs, m, SkinnyForm::kPlain);
-    if (res != nullptr && p.splits < 16u && p.pairs >= 2u * p.splits &&
-        static_cast<uint64_t>(tiles_total) * 2u * p.splits <= 16ull * device_compute_units()) {
-        p.splits *= 2u;   // the residual form's 16-wave workgroups (choose_skinny_waves)
-    }
     p.split_shift = static_cast<uint32_t>(__builtin_ctz(p.splits));
     set_residual(p, res);
     launch_skinny(p, tiles_total, m, false, Epilogue::kNone, res != nullptr ? 2 : (norm ? 1 : 0), stream);

@@ -108,6 +108,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
                                              static_cast<int>(bytes), 0x00020000);
 }
 
+// s_waitcnt operand for vmcnt(n) with the other counters left at their maxima (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt in 6:4, lgkmcnt in 11:8).
+constexpr uint32_t waitcnt_vm(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | 0x70u | 0xF00u; }
+
+// Bytes of LDS that copy_to_lds fills for `bytes` of source: whole KiB.
+constexpr uint32_t lds_copy_bytes(uint32_t bytes) { return (bytes + 1023u) / 1024u * 1024u; }
+
+// One wave copies [src, src + bytes) into LDS at dst with direct buffer-to-LDS loads, no
+// registers: load t moves bytes [1024 t, 1024 t + 1024), lane l its 16 bytes at
+// 1024 t + 16 l; bytes past `bytes` read as zeros (the buffer's bound) into the rest of
+// lds_copy_bytes(bytes). The loads count in vmcnt in issue order: the data is in LDS once
+// the count has drained past them.
+__device__ __forceinline__ void copy_to_lds(const void* src, uint32_t bytes, void* dst, uint32_t lane) {
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src, bytes);
+    for (uint32_t t = 0; t * 1024u < bytes; ++t) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (__attribute__((address_space(3))) void*)(static_cast<uint8_t*>(dst) + t * 1024u), 16,
+            static_cast<int>(lane * 16u), static_cast<int>(t * 1024u), 0, 0);
+    }
+}
+
 // One projection of a (possibly grouped) launch: its 16-row tiles are global tiles
 // [tile_begin, tile_begin + ceil(n / 16)).
 struct SkinnySegment {
