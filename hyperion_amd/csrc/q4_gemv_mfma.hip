@@ -340,7 +340,12 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
             wait_counter(ctr + 2, nstage);
         }
 
-        // Stage x: each thread permutes whole groups (8 words) and sums them.
+        // Stage x: each thread permutes whole groups (8 words) and sums them. The 16-wave
+        // normalising form scales one 16-byte chunk at a time (the same operations per value):
+        // with the whole unit's weights in registers beside x and two weight batches it spilled
+        // (123 VGPRs chunk by chunk), while the 8-wave form measured faster unit by unit
+        // (7.3-7.5 against 7.9 us on the 12B's q/k/v).
+        constexpr bool kChunked = NORM == 1 && NWAVE >= 16;
         for (uint32_t u = xu0; u < units; u += kThreads) {
             const uint32_t m = unit_row<M>(u, G);
             const uint32_t g = u - m * G;
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
 #pragma unroll
                 for (int t = 0; t < 8; ++t) xv[t] = src[t];
             }
-            if constexpr (NORM) {
+            if constexpr (NORM && !kChunked) {
                 normalize_unit(xv, part[units + m]);
                 if (p.norm_w != nullptr) {
                     uint4 wv[8];
@@ -362,16 +367,21 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
             float s1 = 0.0f;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
+                uint4 c = xv[t];
+                if constexpr (kChunked) {
+                    normalize_chunk(c, part[units + m]);
+                    if (p.norm_w != nullptr) weight_chunk(c, nwl[g * 8u + t]);
+                }
                 uint4 o;
-                o.x = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x05040100u);   // (x0, x4)
-                o.y = __builtin_amdgcn_perm(xv[t].z, xv[t].x, 0x07060302u);   // (x1, x5)
-                o.z = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x05040100u);   // (x2, x6)
-                o.w = __builtin_amdgcn_perm(xv[t].w, xv[t].y, 0x07060302u);   // (x3, x7)
+                o.x = __builtin_amdgcn_perm(c.z, c.x, 0x05040100u);   // (x0, x4)
+                o.y = __builtin_amdgcn_perm(c.z, c.x, 0x07060302u);   // (x1, x5)
+                o.z = __builtin_amdgcn_perm(c.w, c.y, 0x05040100u);   // (x2, x6)
+                o.w = __builtin_amdgcn_perm(c.w, c.y, 0x07060302u);   // (x3, x7)
                 xs[m * WS + g * 8u + t] = o;
-                s0 = dot2_bf16(xv[t].x, kOnePair, s0);
-                s1 = dot2_bf16(xv[t].y, kOnePair, s1);
-                s0 = dot2_bf16(xv[t].z, kOnePair, s0);
-                s1 = dot2_bf16(xv[t].w, kOnePair, s1);
+                s0 = dot2_bf16(c.x, kOnePair, s0);
+                s1 = dot2_bf16(c.y, kOnePair, s1);
+                s0 = dot2_bf16(c.z, kOnePair, s0);
+                s1 = dot2_bf16(c.w, kOnePair, s1);
             }
             reinterpret_cast<float*>(sx)[g * 4u + m] = s0 + s1;
         }
@@ -497,8 +507,10 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
 // choose_skinny_splits fixed): a workgroup holds the fewest waves that keep the grid at about
 // one workgroup per compute unit or more - [15360,3840] at m = 1 8 waves (7.69 us against
 // 8.17 with 16), o [3840,4096] 4 (4.30 against 5.76 with 16 waves at 16 splits), the
-// normalised q/k/v 8 (7.71 against 9.04; its 16-wave form spills); 16 when the splits need
-// them (down [3840,15360], 16 splits) and for a plain launch of m >= 2 rows whose grid fills
+// normalised q/k/v 8 when one round of them covers the grid (7.71 against 9.04 with 16 when
+// that form still spilled); 16 when the splits need them (down [3840,15360], 16 splits),
+// for a normalising grid larger than one round of 8-wave workgroups, and for a plain
+// launch of m >= 2 rows whose grid fills
 // the compute units with 16-wave workgroups ([15360,3840] at m = 4: 9.07 against 9.36 us),
 // which stage x once per compute unit.
 uint32_t choose_skinny_waves(uint32_t tiles_total, uint32_t splits, uint32_t m, uint32_t k, int norm) {
@@ -517,7 +529,12 @@ uint32_t choose_skinny_waves(uint32_t tiles_total, uint32_t splits, uint32_t m, 
         w = ts <= 8u * cus ? std::max(splits, 8u) : 16u;
     } else if (norm == 0 && m >= 2u && ts >= 16u * cus * 9u / 10u) {
         w = 16u;
-    } else if (ts >= 8u * cus * 9u / 10u || norm != 0) {
+    } else if (norm == 1) {
+        // As the residual form: 8 waves for one round, else 16 (the 12B's global q/k,
+        // 544 tiles at 4 splits: 8.6 us in 136 16-wave workgroups against 10.6 in 272 8-wave
+        // ones; 7.3-7.5 against 7.7 us at 16 x 8 for its sliding q/k/v, 512 tiles).
+        w = ts <= 8u * cus ? std::max(splits, 8u) : 16u;
+    } else if (ts >= 8u * cus * 9u / 10u) {
         w = std::max(splits, 8u);
     } else {
         w = std::max(splits, 4u);

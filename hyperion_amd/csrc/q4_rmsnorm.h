@@ -16,20 +16,48 @@
 
 namespace hyperion::hip {
 
+// The unit operations below, one 16-byte chunk (8 bf16, k ascending) at a time: a unit's
+// result is the same whether its chunks are taken from registers or streamed from LDS.
+__device__ __forceinline__ float chunk_sumsq(const uint4& c, float ss) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float lo = bf16_bits_to_f32(w[q] & 0xFFFFu);
+        const float hi = bf16_bits_to_f32(w[q] >> 16);
+        ss = fmaf(lo, lo, ss);
+        ss = fmaf(hi, hi, ss);
+    }
+    return ss;
+}
+
+__device__ __forceinline__ void normalize_chunk(uint4& c, float inv) {
+    uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * inv);
+        const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * inv);
+        w[q] = lo | (hi << 16);
+    }
+    c = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ void weight_chunk(uint4& c, const uint4& wc) {
+    uint32_t x[4] = {c.x, c.y, c.z, c.w};
+    const uint32_t w[4] = {wc.x, wc.y, wc.z, wc.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * bf16_bits_to_f32(x[q] & 0xFFFFu));
+        const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * bf16_bits_to_f32(x[q] >> 16));
+        x[q] = lo | (hi << 16);
+    }
+    c = make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 // Sum of squares of one 64-element unit (8 x 16 bytes of bf16, k ascending).
 __device__ __forceinline__ float unit_sumsq(const uint4 (&xv)[8]) {
     float ss = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float lo = bf16_bits_to_f32(w[q] & 0xFFFFu);
-            const float hi = bf16_bits_to_f32(w[q] >> 16);
-            ss = fmaf(lo, lo, ss);
-            ss = fmaf(hi, hi, ss);
-        }
-    }
+    for (int t = 0; t < 8; ++t) ss = chunk_sumsq(xv[t], ss);
     return ss;
 }
 
@@ -49,32 +77,13 @@ __device__ __forceinline__ float rms_inverse(float ss, uint32_t k, float eps) {
 // x <- bf16(x * inv) for the 64 values of a unit.
 __device__ __forceinline__ void normalize_unit(uint4 (&xv)[8], float inv) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * inv);
-            const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * inv);
-            w[q] = lo | (hi << 16);
-        }
-        xv[t] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    for (int t = 0; t < 8; ++t) normalize_chunk(xv[t], inv);
 }
 
 // x <- bf16(w * x) for the 64 values of a unit (the learned scale after normalize_unit).
 __device__ __forceinline__ void weight_unit(uint4 (&xv)[8], const uint4 (&wv)[8]) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        uint32_t x[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-        const uint32_t w[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * bf16_bits_to_f32(x[q] & 0xFFFFu));
-            const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * bf16_bits_to_f32(x[q] >> 16));
-            x[q] = lo | (hi << 16);
-        }
-        xv[t] = make_uint4(x[0], x[1], x[2], x[3]);
-    }
+    for (int t = 0; t < 8; ++t) weight_chunk(xv[t], wv[t]);
 }
 
 }  // namespace hyperion::hip
