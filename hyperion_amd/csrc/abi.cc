@@ -536,6 +536,7 @@ void qmatmul_group(const HypQWeight* weights, uint32_t count, const void* x, uin
         outs[i] = static_cast<uint16_t*>(ys[i]);
     }
     if (rms_eps != nullptr) REQUIRE_ARG(std::isfinite(*rms_eps) && *rms_eps >= 0.0f, "eps must be finite and >= 0");
+    REQUIRE_ARG((reinterpret_cast<uintptr_t>(norm_weight) & 15u) == 0u, "norm_weight must be 16-byte aligned");
     hipStream_t s = stream_of(stream);
     if (m == 0) return;
     REQUIRE_ARG(x != nullptr, "x must be a non-null device pointer");

@@ -342,6 +342,24 @@ def test_qmatmul_group_rejects_mixed_k(stream):
     b.close()
 
 
+def test_qmatmul_group_rmsnorm_rejects_a_misaligned_norm_weight(stream):
+    """norm_weight is copied into LDS by 16-byte direct loads: a pointer off that alignment
+    is refused on the host (INVALID_ARGUMENT) before any launch."""
+    a = hy.QWeight.from_host(*syn.q4_weights(16, 128, seed=1243))
+    x = dev(syn.activations(1, 128, seed=1244), stream)
+    nw = dev(syn.bf16_bits(np.ones(136, np.float32)), stream)
+    ys = [hy.DeviceArray((1, 16), np.uint16)]
+
+    class Shifted:
+        ptr = ctypes.c_void_p(nw.ptr.value + 2)
+
+    with pytest.raises(hy.HypError) as e:
+        hy.qmatmul_group([a], x, 1, ys, stream, rms_eps=1e-6, norm_weight=Shifted())
+    assert e.value.status_name == "INVALID_ARGUMENT"
+    for t in (a, x, nw, *ys):
+        t.close()
+
+
 # ---------------------------------------------------------------- prefill GEMM
 
 @pytest.mark.parametrize("m", [512, 2048])
