@@ -77,6 +77,44 @@ __device__ __forceinline__ void resolve_position(AttnParams& p) {
     p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
 }
 
+// __shfl_xor(v, MASK, 64) for MASK < 16, whose partner lies in the lane's 16-lane row, by DPP
+// moves instead of an LDS permute (register latency instead of an LDS round trip on every
+// step of a butterfly): xor 1 and 2 are quad permutes, xor 4 and 8 take the row shifted
+// left or right by MASK, whichever holds the partner. The same values, so the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+template <int MASK>
+__device__ __forceinline__ float xor_lanes(float v, uint32_t lane) {
+    static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "a partner in the 16-lane row");
+    if constexpr (MASK == 1) {
+        return dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    } else if constexpr (MASK == 2) {
+        return dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    } else {
+        const float up = dpp_mov<0x100 + MASK>(v);     // row_shl: lane i + MASK
+        const float down = dpp_mov<0x110 + MASK>(v);   // row_shr: lane i - MASK
+        return (lane & static_cast<uint32_t>(MASK)) != 0u ? down : up;
+    }
+}
+
+// Max and sum over the 16 lanes of a row, in the order of the xor butterfly 1, 2, 4, 8.
+__device__ __forceinline__ float row16_max(float v, uint32_t lane) {
+    v = fmaxf(v, xor_lanes<1>(v, lane));
+    v = fmaxf(v, xor_lanes<2>(v, lane));
+    v = fmaxf(v, xor_lanes<4>(v, lane));
+    return fmaxf(v, xor_lanes<8>(v, lane));
+}
+
+__device__ __forceinline__ float row16_sum(float v, uint32_t lane) {
+    v += xor_lanes<1>(v, lane);
+    v += xor_lanes<2>(v, lane);
+    v += xor_lanes<4>(v, lane);
+    return v + xor_lanes<8>(v, lane);
+}
+
 template <uint32_t D>
 struct AttnLds {
     static constexpr uint32_t kRow = D * 2u + 16u;           // Q and K rows (bytes)
@@ -262,8 +300,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
                 sv[c] = vis ? s[c][i] * kLog2e : -__builtin_huge_valf();
                 bmax = fmaxf(bmax, sv[c]);
             }
-#pragma unroll
-            for (int mask = 1; mask <= 8; mask <<= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, mask, 64));
+            bmax = row16_max(bmax, lane);
             const float m_new = fmaxf(m[i], bmax);
             const bool any = m_new > -__builtin_huge_valf();
             const float alpha = any ? exp2f(m[i] - m_new) : 1.0f;   // m[i] = -inf -> 0
@@ -275,8 +312,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
                 *reinterpret_cast<uint16_t*>(prow_w + (4u * kb + i) * Lds::kPRow + (16u * c + j16) * 2u) =
                     f32_to_bf16_bits(pv);
             }
-#pragma unroll
-            for (int mask = 1; mask <= 8; mask <<= 1) psum += __shfl_xor(psum, mask, 64);
+            psum = row16_sum(psum, lane);
             l[i] = l[i] * alpha + psum;
             m[i] = any ? m_new : m[i];
 #pragma unroll
@@ -513,8 +549,9 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
             // The prepare's 64-lane butterfly over a row's kU lanes (the rest of its lanes
             // add zeros there).
             float ss = src != nullptr ? unit_sumsq(xv) : 0.0f;
-#pragma unroll
-            for (uint32_t off = kU / 2u; off > 0u; off >>= 1) ss += __shfl_xor(ss, static_cast<int>(off), 64);
+            if constexpr (kU >= 8u) ss += xor_lanes<4>(ss, lane);
+            if constexpr (kU >= 4u) ss += xor_lanes<2>(ss, lane);
+            if constexpr (kU >= 2u) ss += xor_lanes<1>(ss, lane);
             if (src != nullptr) {
                 normalize_unit(xv, rms_inverse(ss, D, p.eps));
                 if (w != nullptr) weight_unit(xv, wv);
@@ -641,8 +678,7 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
                 sv[c] = vis ? sc[c][i] * kLog2e : -__builtin_huge_valf();
                 bmax = fmaxf(bmax, sv[c]);
             }
-#pragma unroll
-            for (int mask = 1; mask <= 8; mask <<= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, mask, 64));
+            bmax = row16_max(bmax, lane);
             const float m_new = fmaxf(m[i], bmax);
             const bool any = m_new > -__builtin_huge_valf();
             const float alpha = any ? exp2f(m[i] - m_new) : 1.0f;
@@ -654,8 +690,7 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
                 *reinterpret_cast<uint16_t*>(my + Lds::kP + (4u * kb + i) * Lds::kPRow + (16u * c + j16) * 2u) =
                     f32_to_bf16_bits(pv);
             }
-#pragma unroll
-            for (int mask = 1; mask <= 8; mask <<= 1) psum += __shfl_xor(psum, mask, 64);
+            psum = row16_sum(psum, lane);
             l[i] = l[i] * alpha + psum;
             m[i] = any ? m_new : m[i];
 #pragma unroll
