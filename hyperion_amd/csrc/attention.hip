@@ -77,29 +77,6 @@ __device__ __forceinline__ void resolve_position(AttnParams& p) {
     p.keys_per_split = ((T + p.splits - 1u) / p.splits + kKeyBlock - 1u) / kKeyBlock * kKeyBlock;
 }
 
-// __shfl_xor(v, MASK, 64) for MASK < 16, whose partner lies in the lane's 16-lane row, by DPP
-// moves instead of an LDS permute (register latency instead of an LDS round trip on every
-// step of a butterfly): xor 1 and 2 are quad permutes, xor 4 and 8 take the row shifted
-// left or right by MASK, whichever holds the partner. The same values, so the same bits.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-
-template <int MASK>
-__device__ __forceinline__ float xor_lanes(float v, uint32_t lane) {
-    static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "a partner in the 16-lane row");
-    if constexpr (MASK == 1) {
-        return dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-    } else if constexpr (MASK == 2) {
-        return dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-    } else {
-        const float up = dpp_mov<0x100 + MASK>(v);     // row_shl: lane i + MASK
-        const float down = dpp_mov<0x110 + MASK>(v);   // row_shr: lane i - MASK
-        return (lane & static_cast<uint32_t>(MASK)) != 0u ? down : up;
-    }
-}
-
 // Max and sum over the 16 lanes of a row, in the order of the xor butterfly 1, 2, 4, 8.
 __device__ __forceinline__ float row16_max(float v, uint32_t lane) {
     v = fmaxf(v, xor_lanes<1>(v, lane));

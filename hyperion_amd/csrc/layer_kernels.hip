@@ -64,8 +64,7 @@ __device__ __forceinline__ void norm_loaded(uint4 (&xv)[8], const uint4 (*wv)[8]
                                             uint32_t lane) {
     const uint32_t units = D / 64u;
     float ss = lane < units ? unit_sumsq(xv) : 0.0f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = butterfly_sum<32>(ss, lane);
     const float inv = rms_inverse(ss, D, eps);
     if (lane < units) {
         normalize_unit(xv, inv);
@@ -218,8 +217,7 @@ __global__ __launch_bounds__(kThreads) void attn_prepare_kernel(PrepareParams p)
         }
     }
     float ss = active ? unit_sumsq(xv) : 0.0f;
-#pragma unroll
-    for (uint32_t off = kU / 2u; off > 0u; off >>= 1) ss += __shfl_xor(ss, static_cast<int>(off), 64);
+    ss = butterfly_sum<kU / 2u>(ss, lane);
     const size_t slot_row = (static_cast<size_t>((base_pos + t) % p.cap) * p.KVH + hd) * D;
     if (active) {
         normalize_unit(xv, rms_inverse(ss, D, p.eps));
@@ -424,8 +422,7 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(const uint16_t* 
     }
     const float sc = scalar != nullptr ? bf16_bits_to_f32(*scalar) : 1.0f;
     float ss = mine ? unit_sumsq(xv) : 0.0f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    ss = butterfly_sum<32>(ss, lane);
     float ss2 = 0.0f;
     if (mine) {
         normalize_unit(xv, rms_inverse(ss, hidden, eps));
@@ -450,8 +447,7 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(const uint16_t* 
         if (w_next != nullptr) ss2 = unit_sumsq(xv);
     }
     if (w_next == nullptr) return;   // uniform over the launch
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss2 += __shfl_xor(ss2, off, 64);
+    ss2 = butterfly_sum<32>(ss2, lane);
     if (mine) {
         normalize_unit(xv, rms_inverse(ss2, hidden, eps));
         weight_unit(xv, nv);
@@ -551,8 +547,7 @@ __global__ __launch_bounds__(64 * kTiledRows) void residual_norm_tiled_kernel(
     // residual_norm_wave_kernel's arithmetic, unit by unit.
     const float sc = scalar != nullptr ? bf16_bits_to_f32(*scalar) : 1.0f;
     float ss = mine ? unit_sumsq(xv) : 0.0f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    ss = butterfly_sum<32>(ss, lane);
     if (mine) {
         normalize_unit(xv, rms_inverse(ss, hidden, eps));
 #pragma unroll
@@ -591,8 +586,7 @@ __global__ __launch_bounds__(64 * kTiledRows) void residual_norm_tiled_kernel(
     if (w_next == nullptr) return;   // uniform over the launch
 
     float ss2 = mine ? unit_sumsq(xv) : 0.0f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss2 += __shfl_xor(ss2, off, 64);
+    ss2 = butterfly_sum<32>(ss2, lane);
     if (mine) {
         normalize_unit(xv, rms_inverse(ss2, hidden, eps));
 #pragma unroll

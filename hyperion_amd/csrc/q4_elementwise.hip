@@ -144,8 +144,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const uint16_t*
         for (int t = 0; t < 8; ++t) xv[t] = xr[lane * 8u + t];
         ss = unit_sumsq(xv);
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = butterfly_sum<32>(ss, lane);
     const float inv = rms_inverse(ss, k, eps);
     if (lane < units) {
         normalize_unit(xv, inv);

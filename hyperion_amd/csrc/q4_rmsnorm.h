@@ -16,6 +16,63 @@
 
 namespace hyperion::hip {
 
+// __shfl_xor(v, MASK, 64) for MASK < 16, whose partner lies in the lane's 16-lane row, by DPP
+// moves instead of an LDS permute (register latency instead of an LDS round trip on every
+// step of a butterfly): xor 1 and 2 are quad permutes, xor 4 and 8 take the row shifted
+// left or right by MASK, whichever holds the partner. The same values, so the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+template <int MASK>
+__device__ __forceinline__ float xor_lanes(float v, uint32_t lane) {
+    static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8, "a partner in the 16-lane row");
+    if constexpr (MASK == 1) {
+        return dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    } else if constexpr (MASK == 2) {
+        return dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    } else {
+        const float up = dpp_mov<0x100 + MASK>(v);     // row_shl: lane i + MASK
+        const float down = dpp_mov<0x110 + MASK>(v);   // row_shr: lane i - MASK
+        return (lane & static_cast<uint32_t>(MASK)) != 0u ? down : up;
+    }
+}
+
+// v + the value of lane l ^ 32 (l ^ 16): with v in both operands v_permlane32_swap
+// (v_permlane16_swap) leaves each lane's own value in one register and its partner's in the
+// other, and the sum of the two is v + partner (addition commutes). Inline assembly: the
+// builtins, given equal inputs, compiled to an add of one output register to itself; the
+// s_nop gives the swap the wait states it needs after a VALU write of its operands.
+__device__ __forceinline__ float add_lane_xor32(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    uint32_t c = u;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(c));
+    return __builtin_bit_cast(float, u) + __builtin_bit_cast(float, c);
+}
+
+__device__ __forceinline__ float add_lane_xor16(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    uint32_t c = u;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(u), "+v"(c));
+    return __builtin_bit_cast(float, u) + __builtin_bit_cast(float, c);
+}
+
+// The xor butterfly sum with offsets TOP, TOP / 2, ..., 1 (TOP a power of two up to 32, or
+// 0 for none), bit for bit `for (off = TOP; off > 0; off >>= 1) v += __shfl_xor(v, off)`,
+// with no LDS permute: lane swaps for 32 and 16, DPP moves below.
+template <uint32_t TOP>
+__device__ __forceinline__ float butterfly_sum(float v, uint32_t lane) {
+    static_assert(TOP <= 32u && (TOP & (TOP - 1u)) == 0u, "a power of two up to 32");
+    if constexpr (TOP >= 32u) v = add_lane_xor32(v);
+    if constexpr (TOP >= 16u) v = add_lane_xor16(v);
+    if constexpr (TOP >= 8u) v += xor_lanes<8>(v, lane);
+    if constexpr (TOP >= 4u) v += xor_lanes<4>(v, lane);
+    if constexpr (TOP >= 2u) v += xor_lanes<2>(v, lane);
+    if constexpr (TOP >= 1u) v += xor_lanes<1>(v, lane);
+    return v;
+}
+
 // The unit operations below, one 16-byte chunk (8 bf16, k ascending) at a time: a unit's
 // result is the same whether its chunks are taken from registers or streamed from LDS.
 __device__ __forceinline__ float chunk_sumsq(const uint4& c, float ss) {
@@ -65,9 +122,7 @@ __device__ __forceinline__ float unit_sumsq(const uint4 (&xv)[8]) {
 __device__ __forceinline__ float row_sumsq(const float* part, uint32_t units, uint32_t lane) {
     float ss = 0.0f;
     for (uint32_t i = lane; i < units; i += 64u) ss += part[i];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    return ss;
+    return butterfly_sum<32>(ss, lane);
 }
 
 __device__ __forceinline__ float rms_inverse(float ss, uint32_t k, float eps) {
