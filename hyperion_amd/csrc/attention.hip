@@ -740,9 +740,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p
 #pragma unroll
         for (uint32_t e = 0; e < kPer; ++e) part[u][e] = sp < p.splits ? o[e] : 0.0f;
     }
-    float mx = ms;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float mx = butterfly_max64(ms, lane);
     const float w = ms == -__builtin_huge_valf() || mx == -__builtin_huge_valf() ? 0.0f : exp2f(ms - mx);
     float num[kPer];
 #pragma unroll
@@ -751,8 +749,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnParams p
 #pragma unroll
     for (uint32_t u = 0; u < kMaxPerWave; ++u) {
         const uint32_t sp = wave + kWaves * u;
-        const float ws = __shfl(w, static_cast<int>(sp), 64);
-        const float lw = __shfl(ls, static_cast<int>(sp), 64);
+        // Split sp's weight and l from lane sp (sp is uniform: a scalar read of one lane).
+        const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), static_cast<int>(sp & 63u)));
+        const float lw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), static_cast<int>(sp & 63u)));
         if (sp >= p.splits || ws == 0.0f) continue;   // uniform: past the splits, or an empty split
         den += ws * lw;
 #pragma unroll

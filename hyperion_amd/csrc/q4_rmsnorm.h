@@ -58,6 +58,31 @@ __device__ __forceinline__ float add_lane_xor16(float v) {
     return __builtin_bit_cast(float, u) + __builtin_bit_cast(float, c);
 }
 
+// max(v, the value of lane l ^ 32) and of lane l ^ 16, by the same swaps.
+__device__ __forceinline__ float max_lane_xor32(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    uint32_t c = u;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(c));
+    return fmaxf(__builtin_bit_cast(float, u), __builtin_bit_cast(float, c));
+}
+
+__device__ __forceinline__ float max_lane_xor16(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    uint32_t c = u;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(u), "+v"(c));
+    return fmaxf(__builtin_bit_cast(float, u), __builtin_bit_cast(float, c));
+}
+
+// The max over all 64 lanes by the xor butterfly 32, 16, ..., 1 (fmaxf, exact in any order).
+__device__ __forceinline__ float butterfly_max64(float v, uint32_t lane) {
+    v = max_lane_xor32(v);
+    v = max_lane_xor16(v);
+    v = fmaxf(v, xor_lanes<8>(v, lane));
+    v = fmaxf(v, xor_lanes<4>(v, lane));
+    v = fmaxf(v, xor_lanes<2>(v, lane));
+    return fmaxf(v, xor_lanes<1>(v, lane));
+}
+
 // The xor butterfly sum with offsets TOP, TOP / 2, ..., 1 (TOP a power of two up to 32, or
 // 0 for none), bit for bit `for (off = TOP; off > 0; off >>= 1) v += __shfl_xor(v, off)`,
 // with no LDS permute: lane swaps for 32 and 16, DPP moves below.
