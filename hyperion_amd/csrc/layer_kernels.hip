@@ -353,19 +353,7 @@ __global__ __launch_bounds__(kThreads) void residual_norm_kernel(const uint16_t*
         weight_unit(xv, wv);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
-            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
-                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
-                if (scalar != nullptr) {
-                    lo = round_bf16(lo * sc);
-                    hi = round_bf16(hi * sc);
-                }
-                hw[q] = cvt_pk_bf16(lo, hi);
-            }
-            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            residual_add_chunk(xv[t], rv[t], scalar != nullptr, sc);
             r4[t] = xv[t];
         }
         if (w_next != nullptr) ss2 = unit_sumsq(xv);
@@ -429,19 +417,7 @@ __global__ __launch_bounds__(64) void residual_norm_wave_kernel(const uint16_t* 
         weight_unit(xv, wv);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
-            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
-                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
-                if (scalar != nullptr) {
-                    lo = round_bf16(lo * sc);
-                    hi = round_bf16(hi * sc);
-                }
-                hw[q] = cvt_pk_bf16(lo, hi);
-            }
-            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            residual_add_chunk(xv[t], rv[t], scalar != nullptr, sc);
             r4[t] = xv[t];
         }
         if (w_next != nullptr) ss2 = unit_sumsq(xv);
@@ -555,19 +531,7 @@ __global__ __launch_bounds__(64 * kTiledRows) void residual_norm_tiled_kernel(
         weight_unit(xv, wv);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
-            uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
-                float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
-                if (scalar != nullptr) {
-                    lo = round_bf16(lo * sc);
-                    hi = round_bf16(hi * sc);
-                }
-                hw[q] = cvt_pk_bf16(lo, hi);
-            }
-            xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            residual_add_chunk(xv[t], rv[t], scalar != nullptr, sc);
         }
     }
 

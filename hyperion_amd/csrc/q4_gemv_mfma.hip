@@ -291,19 +291,7 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
                     const float sc = bf16_bits_to_f32(res_sc);
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
-                        const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
-                        uint32_t hw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            float lo = round_bf16(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(hw[q] & 0xFFFFu));
-                            float hi = round_bf16(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(hw[q] >> 16));
-                            if (p.res_scalar != nullptr) {
-                                lo = round_bf16(lo * sc);
-                                hi = round_bf16(hi * sc);
-                            }
-                            hw[q] = cvt_pk_bf16(lo, hi);
-                        }
-                        xv[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                        residual_add_chunk(xv[t], rv[t], p.res_scalar != nullptr, sc);
                     }
                     if (blockIdx.x == 0u) {
                         uint4* dst = reinterpret_cast<uint4*>(p.res_out + static_cast<size_t>(m) * k + g * 64u);

@@ -99,40 +99,53 @@ __device__ __forceinline__ float butterfly_sum(float v, uint32_t lane) {
 }
 
 // The unit operations below, one 16-byte chunk (8 bf16, k ascending) at a time: a unit's
-// result is the same whether its chunks are taken from registers or streamed from LDS.
+// result is the same whether its chunks are taken from registers or streamed from LDS. A
+// register's two bf16 values widen with one VALU op each, and each pair of results is
+// rounded by one v_cvt_pk_bf16_f32 (round to nearest even per half, the bits of two
+// separate conversions).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
 __device__ __forceinline__ float chunk_sumsq(const uint4& c, float ss) {
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float lo = bf16_bits_to_f32(w[q] & 0xFFFFu);
-        const float hi = bf16_bits_to_f32(w[q] >> 16);
+        const float lo = bf16_lo(w[q]);
+        const float hi = bf16_hi(w[q]);
         ss = fmaf(lo, lo, ss);
         ss = fmaf(hi, hi, ss);
     }
     return ss;
 }
 
+// c <- bf16(c * inv).
 __device__ __forceinline__ void normalize_chunk(uint4& c, float inv) {
     uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * inv);
-        const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * inv);
-        w[q] = lo | (hi << 16);
-    }
+    for (int q = 0; q < 4; ++q) w[q] = cvt_pk_bf16(bf16_lo(w[q]) * inv, bf16_hi(w[q]) * inv);
     c = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// c <- bf16(w * c).
 __device__ __forceinline__ void weight_chunk(uint4& c, const uint4& wc) {
     uint32_t x[4] = {c.x, c.y, c.z, c.w};
     const uint32_t w[4] = {wc.x, wc.y, wc.z, wc.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(w[q] & 0xFFFFu) * bf16_bits_to_f32(x[q] & 0xFFFFu));
-        const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(w[q] >> 16) * bf16_bits_to_f32(x[q] >> 16));
-        x[q] = lo | (hi << 16);
-    }
+    for (int q = 0; q < 4; ++q) x[q] = cvt_pk_bf16(bf16_lo(w[q]) * bf16_lo(x[q]), bf16_hi(w[q]) * bf16_hi(x[q]));
     c = make_uint4(x[0], x[1], x[2], x[3]);
+}
+
+// The residual add of the Gemma sandwich (forward.cc:523-539): h <- bf16(r + h), then
+// h <- bf16(h * sc) when has_scalar (the layer scalar, a bf16 value).
+__device__ __forceinline__ void residual_add_chunk(uint4& h, const uint4& r, bool has_scalar, float sc) {
+    uint32_t x[4] = {h.x, h.y, h.z, h.w};
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        x[q] = cvt_pk_bf16(bf16_lo(w[q]) + bf16_lo(x[q]), bf16_hi(w[q]) + bf16_hi(x[q]));
+        if (has_scalar) x[q] = cvt_pk_bf16(bf16_lo(x[q]) * sc, bf16_hi(x[q]) * sc);
+    }
+    h = make_uint4(x[0], x[1], x[2], x[3]);
 }
 
 // Sum of squares of one 64-element unit (8 x 16 bytes of bf16, k ascending).
