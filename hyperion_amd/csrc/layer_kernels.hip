@@ -15,10 +15,11 @@
 //    residual <- bf16(residual + rms_norm(branch, w_post)), then optionally
 //    residual <- bf16(residual * layer_scalar), then optionally next <- rms_norm(residual,
 //    w_next) (the following block's input norm). One workgroup per row, thread u owning unit
-//    u (one wave, no LDS, for rows of at most 64 units: residual_norm_wave_kernel; from 64
-//    rows on, residual_norm_tiled_kernel, the same lanes' arithmetic behind coalesced
-//    loads and stores through LDS); both statistics in the order of q4_rmsnorm.h, so each norm has the bits of
-//    launch_rms_normalize and of the skinny matmul's normalising prologue.
+//    u (for rows of at most 64 units, residual_norm_lanes_kernel spreads each unit over four
+//    lanes; from 64 rows on, residual_norm_tiled_kernel, the unit-per-thread arithmetic behind
+//    coalesced loads and stores through LDS); both statistics in the order of q4_rmsnorm.h,
+//    so each norm has the bits of launch_rms_normalize and of the skinny matmul's
+//    normalising prologue.
 #include "common.h"
 #include "kernels.h"
 #include "q4_rmsnorm.h"
@@ -376,64 +377,96 @@ __global__ __launch_bounds__(kThreads) void residual_norm_kernel(const uint16_t*
     }
 }
 
-// residual_norm_kernel for rows of at most 64 units, one wave per row: the unit sums stay
-// in registers and meet in the same 64-lane butterfly (after which every lane holds the
-// bits lane 0 of the block form computes), so there is no LDS round trip or workgroup
-// barrier. The same arithmetic as residual_norm_kernel, bit for bit.
-__global__ __launch_bounds__(64) void residual_norm_wave_kernel(const uint16_t* __restrict__ branch,
-                                                                uint16_t* __restrict__ residual,
-                                                                const uint16_t* __restrict__ w_post,
-                                                                const uint16_t* __restrict__ scalar,
-                                                                const uint16_t* __restrict__ w_next,
-                                                                uint16_t* __restrict__ next, uint32_t hidden, float eps) {
-    const uint32_t units = hidden / 64u;
-    const uint32_t lane = threadIdx.x;
-    const size_t row = static_cast<size_t>(blockIdx.x) * hidden;
-    const uint4* b4 = reinterpret_cast<const uint4*>(branch + row) + lane * 8u;
-    uint4* r4 = reinterpret_cast<uint4*>(residual + row) + lane * 8u;
-    const bool mine = lane < units;
+// residual_norm_kernel for rows of at most 64 units, one row per workgroup, each 64-value
+// unit spread over kUnitLanes lanes (kUnitLanes waves): a lane widens, normalises, weights
+// and adds its 64 / kUnitLanes values; the fma chains of the unit sums are handed from lane
+// to lane in the unit's order (scan_sumsq), and the unit sums meet in LDS for the row's
+// butterfly in one wave. The bits of residual_norm_kernel, with a quarter of the vector-ALU
+// instructions per wave of a unit-per-lane form (5.6 -> about 4 us per decode row of 3840
+// in the model's step) and coalesced 32-byte accesses per lane.
+constexpr uint32_t kUnitLanes = 4;
+constexpr uint32_t kUnitChunks = 8u / kUnitLanes;   // 16-byte chunks per lane
 
-    uint4 xv[8];
-    uint4 rv[8];
-    uint4 wv[8];
-    uint4 nv[8];
+__global__ __launch_bounds__(64 * kUnitLanes) void residual_norm_lanes_kernel(
+    const uint16_t* __restrict__ branch, uint16_t* __restrict__ residual, const uint16_t* __restrict__ w_post,
+    const uint16_t* __restrict__ scalar, const uint16_t* __restrict__ w_next, uint16_t* __restrict__ next,
+    uint32_t hidden, float eps) {
+    __shared__ float part[64 + 2];
+    const uint32_t units = hidden / 64u;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    const uint32_t u = tid / kUnitLanes;
+    const uint32_t c = tid % kUnitLanes;
+    const bool mine = u < units;
+    const size_t off = static_cast<size_t>(blockIdx.x) * hidden + u * 64u + c * (64u / kUnitLanes);
+    const uint4* b4 = reinterpret_cast<const uint4*>(branch + off);
+    uint4* r4 = reinterpret_cast<uint4*>(residual + off);
+
+    uint4 xv[kUnitChunks];
+    uint4 rv[kUnitChunks];
+    uint4 wv[kUnitChunks];
+    uint4 nv[kUnitChunks];
     if (mine) {
-        const uint4* w4 = reinterpret_cast<const uint4*>(w_post) + lane * 8u;
-        const uint4* n4 = reinterpret_cast<const uint4*>(w_next != nullptr ? w_next : w_post) + lane * 8u;
+        const size_t woff = u * 64u + c * (64u / kUnitLanes);
+        const uint4* w4 = reinterpret_cast<const uint4*>(w_post + woff);
+        const uint4* n4 = reinterpret_cast<const uint4*>((w_next != nullptr ? w_next : w_post) + woff);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {   // every load of the row issued before the first use
+        for (uint32_t t = 0; t < kUnitChunks; ++t) {   // every load of the row issued before the first use
             xv[t] = b4[t];
             rv[t] = r4[t];
             wv[t] = w4[t];
             nv[t] = n4[t];
         }
+    } else {
+#pragma unroll
+        for (uint32_t t = 0; t < kUnitChunks; ++t) xv[t] = make_uint4(0u, 0u, 0u, 0u);
     }
     const float sc = scalar != nullptr ? bf16_bits_to_f32(*scalar) : 1.0f;
-    float ss = mine ? unit_sumsq(xv) : 0.0f;
-    ss = butterfly_sum<32>(ss, lane);
-    float ss2 = 0.0f;
-    if (mine) {
-        normalize_unit(xv, rms_inverse(ss, hidden, eps));
-        weight_unit(xv, wv);
+    // The row's inverse rms from the lanes' chunks: unit sums to LDS, one wave's butterfly.
+    const auto row_inverse = [&](const uint4 (&v)[kUnitChunks], uint32_t slot) {
+        uint32_t w[4 * kUnitChunks];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (uint32_t t = 0; t < kUnitChunks; ++t) {
+            w[4 * t] = v[t].x;
+            w[4 * t + 1] = v[t].y;
+            w[4 * t + 2] = v[t].z;
+            w[4 * t + 3] = v[t].w;
+        }
+        const float t = scan_sumsq<kUnitLanes>(w, c);
+        if (mine && c == kUnitLanes - 1u) part[u] = t;
+        __syncthreads();
+        if (wave == 0u) {
+            const float ss = row_sumsq(part, units, lane);
+            if (lane == 0u) part[slot] = rms_inverse(ss, hidden, eps);
+        }
+        __syncthreads();
+        return part[slot];
+    };
+    const float inv = row_inverse(xv, 64u);
+    if (mine) {
+#pragma unroll
+        for (uint32_t t = 0; t < kUnitChunks; ++t) {
+            normalize_chunk(xv[t], inv);
+            weight_chunk(xv[t], wv[t]);
             residual_add_chunk(xv[t], rv[t], scalar != nullptr, sc);
             r4[t] = xv[t];
         }
-        if (w_next != nullptr) ss2 = unit_sumsq(xv);
     }
     if (w_next == nullptr) return;   // uniform over the launch
-    ss2 = butterfly_sum<32>(ss2, lane);
+    const float inv2 = row_inverse(xv, 65u);
     if (mine) {
-        normalize_unit(xv, rms_inverse(ss2, hidden, eps));
-        weight_unit(xv, nv);
-        uint4* n4 = reinterpret_cast<uint4*>(next + row) + lane * 8u;
+        uint4* n4 = reinterpret_cast<uint4*>(next + off);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) n4[t] = xv[t];
+        for (uint32_t t = 0; t < kUnitChunks; ++t) {
+            normalize_chunk(xv[t], inv2);
+            weight_chunk(xv[t], nv[t]);
+            n4[t] = xv[t];
+        }
     }
 }
 
-// residual_norm_wave_kernel for many rows (prefill chunks), with the same per-lane
+// residual_norm_kernel for many rows (prefill chunks), with the same per-lane
 // arithmetic (lane u owns unit u) but coalesced memory access: the wave kernel's lanes each
 // read 128 contiguous bytes, so every 16-byte load instruction touches 64 cache lines. Here a
 // wave's loads and stores move 1 KB of consecutive bytes per instruction, and the row and
@@ -520,7 +553,7 @@ __global__ __launch_bounds__(64 * kTiledRows) void residual_norm_tiled_kernel(
         for (int t = 0; t < 8; ++t) rv[t] = tile[unit_slot(lane, t)];
     }
 
-    // residual_norm_wave_kernel's arithmetic, unit by unit.
+    // residual_norm_kernel's arithmetic, unit by unit.
     const float sc = scalar != nullptr ? bf16_bits_to_f32(*scalar) : 1.0f;
     float ss = mine ? unit_sumsq(xv) : 0.0f;
     ss = butterfly_sum<32>(ss, lane);
@@ -655,8 +688,8 @@ void launch_residual_norm(const uint16_t* branch, uint16_t* residual, const uint
                            dim3(64u * kTiledRows), 0, stream, branch, residual, w_post, scalar, w_next, next, m,
                            hidden, eps);
     } else if (hidden <= 64u * 64u) {
-        hipLaunchKernelGGL(residual_norm_wave_kernel, dim3(m), dim3(64), 0, stream, branch, residual, w_post, scalar,
-                           w_next, next, hidden, eps);
+        hipLaunchKernelGGL(residual_norm_lanes_kernel, dim3(m), dim3(64u * kUnitLanes), 0, stream, branch, residual,
+                           w_post, scalar, w_next, next, hidden, eps);
     } else {
         hipLaunchKernelGGL(residual_norm_kernel, dim3(m), dim3(kThreads), 0, stream, branch, residual, w_post, scalar,
                            w_next, next, hidden, eps);

@@ -148,6 +148,36 @@ __device__ __forceinline__ void residual_add_chunk(uint4& h, const uint4& r, boo
     h = make_uint4(x[0], x[1], x[2], x[3]);
 }
 
+// unit_sumsq of a unit spread over CH consecutive lanes: lane c = lane % CH holds its
+// 2 * NQ words (values [c * 4 NQ, (c + 1) * 4 NQ) of the unit, NQ = 16 / CH) in w. The fma
+// chain runs in unit_sumsq's order, each lane continuing the chain of lane c - 1, which a DPP
+// move hands over (CH steps, every lane computing its part each step from what it was
+// handed), so the total - on lane c = CH - 1 - has unit_sumsq's bits.
+template <int CH>
+__device__ __forceinline__ float scan_sumsq(const uint32_t (&w)[32 / CH], uint32_t c) {
+    static_assert(CH == 2 || CH == 4 || CH == 8, "a unit over 2, 4 or 8 lanes");
+    constexpr int NW = 32 / CH;
+    float f[2 * NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+        f[2 * q] = bf16_lo(w[q]);
+        f[2 * q + 1] = bf16_hi(w[q]);
+    }
+    float in = 0.0f;
+    float t = 0.0f;
+#pragma unroll
+    for (int s = 0; s < CH; ++s) {
+        t = in;
+#pragma unroll
+        for (int i = 0; i < 2 * NW; ++i) t = fmaf(f[i], f[i], t);
+        if (s + 1 < CH) {
+            const float prev = dpp_mov<0x111>(t);   // row_shr 1: lane i - 1
+            in = c == 0u ? 0.0f : prev;
+        }
+    }
+    return t;
+}
+
 // Sum of squares of one 64-element unit (8 x 16 bytes of bf16, k ascending).
 __device__ __forceinline__ float unit_sumsq(const uint4 (&xv)[8]) {
     float ss = 0.0f;
