@@ -55,6 +55,61 @@
 namespace hyperion::hip {
 namespace {
 
+// Lanes per 64-value unit in the normalising prologue's spread form.
+constexpr int kSpreadLanes = 4;
+
+// scan_sumsq over a lane's chunks (words in order).
+template <int CH>
+__device__ __forceinline__ float scan_sumsq_chunks(const uint4 (&v)[8 / CH], uint32_t sl) {
+    uint32_t w[32 / CH];
+#pragma unroll
+    for (int t = 0; t < 8 / CH; ++t) {
+        w[4 * t] = v[t].x;
+        w[4 * t + 1] = v[t].y;
+        w[4 * t + 2] = v[t].z;
+        w[4 * t + 3] = v[t].w;
+    }
+    return scan_sumsq<CH>(w, sl);
+}
+
+// A chunk of x (8 values) in the A operand's slot order: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+__device__ __forceinline__ uint4 permute_chunk(const uint4& c) {
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(c.z, c.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(c.z, c.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(c.w, c.y, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(c.w, c.y, 0x07060302u);
+    return o;
+}
+
+// The group sum of x of a unit spread over CH lanes (lane sl holding chunks 8 / CH * sl ..):
+// the staging's two dot2 chains (words x, z of each chunk into s0, y, w into s1, chunks in
+// order) handed from lane to lane by DPP moves, as scan_sumsq hands its chain; s0 and s1
+// are complete on lane sl = CH - 1.
+template <int CH>
+__device__ __forceinline__ void scan_group_sums(const uint4 (&xc)[8 / CH], uint32_t sl, float& s0, float& s1) {
+    float in0 = 0.0f;
+    float in1 = 0.0f;
+#pragma unroll
+    for (int s = 0; s < CH; ++s) {
+        s0 = in0;
+        s1 = in1;
+#pragma unroll
+        for (int t = 0; t < 8 / CH; ++t) {
+            s0 = dot2_bf16(xc[t].x, kOnePair, s0);
+            s1 = dot2_bf16(xc[t].y, kOnePair, s1);
+            s0 = dot2_bf16(xc[t].z, kOnePair, s0);
+            s1 = dot2_bf16(xc[t].w, kOnePair, s1);
+        }
+        if (s + 1 < CH) {
+            const float p0 = dpp_mov<0x111>(s0);   // row_shr 1: lane i - 1
+            const float p1 = dpp_mov<0x111>(s1);
+            in0 = sl == 0u ? 0.0f : p0;
+            in1 = sl == 0u ? 0.0f : p1;
+        }
+    }
+}
+
 // NORM 1: x rows are first rms-normalised (q4_rmsnorm.h) in LDS; the matmul then runs on
 // the normalised rows, which are not written back.
 // NORM 2: the sandwich close of the previous block first: x = in + rms(branch) * res_w
@@ -74,7 +129,7 @@ namespace {
 // The 8-wave residual form is held to 128 VGPRs (four waves per SIMD): its grids run two
 // workgroups on some compute units (the 12B's global q/k: 272 workgroups), and at more
 // registers the second would wait for the first (13.4 against 17.0 us at 134 VGPRs).
-template <int M, bool DUAL, int EPI, int P, int NWAVE, int NORM, bool LOOP>
+template <int M, bool DUAL, int EPI, int P, int NWAVE, int NORM, bool LOOP, int CH>
 __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q4_skinny_kernel(SkinnyParams p) {
     constexpr int NW = 1;
     constexpr uint32_t kThreads = 64u * NWAVE;
@@ -154,7 +209,7 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
     const uint32_t last = first + cnt - 1u;
 
     const uint32_t units = M * G;
-    const uint32_t nstage = max((min(units, kThreads) + 63u) / 64u, NORM ? static_cast<uint32_t>(M) : 1u);
+    const uint32_t nstage = max((min(units * CH, kThreads) + 63u) / 64u, NORM ? static_cast<uint32_t>(M) : 1u);
     const bool stager = wave < nstage;
 
     // x first: thread u's unit is requested before its wave's weight loads (with the early
@@ -170,7 +225,35 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
     uint4 xv[8];
     uint4 rv[8];
     uint16_t res_sc = 0u;   // NORM 2: the layer scalar (bf16)
-    if constexpr (!resid) {
+    // CH > 1 (the normalising forms when CH units' lanes fit the workgroup): unit su = thread
+    // / CH is spread over CH lanes, lane sl = thread % CH holding its values [64 / CH * sl,
+    // 64 / CH * (sl + 1)) as kCC 16-byte chunks (xc, and the residual's in rc).
+    constexpr uint32_t kCC = 8u / CH;
+    const uint32_t su = threadIdx.x / CH;
+    const uint32_t sl = threadIdx.x % CH;
+    const bool sown = su < units;
+    uint4 xc[kCC];
+    uint4 rc[kCC];
+    if constexpr (CH > 1) {
+#pragma unroll
+        for (uint32_t t = 0; t < kCC; ++t) xc[t] = rc[t] = make_uint4(0u, 0u, 0u, 0u);
+        if (sown) {
+            const uint32_t m = unit_row<M>(su, G);
+            const size_t off = static_cast<size_t>(m) * k + (su - m * G) * 64u + sl * (64u / CH);
+            if constexpr (!resid) {
+                const uint4* src = reinterpret_cast<const uint4*>(p.x + off);
+#pragma unroll
+                for (uint32_t t = 0; t < kCC; ++t) xc[t] = src[t];
+            } else {
+                const uint4* bsrc = reinterpret_cast<const uint4*>(p.res_branch + off);
+                const uint4* rsrc = reinterpret_cast<const uint4*>(p.res_in + off);
+#pragma unroll
+                for (uint32_t t = 0; t < kCC; ++t) xc[t] = bsrc[t];
+#pragma unroll
+                for (uint32_t t = 0; t < kCC; ++t) rc[t] = rsrc[t];
+            }
+        }
+    } else if constexpr (!resid) {
         if (xu0 < units) {
             const uint32_t m = unit_row<M>(xu0, G);
             const uint32_t g = xu0 - m * G;
@@ -262,7 +345,71 @@ __global__ __launch_bounds__(64 * NWAVE, NWAVE == 8 && NORM == 2 ? 4 : 1) void q
         for (int q = 0; q < NW; ++q) load_batch<P, !kLaneGroups>(lm[q], first + P, last, bb[q]);
     }
 
-    if (stager) {
+    if constexpr (CH > 1) {
+        if (stager) {
+            // The prologue of the spread form: the unit-per-thread form's operations per value and
+            // its sums in the same order (scan_sumsq, scan_group_sums), so the same bits.
+            const uint32_t m = unit_row<M>(min(su, units - 1u), G);
+            const uint32_t c0 = (su - m * G) * 8u + sl * kCC;   // this lane's first chunk in x's row
+            if constexpr (resid) {
+                const float tb = scan_sumsq_chunks<CH>(xc, sl);
+                if (sown && sl == CH - 1u) part[su] = tb;
+                if (wave == 0u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfterCopy));
+                raise_counter(ctr + 3, lane);
+                wait_counter(ctr + 3, nstage);
+                if (wave < static_cast<uint32_t>(M)) {
+                    const float ss = row_sumsq(part + wave * G, G, lane);
+                    if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+                }
+                raise_counter(ctr + 4, lane);
+                wait_counter(ctr + 4, nstage);
+                if (sown) {
+                    const float inv = part[units + m];
+                    const float sc = bf16_bits_to_f32(res_sc);
+    #pragma unroll
+                    for (uint32_t t = 0; t < kCC; ++t) {
+                        normalize_chunk(xc[t], inv);
+                        weight_chunk(xc[t], rwl[c0 + t]);
+                        residual_add_chunk(xc[t], rc[t], p.res_scalar != nullptr, sc);
+                    }
+                    if (blockIdx.x == 0u) {
+                        uint4* dst = reinterpret_cast<uint4*>(p.res_out + static_cast<size_t>(m) * k) + c0;
+    #pragma unroll
+                        for (uint32_t t = 0; t < kCC; ++t) dst[t] = xc[t];
+                    }
+                }
+                const float tx = scan_sumsq_chunks<CH>(xc, sl);
+                raise_counter(ctr + 5, lane);   // every wave has read its inverse
+                wait_counter(ctr + 5, nstage);
+                if (sown && sl == CH - 1u) part[su] = tx;
+            } else {
+                const float t = scan_sumsq_chunks<CH>(xc, sl);
+                if (sown && sl == CH - 1u) part[su] = t;
+                if (wave == 0u) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kAfterCopy));
+            }
+            raise_counter(ctr + 1, lane);
+            wait_counter(ctr + 1, nstage);
+            if (wave < static_cast<uint32_t>(M)) {
+                const float ss = row_sumsq(part + wave * G, G, lane);
+                if (lane == 0u) part[units + wave] = rms_inverse(ss, k, p.eps);
+            }
+            raise_counter(ctr + 2, lane);
+            wait_counter(ctr + 2, nstage);
+            if (sown) {
+                const float inv = part[units + m];
+    #pragma unroll
+                for (uint32_t t = 0; t < kCC; ++t) {
+                    normalize_chunk(xc[t], inv);
+                    if (p.norm_w != nullptr) weight_chunk(xc[t], nwl[c0 + t]);
+                    xs[m * WS + c0 + t] = permute_chunk(xc[t]);
+                }
+            }
+            float s0, s1;
+            scan_group_sums<CH>(xc, sl, s0, s1);
+            if (sown && sl == CH - 1u) reinterpret_cast<float*>(sx)[(su - m * G) * 4u + m] = s0 + s1;
+            raise_counter(ctr, lane);   // kEarly: every normalising form
+        }
+    } else if (stager) {
         if constexpr (NORM) {
             if constexpr (resid) {
                 // The branch's norm (phases 3, 4), the residual add, then x's statistics
@@ -460,15 +607,15 @@ size_t skinny_lds_bytes(uint32_t m, uint32_t k, bool dual, uint32_t nwave, int n
 
 size_t max_lds_per_block();
 
-template <int M, bool DUAL, int EPI, int NWAVE, int NORM = 0>
+template <int M, bool DUAL, int EPI, int NWAVE, int NORM = 0, int CH = 1>
 void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t stream) {
     // Pairs per register batch (two batches in flight): 4, so that a wave's whole range
     // (at most kSkinnyPairsUpFront pairs) is requested at once; 2 for the softcap head,
     // whose waves loop.
     constexpr int P = EPI != 0 ? 2 : 4;
     const uint32_t per_wave = (p.pairs + p.splits - 1u) / p.splits;
-    auto kernel = per_wave <= 2u * P ? q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false>
-                                     : q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true>;
+    auto kernel = per_wave <= 2u * P ? q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false, CH>
+                                     : q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true, CH>;
     const size_t lds = skinny_lds_bytes(M, p.k, DUAL, NWAVE, NORM);
     HYP_REQUIRE(lds <= max_lds_per_block(), HYP_STATUS_INTERNAL, "skinny: x staging exceeds the device's LDS");
     if (lds > 65536u) {
@@ -476,8 +623,8 @@ void launch_skinny_t(const SkinnyParams& p, uint32_t tiles_total, hipStream_t st
         int dev = 0;
         HYP_HIP_CHECK(hipGetDevice(&dev));
         if (configured_device != dev) {
-            for (const void* f : {reinterpret_cast<const void*>(q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false>),
-                                  reinterpret_cast<const void*>(q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true>)}) {
+            for (const void* f : {reinterpret_cast<const void*>(q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, false, CH>),
+                                  reinterpret_cast<const void*>(q4_skinny_kernel<M, DUAL, EPI, P, NWAVE, NORM, true, CH>)}) {
                 HYP_HIP_CHECK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                   static_cast<int>(max_lds_per_block())));
             }
@@ -541,12 +688,27 @@ void launch_skinny_m(const SkinnyParams& p, uint32_t tiles_total, bool dual, Epi
         launch_skinny_t<M, false, 1, 4>(p, tiles_total, stream);
     } else {
         const uint32_t w = choose_skinny_waves(tiles_total, p.splits, M, p.k, norm);
+        // The normalising prologue with each unit over kSpreadLanes lanes where the spread units
+        // fit four waves, one per SIMD (at most 64 units: one row up to k = 4096). Beyond that the
+        // unit-per-thread form already has a staging wave on every SIMD, and spreading would put
+        // several on each.
+        const bool spread = static_cast<uint64_t>(M) * (p.k / 64u) * kSpreadLanes <= 256u;
         if (norm == 2) {
-            w == 8u ? launch_skinny_t<M, false, 0, 8, 2>(p, tiles_total, stream)
-                    : launch_skinny_t<M, false, 0, 16, 2>(p, tiles_total, stream);
+            if (spread) {
+                w == 8u ? launch_skinny_t<M, false, 0, 8, 2, kSpreadLanes>(p, tiles_total, stream)
+                        : launch_skinny_t<M, false, 0, 16, 2, kSpreadLanes>(p, tiles_total, stream);
+            } else {
+                w == 8u ? launch_skinny_t<M, false, 0, 8, 2>(p, tiles_total, stream)
+                        : launch_skinny_t<M, false, 0, 16, 2>(p, tiles_total, stream);
+            }
         } else if (norm == 1) {
-            w == 8u ? launch_skinny_t<M, false, 0, 8, 1>(p, tiles_total, stream)
-                    : launch_skinny_t<M, false, 0, 16, 1>(p, tiles_total, stream);
+            if (spread) {
+                w == 8u ? launch_skinny_t<M, false, 0, 8, 1, kSpreadLanes>(p, tiles_total, stream)
+                        : launch_skinny_t<M, false, 0, 16, 1, kSpreadLanes>(p, tiles_total, stream);
+            } else {
+                w == 8u ? launch_skinny_t<M, false, 0, 8, 1>(p, tiles_total, stream)
+                        : launch_skinny_t<M, false, 0, 16, 1>(p, tiles_total, stream);
+            }
         } else if (w == 4u) {
             launch_skinny_t<M, false, 0, 4>(p, tiles_total, stream);
         } else if (w == 8u) {
