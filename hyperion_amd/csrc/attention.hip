@@ -411,7 +411,25 @@ __device__ __forceinline__ void rope_rows_lds(uint16_t* rows_base, uint32_t rows
     }
 }
 
-template <uint32_t D, bool PREP>
+// Lanes per 64-value unit in the folded prepare's spread form (CH > 1): at most 16 / (D / 64)
+// so that the row butterfly's lane offsets stay within a 16-lane row (DPP moves).
+template <uint32_t D>
+constexpr uint32_t kPrepLanes = D <= 128u ? 8u : 16u / (D / 64u);
+
+// The value of lane CH - 1 of each group of CH lanes on every lane of the group.
+template <uint32_t CH>
+__device__ __forceinline__ float group_last(float v, uint32_t lane) {
+    static_assert(CH == 2u || CH == 4u || CH == 8u, "groups of 2, 4 or 8 lanes");
+    if constexpr (CH == 2u) return dpp_mov<0xF5>(v);   // quad_perm [1, 1, 3, 3]
+    v = dpp_mov<0xFF>(v);                               // quad_perm [3, 3, 3, 3]
+    if constexpr (CH == 8u) {
+        const float up = dpp_mov<0x104>(v);             // row_shl 4: lane i + 4
+        v = (lane & 4u) != 0u ? v : up;
+    }
+    return v;
+}
+
+template <uint32_t D, bool PREP, uint32_t CH = 1>
 __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel(AttnParams p) {
     resolve_position(p);
     using Lds = DecodeLds<D>;
@@ -469,10 +487,14 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
 #pragma unroll
             for (uint32_t st = 0; st < kSteps; ++st) qa[st] = bf16x8_t{};
         } else {
-            // One 64-value unit per lane: row r = lane / kU is query row r (r < G), the new
-            // key's K (r == G) or its V (r == G + 1); the host folds only when they fit.
-            const uint32_t u = lane % kU;
-            const uint32_t r = lane / kU;
+            // One 64-value unit per CH lanes (lane sl = lane % CH of unit slot lane / CH holds
+            // its values [64 / CH * sl, 64 / CH * (sl + 1))): slot row r = slot / kU is query
+            // row r (r < G), the new key's K (r == G) or its V (r == G + 1); the host folds
+            // only when they fit.
+            constexpr uint32_t kCC = 8u / CH;   // 16-byte chunks per lane
+            const uint32_t sl = lane % CH;
+            const uint32_t u = (lane / CH) % kU;
+            const uint32_t r = lane / CH / kU;
             const bool is_q = r < p.G;
             const bool is_k = fresh_key && r == p.G;
             const bool is_v = fresh_key && r == p.G + 1u;
@@ -488,17 +510,20 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
             } else if (is_v) {
                 src = (p.v_raw != nullptr ? p.v_raw : p.k_raw) + static_cast<size_t>(hk) * D;
             }
-            uint4 xv[8];
-            uint4 wv[8];
-            if (src != nullptr) {
-                const uint4* s4 = reinterpret_cast<const uint4*>(src + u * 64u);
+            const uint32_t voff = u * 64u + sl * (64u / CH);   // this lane's first value in the row
+            uint4 xv[kCC];
+            uint4 wv[kCC];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) xv[t] = s4[t];
+            for (uint32_t t = 0; t < kCC; ++t) xv[t] = make_uint4(0u, 0u, 0u, 0u);
+            if (src != nullptr) {
+                const uint4* s4 = reinterpret_cast<const uint4*>(src + voff);
+#pragma unroll
+                for (uint32_t t = 0; t < kCC; ++t) xv[t] = s4[t];
             }
             if (w != nullptr) {
-                const uint4* w4 = reinterpret_cast<const uint4*>(w + u * 64u);
+                const uint4* w4 = reinterpret_cast<const uint4*>(w + voff);
 #pragma unroll
-                for (int t = 0; t < 8; ++t) wv[t] = w4[t];
+                for (uint32_t t = 0; t < kCC; ++t) wv[t] = w4[t];
             }
             // One dword of every 128-byte line of the first key block's K and V rows, requested
             // behind this prologue's loads and consumed at its end: their HBM fetch overlaps
@@ -523,23 +548,37 @@ __global__ __launch_bounds__(DecodeLds<D>::kWaves * 64u) void attn_decode_kernel
                     }
                 }
             }
-            // The prepare's 64-lane butterfly over a row's kU lanes (the rest of its lanes
-            // add zeros there).
-            float ss = src != nullptr ? unit_sumsq(xv) : 0.0f;
-            if constexpr (kU >= 8u) ss += xor_lanes<4>(ss, lane);
-            if constexpr (kU >= 4u) ss += xor_lanes<2>(ss, lane);
-            if constexpr (kU >= 2u) ss += xor_lanes<1>(ss, lane);
+            // The prepare's 64-lane butterfly over a row's kU units (the rest of its lanes add
+            // zeros there): each unit's sum (its fma chain handed across its CH lanes) on all of
+            // its lanes, then the xor steps kU / 2, ..., 1 between units.
+            float ss;
+            if constexpr (CH == 1u) {
+                ss = src != nullptr ? unit_sumsq(xv) : 0.0f;
+            } else {
+                uint32_t ws[4 * kCC];
+#pragma unroll
+                for (uint32_t t = 0; t < kCC; ++t) {
+                    ws[4 * t] = xv[t].x;
+                    ws[4 * t + 1] = xv[t].y;
+                    ws[4 * t + 2] = xv[t].z;
+                    ws[4 * t + 3] = xv[t].w;
+                }
+                ss = group_last<CH>(scan_sumsq<CH>(ws, sl), lane);
+            }
+            if constexpr (kU >= 8u) ss += xor_lanes<4u * CH>(ss, lane);
+            if constexpr (kU >= 4u) ss += xor_lanes<2u * CH>(ss, lane);
+            if constexpr (kU >= 2u) ss += xor_lanes<1u * CH>(ss, lane);
             if (src != nullptr) {
-                normalize_unit(xv, rms_inverse(ss, D, p.eps));
-                if (w != nullptr) weight_unit(xv, wv);
+                const float inv = rms_inverse(ss, D, p.eps);
                 uint16_t* dst = is_q ? qs + r * D : (is_k ? new_k : new_v);
-                uint4* d4 = reinterpret_cast<uint4*>(dst + u * 64u);
+                uint4* d4 = reinterpret_cast<uint4*>(dst + voff);
+                uint4* vg = reinterpret_cast<uint4*>(p.cv_out + slot_row + voff);
 #pragma unroll
-                for (int t = 0; t < 8; ++t) d4[t] = xv[t];
-                if (is_v) {
-                    uint4* vg = reinterpret_cast<uint4*>(p.cv_out + slot_row + u * 64u);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) vg[t] = xv[t];
+                for (uint32_t t = 0; t < kCC; ++t) {
+                    normalize_chunk(xv[t], inv);
+                    if (w != nullptr) weight_chunk(xv[t], wv[t]);
+                    d4[t] = xv[t];
+                    if (is_v) vg[t] = xv[t];
                 }
             }
             wave_lds_sync();
@@ -850,7 +889,8 @@ void launch_decode_d(const AttnParams& p, bool prep, hipStream_t stream) {
         HYP_HIP_CHECK(hipGetDevice(&dev));
         if (configured_device != dev) {
             for (const void* f : {reinterpret_cast<const void*>(attn_decode_kernel<D, false>),
-                                  reinterpret_cast<const void*>(attn_decode_kernel<D, true>)}) {
+                                  reinterpret_cast<const void*>(attn_decode_kernel<D, true>),
+                                  reinterpret_cast<const void*>(attn_decode_kernel<D, true, kPrepLanes<D>>)}) {
                 HYP_HIP_CHECK(
                     hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
             }
@@ -858,7 +898,11 @@ void launch_decode_d(const AttnParams& p, bool prep, hipStream_t stream) {
         }
     }
     const dim3 grid((p.splits + Lds::kWaves - 1u) / Lds::kWaves, p.KVH);
-    auto kernel = prep ? attn_decode_kernel<D, true> : attn_decode_kernel<D, false>;
+    // The folded prepare spread over kPrepLanes<D> lanes per unit where the G query rows, K and
+    // V of a kv head fit one wave that way.
+    const bool spread = prep && (p.G + 2u) * (D / 64u) * kPrepLanes<D> <= 64u;
+    auto kernel = !prep ? attn_decode_kernel<D, false>
+                        : (spread ? attn_decode_kernel<D, true, kPrepLanes<D>> : attn_decode_kernel<D, true>);
     hipLaunchKernelGGL(kernel, grid, dim3(Lds::kWaves * 64u), lds, stream, p);
     HYP_HIP_CHECK(hipGetLastError());
 }

@@ -536,17 +536,21 @@ def test_residual_rms_norm_bit_exact(stream, m, hidden, scalar, nxt):
 
 
 @pytest.mark.parametrize("prefix", [20, 31, 32, 63, 64])
-def test_folded_prepare_equals_separate(tmp_path, prefix):
+@pytest.mark.parametrize("head_dims", [(64, 128), (256, 512)])
+def test_folded_prepare_equals_separate(tmp_path, prefix, head_dims):
     """A one-token step folds the q/k norms, RoPE and the cache append into the decode
     attention launch; a two-token step at the same position runs them as their own launch
     (attn_prepare_kernel) with every other kernel the same per row. Row 0 of the two-token
     step has the bits of the one-token step, on both layer kinds, with the new key first,
-    last and inside a 32-key block."""
+    last and inside a 32-key block. Head dims 64 and 256 take the folded form with each
+    64-value unit spread over 8 and 4 lanes, 128 and 512 (four query rows per kv head) the
+    unit-per-lane form."""
     cfg = tiny_dims_config(256)
+    cfg["head_dim"], cfg["global_head_dim"] = head_dims
     T = syn.write_model(str(tmp_path), cfg, seed=16, branch_gain=BRANCH_GAIN, qk_gain=QK_GAIN)
     model = hy.Model(hy.geometry_from_config(cfg), str(tmp_path))
     ids = np.random.default_rng(prefix).integers(0, cfg["vocab_size"], size=prefix + 2).astype(np.uint32)
-    say(f"folded prepare: prefix {prefix}")
+    say(f"folded prepare: prefix {prefix}, head dims {head_dims}")
     one, two = model.kvstate(), model.kvstate()
     one.forward_hidden(ids[:prefix], 0)
     two.forward_hidden(ids[:prefix], 0)
