@@ -893,14 +893,16 @@ def test_qmatmul_group_rmsnorm_equals_two_calls(stream, m):
 
 @pytest.mark.parametrize("m,k,ns", [(4, 10240, (512, 256, 256)), (1, 10240, (512, 256, 256)),
                                     (4, 8192, (256, 64, 64)), (3, 3840, (128, 64, 64)),
-                                    (1, 3840, (8192, 512)), (4, 3840, (8192, 512))])
+                                    (1, 3840, (8192, 512)), (4, 3840, (8192, 512)),
+                                    (2, 1024, (256, 64, 64)), (4, 1024, (1024, 256)), (3, 1280, (512,))])
 def test_qmatmul_group_rmsnorm_launch_shapes(stream, m, k, ns):
     """The normalising q/k/v launch in the workgroup shapes its launcher picks for other
     widths and grids - more (row, group) units than an 8-wave workgroup has threads (m = 4,
     k = 10240: 640 units), exactly as many (k = 8192), a grid of a few tiles, more waves
     than one round of 8-wave workgroups holds (the 12B's global q/k: 544 tiles at 4 splits,
-    16-wave workgroups scaling x chunk by chunk) - equals hyp_rms_normalize then
-    hyp_qmatmul_group, bit for bit."""
+    16-wave workgroups scaling x chunk by chunk), and the prologue with each unit spread over
+    four lanes at several rows (m x k / 64 <= 64 units: 32, 64 and 60) - equals
+    hyp_rms_normalize then hyp_qmatmul_group, bit for bit."""
     ws = [syn.q4_weights(n, k, seed=1270 + i) for i, n in enumerate(ns)]
     qws = [hy.QWeight.from_host(*w) for w in ws]
     x = syn.activations(m, k, seed=1280 + m)
