@@ -50,29 +50,6 @@ struct PrepareParams {
     float eps;
 };
 
-// Lanes u < D/64 hold 64-value unit u of a head (loaded by load_head); norm_loaded leaves
-// bf16(w * bf16(x * inv)) (no weight: bf16(x * inv)) there. Every lane takes part in the
-// butterfly. Loads are separate so a caller can issue all of its loads before any use.
-__device__ __forceinline__ void load_head(const uint16_t* src, uint32_t D, uint32_t lane, uint4 (&xv)[8]) {
-    if (lane < D / 64u) {
-        const uint4* s4 = reinterpret_cast<const uint4*>(src) + lane * 8u;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) xv[t] = s4[t];
-    }
-}
-
-__device__ __forceinline__ void norm_loaded(uint4 (&xv)[8], const uint4 (*wv)[8], uint32_t D, float eps,
-                                            uint32_t lane) {
-    const uint32_t units = D / 64u;
-    float ss = lane < units ? unit_sumsq(xv) : 0.0f;
-    ss = butterfly_sum<32>(ss, lane);
-    const float inv = rms_inverse(ss, D, eps);
-    if (lane < units) {
-        normalize_unit(xv, inv);
-        if (wv != nullptr) weight_unit(xv, *wv);
-    }
-}
-
 // rope_kernel's angle arithmetic: inv_freq in double rounded to fp32, theta in fp32, cos and
 // sin in double rounded to fp32.
 __device__ __forceinline__ float2 rope_angle(uint32_t pos, uint32_t i, uint32_t D, uint32_t rotated, double base) {
@@ -84,7 +61,8 @@ __device__ __forceinline__ float2 rope_angle(uint32_t pos, uint32_t i, uint32_t 
 
 // Short chunks (a decode step: a few dozen rows, which attn_prepare_kernel would give to a
 // few waves): grid (L, ceil((H + KVH) / 4)), wave w of workgroup (t, y) takes head 4y + w
-// of token t (q heads first, then kv heads), all 64 lanes in its RoPE. The same bits.
+// of token t (q heads first, then kv heads), 8 values per lane in its norms
+// (norm_row_lanes8) and all 64 lanes in its RoPE. The same bits.
 __global__ __launch_bounds__(kThreads) void attn_prepare_head_kernel(PrepareParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t head[kWaves][kMaxHeadDim];
     const uint32_t t = blockIdx.x;
@@ -112,35 +90,33 @@ __global__ __launch_bounds__(kThreads) void attn_prepare_head_kernel(PreparePara
         }
     }
     if (active) {
-        uint4 xv[8];
-        uint4 wv[8];
+        // 8 values per lane (norm_row_lanes8): every lane of the wave in the norm.
+        const bool has = lane < D / 8u;
+        uint4 xc = make_uint4(0u, 0u, 0u, 0u);
+        uint4 wc = make_uint4(0u, 0u, 0u, 0u);
         const uint32_t kh = hh - p.H;
         const size_t kv_row = (static_cast<size_t>(t) * p.KVH + kh) * D;
         if (is_q) {
             dst = p.q + (static_cast<size_t>(t) * p.H + hh) * D;
-            load_head(dst, D, lane, xv);
-            load_head(p.q_w, D, lane, wv);
+            if (has) {
+                xc = reinterpret_cast<const uint4*>(dst)[lane];
+                wc = reinterpret_cast<const uint4*>(p.q_w)[lane];
+            }
         } else {
             // V: the weightless norm straight into the cache slot; its loads and K's are
             // issued together.
-            uint4 vv[8];
-            load_head(p.v_raw != nullptr ? p.v_raw + kv_row : p.k_raw + kv_row, D, lane, vv);
-            load_head(p.k_raw + kv_row, D, lane, xv);
-            load_head(p.k_w, D, lane, wv);
-            norm_loaded(vv, nullptr, D, p.eps, lane);
-            if (lane < D / 64u) {
-                uint4* v4 = reinterpret_cast<uint4*>(p.cache_v + (slot * p.KVH + kh) * D) + lane * 8u;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v4[u] = vv[u];
+            uint4 vc = make_uint4(0u, 0u, 0u, 0u);
+            if (has) {
+                vc = reinterpret_cast<const uint4*>(p.v_raw != nullptr ? p.v_raw + kv_row : p.k_raw + kv_row)[lane];
+                xc = reinterpret_cast<const uint4*>(p.k_raw + kv_row)[lane];
+                wc = reinterpret_cast<const uint4*>(p.k_w)[lane];
             }
+            norm_row_lanes8(vc, nullptr, D, p.eps, lane);
+            if (has) reinterpret_cast<uint4*>(p.cache_v + (slot * p.KVH + kh) * D)[lane] = vc;
             dst = p.cache_k + (slot * p.KVH + kh) * D;
         }
-        norm_loaded(xv, &wv, D, p.eps, lane);
-        if (lane < D / 64u) {
-            uint4* h4 = reinterpret_cast<uint4*>(hb) + lane * 8u;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) h4[u] = xv[u];
-        }
+        norm_row_lanes8(xc, &wc, D, p.eps, lane);
+        if (has) reinterpret_cast<uint4*>(hb)[lane] = xc;
     }
     __syncthreads();   // the staged head is visible to every lane of its wave
     if (active) {

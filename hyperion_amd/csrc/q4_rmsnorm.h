@@ -209,4 +209,26 @@ __device__ __forceinline__ void weight_unit(uint4 (&xv)[8], const uint4 (&wv)[8]
     for (int t = 0; t < 8; ++t) weight_chunk(xv[t], wv[t]);
 }
 
+// A head row of D <= 512 values held 8 per lane (lane l: values [8l, 8l + 8), one 16-byte
+// chunk; lanes l >= D / 8 hold zeros): c <- bf16(w * bf16(c * inv)) (no weight: bf16(c *
+// inv)) with the bits of the unit-per-lane form. Each unit's fma chain runs over its 8 lanes
+// (scan_sumsq), its total goes to all 8, and the units meet in the xor butterfly's order
+// (offsets D / 128 .. 1 units apart, 8 lanes per unit; the unit-per-lane butterfly's steps
+// below them add zeros). Every lane takes part.
+__device__ __forceinline__ void norm_row_lanes8(uint4& c, const uint4* w, uint32_t D, float eps, uint32_t lane) {
+    const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+    float ss = scan_sumsq<8>(words, lane & 7u);
+    ss = dpp_mov<0xFF>(ss);                     // quad_perm [3, 3, 3, 3]: lane 4q + 3's
+    const float up = dpp_mov<0x104>(ss);        // row_shl 4: lane i + 4
+    ss = (lane & 4u) != 0u ? ss : up;           // lane 8u + 7's total on all 8 lanes
+    const uint32_t units = D / 64u;
+    if (units >= 8u) ss = add_lane_xor32(ss);
+    if (units >= 4u) ss = add_lane_xor16(ss);
+    if (units >= 2u) ss += xor_lanes<8>(ss, lane);
+    if (lane < D / 8u) {
+        normalize_chunk(c, rms_inverse(ss, D, eps));
+        if (w != nullptr) weight_chunk(c, *w);
+    }
+}
+
 }  // namespace hyperion::hip
