@@ -895,23 +895,26 @@ def test_qmatmul_group_rmsnorm_equals_two_calls(stream, m):
                                     (4, 8192, (256, 64, 64)), (3, 3840, (128, 64, 64)),
                                     (1, 3840, (8192, 512)), (4, 3840, (8192, 512)),
                                     (2, 1024, (256, 64, 64)), (4, 1024, (1024, 256)), (3, 1280, (512,))])
-def test_qmatmul_group_rmsnorm_launch_shapes(stream, m, k, ns):
+@pytest.mark.parametrize("weighted", [False, True])
+def test_qmatmul_group_rmsnorm_launch_shapes(stream, m, k, ns, weighted):
     """The normalising q/k/v launch in the workgroup shapes its launcher picks for other
     widths and grids - more (row, group) units than an 8-wave workgroup has threads (m = 4,
     k = 10240: 640 units), exactly as many (k = 8192), a grid of a few tiles, more waves
     than one round of 8-wave workgroups holds (the 12B's global q/k: 544 tiles at 4 splits,
     16-wave workgroups scaling x chunk by chunk), and the prologue with each unit spread over
-    four lanes at several rows (m x k / 64 <= 64 units: 32, 64 and 60) - equals
-    hyp_rms_normalize then hyp_qmatmul_group, bit for bit."""
+    four lanes at several rows (m x k / 64 <= 64 units: 32, 64 and 60), with and without
+    the norm's learned weight - equals hyp_rms_normalize then hyp_qmatmul_group, bit for bit."""
     ws = [syn.q4_weights(n, k, seed=1270 + i) for i, n in enumerate(ns)]
     qws = [hy.QWeight.from_host(*w) for w in ws]
     x = syn.activations(m, k, seed=1280 + m)
     xd = dev(x, stream)
-    say(f"group rmsnorm m={m} k={k} n={ns}")
+    say(f"group rmsnorm m={m} k={k} n={ns} weighted={weighted}")
+    nw = dev(syn.bf16_bits(1.0 + 0.2 * np.random.default_rng(k).standard_normal(k).astype(np.float32)), stream) \
+        if weighted else None
     fused = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
-    hy.qmatmul_group(qws, xd, m, fused, stream, rms_eps=1e-6)
+    hy.qmatmul_group(qws, xd, m, fused, stream, rms_eps=1e-6, norm_weight=nw)
     xn = hy.DeviceArray((m, k), np.uint16)
-    hy.rms_normalize(xd, m, k, xn, stream, eps=1e-6)
+    hy.rms_normalize(xd, m, k, xn, stream, eps=1e-6, weight=nw)
     sep = [hy.DeviceArray((m, w[0].shape[0]), np.uint16) for w in ws]
     hy.qmatmul_group(qws, xn, m, sep, stream)
     xn_host = xn.to_host(stream)
@@ -919,7 +922,7 @@ def test_qmatmul_group_rmsnorm_launch_shapes(stream, m, k, ns):
         yf = f.to_host(stream)
         np.testing.assert_array_equal(yf, g.to_host(stream), err_msg=name)
         assert_within_bf16_rounding(yf, O.qmatmul_f64(xn_host, w, s, b), name)
-    for a in qws + fused + sep + [xd, xn]:
+    for a in qws + fused + sep + [xd, xn] + ([nw] if weighted else []):
         a.close()
 
 
